@@ -1,0 +1,61 @@
+// Shared device/host helpers for the gfx950 quantized-matmul library.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/aether_hip.h"
+
+// GGUF block geometry (src/quant/matmul/common.rs:1-8; gguf.rs:137-173).
+#define Q8_BLOCK_ELEMS 32
+#define Q8_BLOCK_BYTES 34
+#define QK_BLOCK_ELEMS 256
+#define Q4K_BLOCK_BYTES 144
+#define Q6K_BLOCK_BYTES 210
+
+// Records a message for aeth_last_error() and returns `code`.
+int aeth_set_error(int code, const char* fmt, ...);
+
+#define AETH_HIP_CHECK(expr)                                                          \
+    do {                                                                              \
+        hipError_t _e = (expr);                                                       \
+        if (_e != hipSuccess)                                                         \
+            return aeth_set_error(AETH_EHIP, "%s failed: %s (%s:%d)", #expr,          \
+                                  hipGetErrorString(_e), __FILE__, __LINE__);         \
+    } while (0)
+
+#define AETH_LAUNCH_CHECK()                                                           \
+    do {                                                                              \
+        hipError_t _e = hipGetLastError();                                            \
+        if (_e != hipSuccess)                                                         \
+            return aeth_set_error(AETH_EHIP, "kernel launch failed: %s (%s:%d)",     \
+                                  hipGetErrorString(_e), __FILE__, __LINE__);         \
+    } while (0)
+
+// Exact binary16 -> binary32.
+__device__ __forceinline__ float aeth_f16_to_f32(uint32_t bits16) {
+    return __half2float(__ushort_as_half((unsigned short)bits16));
+}
+
+// decode_f16_scale / decode_d (common.rs:19-27, dequant.rs:161-168): K-quant
+// scales whose f16 pattern is NaN or Inf decode to bits/65536 instead.
+__device__ __forceinline__ float aeth_decode_d(uint32_t bits16) {
+    bits16 &= 0xFFFFu;
+    if ((bits16 & 0x7C00u) == 0x7C00u) return (float)bits16 * (1.0f / 65536.0f);
+    return aeth_f16_to_f32(bits16);
+}
+
+__device__ __forceinline__ float aeth_wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float aeth_wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+static inline int64_t aeth_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -1,0 +1,25 @@
+// Internal (non-exported) declarations shared by the library's sources.
+#pragma once
+#include <stdint.h>
+
+// Device copy of one QuantWeight in per-field planes (see aeth_weights.hip).
+struct aeth_weight {
+    int dtype;
+    int64_t n, k;         // out_features, in_features
+    int64_t nb;           // blocks per row
+    int64_t nblk;         // n * nb
+    int64_t block_bytes;  // GGUF bytes per block
+    int64_t bytes;        // nblk * block_bytes
+    uint8_t* base;
+    uint8_t *p0, *p1, *p2, *p3;
+};
+
+int aeth_num_cus();
+int64_t aeth_blocks_per_row(int dtype, int64_t k);
+
+// GEMV on one activation row per launch-row (a: [m][k] f32, c: [m][n]).
+int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags,
+                     hipStream_t s);
+// Q4_K prefill GEMM (m > 1).
+int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
+                         hipStream_t s);

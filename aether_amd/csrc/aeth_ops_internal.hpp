@@ -1,0 +1,24 @@
+// Internal launchers of the decode-step kernels (aeth_decode_ops.hip).
+// Scalars given as (device pointer, value): the pointer wins when non-NULL.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+int aeth_rmsnorm_launch(const float* x, const float* w, int64_t rows, int64_t n, float eps, float* out,
+                        hipStream_t s);
+int aeth_rope_launch(float* x, int64_t n_heads, int64_t head_dim, const int* d_pos, int64_t pos,
+                     const float* sin_t, const float* cos_t, int64_t max_seq, hipStream_t s);
+int aeth_kv_append_launch(float* layer_kv, const float* k, const float* v, int64_t kv_heads, int64_t head_dim,
+                          int64_t max_seq, const int* d_slot, int64_t slot, hipStream_t s);
+int64_t aeth_attn_ws_floats(int64_t n_heads, int64_t head_dim, int64_t max_seq);
+// seq = (d_seq ? *d_seq : seq) + seq_add, clamped to max_seq.
+int aeth_attn_decode_launch(const float* q, const float* layer_kv, int64_t n_heads, int64_t kv_heads,
+                            int64_t head_dim, int64_t max_seq, const int* d_seq, int64_t seq, int seq_add,
+                            float* ws, float* out, hipStream_t s);
+int aeth_silu_mul_launch(float* g, const float* up, int64_t n, hipStream_t s);
+int aeth_add_launch(float* x, const float* y, int64_t n, hipStream_t s);
+int64_t aeth_argmax_ws_bytes();
+int aeth_argmax_launch(const float* x, int64_t n, int* out, int* next_token, void* ws, hipStream_t s);
+int aeth_embed_launch(const float* table, const int* d_token, int64_t token, int64_t d, int64_t vocab, float* x,
+                      hipStream_t s);
+int aeth_state_advance_launch(int* st, int64_t max_seq, hipStream_t s);

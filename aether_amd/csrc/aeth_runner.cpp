@@ -1,0 +1,638 @@
+// LlamaRunner on the device (src/inference/runner.rs) and the aether_* C ABI
+// (aether.h:28-81, src/c_api.rs).
+//
+// Every tensor of a decode step stays in HBM: token id in, logits / next
+// token out. The step reads its scalars {token, pos, cache fill} from a
+// device int[3], so one step is captured once as a HIP graph and replayed
+// for greedy generation without host round trips.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <chrono>
+#include <mutex>
+#include <vector>
+
+#include "../../include/aether.h"
+#include "aeth_common.hpp"
+#include "aeth_internal.hpp"
+#include "aeth_ops_internal.hpp"
+
+struct aeth_runner {
+    aeth_llama_config cfg;
+    hipStream_t stream = nullptr;
+    // weights
+    std::vector<aeth_weight*> wqkv, wo, wgu, wdown;  // per layer (q|k|v and gate|up concatenated by rows)
+    std::vector<int> dtypes;                         // per layer x 7
+    aeth_weight* lm_head = nullptr;
+    float* norms = nullptr;       // [L][2][d]
+    float* final_norm = nullptr;  // [d]
+    float* emb = nullptr;         // [vocab][d]
+    float* rope_sin = nullptr;    // [max_seq][hd/2]
+    float* rope_cos = nullptr;
+    float* kv = nullptr;          // [L][2][kvh][max_seq][hd]
+    // activations
+    float *x = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
+    float* attn_ws = nullptr;
+    void* am_ws = nullptr;
+    int* st = nullptr;      // device {token, pos, fill}
+    int* tok_out = nullptr;  // device argmax
+    int fill = 0;           // host mirror of the cache fill
+    hipGraphExec_t graph = nullptr;
+    // frame budget / partial decode (runner.rs:1201-1282, c_api.rs:313-355)
+    float frame_budget_ms = 0.0f;
+    bool partial_valid = false;
+    int partial_token = 0, partial_pos = 0, partial_layer = 0;
+    std::mutex mu;
+};
+
+namespace {
+
+const int64_t kKvd(const aeth_llama_config& c) { return (int64_t)c.num_kv_heads * c.head_dim; }
+
+int64_t kv_layer_floats(const aeth_llama_config& c) {
+    return 2LL * c.num_kv_heads * (int64_t)c.max_seq_len * c.head_dim;
+}
+
+// precompute_rope (runner.rs:1912-1924) with the host libm (f32 powf/sinf/cosf).
+void precompute_rope(int max_seq, int head_dim, float base, std::vector<float>& s, std::vector<float>& c) {
+    int half = head_dim / 2;
+    s.resize((size_t)max_seq * half);
+    c.resize((size_t)max_seq * half);
+    for (int p = 0; p < max_seq; p++)
+        for (int i = 0; i < half; i++) {
+            float theta = (float)p * powf(base, -2.0f * (float)i / (float)head_dim);
+            s[(size_t)p * half + i] = sinf(theta);
+            c[(size_t)p * half + i] = cosf(theta);
+        }
+}
+
+int make_weight(int dtype, int64_t n, int64_t k, const void* host_raw, uint64_t seed, hipStream_t s,
+                aeth_weight** out) {
+    int be, bb;
+    int rc = aeth_block_geometry(dtype, &be, &bb);
+    if (rc) return rc;
+    if (host_raw) return aeth_weight_create(dtype, n, k, host_raw, 0, s, out);
+    int64_t nblk = n * aeth_blocks_per_row(dtype, k);
+    void* raw = nullptr;
+    AETH_HIP_CHECK(hipMalloc(&raw, (size_t)(nblk * bb)));
+    rc = aeth_fill_synthetic_raw(dtype, seed, raw, nblk, s);
+    if (!rc) rc = aeth_weight_create(dtype, n, k, raw, 1, s, out);
+    hipError_t e = hipStreamSynchronize(s);
+    hipFree(raw);
+    if (!rc && e != hipSuccess) rc = aeth_set_error(AETH_EHIP, "make_weight sync: %s", hipGetErrorString(e));
+    return rc;
+}
+
+// Rows of several host weights concatenated (same dtype and k) into one
+// device weight: row-major [out][in] blocks concatenate byte-wise.
+int make_concat(int dtype, const std::vector<int64_t>& ns, int64_t k, const std::vector<const void*>& hosts,
+                uint64_t seed, hipStream_t s, aeth_weight** out) {
+    int be, bb;
+    int rc = aeth_block_geometry(dtype, &be, &bb);
+    if (rc) return rc;
+    int64_t rowb = aeth_blocks_per_row(dtype, k) * bb, ntot = 0;
+    for (auto n : ns) ntot += n;
+    bool any_host = false, all_host = true;
+    for (auto h : hosts) { any_host |= h != nullptr; all_host &= h != nullptr; }
+    if (any_host && !all_host) return aeth_set_error(AETH_EINVAL, "runner: partial host weights for a fused group");
+    if (!all_host) return make_weight(dtype, ntot, k, nullptr, seed, s, out);
+    std::vector<uint8_t> cat((size_t)(ntot * rowb));
+    size_t off = 0;
+    for (size_t i = 0; i < ns.size(); i++) {
+        memcpy(cat.data() + off, hosts[i], (size_t)(ns[i] * rowb));
+        off += (size_t)(ns[i] * rowb);
+    }
+    return aeth_weight_create(dtype, ntot, k, cat.data(), 0, s, out);
+}
+
+template <typename T>
+int dmalloc(T** p, int64_t count) {
+    AETH_HIP_CHECK(hipMalloc((void**)p, sizeof(T) * (size_t)(count > 0 ? count : 1)));
+    return AETH_OK;
+}
+
+uint64_t mix(uint64_t seed, uint64_t a, uint64_t b) {
+    uint64_t z = seed ^ (a * 0x9E3779B97F4A7C15ull) ^ (b * 0xC2B2AE3D27D4EB4Full);
+    z = (z ^ (z >> 31)) * 0xBF58476D1CE4E5B9ull;
+    return z ^ (z >> 29);
+}
+
+void runner_release(aeth_runner* r) {
+    if (!r) return;
+    if (r->graph) hipGraphExecDestroy(r->graph);
+    for (auto* w : r->wqkv) aeth_weight_free(w);
+    for (auto* w : r->wo) aeth_weight_free(w);
+    for (auto* w : r->wgu) aeth_weight_free(w);
+    for (auto* w : r->wdown) aeth_weight_free(w);
+    aeth_weight_free(r->lm_head);
+    void* bufs[] = {r->norms, r->final_norm, r->emb, r->rope_sin, r->rope_cos, r->kv, r->x, r->normed, r->qkv,
+                    r->attn, r->gu, r->logits, r->attn_ws, r->am_ws, r->st, r->tok_out};
+    for (void* b : bufs)
+        if (b) hipFree(b);
+    if (r->stream) hipStreamDestroy(r->stream);
+    delete r;
+}
+
+// Enqueues one decode step on r->stream, reading {token, pos, fill} from
+// r->st; layers [l0, l1) only when partial (frame budget), the final norm,
+// LM head and argmax only when l1 == num_layers.
+int enqueue_layers(aeth_runner* r, int l0, int l1) {
+    const aeth_llama_config& c = r->cfg;
+    hipStream_t s = r->stream;
+    const int64_t d = c.d_model, hd = c.head_dim, nh = c.num_heads, nkv = c.num_kv_heads;
+    const int64_t qd = nh * hd, kvd = kKvd(c), dff = c.d_ff;
+    int rc;
+    for (int l = l0; l < l1; l++) {
+        float* lkv = r->kv + (int64_t)l * kv_layer_floats(c);
+        if ((rc = aeth_rmsnorm_launch(r->x, r->norms + (int64_t)l * 2 * d, 1, d, c.rms_norm_eps, r->normed, s)))
+            return rc;
+        if ((rc = aeth_qmatmul(r->wqkv[l], r->normed, 1, r->qkv, 0, s))) return rc;
+        // q and k are adjacent in qkv: one rotate-half pass over nh + nkv heads
+        if ((rc = aeth_rope_launch(r->qkv, nh + nkv, hd, r->st + 1, 0, r->rope_sin, r->rope_cos, c.max_seq_len, s)))
+            return rc;
+        if ((rc = aeth_kv_append_launch(lkv, r->qkv + qd, r->qkv + qd + kvd, nkv, hd, c.max_seq_len, r->st + 2, 0, s)))
+            return rc;
+        if ((rc = aeth_attn_decode_launch(r->qkv, lkv, nh, nkv, hd, c.max_seq_len, r->st + 2, 0, 1, r->attn_ws,
+                                          r->attn, s)))
+            return rc;
+        if ((rc = aeth_qmatmul(r->wo[l], r->attn, 1, r->x, AETH_MM_ACCUMULATE, s))) return rc;
+        if ((rc = aeth_rmsnorm_launch(r->x, r->norms + (int64_t)l * 2 * d + d, 1, d, c.rms_norm_eps, r->normed, s)))
+            return rc;
+        if ((rc = aeth_qmatmul(r->wgu[l], r->normed, 1, r->gu, 0, s))) return rc;
+        if ((rc = aeth_silu_mul_launch(r->gu, r->gu + dff, dff, s))) return rc;
+        if ((rc = aeth_qmatmul(r->wdown[l], r->gu, 1, r->x, AETH_MM_ACCUMULATE, s))) return rc;
+    }
+    return AETH_OK;
+}
+
+int enqueue_head(aeth_runner* r) {
+    const aeth_llama_config& c = r->cfg;
+    hipStream_t s = r->stream;
+    int rc;
+    // kv.advance() precedes the final norm in the reference (runner.rs:1639);
+    // state_advance runs after the argmax because nothing below reads the fill.
+    if ((rc = aeth_rmsnorm_launch(r->x, r->final_norm, 1, c.d_model, c.rms_norm_eps, r->normed, s))) return rc;
+    if ((rc = aeth_qmatmul(r->lm_head, r->normed, 1, r->logits, 0, s))) return rc;
+    if ((rc = aeth_argmax_launch(r->logits, c.vocab_size, r->tok_out, r->st, r->am_ws, s))) return rc;
+    return aeth_state_advance_launch(r->st, c.max_seq_len, s);
+}
+
+int enqueue_step(aeth_runner* r) {
+    int rc = aeth_embed_launch(r->emb, r->st, 0, r->cfg.d_model, r->cfg.vocab_size, r->x, r->stream);
+    if (rc) return rc;
+    if ((rc = enqueue_layers(r, 0, r->cfg.num_layers))) return rc;
+    return enqueue_head(r);
+}
+
+int set_state(aeth_runner* r, int token, int pos) {
+    int h[3] = {token, pos, r->fill};
+    AETH_HIP_CHECK(hipMemcpyAsync(r->st, h, sizeof(h), hipMemcpyHostToDevice, r->stream));
+    return AETH_OK;
+}
+
+int check_step_args(aeth_runner* r, int token, int pos) {
+    if (token < 0 || token >= r->cfg.vocab_size)
+        return aeth_set_error(AETH_EINVAL, "decode: token %d out of range [0, %d)", token, r->cfg.vocab_size);
+    if (pos < 0) return aeth_set_error(AETH_EINVAL, "decode: negative pos");
+    if (r->fill >= r->cfg.max_seq_len)
+        return aeth_set_error(AETH_ESTATE, "decode: KV cache full (%d positions)", r->cfg.max_seq_len);
+    return AETH_OK;
+}
+
+}  // namespace
+
+extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const void* const* layer_weights,
+                                           const int32_t* layer_dtypes, const float* const* norms,
+                                           const float* final_norm, const void* lm_head, int32_t lm_dtype,
+                                           const float* embeddings, uint64_t seed, aeth_runner** out) {
+    if (!cfg || !out || !layer_dtypes) return aeth_set_error(AETH_EINVAL, "aeth_runner_create: NULL argument");
+    *out = nullptr;
+    const aeth_llama_config& c = *cfg;
+    if (c.num_layers <= 0 || c.d_model <= 0 || c.num_heads <= 0 || c.num_kv_heads <= 0 || c.head_dim <= 0 ||
+        c.d_ff <= 0 || c.vocab_size <= 0 || c.max_seq_len <= 0 || c.num_heads % c.num_kv_heads != 0 ||
+        c.head_dim % 2 != 0)
+        return aeth_set_error(AETH_EINVAL, "aeth_runner_create: invalid config");
+    bool need_seed = !lm_head || !embeddings || !final_norm || !layer_weights || !norms;
+    if (need_seed && seed == 0)
+        return aeth_set_error(AETH_EINVAL, "aeth_runner_create: missing tensors need a nonzero synthetic_seed");
+    aeth_runner* r = new aeth_runner();
+    r->cfg = c;
+    int rc = AETH_OK;
+#define RC(expr)                        \
+    do {                                \
+        if ((rc = (expr)) != AETH_OK) { \
+            runner_release(r);          \
+            return rc;                  \
+        }                               \
+    } while (0)
+    if (hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete r;
+        return aeth_set_error(AETH_EHIP, "aeth_runner_create: stream creation failed");
+    }
+    hipStream_t s = r->stream;
+    (void)aeth_num_cus();  // cache the device query outside any graph capture
+    const int64_t d = c.d_model, qd = (int64_t)c.num_heads * c.head_dim, kvd = kKvd(c), dff = c.d_ff;
+    r->dtypes.assign(layer_dtypes, layer_dtypes + (size_t)c.num_layers * 7);
+    for (int l = 0; l < c.num_layers; l++) {
+        const int32_t* T = layer_dtypes + (size_t)l * 7;
+        const void* const* W = layer_weights ? layer_weights + (size_t)l * 7 : nullptr;
+        auto hw = [&](int j) -> const void* { return W ? W[j] : nullptr; };
+        aeth_weight* w = nullptr;
+        if (T[0] != T[1] || T[0] != T[2] || T[4] != T[5]) {
+            runner_release(r);
+            return aeth_set_error(AETH_EUNSUPPORTED, "runner: q/k/v and gate/up must share a dtype per layer");
+        }
+        RC(make_concat(T[0], {qd, kvd, kvd}, d, {hw(0), hw(1), hw(2)}, mix(seed, l, 1), s, &w));
+        r->wqkv.push_back(w);
+        RC(make_weight(T[3], d, qd, hw(3), mix(seed, l, 4), s, &w));
+        r->wo.push_back(w);
+        RC(make_concat(T[4], {dff, dff}, d, {hw(4), hw(5)}, mix(seed, l, 5), s, &w));
+        r->wgu.push_back(w);
+        RC(make_weight(T[6], d, dff, hw(6), mix(seed, l, 7), s, &w));
+        r->wdown.push_back(w);
+    }
+    RC(make_weight(lm_dtype, c.vocab_size, d, lm_head, mix(seed, 1000003, 9), s, &r->lm_head));
+    RC(dmalloc(&r->norms, (int64_t)c.num_layers * 2 * d));
+    RC(dmalloc(&r->final_norm, d));
+    RC(dmalloc(&r->emb, (int64_t)c.vocab_size * d));
+    if (norms) {
+        for (int l = 0; l < c.num_layers; l++)
+            for (int j = 0; j < 2; j++)
+                if (hipMemcpy(r->norms + ((int64_t)l * 2 + j) * d, norms[l * 2 + j], sizeof(float) * d,
+                              hipMemcpyHostToDevice) != hipSuccess) {
+                    runner_release(r);
+                    return aeth_set_error(AETH_EHIP, "runner: norm upload failed");
+                }
+    } else {
+        RC(aeth_fill_normal_f32(mix(seed, 2, 2), r->norms, (int64_t)c.num_layers * 2 * d, 1.0f, 0.02f, s));
+    }
+    if (final_norm) {
+        if (hipMemcpy(r->final_norm, final_norm, sizeof(float) * d, hipMemcpyHostToDevice) != hipSuccess) {
+            runner_release(r);
+            return aeth_set_error(AETH_EHIP, "runner: final norm upload failed");
+        }
+    } else {
+        RC(aeth_fill_normal_f32(mix(seed, 3, 3), r->final_norm, d, 1.0f, 0.02f, s));
+    }
+    if (embeddings) {
+        if (hipMemcpy(r->emb, embeddings, sizeof(float) * (size_t)c.vocab_size * d, hipMemcpyHostToDevice) !=
+            hipSuccess) {
+            runner_release(r);
+            return aeth_set_error(AETH_EHIP, "runner: embedding upload failed");
+        }
+    } else {
+        RC(aeth_fill_normal_f32(mix(seed, 4, 4), r->emb, (int64_t)c.vocab_size * d, 0.0f, 1.0f, s));
+    }
+    std::vector<float> rs, rcs;
+    precompute_rope(c.max_seq_len, c.head_dim, c.rope_base, rs, rcs);
+    RC(dmalloc(&r->rope_sin, (int64_t)rs.size()));
+    RC(dmalloc(&r->rope_cos, (int64_t)rcs.size()));
+    if (hipMemcpy(r->rope_sin, rs.data(), rs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(r->rope_cos, rcs.data(), rcs.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        runner_release(r);
+        return aeth_set_error(AETH_EHIP, "runner: rope upload failed");
+    }
+    RC(dmalloc(&r->kv, (int64_t)c.num_layers * kv_layer_floats(c)));
+    if (hipMemsetAsync(r->kv, 0, sizeof(float) * (size_t)c.num_layers * kv_layer_floats(c), s) != hipSuccess) {
+        runner_release(r);
+        return aeth_set_error(AETH_EHIP, "runner: kv clear failed");
+    }
+    RC(dmalloc(&r->x, d));
+    RC(dmalloc(&r->normed, d > dff ? d : dff));
+    RC(dmalloc(&r->qkv, qd + 2 * kvd));
+    RC(dmalloc(&r->attn, qd));
+    RC(dmalloc(&r->gu, 2 * dff));
+    RC(dmalloc(&r->logits, c.vocab_size));
+    RC(dmalloc(&r->attn_ws, aeth_attn_ws_floats(c.num_heads, c.head_dim, c.max_seq_len)));
+    RC(dmalloc((uint8_t**)&r->am_ws, aeth_argmax_ws_bytes()));
+    RC(dmalloc(&r->st, 4));
+    RC(dmalloc(&r->tok_out, 4));
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        runner_release(r);
+        return aeth_set_error(AETH_EHIP, "runner: setup sync failed");
+    }
+#undef RC
+    *out = r;
+    return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_runner_free(aeth_runner* r) {
+    runner_release(r);
+    return AETH_OK;
+}
+
+extern "C" AETH_API void* aeth_runner_stream(const aeth_runner* r) { return r ? (void*)r->stream : nullptr; }
+
+extern "C" AETH_API int aeth_runner_seq_len(const aeth_runner* r) { return r ? r->fill : -1; }
+
+extern "C" AETH_API int aeth_runner_fill_kv(aeth_runner* r, uint64_t seed, int32_t seq_len) {
+    if (!r || seq_len < 0 || seq_len > r->cfg.max_seq_len)
+        return aeth_set_error(AETH_EINVAL, "aeth_runner_fill_kv: bad argument");
+    std::lock_guard<std::mutex> lk(r->mu);
+    const aeth_llama_config& c = r->cfg;
+    // N(0,1) over the whole storage, then the unfilled tail cleared per head.
+    int64_t tot = (int64_t)c.num_layers * kv_layer_floats(c);
+    int rc = aeth_fill_normal_f32(seed, r->kv, tot, 0.0f, 1.0f, r->stream);
+    if (rc) return rc;
+    int64_t rows = (int64_t)c.num_layers * 2 * c.num_kv_heads;
+    int64_t tail = (int64_t)(c.max_seq_len - seq_len) * c.head_dim;
+    if (tail > 0)
+        for (int64_t i = 0; i < rows; i++)
+            AETH_HIP_CHECK(hipMemsetAsync(r->kv + i * c.max_seq_len * c.head_dim + (int64_t)seq_len * c.head_dim, 0,
+                                          sizeof(float) * tail, r->stream));
+    AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
+    r->fill = seq_len;
+    r->partial_valid = false;
+    return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_runner_kv_to_host(aeth_runner* r, float* host, int32_t* seq_len) {
+    if (!r || !host) return aeth_set_error(AETH_EINVAL, "aeth_runner_kv_to_host: NULL");
+    std::lock_guard<std::mutex> lk(r->mu);
+    int64_t tot = (int64_t)r->cfg.num_layers * kv_layer_floats(r->cfg);
+    AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
+    AETH_HIP_CHECK(hipMemcpy(host, r->kv, sizeof(float) * tot, hipMemcpyDeviceToHost));
+    if (seq_len) *seq_len = r->fill;
+    return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_runner_kv_from_host(aeth_runner* r, const float* host, int32_t seq_len) {
+    if (!r || !host || seq_len < 0 || seq_len > r->cfg.max_seq_len)
+        return aeth_set_error(AETH_EINVAL, "aeth_runner_kv_from_host: bad argument");
+    std::lock_guard<std::mutex> lk(r->mu);
+    int64_t tot = (int64_t)r->cfg.num_layers * kv_layer_floats(r->cfg);
+    AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
+    AETH_HIP_CHECK(hipMemcpy(r->kv, host, sizeof(float) * tot, hipMemcpyHostToDevice));
+    r->fill = seq_len;
+    r->partial_valid = false;
+    return AETH_OK;
+}
+
+static int runner_decode_locked(aeth_runner* r, int32_t token, int32_t pos, float* logits, int32_t* next_token) {
+    int rc = check_step_args(r, token, pos);
+    if (rc) return rc;
+    r->partial_valid = false;
+    if ((rc = set_state(r, token, pos))) return rc;
+    if ((rc = enqueue_step(r))) return rc;
+    if (logits)
+        AETH_HIP_CHECK(hipMemcpyAsync(logits, r->logits, sizeof(float) * r->cfg.vocab_size, hipMemcpyDeviceToHost,
+                                      r->stream));
+    int tok = 0;
+    AETH_HIP_CHECK(hipMemcpyAsync(&tok, r->tok_out, sizeof(int), hipMemcpyDeviceToHost, r->stream));
+    AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
+    if (r->fill < r->cfg.max_seq_len) r->fill++;
+    if (next_token) *next_token = tok;
+    return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_runner_decode(aeth_runner* r, int32_t token, int32_t pos, float* logits,
+                                           int32_t* next_token) {
+    if (!r) return aeth_set_error(AETH_EINVAL, "aeth_runner_decode: NULL runner");
+    std::lock_guard<std::mutex> lk(r->mu);
+    return runner_decode_locked(r, token, pos, logits, next_token);
+}
+
+extern "C" AETH_API int aeth_runner_generate(aeth_runner* r, int32_t token, int32_t pos, int32_t n_steps,
+                                             int32_t* tokens, int use_graph) {
+    if (!r || n_steps < 0 || (n_steps > 0 && !tokens))
+        return aeth_set_error(AETH_EINVAL, "aeth_runner_generate: bad argument");
+    std::lock_guard<std::mutex> lk(r->mu);
+    int rc = check_step_args(r, token, pos);
+    if (rc) return rc;
+    if (r->fill + n_steps > r->cfg.max_seq_len)
+        return aeth_set_error(AETH_ESTATE, "generate: %d steps overflow the KV cache (%d of %d used)", n_steps, r->fill,
+                              r->cfg.max_seq_len);
+    r->partial_valid = false;
+    if ((rc = set_state(r, token, pos))) return rc;
+    if (use_graph && !r->graph) {
+        hipGraph_t g = nullptr;
+        AETH_HIP_CHECK(hipStreamBeginCapture(r->stream, hipStreamCaptureModeThreadLocal));
+        rc = enqueue_step(r);
+        hipError_t e = hipStreamEndCapture(r->stream, &g);
+        if (rc) {
+            if (g) hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return aeth_set_error(AETH_EHIP, "graph capture failed: %s", hipGetErrorString(e));
+        e = hipGraphInstantiate(&r->graph, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            r->graph = nullptr;
+            return aeth_set_error(AETH_EHIP, "graph instantiate failed: %s", hipGetErrorString(e));
+        }
+    }
+    for (int i = 0; i < n_steps; i++) {
+        if (use_graph) AETH_HIP_CHECK(hipGraphLaunch(r->graph, r->stream));
+        else if ((rc = enqueue_step(r))) return rc;
+        AETH_HIP_CHECK(hipMemcpyAsync(tokens + i, r->tok_out, sizeof(int), hipMemcpyDeviceToHost, r->stream));
+    }
+    AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
+    r->fill += n_steps;
+    return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_runner_export(const aeth_runner* r, int which, int32_t l, void* host, int64_t host_bytes) {
+    if (!r || !host) return aeth_set_error(AETH_EINVAL, "aeth_runner_export: NULL");
+    const aeth_llama_config& c = r->cfg;
+    const int64_t d = c.d_model, qd = (int64_t)c.num_heads * c.head_dim, kvd = kKvd(c), dff = c.d_ff;
+    AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
+    if (which >= 0 && which <= 6) {
+        if (l < 0 || l >= c.num_layers) return aeth_set_error(AETH_EINVAL, "export: layer out of range");
+        const aeth_weight* w = which <= 2 ? r->wqkv[l] : which == 3 ? r->wo[l] : which <= 5 ? r->wgu[l] : r->wdown[l];
+        std::vector<uint8_t> all((size_t)w->bytes);
+        int rc = aeth_weight_export_raw(w, all.data(), 0, r->stream);
+        if (rc) return rc;
+        int64_t rowb = w->bytes / w->n, r0 = 0, nr = w->n;
+        if (which == 0) { r0 = 0; nr = qd; }
+        else if (which == 1) { r0 = qd; nr = kvd; }
+        else if (which == 2) { r0 = qd + kvd; nr = kvd; }
+        else if (which == 4) { r0 = 0; nr = dff; }
+        else if (which == 5) { r0 = dff; nr = dff; }
+        if (host_bytes < nr * rowb) return aeth_set_error(AETH_EINVAL, "export: buffer too small");
+        memcpy(host, all.data() + r0 * rowb, (size_t)(nr * rowb));
+        return AETH_OK;
+    }
+    const void* src = nullptr;
+    int64_t bytes = 0;
+    switch (which) {
+        case 7: src = r->norms + (int64_t)l * 2 * d; bytes = d * 4; break;
+        case 8: src = r->norms + (int64_t)l * 2 * d + d; bytes = d * 4; break;
+        case 9: src = r->final_norm; bytes = d * 4; break;
+        case 10: {
+            if (host_bytes < r->lm_head->bytes) return aeth_set_error(AETH_EINVAL, "export: buffer too small");
+            return aeth_weight_export_raw(r->lm_head, host, 0, r->stream);
+        }
+        case 11:
+            if (l < 0 || l >= c.vocab_size) return aeth_set_error(AETH_EINVAL, "export: token out of range");
+            src = r->emb + (int64_t)l * d; bytes = d * 4; break;
+        case 12: src = r->rope_sin; bytes = (int64_t)c.max_seq_len * (c.head_dim / 2) * 4; break;
+        case 13: src = r->rope_cos; bytes = (int64_t)c.max_seq_len * (c.head_dim / 2) * 4; break;
+        default: return aeth_set_error(AETH_EINVAL, "export: unknown tensor %d", which);
+    }
+    if (host_bytes < bytes) return aeth_set_error(AETH_EINVAL, "export: buffer too small");
+    AETH_HIP_CHECK(hipMemcpy(host, src, (size_t)bytes, hipMemcpyDeviceToHost));
+    return AETH_OK;
+}
+
+// ── aether.h C ABI (src/c_api.rs) over the device runner ─────────────────
+
+struct aether_model {
+    aeth_runner* runner;
+    float frame_budget_ms;
+};
+
+extern "C" AETHER_API aether_model* aether_model_from_runner(aeth_runner* r) {
+    if (!r) return nullptr;
+    return new aether_model{r, 0.0f};
+}
+
+// GGUF file loading (gguf.rs:297-397) is not part of this build: the two
+// loaders report that through aether_last_error and return NULL.
+extern "C" AETHER_API aether_model* aether_load(const char* path) {
+    aeth_set_error(AETH_EUNSUPPORTED, "aether_load(%s): GGUF file loading is not built; use aeth_runner_create",
+                   path ? path : "(null)");
+    return nullptr;
+}
+
+extern "C" AETHER_API aether_model* aether_load_streaming(const char* path, int max_hot) {
+    (void)max_hot;
+    return aether_load(path);
+}
+
+extern "C" AETHER_API void aether_free(aether_model* m) {
+    if (!m) return;
+    aeth_runner_free(m->runner);
+    delete m;
+}
+
+extern "C" AETHER_API int aether_vocab_size(const aether_model* m) { return m ? m->runner->cfg.vocab_size : 0; }
+extern "C" AETHER_API int aether_context_len(const aether_model* m) { return m ? m->runner->cfg.max_seq_len : 0; }
+extern "C" AETHER_API int aether_num_layers(const aether_model* m) { return m ? m->runner->cfg.num_layers : 0; }
+extern "C" AETHER_API int aether_d_model(const aether_model* m) { return m ? m->runner->cfg.d_model : 0; }
+// Synthetic models carry no tokenizer metadata: the conventional LLaMA ids.
+extern "C" AETHER_API int aether_eos_id(const aether_model* m) { return m ? 2 : -1; }
+extern "C" AETHER_API int aether_bos_id(const aether_model* m) { return m ? 1 : -1; }
+extern "C" AETHER_API int aether_num_gpu_layers(const aether_model* m) { return m ? m->runner->cfg.num_layers : 0; }
+extern "C" AETHER_API int aether_num_cpu_layers(const aether_model* m) { return m ? 0 : 0; }
+
+extern "C" AETHER_API void aether_set_frame_budget(aether_model* m, float max_ms) {
+    if (m) m->frame_budget_ms = max_ms;
+}
+extern "C" AETHER_API float aether_frame_budget(const aether_model* m) { return m ? m->frame_budget_ms : 0.0f; }
+
+// Tokenization needs GGUF tokenizer metadata, which synthetic models lack.
+extern "C" AETHER_API int* aether_encode(const aether_model* m, const char* text, int* out_len) {
+    (void)m;
+    (void)text;
+    if (out_len) *out_len = 0;
+    aeth_set_error(AETH_EUNSUPPORTED, "aether_encode: no tokenizer in this build");
+    return nullptr;
+}
+extern "C" AETHER_API char* aether_decode_token(const aether_model* m, int token) {
+    (void)m;
+    (void)token;
+    aeth_set_error(AETH_EUNSUPPORTED, "aether_decode_token: no tokenizer in this build");
+    return nullptr;
+}
+extern "C" AETHER_API void aether_free_string(char* s) { free(s); }
+extern "C" AETHER_API void aether_free_tokens(int* t) { free(t); }
+
+// aether_prefill (c_api.rs:257-278 → LlamaRunner::prefill, runner.rs:695):
+// the cache restarts at 0 and token i is placed at position i; the logits
+// of the last token are returned.
+extern "C" AETHER_API int aether_prefill(aether_model* m, const int* tokens, int n_tokens, float* logits_out) {
+    if (!m || !tokens || n_tokens <= 0 || !logits_out) return AETHER_ERR;
+    aeth_runner* r = m->runner;
+    std::lock_guard<std::mutex> lk(r->mu);
+    if (n_tokens > r->cfg.max_seq_len) {
+        aeth_set_error(AETH_EINVAL, "prefill: %d tokens exceed max_seq %d", n_tokens, r->cfg.max_seq_len);
+        return AETHER_ERR;
+    }
+    r->fill = 0;
+    for (int i = 0; i < n_tokens; i++) {
+        if (runner_decode_locked(r, tokens[i], i, i == n_tokens - 1 ? logits_out : nullptr, nullptr)) return AETHER_ERR;
+    }
+    return AETHER_OK;
+}
+
+extern "C" AETHER_API int aether_decode(aether_model* m, int token, int pos, float* logits_out) {
+    if (!m || !logits_out) return AETHER_ERR;
+    return aeth_runner_decode(m->runner, token, pos, logits_out, nullptr) == AETH_OK ? AETHER_OK : AETHER_ERR;
+}
+
+// aether_decode_budgeted (c_api.rs:324-355, runner.rs:1201-1282): the
+// deadline is checked before each layer; on expiry the layers done so far
+// are kept (x stays on the device) and AETHER_TIMEOUT is returned without
+// logits; a retry with the same (token, pos) resumes after the last
+// completed layer. The resume index follows the reference exactly,
+// including its saturating_sub: a budget that expires before layer 0
+// records completed_layer = 0 and the retry starts at layer 1.
+extern "C" AETHER_API int aether_decode_budgeted(aether_model* m, int token, int pos, float* logits_out) {
+    if (!m || !logits_out) return AETHER_ERR;
+    aeth_runner* r = m->runner;
+    std::lock_guard<std::mutex> lk(r->mu);
+    if (m->frame_budget_ms <= 0.0f) {
+        return runner_decode_locked(r, token, pos, logits_out, nullptr) == AETH_OK ? AETHER_OK : AETHER_ERR;
+    }
+    if (check_step_args(r, token, pos)) return AETHER_ERR;
+    int start = 0;
+    if (r->partial_valid && r->partial_token == token && r->partial_pos == pos) {
+        start = r->partial_layer + 1;
+    } else {
+        r->partial_valid = false;
+        if (set_state(r, token, pos)) return AETHER_ERR;
+        if (aeth_embed_launch(r->emb, r->st, 0, r->cfg.d_model, r->cfg.vocab_size, r->x, r->stream)) return AETHER_ERR;
+    }
+    auto deadline = std::chrono::steady_clock::now() +
+                    std::chrono::duration_cast<std::chrono::steady_clock::duration>(
+                        std::chrono::duration<double, std::milli>(m->frame_budget_ms));
+    for (int l = start; l < r->cfg.num_layers; l++) {
+        if (std::chrono::steady_clock::now() >= deadline) {
+            if (hipStreamSynchronize(r->stream) != hipSuccess) return AETHER_ERR;
+            r->partial_valid = true;
+            r->partial_token = token;
+            r->partial_pos = pos;
+            r->partial_layer = l > 0 ? l - 1 : 0;
+            return AETHER_TIMEOUT;
+        }
+        if (enqueue_layers(r, l, l + 1)) return AETHER_ERR;
+        if (hipStreamSynchronize(r->stream) != hipSuccess) return AETHER_ERR;
+    }
+    r->partial_valid = false;
+    if (enqueue_head(r)) return AETHER_ERR;
+    if (hipMemcpyAsync(logits_out, r->logits, sizeof(float) * r->cfg.vocab_size, hipMemcpyDeviceToHost, r->stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(r->stream) != hipSuccess)
+        return AETHER_ERR;
+    if (r->fill < r->cfg.max_seq_len) r->fill++;
+    return AETHER_OK;
+}
+
+// Greedy only (temperature ≤ 1e-6, runner.rs:1946-1973); stochastic
+// sampling is not on the measured path.
+extern "C" AETHER_API int aether_sample(const aether_model* m, const float* logits, float temperature, float top_p) {
+    if (!m || !logits) return -1;
+    if (temperature > 1e-6f && top_p > 1e-6f) {
+        aeth_set_error(AETH_EUNSUPPORTED, "aether_sample: only greedy sampling is built");
+        return -1;
+    }
+    return aether_argmax(m, logits);
+}
+
+extern "C" AETHER_API int aether_argmax(const aether_model* m, const float* logits) {
+    if (!m || !logits) return -1;
+    int n = m->runner->cfg.vocab_size, best = 0;
+    for (int i = 1; i < n; i++)
+        if (!(logits[i] < logits[best])) best = i;
+    return best;
+}
+
+extern "C" AETHER_API char* aether_last_error(void) {
+    const char* e = aeth_last_error();
+    size_t len = strlen(e);
+    char* s = (char*)malloc(len + 1);
+    if (s) memcpy(s, e, len + 1);
+    return s;
+}

@@ -1,0 +1,297 @@
+// Runtime state, error reporting, device-resident weights (planar re-layout
+// of GGUF blocks) and the seeded synthetic-input generators.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "aeth_common.hpp"
+#include "aeth_internal.hpp"
+
+static thread_local char g_err[1024];
+
+int aeth_set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+extern "C" AETH_API const char* aeth_last_error(void) { return g_err; }
+
+static int g_num_cus[64];
+
+int aeth_num_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (g_num_cus[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        g_num_cus[dev] = v;
+    }
+    return g_num_cus[dev];
+}
+
+extern "C" AETH_API int aeth_init(int device) {
+    int count = 0;
+    AETH_HIP_CHECK(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count)
+        return aeth_set_error(AETH_EINVAL, "aeth_init: device %d out of range (%d devices)", device, count);
+    AETH_HIP_CHECK(hipSetDevice(device));
+    (void)aeth_num_cus();
+    return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_block_geometry(int dtype, int* block_elems, int* block_bytes) {
+    int e, b;
+    switch (dtype) {
+        case AETH_DTYPE_Q8_0: e = Q8_BLOCK_ELEMS; b = Q8_BLOCK_BYTES; break;
+        case AETH_DTYPE_Q4_K: e = QK_BLOCK_ELEMS; b = Q4K_BLOCK_BYTES; break;
+        case AETH_DTYPE_Q6_K: e = QK_BLOCK_ELEMS; b = Q6K_BLOCK_BYTES; break;
+        default: return aeth_set_error(AETH_EUNSUPPORTED, "unsupported dtype %d", dtype);
+    }
+    if (block_elems) *block_elems = e;
+    if (block_bytes) *block_bytes = b;
+    return AETH_OK;
+}
+
+// Blocks per row as the reference counts them: Q8_0 rows hold ceil(k/32)
+// blocks (q8_0.rs:16, requantize_q8_0); K-quant kernels read k/256 blocks
+// (avx2.rs:26, q4_k.rs:16).
+int64_t aeth_blocks_per_row(int dtype, int64_t k) {
+    if (dtype == AETH_DTYPE_Q8_0) return (k + 31) / 32;
+    return k / 256;
+}
+
+// ── planar layout ────────────────────────────────────────────────────────
+// Q4_K: p0 = hdr[nblk][16] (d, dmin, scales[12]), p1 = qs[nblk][128]
+// Q6_K: p0 = ql[nblk][128], p1 = qh[nblk][64], p2 = sc[nblk][16], p3 = d[nblk] (u16)
+// Q8_0: p0 = qs[nblk][32], p1 = d[nblk] (u16)
+// Block index = row * blocks_per_row + b, so each row's fields are contiguous.
+
+static int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+__global__ void k_relayout(int dtype, uint8_t* __restrict__ raw, uint8_t* __restrict__ p0,
+                           uint8_t* __restrict__ p1, uint8_t* __restrict__ p2, uint8_t* __restrict__ p3,
+                           int64_t total_bytes, int to_planar) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total_bytes) return;
+    uint8_t* dst;
+    if (dtype == AETH_DTYPE_Q4_K) {
+        int64_t blk = i / Q4K_BLOCK_BYTES;
+        int off = (int)(i - blk * Q4K_BLOCK_BYTES);
+        dst = off < 16 ? p0 + blk * 16 + off : p1 + blk * 128 + (off - 16);
+    } else if (dtype == AETH_DTYPE_Q6_K) {
+        int64_t blk = i / Q6K_BLOCK_BYTES;
+        int off = (int)(i - blk * Q6K_BLOCK_BYTES);
+        if (off < 128) dst = p0 + blk * 128 + off;
+        else if (off < 192) dst = p1 + blk * 64 + (off - 128);
+        else if (off < 208) dst = p2 + blk * 16 + (off - 192);
+        else dst = p3 + blk * 2 + (off - 208);
+    } else {
+        int64_t blk = i / Q8_BLOCK_BYTES;
+        int off = (int)(i - blk * Q8_BLOCK_BYTES);
+        dst = off < 2 ? p1 + blk * 2 + off : p0 + blk * 32 + (off - 2);
+    }
+    if (to_planar) *dst = raw[i];
+    else raw[i] = *dst;
+}
+
+static int relayout(aeth_weight* w, uint8_t* d_raw, int to_planar, hipStream_t s) {
+    int64_t total = w->nblk * w->block_bytes;
+    if (total == 0) return AETH_OK;
+    int64_t grid = aeth_cdiv(total, 256);
+    hipLaunchKernelGGL(k_relayout, dim3((unsigned)grid), dim3(256), 0, s, w->dtype, d_raw, w->p0, w->p1, w->p2,
+                       w->p3, total, to_planar);
+    AETH_LAUNCH_CHECK();
+    return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, const void* raw, int raw_is_device,
+                                           void* stream, aeth_weight** out) {
+    if (!out) return aeth_set_error(AETH_EINVAL, "aeth_weight_create: out is NULL");
+    *out = nullptr;
+    int be, bb;
+    int rc = aeth_block_geometry(dtype, &be, &bb);
+    if (rc) return rc;
+    if (n <= 0 || k <= 0) return aeth_set_error(AETH_EINVAL, "aeth_weight_create: bad shape n=%lld k=%lld",
+                                                (long long)n, (long long)k);
+    if (dtype != AETH_DTYPE_Q8_0 && k < 256)
+        return aeth_set_error(AETH_EINVAL, "aeth_weight_create: K-quant needs k >= 256 (k=%lld)", (long long)k);
+    if (!raw) return aeth_set_error(AETH_EINVAL, "aeth_weight_create: raw is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    aeth_weight* w = new aeth_weight();
+    w->dtype = dtype;
+    w->n = n;
+    w->k = k;
+    w->nb = aeth_blocks_per_row(dtype, k);
+    w->nblk = n * w->nb;
+    w->block_bytes = bb;
+    int64_t sz[4] = {0, 0, 0, 0};
+    if (dtype == AETH_DTYPE_Q4_K) { sz[0] = w->nblk * 16; sz[1] = w->nblk * 128; }
+    else if (dtype == AETH_DTYPE_Q6_K) { sz[0] = w->nblk * 128; sz[1] = w->nblk * 64; sz[2] = w->nblk * 16; sz[3] = w->nblk * 2; }
+    else { sz[0] = w->nblk * 32; sz[1] = w->nblk * 2; }
+    int64_t off[4], tot = 0;
+    for (int i = 0; i < 4; i++) { off[i] = tot; tot += align256(sz[i]); }
+    w->bytes = w->nblk * bb;
+    hipError_t e = hipMalloc((void**)&w->base, (size_t)(tot > 0 ? tot : 256));
+    if (e != hipSuccess) {
+        delete w;
+        return aeth_set_error(AETH_ENOMEM, "aeth_weight_create: hipMalloc(%lld) failed: %s", (long long)tot,
+                              hipGetErrorString(e));
+    }
+    w->p0 = w->base + off[0];
+    w->p1 = w->base + off[1];
+    w->p2 = sz[2] ? w->base + off[2] : nullptr;
+    w->p3 = sz[3] ? w->base + off[3] : nullptr;
+    uint8_t* staging = nullptr;
+    if (raw_is_device) {
+        staging = (uint8_t*)raw;
+    } else {
+        e = hipMalloc((void**)&staging, (size_t)w->bytes);
+        if (e != hipSuccess) {
+            hipFree(w->base);
+            delete w;
+            return aeth_set_error(AETH_ENOMEM, "aeth_weight_create: staging hipMalloc failed: %s",
+                                  hipGetErrorString(e));
+        }
+        e = hipMemcpyAsync(staging, raw, (size_t)w->bytes, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) {
+            hipFree(staging);
+            hipFree(w->base);
+            delete w;
+            return aeth_set_error(AETH_EHIP, "aeth_weight_create: H2D copy failed: %s", hipGetErrorString(e));
+        }
+    }
+    rc = relayout(w, staging, 1, s);
+    if (!raw_is_device) {
+        hipError_t e2 = hipStreamSynchronize(s);
+        hipFree(staging);
+        if (rc == AETH_OK && e2 != hipSuccess)
+            rc = aeth_set_error(AETH_EHIP, "aeth_weight_create: sync failed: %s", hipGetErrorString(e2));
+    }
+    if (rc) {
+        hipFree(w->base);
+        delete w;
+        return rc;
+    }
+    *out = w;
+    return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_weight_free(aeth_weight* w) {
+    if (!w) return AETH_OK;
+    if (w->base) AETH_HIP_CHECK(hipFree(w->base));
+    delete w;
+    return AETH_OK;
+}
+
+extern "C" AETH_API int64_t aeth_weight_bytes(const aeth_weight* w) { return w ? w->bytes : 0; }
+
+extern "C" AETH_API int aeth_weight_export_raw(const aeth_weight* w, void* dst, int dst_is_device, void* stream) {
+    if (!w || !dst) return aeth_set_error(AETH_EINVAL, "aeth_weight_export_raw: NULL argument");
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t* tmp = (uint8_t*)dst;
+    if (!dst_is_device) AETH_HIP_CHECK(hipMalloc((void**)&tmp, (size_t)w->bytes));
+    int rc = relayout((aeth_weight*)w, tmp, 0, s);
+    if (!dst_is_device) {
+        if (rc == AETH_OK) {
+            hipError_t e = hipMemcpyAsync(dst, tmp, (size_t)w->bytes, hipMemcpyDeviceToHost, s);
+            if (e == hipSuccess) e = hipStreamSynchronize(s);
+            if (e != hipSuccess) rc = aeth_set_error(AETH_EHIP, "export copy failed: %s", hipGetErrorString(e));
+        }
+        hipFree(tmp);
+    }
+    return rc;
+}
+
+// ── seeded synthetic inputs ──────────────────────────────────────────────
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// N(0,1) by Box-Muller from the counter (key, idx).
+__device__ __forceinline__ float normal_at(uint64_t key, uint64_t idx) {
+    uint64_t h1 = splitmix64(key ^ (idx * 2 + 0x51ull));
+    uint64_t h2 = splitmix64(key ^ (idx * 2 + 0x52ull) ^ 0xD1B54A32D192ED03ull);
+    float u1 = ((float)(h1 >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+    float u2 = (float)(h2 >> 40) * (1.0f / 16777216.0f);           // [0, 1)
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+}
+
+__device__ __forceinline__ uint32_t scale_f16_bits(uint64_t key, uint64_t blk, int which) {
+    float v = fabsf(normal_at(key ^ (0xABCDull + (uint64_t)which), blk)) * 0.01f;
+    return (uint32_t)__half_as_ushort(__float2half_rn(v));
+}
+
+__global__ void k_fill_synthetic(int dtype, uint64_t seed, uint8_t* __restrict__ raw, int64_t total_bytes) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total_bytes) return;
+    uint64_t key = splitmix64(seed);
+    uint8_t v;
+    if (dtype == AETH_DTYPE_Q4_K) {
+        int64_t blk = i / Q4K_BLOCK_BYTES;
+        int off = (int)(i - blk * Q4K_BLOCK_BYTES);
+        if (off < 4) {
+            uint32_t b = scale_f16_bits(key, (uint64_t)blk, off >> 1);
+            v = (uint8_t)((off & 1) ? (b >> 8) : b);
+        } else {
+            v = (uint8_t)splitmix64(key ^ ((uint64_t)i * 0x9E37ull + 0x1234567ull));
+        }
+    } else if (dtype == AETH_DTYPE_Q6_K) {
+        int64_t blk = i / Q6K_BLOCK_BYTES;
+        int off = (int)(i - blk * Q6K_BLOCK_BYTES);
+        uint64_t h = splitmix64(key ^ ((uint64_t)i * 0x9E37ull + 0x7654321ull));
+        if (off < 192) v = (uint8_t)h;
+        else if (off < 208) v = (uint8_t)(int8_t)((int)(h & 127) - 64);
+        else {
+            uint32_t b = scale_f16_bits(key, (uint64_t)blk, 0);
+            v = (uint8_t)((off & 1) ? (b >> 8) : b);
+        }
+    } else {
+        int64_t blk = i / Q8_BLOCK_BYTES;
+        int off = (int)(i - blk * Q8_BLOCK_BYTES);
+        if (off < 2) {
+            uint32_t b = scale_f16_bits(key, (uint64_t)blk, 0);
+            v = (uint8_t)((off & 1) ? (b >> 8) : b);
+        } else {
+            uint64_t h = splitmix64(key ^ ((uint64_t)i * 0x9E37ull + 0x3141592ull));
+            v = (uint8_t)(int8_t)((int)(h % 255ull) - 127);
+        }
+    }
+    raw[i] = v;
+}
+
+extern "C" AETH_API int aeth_fill_synthetic_raw(int dtype, uint64_t seed, void* d_raw, int64_t n_blocks,
+                                                void* stream) {
+    int be, bb;
+    int rc = aeth_block_geometry(dtype, &be, &bb);
+    if (rc) return rc;
+    if (!d_raw || n_blocks < 0) return aeth_set_error(AETH_EINVAL, "aeth_fill_synthetic_raw: bad argument");
+    int64_t total = n_blocks * bb;
+    if (total == 0) return AETH_OK;
+    hipLaunchKernelGGL(k_fill_synthetic, dim3((unsigned)aeth_cdiv(total, 256)), dim3(256), 0,
+                       (hipStream_t)stream, dtype, seed, (uint8_t*)d_raw, total);
+    AETH_LAUNCH_CHECK();
+    return AETH_OK;
+}
+
+__global__ void k_fill_normal(uint64_t seed, float* __restrict__ out, int64_t n, float mean, float stdv) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    out[i] = mean + stdv * normal_at(splitmix64(seed ^ 0x6E6F726D616CULL), (uint64_t)i);
+}
+
+extern "C" AETH_API int aeth_fill_normal_f32(uint64_t seed, float* d_out, int64_t n, float mean, float stdv,
+                                             void* stream) {
+    if (!d_out || n < 0) return aeth_set_error(AETH_EINVAL, "aeth_fill_normal_f32: bad argument");
+    if (n == 0) return AETH_OK;
+    hipLaunchKernelGGL(k_fill_normal, dim3((unsigned)aeth_cdiv(n, 256)), dim3(256), 0, (hipStream_t)stream, seed,
+                       d_out, n, mean, stdv);
+    AETH_LAUNCH_CHECK();
+    return AETH_OK;
+}

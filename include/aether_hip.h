@@ -1,0 +1,195 @@
+/*
+ * aether_hip.h — C ABI of the MI355X (gfx950) quantized-matmul hot path.
+ *
+ * Plain pointers and sizes only. Every function returns an int status
+ * (AETH_OK = 0, negative on error; the message is in aeth_last_error())
+ * and never unwinds. "d_" arguments are device pointers; `stream` is a
+ * hipStream_t (NULL = the null stream). Device-pointer entry points are
+ * asynchronous on `stream`; host-slice entry points synchronise.
+ *
+ * Each entry point names the reference interface it replaces
+ * (theoxfaber/aether, path:line).
+ */
+#ifndef AETHER_HIP_H
+#define AETHER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AETH_API __attribute__((visibility("default")))
+
+#define AETH_OK 0
+#define AETH_EINVAL (-1)
+#define AETH_EHIP (-2)
+#define AETH_ENOMEM (-3)
+#define AETH_EUNSUPPORTED (-4)
+#define AETH_ESTATE (-5)
+
+/* GGUFDtype discriminants, src/loader/gguf.rs:92-110. */
+#define AETH_DTYPE_Q8_0 8
+#define AETH_DTYPE_Q4_K 12
+#define AETH_DTYPE_Q6_K 14
+
+/* aeth_qmatmul flags */
+#define AETH_MM_ACCUMULATE 1u /* c += A·Wᵀ instead of c = A·Wᵀ (fused residual add,
+                                 runner.rs:1609-1611, 1629-1631) */
+
+/* ── runtime ─────────────────────────────────────────────────────────────── */
+
+/* Select the device and create the library's per-device state. */
+AETH_API int aeth_init(int device);
+/* Last error message of the calling thread ("" if none). */
+AETH_API const char* aeth_last_error(void);
+/* Block geometry, GGUFDtype::block_size/block_byte_size (gguf.rs:137-173). */
+AETH_API int aeth_block_geometry(int dtype, int* block_elems, int* block_bytes);
+
+/* ── device-resident weights ─────────────────────────────────────────────
+ * A registered weight is the device copy of one QuantWeight
+ * (src/inference/model_loader.rs:88-93): `raw` holds n rows (out_features)
+ * of k/block_elems GGUF blocks each, row-major, exactly as QuantWeight.data.
+ * On upload it is re-laid into per-field planes (scales / quants split so
+ * every wave load is 16-byte aligned and contiguous); aeth_weight_export_raw
+ * reproduces the original bytes. The QuantKernel host-slice path registers
+ * weights implicitly (see aeth_quantized_matmul_impl). */
+typedef struct aeth_weight aeth_weight;
+
+AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, const void* raw, int raw_is_device,
+                                void* stream, aeth_weight** out);
+AETH_API int aeth_weight_free(aeth_weight* w);
+/* Device bytes held by the weight's planes (== raw GGUF bytes). */
+AETH_API int64_t aeth_weight_bytes(const aeth_weight* w);
+AETH_API int aeth_weight_export_raw(const aeth_weight* w, void* dst, int dst_is_device, void* stream);
+
+/* ── kernels ───────────────────────────────────────────────────────────── */
+
+/* GGUF blocks → f32, bit-exact with dequant_q8_0 / dequant_q4_k /
+ * dequant_q6_k (src/loader/dequant.rs:103-127, 195-227, 301-348).
+ * d_raw holds ceil(n/block_elems) raw blocks; n is rounded down to whole
+ * blocks for the K-quants as the reference does (tail left untouched). */
+AETH_API int aeth_dequant(int dtype, const void* d_raw, int64_t n_elems, float* d_out, void* stream);
+
+/* C[m×n] = A[m×k] · Wᵀ on the device — QuantKernel::matmul
+ * (src/quant/matmul/registry.rs:7-19) / quantized_matmul_impl
+ * (src/quant/matmul/dispatch.rs:98-135) with device operands. m == 1 runs the
+ * decode GEMV; m > 1 runs the prefill GEMM (Q4_K: fp16-split MFMA; others:
+ * row-batched GEMV). */
+AETH_API int aeth_qmatmul(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
+                          void* stream);
+
+/* Same, on GGUF bytes and host slices: quantized_matmul_impl
+ * (dispatch.rs:98-106) with b_shape = [n, k]. The weight bytes are uploaded
+ * once and cached by (pointer, length, dtype, n, k) — the bytes must stay
+ * immutable while cached, as QuantWeight.data is (gguf.rs:177-277); a, c are
+ * copied per call. Fails (no CPU fallback) if no device is usable. */
+AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
+                                        int64_t n, int64_t k, int dtype, float* c);
+/* matmul_q8_0 / matmul_q4_k / matmul_q6_k(a, b, m, n, k, c)
+ * (src/quant/matmul/avx2_dispatch.rs:58-68): argument order as the reference. */
+AETH_API int aeth_matmul_q8_0(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                              int64_t k, float* c);
+AETH_API int aeth_matmul_q4_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                              int64_t k, float* c);
+AETH_API int aeth_matmul_q6_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                              int64_t k, float* c);
+/* QuantKernel registry (registry.rs:33-63): registers the HIP kernels for
+ * Q8_0, Q4_K and Q6_K; a second registration of a dtype fails with
+ * AETH_ESTATE (the reference panics). aeth_dispatch_matmul returns 1 if a
+ * registered kernel handled the call, 0 if none is registered for dtype, <0
+ * on error. */
+AETH_API int aeth_register_hip_kernels(void);
+AETH_API int aeth_registered_kernel_name(int dtype, char* buf, int buf_len);
+AETH_API int aeth_dispatch_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, int64_t n,
+                                  int64_t k, int dtype, float* c);
+/* Drops every cached host-slice weight (frees device memory). */
+AETH_API int aeth_weight_cache_clear(void);
+
+/* rmsnorm_inplace (runner.rs:1739-1746) on `rows` rows of n: out = x/rms*w. */
+AETH_API int aeth_rmsnorm(const float* d_x, const float* d_w, int64_t rows, int64_t n, float eps,
+                          float* d_out, void* stream);
+/* apply_rope_inplace (runner.rs:1886-1909), rotate-half, one position, with
+ * the host-built table of precompute_rope (runner.rs:1912-1924) already on
+ * the device ([max_seq][head_dim/2] each); pos is clamped to max_seq-1. */
+AETH_API int aeth_rope(float* d_x, int64_t n_heads, int64_t head_dim, int64_t pos, const float* d_sin,
+                       const float* d_cos, int64_t max_seq, void* stream);
+/* StaticKVCache::append (kv_cache.rs:40-65) for one layer: copies k, v
+ * ([kv_heads][head_dim]) into slot `slot` of the [2][kv_heads][max_seq][hd]
+ * layer slice d_layer_kv. */
+AETH_API int aeth_kv_append(float* d_layer_kv, const float* d_k, const float* d_v, int64_t kv_heads,
+                            int64_t head_dim, int64_t max_seq, int64_t slot, void* stream);
+/* GQA decode attention (runner.rs:1579-1603 with attn_direct :1757-1801)
+ * over positions [0, seq) of one layer slice of the static cache. */
+AETH_API int aeth_attn_decode(const float* d_q, const float* d_layer_kv, int64_t n_heads, int64_t kv_heads,
+                              int64_t head_dim, int64_t max_seq, int64_t seq, float* d_out, void* stream);
+/* SiLU-MLP glue (runner.rs:1617-1625): g = g * sigmoid(g) * up. */
+AETH_API int aeth_silu_mul(float* d_gate, const float* d_up, int64_t n, void* stream);
+/* Residual add (runner.rs:1609-1611): x += y. */
+AETH_API int aeth_add(float* d_x, const float* d_y, int64_t n, void* stream);
+/* Greedy sample (runner.rs:1964-1973; aether_argmax c_api.rs:384-396):
+ * index of the maximum, the LAST one on ties; result written to d_out. */
+AETH_API int aeth_argmax(const float* d_logits, int64_t n, int32_t* d_out, void* stream);
+
+/* ── synthetic inputs (generated on the device, counter-based, seeded) ───
+ * Raw GGUF blocks as the benchmark configs describe them:
+ *   Q8_0: d = f16(|N(0,1)|*0.01), q uniform int in [-127,127];
+ *   Q4_K: d, dmin = f16(|N(0,1)|*0.01), scales[12] and qs[128] uniform bytes;
+ *   Q6_K: d = f16(|N(0,1)|*0.01), sc uniform int in [-64,63], ql/qh uniform bytes.
+ * The same (seed, block index) always yields the same bytes. */
+AETH_API int aeth_fill_synthetic_raw(int dtype, uint64_t seed, void* d_raw, int64_t n_blocks, void* stream);
+/* out[i] = mean + std * N(0,1) from (seed, i). */
+AETH_API int aeth_fill_normal_f32(uint64_t seed, float* d_out, int64_t n, float mean, float std, void* stream);
+
+/* ── LlamaRunner (src/inference/runner.rs) on the device ─────────────────
+ * Model shape = LlamaConfig (model_loader.rs:71-84). */
+typedef struct aeth_llama_config {
+    int32_t vocab_size, d_model, num_layers, num_heads, num_kv_heads, head_dim, d_ff, max_seq_len;
+    float rope_base, rms_norm_eps;
+} aeth_llama_config;
+
+typedef struct aeth_runner aeth_runner;
+
+/* Creates a runner with device weights and a zeroed StaticKVCache of
+ * max_seq_len positions. Host buffers: per layer l, layer_weights[l*7+j]
+ * for j = q,k,v,o,gate,up,down (raw GGUF blocks, [out][in] as QuantWeight),
+ * layer_dtypes likewise; norms[l*2+{0,1}] = attn_norm, ffn_norm (f32);
+ * final_norm (f32, d_model); lm_head (raw, dtype lm_dtype); embeddings
+ * f32 [vocab][d_model]. Any pointer may be NULL when `synthetic_seed` is
+ * nonzero: the runner then generates that tensor on the device (weights as
+ * aeth_fill_synthetic_raw with the dtypes given, norms 1+N(0,0.02),
+ * embeddings N(0,1)). */
+AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const void* const* layer_weights,
+                                const int32_t* layer_dtypes, const float* const* norms, const float* final_norm,
+                                const void* lm_head, int32_t lm_dtype, const float* embeddings,
+                                uint64_t synthetic_seed, aeth_runner** out);
+AETH_API int aeth_runner_free(aeth_runner* r);
+/* Fills the first `seq_len` cache positions of every layer with N(0,1) from
+ * `seed` and sets the cache fill (prefilled-context benchmark setup). */
+AETH_API int aeth_runner_fill_kv(aeth_runner* r, uint64_t seed, int32_t seq_len);
+/* Copies KV storage [L][2][kv_heads][max_seq][hd] to/from the host and sets the fill. */
+AETH_API int aeth_runner_kv_to_host(aeth_runner* r, float* host, int32_t* seq_len);
+AETH_API int aeth_runner_kv_from_host(aeth_runner* r, const float* host, int32_t seq_len);
+AETH_API int aeth_runner_seq_len(const aeth_runner* r);
+/* One decode step (forward_one_internal, runner.rs:1175-1649): token's
+ * embedding → L layers → final norm → LM head. logits (host, vocab floats)
+ * may be NULL; next_token (host) receives the greedy argmax if non-NULL. */
+AETH_API int aeth_runner_decode(aeth_runner* r, int32_t token, int32_t pos, float* logits, int32_t* next_token);
+/* Greedy decode of n_steps tokens starting from `token` at `pos`; tokens
+ * (host, n_steps) receive each step's argmax (fed back as the next input).
+ * Uses a captured HIP graph per step when use_graph != 0. */
+AETH_API int aeth_runner_generate(aeth_runner* r, int32_t token, int32_t pos, int32_t n_steps, int32_t* tokens,
+                                  int use_graph);
+/* Copies device tensors back for checking: which = 0..6 layer weight j of
+ * layer l (raw GGUF bytes), 7 attn_norm, 8 ffn_norm, 9 final_norm, 10 lm_head
+ * (raw), 11 embedding row `l`, 12 rope sin table, 13 rope cos table. */
+AETH_API int aeth_runner_export(const aeth_runner* r, int which, int32_t l, void* host, int64_t host_bytes);
+/* The stream the runner launches on (hipStream_t). */
+AETH_API void* aeth_runner_stream(const aeth_runner* r);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AETHER_HIP_H */

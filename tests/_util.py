@@ -1,0 +1,58 @@
+"""Shared helpers for the parity tests: seeded synthetic GGUF blocks (numpy)
+and the tolerance rule of the north star."""
+import numpy as np
+
+Q8_0, Q4_K, Q6_K = 8, 12, 14
+GEOM = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+
+def f16_bytes(v):
+    return np.asarray(v, dtype=np.float32).astype(np.float16).view(np.uint8).reshape(-1, 2)
+
+
+def synth_blocks(dtype, n_blocks, seed):
+    """Raw GGUF blocks as BASELINE.json describes the benchmark weights."""
+    rng = np.random.default_rng(seed)
+    be, bb = GEOM[dtype]
+    raw = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
+    scale = lambda: f16_bytes(np.abs(rng.standard_normal(n_blocks)) * 0.01)
+    if dtype == Q8_0:
+        raw[:, 0:2] = scale()
+        raw[:, 2:] = rng.integers(-127, 128, size=(n_blocks, 32)).astype(np.int8).view(np.uint8)
+    elif dtype == Q4_K:
+        raw[:, 0:2] = scale()
+        raw[:, 2:4] = scale()
+    else:
+        raw[:, 192:208] = rng.integers(-64, 64, size=(n_blocks, 16)).astype(np.int8).view(np.uint8)
+        raw[:, 208:210] = scale()
+    return raw.reshape(-1)
+
+
+def weight(dtype, n, k, seed):
+    be, bb = GEOM[dtype]
+    nb = (k + 31) // 32 if dtype == Q8_0 else k // 256
+    return synth_blocks(dtype, n * nb, seed)
+
+
+def close_mask(g, r, tol=1e-3):
+    g = np.asarray(g, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    diff = np.abs(g - r)
+    return (diff <= tol) | (diff / np.maximum(1.0, np.abs(r)) <= tol)
+
+
+def assert_close(g, r, tol=1e-3, cos_min=0.9999, what=""):
+    """Per element |g-r| <= tol or |g-r|/max(1,|r|) <= tol (the reference's own
+    relative form, src/quant/matmul/tests.rs:406), and per-row cosine > cos_min."""
+    g = np.atleast_2d(np.asarray(g, dtype=np.float64))
+    r = np.atleast_2d(np.asarray(r, dtype=np.float64))
+    assert g.shape == r.shape, (g.shape, r.shape)
+    ok = close_mask(g, r, tol)
+    if not ok.all():
+        i = np.argwhere(~ok)[0]
+        raise AssertionError("%s: %d/%d elements out of tolerance; first at %s: got %r ref %r" %
+                             (what, (~ok).sum(), ok.size, tuple(i), g[tuple(i)], r[tuple(i)]))
+    num = (g * r).sum(axis=1)
+    den = np.sqrt((g * g).sum(axis=1) * (r * r).sum(axis=1))
+    cos = np.where(den > 0, num / np.where(den > 0, den, 1), 1.0)
+    assert (cos > cos_min).all(), "%s: row cosine %r <= %r" % (what, cos.min(), cos_min)

@@ -1,0 +1,236 @@
+"""GPU parity of the decode-step kernels and the device LlamaRunner against
+the CPU oracle's restatement of runner.rs (rmsnorm, RoPE, attention, SiLU,
+argmax, one full decode step)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import aether_amd as A
+from oracle import oracle as O
+from tests._util import Q4_K, Q6_K, Q8_0, assert_close, weight
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(torch, arr):
+    return torch.from_numpy(np.ascontiguousarray(arr)).cuda()
+
+
+def test_rmsnorm(gpu):
+    torch = gpu
+    rng = np.random.default_rng(1)
+    n = 4096
+    x = rng.standard_normal((3, n)).astype(np.float32) * 3
+    w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+    xd, wd = dev(torch, x), dev(torch, w)
+    od = torch.empty_like(xd)
+    A.check(A.lib().aeth_rmsnorm(xd.data_ptr(), wd.data_ptr(), 3, n, 1e-5, od.data_ptr(), None))
+    torch.cuda.synchronize()
+    ref = np.stack([O.rmsnorm(x[i], w, 1e-5) for i in range(3)])
+    assert_close(od.cpu().numpy(), ref, tol=1e-5)
+
+
+@pytest.mark.parametrize("pos", [0, 1, 2047, 5000])
+def test_rope(gpu, pos):
+    torch = gpu
+    nh, hd, ms = 40, 128, 4096
+    s, c = O.precompute_rope(ms, hd, 500000.0)
+    x = np.random.default_rng(pos).standard_normal(nh * hd).astype(np.float32)
+    xd = dev(torch, x)
+    A.check(A.lib().aeth_rope(xd.data_ptr(), nh, hd, pos, dev(torch, s).data_ptr(), dev(torch, c).data_ptr(), ms,
+                              None))
+    torch.cuda.synchronize()
+    ref = O.apply_rope(x, nh, hd, pos, s, c, ms)
+    assert_close(xd.cpu().numpy(), ref, tol=1e-5)
+    if pos == 0:
+        assert np.array_equal(xd.cpu().numpy(), x)  # θ = 0: identity
+
+
+@pytest.mark.parametrize("seq", [1, 63, 64, 65, 2049])
+def test_attention_and_kv_append(gpu, seq):
+    torch = gpu
+    L = A.lib()
+    nh, nkv, hd, ms = 32, 8, 128, 2304
+    rng = np.random.default_rng(seq)
+    kv = rng.standard_normal((2, nkv, ms, hd)).astype(np.float32)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k_new = rng.standard_normal(nkv * hd).astype(np.float32)
+    v_new = rng.standard_normal(nkv * hd).astype(np.float32)
+    kvd = dev(torch, kv)
+    slot = seq - 1
+    A.check(L.aeth_kv_append(kvd.data_ptr(), dev(torch, k_new).data_ptr(), dev(torch, v_new).data_ptr(), nkv, hd, ms,
+                             slot, None))
+    od = torch.empty(nh * hd, dtype=torch.float32, device="cuda")
+    A.check(L.aeth_attn_decode(dev(torch, q).data_ptr(), kvd.data_ptr(), nh, nkv, hd, ms, seq, od.data_ptr(), None))
+    torch.cuda.synchronize()
+    kv[0, :, slot, :] = k_new.reshape(nkv, hd)
+    kv[1, :, slot, :] = v_new.reshape(nkv, hd)
+    assert np.array_equal(kvd.cpu().numpy(), kv)
+    ref = np.concatenate([O.attn_direct(q[h * hd:(h + 1) * hd], kv[0, h // (nh // nkv)], kv[1, h // (nh // nkv)], seq,
+                                        hd) for h in range(nh)])
+    assert_close(od.cpu().numpy(), ref, tol=1e-4)
+
+
+def test_attention_one_hot(gpu):
+    """A query aligned with one cached key far above the rest attends only to
+    that position: out = v_t."""
+    torch = gpu
+    nh, nkv, hd, ms, seq = 4, 1, 128, 256, 200
+    kv = np.zeros((2, nkv, ms, hd), dtype=np.float32)
+    rng = np.random.default_rng(3)
+    kv[1] = rng.standard_normal((nkv, ms, hd))
+    kv[0, 0, 77, :] = 1.0
+    q = np.full(nh * hd, 10.0, dtype=np.float32)
+    od = torch.empty(nh * hd, dtype=torch.float32, device="cuda")
+    A.check(A.lib().aeth_attn_decode(dev(torch, q).data_ptr(), dev(torch, kv).data_ptr(), nh, nkv, hd, ms, seq,
+                                     od.data_ptr(), None))
+    torch.cuda.synchronize()
+    got = od.cpu().numpy().reshape(nh, hd)
+    for h in range(nh):
+        np.testing.assert_allclose(got[h], kv[1, 0, 77], rtol=1e-5, atol=1e-5)
+
+
+def test_silu_mul_and_add(gpu):
+    torch = gpu
+    rng = np.random.default_rng(4)
+    n = 14336
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    gd, ud = dev(torch, g), dev(torch, u)
+    A.check(A.lib().aeth_silu_mul(gd.data_ptr(), ud.data_ptr(), n, None))
+    A.check(A.lib().aeth_add(gd.data_ptr(), ud.data_ptr(), n, None))
+    torch.cuda.synchronize()
+    ref = (g * (1.0 / (1.0 + np.exp(-g))) * u + u).astype(np.float32)
+    assert_close(gd.cpu().numpy(), ref, tol=1e-5)
+
+
+def test_argmax_last_max_wins(gpu):
+    torch = gpu
+    n = 128256
+    x = np.random.default_rng(5).standard_normal(n).astype(np.float32)
+    x[[10, 50000, 128000]] = 9.0  # ties: the last index wins (Iterator::max_by)
+    od = torch.empty(1, dtype=torch.int32, device="cuda")
+    A.check(A.lib().aeth_argmax(dev(torch, x).data_ptr(), n, od.data_ptr(), None))
+    torch.cuda.synchronize()
+    assert int(od.cpu()[0]) == 128000 == O.argmax(x)
+
+
+# ── device LlamaRunner vs the oracle's decode step ───────────────────────
+
+TINY = dict(vocab_size=512, d_model=256, num_layers=2, num_heads=4, num_kv_heads=2, head_dim=64, d_ff=512,
+            max_seq_len=64, rope_base=10000.0, rms_norm_eps=1e-5)
+
+
+def build_tiny(seed=1, lm_dtype=Q6_K, layer_dtype=Q4_K):
+    c = TINY
+    rng = np.random.default_rng(seed)
+    d, qd, kvd, dff = c["d_model"], c["num_heads"] * c["head_dim"], c["num_kv_heads"] * c["head_dim"], c["d_ff"]
+    shapes = [(qd, d), (kvd, d), (kvd, d), (d, qd), (dff, d), (dff, d), (d, dff)]
+    layers = [[weight(layer_dtype, n, k, seed * 100 + l * 7 + j) for j, (n, k) in enumerate(shapes)]
+              for l in range(c["num_layers"])]
+    norms = [[(1 + 0.02 * rng.standard_normal(d)).astype(np.float32) for _ in range(2)] for _ in range(c["num_layers"])]
+    final = (1 + 0.02 * rng.standard_normal(d)).astype(np.float32)
+    lm = weight(lm_dtype, c["vocab_size"], d, seed * 31)
+    emb = rng.standard_normal((c["vocab_size"], d)).astype(np.float32)
+    return dict(layers=layers, norms=norms, final=final, lm=lm, emb=emb, lm_dtype=lm_dtype, layer_dtype=layer_dtype)
+
+
+def make_runner(m):
+    c = TINY
+    cfg = A.LlamaConfig(**c)
+    nl = c["num_layers"]
+    wp = (ctypes.c_void_p * (nl * 7))(*[m["layers"][l][j].ctypes.data for l in range(nl) for j in range(7)])
+    dt = (ctypes.c_int32 * (nl * 7))(*([m["layer_dtype"]] * nl * 7))
+    npp = (ctypes.c_void_p * (nl * 2))(*[m["norms"][l][j].ctypes.data for l in range(nl) for j in range(2)])
+    r = ctypes.c_void_p()
+    A.check(A.lib().aeth_runner_create(ctypes.byref(cfg), wp, dt, npp, m["final"].ctypes.data, m["lm"].ctypes.data,
+                                       m["lm_dtype"], m["emb"].ctypes.data, 0, ctypes.byref(r)), "runner_create")
+    return r
+
+
+def oracle_cfg():
+    c = TINY
+    return O.LlamaCfg(c["vocab_size"], c["d_model"], c["num_layers"], c["num_heads"], c["num_kv_heads"], c["head_dim"],
+                      c["d_ff"], c["max_seq_len"], c["rope_base"], c["rms_norm_eps"])
+
+
+@pytest.mark.parametrize("layer_dtype", [Q4_K, Q8_0, Q6_K])
+def test_runner_decode_matches_oracle(gpu, layer_dtype):
+    m = build_tiny(seed=2, layer_dtype=layer_dtype)
+    r = make_runner(m)
+    L = A.lib()
+    c = TINY
+    ocfg = oracle_cfg()
+    s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
+    kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), dtype=np.float32)
+    fill = 0
+    tok = 1
+    try:
+        for step in range(6):
+            logits = np.empty(c["vocab_size"], dtype=np.float32)
+            nxt = ctypes.c_int32()
+            A.check(L.aeth_runner_decode(r, tok, step, logits.ctypes.data, ctypes.byref(nxt)), "decode")
+            ref, fill = O.decode_step(ocfg, m["emb"][tok], step, m["layers"], [layer_dtype] * 7, m["norms"], m["final"],
+                                      m["lm"], m["lm_dtype"], s, co, kv, fill)
+            assert_close(logits, ref, what="step %d" % step)
+            assert nxt.value == O.argmax(logits)
+            tok = O.argmax(ref)  # teacher forcing on the CPU's token
+        assert L.aeth_runner_seq_len(r) == 6
+        kv_dev = np.empty_like(kv)
+        fl = ctypes.c_int32()
+        A.check(L.aeth_runner_kv_to_host(r, kv_dev.ctypes.data, ctypes.byref(fl)))
+        assert fl.value == 6
+        assert_close(kv_dev.reshape(-1, c["head_dim"]), kv.reshape(-1, c["head_dim"]), tol=1e-4, cos_min=0.0)
+    finally:
+        L.aeth_runner_free(r)
+
+
+def test_runner_generate_graph_matches_eager(gpu):
+    m = build_tiny(seed=3)
+    L = A.lib()
+    outs = []
+    for use_graph in (0, 1, 1):
+        r = make_runner(m)
+        toks = (ctypes.c_int32 * 10)()
+        A.check(L.aeth_runner_generate(r, 1, 0, 10, toks, use_graph), "generate")
+        if use_graph:  # a second replay batch continues the sequence
+            more = (ctypes.c_int32 * 5)()
+            A.check(L.aeth_runner_generate(r, toks[9], 10, 5, more, use_graph), "generate 2")
+            outs.append(list(toks) + list(more))
+        else:
+            more = (ctypes.c_int32 * 5)()
+            A.check(L.aeth_runner_generate(r, toks[9], 10, 5, more, 0), "generate 2")
+            outs.append(list(toks) + list(more))
+        L.aeth_runner_free(r)
+    assert outs[0] == outs[1] == outs[2]
+
+
+def test_c_api_surface(gpu):
+    """aether_* over a device runner: queries, decode, argmax, budget."""
+    L = A.lib()
+    m = build_tiny(seed=4)
+    r = make_runner(m)
+    model = L.aether_model_from_runner(r)
+    assert model
+    try:
+        assert L.aether_vocab_size(model) == TINY["vocab_size"]
+        assert L.aether_num_layers(model) == TINY["num_layers"]
+        assert L.aether_d_model(model) == TINY["d_model"]
+        assert L.aether_context_len(model) == TINY["max_seq_len"]
+        logits = np.empty(TINY["vocab_size"], dtype=np.float32)
+        toks = (ctypes.c_int * 3)(1, 5, 9)
+        assert L.aether_prefill(model, toks, 3, logits.ctypes.data) == 0
+        assert L.aeth_runner_seq_len(r) == 3
+        t = L.aether_argmax(model, logits.ctypes.data)
+        assert t == O.argmax(logits)
+        assert L.aether_sample(model, logits.ctypes.data, 0.0, 1.0) == t
+        assert L.aether_decode(model, t, 3, logits.ctypes.data) == 0
+        # a generous budget completes like aether_decode
+        L.aether_set_frame_budget(model, 10000.0)
+        assert abs(L.aether_frame_budget(model) - 10000.0) < 1e-3
+        assert L.aether_decode_budgeted(model, 2, 4, logits.ctypes.data) == 0
+        assert L.aeth_runner_seq_len(r) == 5
+        assert L.aether_load(b"/nonexistent.gguf") is None
+    finally:
+        L.aether_free(model)
