@@ -39,7 +39,7 @@ def command(out=LIB):
         "-fPIC",
         "-shared",
         "-fvisibility=hidden",
-        "-ffp-contract=fast",
+        "-ffp-contract=fast-honor-pragmas",
         # packed-FP32 VALU forms are kept out of the device code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wall",

@@ -1,9 +1,10 @@
 // GGUF block → f32 dequantization, bit-exact with src/loader/dequant.rs.
 //
-// Every product below is exact in f32 before its single rounding step
-// (f16 scale: 11 significant bits; 6-bit sub-scales; 4/6/8-bit quants), so
-// the results do not depend on FMA contraction; the pragma keeps the
-// reference's separate multiply/subtract anyway.
+// The reference rounds every multiply and subtract separately (Rust never
+// fuses). With a NaN/Inf-pattern scale (bits/65536: 16 significant bits) the
+// product d1*q is not exact in f32, so fusing it with the subtraction would
+// change results: contraction is switched off for this file (the library is
+// built with -ffp-contract=fast-honor-pragmas, which honours the pragma).
 #include "aeth_common.hpp"
 #include "aeth_internal.hpp"
 

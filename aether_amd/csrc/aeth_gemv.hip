@@ -1,20 +1,24 @@
 // Decode GEMV for Q8_0 / Q4_K / Q6_K weights on gfx950:  y[r] = Σ_k x[k]·W[r][k].
 //
-// Design (MI355X-first; see DESIGN.md for the derivation):
-//  * The weight planes are streamed with 16-byte loads; chunk c of a row is
-//    bytes [16c, 16c+16) of that row's quant plane, so lane L of a wave reads
-//    bytes [16L, 16L+16) — one wave instruction covers 1 KiB contiguous.
-//  * The activation row is converted once per workgroup (in LDS) into an exact
-//    integer form: per 16-element group g, x ≈ x_int·2^-S_g with
-//    |x_int| ≤ 2^22 (22 bits + sign relative to the group maximum — the f32
-//    rounding of x itself is 2^-24), split into three balanced signed byte
-//    digits d0 + 256·d1 + 65536·d2. A 4-element weight quad is then dotted
-//    with v_dot4_i32_i8 per digit: integer-exact sub-block dots at ~1 VALU op
-//    per weight instead of unpack+convert+FMA (~2.4).
-//  * Per-sub-block scales are applied in f32 once per 16-element group.
-//  * Persistent workgroups: a fixed grid (a small multiple of the CU count)
-//    amortises the activation conversion; each wave owns a contiguous run of
-//    rows and processes R of them per pass with all loads issued up front.
+// Design (MI355X-first):
+//  * Weights are read from the planar device layout (aeth_weights.hip) in
+//    "units" of 32 (Q4_K, Q8_0) or 48 (Q6_K) quant bytes per lane, as
+//    16-byte loads; consecutive lanes take consecutive units of a row, so each
+//    wave load instruction covers a contiguous span of the row.
+//  * The activation row becomes an exact integer form once per workgroup:
+//    per 32 elements, x ≈ x_int·2^-S with |x_int| ≤ 2^22 (22 bits + sign
+//    relative to the group maximum; f32 itself keeps 24), split into three
+//    balanced signed byte digits x_int = d0 + 256·d1 + 65536·d2. A quad of
+//    4-bit / 6-bit / 8-bit quants is dotted with v_dot4_i32_i8 per digit:
+//    integer-exact sub-block dots for ~1 VALU op per weight instead of
+//    unpack + convert + FMA. Scales are applied in f32 per sub-block.
+//  * The digits are laid out in LDS per lane unit ("records", strides chosen
+//    so that 8 consecutive lanes hit distinct 16-byte bank groups) and, when a
+//    lane owns one or two units per row, held in registers for all its rows.
+//  * One persistent workgroup of 8 waves per CU; each wave owns a contiguous
+//    run of rows, processed R at a time. The first pass's weight loads are
+//    issued before the activation conversion, and each pass prefetches the
+//    next, so HBM streams while the VALU works.
 #include <math.h>
 #include <stdlib.h>
 
@@ -24,51 +28,79 @@
 #define GEMV_THREADS 512
 #define GEMV_WAVES (GEMV_THREADS / 64)
 
-// LDS image of one activation row.
-struct XDigits {
-    int* dig;      // [3][ngroups*4] dwords: 4 signed bytes = digit k of a quad
-    int* gexp;     // [ngroups] S_g
-    float* gfsum;  // [ngroups] Σx over the group (Q4_K min term)
-    int* gisum;    // [3][ngroups] 32·Σ digit_k over the group (Q6_K −32 offset)
-    int ngroups;
-};
+enum { FMT_Q80 = 0, FMT_Q4K = 1, FMT_Q6K = 2 };
+
+// Per-format geometry. UE: activation elements per unit; RECB: bytes of one
+// LDS digit record; NQ: int4 weight loads per unit.
+template <int F> struct Fmt;
+template <> struct Fmt<FMT_Q4K> { static constexpr int UE = 64, RECB = 208; };
+template <> struct Fmt<FMT_Q6K> { static constexpr int UE = 64, RECB = 272; };
+template <> struct Fmt<FMT_Q80> { static constexpr int UE = 32, RECB = 112; };
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
-    return (a & 0xFF) | ((b & 0xFF) << 8) | ((c & 0xFF) << 16) | ((int)((unsigned)d << 24));
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
 }
 
-// Builds the digit image of x[0..k) (zero-padded to ngroups*16) in LDS.
-// Returns nonzero (uniformly) if x holds a non-finite value.
-__device__ int build_digits(const float* __restrict__ x, int k, XDigits X, int* flag_smem) {
-    const int tid = threadIdx.x;
-    if (tid == 0) *flag_smem = 0;
-    __syncthreads();
-    const int nhalf = X.ngroups * 2;  // half-groups of 8 elements
-    int bad = 0;
-    // every thread runs the same number of iterations so the pair shuffles stay converged
-    for (int base = 0; base < nhalf; base += GEMV_THREADS) {
-        int hg = base + tid;
-        bool live = hg < nhalf;
-        float v[8];
-        int e0 = hg * 8;
+// ── activation → digit records (LDS) ─────────────────────────────────────
+// Thread t owns octets o = t + 512·i (i < XO): elements [8o, 8o+8). They are
+// loaded first (before any weight traffic is queued), converted after the
+// weight loads are in flight. Four consecutive lanes form a 32-element group
+// with one exponent S.
+// Record contents by format (unit = the weights one lane handles per row):
+//  Q4_K unit u = 4b+j: sub-blocks 2j (slot 0) and 2j+1 (slot 1) of block b;
+//       slot s digits at s*96 + k*32 (8 dwords = 32 elements), meta at 192:
+//       {S0, S1, Σx slot0, Σx slot1}.
+//  Q6_K unit u = 4b+2h+g: 16 elements h*128+16g+32v+t (t<16) for v = 0..3;
+//       slot v digits at v*48 + k*16, meta at 192+16v: {S, 32Σd0, 32Σd1, 32Σd2}.
+//  Q8_0 unit u = block u: digits at k*32, meta at 96: {S}.
+template <int XO>
+__device__ __forceinline__ void load_x(const float* __restrict__ x, int k, int noct, float (&xv)[XO][8]) {
+    const bool vec = (k & 7) == 0;
 #pragma unroll
-        for (int t = 0; t < 8; t++) v[t] = (live && e0 + t < k) ? x[e0 + t] : 0.0f;
+    for (int i = 0; i < XO; i++) {
+        const int o = threadIdx.x + GEMV_THREADS * i;
+        const int e0 = o * 8;
+        if (vec && o < noct && e0 + 8 <= k) {
+            float4 a = *(const float4*)(x + e0), b = *(const float4*)(x + e0 + 4);
+            xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
+            xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; t++) xv[i][t] = (o < noct && e0 + t < k) ? x[e0 + t] : 0.0f;
+        }
+    }
+}
+
+template <int F, int XO>
+__device__ int build_records(const float (&xv)[XO][8], int noct, char* rec, int* flag) {
+    const int tid = threadIdx.x;
+    if (tid == 0) *flag = 0;
+    __syncthreads();
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < XO; i++) {
+        const int o = tid + GEMV_THREADS * i;
+        const bool live = o < noct;
+        const int e0 = o * 8;
+        const float* v = xv[i];
         float mx = 0.0f;
 #pragma unroll
         for (int t = 0; t < 8; t++) mx = fmaxf(mx, fabsf(v[t]));
         mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-        if (!isfinite(mx)) bad = 1;
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const bool fin = isfinite(mx);
+        if (!fin) bad = 1;
         int E = 0;
-        if (mx > 0.0f) (void)frexpf(mx, &E);
-        int S = (mx > 0.0f) ? 22 - E : 0;
+        if (mx > 0.0f && fin) (void)frexpf(mx, &E);
+        const int S = (mx > 0.0f && fin) ? 22 - E : 0;
         int d0[8], d1[8], d2[8];
-        float fs = 0.0f;
         int s0 = 0, s1 = 0, s2 = 0;
+        float fs = 0.0f;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            int xi = (mx > 0.0f && isfinite(mx)) ? (int)rintf(ldexpf(v[t], S)) : 0;
+            int xi = (mx > 0.0f && fin) ? (int)rintf(ldexpf(v[t], S)) : 0;
             int a = (xi << 24) >> 24;
             int r = (xi - a) >> 8;
             int b = (r << 24) >> 24;
@@ -77,334 +109,393 @@ __device__ int build_digits(const float* __restrict__ x, int k, XDigits X, int* 
             s0 += a; s1 += b; s2 += c;
             fs += v[t];
         }
-        fs += __shfl_xor(fs, 1, 64);
-        s0 += __shfl_xor(s0, 1, 64);
-        s1 += __shfl_xor(s1, 1, 64);
-        s2 += __shfl_xor(s2, 1, 64);
-        if (live) {
-            int q = hg * 2;
-            X.dig[q] = pack4(d0[0], d0[1], d0[2], d0[3]);
-            X.dig[q + 1] = pack4(d0[4], d0[5], d0[6], d0[7]);
-            X.dig[X.ngroups * 4 + q] = pack4(d1[0], d1[1], d1[2], d1[3]);
-            X.dig[X.ngroups * 4 + q + 1] = pack4(d1[4], d1[5], d1[6], d1[7]);
-            X.dig[X.ngroups * 8 + q] = pack4(d2[0], d2[1], d2[2], d2[3]);
-            X.dig[X.ngroups * 8 + q + 1] = pack4(d2[4], d2[5], d2[6], d2[7]);
-            if ((hg & 1) == 0) {
-                int g = hg >> 1;
-                X.gexp[g] = S;
-                X.gfsum[g] = fs;
-                X.gisum[g] = s0 << 5;
-                X.gisum[X.ngroups + g] = s1 << 5;
-                X.gisum[2 * X.ngroups + g] = s2 << 5;
+        const int qq = o & 3;  // octet within its 32-group
+        char* dst;
+        int koff;  // byte stride between the three digits
+        if (F == FMT_Q4K) {
+            const int G = e0 >> 5, b = G >> 3, sbi = G & 7;
+            char* r = rec + (size_t)(b * 4 + (sbi >> 1)) * Fmt<F>::RECB;
+            dst = r + (sbi & 1) * 96 + qq * 8;
+            koff = 32;
+            fs += __shfl_xor(fs, 1, 64);
+            fs += __shfl_xor(fs, 2, 64);
+            if (live && qq == 0) {
+                ((int*)(r + 192))[sbi & 1] = S;
+                ((float*)(r + 200))[sbi & 1] = fs;
             }
+        } else if (F == FMT_Q6K) {
+            const int b = e0 >> 8, eb = e0 & 255, h = eb >> 7, rr = eb & 127, vv = rr >> 5, w32 = rr & 31;
+            const int g = w32 >> 4, half8 = (w32 >> 3) & 1;
+            char* r = rec + (size_t)(b * 4 + h * 2 + g) * Fmt<F>::RECB;
+            dst = r + vv * 48 + half8 * 8;
+            koff = 16;
+            s0 += __shfl_xor(s0, 1, 64);
+            s1 += __shfl_xor(s1, 1, 64);
+            s2 += __shfl_xor(s2, 1, 64);
+            if (live && half8 == 0) {
+                int4 m;
+                m.x = S; m.y = s0 << 5; m.z = s1 << 5; m.w = s2 << 5;
+                *(int4*)(r + 192 + 16 * vv) = m;
+            }
+        } else {
+            char* r = rec + (size_t)(e0 >> 5) * Fmt<F>::RECB;
+            dst = r + qq * 8;
+            koff = 32;
+            if (live && qq == 0) *(int*)(r + 96) = S;
+        }
+        if (live) {
+            *(uint2*)(dst) = make_uint2(pack4(d0[0], d0[1], d0[2], d0[3]), pack4(d0[4], d0[5], d0[6], d0[7]));
+            *(uint2*)(dst + koff) = make_uint2(pack4(d1[0], d1[1], d1[2], d1[3]), pack4(d1[4], d1[5], d1[6], d1[7]));
+            *(uint2*)(dst + 2 * koff) =
+                make_uint2(pack4(d2[0], d2[1], d2[2], d2[3]), pack4(d2[4], d2[5], d2[6], d2[7]));
         }
     }
-    if (bad) *flag_smem = 1;
+    if (bad) *flag = 1;
     __syncthreads();
-    return *flag_smem;
+    return *flag;
 }
 
-__device__ __forceinline__ XDigits carve_lds(char* smem, int ngroups) {
-    XDigits X;
-    X.ngroups = ngroups;
-    X.dig = (int*)smem;
-    X.gexp = X.dig + 12 * ngroups;
-    X.gfsum = (float*)(X.gexp + ngroups);
-    X.gisum = (int*)(X.gfsum + ngroups);
-    return X;
+// ── per-format unit data, loads and dot products ─────────────────────────
+
+struct UQ4K { int4 q0, q1; uint4 hdr; };
+struct UQ6K { int4 a, b, h; uint2 sc; uint32_t d; };
+struct UQ80 { int4 q0, q1; uint32_t d; };
+
+template <int F> struct UnitT;
+template <> struct UnitT<FMT_Q4K> { typedef UQ4K T; };
+template <> struct UnitT<FMT_Q6K> { typedef UQ6K T; };
+template <> struct UnitT<FMT_Q80> { typedef UQ80 T; };
+
+struct Planes {
+    const uint8_t* p0;
+    const uint8_t* p1;
+    const uint8_t* p2;
+    const uint8_t* p3;
+};
+
+__device__ __forceinline__ void load_unit(UQ4K& d, const Planes& P, int64_t row, int nb, int u) {
+    const uint8_t* q = P.p1 + (row * nb) * 128 + (int64_t)u * 16;
+    d.q0 = *(const int4*)q;
+    d.q1 = *(const int4*)(q + nb * 64);
+    d.hdr = *(const uint4*)(P.p0 + (row * nb + (u >> 2)) * 16);
 }
 
-static inline size_t xdigits_lds_bytes(int ngroups) { return (size_t)ngroups * (12 + 1 + 1 + 3) * 4 + 16; }
-
-// Integer dot of 16 weights (4 dwords of signed/unsigned bytes) with the
-// digits of group g: returns the three digit accumulators.
-struct Dot3 { int a0, a1, a2; };
-
-__device__ __forceinline__ Dot3 dot16(const int4 wq, const XDigits& X, int g) {
-    const int4 D0 = *(const int4*)(X.dig + g * 4);
-    const int4 D1 = *(const int4*)(X.dig + X.ngroups * 4 + g * 4);
-    const int4 D2 = *(const int4*)(X.dig + X.ngroups * 8 + g * 4);
-    Dot3 r;
-    r.a0 = sdot4(wq.w, D0.w, sdot4(wq.z, D0.z, sdot4(wq.y, D0.y, sdot4(wq.x, D0.x, 0))));
-    r.a1 = sdot4(wq.w, D1.w, sdot4(wq.z, D1.z, sdot4(wq.y, D1.y, sdot4(wq.x, D1.x, 0))));
-    r.a2 = sdot4(wq.w, D2.w, sdot4(wq.z, D2.z, sdot4(wq.y, D2.y, sdot4(wq.x, D2.x, 0))));
-    return r;
+__device__ __forceinline__ void load_unit(UQ6K& d, const Planes& P, int64_t row, int nb, int u) {
+    const int b = u >> 2, h = (u >> 1) & 1;
+    const int64_t blk = row * nb + b;
+    const uint8_t* ql = P.p0 + (row * nb) * 128 + (int64_t)u * 16;
+    d.a = *(const int4*)ql;
+    d.b = *(const int4*)(ql + nb * 64);
+    d.h = *(const int4*)(P.p1 + (row * nb) * 64 + (int64_t)u * 16);
+    d.sc = *(const uint2*)(P.p2 + blk * 16 + h * 8);
+    d.d = ((const uint16_t*)P.p3)[blk];
 }
 
-// Σ q·x over the group as f32 from the digit accumulators.
-__device__ __forceinline__ float dot3_value(Dot3 r, int S) {
-    float v = (float)r.a2 * 65536.0f + (float)(r.a0 + (r.a1 << 8));
-    return ldexpf(v, -S);
+__device__ __forceinline__ void load_unit(UQ80& d, const Planes& P, int64_t row, int nb, int u) {
+    const uint8_t* q = P.p0 + (row * nb) * 32 + (int64_t)u * 16;
+    d.q0 = *(const int4*)q;
+    d.q1 = *(const int4*)(q + nb * 16);
+    d.d = ((const uint16_t*)P.p1)[row * nb + u];
 }
 
-// get_scale_min_k4 (common.rs:29-38) on the header dwords y = scales[0..3],
-// z = scales[4..7], w = scales[8..11], for sub-block s in [0,8).
-__device__ __forceinline__ void k4_scale_min(uint32_t y, uint32_t z, uint32_t w, int s, float& sc, float& m) {
-    int t = s & 3;
-    uint32_t ylo = (y >> (8 * t)) & 0xFFu, zlo = (z >> (8 * t)) & 0xFFu, wb = (w >> (8 * t)) & 0xFFu;
-    uint32_t sc_lo = ylo & 63u, m_lo = zlo & 63u;
-    uint32_t sc_hi = (wb & 0x0Fu) | ((ylo >> 6) << 4), m_hi = (wb >> 4) | ((zlo >> 6) << 4);
-    bool hi = s >= 4;
-    sc = (float)(hi ? sc_hi : sc_lo);
-    m = (float)(hi ? m_hi : m_lo);
+// Digit record held in registers (or read from LDS per use).
+template <int F> struct Rec { uint4 v[Fmt<F>::RECB / 16]; };
+
+template <int F>
+__device__ __forceinline__ void read_rec(Rec<F>& r, const char* p) {
+#pragma unroll
+    for (int i = 0; i < Fmt<F>::RECB / 16; i++) r.v[i] = *(const uint4*)(p + 16 * i);
 }
 
-struct RowRange { int64_t begin, end; };
+__device__ __forceinline__ int dot8(const int* q, const uint4* D0) {
+    const int* d = (const int*)D0;
+    int a = 0;
+#pragma unroll
+    for (int m = 0; m < 8; m++) a = sdot4(q[m], d[m], a);
+    return a;
+}
 
-// Contiguous rows of this wave: the grid splits [0,n) evenly over workgroups,
-// each workgroup evenly over its waves.
-__device__ __forceinline__ RowRange wave_rows(int64_t n) {
-    int64_t per_wg = (n + gridDim.x - 1) / gridDim.x;
-    int64_t wg0 = (int64_t)blockIdx.x * per_wg;
-    int64_t wg1 = min(n, wg0 + per_wg);
-    int64_t per_wave = (per_wg + GEMV_WAVES - 1) / GEMV_WAVES;
-    int wave = threadIdx.x >> 6;
-    RowRange r;
-    r.begin = min(wg1, wg0 + wave * per_wave);
-    r.end = min(wg1, r.begin + per_wave);
-    return r;
+__device__ __forceinline__ int dot4v(const int* q, const uint4& D) {
+    return sdot4(q[3], (int)D.w, sdot4(q[2], (int)D.z, sdot4(q[1], (int)D.y, sdot4(q[0], (int)D.x, 0))));
+}
+
+// get_scale_min_k4 (common.rs:29-38) for sub-blocks 2j and 2j+1 on the
+// header dwords y = scales[0..3], z = scales[4..7], w = scales[8..11].
+__device__ __forceinline__ void k4_pair(uint32_t y, uint32_t z, uint32_t w, int j, float& sc0, float& m0,
+                                        float& sc1, float& m1) {
+    // bytes of the 4 low (j<2) or 4 high (j>=2) sub-blocks' 6-bit values
+    uint32_t sc4 = (j < 2) ? (y & 0x3F3F3F3Fu) : ((w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u));
+    uint32_t m4 = (j < 2) ? (z & 0x3F3F3F3Fu) : (((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u));
+    const int sh = (j & 1) * 16;
+    sc4 >>= sh;
+    m4 >>= sh;
+    sc0 = (float)(sc4 & 0xFFu);
+    sc1 = (float)((sc4 >> 8) & 0xFFu);
+    m0 = (float)(m4 & 0xFFu);
+    m1 = (float)((m4 >> 8) & 0xFFu);
+}
+
+// Q4_K unit u = 4b + j of a row: qs bytes [32j, 32j+32) of block b.
+__device__ __forceinline__ float unit_dot(const UQ4K& d, const Rec<FMT_Q4K>& R, int j) {
+    int lo[8], hi[8];
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        int w = m < 4 ? ((const int*)&d.q0)[m] : ((const int*)&d.q1)[m - 4];
+        lo[m] = w & 0x0F0F0F0F;
+        hi[m] = (w >> 4) & 0x0F0F0F0F;
+    }
+    // slot 0 digits: R.v[0..5] (k*2 int4 each), slot 1: R.v[6..11], meta R.v[12]
+    int l0 = dot8(lo, &R.v[0]), l1 = dot8(lo, &R.v[2]), l2 = dot8(lo, &R.v[4]);
+    int h0 = dot8(hi, &R.v[6]), h1 = dot8(hi, &R.v[8]), h2 = dot8(hi, &R.v[10]);
+    // |Σ q·x_int| ≤ 32·15·2^22 < 2^31: digits recombine exactly in i32
+    float vlo = ldexpf((float)(l0 + (l1 << 8) + (l2 << 16)), -(int)R.v[12].x);
+    float vhi = ldexpf((float)(h0 + (h1 << 8) + (h2 << 16)), -(int)R.v[12].y);
+    float fslo = __int_as_float((int)R.v[12].z), fshi = __int_as_float((int)R.v[12].w);
+    float dd = aeth_decode_d(d.hdr.x), dmin = aeth_decode_d(d.hdr.x >> 16);
+    float sc0, m0, sc1, m1;
+    k4_pair(d.hdr.y, d.hdr.z, d.hdr.w, j, sc0, m0, sc1, m1);
+    return dd * (sc0 * vlo + sc1 * vhi) - dmin * (m0 * fslo + m1 * fshi);
+}
+
+// Q6_K unit u = 4b + 2h + g.
+__device__ __forceinline__ float unit_dot(const UQ6K& d, const Rec<FMT_Q6K>& R, int /*unused*/) {
+    const int* A = (const int*)&d.a;
+    const int* B = (const int*)&d.b;
+    const int* H = (const int*)&d.h;
+    float part = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        int q[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (v == 0) q[e] = (A[e] & 0x0F0F0F0F) | ((H[e] << 4) & 0x30303030);
+            else if (v == 1) q[e] = (B[e] & 0x0F0F0F0F) | ((H[e] << 2) & 0x30303030);
+            else if (v == 2) q[e] = ((A[e] >> 4) & 0x0F0F0F0F) | (H[e] & 0x30303030);
+            else q[e] = ((B[e] >> 4) & 0x0F0F0F0F) | ((H[e] >> 2) & 0x30303030);
+        }
+        const uint4 meta = R.v[12 + v];
+        // quants are stored as q+32 in [0,63]: subtract 32·Σdigit per digit (exact)
+        int a0 = dot4v(q, R.v[3 * v]) - (int)meta.y;
+        int a1 = dot4v(q, R.v[3 * v + 1]) - (int)meta.z;
+        int a2 = dot4v(q, R.v[3 * v + 2]) - (int)meta.w;
+        float val = ldexpf((float)a2 * 65536.0f + (float)(a0 + (a1 << 8)), -(int)meta.x);
+        uint32_t sw = v < 2 ? d.sc.x : d.sc.y;  // sc[h*8 + g + 2v], pre-shifted by fix_unit
+        float sc = (float)(int8_t)((sw >> (16 * (v & 1))) & 0xFFu);
+        part += sc * val;
+    }
+    return aeth_decode_d(d.d) * part;
+}
+
+// Q8_0 unit = one block.
+__device__ __forceinline__ float unit_dot(const UQ80& d, const Rec<FMT_Q80>& R, int /*unused*/) {
+    int q[8];
+#pragma unroll
+    for (int m = 0; m < 4; m++) { q[m] = ((const int*)&d.q0)[m]; q[m + 4] = ((const int*)&d.q1)[m]; }
+    int a0 = dot8(q, &R.v[0]), a1 = dot8(q, &R.v[2]), a2 = dot8(q, &R.v[4]);
+    float val = ldexpf((float)a2 * 65536.0f + (float)(a0 + (a1 << 8)), -(int)R.v[6].x);
+    return aeth_f16_to_f32(d.d) * val;
+}
+
+// Q6_K scale bytes: the lane's g selects odd/even bytes of sc[h*8 .. h*8+8);
+// shifting once per load leaves byte g+2v at bit 16(v&1) of word v/2.
+__device__ __forceinline__ void fix_unit(UQ6K& d, int g) {  // g = u & 1
+    d.sc.x >>= 8 * g;
+    d.sc.y >>= 8 * g;
+}
+__device__ __forceinline__ void fix_unit(UQ4K&, int) {}
+__device__ __forceinline__ void fix_unit(UQ80&, int) {}
+
+// ── reductions: R row sums spread over the wave → one value per row ──────
+// Reduce-scatter butterfly: each of the first log2(R) exchange steps halves
+// the number of live row sums per lane (lanes on the two sides of the step's
+// bit keep different halves), the remaining steps finish the sum. Afterwards
+// lane L holds the total of row_of_lane<R>(L), written by the lanes where
+// (L & (64/R - 1)) == 0. Six exchange steps move R-1 + 6-log2(R) values
+// per lane instead of 6·R.
+template <int R>
+__device__ __forceinline__ float wave_reduce_rows(const float (&a)[R], int lane) {
+    float v[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) v[i] = a[i];
+    int bit = 32;
+#pragma unroll
+    for (int n = R; n > 1; n >>= 1) {
+        const bool hi = lane & bit;
+#pragma unroll
+        for (int i = 0; i < n / 2; i++) {
+            float keep = hi ? v[n / 2 + i] : v[i];
+            float send = hi ? v[i] : v[n / 2 + i];
+            v[i] = keep + __shfl_xor(send, bit, 64);
+        }
+        bit >>= 1;
+    }
+#pragma unroll
+    for (int off = 64 / R / 2; off >= 1; off >>= 1) v[0] += __shfl_xor(v[0], off, 64);
+    return v[0];
 }
 
 template <int R>
-__device__ __forceinline__ void store_rows(float (&acc)[R], int64_t row0, int64_t row_end, float* y,
-                                           const float* resid) {
+__device__ __forceinline__ int row_of_lane(int lane) {
+    int row = 0, bit = 32, w = R / 2;
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = aeth_wave_sum(acc[r]);
-    if ((threadIdx.x & 63) == 0) {
+    for (int n = R; n > 1; n >>= 1) {
+        if (lane & bit) row += w;
+        w >>= 1;
+        bit >>= 1;
+    }
+    return row;
+}
+
+// ── the kernel ───────────────────────────────────────────────────────────
+// WPR waves share a row (wave w of a row handles units [64w, 64w+64)), so
+// each lane owns exactly one unit and keeps its digit record in registers;
+// the 8 waves form 8/WPR row streams. R rows per pass; XO activation octets
+// per thread.
+template <int F, int WPR, int R, int XO>
+__global__ void __launch_bounds__(GEMV_THREADS) k_gemv(Planes P, int64_t n, int nb, int upr,
+                                                     const float* __restrict__ x, int k, int64_t x_stride,
+                                                     float* __restrict__ y, int64_t y_stride, int accumulate,
+                                                     int64_t rows_per_wg, int npass) {
+    constexpr int STREAMS = GEMV_WAVES / WPR;
+    extern __shared__ __attribute__((aligned(16))) char rec[];
+    __shared__ int flag;
+    typedef typename UnitT<F>::T U;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int stream = wave / WPR, wir = wave - stream * WPR;
+    const int u = wir * 64 + lane;
+    const bool valid = u < upr;
+    const float* xr = x + (int64_t)blockIdx.y * x_stride;
+    float* yr = y + (int64_t)blockIdx.y * y_stride;
+    const int64_t wg0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int64_t wg1 = min(n, wg0 + rows_per_wg);
+    const int64_t rps = (rows_per_wg + STREAMS - 1) / STREAMS;
+    const int64_t sb = min(wg1, wg0 + stream * rps);
+    const int64_t se = min(wg1, sb + rps);
+    const int j4 = u & 3;  // Q4_K: sub-block pair of this lane's unit
+    const int noct = upr * Fmt<F>::UE / 8;
+    float* red = (float*)(rec + (size_t)upr * Fmt<F>::RECB);  // [2][STREAMS][WPR][R] when WPR > 1
+
+    float xv[XO][8];
+    load_x<XO>(xr, k, noct, xv);
+
+    // Ring of R row buffers: row i of this stream lives in buf[i % R]; each
+    // buffer is refilled with the row R ahead as soon as it has been consumed,
+    // so every wave keeps R rows of loads in flight and computes on arrival.
+    U buf[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        if (valid && sb < se) {
+            load_unit(buf[r], P, min(sb + r, se - 1), nb, u);
+            fix_unit(buf[r], u & 1);
+        }
+    }
+
+    if (build_records<F, XO>(xv, noct, rec, &flag)) {
+        if (wir == 0)
+            for (int64_t row = sb + lane; row < se; row += 64) yr[row] = __int_as_float(0x7FC00000);
+        return;
+    }
+    Rec<F> reg;
+    if (valid) read_rec<F>(reg, rec + (size_t)u * Fmt<F>::RECB);
+
+    for (int p = 0; p < npass; p++) {
+        const int64_t row0 = sb + (int64_t)p * R;
+        float acc[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            int64_t row = row0 + r;
-            if (row < row_end) y[row] = resid ? resid[row] + acc[r] : acc[r];
-        }
-    }
-}
-
-__device__ __forceinline__ void fill_nan(int64_t n, float* y) {
-    RowRange rr = wave_rows(n);
-    for (int64_t row = rr.begin + (threadIdx.x & 63); row < rr.end; row += 64) y[row] = __int_as_float(0x7FC00000);
-}
-
-// ── Q4_K: planes hdr[row*nb+b][16], qs[row*nb+b][128]. Chunk c (of nb*8):
-// block b = c/8, i = c%8 → qs bytes [16i,16i+16): low nibbles are elements
-// 64j+16h+t (sub-block 2j), high nibbles 64j+32+16h+t (sub-block 2j+1),
-// j = i/2, h = i%2, t = 0..15.
-template <int R>
-__global__ void __launch_bounds__(GEMV_THREADS) k_gemv_q4k(const uint8_t* __restrict__ hdr,
-                                                         const uint8_t* __restrict__ qs, int64_t n, int nb,
-                                                         const float* __restrict__ x, int k, int64_t x_stride,
-                                                         float* __restrict__ y, int64_t y_stride, int accumulate) {
-    extern __shared__ char smem[];
-    __shared__ int flag;
-    const int ngroups = nb * 16;
-    XDigits X = carve_lds(smem, ngroups);
-    const float* xr = x + (int64_t)blockIdx.y * x_stride;
-    float* yr = y + (int64_t)blockIdx.y * y_stride;
-    if (build_digits(xr, k, X, &flag)) { fill_nan(n, yr); return; }
-    const float* resid = accumulate ? yr : nullptr;
-    const int lane = threadIdx.x & 63;
-    const int cpr = nb * 8;
-    RowRange rr = wave_rows(n);
-    for (int64_t row0 = rr.begin; row0 < rr.end; row0 += R) {
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = 0.0f;
-        for (int c = lane; c < cpr; c += 64) {
-            const int b = c >> 3, i = c & 7, j = i >> 1, h = i & 1;
-            const int glo = b * 16 + j * 4 + h, ghi = glo + 2;
-            int4 wv[R];
-            uint4 hv[R];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                int64_t row = min(row0 + r, rr.end - 1);
-                wv[r] = *(const int4*)(qs + (row * nb) * 128 + (int64_t)c * 16);
-                hv[r] = *(const uint4*)(hdr + (row * nb + b) * 16);
-            }
-            const int Slo = X.gexp[glo], Shi = X.gexp[ghi];
-            const float fslo = X.gfsum[glo], fshi = X.gfsum[ghi];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                int4 lo, hi;
-                lo.x = wv[r].x & 0x0F0F0F0F; hi.x = (wv[r].x >> 4) & 0x0F0F0F0F;
-                lo.y = wv[r].y & 0x0F0F0F0F; hi.y = (wv[r].y >> 4) & 0x0F0F0F0F;
-                lo.z = wv[r].z & 0x0F0F0F0F; hi.z = (wv[r].z >> 4) & 0x0F0F0F0F;
-                lo.w = wv[r].w & 0x0F0F0F0F; hi.w = (wv[r].w >> 4) & 0x0F0F0F0F;
-                Dot3 dl = dot16(lo, X, glo), dh = dot16(hi, X, ghi);
-                // |Σ q·x_int| < 16·15·2^22 < 2^31: the digits combine exactly in i32.
-                float vlo = ldexpf((float)(dl.a0 + (dl.a1 << 8) + (dl.a2 << 16)), -Slo);
-                float vhi = ldexpf((float)(dh.a0 + (dh.a1 << 8) + (dh.a2 << 16)), -Shi);
-                float d = aeth_decode_d(hv[r].x), dmin = aeth_decode_d(hv[r].x >> 16);
-                float sclo, mlo, schi, mhi;
-                k4_scale_min(hv[r].y, hv[r].z, hv[r].w, 2 * j, sclo, mlo);
-                k4_scale_min(hv[r].y, hv[r].z, hv[r].w, 2 * j + 1, schi, mhi);
-                acc[r] += d * (sclo * vlo + schi * vhi) - dmin * (mlo * fslo + mhi * fshi);
+            acc[r] = (valid && row0 + r < se) ? unit_dot(buf[r], reg, j4) : 0.0f;
+            if (valid && p + 1 < npass && row0 + R < se) {
+                load_unit(buf[r], P, min(row0 + R + r, se - 1), nb, u);
+                fix_unit(buf[r], u & 1);
             }
         }
-        store_rows<R>(acc, row0, rr.end, yr, resid);
-    }
-}
-
-// ── Q6_K: planes ql[row*nb+b][128], qh[..][64], sc[..][16], d[..] (f16).
-// Chunk c (of nb*4): block b = c/4, half h = (c/2)%2, g = c%2, t = 0..15:
-// A = ql[h*64+16g+t], B = ql[h*64+32+16g+t], H = qh[h*32+16g+t] give the
-// 6-bit quants of elements h*128 + 16g + 32u + t for u = 0..3, whose scale
-// is sc[h*8 + g + 2u] (dequant.rs:301-348).
-template <int R>
-__global__ void __launch_bounds__(GEMV_THREADS) k_gemv_q6k(const uint8_t* __restrict__ ql,
-                                                         const uint8_t* __restrict__ qh,
-                                                         const uint8_t* __restrict__ scp,
-                                                         const uint16_t* __restrict__ dp, int64_t n, int nb,
-                                                         const float* __restrict__ x, int k, int64_t x_stride,
-                                                         float* __restrict__ y, int64_t y_stride, int accumulate) {
-    extern __shared__ char smem[];
-    __shared__ int flag;
-    const int ngroups = nb * 16;
-    XDigits X = carve_lds(smem, ngroups);
-    const float* xr = x + (int64_t)blockIdx.y * x_stride;
-    float* yr = y + (int64_t)blockIdx.y * y_stride;
-    if (build_digits(xr, k, X, &flag)) { fill_nan(n, yr); return; }
-    const float* resid = accumulate ? yr : nullptr;
-    const int lane = threadIdx.x & 63;
-    const int cpr = nb * 4;
-    RowRange rr = wave_rows(n);
-    for (int64_t row0 = rr.begin; row0 < rr.end; row0 += R) {
-        float acc[R];
+        float tot = wave_reduce_rows<R>(acc, lane);
+        const int myrow = row_of_lane<R>(lane);
+        const bool writer = (lane & (64 / R - 1)) == 0;
+        if (WPR == 1) {
+            const int64_t row = row0 + myrow;
+            if (writer && row < se) yr[row] = accumulate ? yr[row] + tot : tot;
+        } else {
+            float* rb = red + (p & 1) * (STREAMS * WPR * R);
+            if (writer) rb[(stream * WPR + wir) * R + myrow] = tot;
+            __syncthreads();
+            if (threadIdx.x < STREAMS * R) {
+                const int s2 = threadIdx.x / R, r2 = threadIdx.x - s2 * R;
+                const int64_t sb2 = min(wg1, wg0 + s2 * rps), se2 = min(wg1, sb2 + rps);
+                const int64_t row = sb2 + (int64_t)p * R + r2;
+                if (row < se2) {
+                    float t = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = 0.0f;
-        for (int c = lane; c < cpr; c += 64) {
-            const int b = c >> 2, h = (c >> 1) & 1, g = c & 1;
-            const int g0 = b * 16 + h * 8 + g;  // group of u = 0; u adds 2
-            int4 Av[R], Bv[R], Hv[R];
-            uint2 Sv[R];
-            uint32_t dv[R];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                int64_t row = min(row0 + r, rr.end - 1);
-                int64_t blk = row * nb + b;
-                Av[r] = *(const int4*)(ql + blk * 128 + h * 64 + g * 16);
-                Bv[r] = *(const int4*)(ql + blk * 128 + h * 64 + 32 + g * 16);
-                Hv[r] = *(const int4*)(qh + blk * 64 + h * 32 + g * 16);
-                Sv[r] = *(const uint2*)(scp + blk * 16 + h * 8);
-                dv[r] = dp[blk];
-            }
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float part = 0.0f;
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    int4 q;
-                    const int* A = (const int*)&Av[r];
-                    const int* B = (const int*)&Bv[r];
-                    const int* H = (const int*)&Hv[r];
-                    int* Q = (int*)&q;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        int v;
-                        if (u == 0) v = (A[e] & 0x0F0F0F0F) | ((H[e] << 4) & 0x30303030);
-                        else if (u == 1) v = (B[e] & 0x0F0F0F0F) | ((H[e] << 2) & 0x30303030);
-                        else if (u == 2) v = ((A[e] >> 4) & 0x0F0F0F0F) | (H[e] & 0x30303030);
-                        else v = ((B[e] >> 4) & 0x0F0F0F0F) | ((H[e] >> 2) & 0x30303030);
-                        Q[e] = v;
-                    }
-                    const int grp = g0 + 2 * u;
-                    Dot3 dd = dot16(q, X, grp);
-                    // quants are stored as q+32 in [0,63]; subtract 32·Σdigit per digit (exact)
-                    dd.a0 -= X.gisum[grp];
-                    dd.a1 -= X.gisum[X.ngroups + grp];
-                    dd.a2 -= X.gisum[2 * X.ngroups + grp];
-                    float v = dot3_value(dd, X.gexp[grp]);
-                    int sbyte = g + 2 * u;  // byte within sc[h*8 .. h*8+8)
-                    uint32_t sw = sbyte < 4 ? Sv[r].x : Sv[r].y;
-                    float sc = (float)(int8_t)((sw >> (8 * (sbyte & 3))) & 0xFFu);
-                    part += sc * v;
+                    for (int w = 0; w < WPR; w++) t += rb[(s2 * WPR + w) * R + r2];
+                    yr[row] = accumulate ? yr[row] + t : t;
                 }
-                acc[r] += aeth_decode_d(dv[r]) * part;
             }
         }
-        store_rows<R>(acc, row0, rr.end, yr, resid);
     }
 }
 
-// ── Q8_0: planes qs[row*nb+b][32] (int8), d[row*nb+b] (f16). Chunk c (of
-// nb*2) = elements [16c, 16c+16) = group c, block c/2.
-template <int R>
-__global__ void __launch_bounds__(GEMV_THREADS) k_gemv_q8_0(const uint8_t* __restrict__ qs,
-                                                          const uint16_t* __restrict__ dp, int64_t n, int nb,
-                                                          const float* __restrict__ x, int k, int64_t x_stride,
-                                                          float* __restrict__ y, int64_t y_stride, int accumulate) {
-    extern __shared__ char smem[];
-    __shared__ int flag;
-    const int ngroups = nb * 2;
-    XDigits X = carve_lds(smem, ngroups);
-    const float* xr = x + (int64_t)blockIdx.y * x_stride;
-    float* yr = y + (int64_t)blockIdx.y * y_stride;
-    if (build_digits(xr, k, X, &flag)) { fill_nan(n, yr); return; }
-    const float* resid = accumulate ? yr : nullptr;
-    const int lane = threadIdx.x & 63;
-    const int cpr = nb * 2;
-    RowRange rr = wave_rows(n);
-    for (int64_t row0 = rr.begin; row0 < rr.end; row0 += R) {
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = 0.0f;
-        for (int c = lane; c < cpr; c += 64) {
-            int4 wv[R];
-            uint32_t dv[R];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                int64_t row = min(row0 + r, rr.end - 1);
-                wv[r] = *(const int4*)(qs + (row * nb) * 32 + (int64_t)c * 16);
-                dv[r] = dp[row * nb + (c >> 1)];
-            }
-            const int S = X.gexp[c];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                Dot3 dd = dot16(wv[r], X, c);
-                acc[r] += aeth_f16_to_f32(dv[r]) * dot3_value(dd, S);
-            }
-        }
-        store_rows<R>(acc, row0, rr.end, yr, resid);
-    }
+// ── dispatch ─────────────────────────────────────────────────────────────
+
+static int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
 }
 
-static int gemv_grid(int64_t n) {
-    static int wg_per_cu = -1;
-    if (wg_per_cu < 0) {
-        const char* e = getenv("AETH_GEMV_WG_PER_CU");
-        wg_per_cu = e ? atoi(e) : 2;
-        if (wg_per_cu < 1) wg_per_cu = 1;
-    }
-    int64_t g = (int64_t)aeth_num_cus() * wg_per_cu;
-    int64_t need = (n + GEMV_WAVES - 1) / GEMV_WAVES;
-    if (need < g) g = need;
-    return (int)(g < 1 ? 1 : g);
+template <int F, int WPR, int R, int XO>
+static void launch(dim3 grid, size_t lds, hipStream_t s, const Planes& P, int64_t n, int nb, int upr, const float* x,
+                   int k, float* y, int acc, int64_t rpg) {
+    constexpr int STREAMS = GEMV_WAVES / WPR;
+    const int64_t rps = (rpg + STREAMS - 1) / STREAMS;
+    const int npass = (int)((rps + R - 1) / R);
+    hipLaunchKernelGGL((k_gemv<F, WPR, R, XO>), grid, dim3(GEMV_THREADS), lds, s, P, n, nb, upr, x, k, (int64_t)k, y,
+                       n, acc, rpg, npass);
 }
 
-int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags,
-                     hipStream_t s) {
+template <int F>
+static int dispatch_fmt(const Planes& P, int64_t n, int nb, int k, int upr, const float* x, int64_t m, float* y,
+                        int acc, hipStream_t s) {
+    static const int wg_per_cu = env_int("AETH_GEMV_WG_PER_CU", 1);
+    static const int rsel = env_int("AETH_GEMV_R", 4);
+    int wpr = 1;
+    while (wpr * 64 < upr) wpr *= 2;
+    const int noct = upr * Fmt<F>::UE / 8;
+    int xo = 1;
+    while (xo * GEMV_THREADS < noct) xo *= 2;
+    const size_t lds = (size_t)upr * Fmt<F>::RECB + (wpr > 1 ? 2 * GEMV_WAVES * 4 * sizeof(float) : 0);
+    if (wpr > 8 || xo > 4 || lds > 64 * 1024)
+        return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d is beyond this kernel's range", k);
+    int64_t grid = (int64_t)aeth_num_cus() * (wg_per_cu < 1 ? 1 : wg_per_cu);
+    const int64_t need = (n + (GEMV_WAVES / wpr) - 1) / (GEMV_WAVES / wpr);
+    if (need < grid) grid = need;
+    if (grid < 1) grid = 1;
+    const int64_t rpg = (n + grid - 1) / grid;
+    dim3 g((unsigned)grid, (unsigned)m);
+#define L_(W, RR, X) launch<F, W, RR, X>(g, lds, s, P, n, nb, upr, x, k, y, acc, rpg)
+    if (wpr == 1 && xo == 1) {
+        if (rsel == 2) L_(1, 2, 1);
+        else if (rsel == 8) L_(1, 8, 1);
+        else L_(1, 4, 1);
+    } else if (wpr == 2 && xo == 1) L_(2, 4, 1);
+    else if (wpr == 2 && xo == 2) L_(2, 4, 2);
+    else if (wpr == 4 && xo == 2) L_(4, 4, 2);
+    else if (wpr == 4 && xo == 4) L_(4, 4, 4);
+    else if (wpr == 8 && xo == 4) L_(8, 4, 4);
+    else if (wpr == 1 && xo == 2) L_(1, 4, 2);
+    else if (wpr == 2 && xo == 4) L_(2, 4, 4);
+    else return aeth_set_error(AETH_EUNSUPPORTED, "gemv: no kernel for k=%d (wpr %d, xo %d)", k, wpr, xo);
+#undef L_
+    AETH_LAUNCH_CHECK();
+    return AETH_OK;
+}
+
+int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags, hipStream_t s) {
     if (m > 65535) return aeth_set_error(AETH_EINVAL, "gemv: m=%lld exceeds 65535", (long long)m);
     const int nb = (int)w->nb;
     const int k = (int)w->k;
     const int acc = (flags & AETH_MM_ACCUMULATE) ? 1 : 0;
-    dim3 grid(gemv_grid(w->n), (unsigned)m);
-    dim3 block(GEMV_THREADS);
-    if (w->dtype == AETH_DTYPE_Q4_K) {
-        size_t lds = xdigits_lds_bytes(nb * 16);
-        if (lds > 150 * 1024) return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d too large for LDS", k);
-        hipLaunchKernelGGL(k_gemv_q4k<4>, grid, block, lds, s, w->p0, w->p1, w->n, nb, d_x, k, (int64_t)k, d_y,
-                           w->n, acc);
-    } else if (w->dtype == AETH_DTYPE_Q6_K) {
-        size_t lds = xdigits_lds_bytes(nb * 16);
-        if (lds > 150 * 1024) return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d too large for LDS", k);
-        hipLaunchKernelGGL(k_gemv_q6k<4>, grid, block, lds, s, w->p0, w->p1, w->p2, (const uint16_t*)w->p3, w->n,
-                           nb, d_x, k, (int64_t)k, d_y, w->n, acc);
-    } else if (w->dtype == AETH_DTYPE_Q8_0) {
-        size_t lds = xdigits_lds_bytes(nb * 2);
-        if (lds > 150 * 1024) return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d too large for LDS", k);
-        hipLaunchKernelGGL(k_gemv_q8_0<4>, grid, block, lds, s, w->p0, (const uint16_t*)w->p1, w->n, nb, d_x, k,
-                           (int64_t)k, d_y, w->n, acc);
-    } else {
-        return aeth_set_error(AETH_EUNSUPPORTED, "gemv: dtype %d", w->dtype);
-    }
-    AETH_LAUNCH_CHECK();
-    return AETH_OK;
+    Planes P{w->p0, w->p1, w->p2, w->p3};
+    if (w->dtype == AETH_DTYPE_Q4_K) return dispatch_fmt<FMT_Q4K>(P, w->n, nb, k, nb * 4, d_x, m, d_y, acc, s);
+    if (w->dtype == AETH_DTYPE_Q6_K) return dispatch_fmt<FMT_Q6K>(P, w->n, nb, k, nb * 4, d_x, m, d_y, acc, s);
+    if (w->dtype == AETH_DTYPE_Q8_0) return dispatch_fmt<FMT_Q80>(P, w->n, nb, k, nb, d_x, m, d_y, acc, s);
+    return aeth_set_error(AETH_EUNSUPPORTED, "gemv: dtype %d", w->dtype);
 }

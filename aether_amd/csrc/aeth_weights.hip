@@ -64,35 +64,58 @@ int64_t aeth_blocks_per_row(int dtype, int64_t k) {
 }
 
 // ── planar layout ────────────────────────────────────────────────────────
-// Q4_K: p0 = hdr[nblk][16] (d, dmin, scales[12]), p1 = qs[nblk][128]
-// Q6_K: p0 = ql[nblk][128], p1 = qh[nblk][64], p2 = sc[nblk][16], p3 = d[nblk] (u16)
-// Q8_0: p0 = qs[nblk][32], p1 = d[nblk] (u16)
-// Block index = row * blocks_per_row + b, so each row's fields are contiguous.
+// Per row (nb blocks), fields are split into planes and the quant bytes are
+// ordered by the GEMV's lane "units" so that every wave load is contiguous:
+//  Q4_K: p0 = hdr[row*nb + b][16] (d, dmin, scales[12]);
+//        p1 = qs, per row 2 halves of nb*64 bytes: unit u = 4b+j owns qs bytes
+//        [32j, 32j+32) of block b; its first 16 bytes sit at 16u, its second
+//        16 bytes at nb*64 + 16u.
+//  Q6_K: p0 = ql, per row 2 halves of nb*64 bytes: unit u = 4b+2h+g owns
+//        A = ql[h*64+16g, +16) at 16u and B = ql[h*64+32+16g, +16) at
+//        nb*64 + 16u; p1 = qh[row*nb + b][64] (= 16 bytes per unit in unit
+//        order); p2 = sc[row*nb + b][16]; p3 = d[row*nb + b] (f16).
+//  Q8_0: p0 = qs, per row 2 halves of nb*16 bytes: block b's quants [0,16)
+//        at 16b and [16,32) at nb*16 + 16b; p1 = d[row*nb + b] (f16).
 
 static int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
-__global__ void k_relayout(int dtype, uint8_t* __restrict__ raw, uint8_t* __restrict__ p0,
+// Maps raw GGUF byte i (block-major over all rows) to its planar address.
+__device__ __forceinline__ uint8_t* planar_addr(int dtype, int64_t i, int64_t nb, uint8_t* p0, uint8_t* p1,
+                                                uint8_t* p2, uint8_t* p3) {
+    if (dtype == AETH_DTYPE_Q4_K) {
+        int64_t blk = i / Q4K_BLOCK_BYTES;
+        int off = (int)(i - blk * Q4K_BLOCK_BYTES);
+        if (off < 16) return p0 + blk * 16 + off;
+        int64_t row = blk / nb, b = blk - row * nb;
+        int t = off - 16, j = t >> 5, half = (t >> 4) & 1, pos = t & 15;
+        return p1 + row * nb * 128 + half * (nb * 64) + (b * 4 + j) * 16 + pos;
+    }
+    if (dtype == AETH_DTYPE_Q6_K) {
+        int64_t blk = i / Q6K_BLOCK_BYTES;
+        int off = (int)(i - blk * Q6K_BLOCK_BYTES);
+        if (off < 128) {
+            int64_t row = blk / nb, b = blk - row * nb;
+            int h = off >> 6, r = off & 63, half = r >> 5, g = (r >> 4) & 1, pos = r & 15;
+            return p0 + row * nb * 128 + half * (nb * 64) + (b * 4 + h * 2 + g) * 16 + pos;
+        }
+        if (off < 192) return p1 + blk * 64 + (off - 128);
+        if (off < 208) return p2 + blk * 16 + (off - 192);
+        return p3 + blk * 2 + (off - 208);
+    }
+    int64_t blk = i / Q8_BLOCK_BYTES;
+    int off = (int)(i - blk * Q8_BLOCK_BYTES);
+    if (off < 2) return p1 + blk * 2 + off;
+    int64_t row = blk / nb, b = blk - row * nb;
+    int t = off - 2, half = t >> 4, pos = t & 15;
+    return p0 + row * nb * 32 + half * (nb * 16) + b * 16 + pos;
+}
+
+__global__ void k_relayout(int dtype, int64_t nb, uint8_t* __restrict__ raw, uint8_t* __restrict__ p0,
                            uint8_t* __restrict__ p1, uint8_t* __restrict__ p2, uint8_t* __restrict__ p3,
                            int64_t total_bytes, int to_planar) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total_bytes) return;
-    uint8_t* dst;
-    if (dtype == AETH_DTYPE_Q4_K) {
-        int64_t blk = i / Q4K_BLOCK_BYTES;
-        int off = (int)(i - blk * Q4K_BLOCK_BYTES);
-        dst = off < 16 ? p0 + blk * 16 + off : p1 + blk * 128 + (off - 16);
-    } else if (dtype == AETH_DTYPE_Q6_K) {
-        int64_t blk = i / Q6K_BLOCK_BYTES;
-        int off = (int)(i - blk * Q6K_BLOCK_BYTES);
-        if (off < 128) dst = p0 + blk * 128 + off;
-        else if (off < 192) dst = p1 + blk * 64 + (off - 128);
-        else if (off < 208) dst = p2 + blk * 16 + (off - 192);
-        else dst = p3 + blk * 2 + (off - 208);
-    } else {
-        int64_t blk = i / Q8_BLOCK_BYTES;
-        int off = (int)(i - blk * Q8_BLOCK_BYTES);
-        dst = off < 2 ? p1 + blk * 2 + off : p0 + blk * 32 + (off - 2);
-    }
+    uint8_t* dst = planar_addr(dtype, i, nb, p0, p1, p2, p3);
     if (to_planar) *dst = raw[i];
     else raw[i] = *dst;
 }
@@ -101,8 +124,8 @@ static int relayout(aeth_weight* w, uint8_t* d_raw, int to_planar, hipStream_t s
     int64_t total = w->nblk * w->block_bytes;
     if (total == 0) return AETH_OK;
     int64_t grid = aeth_cdiv(total, 256);
-    hipLaunchKernelGGL(k_relayout, dim3((unsigned)grid), dim3(256), 0, s, w->dtype, d_raw, w->p0, w->p1, w->p2,
-                       w->p3, total, to_planar);
+    hipLaunchKernelGGL(k_relayout, dim3((unsigned)grid), dim3(256), 0, s, w->dtype, w->nb, d_raw, w->p0, w->p1,
+                       w->p2, w->p3, total, to_planar);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }

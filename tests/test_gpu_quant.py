@@ -55,7 +55,8 @@ def test_dequant_bit_exact_random_bytes(gpu, dtype):
     n = nblk * be
     ref = O.dequant(dtype, raw, n)
     out = torch.full((n,), float("nan"), dtype=torch.float32, device="cuda")
-    A.check(A.lib().aeth_dequant(dtype, dev(torch, raw).data_ptr(), n, out.data_ptr(), None), "dequant")
+    rd = dev(torch, raw)
+    A.check(A.lib().aeth_dequant(dtype, rd.data_ptr(), n, out.data_ptr(), None), "dequant")
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
@@ -70,7 +71,8 @@ def test_dequant_bit_exact_benchmark_blocks(gpu, dtype):
     n = nblk * be
     ref = O.dequant(dtype, raw, n)
     out = torch.empty(n, dtype=torch.float32, device="cuda")
-    A.check(A.lib().aeth_dequant(dtype, dev(torch, raw).data_ptr(), n, out.data_ptr(), None), "dequant")
+    rd = dev(torch, raw)
+    A.check(A.lib().aeth_dequant(dtype, rd.data_ptr(), n, out.data_ptr(), None), "dequant")
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
