@@ -88,123 +88,262 @@ int aeth_kv_append_launch(float* layer_kv, const float* k, const float* v, int64
     return AETH_OK;
 }
 
-// ── GQA decode attention (runner.rs:1579-1603, attn_direct :1757-1801).
-// Pass 1: workgroup (kv_head, chunk of ATTN_T positions) computes, for each of
-// its `groups` query heads, the chunk's max score m, Σexp(s−m) and
-// Σexp(s−m)·v. Pass 2 merges the chunks: out = Σ e^{m_c−M} o_c / Σ e^{m_c−M} l_c.
-// seq may come from the device (d_seq: cache fill + 1 after append); grids are
-// sized for the largest seq and surplus chunks exit.
+// ── GQA decode attention (runner.rs:1579-1603, attn_direct :1757-1801),
+// fused with the RoPE of q and k (apply_rope_inplace :1886-1909) and the KV
+// append of the new token (StaticKVCache::append, kv_cache.rs:40-65).
+//
+// Workgroup (chunk c, kv head h) covers positions [64c, 64c+64) of the
+// sequence [0, seq) for the `groups` query heads sharing h. It writes the
+// chunk's softmax partials (max m, Σe^{s-m}, Σe^{s-m}·v); k_attn_merge then
+// combines them: out = Σ_c e^{m_c-M} o_c / Σ_c e^{m_c-M} l_c.
+//
+// With `qkv` set, q/k/v come unrotated from the fused projection output
+// [q (n_heads·hd) | k (kv_heads·hd) | v (kv_heads·hd)]: q and the new k are
+// rotated here with the table row min(pos, max_seq-1), and the new token is
+// position `fill` (the cache fill before this step; seq = fill + 1). The
+// chunk holding it reads k/v from registers and stores them in the cache.
 #define ATTN_T 64
 #define ATTN_MAX_GROUPS 8
+#define ATTN_MAX_CHUNKS 128  // max_seq <= 8192
 
-__global__ void __launch_bounds__(256) k_attn_partial(const float* __restrict__ q, const float* __restrict__ layer_kv,
-                                                      int n_heads, int kv_heads, int head_dim, int64_t max_seq,
-                                                      const int* d_seq, int64_t seq_v, int seq_add,
-                                                      float* __restrict__ ws, int max_chunks) {
-    __shared__ float qs[ATTN_MAX_GROUPS][256];
-    __shared__ float ps[ATTN_MAX_GROUPS][ATTN_T];
-    const int kvh = blockIdx.y;
-    const int chunk = blockIdx.x;
-    int64_t seq = scalar_or(d_seq, seq_v) + seq_add;
-    if (seq > max_seq) seq = max_seq;
+struct AttnArgs {
+    const float* q;      // [n_heads][hd] (already rotated) when qkv == nullptr
+    const float* qkv;    // fused projection output, rotated here
+    float* layer_kv;     // [2][kv_heads][max_seq][hd]
+    const float* sin_t;  // [max_seq][hd/2]
+    const float* cos_t;
+    const int* st;       // device {token, pos, fill} or nullptr
+    int64_t seq_host;    // seq when st == nullptr
+    int n_heads, kv_heads, head_dim;
+    int64_t max_seq;
+    float* ws;           // [n_heads][max_chunks][hd + 2]
+    int max_chunks;
+    float* out;          // [n_heads][hd]
+};
+
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
+    constexpr int HALF = HD / 2;
+    constexpr int TPP = HD / 16;   // threads per position in the score pass (16 dims each)
+    constexpr int PPW = 256 / TPP;  // positions per score pass
+    constexpr int VT = ATTN_T / 2;  // positions per thread in the V pass (two halves of the chunk)
+    __shared__ float qs[ATTN_MAX_GROUPS][HD];
+    __shared__ float knew[HD], vnew[HD];
+    __shared__ float sc[ATTN_MAX_GROUPS][ATTN_T];
+    __shared__ float ov[2][ATTN_MAX_GROUPS][HD];
+    __shared__ float mstat[ATTN_MAX_GROUPS][2];
+    const int kvh = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x;
+    const int groups = A.n_heads / A.kv_heads;
+    int64_t fill = -1, pos = 0, seq;
+    if (A.st) {
+        fill = A.st[2];
+        pos = A.st[1];
+        seq = fill + 1;
+    } else {
+        seq = A.seq_host;
+    }
+    if (seq > A.max_seq) seq = A.max_seq;
     const int64_t t0 = (int64_t)chunk * ATTN_T;
     if (t0 >= seq) return;
-    const int groups = n_heads / kv_heads;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float scale = 1.0f / sqrtf((float)head_dim);
-    const int64_t hs = max_seq * head_dim;
-    const float* K = layer_kv + (int64_t)kvh * hs;
-    const float* V = layer_kv + (int64_t)kv_heads * hs + (int64_t)kvh * hs;
-    for (int i = tid; i < groups * head_dim; i += 256) qs[i / head_dim][i % head_dim] = q[(int64_t)(kvh * groups) * head_dim + i];
-    __syncthreads();
-    const int nt = (int)min((int64_t)ATTN_T, seq - t0);
-    // scores: wave w handles heads w, w+4, ...; lane = position
-    for (int g = wave; g < groups; g += 4) {
-        float s = -INFINITY;
-        if (lane < nt) {
-            const float4* kr = (const float4*)(K + (t0 + lane) * head_dim);
-            float dot = 0.0f;
-            for (int e = 0; e < head_dim / 4; e++) {
-                float4 kv4 = kr[e];
-                dot += qs[g][4 * e] * kv4.x;
-                dot += qs[g][4 * e + 1] * kv4.y;
-                dot += qs[g][4 * e + 2] * kv4.z;
-                dot += qs[g][4 * e + 3] * kv4.w;
-            }
-            s = dot * scale;
+    const int64_t hs = A.max_seq * HD;
+    float* K = A.layer_kv + (int64_t)kvh * hs;
+    float* V = A.layer_kv + (int64_t)A.kv_heads * hs + (int64_t)kvh * hs;
+    const float scale = 1.0f / sqrtf((float)HD);
+    int64_t prow = pos;
+    if (prow > A.max_seq - 1) prow = A.max_seq - 1;
+    if (prow < 0) prow = 0;
+
+    // q (rotated) for this kv head's query heads; the new k/v when fused
+    if (A.qkv) {
+        const float* qsrc = A.qkv + (int64_t)kvh * groups * HD;
+        for (int i = tid; i < groups * HALF; i += 256) {
+            const int g = i / HALF, e = i - g * HALF;
+            const float x0 = qsrc[g * HD + e], x1 = qsrc[g * HD + e + HALF];
+            const float sn = A.sin_t[prow * HALF + e], cs = A.cos_t[prow * HALF + e];
+            qs[g][e] = x0 * cs - x1 * sn;
+            qs[g][e + HALF] = x0 * sn + x1 * cs;
         }
-        float m = aeth_wave_max(s);
-        float p = lane < nt ? expf(s - m) : 0.0f;
-        float l = aeth_wave_sum(p);
-        ps[g][lane] = p;
-        if (lane == 0) {
-            float* meta = ws + ((int64_t)(kvh * groups + g) * max_chunks + chunk) * (head_dim + 2);
-            meta[head_dim] = m;
-            meta[head_dim + 1] = l;
+        const float* ksrc = A.qkv + (int64_t)A.n_heads * HD + (int64_t)kvh * HD;
+        const float* vsrc = A.qkv + (int64_t)(A.n_heads + A.kv_heads) * HD + (int64_t)kvh * HD;
+        for (int e = tid; e < HALF; e += 256) {
+            const float x0 = ksrc[e], x1 = ksrc[e + HALF];
+            const float sn = A.sin_t[prow * HALF + e], cs = A.cos_t[prow * HALF + e];
+            knew[e] = x0 * cs - x1 * sn;
+            knew[e + HALF] = x0 * sn + x1 * cs;
+        }
+        for (int e = tid; e < HD; e += 256) vnew[e] = vsrc[e];
+    } else {
+        for (int i = tid; i < groups * HD; i += 256) qs[i / HD][i % HD] = A.q[(int64_t)kvh * groups * HD + i];
+    }
+    __syncthreads();
+    const bool has_new = A.qkv && fill >= t0 && fill < t0 + ATTN_T && fill < A.max_seq;
+    if (has_new) {  // StaticKVCache::append at slot `fill`
+        for (int e = tid; e < HD; e += 256) {
+            K[fill * HD + e] = knew[e];
+            V[fill * HD + e] = vnew[e];
+        }
+    }
+    const int nt = (int)min((int64_t)ATTN_T, seq - t0);
+
+    // scores: TPP threads per position, 16 dims each; all passes' K loads first
+    constexpr int NP = ATTN_T / PPW;
+    float kk[NP][16];
+#pragma unroll
+    for (int pp = 0; pp < NP; pp++) {
+        const int tp = pp * PPW + tid / TPP, part = tid % TPP;
+        const int64_t t = t0 + tp;
+        if (tp < nt && !(has_new && t == fill)) {
+            const float4* kr = (const float4*)(K + t * HD + part * 16);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float4 v4 = kr[e];
+                kk[pp][4 * e] = v4.x; kk[pp][4 * e + 1] = v4.y; kk[pp][4 * e + 2] = v4.z; kk[pp][4 * e + 3] = v4.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++) kk[pp][e] = (tp < nt) ? knew[part * 16 + e] : 0.0f;
+        }
+    }
+    // V rows of this thread's half-chunk are loaded right after K, in one batch, and
+    // consumed after the softmax
+    const int vd = tid % HD, vh = tid / HD;  // HD = 128: vh in {0, 1}
+    float vv[VT];
+#pragma unroll
+    for (int i = 0; i < VT; i++) {
+        const int tp = vh * VT + i;
+        const int64_t t = t0 + tp;
+        vv[i] = (tp < nt) ? ((has_new && t == fill) ? vnew[vd] : V[t * HD + vd]) : 0.0f;
+    }
+
+#pragma unroll
+    for (int pp = 0; pp < NP; pp++) {
+        const int tp = pp * PPW + tid / TPP, part = tid % TPP;
+#pragma unroll
+        for (int g = 0; g < ATTN_MAX_GROUPS; g++) {
+            if (g < groups) {
+                float a = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) a += qs[g][part * 16 + e] * kk[pp][e];
+#pragma unroll
+                for (int off = TPP / 2; off >= 1; off >>= 1) a += __shfl_xor(a, off, 64);
+                if (part == 0) sc[g][tp] = tp < nt ? a * scale : -INFINITY;
+            }
         }
     }
     __syncthreads();
-    // weighted V: thread handles dims d = tid, tid+256 for every head
-    for (int d = tid; d < head_dim; d += 256) {
+    // per-head max / exp / sum over the chunk: wave w handles heads w, w+4
+    {
+        const int lane = tid & 63, wave = tid >> 6;
+        for (int g = wave; g < groups; g += 4) {
+            float sv = lane < ATTN_T ? sc[g][lane] : -INFINITY;
+            float m = aeth_wave_max(sv);
+            float pr = lane < nt ? expf(sv - m) : 0.0f;
+            float l = aeth_wave_sum(pr);
+            if (lane < ATTN_T) sc[g][lane] = pr;
+            if (lane == 0) { mstat[g][0] = m; mstat[g][1] = l; }
+        }
+    }
+    __syncthreads();
+    // Σ p_t v_t over this thread's half-chunk
+    {
         float o[ATTN_MAX_GROUPS];
 #pragma unroll
         for (int g = 0; g < ATTN_MAX_GROUPS; g++) o[g] = 0.0f;
-        for (int t = 0; t < nt; t++) {
-            float vv = V[(t0 + t) * head_dim + d];
+#pragma unroll
+        for (int i = 0; i < VT; i++) {
 #pragma unroll
             for (int g = 0; g < ATTN_MAX_GROUPS; g++)
-                if (g < groups) o[g] += ps[g][t] * vv;
+                if (g < groups) o[g] += sc[g][vh * VT + i] * vv[i];
         }
 #pragma unroll
         for (int g = 0; g < ATTN_MAX_GROUPS; g++)
-            if (g < groups) ws[((int64_t)(kvh * groups + g) * max_chunks + chunk) * (head_dim + 2) + d] = o[g];
+            if (g < groups) ov[vh][g][vd] = o[g];
+    }
+    __syncthreads();
+    for (int i = tid; i < groups * HD; i += 256) {
+        const int g = i / HD, d = i - g * HD;
+        float* dst = A.ws + ((int64_t)(kvh * groups + g) * A.max_chunks + chunk) * (HD + 2);
+        dst[d] = ov[0][g][d] + ov[1][g][d];
+    }
+    if (tid < groups) {
+        float* dst = A.ws + ((int64_t)(kvh * groups + tid) * A.max_chunks + chunk) * (HD + 2);
+        dst[HD] = mstat[tid][0];
+        dst[HD + 1] = mstat[tid][1];
     }
 }
 
-__global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ ws, int head_dim, int64_t max_seq,
-                                                      const int* d_seq, int64_t seq_v, int seq_add, int max_chunks,
-                                                      float* __restrict__ out) {
-    const int h = blockIdx.x;
-    int64_t seq = scalar_or(d_seq, seq_v) + seq_add;
-    if (seq > max_seq) seq = max_seq;
+// Merge of the chunk partials of one query head (grid = n_heads, HD threads):
+// out = Σ_c e^{m_c-M} o_c / Σ_c e^{m_c-M} l_c. A separate launch: a kernel
+// boundary makes every chunk's partials visible across the XCDs' L2s, which a
+// device-scope fence inside one kernel would buy with L2 write-backs.
+template <int HD>
+__global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
+    __shared__ float cw[ATTN_MAX_CHUNKS];
+    __shared__ float cl;
+    const int h = blockIdx.x, tid = threadIdx.x;
+    int64_t seq = A.st ? (int64_t)A.st[2] + 1 : A.seq_host;
+    if (seq > A.max_seq) seq = A.max_seq;
     const int nch = (int)((seq + ATTN_T - 1) / ATTN_T);
-    const float* base = ws + (int64_t)h * max_chunks * (head_dim + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < nch; c++) M = fmaxf(M, base[(int64_t)c * (head_dim + 2) + head_dim]);
-    float L = 0.0f;
-    for (int c = 0; c < nch; c++) {
-        const float* mc = base + (int64_t)c * (head_dim + 2);
-        L += expf(mc[head_dim] - M) * mc[head_dim + 1];
-    }
-    for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
-        float acc = 0.0f;
-        for (int c = 0; c < nch; c++) {
-            const float* mc = base + (int64_t)c * (head_dim + 2);
-            acc += expf(mc[head_dim] - M) * mc[d];
+    const float* base = A.ws + (int64_t)h * A.max_chunks * (HD + 2);
+    if (tid < 64) {
+        float M = -INFINITY;
+        for (int c = tid; c < nch; c += 64) M = fmaxf(M, base[(int64_t)c * (HD + 2) + HD]);
+        M = aeth_wave_max(M);
+        float L = 0.0f;
+        for (int c = tid; c < nch; c += 64) {
+            const float* mc = base + (int64_t)c * (HD + 2);
+            const float w = expf(mc[HD] - M);
+            cw[c] = w;
+            L += w * mc[HD + 1];
         }
-        out[(int64_t)h * head_dim + d] = acc / L;
+        L = aeth_wave_sum(L);
+        if (tid == 0) cl = L;
     }
+    __syncthreads();
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = (c0 + j < nch) ? base[(int64_t)(c0 + j) * (HD + 2) + tid] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (c0 + j < nch) acc += cw[c0 + j] * v[j];
+    }
+    A.out[(int64_t)h * HD + tid] = acc / cl;
 }
 
 int64_t aeth_attn_ws_floats(int64_t n_heads, int64_t head_dim, int64_t max_seq) {
     return n_heads * aeth_cdiv(max_seq, ATTN_T) * (head_dim + 2);
 }
 
-int aeth_attn_decode_launch(const float* q, const float* layer_kv, int64_t n_heads, int64_t kv_heads,
-                            int64_t head_dim, int64_t max_seq, const int* d_seq, int64_t seq, int seq_add,
-                            float* ws, float* out, hipStream_t s) {
-    if (kv_heads <= 0 || n_heads % kv_heads != 0 || n_heads / kv_heads > ATTN_MAX_GROUPS || head_dim % 4 != 0 ||
-        head_dim > 256)
-        return aeth_set_error(AETH_EUNSUPPORTED, "attn: unsupported heads=%lld kv_heads=%lld head_dim=%lld",
-                              (long long)n_heads, (long long)kv_heads, (long long)head_dim);
-    int max_chunks = (int)aeth_cdiv(max_seq, ATTN_T);
-    int grid_chunks = d_seq ? max_chunks : (int)aeth_cdiv(min(seq + seq_add, max_seq), ATTN_T);
+// ws: aeth_attn_ws_floats(...) floats of chunk partials.
+int aeth_attn_launch(const float* q, const float* qkv, float* layer_kv, const float* sin_t, const float* cos_t,
+                     const int* d_st, int64_t seq, int64_t n_heads, int64_t kv_heads, int64_t head_dim,
+                     int64_t max_seq, float* ws, float* out, hipStream_t s) {
+    if (kv_heads <= 0 || n_heads % kv_heads != 0 || n_heads / kv_heads > ATTN_MAX_GROUPS || head_dim != 128 ||
+        kv_heads > 64 || aeth_cdiv(max_seq, ATTN_T) > ATTN_MAX_CHUNKS)
+        return aeth_set_error(AETH_EUNSUPPORTED, "attn: unsupported heads=%lld kv_heads=%lld head_dim=%lld max_seq=%lld",
+                              (long long)n_heads, (long long)kv_heads, (long long)head_dim, (long long)max_seq);
+    AttnArgs A;
+    A.q = q;
+    A.qkv = qkv;
+    A.layer_kv = layer_kv;
+    A.sin_t = sin_t;
+    A.cos_t = cos_t;
+    A.st = d_st;
+    A.seq_host = seq;
+    A.n_heads = (int)n_heads;
+    A.kv_heads = (int)kv_heads;
+    A.head_dim = (int)head_dim;
+    A.max_seq = max_seq;
+    A.max_chunks = (int)aeth_cdiv(max_seq, ATTN_T);
+    A.ws = ws;
+    A.out = out;
+    const int grid_chunks = d_st ? A.max_chunks : (int)aeth_cdiv(min(seq, max_seq), ATTN_T);
     if (grid_chunks <= 0) return AETH_OK;
-    hipLaunchKernelGGL(k_attn_partial, dim3(grid_chunks, (unsigned)kv_heads), dim3(256), 0, s, q, layer_kv,
-                       (int)n_heads, (int)kv_heads, (int)head_dim, max_seq, d_seq, seq, seq_add, ws, max_chunks);
+    hipLaunchKernelGGL(k_attn<128>, dim3(grid_chunks, (unsigned)kv_heads), dim3(256), 0, s, A);
     AETH_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)n_heads), dim3(128), 0, s, ws, (int)head_dim, max_seq, d_seq,
-                       seq, seq_add, max_chunks, out);
+    hipLaunchKernelGGL(k_attn_merge<128>, dim3((unsigned)n_heads), dim3(128), 0, s, A);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
@@ -318,15 +457,20 @@ int aeth_embed_launch(const float* table, const int* d_token, int64_t token, int
 // Advances the device decode state {token, pos, fill} after a step:
 // StaticKVCache::advance (kv_cache.rs:67-71) and pos += 1; the next token was
 // written by the argmax.
-__global__ void k_state_advance(int* st, int64_t max_seq) {
+__global__ void k_state_advance(int* st, unsigned long long* amax, int64_t max_seq) {
     if (threadIdx.x == 0 && blockIdx.x == 0) {
+        if (amax) {
+            st[0] = (int)(uint32_t)(*amax & 0xFFFFFFFFull);
+            st[3] = st[0];
+            *amax = 0ull;
+        }
         st[1] += 1;
         if (st[2] < max_seq) st[2] += 1;
     }
 }
 
-int aeth_state_advance_launch(int* st, int64_t max_seq, hipStream_t s) {
-    hipLaunchKernelGGL(k_state_advance, dim3(1), dim3(64), 0, s, st, max_seq);
+int aeth_state_advance_launch(int* st, unsigned long long* amax, int64_t max_seq, hipStream_t s) {
+    hipLaunchKernelGGL(k_state_advance, dim3(1), dim3(64), 0, s, st, amax, max_seq);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }

@@ -351,32 +351,69 @@ __device__ __forceinline__ int row_of_lane(int lane) {
 // each lane owns exactly one unit and keeps its digit record in registers;
 // the 8 waves form 8/WPR row streams. R rows per pass; XO activation octets
 // per thread.
+//
+// Optional fusions (GemvParams):
+//  norm_w   : x ← x / sqrt(Σx²/k + eps) · norm_w before the product
+//             (rmsnorm_inplace, runner.rs:1739-1746);
+//  swiglu   : rows come in (gate_i, up_i) pairs at 2i, 2i+1 and the output is
+//             y[i] = g·σ(g)·u (runner.rs:1617-1625) — WPR == 1 only;
+//  amax     : greedy argmax of y folded into a 64-bit atomic max of
+//             (orderable(value) << 32 | row): last maximal row wins on ties,
+//             as Iterator::max_by (runner.rs:1964-1973);
+//  accumulate: y += result (residual adds, runner.rs:1609-1611, 1629-1631).
+struct GemvParams {
+    Planes P;
+    int64_t n;
+    int nb, upr;
+    const float* x;
+    int k;
+    int64_t x_stride;
+    float* y;
+    int64_t y_stride;
+    int accumulate;
+    int64_t rows_per_wg;
+    int npass;
+    const float* norm_w;
+    float eps;
+    int swiglu;
+    unsigned long long* amax;
+};
+
+__device__ __forceinline__ unsigned long long amax_key(float v, int64_t row) {
+    uint32_t f = __float_as_uint(v);
+    uint32_t o = (f & 0x80000000u) ? ~f : (f | 0x80000000u);
+    return ((unsigned long long)o << 32) | (unsigned long long)(uint32_t)row;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g * (1.0f / (1.0f + expf(-g))) * u; }
+
 template <int F, int WPR, int R, int XO>
-__global__ void __launch_bounds__(GEMV_THREADS) k_gemv(Planes P, int64_t n, int nb, int upr,
-                                                     const float* __restrict__ x, int k, int64_t x_stride,
-                                                     float* __restrict__ y, int64_t y_stride, int accumulate,
-                                                     int64_t rows_per_wg, int npass) {
+__global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvParams G) {
     constexpr int STREAMS = GEMV_WAVES / WPR;
     extern __shared__ __attribute__((aligned(16))) char rec[];
     __shared__ int flag;
+    __shared__ float ssum[GEMV_WAVES];
+    __shared__ unsigned long long kmax[GEMV_WAVES];
     typedef typename UnitT<F>::T U;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int stream = wave / WPR, wir = wave - stream * WPR;
     const int u = wir * 64 + lane;
+    const int upr = G.upr, nb = G.nb;
     const bool valid = u < upr;
-    const float* xr = x + (int64_t)blockIdx.y * x_stride;
-    float* yr = y + (int64_t)blockIdx.y * y_stride;
-    const int64_t wg0 = (int64_t)blockIdx.x * rows_per_wg;
-    const int64_t wg1 = min(n, wg0 + rows_per_wg);
-    const int64_t rps = (rows_per_wg + STREAMS - 1) / STREAMS;
+    const float* xr = G.x + (int64_t)blockIdx.y * G.x_stride;
+    float* yr = G.y + (int64_t)blockIdx.y * G.y_stride;
+    const int64_t wg0 = (int64_t)blockIdx.x * G.rows_per_wg;
+    const int64_t wg1 = min(G.n, wg0 + G.rows_per_wg);
+    const int64_t rps = (G.rows_per_wg + STREAMS - 1) / STREAMS;
     const int64_t sb = min(wg1, wg0 + stream * rps);
     const int64_t se = min(wg1, sb + rps);
     const int j4 = u & 3;  // Q4_K: sub-block pair of this lane's unit
     const int noct = upr * Fmt<F>::UE / 8;
     float* red = (float*)(rec + (size_t)upr * Fmt<F>::RECB);  // [2][STREAMS][WPR][R] when WPR > 1
 
-    float xv[XO][8];
-    load_x<XO>(xr, k, noct, xv);
+    float xv[XO][8], wv[XO][8];
+    load_x<XO>(xr, G.k, noct, xv);
+    if (G.norm_w) load_x<XO>(G.norm_w, G.k, noct, wv);
 
     // Ring of R row buffers: row i of this stream lives in buf[i % R]; each
     // buffer is refilled with the row R ahead as soon as it has been consumed,
@@ -385,27 +422,48 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(Planes P, int64_t n, int 
 #pragma unroll
     for (int r = 0; r < R; r++) {
         if (valid && sb < se) {
-            load_unit(buf[r], P, min(sb + r, se - 1), nb, u);
+            load_unit(buf[r], G.P, min(sb + r, se - 1), nb, u);
             fix_unit(buf[r], u & 1);
         }
     }
 
+    if (G.norm_w) {  // fused RMSNorm: every workgroup normalises the full row
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XO; i++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) ss += xv[i][t] * xv[i][t];
+        ss = aeth_wave_sum(ss);
+        if (lane == 0) ssum[wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < GEMV_WAVES; w++) tot += ssum[w];
+        const float rms = sqrtf(tot / (float)G.k + G.eps);
+#pragma unroll
+        for (int i = 0; i < XO; i++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) xv[i][t] = xv[i][t] / rms * wv[i][t];
+    }
+
     if (build_records<F, XO>(xv, noct, rec, &flag)) {
+        const int64_t oe = G.swiglu ? se / 2 : se;
         if (wir == 0)
-            for (int64_t row = sb + lane; row < se; row += 64) yr[row] = __int_as_float(0x7FC00000);
+            for (int64_t row = (G.swiglu ? sb / 2 : sb) + lane; row < oe; row += 64) yr[row] = __int_as_float(0x7FC00000);
         return;
     }
     Rec<F> reg;
     if (valid) read_rec<F>(reg, rec + (size_t)u * Fmt<F>::RECB);
 
-    for (int p = 0; p < npass; p++) {
+    unsigned long long best = 0;
+    for (int p = 0; p < G.npass; p++) {
         const int64_t row0 = sb + (int64_t)p * R;
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
             acc[r] = (valid && row0 + r < se) ? unit_dot(buf[r], reg, j4) : 0.0f;
-            if (valid && p + 1 < npass && row0 + R < se) {
-                load_unit(buf[r], P, min(row0 + R + r, se - 1), nb, u);
+            if (valid && p + 1 < G.npass && row0 + R < se) {
+                load_unit(buf[r], G.P, min(row0 + R + r, se - 1), nb, u);
                 fix_unit(buf[r], u & 1);
             }
         }
@@ -414,7 +472,14 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(Planes P, int64_t n, int 
         const bool writer = (lane & (64 / R - 1)) == 0;
         if (WPR == 1) {
             const int64_t row = row0 + myrow;
-            if (writer && row < se) yr[row] = accumulate ? yr[row] + tot : tot;
+            if (G.swiglu) {
+                const float up = __shfl_xor(tot, 64 / R, 64);  // partner row = row ^ 1
+                if (writer && (myrow & 1) == 0 && row < se) yr[row >> 1] = silu_mul(tot, up);
+            } else if (writer && row < se) {
+                const float v = G.accumulate ? yr[row] + tot : tot;
+                yr[row] = v;
+                if (G.amax) { unsigned long long kk = amax_key(v, row); best = kk > best ? kk : best; }
+            }
         } else {
             float* rb = red + (p & 1) * (STREAMS * WPR * R);
             if (writer) rb[(stream * WPR + wir) * R + myrow] = tot;
@@ -427,9 +492,26 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(Planes P, int64_t n, int 
                     float t = 0.0f;
 #pragma unroll
                     for (int w = 0; w < WPR; w++) t += rb[(s2 * WPR + w) * R + r2];
-                    yr[row] = accumulate ? yr[row] + t : t;
+                    const float v = G.accumulate ? yr[row] + t : t;
+                    yr[row] = v;
+                    if (G.amax) { unsigned long long kk = amax_key(v, row); best = kk > best ? kk : best; }
                 }
             }
+        }
+    }
+    if (G.amax) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            unsigned long long o = __shfl_xor(best, off, 64);
+            best = o > best ? o : best;
+        }
+        if (lane == 0) kmax[wave] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long m = kmax[0];
+#pragma unroll
+            for (int w = 1; w < GEMV_WAVES; w++) m = kmax[w] > m ? kmax[w] : m;
+            atomicMax(G.amax, m);
         }
     }
 }
@@ -442,20 +524,18 @@ static int env_int(const char* name, int dflt) {
 }
 
 template <int F, int WPR, int R, int XO>
-static void launch(dim3 grid, size_t lds, hipStream_t s, const Planes& P, int64_t n, int nb, int upr, const float* x,
-                   int k, float* y, int acc, int64_t rpg) {
+static void launch(dim3 grid, size_t lds, hipStream_t s, GemvParams G) {
     constexpr int STREAMS = GEMV_WAVES / WPR;
-    const int64_t rps = (rpg + STREAMS - 1) / STREAMS;
-    const int npass = (int)((rps + R - 1) / R);
-    hipLaunchKernelGGL((k_gemv<F, WPR, R, XO>), grid, dim3(GEMV_THREADS), lds, s, P, n, nb, upr, x, k, (int64_t)k, y,
-                       n, acc, rpg, npass);
+    const int64_t rps = (G.rows_per_wg + STREAMS - 1) / STREAMS;
+    G.npass = (int)((rps + R - 1) / R);
+    hipLaunchKernelGGL((k_gemv<F, WPR, R, XO>), grid, dim3(GEMV_THREADS), lds, s, G);
 }
 
 template <int F>
-static int dispatch_fmt(const Planes& P, int64_t n, int nb, int k, int upr, const float* x, int64_t m, float* y,
-                        int acc, hipStream_t s) {
+static int dispatch_fmt(GemvParams G, int64_t m, hipStream_t s) {
     static const int wg_per_cu = env_int("AETH_GEMV_WG_PER_CU", 1);
     static const int rsel = env_int("AETH_GEMV_R", 4);
+    const int upr = G.upr;
     int wpr = 1;
     while (wpr * 64 < upr) wpr *= 2;
     const int noct = upr * Fmt<F>::UE / 8;
@@ -463,14 +543,19 @@ static int dispatch_fmt(const Planes& P, int64_t n, int nb, int k, int upr, cons
     while (xo * GEMV_THREADS < noct) xo *= 2;
     const size_t lds = (size_t)upr * Fmt<F>::RECB + (wpr > 1 ? 2 * GEMV_WAVES * 4 * sizeof(float) : 0);
     if (wpr > 8 || xo > 4 || lds > 64 * 1024)
-        return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d is beyond this kernel's range", k);
+        return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d is beyond this kernel's range", G.k);
+    if (G.swiglu && (wpr != 1 || (G.n & 1)))
+        return aeth_set_error(AETH_EUNSUPPORTED, "gemv: fused SwiGLU needs k <= 4096-wide rows and paired rows");
+    const int streams = GEMV_WAVES / wpr;
     int64_t grid = (int64_t)aeth_num_cus() * (wg_per_cu < 1 ? 1 : wg_per_cu);
-    const int64_t need = (n + (GEMV_WAVES / wpr) - 1) / (GEMV_WAVES / wpr);
+    const int64_t need = (G.n + streams - 1) / streams;
     if (need < grid) grid = need;
     if (grid < 1) grid = 1;
-    const int64_t rpg = (n + grid - 1) / grid;
+    int64_t rpg = (G.n + grid - 1) / grid;
+    if (G.swiglu) rpg = (rpg + 2 * streams - 1) / (2 * streams) * (2 * streams);  // even rows per stream
+    G.rows_per_wg = rpg;
     dim3 g((unsigned)grid, (unsigned)m);
-#define L_(W, RR, X) launch<F, W, RR, X>(g, lds, s, P, n, nb, upr, x, k, y, acc, rpg)
+#define L_(W, RR, X) launch<F, W, RR, X>(g, lds, s, G)
     if (wpr == 1 && xo == 1) {
         if (rsel == 2) L_(1, 2, 1);
         else if (rsel == 8) L_(1, 8, 1);
@@ -482,20 +567,40 @@ static int dispatch_fmt(const Planes& P, int64_t n, int nb, int k, int upr, cons
     else if (wpr == 8 && xo == 4) L_(8, 4, 4);
     else if (wpr == 1 && xo == 2) L_(1, 4, 2);
     else if (wpr == 2 && xo == 4) L_(2, 4, 4);
-    else return aeth_set_error(AETH_EUNSUPPORTED, "gemv: no kernel for k=%d (wpr %d, xo %d)", k, wpr, xo);
+    else return aeth_set_error(AETH_EUNSUPPORTED, "gemv: no kernel for k=%d (wpr %d, xo %d)", G.k, wpr, xo);
 #undef L_
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
 
-int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags, hipStream_t s) {
+int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, const GemvEpi& e,
+                        hipStream_t s) {
     if (m > 65535) return aeth_set_error(AETH_EINVAL, "gemv: m=%lld exceeds 65535", (long long)m);
-    const int nb = (int)w->nb;
-    const int k = (int)w->k;
-    const int acc = (flags & AETH_MM_ACCUMULATE) ? 1 : 0;
-    Planes P{w->p0, w->p1, w->p2, w->p3};
-    if (w->dtype == AETH_DTYPE_Q4_K) return dispatch_fmt<FMT_Q4K>(P, w->n, nb, k, nb * 4, d_x, m, d_y, acc, s);
-    if (w->dtype == AETH_DTYPE_Q6_K) return dispatch_fmt<FMT_Q6K>(P, w->n, nb, k, nb * 4, d_x, m, d_y, acc, s);
-    if (w->dtype == AETH_DTYPE_Q8_0) return dispatch_fmt<FMT_Q80>(P, w->n, nb, k, nb, d_x, m, d_y, acc, s);
+    GemvParams G;
+    G.P = Planes{w->p0, w->p1, w->p2, w->p3};
+    G.n = w->n;
+    G.nb = (int)w->nb;
+    G.upr = w->dtype == AETH_DTYPE_Q8_0 ? (int)w->nb : (int)w->nb * 4;
+    G.x = d_x;
+    G.k = (int)w->k;
+    G.x_stride = w->k;
+    G.y = d_y;
+    G.y_stride = e.swiglu ? w->n / 2 : w->n;
+    G.accumulate = (e.flags & AETH_MM_ACCUMULATE) ? 1 : 0;
+    G.rows_per_wg = 0;
+    G.npass = 0;
+    G.norm_w = e.norm_w;
+    G.eps = e.eps;
+    G.swiglu = e.swiglu;
+    G.amax = e.amax;
+    if (w->dtype == AETH_DTYPE_Q4_K) return dispatch_fmt<FMT_Q4K>(G, m, s);
+    if (w->dtype == AETH_DTYPE_Q6_K) return dispatch_fmt<FMT_Q6K>(G, m, s);
+    if (w->dtype == AETH_DTYPE_Q8_0) return dispatch_fmt<FMT_Q80>(G, m, s);
     return aeth_set_error(AETH_EUNSUPPORTED, "gemv: dtype %d", w->dtype);
+}
+
+int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags, hipStream_t s) {
+    GemvEpi e;
+    e.flags = flags;
+    return aeth_gemv_launch_ex(w, d_x, m, d_y, e, s);
 }

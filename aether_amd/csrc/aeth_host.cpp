@@ -15,26 +15,28 @@
 #include "aeth_ops_internal.hpp"
 
 // ── per-device scratch for the standalone decode-op entry points ─────────
-// Calls that overlap on one device (different host threads or streams) share
-// it and race; the runner uses its own buffers.
+// One buffer per (device, use); calls that overlap on one device (different
+// host threads or streams) share it and race; the runner uses its own.
 namespace {
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
 std::mutex g_ws_mu;
-std::map<int, Workspace> g_ws;
+std::map<std::pair<int, int>, Workspace> g_ws;
+enum { WS_ATTN = 0, WS_ARGMAX = 1 };
 
-int workspace(size_t bytes, void** out) {
+int workspace(int use, size_t bytes, void** out) {
     int dev = 0;
     AETH_HIP_CHECK(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace& w = g_ws[dev];
+    Workspace& w = g_ws[std::make_pair(dev, use)];
     if (w.bytes < bytes) {
         if (w.ptr) AETH_HIP_CHECK(hipFree(w.ptr));
         w.ptr = nullptr;
         w.bytes = 0;
         AETH_HIP_CHECK(hipMalloc(&w.ptr, bytes));
+        AETH_HIP_CHECK(hipMemset(w.ptr, 0, bytes));
         w.bytes = bytes;
     }
     *out = w.ptr;
@@ -77,10 +79,10 @@ extern "C" AETH_API int aeth_attn_decode(const float* d_q, const float* d_layer_
         return aeth_set_error(AETH_EINVAL, "aeth_attn_decode: bad argument (seq %lld, max_seq %lld)", (long long)seq,
                               (long long)max_seq);
     void* ws = nullptr;
-    int rc = workspace(sizeof(float) * aeth_attn_ws_floats(n_heads, head_dim, max_seq), &ws);
+    int rc = workspace(WS_ATTN, sizeof(float) * aeth_attn_ws_floats(n_heads, head_dim, max_seq), &ws);
     if (rc) return rc;
-    return aeth_attn_decode_launch(d_q, d_layer_kv, n_heads, kv_heads, head_dim, max_seq, nullptr, seq, 0,
-                                   (float*)ws, d_out, (hipStream_t)stream);
+    return aeth_attn_launch(d_q, nullptr, (float*)d_layer_kv, nullptr, nullptr, nullptr, seq, n_heads, kv_heads,
+                            head_dim, max_seq, (float*)ws, d_out, (hipStream_t)stream);
 }
 
 extern "C" AETH_API int aeth_silu_mul(float* d_gate, const float* d_up, int64_t n, void* stream) {
@@ -96,7 +98,7 @@ extern "C" AETH_API int aeth_add(float* d_x, const float* d_y, int64_t n, void* 
 extern "C" AETH_API int aeth_argmax(const float* d_logits, int64_t n, int32_t* d_out, void* stream) {
     if (!d_logits || !d_out) return aeth_set_error(AETH_EINVAL, "aeth_argmax: bad argument");
     void* ws = nullptr;
-    int rc = workspace((size_t)aeth_argmax_ws_bytes(), &ws);
+    int rc = workspace(WS_ARGMAX, (size_t)aeth_argmax_ws_bytes(), &ws);
     if (rc) return rc;
     return aeth_argmax_launch(d_logits, n, d_out, nullptr, ws, (hipStream_t)stream);
 }

@@ -1,5 +1,6 @@
 // Internal (non-exported) declarations shared by the library's sources.
 #pragma once
+#include <hip/hip_runtime.h>
 #include <stdint.h>
 
 // Device copy of one QuantWeight in per-field planes (see aeth_weights.hip).
@@ -17,7 +18,18 @@ struct aeth_weight {
 int aeth_num_cus();
 int64_t aeth_blocks_per_row(int dtype, int64_t k);
 
+// Fusions around the GEMV (see k_gemv in aeth_gemv.hip).
+struct GemvEpi {
+    unsigned flags = 0;                   // AETH_MM_ACCUMULATE
+    const float* norm_w = nullptr;        // fused RMSNorm weight (length k)
+    float eps = 0.0f;
+    int swiglu = 0;                       // rows are (gate, up) pairs; y gets n/2 outputs
+    unsigned long long* amax = nullptr;   // fused greedy argmax key
+};
+
 // GEMV on one activation row per launch-row (a: [m][k] f32, c: [m][n]).
+int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, const GemvEpi& e,
+                        hipStream_t s);
 int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags,
                      hipStream_t s);
 // Q4_K prefill GEMM (m > 1).

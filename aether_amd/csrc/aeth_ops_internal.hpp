@@ -10,15 +10,20 @@ int aeth_rope_launch(float* x, int64_t n_heads, int64_t head_dim, const int* d_p
                      const float* sin_t, const float* cos_t, int64_t max_seq, hipStream_t s);
 int aeth_kv_append_launch(float* layer_kv, const float* k, const float* v, int64_t kv_heads, int64_t head_dim,
                           int64_t max_seq, const int* d_slot, int64_t slot, hipStream_t s);
+// Attention workspace (floats): the chunk softmax partials.
 int64_t aeth_attn_ws_floats(int64_t n_heads, int64_t head_dim, int64_t max_seq);
-// seq = (d_seq ? *d_seq : seq) + seq_add, clamped to max_seq.
-int aeth_attn_decode_launch(const float* q, const float* layer_kv, int64_t n_heads, int64_t kv_heads,
-                            int64_t head_dim, int64_t max_seq, const int* d_seq, int64_t seq, int seq_add,
-                            float* ws, float* out, hipStream_t s);
+// Decode attention over one layer slice of the cache. Either q (rotated, with
+// seq given) or qkv (fused projection output: RoPE of q/k and the KV append
+// of the new token happen here, scalars from d_st = {token, pos, fill}).
+int aeth_attn_launch(const float* q, const float* qkv, float* layer_kv, const float* sin_t, const float* cos_t,
+                     const int* d_st, int64_t seq, int64_t n_heads, int64_t kv_heads, int64_t head_dim,
+                     int64_t max_seq, float* ws, float* out, hipStream_t s);
 int aeth_silu_mul_launch(float* g, const float* up, int64_t n, hipStream_t s);
 int aeth_add_launch(float* x, const float* y, int64_t n, hipStream_t s);
 int64_t aeth_argmax_ws_bytes();
 int aeth_argmax_launch(const float* x, int64_t n, int* out, int* next_token, void* ws, hipStream_t s);
 int aeth_embed_launch(const float* table, const int* d_token, int64_t token, int64_t d, int64_t vocab, float* x,
                       hipStream_t s);
-int aeth_state_advance_launch(int* st, int64_t max_seq, hipStream_t s);
+// After a step: token = argmax key's row (key reset to 0), pos += 1, fill
+// advanced (StaticKVCache::advance).
+int aeth_state_advance_launch(int* st, unsigned long long* amax, int64_t max_seq, hipStream_t s);

@@ -23,7 +23,9 @@ struct aeth_runner {
     aeth_llama_config cfg;
     hipStream_t stream = nullptr;
     // weights
-    std::vector<aeth_weight*> wqkv, wo, wgu, wdown;  // per layer (q|k|v and gate|up concatenated by rows)
+    // per layer: q|k|v rows concatenated; gate and up rows interleaved
+    // (row 2i = gate_i, row 2i+1 = up_i) for the fused SwiGLU epilogue
+    std::vector<aeth_weight*> wqkv, wo, wgu, wdown;
     std::vector<int> dtypes;                         // per layer x 7
     aeth_weight* lm_head = nullptr;
     float* norms = nullptr;       // [L][2][d]
@@ -36,8 +38,9 @@ struct aeth_runner {
     float *x = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
     float* attn_ws = nullptr;
     void* am_ws = nullptr;
-    int* st = nullptr;      // device {token, pos, fill}
-    int* tok_out = nullptr;  // device argmax
+    int* st = nullptr;       // device {token, pos, fill, next token}
+    unsigned long long* amax = nullptr;  // fused LM-head argmax key (reset by the state kernel)
+    int* tok_out = nullptr;  // unused slot kept for the release list
     int fill = 0;           // host mirror of the cache fill
     hipGraphExec_t graph = nullptr;
     // frame budget / partial decode (runner.rs:1201-1282, c_api.rs:313-355)
@@ -107,6 +110,23 @@ int make_concat(int dtype, const std::vector<int64_t>& ns, int64_t k, const std:
     return aeth_weight_create(dtype, ntot, k, cat.data(), 0, s, out);
 }
 
+// gate (rows 0..dff) and up interleaved row by row: row 2i = gate_i, 2i+1 = up_i.
+int make_interleaved(int dtype, int64_t dff, int64_t k, const void* gate, const void* up, uint64_t seed,
+                     hipStream_t s, aeth_weight** out) {
+    if (!gate && !up) return make_weight(dtype, 2 * dff, k, nullptr, seed, s, out);
+    if (!gate || !up) return aeth_set_error(AETH_EINVAL, "runner: gate/up must both be given");
+    int be, bb;
+    int rc = aeth_block_geometry(dtype, &be, &bb);
+    if (rc) return rc;
+    const int64_t rowb = aeth_blocks_per_row(dtype, k) * bb;
+    std::vector<uint8_t> cat((size_t)(2 * dff * rowb));
+    for (int64_t i = 0; i < dff; i++) {
+        memcpy(cat.data() + (size_t)(2 * i) * rowb, (const uint8_t*)gate + i * rowb, (size_t)rowb);
+        memcpy(cat.data() + (size_t)(2 * i + 1) * rowb, (const uint8_t*)up + i * rowb, (size_t)rowb);
+    }
+    return aeth_weight_create(dtype, 2 * dff, k, cat.data(), 0, s, out);
+}
+
 template <typename T>
 int dmalloc(T** p, int64_t count) {
     AETH_HIP_CHECK(hipMalloc((void**)p, sizeof(T) * (size_t)(count > 0 ? count : 1)));
@@ -128,55 +148,59 @@ void runner_release(aeth_runner* r) {
     for (auto* w : r->wdown) aeth_weight_free(w);
     aeth_weight_free(r->lm_head);
     void* bufs[] = {r->norms, r->final_norm, r->emb, r->rope_sin, r->rope_cos, r->kv, r->x, r->normed, r->qkv,
-                    r->attn, r->gu, r->logits, r->attn_ws, r->am_ws, r->st, r->tok_out};
+                    r->attn, r->gu, r->logits, r->attn_ws, r->am_ws, r->st, r->tok_out, r->amax};
     for (void* b : bufs)
         if (b) hipFree(b);
     if (r->stream) hipStreamDestroy(r->stream);
     delete r;
 }
 
-// Enqueues one decode step on r->stream, reading {token, pos, fill} from
-// r->st; layers [l0, l1) only when partial (frame budget), the final norm,
-// LM head and argmax only when l1 == num_layers.
+// Enqueues layers [l0, l1) of one decode step on r->stream; scalars come
+// from r->st = {token, pos, fill, next token}. Per layer (runner.rs:1557-1632):
+//   qkv  = rmsnorm(x, attn_norm) · Wqkvᵀ          (norm fused into the GEMV)
+//   attn = GQA attention with RoPE + KV append   (one kernel)
+//   x   += attn · Woᵀ                              (residual fused)
+//   h    = silu(g)·u, [g|u] = rmsnorm(x, ffn_norm) · Wguᵀ (norm + SwiGLU fused)
+//   x   += h · Wdownᵀ                              (residual fused)
 int enqueue_layers(aeth_runner* r, int l0, int l1) {
     const aeth_llama_config& c = r->cfg;
     hipStream_t s = r->stream;
     const int64_t d = c.d_model, hd = c.head_dim, nh = c.num_heads, nkv = c.num_kv_heads;
-    const int64_t qd = nh * hd, kvd = kKvd(c), dff = c.d_ff;
     int rc;
     for (int l = l0; l < l1; l++) {
         float* lkv = r->kv + (int64_t)l * kv_layer_floats(c);
-        if ((rc = aeth_rmsnorm_launch(r->x, r->norms + (int64_t)l * 2 * d, 1, d, c.rms_norm_eps, r->normed, s)))
+        GemvEpi e1;
+        e1.norm_w = r->norms + (int64_t)l * 2 * d;
+        e1.eps = c.rms_norm_eps;
+        if ((rc = aeth_gemv_launch_ex(r->wqkv[l], r->x, 1, r->qkv, e1, s))) return rc;
+        if ((rc = aeth_attn_launch(nullptr, r->qkv, lkv, r->rope_sin, r->rope_cos, r->st, 0, nh, nkv, hd,
+                                   c.max_seq_len, r->attn_ws, r->attn, s)))
             return rc;
-        if ((rc = aeth_qmatmul(r->wqkv[l], r->normed, 1, r->qkv, 0, s))) return rc;
-        // q and k are adjacent in qkv: one rotate-half pass over nh + nkv heads
-        if ((rc = aeth_rope_launch(r->qkv, nh + nkv, hd, r->st + 1, 0, r->rope_sin, r->rope_cos, c.max_seq_len, s)))
-            return rc;
-        if ((rc = aeth_kv_append_launch(lkv, r->qkv + qd, r->qkv + qd + kvd, nkv, hd, c.max_seq_len, r->st + 2, 0, s)))
-            return rc;
-        if ((rc = aeth_attn_decode_launch(r->qkv, lkv, nh, nkv, hd, c.max_seq_len, r->st + 2, 0, 1, r->attn_ws,
-                                          r->attn, s)))
-            return rc;
-        if ((rc = aeth_qmatmul(r->wo[l], r->attn, 1, r->x, AETH_MM_ACCUMULATE, s))) return rc;
-        if ((rc = aeth_rmsnorm_launch(r->x, r->norms + (int64_t)l * 2 * d + d, 1, d, c.rms_norm_eps, r->normed, s)))
-            return rc;
-        if ((rc = aeth_qmatmul(r->wgu[l], r->normed, 1, r->gu, 0, s))) return rc;
-        if ((rc = aeth_silu_mul_launch(r->gu, r->gu + dff, dff, s))) return rc;
-        if ((rc = aeth_qmatmul(r->wdown[l], r->gu, 1, r->x, AETH_MM_ACCUMULATE, s))) return rc;
+        GemvEpi e2;
+        e2.flags = AETH_MM_ACCUMULATE;
+        if ((rc = aeth_gemv_launch_ex(r->wo[l], r->attn, 1, r->x, e2, s))) return rc;
+        GemvEpi e3;
+        e3.norm_w = r->norms + (int64_t)l * 2 * d + d;
+        e3.eps = c.rms_norm_eps;
+        e3.swiglu = 1;
+        if ((rc = aeth_gemv_launch_ex(r->wgu[l], r->x, 1, r->gu, e3, s))) return rc;
+        if ((rc = aeth_gemv_launch_ex(r->wdown[l], r->gu, 1, r->x, e2, s))) return rc;
     }
     return AETH_OK;
 }
 
+// Final norm + LM head with the greedy argmax fused, then the state update
+// (StaticKVCache::advance, runner.rs:1639; next token = argmax).
 int enqueue_head(aeth_runner* r) {
     const aeth_llama_config& c = r->cfg;
     hipStream_t s = r->stream;
     int rc;
-    // kv.advance() precedes the final norm in the reference (runner.rs:1639);
-    // state_advance runs after the argmax because nothing below reads the fill.
-    if ((rc = aeth_rmsnorm_launch(r->x, r->final_norm, 1, c.d_model, c.rms_norm_eps, r->normed, s))) return rc;
-    if ((rc = aeth_qmatmul(r->lm_head, r->normed, 1, r->logits, 0, s))) return rc;
-    if ((rc = aeth_argmax_launch(r->logits, c.vocab_size, r->tok_out, r->st, r->am_ws, s))) return rc;
-    return aeth_state_advance_launch(r->st, c.max_seq_len, s);
+    GemvEpi e;
+    e.norm_w = r->final_norm;
+    e.eps = c.rms_norm_eps;
+    e.amax = r->amax;
+    if ((rc = aeth_gemv_launch_ex(r->lm_head, r->x, 1, r->logits, e, s))) return rc;
+    return aeth_state_advance_launch(r->st, r->amax, c.max_seq_len, s);
 }
 
 int enqueue_step(aeth_runner* r) {
@@ -187,7 +211,7 @@ int enqueue_step(aeth_runner* r) {
 }
 
 int set_state(aeth_runner* r, int token, int pos) {
-    int h[3] = {token, pos, r->fill};
+    int h[4] = {token, pos, r->fill, token};
     AETH_HIP_CHECK(hipMemcpyAsync(r->st, h, sizeof(h), hipMemcpyHostToDevice, r->stream));
     return AETH_OK;
 }
@@ -214,6 +238,9 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
         c.d_ff <= 0 || c.vocab_size <= 0 || c.max_seq_len <= 0 || c.num_heads % c.num_kv_heads != 0 ||
         c.head_dim % 2 != 0)
         return aeth_set_error(AETH_EINVAL, "aeth_runner_create: invalid config");
+    if (c.head_dim != 128 || c.num_heads / c.num_kv_heads > 8)
+        return aeth_set_error(AETH_EUNSUPPORTED, "aeth_runner_create: the attention kernel needs head_dim 128 and "
+                                                 "at most 8 query heads per KV head");
     bool need_seed = !lm_head || !embeddings || !final_norm || !layer_weights || !norms;
     if (need_seed && seed == 0)
         return aeth_set_error(AETH_EINVAL, "aeth_runner_create: missing tensors need a nonzero synthetic_seed");
@@ -248,7 +275,7 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
         r->wqkv.push_back(w);
         RC(make_weight(T[3], d, qd, hw(3), mix(seed, l, 4), s, &w));
         r->wo.push_back(w);
-        RC(make_concat(T[4], {dff, dff}, d, {hw(4), hw(5)}, mix(seed, l, 5), s, &w));
+        RC(make_interleaved(T[4], dff, d, hw(4), hw(5), mix(seed, l, 5), s, &w));
         r->wgu.push_back(w);
         RC(make_weight(T[6], d, dff, hw(6), mix(seed, l, 7), s, &w));
         r->wdown.push_back(w);
@@ -303,9 +330,19 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
     RC(dmalloc(&r->normed, d > dff ? d : dff));
     RC(dmalloc(&r->qkv, qd + 2 * kvd));
     RC(dmalloc(&r->attn, qd));
-    RC(dmalloc(&r->gu, 2 * dff));
+    RC(dmalloc(&r->gu, dff));
     RC(dmalloc(&r->logits, c.vocab_size));
     RC(dmalloc(&r->attn_ws, aeth_attn_ws_floats(c.num_heads, c.head_dim, c.max_seq_len)));
+    if (hipMemset(r->attn_ws, 0, sizeof(float) * aeth_attn_ws_floats(c.num_heads, c.head_dim, c.max_seq_len)) !=
+        hipSuccess) {
+        runner_release(r);
+        return aeth_set_error(AETH_EHIP, "runner: workspace clear failed");
+    }
+    RC(dmalloc(&r->amax, 1));
+    if (hipMemset(r->amax, 0, sizeof(unsigned long long)) != hipSuccess) {
+        runner_release(r);
+        return aeth_set_error(AETH_EHIP, "runner: argmax slot clear failed");
+    }
     RC(dmalloc((uint8_t**)&r->am_ws, aeth_argmax_ws_bytes()));
     RC(dmalloc(&r->st, 4));
     RC(dmalloc(&r->tok_out, 4));
@@ -380,7 +417,7 @@ static int runner_decode_locked(aeth_runner* r, int32_t token, int32_t pos, floa
         AETH_HIP_CHECK(hipMemcpyAsync(logits, r->logits, sizeof(float) * r->cfg.vocab_size, hipMemcpyDeviceToHost,
                                       r->stream));
     int tok = 0;
-    AETH_HIP_CHECK(hipMemcpyAsync(&tok, r->tok_out, sizeof(int), hipMemcpyDeviceToHost, r->stream));
+    AETH_HIP_CHECK(hipMemcpyAsync(&tok, r->st + 3, sizeof(int), hipMemcpyDeviceToHost, r->stream));
     AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
     if (r->fill < r->cfg.max_seq_len) r->fill++;
     if (next_token) *next_token = tok;
@@ -426,7 +463,7 @@ extern "C" AETH_API int aeth_runner_generate(aeth_runner* r, int32_t token, int3
     for (int i = 0; i < n_steps; i++) {
         if (use_graph) AETH_HIP_CHECK(hipGraphLaunch(r->graph, r->stream));
         else if ((rc = enqueue_step(r))) return rc;
-        AETH_HIP_CHECK(hipMemcpyAsync(tokens + i, r->tok_out, sizeof(int), hipMemcpyDeviceToHost, r->stream));
+        AETH_HIP_CHECK(hipMemcpyAsync(tokens + i, r->st + 3, sizeof(int), hipMemcpyDeviceToHost, r->stream));
     }
     AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
     r->fill += n_steps;
@@ -437,6 +474,7 @@ extern "C" AETH_API int aeth_runner_export(const aeth_runner* r, int which, int3
     if (!r || !host) return aeth_set_error(AETH_EINVAL, "aeth_runner_export: NULL");
     const aeth_llama_config& c = r->cfg;
     const int64_t d = c.d_model, qd = (int64_t)c.num_heads * c.head_dim, kvd = kKvd(c), dff = c.d_ff;
+    (void)dff;
     AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
     if (which >= 0 && which <= 6) {
         if (l < 0 || l >= c.num_layers) return aeth_set_error(AETH_EINVAL, "export: layer out of range");
@@ -448,10 +486,14 @@ extern "C" AETH_API int aeth_runner_export(const aeth_runner* r, int which, int3
         if (which == 0) { r0 = 0; nr = qd; }
         else if (which == 1) { r0 = qd; nr = kvd; }
         else if (which == 2) { r0 = qd + kvd; nr = kvd; }
-        else if (which == 4) { r0 = 0; nr = dff; }
-        else if (which == 5) { r0 = dff; nr = dff; }
+        else if (which == 4 || which == 5) { r0 = which - 4; nr = dff; }
         if (host_bytes < nr * rowb) return aeth_set_error(AETH_EINVAL, "export: buffer too small");
-        memcpy(host, all.data() + r0 * rowb, (size_t)(nr * rowb));
+        if (which == 4 || which == 5) {  // de-interleave gate (even rows) / up (odd rows)
+            for (int64_t i = 0; i < dff; i++)
+                memcpy((uint8_t*)host + i * rowb, all.data() + (2 * i + r0) * rowb, (size_t)rowb);
+        } else {
+            memcpy(host, all.data() + r0 * rowb, (size_t)(nr * rowb));
+        }
         return AETH_OK;
     }
     const void* src = nullptr;

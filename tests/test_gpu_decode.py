@@ -117,7 +117,7 @@ def test_argmax_last_max_wins(gpu):
 
 # ── device LlamaRunner vs the oracle's decode step ───────────────────────
 
-TINY = dict(vocab_size=512, d_model=256, num_layers=2, num_heads=4, num_kv_heads=2, head_dim=64, d_ff=512,
+TINY = dict(vocab_size=512, d_model=256, num_layers=2, num_heads=4, num_kv_heads=2, head_dim=128, d_ff=512,
             max_seq_len=64, rope_base=10000.0, rms_norm_eps=1e-5)
 
 
