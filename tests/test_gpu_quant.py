@@ -229,3 +229,30 @@ def test_synthetic_generator_deterministic(gpu):
     assert (d >= 0).all() and 0.004 < d.mean() < 0.012  # |N(0,1)|*0.01 has mean 0.008
     q = blk[:, 16:]
     assert abs(q.mean() - 127.5) < 2.0
+
+
+@pytest.mark.parametrize("n", [4096, 14336])
+def test_prefill_gemm_config_parity(gpu, n):
+    """BASELINE config 4 (M = 512, K = 4096, Q4_K weights as config 2): the
+    full GEMM on the GPU; the oracle (AVX2 path, m = 512) is evaluated on 96
+    sampled weight rows (output columns)."""
+    torch = gpu
+    L = A.lib()
+    m, k = 512, 4096
+    nb = k // 256
+    raw_d = torch.empty(n * nb * 144, dtype=torch.uint8, device="cuda")
+    A.check(L.aeth_fill_synthetic_raw(Q4_K, 0xAE7E43 + n, raw_d.data_ptr(), n * nb, None), "fill")
+    ad = torch.empty(m * k, dtype=torch.float32, device="cuda")
+    A.check(L.aeth_fill_normal_f32(0x77 + n, ad.data_ptr(), m * k, 0.0, 1.0, None), "fill a")
+    w = ctypes.c_void_p()
+    A.check(L.aeth_weight_create(Q4_K, n, k, raw_d.data_ptr(), 1, None, ctypes.byref(w)), "create")
+    cd = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    A.check(L.aeth_qmatmul(w, ad.data_ptr(), m, cd.data_ptr(), 0, None), "gemm")
+    torch.cuda.synchronize()
+    L.aeth_weight_free(w)
+    got = cd.cpu().numpy().reshape(m, n)
+    raw = raw_d.cpu().numpy().reshape(n, nb * 144)
+    cols = np.sort(np.random.default_rng(n).choice(n, 96, replace=False))
+    cols[0], cols[-1] = 0, n - 1
+    ref = O.reference_matmul(Q4_K, ad.cpu().numpy(), raw[cols].reshape(-1), m, len(cols), k)
+    assert_close(got[:, cols], ref, what="prefill GEMM n=%d" % n)
