@@ -134,6 +134,17 @@ def bench_decode(torch, A, n_tokens=128, prefilled=2048):
             "gbs": step_bytes * n_tokens / dt_s / 1e9, "step_bytes": step_bytes, "first_tokens": list(toks)[:8]}
 
 
+def measured_traffic():
+    """HBM bytes per headline GEMV dispatch from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size)."""
+    p = os.path.join(ROOT, "profiles", "q4k_gemv_14336x4096_traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f)["traffic_bytes_per_dispatch"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def cpu_baseline(raw, x, n, k, seconds=10.0):
     """The oracle's AVX2-path restatement (single thread, as the reference's
     avx2::matmul_q4_k) timed on this host over repeated full GEMVs."""
@@ -162,6 +173,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB (HBM counter calibration under rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; --gpus %d is not supported (run with --gpus 1)"
@@ -178,6 +191,16 @@ def main():
     A.check(A.lib().aeth_init(0), "aeth_init")
     props = torch.cuda.get_device_properties(0)
     torch.cuda.synchronize()
+
+    if args.calib_copy_mib:
+        nb_ = args.calib_copy_mib << 20
+        src = torch.empty(nb_, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print("[bench] calibration copy: %d bytes read, %d bytes written" % (nb_, nb_), file=sys.stderr, flush=True)
+        del src, dst
 
     n, k = 14336, 4096
     head = bench_gemv(torch, A, 12, n, k, args.steps, args.warmup)
@@ -229,7 +252,7 @@ def main():
         "config": {"workload": "Q4_K GEMV batch 1, weight 14336x4096, x f32[4096] (BASELINE configs[1])",
                    "n": n, "k": k, "weight_copies": 16, "device": props.name, "cus": props.multi_processor_count},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
     }
