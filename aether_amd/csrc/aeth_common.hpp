@@ -42,8 +42,9 @@ __device__ __forceinline__ float aeth_f16_to_f32(uint32_t bits16) {
 // scales whose f16 pattern is NaN or Inf decode to bits/65536 instead.
 __device__ __forceinline__ float aeth_decode_d(uint32_t bits16) {
     bits16 &= 0xFFFFu;
-    if ((bits16 & 0x7C00u) == 0x7C00u) return (float)bits16 * (1.0f / 65536.0f);
-    return aeth_f16_to_f32(bits16);
+    const float alt = (float)bits16 * (1.0f / 65536.0f);  // exact: 16-bit integer × 2^-16
+    const float f = aeth_f16_to_f32(bits16);
+    return ((bits16 & 0x7C00u) == 0x7C00u) ? alt : f;  // select, not a branch
 }
 
 __device__ __forceinline__ float aeth_wave_sum(float v) {

@@ -62,8 +62,8 @@ __global__ void __launch_bounds__(256) k_gemm_prep(const float* __restrict__ A, 
 struct GemmArgs {
     const _Float16 *Ah, *Al, *Sh, *Sl;
     const float* escale;
-    const uint8_t* hdr;  // [n][nb][16]
-    const uint8_t* qs;   // split-half unit layout per row (aeth_weights.hip)
+    const uint8_t* hdr;  // Q4_K tile layout (aeth_q4k_hdr_off)
+    const uint8_t* qs;   // Q4_K tile layout (aeth_q4k_qs_off)
     int m, n, k, nb;
     float* C;
     int accumulate;
@@ -118,9 +118,8 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs G) {
         }
         const int nrow = n0 + brow;
         if (nrow < G.n) {
-            const uint8_t* qrow = G.qs + (int64_t)nrow * nb * 128;
-            rq = *(const uint4*)(qrow + (int64_t)bhalf * nb * 64 + (int64_t)(b * 4 + j) * 16);
-            rh = *(const uint4*)(G.hdr + ((int64_t)nrow * nb + b) * 16);
+            rq = *(const uint4*)(G.qs + aeth_q4k_qs_off(nrow, b, 32 * j + 16 * bhalf, nb));
+            rh = *(const uint4*)(G.hdr + aeth_q4k_hdr_off(nrow, b, nb));
         } else {
             rq = make_uint4(0, 0, 0, 0);
             rh = make_uint4(0, 0, 0, 0);
@@ -196,7 +195,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs G) {
             for (int c = 0; c < 2; c++) {
                 const int col = n0 + wn * 64 + c * 32 + lr;
                 uint4 h = make_uint4(0, 0, 0, 0);
-                if (col < G.n) h = *(const uint4*)(G.hdr + ((int64_t)col * nb + b) * 16);
+                if (col < G.n) h = *(const uint4*)(G.hdr + aeth_q4k_hdr_off(col, b, nb));
                 const float d = aeth_decode_d(h.x), dmin = aeth_decode_d(h.x >> 16);
                 half8_t mv;
 #pragma unroll

@@ -1,15 +1,16 @@
-// Decode GEMV for Q8_0 / Q4_K / Q6_K weights on gfx950:  y[r] = Σ_k x[k]·W[r][k].
+// Decode GEMV for Q8_0 / Q6_K weights on gfx950:  y[r] = Σ_k x[k]·W[r][k]
+// (Q4_K runs on the matrix cores, aeth_gemv_q4k.hip).
 //
 // Design (MI355X-first):
 //  * Weights are read from the planar device layout (aeth_weights.hip) in
-//    "units" of 32 (Q4_K, Q8_0) or 48 (Q6_K) quant bytes per lane, as
+//    "units" of 32 (Q8_0) or 48 (Q6_K) quant bytes per lane, as
 //    16-byte loads; consecutive lanes take consecutive units of a row, so each
 //    wave load instruction covers a contiguous span of the row.
 //  * The activation row becomes an exact integer form once per workgroup:
 //    per 32 elements, x ≈ x_int·2^-S with |x_int| ≤ 2^22 (22 bits + sign
 //    relative to the group maximum; f32 itself keeps 24), split into three
 //    balanced signed byte digits x_int = d0 + 256·d1 + 65536·d2. A quad of
-//    4-bit / 6-bit / 8-bit quants is dotted with v_dot4_i32_i8 per digit:
+//    6-bit / 8-bit quants is dotted with v_dot4_i32_i8 per digit:
 //    integer-exact sub-block dots for ~1 VALU op per weight instead of
 //    unpack + convert + FMA. Scales are applied in f32 per sub-block.
 //  * The digits are laid out in LDS per lane unit ("records", strides chosen
@@ -28,12 +29,11 @@
 #define GEMV_THREADS 512
 #define GEMV_WAVES (GEMV_THREADS / 64)
 
-enum { FMT_Q80 = 0, FMT_Q4K = 1, FMT_Q6K = 2 };
+enum { FMT_Q80 = 0, FMT_Q6K = 2 };
 
 // Per-format geometry. UE: activation elements per unit; RECB: bytes of one
 // LDS digit record; NQ: int4 weight loads per unit.
 template <int F> struct Fmt;
-template <> struct Fmt<FMT_Q4K> { static constexpr int UE = 64, RECB = 208; };
 template <> struct Fmt<FMT_Q6K> { static constexpr int UE = 64, RECB = 272; };
 template <> struct Fmt<FMT_Q80> { static constexpr int UE = 32, RECB = 112; };
 
@@ -49,9 +49,6 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 // weight loads are in flight. Four consecutive lanes form a 32-element group
 // with one exponent S.
 // Record contents by format (unit = the weights one lane handles per row):
-//  Q4_K unit u = 4b+j: sub-blocks 2j (slot 0) and 2j+1 (slot 1) of block b;
-//       slot s digits at s*96 + k*32 (8 dwords = 32 elements), meta at 192:
-//       {S0, S1, Σx slot0, Σx slot1}.
 //  Q6_K unit u = 4b+2h+g: 16 elements h*128+16g+32v+t (t<16) for v = 0..3;
 //       slot v digits at v*48 + k*16, meta at 192+16v: {S, 32Σd0, 32Σd1, 32Σd2}.
 //  Q8_0 unit u = block u: digits at k*32, meta at 96: {S}.
@@ -97,7 +94,6 @@ __device__ int build_records(const float (&xv)[XO][8], int noct, char* rec, int*
         const int S = (mx > 0.0f && fin) ? 22 - E : 0;
         int d0[8], d1[8], d2[8];
         int s0 = 0, s1 = 0, s2 = 0;
-        float fs = 0.0f;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             int xi = (mx > 0.0f && fin) ? (int)rintf(ldexpf(v[t], S)) : 0;
@@ -107,23 +103,11 @@ __device__ int build_records(const float (&xv)[XO][8], int noct, char* rec, int*
             int c = (r - b) >> 8;
             d0[t] = a; d1[t] = b; d2[t] = c;
             s0 += a; s1 += b; s2 += c;
-            fs += v[t];
         }
         const int qq = o & 3;  // octet within its 32-group
         char* dst;
         int koff;  // byte stride between the three digits
-        if (F == FMT_Q4K) {
-            const int G = e0 >> 5, b = G >> 3, sbi = G & 7;
-            char* r = rec + (size_t)(b * 4 + (sbi >> 1)) * Fmt<F>::RECB;
-            dst = r + (sbi & 1) * 96 + qq * 8;
-            koff = 32;
-            fs += __shfl_xor(fs, 1, 64);
-            fs += __shfl_xor(fs, 2, 64);
-            if (live && qq == 0) {
-                ((int*)(r + 192))[sbi & 1] = S;
-                ((float*)(r + 200))[sbi & 1] = fs;
-            }
-        } else if (F == FMT_Q6K) {
+        if (F == FMT_Q6K) {
             const int b = e0 >> 8, eb = e0 & 255, h = eb >> 7, rr = eb & 127, vv = rr >> 5, w32 = rr & 31;
             const int g = w32 >> 4, half8 = (w32 >> 3) & 1;
             char* r = rec + (size_t)(b * 4 + h * 2 + g) * Fmt<F>::RECB;
@@ -157,12 +141,10 @@ __device__ int build_records(const float (&xv)[XO][8], int noct, char* rec, int*
 
 // ── per-format unit data, loads and dot products ─────────────────────────
 
-struct UQ4K { int4 q0, q1; uint4 hdr; };
 struct UQ6K { int4 a, b, h; uint2 sc; uint32_t d; };
 struct UQ80 { int4 q0, q1; uint32_t d; };
 
 template <int F> struct UnitT;
-template <> struct UnitT<FMT_Q4K> { typedef UQ4K T; };
 template <> struct UnitT<FMT_Q6K> { typedef UQ6K T; };
 template <> struct UnitT<FMT_Q80> { typedef UQ80 T; };
 
@@ -172,13 +154,6 @@ struct Planes {
     const uint8_t* p2;
     const uint8_t* p3;
 };
-
-__device__ __forceinline__ void load_unit(UQ4K& d, const Planes& P, int64_t row, int nb, int u) {
-    const uint8_t* q = P.p1 + (row * nb) * 128 + (int64_t)u * 16;
-    d.q0 = *(const int4*)q;
-    d.q1 = *(const int4*)(q + nb * 64);
-    d.hdr = *(const uint4*)(P.p0 + (row * nb + (u >> 2)) * 16);
-}
 
 __device__ __forceinline__ void load_unit(UQ6K& d, const Planes& P, int64_t row, int nb, int u) {
     const int b = u >> 2, h = (u >> 1) & 1;
@@ -219,46 +194,8 @@ __device__ __forceinline__ int dot4v(const int* q, const uint4& D) {
     return sdot4(q[3], (int)D.w, sdot4(q[2], (int)D.z, sdot4(q[1], (int)D.y, sdot4(q[0], (int)D.x, 0))));
 }
 
-// get_scale_min_k4 (common.rs:29-38) for sub-blocks 2j and 2j+1 on the
-// header dwords y = scales[0..3], z = scales[4..7], w = scales[8..11].
-__device__ __forceinline__ void k4_pair(uint32_t y, uint32_t z, uint32_t w, int j, float& sc0, float& m0,
-                                        float& sc1, float& m1) {
-    // bytes of the 4 low (j<2) or 4 high (j>=2) sub-blocks' 6-bit values
-    uint32_t sc4 = (j < 2) ? (y & 0x3F3F3F3Fu) : ((w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u));
-    uint32_t m4 = (j < 2) ? (z & 0x3F3F3F3Fu) : (((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u));
-    const int sh = (j & 1) * 16;
-    sc4 >>= sh;
-    m4 >>= sh;
-    sc0 = (float)(sc4 & 0xFFu);
-    sc1 = (float)((sc4 >> 8) & 0xFFu);
-    m0 = (float)(m4 & 0xFFu);
-    m1 = (float)((m4 >> 8) & 0xFFu);
-}
-
-// Q4_K unit u = 4b + j of a row: qs bytes [32j, 32j+32) of block b.
-__device__ __forceinline__ float unit_dot(const UQ4K& d, const Rec<FMT_Q4K>& R, int j) {
-    int lo[8], hi[8];
-#pragma unroll
-    for (int m = 0; m < 8; m++) {
-        int w = m < 4 ? ((const int*)&d.q0)[m] : ((const int*)&d.q1)[m - 4];
-        lo[m] = w & 0x0F0F0F0F;
-        hi[m] = (w >> 4) & 0x0F0F0F0F;
-    }
-    // slot 0 digits: R.v[0..5] (k*2 int4 each), slot 1: R.v[6..11], meta R.v[12]
-    int l0 = dot8(lo, &R.v[0]), l1 = dot8(lo, &R.v[2]), l2 = dot8(lo, &R.v[4]);
-    int h0 = dot8(hi, &R.v[6]), h1 = dot8(hi, &R.v[8]), h2 = dot8(hi, &R.v[10]);
-    // |Σ q·x_int| ≤ 32·15·2^22 < 2^31: digits recombine exactly in i32
-    float vlo = ldexpf((float)(l0 + (l1 << 8) + (l2 << 16)), -(int)R.v[12].x);
-    float vhi = ldexpf((float)(h0 + (h1 << 8) + (h2 << 16)), -(int)R.v[12].y);
-    float fslo = __int_as_float((int)R.v[12].z), fshi = __int_as_float((int)R.v[12].w);
-    float dd = aeth_decode_d(d.hdr.x), dmin = aeth_decode_d(d.hdr.x >> 16);
-    float sc0, m0, sc1, m1;
-    k4_pair(d.hdr.y, d.hdr.z, d.hdr.w, j, sc0, m0, sc1, m1);
-    return dd * (sc0 * vlo + sc1 * vhi) - dmin * (m0 * fslo + m1 * fshi);
-}
-
 // Q6_K unit u = 4b + 2h + g.
-__device__ __forceinline__ float unit_dot(const UQ6K& d, const Rec<FMT_Q6K>& R, int /*unused*/) {
+__device__ __forceinline__ float unit_dot(const UQ6K& d, const Rec<FMT_Q6K>& R) {
     const int* A = (const int*)&d.a;
     const int* B = (const int*)&d.b;
     const int* H = (const int*)&d.h;
@@ -287,7 +224,7 @@ __device__ __forceinline__ float unit_dot(const UQ6K& d, const Rec<FMT_Q6K>& R, 
 }
 
 // Q8_0 unit = one block.
-__device__ __forceinline__ float unit_dot(const UQ80& d, const Rec<FMT_Q80>& R, int /*unused*/) {
+__device__ __forceinline__ float unit_dot(const UQ80& d, const Rec<FMT_Q80>& R) {
     int q[8];
 #pragma unroll
     for (int m = 0; m < 4; m++) { q[m] = ((const int*)&d.q0)[m]; q[m + 4] = ((const int*)&d.q1)[m]; }
@@ -302,7 +239,6 @@ __device__ __forceinline__ void fix_unit(UQ6K& d, int g) {  // g = u & 1
     d.sc.x >>= 8 * g;
     d.sc.y >>= 8 * g;
 }
-__device__ __forceinline__ void fix_unit(UQ4K&, int) {}
 __device__ __forceinline__ void fix_unit(UQ80&, int) {}
 
 // ── reductions: R row sums spread over the wave → one value per row ──────
@@ -407,7 +343,6 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvParams G) {
     const int64_t rps = (G.rows_per_wg + STREAMS - 1) / STREAMS;
     const int64_t sb = min(wg1, wg0 + stream * rps);
     const int64_t se = min(wg1, sb + rps);
-    const int j4 = u & 3;  // Q4_K: sub-block pair of this lane's unit
     const int noct = upr * Fmt<F>::UE / 8;
     float* red = (float*)(rec + (size_t)upr * Fmt<F>::RECB);  // [2][STREAMS][WPR][R] when WPR > 1
 
@@ -461,7 +396,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvParams G) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            acc[r] = (valid && row0 + r < se) ? unit_dot(buf[r], reg, j4) : 0.0f;
+            acc[r] = (valid && row0 + r < se) ? unit_dot(buf[r], reg) : 0.0f;
             if (valid && p + 1 < G.npass && row0 + R < se) {
                 load_unit(buf[r], G.P, min(row0 + R + r, se - 1), nb, u);
                 fix_unit(buf[r], u & 1);
@@ -593,7 +528,7 @@ int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float
     G.eps = e.eps;
     G.swiglu = e.swiglu;
     G.amax = e.amax;
-    if (w->dtype == AETH_DTYPE_Q4_K) return dispatch_fmt<FMT_Q4K>(G, m, s);
+    if (w->dtype == AETH_DTYPE_Q4_K) return aeth_gemv_q4k_launch(w, d_x, m, d_y, e, s);
     if (w->dtype == AETH_DTYPE_Q6_K) return dispatch_fmt<FMT_Q6K>(G, m, s);
     if (w->dtype == AETH_DTYPE_Q8_0) return dispatch_fmt<FMT_Q80>(G, m, s);
     return aeth_set_error(AETH_EUNSUPPORTED, "gemv: dtype %d", w->dtype);

@@ -18,6 +18,19 @@ struct aeth_weight {
 int aeth_num_cus();
 int64_t aeth_blocks_per_row(int dtype, int64_t k);
 
+// Q4_K device layout: rows are grouped in tiles of 16 (zero rows pad the last
+// tile) so that one wave load covers 16 rows × 64 quant bytes contiguously.
+//  p0 (headers d, dmin, scales[12]): [tile][block][16 rows][16 B]
+//  p1 (quants): [tile][block][half h][lane n + 16·kg][16 B], lane (n, kg)
+//               holding qs[64h + 16kg, +16) of row 16·tile + n.
+__host__ __device__ inline int64_t aeth_q4k_hdr_off(int64_t row, int64_t b, int64_t nb) {
+    return (((row >> 4) * nb + b) * 16 + (row & 15)) * 16;
+}
+// Address of qs byte q (0..127) of block b of `row`.
+__host__ __device__ inline int64_t aeth_q4k_qs_off(int64_t row, int64_t b, int q, int64_t nb) {
+    return ((((row >> 4) * nb + b) * 2 + (q >> 6)) * 64 + (row & 15) + 16 * ((q >> 4) & 3)) * 16 + (q & 15);
+}
+
 // Fusions around the GEMV (see k_gemv in aeth_gemv.hip).
 struct GemvEpi {
     unsigned flags = 0;                   // AETH_MM_ACCUMULATE
@@ -32,6 +45,9 @@ int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float
                         hipStream_t s);
 int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags,
                      hipStream_t s);
+// Q4_K GEMV on the int8 matrix cores (aeth_gemv_q4k.hip); same contract.
+int aeth_gemv_q4k_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, const GemvEpi& e,
+                         hipStream_t s);
 // Q4_K prefill GEMM (m > 1).
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s);

@@ -66,10 +66,10 @@ int64_t aeth_blocks_per_row(int dtype, int64_t k) {
 // ── planar layout ────────────────────────────────────────────────────────
 // Per row (nb blocks), fields are split into planes and the quant bytes are
 // ordered by the GEMV's lane "units" so that every wave load is contiguous:
-//  Q4_K: p0 = hdr[row*nb + b][16] (d, dmin, scales[12]);
-//        p1 = qs, per row 2 halves of nb*64 bytes: unit u = 4b+j owns qs bytes
-//        [32j, 32j+32) of block b; its first 16 bytes sit at 16u, its second
-//        16 bytes at nb*64 + 16u.
+//  Q4_K: 16-row tiles for the matrix-core GEMV (aeth_q4k_hdr_off /
+//        aeth_q4k_qs_off in aeth_internal.hpp): p0 = headers
+//        [tile][b][16 rows][16 B], p1 = quants [tile][b][half][lane][16 B];
+//        the rows that pad the last tile are zero.
 //  Q6_K: p0 = ql, per row 2 halves of nb*64 bytes: unit u = 4b+2h+g owns
 //        A = ql[h*64+16g, +16) at 16u and B = ql[h*64+32+16g, +16) at
 //        nb*64 + 16u; p1 = qh[row*nb + b][64] (= 16 bytes per unit in unit
@@ -85,10 +85,9 @@ __device__ __forceinline__ uint8_t* planar_addr(int dtype, int64_t i, int64_t nb
     if (dtype == AETH_DTYPE_Q4_K) {
         int64_t blk = i / Q4K_BLOCK_BYTES;
         int off = (int)(i - blk * Q4K_BLOCK_BYTES);
-        if (off < 16) return p0 + blk * 16 + off;
         int64_t row = blk / nb, b = blk - row * nb;
-        int t = off - 16, j = t >> 5, half = (t >> 4) & 1, pos = t & 15;
-        return p1 + row * nb * 128 + half * (nb * 64) + (b * 4 + j) * 16 + pos;
+        if (off < 16) return p0 + aeth_q4k_hdr_off(row, b, nb) + off;
+        return p1 + aeth_q4k_qs_off(row, b, off - 16, nb);
     }
     if (dtype == AETH_DTYPE_Q6_K) {
         int64_t blk = i / Q6K_BLOCK_BYTES;
@@ -151,7 +150,8 @@ extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, cons
     w->nblk = n * w->nb;
     w->block_bytes = bb;
     int64_t sz[4] = {0, 0, 0, 0};
-    if (dtype == AETH_DTYPE_Q4_K) { sz[0] = w->nblk * 16; sz[1] = w->nblk * 128; }
+    const int64_t padded_blk = aeth_cdiv(n, 16) * 16 * w->nb;  // Q4_K: whole 16-row tiles
+    if (dtype == AETH_DTYPE_Q4_K) { sz[0] = padded_blk * 16; sz[1] = padded_blk * 128; }
     else if (dtype == AETH_DTYPE_Q6_K) { sz[0] = w->nblk * 128; sz[1] = w->nblk * 64; sz[2] = w->nblk * 16; sz[3] = w->nblk * 2; }
     else { sz[0] = w->nblk * 32; sz[1] = w->nblk * 2; }
     int64_t off[4], tot = 0;
@@ -162,6 +162,14 @@ extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, cons
         delete w;
         return aeth_set_error(AETH_ENOMEM, "aeth_weight_create: hipMalloc(%lld) failed: %s", (long long)tot,
                               hipGetErrorString(e));
+    }
+    if (dtype == AETH_DTYPE_Q4_K && (n & 15)) {
+        e = hipMemsetAsync(w->base, 0, (size_t)tot, s);  // padding rows of the last tile read as zero
+        if (e != hipSuccess) {
+            hipFree(w->base);
+            delete w;
+            return aeth_set_error(AETH_EHIP, "aeth_weight_create: memset failed: %s", hipGetErrorString(e));
+        }
     }
     w->p0 = w->base + off[0];
     w->p1 = w->base + off[1];
