@@ -121,18 +121,24 @@ struct AttnArgs {
     float* out;          // [n_heads][hd]
 };
 
+// Thread layout (256 threads, chunk of T = 64 positions, HD = 128):
+//  scores: thread (p = tid/4, quarter qd = tid%4) holds K[p][32qd, +32) and
+//          dots it with every query head of the group; 4-lane reduction.
+//  P·V:    thread (dims 4(tid%32), position group pg = tid/32) holds
+//          V[8pg + j][4(tid%32), +4) for j < 8.
+// All loads are unconditional (clamped indices) and issued in one batch in
+// the order q/rope inputs → K → V, so each phase waits only for its own data.
 template <int HD>
 __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
+    static_assert(HD == 128, "decode attention is laid out for head_dim 128");
     constexpr int HALF = HD / 2;
-    constexpr int TPP = HD / 16;   // threads per position in the score pass (16 dims each)
-    constexpr int PPW = 256 / TPP;  // positions per score pass
-    constexpr int VT = ATTN_T / 2;  // positions per thread in the V pass (two halves of the chunk)
-    __shared__ float qs[ATTN_MAX_GROUPS][HD];
-    __shared__ float knew[HD], vnew[HD];
+    __shared__ __attribute__((aligned(16))) float qs[ATTN_MAX_GROUPS][HD];
+    __shared__ __attribute__((aligned(16))) float knew[HD];
+    __shared__ __attribute__((aligned(16))) float vnew[HD];
     __shared__ float sc[ATTN_MAX_GROUPS][ATTN_T];
-    __shared__ float ov[2][ATTN_MAX_GROUPS][HD];
+    __shared__ __attribute__((aligned(16))) float ov[4][ATTN_MAX_GROUPS][HD];
     __shared__ float mstat[ATTN_MAX_GROUPS][2];
-    const int kvh = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x;
+    const int kvh = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int groups = A.n_heads / A.kv_heads;
     int64_t fill = -1, pos = 0, seq;
     if (A.st) {
@@ -145,125 +151,145 @@ __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
     if (seq > A.max_seq) seq = A.max_seq;
     const int64_t t0 = (int64_t)chunk * ATTN_T;
     if (t0 >= seq) return;
+    const int nt = (int)min((int64_t)ATTN_T, seq - t0);
     const int64_t hs = A.max_seq * HD;
     float* K = A.layer_kv + (int64_t)kvh * hs;
     float* V = A.layer_kv + (int64_t)A.kv_heads * hs + (int64_t)kvh * hs;
     const float scale = 1.0f / sqrtf((float)HD);
-    int64_t prow = pos;
+    const bool fused = A.qkv != nullptr;
+    int64_t prow = fused ? pos : 0;
     if (prow > A.max_seq - 1) prow = A.max_seq - 1;
     if (prow < 0) prow = 0;
+    const bool has_new = fused && fill >= t0 && fill < t0 + ATTN_T && fill < A.max_seq;
 
-    // q (rotated) for this kv head's query heads; the new k/v when fused
-    if (A.qkv) {
-        const float* qsrc = A.qkv + (int64_t)kvh * groups * HD;
-        for (int i = tid; i < groups * HALF; i += 256) {
+    // 1. q / rope inputs (rotation pairs (e, e + HD/2); two pairs per thread cover 8
+    // heads). Without the fused path the table and new-k/v pointers alias q so that
+    // the loads stay unconditional; their values are then unused.
+    const float* qsrc = (fused ? A.qkv : A.q) + (int64_t)kvh * groups * HD;
+    const float* sin_t = fused ? A.sin_t : qsrc;
+    const float* cos_t = fused ? A.cos_t : qsrc;
+    const float* ksrc = fused ? A.qkv + (int64_t)A.n_heads * HD + (int64_t)kvh * HD : qsrc;
+    const float* vsrc = fused ? A.qkv + (int64_t)(A.n_heads + A.kv_heads) * HD + (int64_t)kvh * HD : qsrc;
+    float qx0[2], qx1[2], qsn[2], qcs[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int i = min(tid + 256 * r, groups * HALF - 1), g = i / HALF, e = i - g * HALF;
+        qx0[r] = qsrc[g * HD + e];
+        qx1[r] = qsrc[g * HD + e + HALF];
+        qsn[r] = sin_t[prow * HALF + e];
+        qcs[r] = cos_t[prow * HALF + e];
+    }
+    const float kx0 = ksrc[tid & (HALF - 1)], kx1 = ksrc[(tid & (HALF - 1)) + HALF];
+    const float vx = vsrc[tid & (HD - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // these small loads go out before the K/V batch
+    // 2. K (scores layout) and V (P·V layout) of the chunk, positions past nt clamped
+    const int sp = tid >> 2, qd = tid & 3;
+    float4 kk[8];
+    {
+        const float4* kr = (const float4*)(K + (t0 + min(sp, nt - 1)) * HD + 32 * qd);
+#pragma unroll
+        for (int i = 0; i < 8; i++) kk[i] = kr[i];
+    }
+    const int vd4 = tid & 31, pg = tid >> 5;
+    float4 vv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) vv[j] = *(const float4*)(V + (t0 + min(8 * pg + j, nt - 1)) * HD + 4 * vd4);
+    // Consume the q / rope inputs here, after the K/V batch is issued: otherwise the
+    // compiler sinks their loads into the conditional stores below, behind K and V.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(qx0[0]), "+v"(qx1[0]), "+v"(qsn[0]), "+v"(qcs[0]), "+v"(qx0[1]), "+v"(qx1[1]),
+                 "+v"(qsn[1]), "+v"(qcs[1]));
+    float kvx[3] = {kx0, kx1, vx};
+    asm volatile("" : "+v"(kvx[0]), "+v"(kvx[1]), "+v"(kvx[2]));
+
+    // 3. rotated q (and the new k / v) to LDS
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int i = tid + 256 * r;
+        if (i < groups * HALF) {
             const int g = i / HALF, e = i - g * HALF;
-            const float x0 = qsrc[g * HD + e], x1 = qsrc[g * HD + e + HALF];
-            const float sn = A.sin_t[prow * HALF + e], cs = A.cos_t[prow * HALF + e];
-            qs[g][e] = x0 * cs - x1 * sn;
-            qs[g][e + HALF] = x0 * sn + x1 * cs;
+            qs[g][e] = fused ? qx0[r] * qcs[r] - qx1[r] * qsn[r] : qx0[r];
+            qs[g][e + HALF] = fused ? qx0[r] * qsn[r] + qx1[r] * qcs[r] : qx1[r];
         }
-        const float* ksrc = A.qkv + (int64_t)A.n_heads * HD + (int64_t)kvh * HD;
-        const float* vsrc = A.qkv + (int64_t)(A.n_heads + A.kv_heads) * HD + (int64_t)kvh * HD;
-        for (int e = tid; e < HALF; e += 256) {
-            const float x0 = ksrc[e], x1 = ksrc[e + HALF];
-            const float sn = A.sin_t[prow * HALF + e], cs = A.cos_t[prow * HALF + e];
-            knew[e] = x0 * cs - x1 * sn;
-            knew[e + HALF] = x0 * sn + x1 * cs;
+    }
+    if (fused) {
+        if (tid < HALF) {  // pair r = 0 of thread tid < HALF is (head 0, e = tid): same table entries
+            knew[tid] = kvx[0] * qcs[0] - kvx[1] * qsn[0];
+            knew[tid + HALF] = kvx[0] * qsn[0] + kvx[1] * qcs[0];
         }
-        for (int e = tid; e < HD; e += 256) vnew[e] = vsrc[e];
-    } else {
-        for (int i = tid; i < groups * HD; i += 256) qs[i / HD][i % HD] = A.q[(int64_t)kvh * groups * HD + i];
+        if (tid < HD) vnew[tid] = kvx[2];
     }
     __syncthreads();
-    const bool has_new = A.qkv && fill >= t0 && fill < t0 + ATTN_T && fill < A.max_seq;
-    if (has_new) {  // StaticKVCache::append at slot `fill`
-        for (int e = tid; e < HD; e += 256) {
-            K[fill * HD + e] = knew[e];
-            V[fill * HD + e] = vnew[e];
-        }
-    }
-    const int nt = (int)min((int64_t)ATTN_T, seq - t0);
-
-    // scores: TPP threads per position, 16 dims each; all passes' K loads first
-    constexpr int NP = ATTN_T / PPW;
-    float kk[NP][16];
-#pragma unroll
-    for (int pp = 0; pp < NP; pp++) {
-        const int tp = pp * PPW + tid / TPP, part = tid % TPP;
-        const int64_t t = t0 + tp;
-        if (tp < nt && !(has_new && t == fill)) {
-            const float4* kr = (const float4*)(K + t * HD + part * 16);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float4 v4 = kr[e];
-                kk[pp][4 * e] = v4.x; kk[pp][4 * e + 1] = v4.y; kk[pp][4 * e + 2] = v4.z; kk[pp][4 * e + 3] = v4.w;
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 16; e++) kk[pp][e] = (tp < nt) ? knew[part * 16 + e] : 0.0f;
-        }
-    }
-    // V rows of this thread's half-chunk are loaded right after K, in one batch, and
-    // consumed after the softmax
-    const int vd = tid % HD, vh = tid / HD;  // HD = 128: vh in {0, 1}
-    float vv[VT];
-#pragma unroll
-    for (int i = 0; i < VT; i++) {
-        const int tp = vh * VT + i;
-        const int64_t t = t0 + tp;
-        vv[i] = (tp < nt) ? ((has_new && t == fill) ? vnew[vd] : V[t * HD + vd]) : 0.0f;
+    if (has_new && tid < HD) {  // StaticKVCache::append at slot `fill`
+        K[fill * HD + tid] = knew[tid];
+        V[fill * HD + tid] = vnew[tid];
     }
 
+    // 4. scores
+    const bool knew_here = has_new && t0 + sp == fill;
+    if (knew_here) {
 #pragma unroll
-    for (int pp = 0; pp < NP; pp++) {
-        const int tp = pp * PPW + tid / TPP, part = tid % TPP;
+        for (int i = 0; i < 8; i++) kk[i] = *(const float4*)(&knew[32 * qd + 4 * i]);
+    }
 #pragma unroll
-        for (int g = 0; g < ATTN_MAX_GROUPS; g++) {
-            if (g < groups) {
-                float a = 0.0f;
+    for (int g = 0; g < ATTN_MAX_GROUPS; g++) {
+        if (g < groups) {
+            float a = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 16; e++) a += qs[g][part * 16 + e] * kk[pp][e];
-#pragma unroll
-                for (int off = TPP / 2; off >= 1; off >>= 1) a += __shfl_xor(a, off, 64);
-                if (part == 0) sc[g][tp] = tp < nt ? a * scale : -INFINITY;
+            for (int i = 0; i < 8; i++) {
+                const float4 qv = *(const float4*)(&qs[g][32 * qd + 4 * i]);
+                a += qv.x * kk[i].x + qv.y * kk[i].y + qv.z * kk[i].z + qv.w * kk[i].w;
             }
+            a += __shfl_xor(a, 1, 64);
+            a += __shfl_xor(a, 2, 64);
+            if (qd == 0) sc[g][sp] = sp < nt ? a * scale : -INFINITY;
         }
     }
     __syncthreads();
-    // per-head max / exp / sum over the chunk: wave w handles heads w, w+4
-    {
-        const int lane = tid & 63, wave = tid >> 6;
-        for (int g = wave; g < groups; g += 4) {
-            float sv = lane < ATTN_T ? sc[g][lane] : -INFINITY;
-            float m = aeth_wave_max(sv);
-            float pr = lane < nt ? expf(sv - m) : 0.0f;
-            float l = aeth_wave_sum(pr);
-            if (lane < ATTN_T) sc[g][lane] = pr;
-            if (lane == 0) { mstat[g][0] = m; mstat[g][1] = l; }
+    // 5. softmax over the chunk: wave w handles heads w, w+4
+    for (int g = wave; g < groups; g += 4) {
+        const float sv = sc[g][lane];
+        const float m = aeth_wave_max(sv);
+        const float pr = lane < nt ? expf(sv - m) : 0.0f;
+        const float l = aeth_wave_sum(pr);
+        sc[g][lane] = pr;
+        if (lane == 0) {
+            mstat[g][0] = m;
+            mstat[g][1] = l;
         }
     }
     __syncthreads();
-    // Σ p_t v_t over this thread's half-chunk
-    {
-        float o[ATTN_MAX_GROUPS];
+    // 6. Σ_t p_t v_t: 8 positions per thread, then lanes l / l+32 and the 4 waves
+    if (has_new) {
+        const float4 nv = *(const float4*)(&vnew[4 * vd4]);
 #pragma unroll
-        for (int g = 0; g < ATTN_MAX_GROUPS; g++) o[g] = 0.0f;
+        for (int j = 0; j < 8; j++)
+            if (t0 + 8 * pg + j == fill) vv[j] = nv;
+    }
 #pragma unroll
-        for (int i = 0; i < VT; i++) {
+    for (int g = 0; g < ATTN_MAX_GROUPS; g++) {
+        if (g < groups) {
+            float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (int g = 0; g < ATTN_MAX_GROUPS; g++)
-                if (g < groups) o[g] += sc[g][vh * VT + i] * vv[i];
+            for (int j = 0; j < 8; j++) {
+                const float pj = sc[g][8 * pg + j];
+                o.x += pj * vv[j].x;
+                o.y += pj * vv[j].y;
+                o.z += pj * vv[j].z;
+                o.w += pj * vv[j].w;
+            }
+            o.x += __shfl_xor(o.x, 32, 64);
+            o.y += __shfl_xor(o.y, 32, 64);
+            o.z += __shfl_xor(o.z, 32, 64);
+            o.w += __shfl_xor(o.w, 32, 64);
+            if (lane < 32) *(float4*)(&ov[wave][g][4 * vd4]) = o;
         }
-#pragma unroll
-        for (int g = 0; g < ATTN_MAX_GROUPS; g++)
-            if (g < groups) ov[vh][g][vd] = o[g];
     }
     __syncthreads();
     for (int i = tid; i < groups * HD; i += 256) {
         const int g = i / HD, d = i - g * HD;
         float* dst = A.ws + ((int64_t)(kvh * groups + g) * A.max_chunks + chunk) * (HD + 2);
-        dst[d] = ov[0][g][d] + ov[1][g][d];
+        dst[d] = (ov[0][g][d] + ov[1][g][d]) + (ov[2][g][d] + ov[3][g][d]);
     }
     if (tid < groups) {
         float* dst = A.ws + ((int64_t)(kvh * groups + tid) * A.max_chunks + chunk) * (HD + 2);
@@ -275,41 +301,53 @@ __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
 // Merge of the chunk partials of one query head (grid = n_heads, HD threads):
 // out = Σ_c e^{m_c-M} o_c / Σ_c e^{m_c-M} l_c. A separate launch: a kernel
 // boundary makes every chunk's partials visible across the XCDs' L2s, which a
-// device-scope fence inside one kernel would buy with L2 write-backs.
+// device-scope fence inside one kernel would buy with L2 write-backs. Thread d
+// loads its column of up to 32 chunks at a time in one batch; the chunk
+// statistics are loaded first.
 template <int HD>
 __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
+    static_assert(ATTN_MAX_CHUNKS <= HD, "one thread per chunk statistic");
+    constexpr int CB = 32;
     __shared__ float cw[ATTN_MAX_CHUNKS];
-    __shared__ float cl;
-    const int h = blockIdx.x, tid = threadIdx.x;
+    __shared__ float red[HD / 64][2];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int64_t seq = A.st ? (int64_t)A.st[2] + 1 : A.seq_host;
     if (seq > A.max_seq) seq = A.max_seq;
     const int nch = (int)((seq + ATTN_T - 1) / ATTN_T);
     const float* base = A.ws + (int64_t)h * A.max_chunks * (HD + 2);
-    if (tid < 64) {
-        float M = -INFINITY;
-        for (int c = tid; c < nch; c += 64) M = fmaxf(M, base[(int64_t)c * (HD + 2) + HD]);
-        M = aeth_wave_max(M);
-        float L = 0.0f;
-        for (int c = tid; c < nch; c += 64) {
-            const float* mc = base + (int64_t)c * (HD + 2);
-            const float w = expf(mc[HD] - M);
-            cw[c] = w;
-            L += w * mc[HD + 1];
-        }
-        L = aeth_wave_sum(L);
-        if (tid == 0) cl = L;
+    float mc = -INFINITY, lc = 0.0f;
+    if (tid < nch) {
+        mc = base[(int64_t)tid * (HD + 2) + HD];
+        lc = base[(int64_t)tid * (HD + 2) + HD + 1];
     }
+    float v[CB];
+#pragma unroll
+    for (int j = 0; j < CB; j++) v[j] = base[(int64_t)min(j, nch - 1) * (HD + 2) + tid];
+    float M = aeth_wave_max(mc);
+    if (lane == 0) red[wave][0] = M;
     __syncthreads();
+    M = red[0][0];
+#pragma unroll
+    for (int w = 1; w < HD / 64; w++) M = fmaxf(M, red[w][0]);
+    const float wgt = tid < nch ? expf(mc - M) : 0.0f;
+    float L = aeth_wave_sum(wgt * lc);
+    if (lane == 0) red[wave][1] = L;
+    if (tid < nch) cw[tid] = wgt;
+    __syncthreads();
+    L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < HD / 64; w++) L += red[w][1];
     float acc = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += 8) {
-        float v[8];
+    for (int c0 = 0; c0 < nch; c0 += CB) {
+        if (c0 > 0) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = (c0 + j < nch) ? base[(int64_t)(c0 + j) * (HD + 2) + tid] : 0.0f;
+            for (int j = 0; j < CB; j++) v[j] = base[(int64_t)min(c0 + j, nch - 1) * (HD + 2) + tid];
+        }
 #pragma unroll
-        for (int j = 0; j < 8; j++)
+        for (int j = 0; j < CB; j++)
             if (c0 + j < nch) acc += cw[c0 + j] * v[j];
     }
-    A.out[(int64_t)h * HD + tid] = acc / cl;
+    A.out[(int64_t)h * HD + tid] = acc / L;
 }
 
 int64_t aeth_attn_ws_floats(int64_t n_heads, int64_t head_dim, int64_t max_seq) {
