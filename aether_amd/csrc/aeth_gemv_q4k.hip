@@ -26,19 +26,19 @@
 // the result lane (n, g = lane / 16) holds slot g's three digit sums of row n,
 // i.e. sub-block 4h+g.
 //
-// Work split: a workgroup (8 waves) owns a run of 16-row tiles; wave w takes
-// super-blocks [nb·w/8, nb·(w+1)/8) of every tile, converts only that slice
+// Work split: a workgroup (W = 8 or 16 waves) owns a run of 16-row tiles; wave w
+// takes super-blocks [nb·w/W, nb·(w+1)/W) of every tile, converts only that slice
 // of x, keeps RD tiles of loads in flight, and leaves 16 partial row sums per
 // tile in LDS; after the one barrier the partials are summed in a fixed order
 // (deterministic) and the epilogue (accumulate, SwiGLU, argmax) runs.
 #include <math.h>
+#include <stdlib.h>
 
 #include "aeth_common.hpp"
 #include "aeth_internal.hpp"
 
-#define MQ_THREADS 512
-#define MQ_WAVES 8
-#define MQ_TPW_MAX 32   // tiles per workgroup (LDS partials: 512 B each)
+#define MQ_WAVES_MAX 16
+#define MQ_TPW_MAX 32   // tiles per workgroup (LDS partials: 64 B per wave each)
 #define MQ_NB_MAX 64    // super-blocks per row (k ≤ 16384): LDS digits 2 KiB each
 
 typedef int mq_v4i __attribute__((ext_vector_type(4)));
@@ -214,11 +214,11 @@ __device__ __forceinline__ unsigned long long mq_amax_key(float v, int64_t row) 
 //  accumulate: y += result (residual adds, runner.rs:1609-1611, 1629-1631).
 // RING = false: the workgroup's tiles all fit the RD load slots (issued up
 // front); RING = true: the slots are refilled as they are consumed.
-template <int NBW, int RD, int XO, bool RING>
-__global__ void __launch_bounds__(MQ_THREADS) k_gemv_q4k(MqParams G) {
+template <int NBW, int RD, int XO, bool RING, int W>
+__global__ void __launch_bounds__(64 * W) k_gemv_q4k(MqParams G) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    __shared__ float ssum[MQ_WAVES];
-    __shared__ unsigned long long kmax[MQ_WAVES];
+    __shared__ float ssum[W];
+    __shared__ unsigned long long kmax[W];
     const int nb = G.nb;
     char* V = smem;
     int2* meta = (int2*)(smem + (size_t)nb * 2048);
@@ -228,7 +228,7 @@ __global__ void __launch_bounds__(MQ_THREADS) k_gemv_q4k(MqParams G) {
     float* yr = G.y + (int64_t)blockIdx.y * G.y_stride;
     const int64_t t0 = (int64_t)blockIdx.x * G.tpw;
     const int ntw = (int)min((int64_t)G.tpw, (int64_t)G.ntiles - t0);
-    const int bA = nb * wave / MQ_WAVES, nbw = nb * (wave + 1) / MQ_WAVES - bA;
+    const int bA = nb * wave / W, nbw = nb * (wave + 1) / W - bA;
     const int o0 = 32 * bA, o1 = 32 * (bA + nbw);  // this wave's activation octets
 
     float xv[XO][8], wv[XO][8];
@@ -251,7 +251,7 @@ __global__ void __launch_bounds__(MQ_THREADS) k_gemv_q4k(MqParams G) {
         __syncthreads();
         float tot = 0.0f;
 #pragma unroll
-        for (int w = 0; w < MQ_WAVES; w++) tot += ssum[w];
+        for (int w = 0; w < W; w++) tot += ssum[w];
         const float rms = sqrtf(tot / (float)G.k + G.eps);
 #pragma unroll
         for (int i = 0; i < XO; i++)
@@ -269,7 +269,7 @@ __global__ void __launch_bounds__(MQ_THREADS) k_gemv_q4k(MqParams G) {
                 float acc = mq_tile<NBW>(q[r], h[r], V, meta, bA, nbw, lane);
                 acc += __shfl_xor(acc, 16, 64);
                 acc += __shfl_xor(acc, 32, 64);
-                if (lane < 16) part[(r * MQ_WAVES + wave) * 16 + lane] = acc + poison;
+                if (lane < 16) part[(r * W + wave) * 16 + lane] = acc + poison;
             }
             __builtin_amdgcn_sched_barrier(0);  // tiles in arrival order: wait for each one alone
         }
@@ -282,7 +282,7 @@ __global__ void __launch_bounds__(MQ_THREADS) k_gemv_q4k(MqParams G) {
                     float acc = mq_tile<NBW>(q[r], h[r], V, meta, bA, nbw, lane);
                     acc += __shfl_xor(acc, 16, 64);
                     acc += __shfl_xor(acc, 32, 64);
-                    if (lane < 16) part[(j * MQ_WAVES + wave) * 16 + lane] = acc + poison;
+                    if (lane < 16) part[(j * W + wave) * 16 + lane] = acc + poison;
                 }
                 mq_load<NBW>(q[r], h[r], G, t0 + min(j + RD, ntw - 1), bA, nbw, lane);
                 __builtin_amdgcn_sched_barrier(0);
@@ -292,18 +292,18 @@ __global__ void __launch_bounds__(MQ_THREADS) k_gemv_q4k(MqParams G) {
     __syncthreads();
 
     unsigned long long best = 0;
-    for (int idx = threadIdx.x; idx < ntw * 16; idx += MQ_THREADS) {
+    for (int idx = threadIdx.x; idx < ntw * 16; idx += 64 * W) {
         const int jt = idx >> 4, nn = idx & 15;
         const int64_t row = (t0 + jt) * 16 + nn;
         if (row >= G.n) continue;
         float sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < MQ_WAVES; w++) sum += part[(jt * MQ_WAVES + w) * 16 + nn];
+        for (int w = 0; w < W; w++) sum += part[(jt * W + w) * 16 + nn];
         if (G.swiglu) {
             if ((nn & 1) == 0) {
                 float up = 0.0f;
 #pragma unroll
-                for (int w = 0; w < MQ_WAVES; w++) up += part[(jt * MQ_WAVES + w) * 16 + nn + 1];
+                for (int w = 0; w < W; w++) up += part[(jt * W + w) * 16 + nn + 1];
                 yr[row >> 1] = sum * (1.0f / (1.0f + expf(-sum))) * up;
             }
         } else {
@@ -326,28 +326,29 @@ __global__ void __launch_bounds__(MQ_THREADS) k_gemv_q4k(MqParams G) {
         if (threadIdx.x == 0) {
             unsigned long long m = kmax[0];
 #pragma unroll
-            for (int w = 1; w < MQ_WAVES; w++) m = kmax[w] > m ? kmax[w] : m;
+            for (int w = 1; w < W; w++) m = kmax[w] > m ? kmax[w] : m;
             atomicMax(G.amax, m);
         }
     }
 }
 
-template <int NBW, int RD, int XO, bool RING>
+template <int NBW, int RD, int XO, bool RING, int W>
 static int mq_launch_k(dim3 grid, size_t lds, hipStream_t s, const MqParams& G) {
     static size_t opted = 64 * 1024;  // dynamic LDS above 64 KiB is opted into per kernel
     if (lds > opted) {
-        AETH_HIP_CHECK(hipFuncSetAttribute((const void*)k_gemv_q4k<NBW, RD, XO, RING>,
+        AETH_HIP_CHECK(hipFuncSetAttribute((const void*)k_gemv_q4k<NBW, RD, XO, RING, W>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         opted = lds;
     }
-    hipLaunchKernelGGL((k_gemv_q4k<NBW, RD, XO, RING>), grid, dim3(MQ_THREADS), lds, s, G);
+    hipLaunchKernelGGL((k_gemv_q4k<NBW, RD, XO, RING, W>), grid, dim3(64 * W), lds, s, G);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
 
-template <int NBW, int RD, int XO>
+template <int NBW, int RD, int XO, int W>
 static int mq_launch(dim3 grid, size_t lds, hipStream_t s, const MqParams& G) {
-    return G.tpw <= RD ? mq_launch_k<NBW, RD, XO, false>(grid, lds, s, G) : mq_launch_k<NBW, RD, XO, true>(grid, lds, s, G);
+    return G.tpw <= RD ? mq_launch_k<NBW, RD, XO, false, W>(grid, lds, s, G)
+                       : mq_launch_k<NBW, RD, XO, true, W>(grid, lds, s, G);
 }
 
 int aeth_gemv_q4k_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, const GemvEpi& e,
@@ -369,14 +370,23 @@ int aeth_gemv_q4k_launch(const aeth_weight* w, const float* d_x, int64_t m, floa
     G.n = w->n;
     G.nb = nb;
     G.ntiles = (int)aeth_cdiv(w->n, 16);
-    // RD tiles per workgroup, all loads issued up front (about two workgroups
-    // resident per CU): short memory queues, so each wave's tiles arrive early
-    // and their compute overlaps the stream (measured best at 6144..28672
-    // rows). Taller matrices use the ring with ~2 workgroups per CU so that the
-    // per-workgroup activation conversion stays amortised.
-    const int rd = (nb + MQ_WAVES - 1) / MQ_WAVES <= 4 ? 2 : 1;
+    // Shape choice: W waves split K; RD tiles per workgroup with all loads issued
+    // up front (short memory queues, so each wave's tiles arrive early and
+    // their compute overlaps the stream). Taller matrices use the ring with ~2
+    // workgroups per CU so the per-workgroup activation conversion stays
+    // amortised.
     const int64_t cus = aeth_num_cus();
-    int64_t tpw = G.ntiles <= 8 * cus ? rd : aeth_cdiv(G.ntiles, 2 * cus);
+    // tuning overrides, read once: AETH_GEMV_WAVES (8 | 16), AETH_GEMV_TPW (tiles per workgroup)
+    static const int env_w = getenv("AETH_GEMV_WAVES") ? atoi(getenv("AETH_GEMV_WAVES")) : 0;
+    static const int env_tpw = getenv("AETH_GEMV_TPW") ? atoi(getenv("AETH_GEMV_TPW")) : 0;
+    // (measured: 16 waves pay off only for long rows, k ≥ 8192; one tile per
+    // workgroup when there are no more tiles than CUs)
+    int W = nb >= 32 ? 16 : 8;
+    if (env_w) W = env_w == 16 ? 16 : 8;
+    const int nbw = (nb + W - 1) / W;
+    const int rd = W == 16 ? (nbw <= 2 ? 2 : 1) : (nbw <= 4 ? 2 : 1);
+    int64_t tpw = G.ntiles <= cus ? 1 : G.ntiles <= 8 * cus ? rd : aeth_cdiv(G.ntiles, 2 * cus);
+    if (env_tpw > 0) tpw = env_tpw;
     if (tpw > MQ_TPW_MAX) tpw = MQ_TPW_MAX;
     G.tpw = (int)tpw;
     G.x = d_x;
@@ -390,10 +400,14 @@ int aeth_gemv_q4k_launch(const aeth_weight* w, const float* d_x, int64_t m, floa
     G.swiglu = e.swiglu;
     G.amax = e.amax;
     const dim3 grid((unsigned)aeth_cdiv(G.ntiles, tpw), (unsigned)m);
-    const size_t lds = (size_t)nb * 2048 + (size_t)nb * 64 + (size_t)tpw * MQ_WAVES * 16 * 4;
-    const int nbw = (nb + MQ_WAVES - 1) / MQ_WAVES;
-    if (nbw <= 1) return mq_launch<1, 2, 1>(grid, lds, s, G);
-    if (nbw <= 2) return mq_launch<2, 2, 1>(grid, lds, s, G);
-    if (nbw <= 4) return mq_launch<4, 2, 2>(grid, lds, s, G);
-    return mq_launch<8, 1, 4>(grid, lds, s, G);
+    const size_t lds = (size_t)nb * 2048 + (size_t)nb * 64 + (size_t)tpw * W * 16 * 4;
+    if (W == 16) {
+        if (nbw <= 1) return mq_launch<1, 2, 1, 16>(grid, lds, s, G);
+        if (nbw <= 2) return mq_launch<2, 2, 1, 16>(grid, lds, s, G);
+        return mq_launch<4, 1, 2, 16>(grid, lds, s, G);
+    }
+    if (nbw <= 1) return mq_launch<1, 2, 1, 8>(grid, lds, s, G);
+    if (nbw <= 2) return mq_launch<2, 2, 1, 8>(grid, lds, s, G);
+    if (nbw <= 4) return mq_launch<4, 2, 2, 8>(grid, lds, s, G);
+    return mq_launch<8, 1, 4, 8>(grid, lds, s, G);
 }
