@@ -13,7 +13,6 @@ SOURCES = [
     "aeth_weights.hip",
     "aeth_dequant.hip",
     "aeth_gemv.hip",
-    "aeth_gemv_q4k.hip",
     "aeth_gemm.hip",
     "aeth_decode_ops.hip",
     "aeth_host.cpp",

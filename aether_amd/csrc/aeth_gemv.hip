@@ -1,379 +1,395 @@
-// Decode GEMV for Q8_0 / Q6_K weights on gfx950:  y[r] = Σ_k x[k]·W[r][k]
-// (Q4_K runs on the matrix cores, aeth_gemv_q4k.hip).
+// Decode GEMV for Q4_K / Q6_K / Q8_0 weights on the int8 matrix cores of gfx950:
+//   y[r] = Σ_k x[k]·W[r][k]  (avx2::matmul_q4_k / matmul_q6_k, src/quant/avx2.rs:23-94;
+//   scalar matmul_q8_0, src/quant/matmul/q8_0.rs:5-89), one activation row per grid.y.
 //
-// Design (MI355X-first):
-//  * Weights are read from the planar device layout (aeth_weights.hip) in
-//    "units" of 32 (Q8_0) or 48 (Q6_K) quant bytes per lane, as
-//    16-byte loads; consecutive lanes take consecutive units of a row, so each
-//    wave load instruction covers a contiguous span of the row.
-//  * The activation row becomes an exact integer form once per workgroup:
-//    per 32 elements, x ≈ x_int·2^-S with |x_int| ≤ 2^22 (22 bits + sign
-//    relative to the group maximum; f32 itself keeps 24), split into three
-//    balanced signed byte digits x_int = d0 + 256·d1 + 65536·d2. A quad of
-//    6-bit / 8-bit quants is dotted with v_dot4_i32_i8 per digit:
-//    integer-exact sub-block dots for ~1 VALU op per weight instead of
-//    unpack + convert + FMA. Scales are applied in f32 per sub-block.
-//  * The digits are laid out in LDS per lane unit ("records", strides chosen
-//    so that 8 consecutive lanes hit distinct 16-byte bank groups) and, when a
-//    lane owns one or two units per row, held in registers for all its rows.
-//  * One persistent workgroup of 8 waves per CU; each wave owns a contiguous
-//    run of rows, processed R at a time. The first pass's weight loads are
-//    issued before the activation conversion, and each pass prefetches the
-//    next, so HBM streams while the VALU works.
+// Exact integer core. Each wave turns its slice of the activation row into an
+// exact integer form: per group of 32 (Q4_K, Q8_0) or 16 (Q6_K) elements,
+// x ≈ x_int·2^-S with |x_int| ≤ 2^22 (22 bits + sign against the group
+// maximum), split into three balanced signed byte digits
+// x_int = d0 + 256·d1 + 65536·d2. The digits are the A operand of
+// v_mfma_i32_16x16x64_i8 — M = 4 output slots × 4 digit rows (the fourth row
+// zero) — and 16 weight rows are the B operand (N). Lane (n, kg) (n = lane % 16,
+// kg = lane / 16) supplies 16 k-slots of row n; A lane (m, kg) holds the
+// digits that pair with them, nonzero only where slot m/4 owns those k-slots.
+// One MFMA so returns the exact integer dot of every digit with 64 quants of 16
+// rows, already split by scale group; the output lane (n, g) holds slot g's
+// three digit sums for row n and applies that group's scales in f32.
+//
+// Per format ("chunk" = the unit of K a wave steps through):
+//  Q4_K, chunk = super-block (256). Per half h, lane (n, kg) loads
+//    qs[64h + 16kg, +16) of row n: low nibbles are sub-block 4h + 2(kg ≥ 2),
+//    high nibbles the next one. Two MFMAs (low / high nibbles) share one A;
+//    slot g ↔ sub-block 4h + g, the even slots exact in the first result, the
+//    odd ones in the second. |Σ q·x_int| ≤ 32·15·2^22 < 2^31: digits recombine
+//    in i32;  acc += 2^-S·Σq·x_int·d·sc − dmin·m·Σx.
+//  Q8_0, chunk = 4 blocks (128). MFMA j, lane (n, kg): the 16 raw quant bytes
+//    [16(kg & 1), +16) of block 2j + (kg ≥ 2) — no unpacking; slot g ↔ block g.
+//    acc += 2^-S·(Σ q·x_int)·d (the top digit joins in f32).
+//  Q6_K, chunk = super-block. Lane (n, kg) loads the 48 bytes of its 2×16
+//    elements of half h = kg / 2, g' = kg % 2: ql[64h + 16g', +16),
+//    ql[64h + 32 + 16g', +16), qh[32h + 16g', +16), and MFMA v (0..3) takes
+//    sub-block (h, v, g') = elements 128h + 32v + 16g' + [0, 16) as the 6-bit
+//    q + 32 ∈ [0, 63]; slot g ↔ lane group kg = g. The offset is removed
+//    exactly per digit (−32·Σ digit) before   acc += 2^-S·Σ(q)·x_int·sc·d.
+//
+// A operands are kept compact in LDS: only the three digit rows, 16-byte
+// vectors indexed (region, kg, slot, digit), 3 bytes per activation element.
+// A lane whose (m, kg) holds no digits for an MFMA reads a 16-byte zero slot
+// instead (one address select per operand read).
+//
+// Work split: a workgroup (W = 8 or 16 waves) owns a run of 16-row tiles; wave
+// w takes chunks [nc·w/W, nc·(w+1)/W) of every tile, converts only that slice
+// of x (no barrier: LDS operations of one wave execute in order), keeps RD
+// tiles of loads in flight, and leaves 16 partial row sums per tile in LDS;
+// after the one barrier the partials are summed in a fixed order
+// (deterministic) and the epilogue (accumulate, SwiGLU, argmax) runs.
+//
+// Every global load is issued unconditionally (out-of-range indices clamped to
+// valid addresses, values discarded): the compiler can then count outstanding
+// loads exactly and wait for each one alone, instead of draining the whole
+// weight stream at the first use of x.
 #include <math.h>
 #include <stdlib.h>
 
 #include "aeth_common.hpp"
 #include "aeth_internal.hpp"
 
-#define GEMV_THREADS 512
-#define GEMV_WAVES (GEMV_THREADS / 64)
+#define MQ_TPW_MAX 32  // tiles per workgroup (LDS partials: 64 B per wave each)
+#define MQ_LDS_MAX (160 * 1024)
 
-enum { FMT_Q80 = 0, FMT_Q6K = 2 };
+typedef int mq_v4i __attribute__((ext_vector_type(4)));
 
-// Per-format geometry. UE: activation elements per unit; RECB: bytes of one
-// LDS digit record; NQ: int4 weight loads per unit.
-template <int F> struct Fmt;
-template <> struct Fmt<FMT_Q6K> { static constexpr int UE = 64, RECB = 272; };
-template <> struct Fmt<FMT_Q80> { static constexpr int UE = 32, RECB = 112; };
+enum { FQ4K = 0, FQ6K = 1, FQ80 = 2 };
 
-__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
-
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
-}
-
-// ── activation → digit records (LDS) ─────────────────────────────────────
-// Thread t owns octets o = t + 512·i (i < XO): elements [8o, 8o+8). They are
-// loaded first (before any weight traffic is queued), converted after the
-// weight loads are in flight. Four consecutive lanes form a 32-element group
-// with one exponent S.
-// Record contents by format (unit = the weights one lane handles per row):
-//  Q6_K unit u = 4b+2h+g: 16 elements h*128+16g+32v+t (t<16) for v = 0..3;
-//       slot v digits at v*48 + k*16, meta at 192+16v: {S, 32Σd0, 32Σd1, 32Σd2}.
-//  Q8_0 unit u = block u: digits at k*32, meta at 96: {S}.
-template <int XO>
-__device__ __forceinline__ void load_x(const float* __restrict__ x, int k, int noct, float (&xv)[XO][8]) {
-    const bool vec = (k & 7) == 0;
-#pragma unroll
-    for (int i = 0; i < XO; i++) {
-        const int o = threadIdx.x + GEMV_THREADS * i;
-        const int e0 = o * 8;
-        if (vec && o < noct && e0 + 8 <= k) {
-            float4 a = *(const float4*)(x + e0), b = *(const float4*)(x + e0 + 4);
-            xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
-            xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
-        } else {
-#pragma unroll
-            for (int t = 0; t < 8; t++) xv[i][t] = (o < noct && e0 + t < k) ? x[e0 + t] : 0.0f;
-        }
-    }
-}
-
-template <int F, int XO>
-__device__ int build_records(const float (&xv)[XO][8], int noct, char* rec, int* flag) {
-    const int tid = threadIdx.x;
-    if (tid == 0) *flag = 0;
-    __syncthreads();
-    int bad = 0;
-#pragma unroll
-    for (int i = 0; i < XO; i++) {
-        const int o = tid + GEMV_THREADS * i;
-        const bool live = o < noct;
-        const int e0 = o * 8;
-        const float* v = xv[i];
-        float mx = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 8; t++) mx = fmaxf(mx, fabsf(v[t]));
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-        const bool fin = isfinite(mx);
-        if (!fin) bad = 1;
-        int E = 0;
-        if (mx > 0.0f && fin) (void)frexpf(mx, &E);
-        const int S = (mx > 0.0f && fin) ? 22 - E : 0;
-        int d0[8], d1[8], d2[8];
-        int s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            int xi = (mx > 0.0f && fin) ? (int)rintf(ldexpf(v[t], S)) : 0;
-            int a = (xi << 24) >> 24;
-            int r = (xi - a) >> 8;
-            int b = (r << 24) >> 24;
-            int c = (r - b) >> 8;
-            d0[t] = a; d1[t] = b; d2[t] = c;
-            s0 += a; s1 += b; s2 += c;
-        }
-        const int qq = o & 3;  // octet within its 32-group
-        char* dst;
-        int koff;  // byte stride between the three digits
-        if (F == FMT_Q6K) {
-            const int b = e0 >> 8, eb = e0 & 255, h = eb >> 7, rr = eb & 127, vv = rr >> 5, w32 = rr & 31;
-            const int g = w32 >> 4, half8 = (w32 >> 3) & 1;
-            char* r = rec + (size_t)(b * 4 + h * 2 + g) * Fmt<F>::RECB;
-            dst = r + vv * 48 + half8 * 8;
-            koff = 16;
-            s0 += __shfl_xor(s0, 1, 64);
-            s1 += __shfl_xor(s1, 1, 64);
-            s2 += __shfl_xor(s2, 1, 64);
-            if (live && half8 == 0) {
-                int4 m;
-                m.x = S; m.y = s0 << 5; m.z = s1 << 5; m.w = s2 << 5;
-                *(int4*)(r + 192 + 16 * vv) = m;
-            }
-        } else {
-            char* r = rec + (size_t)(e0 >> 5) * Fmt<F>::RECB;
-            dst = r + qq * 8;
-            koff = 32;
-            if (live && qq == 0) *(int*)(r + 96) = S;
-        }
-        if (live) {
-            *(uint2*)(dst) = make_uint2(pack4(d0[0], d0[1], d0[2], d0[3]), pack4(d0[4], d0[5], d0[6], d0[7]));
-            *(uint2*)(dst + koff) = make_uint2(pack4(d1[0], d1[1], d1[2], d1[3]), pack4(d1[4], d1[5], d1[6], d1[7]));
-            *(uint2*)(dst + 2 * koff) =
-                make_uint2(pack4(d2[0], d2[1], d2[2], d2[3]), pack4(d2[4], d2[5], d2[6], d2[7]));
-        }
-    }
-    if (bad) *flag = 1;
-    __syncthreads();
-    return *flag;
-}
-
-// ── per-format unit data, loads and dot products ─────────────────────────
-
-struct UQ6K { int4 a, b, h; uint2 sc; uint32_t d; };
-struct UQ80 { int4 q0, q1; uint32_t d; };
-
-template <int F> struct UnitT;
-template <> struct UnitT<FMT_Q6K> { typedef UQ6K T; };
-template <> struct UnitT<FMT_Q80> { typedef UQ80 T; };
-
-struct Planes {
+struct MqParams {
     const uint8_t* p0;
     const uint8_t* p1;
     const uint8_t* p2;
-    const uint8_t* p3;
-};
-
-__device__ __forceinline__ void load_unit(UQ6K& d, const Planes& P, int64_t row, int nb, int u) {
-    const int b = u >> 2, h = (u >> 1) & 1;
-    const int64_t blk = row * nb + b;
-    const uint8_t* ql = P.p0 + (row * nb) * 128 + (int64_t)u * 16;
-    d.a = *(const int4*)ql;
-    d.b = *(const int4*)(ql + nb * 64);
-    d.h = *(const int4*)(P.p1 + (row * nb) * 64 + (int64_t)u * 16);
-    d.sc = *(const uint2*)(P.p2 + blk * 16 + h * 8);
-    d.d = ((const uint16_t*)P.p3)[blk];
-}
-
-__device__ __forceinline__ void load_unit(UQ80& d, const Planes& P, int64_t row, int nb, int u) {
-    const uint8_t* q = P.p0 + (row * nb) * 32 + (int64_t)u * 16;
-    d.q0 = *(const int4*)q;
-    d.q1 = *(const int4*)(q + nb * 16);
-    d.d = ((const uint16_t*)P.p1)[row * nb + u];
-}
-
-// Digit record held in registers (or read from LDS per use).
-template <int F> struct Rec { uint4 v[Fmt<F>::RECB / 16]; };
-
-template <int F>
-__device__ __forceinline__ void read_rec(Rec<F>& r, const char* p) {
-#pragma unroll
-    for (int i = 0; i < Fmt<F>::RECB / 16; i++) r.v[i] = *(const uint4*)(p + 16 * i);
-}
-
-__device__ __forceinline__ int dot8(const int* q, const uint4* D0) {
-    const int* d = (const int*)D0;
-    int a = 0;
-#pragma unroll
-    for (int m = 0; m < 8; m++) a = sdot4(q[m], d[m], a);
-    return a;
-}
-
-__device__ __forceinline__ int dot4v(const int* q, const uint4& D) {
-    return sdot4(q[3], (int)D.w, sdot4(q[2], (int)D.z, sdot4(q[1], (int)D.y, sdot4(q[0], (int)D.x, 0))));
-}
-
-// Q6_K unit u = 4b + 2h + g.
-__device__ __forceinline__ float unit_dot(const UQ6K& d, const Rec<FMT_Q6K>& R) {
-    const int* A = (const int*)&d.a;
-    const int* B = (const int*)&d.b;
-    const int* H = (const int*)&d.h;
-    float part = 0.0f;
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-        int q[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            if (v == 0) q[e] = (A[e] & 0x0F0F0F0F) | ((H[e] << 4) & 0x30303030);
-            else if (v == 1) q[e] = (B[e] & 0x0F0F0F0F) | ((H[e] << 2) & 0x30303030);
-            else if (v == 2) q[e] = ((A[e] >> 4) & 0x0F0F0F0F) | (H[e] & 0x30303030);
-            else q[e] = ((B[e] >> 4) & 0x0F0F0F0F) | ((H[e] >> 2) & 0x30303030);
-        }
-        const uint4 meta = R.v[12 + v];
-        // quants are stored as q+32 in [0,63]: subtract 32·Σdigit per digit (exact)
-        int a0 = dot4v(q, R.v[3 * v]) - (int)meta.y;
-        int a1 = dot4v(q, R.v[3 * v + 1]) - (int)meta.z;
-        int a2 = dot4v(q, R.v[3 * v + 2]) - (int)meta.w;
-        float val = ldexpf((float)a2 * 65536.0f + (float)(a0 + (a1 << 8)), -(int)meta.x);
-        uint32_t sw = v < 2 ? d.sc.x : d.sc.y;  // sc[h*8 + g + 2v], pre-shifted by fix_unit
-        float sc = (float)(int8_t)((sw >> (16 * (v & 1))) & 0xFFu);
-        part += sc * val;
-    }
-    return aeth_decode_d(d.d) * part;
-}
-
-// Q8_0 unit = one block.
-__device__ __forceinline__ float unit_dot(const UQ80& d, const Rec<FMT_Q80>& R) {
-    int q[8];
-#pragma unroll
-    for (int m = 0; m < 4; m++) { q[m] = ((const int*)&d.q0)[m]; q[m + 4] = ((const int*)&d.q1)[m]; }
-    int a0 = dot8(q, &R.v[0]), a1 = dot8(q, &R.v[2]), a2 = dot8(q, &R.v[4]);
-    float val = ldexpf((float)a2 * 65536.0f + (float)(a0 + (a1 << 8)), -(int)R.v[6].x);
-    return aeth_f16_to_f32(d.d) * val;
-}
-
-// Q6_K scale bytes: the lane's g selects odd/even bytes of sc[h*8 .. h*8+8);
-// shifting once per load leaves byte g+2v at bit 16(v&1) of word v/2.
-__device__ __forceinline__ void fix_unit(UQ6K& d, int g) {  // g = u & 1
-    d.sc.x >>= 8 * g;
-    d.sc.y >>= 8 * g;
-}
-__device__ __forceinline__ void fix_unit(UQ80&, int) {}
-
-// ── reductions: R row sums spread over the wave → one value per row ──────
-// Reduce-scatter butterfly: each of the first log2(R) exchange steps halves
-// the number of live row sums per lane (lanes on the two sides of the step's
-// bit keep different halves), the remaining steps finish the sum. Afterwards
-// lane L holds the total of row_of_lane<R>(L), written by the lanes where
-// (L & (64/R - 1)) == 0. Six exchange steps move R-1 + 6-log2(R) values
-// per lane instead of 6·R.
-template <int R>
-__device__ __forceinline__ float wave_reduce_rows(const float (&a)[R], int lane) {
-    float v[R];
-#pragma unroll
-    for (int i = 0; i < R; i++) v[i] = a[i];
-    int bit = 32;
-#pragma unroll
-    for (int n = R; n > 1; n >>= 1) {
-        const bool hi = lane & bit;
-#pragma unroll
-        for (int i = 0; i < n / 2; i++) {
-            float keep = hi ? v[n / 2 + i] : v[i];
-            float send = hi ? v[i] : v[n / 2 + i];
-            v[i] = keep + __shfl_xor(send, bit, 64);
-        }
-        bit >>= 1;
-    }
-#pragma unroll
-    for (int off = 64 / R / 2; off >= 1; off >>= 1) v[0] += __shfl_xor(v[0], off, 64);
-    return v[0];
-}
-
-template <int R>
-__device__ __forceinline__ int row_of_lane(int lane) {
-    int row = 0, bit = 32, w = R / 2;
-#pragma unroll
-    for (int n = R; n > 1; n >>= 1) {
-        if (lane & bit) row += w;
-        w >>= 1;
-        bit >>= 1;
-    }
-    return row;
-}
-
-// ── the kernel ───────────────────────────────────────────────────────────
-// WPR waves share a row (wave w of a row handles units [64w, 64w+64)), so
-// each lane owns exactly one unit and keeps its digit record in registers;
-// the 8 waves form 8/WPR row streams. R rows per pass; XO activation octets
-// per thread.
-//
-// Optional fusions (GemvParams):
-//  norm_w   : x ← x / sqrt(Σx²/k + eps) · norm_w before the product
-//             (rmsnorm_inplace, runner.rs:1739-1746);
-//  swiglu   : rows come in (gate_i, up_i) pairs at 2i, 2i+1 and the output is
-//             y[i] = g·σ(g)·u (runner.rs:1617-1625) — WPR == 1 only;
-//  amax     : greedy argmax of y folded into a 64-bit atomic max of
-//             (orderable(value) << 32 | row): last maximal row wins on ties,
-//             as Iterator::max_by (runner.rs:1964-1973);
-//  accumulate: y += result (residual adds, runner.rs:1609-1611, 1629-1631).
-struct GemvParams {
-    Planes P;
     int64_t n;
-    int nb, upr;
+    int nc, ntiles, tpw;  // chunks per row, 16-row tiles, tiles per workgroup
     const float* x;
-    int k;
     int64_t x_stride;
+    int k, kx;            // k; activation elements the product reads (kx ≤ k)
     float* y;
     int64_t y_stride;
     int accumulate;
-    int64_t rows_per_wg;
-    int npass;
     const float* norm_w;
     float eps;
     int swiglu;
     unsigned long long* amax;
 };
 
-__device__ __forceinline__ unsigned long long amax_key(float v, int64_t row) {
-    uint32_t f = __float_as_uint(v);
-    uint32_t o = (f & 0x80000000u) ? ~f : (f | 0x80000000u);
+__device__ __forceinline__ uint32_t mq_pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
+}
+
+__device__ __forceinline__ mq_v4i mq_mfma(const mq_v4i& a, const mq_v4i& b, const mq_v4i& c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// ── per-format traits ────────────────────────────────────────────────────
+// CE: activation elements per chunk; AB: LDS bytes of A operands per chunk;
+// MB: LDS meta bytes per chunk; GE: elements per exponent group.
+template <int F> struct MF;
+
+// Lane constants for reading A: (m, kg) of this lane.
+struct MqLane {
+    int m, kg, s, d;
+};
+
+template <> struct MF<FQ4K> {
+    static constexpr int CE = 256, AB = 768, MB = 64, GE = 32;
+    struct D { int4 q[2]; uint4 h; };
+    // planes: p0 = headers [tile][sb][16 rows][16 B], p1 = quants [tile][sb][h][64][16 B]
+    __device__ static void load(D& d, const MqParams& G, int64_t c, int lane) {  // c = tile·nc + chunk
+        d.q[0] = *(const int4*)(G.p1 + (c * 2) * 1024 + lane * 16);
+        d.q[1] = *(const int4*)(G.p1 + (c * 2 + 1) * 1024 + lane * 16);
+        d.h = *(const uint4*)(G.p0 + (c * 16 + (lane & 15)) * 16);
+    }
+    // compact A: per half h, vector ((kg·2 + (s & 1))·3 + d), kg ∈ the pair of slot s.
+    // byte offset of an octet's digit-0 piece (digit d: +16·d)
+    __device__ static int aoff(int ec) {
+        const int h = ec >> 7, s = (ec >> 5) & 3, p = ec & 31, kg = 2 * (s >> 1) + (p >> 4);
+        return h * 384 + ((kg * 2 + (s & 1)) * 3) * 16 + (p & 8);
+    }
+    __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
+                                const char* zs) {
+        const int g = lane >> 4;
+        const bool va = (L.s >> 1) == (L.kg >> 1) && L.d < 3;
+        const int vo = ((L.kg * 2 + (L.s & 1)) * 3 + L.d) * 16;
+        const bool odd = g & 1;
+        const mq_v4i zero = {0, 0, 0, 0};
+        const float d = aeth_decode_d(dd.h.x), dmin = aeth_decode_d(dd.h.x >> 16);
+        // get_scale_min_k4 (common.rs:29-38) for sub-blocks g and 4 + g
+        const uint32_t yb = (dd.h.y >> (8 * g)) & 0xFFu, zb = (dd.h.z >> (8 * g)) & 0xFFu;
+        const uint32_t wb = (dd.h.w >> (8 * g)) & 0xFFu;
+        const float sc[2] = {(float)(yb & 63u), (float)((wb & 15u) | ((yb >> 6) << 4))};
+        const float mn[2] = {(float)(zb & 63u), (float)((wb >> 4) | ((zb >> 6) << 4))};
+        float acc = 0.0f;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int4 Q = dd.q[hh];
+            mq_v4i lo, hi;
+            lo.x = Q.x & 0x0F0F0F0F; lo.y = Q.y & 0x0F0F0F0F; lo.z = Q.z & 0x0F0F0F0F; lo.w = Q.w & 0x0F0F0F0F;
+            hi.x = (Q.x >> 4) & 0x0F0F0F0F; hi.y = (Q.y >> 4) & 0x0F0F0F0F;
+            hi.z = (Q.z >> 4) & 0x0F0F0F0F; hi.w = (Q.w >> 4) & 0x0F0F0F0F;
+            const mq_v4i a = *(const mq_v4i*)(va ? A + hh * 384 + vo : zs);
+            const mq_v4i D1 = mq_mfma(a, lo, zero), D2 = mq_mfma(a, hi, zero);
+            const int e0 = odd ? D2.x : D1.x, e1 = odd ? D2.y : D1.y, e2 = odd ? D2.z : D1.z;
+            const int v = e0 + e1 * 256 + e2 * 65536;
+            const int2 mt = ((const int2*)meta)[4 * hh + g];
+            acc = fmaf(ldexpf((float)v, mt.x), d * sc[hh], acc);
+            acc = fmaf(-dmin * mn[hh], __int_as_float(mt.y), acc);
+        }
+        return acc;
+    }
+};
+
+template <> struct MF<FQ80> {
+    static constexpr int CE = 128, AB = 384, MB = 32, GE = 32;
+    struct D { int4 q[2]; uint32_t d; };
+    // planes: p0 = quants [tile][group][j][64][16 B], p1 = d [tile][group][4 blocks][16 rows] (f16)
+    __device__ static void load(D& d, const MqParams& G, int64_t c, int lane) {
+        d.q[0] = *(const int4*)(G.p0 + (c * 2) * 1024 + lane * 16);
+        d.q[1] = *(const int4*)(G.p0 + (c * 2 + 1) * 1024 + lane * 16);
+        d.d = ((const uint16_t*)G.p1)[c * 64 + lane];
+    }
+    // compact A: per MFMA j, vector (kg·3 + d) (slot s = 2j + (kg ≥ 2))
+    __device__ static int aoff(int ec) {
+        const int s = ec >> 5, p = ec & 31, kg = 2 * (s & 1) + (p >> 4);
+        return (s >> 1) * 192 + (kg * 3) * 16 + (p & 8);
+    }
+    __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
+                                const char* zs) {
+        const int g = lane >> 4;
+        const mq_v4i zero = {0, 0, 0, 0};
+        const int vo = (L.kg * 3 + L.d) * 16;
+        const bool v0 = L.s == (L.kg >> 1) && L.d < 3, v1 = L.s == 2 + (L.kg >> 1) && L.d < 3;
+        const mq_v4i a0 = *(const mq_v4i*)(v0 ? A + vo : zs), a1 = *(const mq_v4i*)(v1 ? A + 192 + vo : zs);
+        const mq_v4i b0 = {dd.q[0].x, dd.q[0].y, dd.q[0].z, dd.q[0].w};
+        const mq_v4i b1 = {dd.q[1].x, dd.q[1].y, dd.q[1].z, dd.q[1].w};
+        const mq_v4i D = mq_mfma(a1, b1, mq_mfma(a0, b0, zero));
+        // |Σ q·d_k| ≤ 32·127·128: d0 + 256·d1 exact in i32, the top digit joins in f32
+        const float val = (float)(D.x + D.y * 256) + 65536.0f * (float)D.z;
+        const int2 mt = ((const int2*)meta)[g];
+        return ldexpf(val, mt.x) * aeth_f16_to_f32(dd.d);  // Q8_0 scales are plain f16 (q8_0.rs)
+    }
+};
+
+template <> struct MF<FQ6K> {
+    static constexpr int CE = 256, AB = 768, MB = 256, GE = 16;
+    struct D { int4 a, b, h; uint2 sc; uint32_t d; };
+    // planes: p0 = [tile][sb][part A|B|H][64][16 B], p1 = sc [tile][sb][16 rows][16 B],
+    //         p2 = d [tile][sb][16 rows] (f16)
+    __device__ static void load(D& d, const MqParams& G, int64_t c, int lane) {
+        d.a = *(const int4*)(G.p0 + (c * 3) * 1024 + lane * 16);
+        d.b = *(const int4*)(G.p0 + (c * 3 + 1) * 1024 + lane * 16);
+        d.h = *(const int4*)(G.p0 + (c * 3 + 2) * 1024 + lane * 16);
+        d.sc = *(const uint2*)(G.p1 + (c * 16 + (lane & 15)) * 16 + ((lane >> 5) & 1) * 8);
+        d.d = ((const uint16_t*)G.p2)[c * 16 + (lane & 15)];
+    }
+    // compact A: per MFMA v, vector (kg·3 + d) (slot = kg)
+    __device__ static int aoff(int ec) {
+        const int h = ec >> 7, r = ec & 127, v = r >> 5, kg = 2 * h + ((r >> 4) & 1);
+        return v * 192 + (kg * 3) * 16 + (r & 8);
+    }
+    __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
+                                const char* zs) {
+        const int g = lane >> 4;
+        const bool va = L.s == L.kg && L.d < 3;
+        const int vo = (L.kg * 3 + L.d) * 16;
+        const mq_v4i zero = {0, 0, 0, 0};
+        const int* Aw = (const int*)&dd.a;
+        const int* Bw = (const int*)&dd.b;
+        const int* Hw = (const int*)&dd.h;
+        // scale bytes sc[8h + 2v + g'] (the half h = g / 2 was picked at load; g' = g % 2)
+        const uint32_t s01 = dd.sc.x >> (8 * (g & 1)), s23 = dd.sc.y >> (8 * (g & 1));
+        float part = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            mq_v4i q;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                int w;
+                if (v == 0) w = (Aw[e] & 0x0F0F0F0F) | ((Hw[e] << 4) & 0x30303030);
+                else if (v == 1) w = (Bw[e] & 0x0F0F0F0F) | ((Hw[e] << 2) & 0x30303030);
+                else if (v == 2) w = ((Aw[e] >> 4) & 0x0F0F0F0F) | (Hw[e] & 0x30303030);
+                else w = ((Bw[e] >> 4) & 0x0F0F0F0F) | ((Hw[e] >> 2) & 0x30303030);
+                q[e] = w;
+            }
+            const mq_v4i a = *(const mq_v4i*)(va ? A + v * 192 + vo : zs);
+            const mq_v4i Dv = mq_mfma(a, q, zero);
+            const int4 mt = ((const int4*)meta)[8 * (g >> 1) + 2 * v + (g & 1)];
+            // stored q + 32 ∈ [0, 63]: subtract 32·Σ digit per digit (exact)
+            const int a0 = Dv.x - mt.y, a1 = Dv.y - mt.z, a2 = Dv.z - mt.w;
+            const float val = ldexpf((float)a2 * 65536.0f + (float)(a0 + a1 * 256), mt.x);
+            const uint32_t sw = v < 2 ? s01 : s23;
+            part += (float)(int8_t)((sw >> (16 * (v & 1))) & 0xFFu) * val;
+        }
+        return aeth_decode_d(dd.d) * part;
+    }
+};
+
+// Lane l of the wave owns activation octets o = o0 + l + 64·i (elements
+// [8o, 8o+8)) below o1; elements at or past kx read as zero.
+template <int XO, bool RAG>
+__device__ __forceinline__ void mq_load_x(const float* __restrict__ x, int o0, int o1, int kx,
+                                          float (&xv)[XO][8]) {
+#pragma unroll
+    for (int i = 0; i < XO; i++) {
+        const int o = o0 + (threadIdx.x & 63) + 64 * i;
+        if (!RAG) {  // kx % 8 == 0: copies past o1 / kx are masked at their uses
+            const int oc = min(o, max(min(o1, kx / 8) - 1, 0));
+            const float4 a = *(const float4*)(x + 8 * oc), b = *(const float4*)(x + 8 * oc + 4);
+            xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
+            xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
+        } else {  // k not a multiple of 8 (Q8_0 only): element-wise
+#pragma unroll
+            for (int t = 0; t < 8; t++) xv[i][t] = x[min(8 * o + t, kx - 1)];
+        }
+    }
+}
+
+// The wave's activation slice → compact A operands (every byte of the slice's
+// regions is written) and per-group meta: Q4_K {−S, Σx}, Q8_0 {−S, 0}, Q6_K
+// {−S, 32·Σd0, 32·Σd1, 32·Σd2}. Written and later read by this wave only.
+// Returns nonzero (wave-uniform) if the slice holds a NaN or an infinity.
+template <int F, int XO>
+__device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase, char* Mbase) {
+    typedef MF<F> T;
+    const int lane = threadIdx.x & 63;
+    const int o0 = c0 * (T::CE / 8), o1 = (c0 + nbw) * (T::CE / 8);
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < XO; i++) {
+        const int o = o0 + lane + 64 * i;
+        const bool live = o < o1;
+        float* v = xv[i];
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+            if (8 * o + t >= kx) v[t] = 0.0f;  // past k (Q8_0 padding blocks) or past the slice
+        float mx = 0.0f;
+        bool nan = false;  // fmaxf drops NaN operands: test for them explicitly
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            mx = fmaxf(mx, fabsf(v[t]));
+            nan |= v[t] != v[t];
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));  // the octets of a group are adjacent lanes
+        if (T::GE == 32) mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const bool fin = isfinite(mx);
+        if ((!fin || nan) && live) bad = 1;
+        const bool use = mx > 0.0f && fin;
+        int E = 0;
+        if (use) (void)frexpf(mx, &E);
+        const int S = use ? 22 - E : 0;
+        int d0[8], d1[8], d2[8];
+        int s0 = 0, s1 = 0, s2 = 0;
+        float fs = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int xi = use ? (int)rintf(ldexpf(v[t], S)) : 0;
+            const int a = (xi << 24) >> 24;
+            const int r = (xi - a) >> 8;
+            const int b = (r << 24) >> 24;
+            d0[t] = a;
+            d1[t] = b;
+            d2[t] = (r - b) >> 8;
+            s0 += a;
+            s1 += b;
+            s2 += d2[t];
+            fs += v[t];
+        }
+        if (F == FQ4K) {
+            fs += __shfl_xor(fs, 1, 64);
+            fs += __shfl_xor(fs, 2, 64);
+        }
+        if (F == FQ6K) {
+            s0 += __shfl_xor(s0, 1, 64);
+            s1 += __shfl_xor(s1, 1, 64);
+            s2 += __shfl_xor(s2, 1, 64);
+        }
+        if (live) {
+            const int c = o / (T::CE / 8), ec = 8 * o - c * T::CE;
+            char* dst = Abase + (size_t)c * T::AB + T::aoff(ec);
+            *(uint2*)(dst) = make_uint2(mq_pack4(d0[0], d0[1], d0[2], d0[3]), mq_pack4(d0[4], d0[5], d0[6], d0[7]));
+            *(uint2*)(dst + 16) =
+                make_uint2(mq_pack4(d1[0], d1[1], d1[2], d1[3]), mq_pack4(d1[4], d1[5], d1[6], d1[7]));
+            *(uint2*)(dst + 32) =
+                make_uint2(mq_pack4(d2[0], d2[1], d2[2], d2[3]), mq_pack4(d2[4], d2[5], d2[6], d2[7]));
+            char* mb = Mbase + (size_t)c * T::MB;
+            if (F == FQ4K && (ec & 31) == 0) ((int2*)mb)[ec >> 5] = make_int2(-S, __float_as_int(fs));
+            if (F == FQ80 && (ec & 31) == 0) ((int2*)mb)[ec >> 5] = make_int2(-S, 0);
+            if (F == FQ6K && (ec & 15) == 0) ((int4*)mb)[ec >> 4] = make_int4(-S, 32 * s0, 32 * s1, 32 * s2);
+        }
+    }
+    return __any(bad);
+}
+
+__device__ __forceinline__ unsigned long long mq_amax_key(float v, int64_t row) {
+    const uint32_t f = __float_as_uint(v);
+    const uint32_t o = (f & 0x80000000u) ? ~f : (f | 0x80000000u);
     return ((unsigned long long)o << 32) | (unsigned long long)(uint32_t)row;
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g * (1.0f / (1.0f + expf(-g))) * u; }
-
-template <int F, int WPR, int R, int XO>
-__global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvParams G) {
-    constexpr int STREAMS = GEMV_WAVES / WPR;
-    extern __shared__ __attribute__((aligned(16))) char rec[];
-    __shared__ int flag;
-    __shared__ float ssum[GEMV_WAVES];
-    __shared__ unsigned long long kmax[GEMV_WAVES];
-    typedef typename UnitT<F>::T U;
+// Fusions:
+//  norm_w    : x ← x / sqrt(Σx²/k + eps) · norm_w first (rmsnorm_inplace, runner.rs:1739-1746);
+//  swiglu    : rows (2i, 2i+1) = (gate_i, up_i); y[i] = g·σ(g)·u (runner.rs:1617-1625);
+//  amax      : 64-bit atomic max of (orderable(y) << 32 | row) — ties → last row
+//              (Iterator::max_by, runner.rs:1964-1973);
+//  accumulate: y += result (residual adds, runner.rs:1609-1611, 1629-1631).
+// RING = false: the workgroup's tiles all fit the RD load slots (issued up
+// front); RING = true: the slots are refilled as they are consumed.
+template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG>
+__global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
+    typedef MF<F> T;
+    typedef typename T::D Dt;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    __shared__ float ssum[W];
+    __shared__ unsigned long long kmax[W];
+    const int nc = G.nc;
+    char* Abase = smem;
+    char* Mbase = smem + (size_t)nc * T::AB;
+    float* part = (float*)(smem + (size_t)nc * (T::AB + T::MB));
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int stream = wave / WPR, wir = wave - stream * WPR;
-    const int u = wir * 64 + lane;
-    const int upr = G.upr, nb = G.nb;
-    const bool valid = u < upr;
+    char* zs = (char*)(part + (size_t)G.tpw * W * 16) + 16 * wave;  // this wave's zero slot
+    MqLane L;
+    L.m = lane & 15;
+    L.kg = lane >> 4;
+    L.s = L.m >> 2;
+    L.d = L.m & 3;
     const float* xr = G.x + (int64_t)blockIdx.y * G.x_stride;
     float* yr = G.y + (int64_t)blockIdx.y * G.y_stride;
-    const int64_t wg0 = (int64_t)blockIdx.x * G.rows_per_wg;
-    const int64_t wg1 = min(G.n, wg0 + G.rows_per_wg);
-    const int64_t rps = (G.rows_per_wg + STREAMS - 1) / STREAMS;
-    const int64_t sb = min(wg1, wg0 + stream * rps);
-    const int64_t se = min(wg1, sb + rps);
-    const int noct = upr * Fmt<F>::UE / 8;
-    float* red = (float*)(rec + (size_t)upr * Fmt<F>::RECB);  // [2][STREAMS][WPR][R] when WPR > 1
+    const int64_t t0 = (int64_t)blockIdx.x * G.tpw;
+    const int ntw = (int)min((int64_t)G.tpw, (int64_t)G.ntiles - t0);
+    const int c0 = nc * wave / W, nbw = nc * (wave + 1) / W - c0;
+    const int o0 = c0 * (T::CE / 8), o1 = (c0 + nbw) * (T::CE / 8);
 
     float xv[XO][8], wv[XO][8];
-    load_x<XO>(xr, G.k, noct, xv);
-    if (G.norm_w) load_x<XO>(G.norm_w, G.k, noct, wv);
-
-    // Ring of R row buffers: row i of this stream lives in buf[i % R]; each
-    // buffer is refilled with the row R ahead as soon as it has been consumed,
-    // so every wave keeps R rows of loads in flight and computes on arrival.
-    U buf[R];
+    mq_load_x<XO, RAG>(xr, o0, o1, G.kx, xv);
+    mq_load_x<XO, RAG>(G.norm_w ? G.norm_w : xr, o0, o1, G.kx, wv);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight stream
+    Dt buf[RD][NBW];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        if (valid && sb < se) {
-            load_unit(buf[r], G.P, min(sb + r, se - 1), nb, u);
-            fix_unit(buf[r], u & 1);
-        }
-    }
+    for (int r = 0; r < RD; r++)
+#pragma unroll
+        for (int i = 0; i < NBW; i++)
+            T::load(buf[r][i], G, (t0 + min(r, ntw - 1)) * nc + c0 + min(i, max(nbw - 1, 0)), lane);
 
-    if (G.norm_w) {  // fused RMSNorm: every workgroup normalises the full row
+    if (G.norm_w) {  // fused RMSNorm: the waves' slices tile the row; one barrier
         float ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < XO; i++)
+        for (int i = 0; i < XO; i++) {
+            const int o = o0 + lane + 64 * i;
 #pragma unroll
-            for (int t = 0; t < 8; t++) ss += xv[i][t] * xv[i][t];
+            for (int t = 0; t < 8; t++) ss += (o < o1 && 8 * o + t < G.kx) ? xv[i][t] * xv[i][t] : 0.0f;
+        }
         ss = aeth_wave_sum(ss);
         if (lane == 0) ssum[wave] = ss;
         __syncthreads();
         float tot = 0.0f;
 #pragma unroll
-        for (int w = 0; w < GEMV_WAVES; w++) tot += ssum[w];
+        for (int w = 0; w < W; w++) tot += ssum[w];
         const float rms = sqrtf(tot / (float)G.k + G.eps);
 #pragma unroll
         for (int i = 0; i < XO; i++)
@@ -381,63 +397,75 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvParams G) {
             for (int t = 0; t < 8; t++) xv[i][t] = xv[i][t] / rms * wv[i][t];
     }
 
-    if (build_records<F, XO>(xv, noct, rec, &flag)) {
-        const int64_t oe = G.swiglu ? se / 2 : se;
-        if (wir == 0)
-            for (int64_t row = (G.swiglu ? sb / 2 : sb) + lane; row < oe; row += 64) yr[row] = __int_as_float(0x7FC00000);
-        return;
-    }
-    Rec<F> reg;
-    if (valid) read_rec<F>(reg, rec + (size_t)u * Fmt<F>::RECB);
+    // a NaN or infinity in the slice makes every partial of this wave NaN
+    if (lane == 0) *(uint4*)zs = make_uint4(0u, 0u, 0u, 0u);
+    const float poison = mq_build<F, XO>(xv, c0, nbw, G.kx, Abase, Mbase) ? __int_as_float(0x7FC00000) : 0.0f;
 
-    unsigned long long best = 0;
-    for (int p = 0; p < G.npass; p++) {
-        const int64_t row0 = sb + (int64_t)p * R;
-        float acc[R];
+    auto tile = [&](const Dt (&b)[NBW]) {
+        float acc = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            acc[r] = (valid && row0 + r < se) ? unit_dot(buf[r], reg) : 0.0f;
-            if (valid && p + 1 < G.npass && row0 + R < se) {
-                load_unit(buf[r], G.P, min(row0 + R + r, se - 1), nb, u);
-                fix_unit(buf[r], u & 1);
+        for (int i = 0; i < NBW; i++)
+            if (i < nbw)
+                acc += T::dot(b[i], Abase + (size_t)(c0 + i) * T::AB, Mbase + (size_t)(c0 + i) * T::MB, lane, L, zs);
+        acc += __shfl_xor(acc, 16, 64);
+        acc += __shfl_xor(acc, 32, 64);
+        return acc + poison;
+    };
+    if (!RING) {  // every tile already in flight: no refills
+#pragma unroll
+        for (int r = 0; r < RD; r++) {
+            if (r < ntw) {
+                const float acc = tile(buf[r]);
+                if (lane < 16) part[(r * W + wave) * 16 + lane] = acc;
+            }
+            __builtin_amdgcn_sched_barrier(0);  // tiles in arrival order: wait for each one alone
+        }
+    } else {  // ring of RD tiles; each consumed slot is refilled at once (clamped past the end)
+        for (int j0 = 0; j0 < ntw; j0 += RD) {
+#pragma unroll
+            for (int r = 0; r < RD; r++) {
+                const int j = j0 + r;
+                if (j < ntw) {
+                    const float acc = tile(buf[r]);
+                    if (lane < 16) part[(j * W + wave) * 16 + lane] = acc;
+                }
+#pragma unroll
+                for (int i = 0; i < NBW; i++)
+                    T::load(buf[r][i], G, (t0 + min(j + RD, ntw - 1)) * nc + c0 + min(i, max(nbw - 1, 0)), lane);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        float tot = wave_reduce_rows<R>(acc, lane);
-        const int myrow = row_of_lane<R>(lane);
-        const bool writer = (lane & (64 / R - 1)) == 0;
-        if (WPR == 1) {
-            const int64_t row = row0 + myrow;
-            if (G.swiglu) {
-                const float up = __shfl_xor(tot, 64 / R, 64);  // partner row = row ^ 1
-                if (writer && (myrow & 1) == 0 && row < se) yr[row >> 1] = silu_mul(tot, up);
-            } else if (writer && row < se) {
-                const float v = G.accumulate ? yr[row] + tot : tot;
-                yr[row] = v;
-                if (G.amax) { unsigned long long kk = amax_key(v, row); best = kk > best ? kk : best; }
+    }
+    __syncthreads();
+
+    unsigned long long best = 0;
+    for (int idx = threadIdx.x; idx < ntw * 16; idx += 64 * W) {
+        const int jt = idx >> 4, nn = idx & 15;
+        const int64_t row = (t0 + jt) * 16 + nn;
+        if (row >= G.n) continue;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) sum += part[(jt * W + w) * 16 + nn];
+        if (G.swiglu) {
+            if ((nn & 1) == 0) {
+                float up = 0.0f;
+#pragma unroll
+                for (int w = 0; w < W; w++) up += part[(jt * W + w) * 16 + nn + 1];
+                yr[row >> 1] = sum * (1.0f / (1.0f + expf(-sum))) * up;
             }
         } else {
-            float* rb = red + (p & 1) * (STREAMS * WPR * R);
-            if (writer) rb[(stream * WPR + wir) * R + myrow] = tot;
-            __syncthreads();
-            if (threadIdx.x < STREAMS * R) {
-                const int s2 = threadIdx.x / R, r2 = threadIdx.x - s2 * R;
-                const int64_t sb2 = min(wg1, wg0 + s2 * rps), se2 = min(wg1, sb2 + rps);
-                const int64_t row = sb2 + (int64_t)p * R + r2;
-                if (row < se2) {
-                    float t = 0.0f;
-#pragma unroll
-                    for (int w = 0; w < WPR; w++) t += rb[(s2 * WPR + w) * R + r2];
-                    const float v = G.accumulate ? yr[row] + t : t;
-                    yr[row] = v;
-                    if (G.amax) { unsigned long long kk = amax_key(v, row); best = kk > best ? kk : best; }
-                }
+            const float v = G.accumulate ? yr[row] + sum : sum;
+            yr[row] = v;
+            if (G.amax) {
+                const unsigned long long kk = mq_amax_key(v, row);
+                best = kk > best ? kk : best;
             }
         }
     }
     if (G.amax) {
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
-            unsigned long long o = __shfl_xor(best, off, 64);
+            const unsigned long long o = __shfl_xor(best, off, 64);
             best = o > best ? o : best;
         }
         if (lane == 0) kmax[wave] = best;
@@ -445,7 +473,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvParams G) {
         if (threadIdx.x == 0) {
             unsigned long long m = kmax[0];
 #pragma unroll
-            for (int w = 1; w < GEMV_WAVES; w++) m = kmax[w] > m ? kmax[w] : m;
+            for (int w = 1; w < W; w++) m = kmax[w] > m ? kmax[w] : m;
             atomicMax(G.amax, m);
         }
     }
@@ -453,84 +481,102 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvParams G) {
 
 // ── dispatch ─────────────────────────────────────────────────────────────
 
-static int env_int(const char* name, int dflt) {
-    const char* e = getenv(name);
-    return e ? atoi(e) : dflt;
-}
-
-template <int F, int WPR, int R, int XO>
-static void launch(dim3 grid, size_t lds, hipStream_t s, GemvParams G) {
-    constexpr int STREAMS = GEMV_WAVES / WPR;
-    const int64_t rps = (G.rows_per_wg + STREAMS - 1) / STREAMS;
-    G.npass = (int)((rps + R - 1) / R);
-    hipLaunchKernelGGL((k_gemv<F, WPR, R, XO>), grid, dim3(GEMV_THREADS), lds, s, G);
-}
-
-template <int F>
-static int dispatch_fmt(GemvParams G, int64_t m, hipStream_t s) {
-    static const int wg_per_cu = env_int("AETH_GEMV_WG_PER_CU", 1);
-    static const int rsel = env_int("AETH_GEMV_R", 4);
-    const int upr = G.upr;
-    int wpr = 1;
-    while (wpr * 64 < upr) wpr *= 2;
-    const int noct = upr * Fmt<F>::UE / 8;
-    int xo = 1;
-    while (xo * GEMV_THREADS < noct) xo *= 2;
-    const size_t lds = (size_t)upr * Fmt<F>::RECB + (wpr > 1 ? 2 * GEMV_WAVES * 4 * sizeof(float) : 0);
-    if (wpr > 8 || xo > 4 || lds > 64 * 1024)
-        return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d is beyond this kernel's range", G.k);
-    if (G.swiglu && (wpr != 1 || (G.n & 1)))
-        return aeth_set_error(AETH_EUNSUPPORTED, "gemv: fused SwiGLU needs k <= 4096-wide rows and paired rows");
-    const int streams = GEMV_WAVES / wpr;
-    int64_t grid = (int64_t)aeth_num_cus() * (wg_per_cu < 1 ? 1 : wg_per_cu);
-    const int64_t need = (G.n + streams - 1) / streams;
-    if (need < grid) grid = need;
-    if (grid < 1) grid = 1;
-    int64_t rpg = (G.n + grid - 1) / grid;
-    if (G.swiglu) rpg = (rpg + 2 * streams - 1) / (2 * streams) * (2 * streams);  // even rows per stream
-    G.rows_per_wg = rpg;
-    dim3 g((unsigned)grid, (unsigned)m);
-#define L_(W, RR, X) launch<F, W, RR, X>(g, lds, s, G)
-    if (wpr == 1 && xo == 1) {
-        if (rsel == 2) L_(1, 2, 1);
-        else if (rsel == 8) L_(1, 8, 1);
-        else L_(1, 4, 1);
-    } else if (wpr == 2 && xo == 1) L_(2, 4, 1);
-    else if (wpr == 2 && xo == 2) L_(2, 4, 2);
-    else if (wpr == 4 && xo == 2) L_(4, 4, 2);
-    else if (wpr == 4 && xo == 4) L_(4, 4, 4);
-    else if (wpr == 8 && xo == 4) L_(8, 4, 4);
-    else if (wpr == 1 && xo == 2) L_(1, 4, 2);
-    else if (wpr == 2 && xo == 4) L_(2, 4, 4);
-    else return aeth_set_error(AETH_EUNSUPPORTED, "gemv: no kernel for k=%d (wpr %d, xo %d)", G.k, wpr, xo);
-#undef L_
+template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG>
+static int mq_launch_k(dim3 grid, size_t lds, hipStream_t s, const MqParams& G) {
+    static size_t opted = 64 * 1024;  // dynamic LDS above 64 KiB is opted into per kernel
+    if (lds > opted) {
+        AETH_HIP_CHECK(hipFuncSetAttribute((const void*)k_gemv_mf<F, NBW, RD, XO, RING, W, RAG>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        opted = lds;
+    }
+    hipLaunchKernelGGL((k_gemv_mf<F, NBW, RD, XO, RING, W, RAG>), grid, dim3(64 * W), lds, s, G);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
+}
+
+template <int F, int NBW, int RD, int W, bool RAG>
+static int mq_launch(dim3 grid, size_t lds, hipStream_t s, const MqParams& G) {
+    constexpr int XO = (NBW * MF<F>::CE / 8 + 63) / 64;
+    return G.tpw <= RD ? mq_launch_k<F, NBW, RD, XO, false, W, RAG>(grid, lds, s, G)
+                       : mq_launch_k<F, NBW, RD, XO, true, W, RAG>(grid, lds, s, G);
+}
+
+template <int F, bool RAG>
+static int mq_dispatch(MqParams G, int64_t m, hipStream_t s) {
+    typedef MF<F> T;
+    const int nc = G.nc;
+    // Shape choice (measured on the decode and benchmark shapes): W waves split
+    // K, 16 only for long rows; RD tiles per workgroup with all loads issued up
+    // front (short memory queues, so each wave's tiles arrive early and their
+    // compute overlaps the stream); one tile per workgroup when there are no
+    // more tiles than CUs; taller matrices use the ring with ~2 workgroups per
+    // CU so the per-workgroup activation conversion stays amortised.
+    // Tuning overrides, read once: AETH_GEMV_WAVES (8 | 16), AETH_GEMV_TPW.
+    static const int env_w = getenv("AETH_GEMV_WAVES") ? atoi(getenv("AETH_GEMV_WAVES")) : 0;
+    static const int env_tpw = getenv("AETH_GEMV_TPW") ? atoi(getenv("AETH_GEMV_TPW")) : 0;
+    const int64_t cus = aeth_num_cus();
+    int W = (int64_t)nc * T::CE >= 8192 ? 16 : 8;
+    if (env_w) W = env_w == 16 ? 16 : 8;
+    const int nbw = (nc + W - 1) / W;
+    const int NBW = nbw <= 1 ? 1 : nbw <= 2 ? 2 : nbw <= 4 ? 4 : 8;
+    if (nbw > 8) return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d is beyond this kernel's range", G.k);
+    const int RD = NBW <= 2 || (W == 8 && NBW == 4 && F != FQ6K) ? 2 : 1;
+    int64_t tpw = G.ntiles <= cus ? 1 : G.ntiles <= 8 * cus ? RD : aeth_cdiv(G.ntiles, 2 * cus);
+    if (env_tpw > 0) tpw = env_tpw;
+    if (tpw > MQ_TPW_MAX) tpw = MQ_TPW_MAX;
+    G.tpw = (int)tpw;
+    const size_t lds = (size_t)nc * (T::AB + T::MB) + (size_t)tpw * W * 16 * 4 + (size_t)W * 16;
+    if (lds > MQ_LDS_MAX)
+        return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d needs %zu B of LDS (max %d)", G.k, lds, MQ_LDS_MAX);
+    const dim3 grid((unsigned)aeth_cdiv(G.ntiles, tpw), (unsigned)m);
+    if (W == 16) {
+        if (NBW == 1) return mq_launch<F, 1, 2, 16, RAG>(grid, lds, s, G);
+        if (NBW == 2) return mq_launch<F, 2, 2, 16, RAG>(grid, lds, s, G);
+        if (NBW == 4) return mq_launch<F, 4, 1, 16, RAG>(grid, lds, s, G);
+        return mq_launch<F, 8, 1, 16, RAG>(grid, lds, s, G);
+    }
+    if (NBW == 1) return mq_launch<F, 1, 2, 8, RAG>(grid, lds, s, G);
+    if (NBW == 2) return mq_launch<F, 2, 2, 8, RAG>(grid, lds, s, G);
+    if (NBW == 4) {
+        if (RD == 2) return mq_launch<F, 4, 2, 8, RAG>(grid, lds, s, G);
+        return mq_launch<F, 4, 1, 8, RAG>(grid, lds, s, G);
+    }
+    return mq_launch<F, 8, 1, 8, RAG>(grid, lds, s, G);
 }
 
 int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, const GemvEpi& e,
                         hipStream_t s) {
     if (m > 65535) return aeth_set_error(AETH_EINVAL, "gemv: m=%lld exceeds 65535", (long long)m);
-    GemvParams G;
-    G.P = Planes{w->p0, w->p1, w->p2, w->p3};
+    MqParams G;
+    G.p0 = w->p0;
+    G.p1 = w->p1;
+    G.p2 = w->p2;
     G.n = w->n;
-    G.nb = (int)w->nb;
-    G.upr = w->dtype == AETH_DTYPE_Q8_0 ? (int)w->nb : (int)w->nb * 4;
+    G.ntiles = (int)aeth_cdiv(w->n, 16);
+    G.tpw = 1;
     G.x = d_x;
-    G.k = (int)w->k;
     G.x_stride = w->k;
+    G.k = (int)w->k;
     G.y = d_y;
     G.y_stride = e.swiglu ? w->n / 2 : w->n;
     G.accumulate = (e.flags & AETH_MM_ACCUMULATE) ? 1 : 0;
-    G.rows_per_wg = 0;
-    G.npass = 0;
     G.norm_w = e.norm_w;
     G.eps = e.eps;
     G.swiglu = e.swiglu;
     G.amax = e.amax;
-    if (w->dtype == AETH_DTYPE_Q4_K) return aeth_gemv_q4k_launch(w, d_x, m, d_y, e, s);
-    if (w->dtype == AETH_DTYPE_Q6_K) return dispatch_fmt<FMT_Q6K>(G, m, s);
-    if (w->dtype == AETH_DTYPE_Q8_0) return dispatch_fmt<FMT_Q80>(G, m, s);
+    const bool q8 = w->dtype == AETH_DTYPE_Q8_0;
+    G.nc = q8 ? (int)aeth_cdiv(w->nb, 4) : (int)w->nb;
+    G.kx = q8 ? (int)w->k : (int)w->nb * 256;  // K-quants read k/256 whole blocks (avx2.rs:26)
+    if (G.nc < 1) return aeth_set_error(AETH_EINVAL, "gemv: empty rows (k=%d)", G.k);
+    if (e.swiglu && (w->n & 1)) return aeth_set_error(AETH_EUNSUPPORTED, "gemv: fused SwiGLU needs paired rows");
+    if (e.norm_w && G.kx != G.k)
+        return aeth_set_error(AETH_EUNSUPPORTED, "gemv: fused RMSNorm needs k a multiple of 256");
+    const bool rag = (G.kx & 7) != 0;
+    if (!rag && (((uintptr_t)d_x & 15) || (e.norm_w && ((uintptr_t)e.norm_w & 15)) || (m > 1 && (G.k & 3))))
+        return aeth_set_error(AETH_EINVAL, "gemv: x rows and the norm weight must be 16-byte aligned");
+    if (w->dtype == AETH_DTYPE_Q4_K) return mq_dispatch<FQ4K, false>(G, m, s);
+    if (w->dtype == AETH_DTYPE_Q6_K) return mq_dispatch<FQ6K, false>(G, m, s);
+    if (q8) return rag ? mq_dispatch<FQ80, true>(G, m, s) : mq_dispatch<FQ80, false>(G, m, s);
     return aeth_set_error(AETH_EUNSUPPORTED, "gemv: dtype %d", w->dtype);
 }
 

@@ -3,7 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// Device copy of one QuantWeight in per-field planes (see aeth_weights.hip).
+// Device copy of one QuantWeight in per-field planes, rows in 16-row tiles
+// (layouts in aeth_weights.hip).
 struct aeth_weight {
     int dtype;
     int64_t n, k;         // out_features, in_features
@@ -31,7 +32,7 @@ __host__ __device__ inline int64_t aeth_q4k_qs_off(int64_t row, int64_t b, int q
     return ((((row >> 4) * nb + b) * 2 + (q >> 6)) * 64 + (row & 15) + 16 * ((q >> 4) & 3)) * 16 + (q & 15);
 }
 
-// Fusions around the GEMV (see k_gemv in aeth_gemv.hip).
+// Fusions around the GEMV (see k_gemv_mf in aeth_gemv.hip).
 struct GemvEpi {
     unsigned flags = 0;                   // AETH_MM_ACCUMULATE
     const float* norm_w = nullptr;        // fused RMSNorm weight (length k)
@@ -45,9 +46,6 @@ int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float
                         hipStream_t s);
 int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags,
                      hipStream_t s);
-// Q4_K GEMV on the int8 matrix cores (aeth_gemv_q4k.hip); same contract.
-int aeth_gemv_q4k_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, const GemvEpi& e,
-                         hipStream_t s);
 // Q4_K prefill GEMM (m > 1).
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s);

@@ -63,50 +63,56 @@ int64_t aeth_blocks_per_row(int dtype, int64_t k) {
     return k / 256;
 }
 
-// ── planar layout ────────────────────────────────────────────────────────
-// Per row (nb blocks), fields are split into planes and the quant bytes are
-// ordered by the GEMV's lane "units" so that every wave load is contiguous:
-//  Q4_K: 16-row tiles for the matrix-core GEMV (aeth_q4k_hdr_off /
-//        aeth_q4k_qs_off in aeth_internal.hpp): p0 = headers
-//        [tile][b][16 rows][16 B], p1 = quants [tile][b][half][lane][16 B];
-//        the rows that pad the last tile are zero.
-//  Q6_K: p0 = ql, per row 2 halves of nb*64 bytes: unit u = 4b+2h+g owns
-//        A = ql[h*64+16g, +16) at 16u and B = ql[h*64+32+16g, +16) at
-//        nb*64 + 16u; p1 = qh[row*nb + b][64] (= 16 bytes per unit in unit
-//        order); p2 = sc[row*nb + b][16]; p3 = d[row*nb + b] (f16).
-//  Q8_0: p0 = qs, per row 2 halves of nb*16 bytes: block b's quants [0,16)
-//        at 16b and [16,32) at nb*16 + 16b; p1 = d[row*nb + b] (f16).
+// ── device layout ────────────────────────────────────────────────────────
+// Rows are grouped in tiles of 16 (zero rows pad the last tile) so that each
+// wave load of the matrix-core GEMV (aeth_gemv.hip) covers 16 rows
+// contiguously; lane (n, kg) = lane n + 16·kg of a 64-lane wave.
+//  Q4_K: p0 = headers [tile][b][16 rows][16 B]; p1 = quants [tile][b][half h][lane][16 B],
+//        lane (n, kg) = qs[64h + 16kg, +16) of row n (aeth_q4k_*_off).
+//  Q6_K: p0 = [tile][b][part][lane][16 B], lane (n, kg = 2h + g'): part 0 =
+//        ql[64h + 16g', +16), part 1 = ql[64h + 32 + 16g', +16), part 2 =
+//        qh[32h + 16g', +16); p1 = sc [tile][b][16 rows][16 B]; p2 = d [tile][b][16 rows].
+//  Q8_0: blocks in groups of 4 (zero blocks pad the row to whole groups);
+//        p0 = quants [tile][group][j][lane][16 B], lane (n, kg) = bytes
+//        [16(kg & 1), +16) of block 4·group + 2j + (kg ≥ 2); p1 = d [tile][group][4][16 rows].
 
 static int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
-// Maps raw GGUF byte i (block-major over all rows) to its planar address.
+// Maps raw GGUF byte i (block-major over all rows) to its device address.
 __device__ __forceinline__ uint8_t* planar_addr(int dtype, int64_t i, int64_t nb, uint8_t* p0, uint8_t* p1,
                                                 uint8_t* p2, uint8_t* p3) {
+    (void)p3;
     if (dtype == AETH_DTYPE_Q4_K) {
-        int64_t blk = i / Q4K_BLOCK_BYTES;
-        int off = (int)(i - blk * Q4K_BLOCK_BYTES);
-        int64_t row = blk / nb, b = blk - row * nb;
+        const int64_t blk = i / Q4K_BLOCK_BYTES;
+        const int off = (int)(i - blk * Q4K_BLOCK_BYTES);
+        const int64_t row = blk / nb, b = blk - row * nb;
         if (off < 16) return p0 + aeth_q4k_hdr_off(row, b, nb) + off;
         return p1 + aeth_q4k_qs_off(row, b, off - 16, nb);
     }
     if (dtype == AETH_DTYPE_Q6_K) {
-        int64_t blk = i / Q6K_BLOCK_BYTES;
-        int off = (int)(i - blk * Q6K_BLOCK_BYTES);
-        if (off < 128) {
-            int64_t row = blk / nb, b = blk - row * nb;
-            int h = off >> 6, r = off & 63, half = r >> 5, g = (r >> 4) & 1, pos = r & 15;
-            return p0 + row * nb * 128 + half * (nb * 64) + (b * 4 + h * 2 + g) * 16 + pos;
+        const int64_t blk = i / Q6K_BLOCK_BYTES;
+        const int off = (int)(i - blk * Q6K_BLOCK_BYTES);
+        const int64_t row = blk / nb, b = blk - row * nb;
+        const int64_t tb = (row >> 4) * nb + b, n = row & 15;
+        if (off < 128) {  // ql
+            const int h = off >> 6, r = off & 63, part = r >> 5, kg = 2 * h + ((r >> 4) & 1);
+            return p0 + ((tb * 3 + part) * 64 + n + 16 * kg) * 16 + (r & 15);
         }
-        if (off < 192) return p1 + blk * 64 + (off - 128);
-        if (off < 208) return p2 + blk * 16 + (off - 192);
-        return p3 + blk * 2 + (off - 208);
+        if (off < 192) {  // qh
+            const int q = off - 128, kg = 2 * (q >> 5) + ((q >> 4) & 1);
+            return p0 + ((tb * 3 + 2) * 64 + n + 16 * kg) * 16 + (q & 15);
+        }
+        if (off < 208) return p1 + (tb * 16 + n) * 16 + (off - 192);
+        return p2 + (tb * 16 + n) * 2 + (off - 208);
     }
-    int64_t blk = i / Q8_BLOCK_BYTES;
-    int off = (int)(i - blk * Q8_BLOCK_BYTES);
-    if (off < 2) return p1 + blk * 2 + off;
-    int64_t row = blk / nb, b = blk - row * nb;
-    int t = off - 2, half = t >> 4, pos = t & 15;
-    return p0 + row * nb * 32 + half * (nb * 16) + b * 16 + pos;
+    const int64_t blk = i / Q8_BLOCK_BYTES;
+    const int off = (int)(i - blk * Q8_BLOCK_BYTES);
+    const int64_t row = blk / nb, b = blk - row * nb, ngr = (nb + 3) / 4;
+    const int64_t tg = (row >> 4) * ngr + (b >> 2), n = row & 15;
+    const int s = (int)(b & 3);
+    if (off < 2) return p1 + ((tg * 4 + s) * 16 + n) * 2 + off;
+    const int p = off - 2, kg = 2 * (s & 1) + (p >> 4);
+    return p0 + ((tg * 2 + (s >> 1)) * 64 + n + 16 * kg) * 16 + (p & 15);
 }
 
 __global__ void k_relayout(int dtype, int64_t nb, uint8_t* __restrict__ raw, uint8_t* __restrict__ p0,
@@ -150,10 +156,10 @@ extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, cons
     w->nblk = n * w->nb;
     w->block_bytes = bb;
     int64_t sz[4] = {0, 0, 0, 0};
-    const int64_t padded_blk = aeth_cdiv(n, 16) * 16 * w->nb;  // Q4_K: whole 16-row tiles
-    if (dtype == AETH_DTYPE_Q4_K) { sz[0] = padded_blk * 16; sz[1] = padded_blk * 128; }
-    else if (dtype == AETH_DTYPE_Q6_K) { sz[0] = w->nblk * 128; sz[1] = w->nblk * 64; sz[2] = w->nblk * 16; sz[3] = w->nblk * 2; }
-    else { sz[0] = w->nblk * 32; sz[1] = w->nblk * 2; }
+    const int64_t prow = aeth_cdiv(n, 16) * 16;  // whole 16-row tiles
+    if (dtype == AETH_DTYPE_Q4_K) { sz[0] = prow * w->nb * 16; sz[1] = prow * w->nb * 128; }
+    else if (dtype == AETH_DTYPE_Q6_K) { sz[0] = prow * w->nb * 192; sz[1] = prow * w->nb * 16; sz[2] = prow * w->nb * 2; }
+    else { const int64_t pb = aeth_cdiv(w->nb, 4) * 4; sz[0] = prow * pb * 32; sz[1] = prow * pb * 2; }
     int64_t off[4], tot = 0;
     for (int i = 0; i < 4; i++) { off[i] = tot; tot += align256(sz[i]); }
     w->bytes = w->nblk * bb;
@@ -163,8 +169,8 @@ extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, cons
         return aeth_set_error(AETH_ENOMEM, "aeth_weight_create: hipMalloc(%lld) failed: %s", (long long)tot,
                               hipGetErrorString(e));
     }
-    if (dtype == AETH_DTYPE_Q4_K && (n & 15)) {
-        e = hipMemsetAsync(w->base, 0, (size_t)tot, s);  // padding rows of the last tile read as zero
+    {
+        e = hipMemsetAsync(w->base, 0, (size_t)tot, s);  // padding rows / blocks read as zero
         if (e != hipSuccess) {
             hipFree(w->base);
             delete w;

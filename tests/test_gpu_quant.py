@@ -92,7 +92,8 @@ def test_weight_relayout_round_trip(gpu, dtype):
 
 # ── GEMV / GEMM parity ────────────────────────────────────────────────────
 
-SHAPES = [(1, 64, 256), (1, 300, 512), (1, 1000, 4096), (1, 333, 14336), (3, 8, 256), (4, 129, 1024)]
+SHAPES = [(1, 64, 256), (1, 300, 512), (1, 1000, 4096), (1, 333, 14336), (3, 8, 256), (4, 129, 1024),
+          (1, 16, 768), (2, 48, 2048), (1, 5000, 8192)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -106,6 +107,39 @@ def test_matmul_parity(gpu, dtype, m, n, k):
     A.lib().aeth_weight_free(w)
     ref = O.reference_matmul(dtype, x, raw, m, n, k)
     assert_close(got, ref, what="%d m=%d n=%d k=%d" % (dtype, m, n, k))
+
+
+# Q8_0 rows hold ceil(k/32) blocks (q8_0.rs:16); the last block's quants past k
+# are ignored. k = 200 pads the device layout with a zero block (groups of 4),
+# k = 100 / 1000 are not multiples of 8 (element-wise activation loads).
+@pytest.mark.parametrize("m,n,k", [(1, 70, 200), (1, 45, 100), (2, 33, 1000), (1, 17, 32), (3, 40, 4128)])
+def test_matmul_parity_q8_0_ragged_k(gpu, m, n, k):
+    rng = np.random.default_rng(n * 7 + k)
+    raw = weight(Q8_0, n, k, n + 3 * k)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = make_weight(gpu, Q8_0, n, k, raw)
+    back = np.zeros_like(raw)
+    A.check(A.lib().aeth_weight_export_raw(w, back.ctypes.data, 0, None), "export")
+    assert np.array_equal(back, raw)
+    got = gemv(gpu, w, x, n, m)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q8_0, x, raw, m, n, k)
+    assert_close(got, ref, what="q8_0 m=%d n=%d k=%d" % (m, n, k))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_matmul_nonfinite_activation_gives_nan_rows(gpu, dtype):
+    """A NaN activation makes every output NaN, as NaN·w does in every row of the
+    reference's sums (an infinity also yields NaN rows here, see DESIGN)."""
+    n, k = 40, 512
+    raw = weight(dtype, n, k, 5)
+    x = np.random.default_rng(1).standard_normal(k).astype(np.float32)
+    x[300] = np.nan
+    w = make_weight(gpu, dtype, n, k, raw)
+    got = gemv(gpu, w, x, n, 1)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(dtype, x, raw, 1, n, k)
+    assert np.isnan(ref).all() and np.isnan(got).all()
 
 
 @pytest.mark.parametrize("dtype", [Q4_K, Q6_K])
