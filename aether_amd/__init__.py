@@ -72,6 +72,7 @@ _SIGS = {
     "aeth_runner_kv_from_host": (_INT, [_P, _P, _I32]),
     "aeth_runner_seq_len": (_INT, [_P]),
     "aeth_runner_decode": (_INT, [_P, _I32, _I32, _P, _P]),
+    "aeth_runner_prefill": (_INT, [_P, _P, _I32, _P, _P]),
     "aeth_runner_generate": (_INT, [_P, _I32, _I32, _I32, _P, _INT]),
     "aeth_runner_export": (_INT, [_P, _INT, _I32, _P, _I64]),
     "aeth_runner_stream": (_P, [_P]),

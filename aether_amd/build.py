@@ -15,6 +15,7 @@ SOURCES = [
     "aeth_gemv.hip",
     "aeth_gemm.hip",
     "aeth_decode_ops.hip",
+    "aeth_prefill.hip",
     "aeth_host.cpp",
     "aeth_runner.cpp",
 ]

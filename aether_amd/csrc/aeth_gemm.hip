@@ -12,6 +12,14 @@
 //    Scales are therefore applied once per super-block, not per element.
 // Each product A_hi·w and A_lo·w costs one MFMA pass, so the useful rate is
 // half the fp16 MFMA rate.
+//
+// Weight dequantisation in packed fp16: the half with bits 0x6400 | q is
+// 1024 + q (q < 1024), and one v_pk_fma_f16 with (sc, −1024·sc) gives q·sc
+// exactly (the fused product is exact, the result an integer below 2048).
+// Masking a dword with 0x000F000F yields the pair (elements 0, 2) of its four
+// bytes and (w >> 8) the pair (1, 3), so each group of 4 k-positions is stored
+// in the order [0, 2, 1, 3]; the activation prep writes A in the same order,
+// and every dot product is unchanged.
 #include <math.h>
 #include <stdlib.h>
 
@@ -19,6 +27,7 @@
 #include "aeth_internal.hpp"
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // ── activation prep: A (f32) → Ah, Al (fp16), Sh, Sl (fp16 sub-block sums),
@@ -42,8 +51,9 @@ __global__ void __launch_bounds__(256) k_gemm_prep(const float* __restrict__ A, 
     for (int i = tid; i < k; i += 256) {
         const float v = ldexpf(a[i], -e);
         const _Float16 h = (_Float16)v;
-        Ah[(int64_t)m * k + i] = h;
-        Al[(int64_t)m * k + i] = (_Float16)(v - (float)h);
+        const int pi = (i & ~3) | ((0x3120 >> (4 * (i & 3))) & 3);  // positions 1 and 2 of each 4 swapped
+        Ah[(int64_t)m * k + pi] = h;
+        Al[(int64_t)m * k + pi] = (_Float16)(v - (float)h);
     }
     for (int s = tid; s < k / 32; s += 256) {
         float sum = 0.0f;
@@ -85,8 +95,12 @@ __device__ __forceinline__ void k4_sm(const uint4& h, int s, int& sc, int& m) {
 
 // Workgroup: BM × 128 tile of C, 4 waves in 2 × 2, wave tile (BM/2) × 64 =
 // TM × 2 MFMA tiles of 32 × 32. K advances by 64 (a quarter super-block).
-template <int BM>
+// Global loads run D steps ahead of the LDS stores (register staging slots
+// j % D of the 4 unrolled steps of a super-block), so each step's loads have D
+// steps of MFMA work to arrive in.
+template <int BM, int D>
 __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs G) {
+    static_assert(D == 1 || D == 2 || D == 4, "prefetch distance divides the 4 steps of a super-block");
     constexpr int TM = BM / 64;  // 32-row MFMA tiles per wave
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][2][BM * GEMM_LDR];  // [buf][hi/lo]
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][GEMM_BN * GEMM_LDR];
@@ -96,61 +110,64 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs G) {
     const int nb = G.nb;
     const int nsteps = nb * 4;
 
-    // global → register staging for one K-step
+    // global → register staging for one K-step. Every load is unconditional
+    // (rows past m / n are clamped to valid rows and never written back).
     // A: BM rows × 64 halves × {hi, lo}: 16-byte pieces, 8 per row per part
     constexpr int A_PIECES = BM * 8 * 2;
     constexpr int A_PER_T = A_PIECES / 256;
-    uint4 ra[A_PER_T];
+    // piece i = tid + 256·i: part (hi/lo) = 256·i / (8·BM) is known at compile time
+    uint4 ra[D][A_PER_T];
+    const int a_rr = (tid / 8) % BM, a_c = tid % 8;
     // B: 128 rows × one Q4_K unit (32 qs bytes): 2 threads per row, 16 bytes each
-    uint4 rq;
-    uint4 rh;
+    uint4 rq[D];
+    uint4 rh[D];
     const int brow = tid >> 1, bhalf = tid & 1;
+    const int64_t nrow = min(n0 + brow, G.n - 1);
+    const uint8_t* q_src = G.qs + aeth_q4k_qs_off(nrow, 0, 16 * bhalf, nb);
+    const uint8_t* h_src = G.hdr + aeth_q4k_hdr_off(nrow, 0, nb);
 
-    auto load_step = [&](int step) {
+    auto load_step = [&](int step, int slot) {
         const int b = step >> 2, j = step & 3;
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) {
-            const int p = tid + 256 * i;
-            const int part = p / (BM * 8), rr = (p / 8) % BM, c = p % 8;
-            const int row = m0 + rr;
-            const _Float16* src = part ? G.Al : G.Ah;
-            ra[i] = row < G.m ? *(const uint4*)(src + (int64_t)row * G.k + b * 256 + j * 64 + c * 8) : make_uint4(0, 0, 0, 0);
+            const int part = (256 * i) / (BM * 8), rshift = ((256 * i) % (BM * 8)) / 8;
+            const int row_i = min(m0 + (a_rr + rshift) % BM, G.m - 1);
+            ra[slot][i] = *(const uint4*)((part ? G.Al : G.Ah) + (int64_t)row_i * G.k + a_c * 8 + step * 64);
         }
-        const int nrow = n0 + brow;
-        if (nrow < G.n) {
-            rq = *(const uint4*)(G.qs + aeth_q4k_qs_off(nrow, b, 32 * j + 16 * bhalf, nb));
-            rh = *(const uint4*)(G.hdr + aeth_q4k_hdr_off(nrow, b, nb));
-        } else {
-            rq = make_uint4(0, 0, 0, 0);
-            rh = make_uint4(0, 0, 0, 0);
-        }
+        rq[slot] = *(const uint4*)(q_src + b * 2048 + (j >> 1) * 1024 + (j & 1) * 512);
+        rh[slot] = *(const uint4*)(h_src + b * 256);
     };
-    auto store_step = [&](int step, int buf) {
+    auto store_step = [&](int step, int buf, int slot) {
         const int j = step & 3;
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) {
-            const int p = tid + 256 * i;
-            const int part = p / (BM * 8), rr = (p / 8) % BM, c = p % 8;
-            *(uint4*)(&sA[buf][part][rr * GEMM_LDR + c * 8]) = ra[i];
+            const int part = (256 * i) / (BM * 8), rshift = ((256 * i) % (BM * 8)) / 8;
+            *(uint4*)(&sA[buf][part][((a_rr + rshift) % BM) * GEMM_LDR + a_c * 8]) = ra[slot][i];
         }
         // unit bytes [16·bhalf, 16·bhalf+16) of qs[32j .. 32j+32): byte l → low nibble
         // is element l (sub-block 2j), high nibble element 32 + l (sub-block 2j+1)
         int sc0, m_, sc1;
-        k4_sm(rh, 2 * j, sc0, m_);
-        k4_sm(rh, 2 * j + 1, sc1, m_);
-        const uint32_t* qw = (const uint32_t*)&rq;
-        _Float16 lo[16], hi[16];
+        k4_sm(rh[slot], 2 * j, sc0, m_);
+        k4_sm(rh[slot], 2 * j + 1, sc1, m_);
+        const half2_t s0 = {(_Float16)sc0, (_Float16)sc0}, z0 = {(_Float16)(-1024 * sc0), (_Float16)(-1024 * sc0)};
+        const half2_t s1 = {(_Float16)sc1, (_Float16)sc1}, z1 = {(_Float16)(-1024 * sc1), (_Float16)(-1024 * sc1)};
+        const uint32_t* qw = (const uint32_t*)&rq[slot];
+        uint32_t lo[8], hi[8];
 #pragma unroll
-        for (int t = 0; t < 16; t++) {
-            const uint32_t byte = (qw[t >> 2] >> (8 * (t & 3))) & 0xFFu;
-            lo[t] = (_Float16)(float)((int)(byte & 15u) * sc0);
-            hi[t] = (_Float16)(float)((int)(byte >> 4) * sc1);
+        for (int e = 0; e < 4; e++) {
+            const uint32_t w = qw[e];
+            const uint32_t q[4] = {(w & 0x000F000Fu) | 0x64006400u, ((w >> 8) & 0x000F000Fu) | 0x64006400u,
+                                   ((w >> 4) & 0x000F000Fu) | 0x64006400u, ((w >> 12) & 0x000F000Fu) | 0x64006400u};
+            lo[2 * e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2_t, q[0]), s0, z0));
+            lo[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2_t, q[1]), s0, z0));
+            hi[2 * e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2_t, q[2]), s1, z1));
+            hi[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2_t, q[3]), s1, z1));
         }
         _Float16* dst = &sB[buf][brow * GEMM_LDR];
-        *(half8_t*)(dst + bhalf * 16) = *(half8_t*)&lo[0];
-        *(half8_t*)(dst + bhalf * 16 + 8) = *(half8_t*)&lo[8];
-        *(half8_t*)(dst + 32 + bhalf * 16) = *(half8_t*)&hi[0];
-        *(half8_t*)(dst + 32 + bhalf * 16 + 8) = *(half8_t*)&hi[8];
+        *(uint4*)(dst + bhalf * 16) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        *(uint4*)(dst + bhalf * 16 + 8) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+        *(uint4*)(dst + 32 + bhalf * 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        *(uint4*)(dst + 32 + bhalf * 16 + 8) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
     };
 
     f32x16 acc[TM][2], part[TM][2];
@@ -162,65 +179,73 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs G) {
             part[a][c] = (f32x16){};
         }
 
-    load_step(0);
-    store_step(0, 0);
-    __syncthreads();
+#pragma unroll
+    for (int d = 0; d < D; d++) load_step(min(d, nsteps - 1), d);
     const int lr = lane & 31, lk = (lane >> 5) * 8;
-    for (int step = 0; step < nsteps; step++) {
-        const int buf = step & 1;
-        if (step + 1 < nsteps) load_step(step + 1);
-        // MFMAs of this K-step: 4 k-slices of 16, hi and lo parts
+    int hcol[2], srow[TM];
 #pragma unroll
-        for (int ks = 0; ks < GEMM_BK / 16; ks++) {
-            half8_t bv[2];
+    for (int c = 0; c < 2; c++) hcol[c] = min(n0 + wn * 64 + c * 32 + lr, G.n - 1);
 #pragma unroll
-            for (int c = 0; c < 2; c++)
-                bv[c] = *(const half8_t*)(&sB[buf][(wn * 64 + c * 32 + lr) * GEMM_LDR + ks * 16 + lk]);
+    for (int a = 0; a < TM; a++) srow[a] = min(m0 + wm * (BM / 2) + a * 32 + lr, G.m - 1);
+    for (int b = 0; b < nb; b++) {
+        // this super-block's scales and sub-block sums, issued ahead of the steps' loads
+        uint4 h[2];
+        half8_t sv[TM];
 #pragma unroll
-            for (int a = 0; a < TM; a++) {
-                const int row = wm * (BM / 2) + a * 32 + lr;
-                const half8_t ah = *(const half8_t*)(&sA[buf][0][row * GEMM_LDR + ks * 16 + lk]);
-                const half8_t al = *(const half8_t*)(&sA[buf][1][row * GEMM_LDR + ks * 16 + lk]);
+        for (int c = 0; c < 2; c++) h[c] = *(const uint4*)(G.hdr + aeth_q4k_hdr_off(hcol[c], b, nb));
 #pragma unroll
-                for (int c = 0; c < 2; c++) {
-                    part[a][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bv[c], part[a][c], 0, 0, 0);
-                    part[a][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bv[c], part[a][c], 0, 0, 0);
-                }
-            }
-        }
-        if ((step & 3) == 3) {
-            // super-block done: C += d·P − dmin·Q, Q = Σ_s m_s·S_s (hi/lo) by one MFMA per tile
-            const int b = step >> 2;
+        for (int a = 0; a < TM; a++)
+            sv[a] = *(const half8_t*)((lk ? G.Sl : G.Sh) + (int64_t)srow[a] * (G.k / 32) + b * 8);
 #pragma unroll
-            for (int c = 0; c < 2; c++) {
-                const int col = n0 + wn * 64 + c * 32 + lr;
-                uint4 h = make_uint4(0, 0, 0, 0);
-                if (col < G.n) h = *(const uint4*)(G.hdr + aeth_q4k_hdr_off(col, b, nb));
-                const float d = aeth_decode_d(h.x), dmin = aeth_decode_d(h.x >> 16);
-                half8_t mv;
+        for (int j = 0; j < 4; j++) {
+            const int step = 4 * b + j, buf = j & 1;
+            // LDS buffer buf was last read by step - 2, which every wave finished before
+            // the barrier of step - 1
+            store_step(step, buf, j % D);
+            __syncthreads();
+            load_step(min(step + D, nsteps - 1), j % D);
+            // MFMAs of this K-step: 4 k-slices of 16, hi and lo parts
 #pragma unroll
-                for (int s = 0; s < 8; s++) {
-                    int scv, mm;
-                    k4_sm(h, s, scv, mm);
-                    mv[s] = (_Float16)(float)mm;
-                }
+            for (int ks = 0; ks < GEMM_BK / 16; ks++) {
+                half8_t bv[2];
+#pragma unroll
+                for (int c = 0; c < 2; c++)
+                    bv[c] = *(const half8_t*)(&sB[buf][(wn * 64 + c * 32 + lr) * GEMM_LDR + ks * 16 + lk]);
 #pragma unroll
                 for (int a = 0; a < TM; a++) {
-                    const int row = m0 + wm * (BM / 2) + a * 32 + lr;
-                    half8_t sv = (half8_t){};
-                    if (row < G.m) sv = *(const half8_t*)((lk ? G.Sl : G.Sh) + (int64_t)row * (G.k / 32) + b * 8);
-                    f32x16 q = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv, mv, (f32x16){}, 0, 0, 0);
-                    // S was scaled by 2^-(e+5) against A's 2^-e: fold the 2^5 into dmin
-                    const float dm = dmin * 32.0f;
+                    const int row = wm * (BM / 2) + a * 32 + lr;
+                    const half8_t ah = *(const half8_t*)(&sA[buf][0][row * GEMM_LDR + ks * 16 + lk]);
+                    const half8_t al = *(const half8_t*)(&sA[buf][1][row * GEMM_LDR + ks * 16 + lk]);
 #pragma unroll
-                    for (int r = 0; r < 16; r++) acc[a][c][r] += d * part[a][c][r] - dm * q[r];
-                    part[a][c] = (f32x16){};
+                    for (int c = 0; c < 2; c++) {
+                        part[a][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bv[c], part[a][c], 0, 0, 0);
+                        part[a][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bv[c], part[a][c], 0, 0, 0);
+                    }
                 }
             }
-        }
-        if (step + 1 < nsteps) {
-            store_step(step + 1, buf ^ 1);
-            __syncthreads();
+            if (j == 3) {
+                // super-block done: C += d·P − dmin·Q, Q = Σ_s m_s·S_s (hi/lo) by one MFMA per tile
+#pragma unroll
+                for (int c = 0; c < 2; c++) {
+                    const float d = aeth_decode_d(h[c].x), dmin = aeth_decode_d(h[c].x >> 16);
+                    half8_t mv;
+#pragma unroll
+                    for (int s = 0; s < 8; s++) {
+                        int scv, mm;
+                        k4_sm(h[c], s, scv, mm);
+                        mv[s] = (_Float16)(float)mm;
+                    }
+#pragma unroll
+                    for (int a = 0; a < TM; a++) {
+                        f32x16 q = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv[a], mv, (f32x16){}, 0, 0, 0);
+                        // S was scaled by 2^-(e+5) against A's 2^-e: fold the 2^5 into dmin
+                        const float dm = dmin * 32.0f;
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[a][c][r] += d * part[a][c][r] - dm * q[r];
+                        part[a][c] = (f32x16){};
+                    }
+                }
+            }
         }
     }
     // epilogue: undo the row scale 2^-e, write (or accumulate) C
@@ -277,12 +302,18 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     GemmArgs G{Ah, Al, Sh, Sl, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, d_c,
                (flags & AETH_MM_ACCUMULATE) ? 1 : 0};
     const int64_t tiles128 = aeth_cdiv(w->n, GEMM_BN) * aeth_cdiv(m, 128);
-    if (tiles128 >= aeth_num_cus()) {
+    // tuning override, read once: AETH_GEMM_D (prefetch distance 1, 2 or 4)
+    static const int env_d = getenv("AETH_GEMM_D") ? atoi(getenv("AETH_GEMM_D")) : 0;
+    static const int env_bm = getenv("AETH_GEMM_BM") ? atoi(getenv("AETH_GEMM_BM")) : 0;
+    if (env_bm != 64 && (env_bm == 128 || tiles128 >= aeth_num_cus())) {
         dim3 grid((unsigned)aeth_cdiv(w->n, GEMM_BN), (unsigned)aeth_cdiv(m, 128));
-        hipLaunchKernelGGL(k_gemm_q4k<128>, grid, dim3(256), 0, s, G);
+        if (env_d == 1) hipLaunchKernelGGL((k_gemm_q4k<128, 1>), grid, dim3(256), 0, s, G);
+        else hipLaunchKernelGGL((k_gemm_q4k<128, 2>), grid, dim3(256), 0, s, G);
     } else {
         dim3 grid((unsigned)aeth_cdiv(w->n, GEMM_BN), (unsigned)aeth_cdiv(m, 64));
-        hipLaunchKernelGGL(k_gemm_q4k<64>, grid, dim3(256), 0, s, G);
+        if (env_d == 1) hipLaunchKernelGGL((k_gemm_q4k<64, 1>), grid, dim3(256), 0, s, G);
+        else if (env_d == 2) hipLaunchKernelGGL((k_gemm_q4k<64, 2>), grid, dim3(256), 0, s, G);
+        else hipLaunchKernelGGL((k_gemm_q4k<64, 4>), grid, dim3(256), 0, s, G);
     }
     AETH_LAUNCH_CHECK();
     return AETH_OK;

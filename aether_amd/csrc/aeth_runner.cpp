@@ -43,6 +43,11 @@ struct aeth_runner {
     int* tok_out = nullptr;  // unused slot kept for the release list
     int fill = 0;           // host mirror of the cache fill
     hipGraphExec_t graph = nullptr;
+    // batched prefill buffers (grow-only): rows of x, normed x, q|k|v, attention
+    // output, interleaved gate|up, SiLU product; prompt token ids
+    float *p_x = nullptr, *p_n = nullptr, *p_qkv = nullptr, *p_att = nullptr, *p_gu = nullptr, *p_h = nullptr;
+    int* p_tok = nullptr;
+    int64_t p_cap = 0;
     // frame budget / partial decode (runner.rs:1201-1282, c_api.rs:313-355)
     float frame_budget_ms = 0.0f;
     bool partial_valid = false;
@@ -148,7 +153,8 @@ void runner_release(aeth_runner* r) {
     for (auto* w : r->wdown) aeth_weight_free(w);
     aeth_weight_free(r->lm_head);
     void* bufs[] = {r->norms, r->final_norm, r->emb, r->rope_sin, r->rope_cos, r->kv, r->x, r->normed, r->qkv,
-                    r->attn, r->gu, r->logits, r->attn_ws, r->am_ws, r->st, r->tok_out, r->amax};
+                    r->attn, r->gu, r->logits, r->attn_ws, r->am_ws, r->st, r->tok_out, r->amax,
+                    r->p_x, r->p_n, r->p_qkv, r->p_att, r->p_gu, r->p_h, r->p_tok};
     for (void* b : bufs)
         if (b) hipFree(b);
     if (r->stream) hipStreamDestroy(r->stream);
@@ -208,6 +214,84 @@ int enqueue_step(aeth_runner* r) {
     if (rc) return rc;
     if ((rc = enqueue_layers(r, 0, r->cfg.num_layers))) return rc;
     return enqueue_head(r);
+}
+
+int set_state(aeth_runner* r, int token, int pos);
+
+// Batched prefill (forward_batch, runner.rs:833-993; LlamaRunner::prefill :695-704):
+// tokens at positions 0..n-1, K/V at cache slots 0..n-1, per layer
+//   xn = rmsnorm(x, attn_norm); qkv = xn · Wqkvᵀ (GEMM, m = n); RoPE + cache write;
+//   att = causal attention; x += att · Woᵀ; xn = rmsnorm(x, ffn_norm);
+//   [g|u] = xn · Wguᵀ; h = g·σ(g)·u; x += h · Wdownᵀ
+// then the decode head on the last row (final norm, LM head, greedy argmax).
+int ensure_prefill_buffers(aeth_runner* r, int64_t n) {
+    if (n <= r->p_cap) return AETH_OK;
+    const aeth_llama_config& c = r->cfg;
+    const int64_t d = c.d_model, qd = (int64_t)c.num_heads * c.head_dim, kvd = kKvd(c), dff = c.d_ff;
+    AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
+    float** bufs[] = {&r->p_x, &r->p_n, &r->p_qkv, &r->p_att, &r->p_gu, &r->p_h};
+    const int64_t sizes[] = {n * d, n * (d > dff ? d : dff), n * (qd + 2 * kvd), n * qd, n * 2 * dff, n * dff};
+    for (int i = 0; i < 6; i++) {
+        if (*bufs[i]) AETH_HIP_CHECK(hipFree(*bufs[i]));
+        *bufs[i] = nullptr;
+    }
+    if (r->p_tok) AETH_HIP_CHECK(hipFree(r->p_tok));
+    r->p_tok = nullptr;
+    r->p_cap = 0;
+    for (int i = 0; i < 6; i++) {
+        int rc = dmalloc(bufs[i], sizes[i]);
+        if (rc) return rc;
+    }
+    int rc = dmalloc(&r->p_tok, n);
+    if (rc) return rc;
+    r->p_cap = n;
+    return AETH_OK;
+}
+
+int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, float* logits, int32_t* next_token) {
+    const aeth_llama_config& c = r->cfg;
+    if (!tokens || n <= 0) return aeth_set_error(AETH_EINVAL, "prefill: empty prompt");
+    if (n > c.max_seq_len)
+        return aeth_set_error(AETH_EINVAL, "prefill: %d tokens exceed max_seq %d", n, c.max_seq_len);
+    for (int32_t i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= c.vocab_size)
+            return aeth_set_error(AETH_EINVAL, "prefill: token %d out of range [0, %d)", tokens[i], c.vocab_size);
+    int rc = ensure_prefill_buffers(r, n);
+    if (rc) return rc;
+    r->partial_valid = false;
+    hipStream_t s = r->stream;
+    const int64_t d = c.d_model, hd = c.head_dim, nh = c.num_heads, nkv = c.num_kv_heads, dff = c.d_ff;
+    AETH_HIP_CHECK(hipMemcpyAsync(r->p_tok, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, s));
+    if ((rc = aeth_embed_rows_launch(r->emb, r->p_tok, n, d, r->p_x, s))) return rc;
+    for (int l = 0; l < c.num_layers; l++) {
+        float* lkv = r->kv + (int64_t)l * kv_layer_floats(c);
+        if ((rc = aeth_rmsnorm_launch(r->p_x, r->norms + (int64_t)l * 2 * d, n, d, c.rms_norm_eps, r->p_n, s)))
+            return rc;
+        if ((rc = aeth_qmatmul(r->wqkv[l], r->p_n, n, r->p_qkv, 0, s))) return rc;
+        if ((rc = aeth_prefill_rope_kv_launch(r->p_qkv, n, nh, nkv, hd, r->rope_sin, r->rope_cos, c.max_seq_len,
+                                              lkv, s)))
+            return rc;
+        if ((rc = aeth_attn_prefill_launch(r->p_qkv, lkv, n, nh, nkv, hd, c.max_seq_len, r->p_att, s))) return rc;
+        if ((rc = aeth_qmatmul(r->wo[l], r->p_att, n, r->p_x, AETH_MM_ACCUMULATE, s))) return rc;
+        if ((rc = aeth_rmsnorm_launch(r->p_x, r->norms + (int64_t)l * 2 * d + d, n, d, c.rms_norm_eps, r->p_n, s)))
+            return rc;
+        if ((rc = aeth_qmatmul(r->wgu[l], r->p_n, n, r->p_gu, 0, s))) return rc;
+        if ((rc = aeth_silu_pairs_launch(r->p_gu, n * dff, r->p_h, s))) return rc;
+        if ((rc = aeth_qmatmul(r->wdown[l], r->p_h, n, r->p_x, AETH_MM_ACCUMULATE, s))) return rc;
+    }
+    // head on the last row; the state update then leaves pos = fill = n
+    AETH_HIP_CHECK(hipMemcpyAsync(r->x, r->p_x + (int64_t)(n - 1) * d, sizeof(float) * d, hipMemcpyDeviceToDevice, s));
+    r->fill = n - 1;
+    if ((rc = set_state(r, tokens[n - 1], n - 1))) return rc;
+    if ((rc = enqueue_head(r))) return rc;
+    if (logits)
+        AETH_HIP_CHECK(hipMemcpyAsync(logits, r->logits, sizeof(float) * c.vocab_size, hipMemcpyDeviceToHost, s));
+    int tok = 0;
+    AETH_HIP_CHECK(hipMemcpyAsync(&tok, r->st + 3, sizeof(int), hipMemcpyDeviceToHost, s));
+    AETH_HIP_CHECK(hipStreamSynchronize(s));
+    r->fill = n;
+    if (next_token) *next_token = tok;
+    return AETH_OK;
 }
 
 int set_state(aeth_runner* r, int token, int pos) {
@@ -431,6 +515,13 @@ extern "C" AETH_API int aeth_runner_decode(aeth_runner* r, int32_t token, int32_
     return runner_decode_locked(r, token, pos, logits, next_token);
 }
 
+extern "C" AETH_API int aeth_runner_prefill(aeth_runner* r, const int32_t* tokens, int32_t n, float* logits,
+                                            int32_t* next_token) {
+    if (!r) return aeth_set_error(AETH_EINVAL, "aeth_runner_prefill: NULL runner");
+    std::lock_guard<std::mutex> lk(r->mu);
+    return runner_prefill_locked(r, tokens, n, logits, next_token);
+}
+
 extern "C" AETH_API int aeth_runner_generate(aeth_runner* r, int32_t token, int32_t pos, int32_t n_steps,
                                              int32_t* tokens, int use_graph) {
     if (!r || n_steps < 0 || (n_steps > 0 && !tokens))
@@ -582,8 +673,8 @@ extern "C" AETHER_API void aether_free_string(char* s) { free(s); }
 extern "C" AETHER_API void aether_free_tokens(int* t) { free(t); }
 
 // aether_prefill (c_api.rs:257-278 → LlamaRunner::prefill, runner.rs:695):
-// the cache restarts at 0 and token i is placed at position i; the logits
-// of the last token are returned.
+// the batched device prefill; token i at position i / cache slot i, the
+// logits of the last token are returned.
 extern "C" AETHER_API int aether_prefill(aether_model* m, const int* tokens, int n_tokens, float* logits_out) {
     if (!m || !tokens || n_tokens <= 0 || !logits_out) return AETHER_ERR;
     aeth_runner* r = m->runner;
@@ -592,11 +683,8 @@ extern "C" AETHER_API int aether_prefill(aether_model* m, const int* tokens, int
         aeth_set_error(AETH_EINVAL, "prefill: %d tokens exceed max_seq %d", n_tokens, r->cfg.max_seq_len);
         return AETHER_ERR;
     }
-    r->fill = 0;
-    for (int i = 0; i < n_tokens; i++) {
-        if (runner_decode_locked(r, tokens[i], i, i == n_tokens - 1 ? logits_out : nullptr, nullptr)) return AETHER_ERR;
-    }
-    return AETHER_OK;
+    return runner_prefill_locked(r, (const int32_t*)tokens, n_tokens, logits_out, nullptr) == AETH_OK ? AETHER_OK
+                                                                                                : AETHER_ERR;
 }
 
 extern "C" AETHER_API int aether_decode(aether_model* m, int token, int pos, float* logits_out) {

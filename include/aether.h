@@ -11,8 +11,8 @@
  *     aether_model_from_runner — no counterpart in the reference.
  *   - aether_encode / aether_decode_token: no tokenizer (NULL).
  *   - aether_sample: greedy only (temperature <= 1e-6 or top_p <= 1e-6).
- *   - aether_prefill runs the prompt token by token on the decode path
- *     (positions 0..n-1, cache restarted), returning the last logits.
+ *   - aether_prefill runs the batched device prefill (aeth_runner_prefill:
+ *     positions 0..n-1, cache slots 0..n-1), returning the last logits.
  */
 #ifndef AETHER_H
 #define AETHER_H

@@ -176,6 +176,14 @@ AETH_API int aeth_runner_seq_len(const aeth_runner* r);
  * embedding → L layers → final norm → LM head. logits (host, vocab floats)
  * may be NULL; next_token (host) receives the greedy argmax if non-NULL. */
 AETH_API int aeth_runner_decode(aeth_runner* r, int32_t token, int32_t pos, float* logits, int32_t* next_token);
+/* Batched prefill (LlamaRunner::prefill, runner.rs:695-704 → forward_batch,
+ * :833-993): the n prompt tokens (host) are placed at positions 0..n-1 in
+ * one pass (GEMM projections, causal attention_batch :1809-1883), K/V written
+ * to cache slots 0..n-1, and the cache fill becomes n. logits (host, vocab
+ * floats) receive the last token's logits and next_token its greedy argmax;
+ * either may be NULL. 1 <= n <= max_seq_len. */
+AETH_API int aeth_runner_prefill(aeth_runner* r, const int32_t* tokens, int32_t n, float* logits,
+                                 int32_t* next_token);
 /* Greedy decode of n_steps tokens starting from `token` at `pos`; tokens
  * (host, n_steps) receive each step's argmax (fed back as the next input).
  * Uses a captured HIP graph per step when use_graph != 0. */

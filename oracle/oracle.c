@@ -812,11 +812,15 @@ typedef struct {
 
 enum { ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14 };
 
-/* quantized_matmul_impl's x86 route (dispatch.rs:98-135 → avx2_dispatch.rs). */
+/* quantized_matmul_impl's x86 route (dispatch.rs:98-135 → avx2_dispatch.rs), m rows. */
+static void orc_qmatmul_m(int dtype, const float* a, size_t m, const uint8_t* w, size_t n, size_t k, float* c) {
+    if (dtype == ORC_Q4_K) orc_avx2_matmul_q4_k(a, w, m, n, k, c);
+    else if (dtype == ORC_Q6_K) orc_avx2_matmul_q6_k(a, w, m, n, k, c);
+    else orc_scalar_matmul_q8_0(a, w, n * ((k + 31) / 32) * 34, m, n, k, c);
+}
+
 static void orc_qmatmul(int dtype, const float* a, const uint8_t* w, size_t n, size_t k, float* c) {
-    if (dtype == ORC_Q4_K) orc_avx2_matmul_q4_k(a, w, 1, n, k, c);
-    else if (dtype == ORC_Q6_K) orc_avx2_matmul_q6_k(a, w, 1, n, k, c);
-    else orc_scalar_matmul_q8_0(a, w, n * ((k + 31) / 32) * 34, 1, n, k, c);
+    orc_qmatmul_m(dtype, a, 1, w, n, k, c);
 }
 
 /* weights[l*7 + {0..6}] = q,k,v,o,gate,up,down raw row-major [out][in] blocks;
@@ -885,5 +889,109 @@ ORC_API int orc_decode_step(const orc_llama_cfg* cfg, const float* x_embed, int3
     orc_qmatmul(lm_dtype, normed, lm_head, (size_t)cfg->vocab, d, logits);
     free(x); free(normed); free(q); free(kk); free(vv); free(attn); free(proj);
     free(gate); free(up); free(scores);
+    return 0;
+}
+
+/* ── Batched prefill: forward_batch, CPU path (runner.rs:833-993) ─────────
+ * All n prompt tokens in one pass: token i at position i, its K/V at cache
+ * slot i (the cache is written from slot 0; LlamaRunner::prefill then sets
+ * seq_len = n, runner.rs:695-704), batched matmuls with m = n, causal
+ * attention_batch (runner.rs:1809-1883, no sliding window), logits of the
+ * last token only. x_embeds holds the n embedding rows. */
+static void orc_attention_batch(const float* q, const float* k, const float* v, size_t n, size_t nh, size_t nkv,
+                                size_t hd, float* out, float* scores) {
+    float scale = 1.0f / sqrtf((float)hd);
+    size_t groups = nh / nkv, q_stride = nh * hd, kv_stride = nkv * hd;
+    for (size_t h = 0; h < nh; h++) {
+        size_t kvh = h / groups;
+        for (size_t i = 0; i < n; i++) {
+            const float* qr = q + i * q_stride + h * hd;
+            float* row = scores + i * n;
+            for (size_t j = 0; j <= i; j++) {
+                const float* kr = k + j * kv_stride + kvh * hd;
+                float dot = 0.0f;
+                for (size_t e = 0; e < hd; e++) dot += qr[e] * kr[e];
+                row[j] = dot * scale;
+            }
+            for (size_t j = i + 1; j < n; j++) row[j] = -INFINITY;
+        }
+        for (size_t i = 0; i < n; i++) {
+            float* row = scores + i * n;
+            float mx = -INFINITY;
+            for (size_t j = 0; j < n; j++) mx = fmaxf(mx, row[j]);
+            float sum = 0.0f;
+            for (size_t j = 0; j < n; j++)
+                if (row[j] > -INFINITY / 2.0f) {
+                    row[j] = expf(row[j] - mx);
+                    sum += row[j];
+                }
+            for (size_t j = 0; j < n; j++)
+                if (row[j] > 0.0f) row[j] /= sum;
+        }
+        for (size_t i = 0; i < n; i++) {
+            const float* row = scores + i * n;
+            float* o = out + i * q_stride + h * hd;
+            for (size_t e = 0; e < hd; e++) o[e] = 0.0f;
+            for (size_t j = 0; j <= i; j++) {
+                float w = row[j];
+                if (w <= 0.0f) continue;
+                const float* vr = v + j * kv_stride + kvh * hd;
+                for (size_t e = 0; e < hd; e++) o[e] += w * vr[e];
+            }
+        }
+    }
+}
+
+ORC_API int orc_forward_batch(const orc_llama_cfg* cfg, const float* x_embeds, int32_t n_tokens,
+                              const uint8_t* const* weights, const int32_t* wdtype, const float* const* norms,
+                              const float* final_norm, const uint8_t* lm_head, int32_t lm_dtype,
+                              const float* rope_sin, const float* rope_cos, float* kv, float* logits) {
+    size_t d = (size_t)cfg->d_model, hd = (size_t)cfg->head_dim, nh = (size_t)cfg->n_heads;
+    size_t nkv = (size_t)cfg->n_kv_heads, dff = (size_t)cfg->d_ff, ms = (size_t)cfg->max_seq;
+    size_t kvd = nkv * hd, qd = nh * hd, n = (size_t)n_tokens;
+    if (n_tokens <= 0 || n > ms) return -2; /* an empty prompt is an error; slots must fit */
+    float* X = malloc(n * d * 4);
+    float* N = malloc(n * d * 4);
+    float* Q = malloc(n * qd * 4);
+    float* K = malloc(n * kvd * 4);
+    float* V = malloc(n * kvd * 4);
+    float* A = malloc(n * qd * 4);
+    float* P = malloc(n * d * 4);
+    float* G = malloc(n * dff * 4);
+    float* U = malloc(n * dff * 4);
+    float* S = malloc(n * n * 4);
+    if (!X || !N || !Q || !K || !V || !A || !P || !G || !U || !S) return -1;
+    memcpy(X, x_embeds, n * d * 4);
+    size_t head_stride = ms * hd, layer_stride = 2 * nkv * head_stride;
+    for (int32_t l = 0; l < cfg->n_layers; l++) {
+        const uint8_t* const* W = weights + (size_t)l * 7;
+        const int32_t* T = wdtype + (size_t)l * 7;
+        for (size_t i = 0; i < n; i++) orc_rmsnorm(X + i * d, norms[l * 2], d, cfg->eps, N + i * d);
+        orc_qmatmul_m(T[0], N, n, W[0], qd, d, Q);
+        orc_qmatmul_m(T[1], N, n, W[1], kvd, d, K);
+        orc_qmatmul_m(T[2], N, n, W[2], kvd, d, V);
+        for (size_t i = 0; i < n; i++) {
+            orc_apply_rope(Q + i * qd, nh, hd, i, rope_sin, rope_cos, ms);
+            orc_apply_rope(K + i * kvd, nkv, hd, i, rope_sin, rope_cos, ms);
+        }
+        float* lb = kv + (size_t)l * layer_stride;
+        for (size_t i = 0; i < n; i++)
+            for (size_t h = 0; h < nkv; h++) {
+                memcpy(lb + h * head_stride + i * hd, K + (i * nkv + h) * hd, hd * 4);
+                memcpy(lb + nkv * head_stride + h * head_stride + i * hd, V + (i * nkv + h) * hd, hd * 4);
+            }
+        orc_attention_batch(Q, K, V, n, nh, nkv, hd, A, S);
+        orc_qmatmul_m(T[3], A, n, W[3], d, qd, P);
+        for (size_t i = 0; i < n * d; i++) X[i] += P[i];
+        for (size_t i = 0; i < n; i++) orc_rmsnorm(X + i * d, norms[l * 2 + 1], d, cfg->eps, N + i * d);
+        orc_qmatmul_m(T[4], N, n, W[4], dff, d, G);
+        orc_qmatmul_m(T[5], N, n, W[5], dff, d, U);
+        for (size_t i = 0; i < n * dff; i++) G[i] = G[i] * (1.0f / (1.0f + expf(-G[i]))) * U[i];
+        orc_qmatmul_m(T[6], G, n, W[6], d, dff, P);
+        for (size_t i = 0; i < n * d; i++) X[i] += P[i];
+    }
+    orc_rmsnorm(X + (n - 1) * d, final_norm, d, cfg->eps, N);
+    orc_qmatmul(lm_dtype, N, lm_head, (size_t)cfg->vocab, d, logits);
+    free(X); free(N); free(Q); free(K); free(V); free(A); free(P); free(G); free(U); free(S);
     return 0;
 }

@@ -46,6 +46,7 @@ def lib():
         L.orc_argmax.restype = ctypes.c_int32
         L.orc_argmax.argtypes = [f32p, sz]
         L.orc_decode_step.restype = ctypes.c_int
+        L.orc_forward_batch.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -269,3 +270,46 @@ def decode_step(cfg, x_embed, pos, layer_weights, layer_dtypes, norms, final_nor
     if rc_ != 0:
         raise RuntimeError("orc_decode_step failed: %d" % rc_)
     return logits, sl.value
+
+
+def _model_ptrs(cfg, layer_weights, layer_dtypes, norms):
+    nl = cfg.n_layers
+    keep = []
+    wp = (ctypes.POINTER(ctypes.c_uint8) * (nl * 7))()
+    wt = (ctypes.c_int32 * (nl * 7))()
+    for l in range(nl):
+        for j in range(7):
+            arr = _u8(layer_weights[l][j])
+            keep.append(arr)
+            wp[l * 7 + j] = _p(arr, ctypes.c_uint8)
+            wt[l * 7 + j] = layer_dtypes[l][j] if isinstance(layer_dtypes[l], (list, tuple)) else layer_dtypes[j]
+    npp = (ctypes.POINTER(ctypes.c_float) * (nl * 2))()
+    for l in range(nl):
+        for j in range(2):
+            arr = _f32(norms[l][j])
+            keep.append(arr)
+            npp[l * 2 + j] = _p(arr, ctypes.c_float)
+    return keep, wp, wt, npp
+
+
+def forward_batch(cfg, x_embeds, layer_weights, layer_dtypes, norms, final_norm, lm_head, lm_dtype,
+                  rope_sin, rope_cos, kv):
+    """Batched prefill (forward_batch, runner.rs:833-993): x_embeds [n][d] are
+    the prompt's embedding rows at positions 0..n-1; kv is written at slots
+    0..n-1 in place. Returns the last token's logits."""
+    L = lib()
+    keep, wp, wt, npp = _model_ptrs(cfg, layer_weights, layer_dtypes, norms)
+    x = _f32(x_embeds)
+    n = x.size // cfg.d_model
+    fn_, lm = _f32(final_norm), _u8(lm_head)
+    rs, rc = _f32(rope_sin), _f32(rope_cos)
+    assert kv.dtype == np.float32 and kv.flags.c_contiguous
+    logits = np.empty(cfg.vocab, dtype=np.float32)
+    rc_ = L.orc_forward_batch(ctypes.byref(cfg), _p(x, ctypes.c_float), ctypes.c_int32(n), wp, wt, npp,
+                              _p(fn_, ctypes.c_float), _p(lm, ctypes.c_uint8), ctypes.c_int32(lm_dtype),
+                              _p(rs, ctypes.c_float), _p(rc, ctypes.c_float), _p(kv, ctypes.c_float),
+                              _p(logits, ctypes.c_float))
+    if rc_ != 0:
+        raise RuntimeError("orc_forward_batch failed: %d" % rc_)
+    del keep
+    return logits

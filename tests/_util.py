@@ -56,3 +56,19 @@ def assert_close(g, r, tol=1e-3, cos_min=0.9999, what=""):
     den = np.sqrt((g * g).sum(axis=1) * (r * r).sum(axis=1))
     cos = np.where(den > 0, num / np.where(den > 0, den, 1), 1.0)
     assert (cos > cos_min).all(), "%s: row cosine %r <= %r" % (what, cos.min(), cos_min)
+
+
+def assert_close_rows(g, r, tol=1e-3, what=""):
+    """For intermediate state (the KV cache): per row, |g-r| <= tol·max(1, max|r_row|).
+    An entry's float error scales with the magnitudes summed into it, i.e. with
+    its row, so small entries of large rows get the row's absolute bar; the
+    element-wise output bar (assert_close) stays on logits."""
+    g = np.atleast_2d(np.asarray(g, dtype=np.float64))
+    r = np.atleast_2d(np.asarray(r, dtype=np.float64))
+    assert g.shape == r.shape, (g.shape, r.shape)
+    scale = np.maximum(1.0, np.abs(r).max(axis=1, keepdims=True))
+    bad = np.abs(g - r) > tol * scale
+    if bad.any():
+        i = tuple(np.argwhere(bad)[0])
+        raise AssertionError("%s: %d/%d elements out of row tolerance; first at %s: got %r ref %r (row scale %r)" %
+                             (what, bad.sum(), bad.size, i, g[i], r[i], scale[i[0], 0]))

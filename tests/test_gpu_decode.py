@@ -8,7 +8,7 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import Q4_K, Q6_K, Q8_0, assert_close, weight
+from tests._util import Q4_K, Q6_K, Q8_0, assert_close, assert_close_rows, weight
 
 pytestmark = pytest.mark.gpu
 
@@ -135,8 +135,7 @@ def build_tiny(seed=1, lm_dtype=Q6_K, layer_dtype=Q4_K):
     return dict(layers=layers, norms=norms, final=final, lm=lm, emb=emb, lm_dtype=lm_dtype, layer_dtype=layer_dtype)
 
 
-def make_runner(m):
-    c = TINY
+def make_runner(m, c=TINY):
     cfg = A.LlamaConfig(**c)
     nl = c["num_layers"]
     wp = (ctypes.c_void_p * (nl * 7))(*[m["layers"][l][j].ctypes.data for l in range(nl) for j in range(7)])
@@ -148,8 +147,7 @@ def make_runner(m):
     return r
 
 
-def oracle_cfg():
-    c = TINY
+def oracle_cfg(c=TINY):
     return O.LlamaCfg(c["vocab_size"], c["d_model"], c["num_layers"], c["num_heads"], c["num_kv_heads"], c["head_dim"],
                       c["d_ff"], c["max_seq_len"], c["rope_base"], c["rms_norm_eps"])
 
@@ -180,7 +178,61 @@ def test_runner_decode_matches_oracle(gpu, layer_dtype):
         fl = ctypes.c_int32()
         A.check(L.aeth_runner_kv_to_host(r, kv_dev.ctypes.data, ctypes.byref(fl)))
         assert fl.value == 6
-        assert_close(kv_dev.reshape(-1, c["head_dim"]), kv.reshape(-1, c["head_dim"]), cos_min=0.0)
+        assert_close_rows(kv_dev.reshape(-1, c["head_dim"]), kv.reshape(-1, c["head_dim"]), what="kv")
+    finally:
+        L.aeth_runner_free(r)
+
+
+# Batched prefill (forward_batch) against the oracle's restatement: one query /
+# key block (37), a full cache (64), a single token, and several ragged blocks
+# with the GEMM path (150 of 192); GEMM for Q4_K, row-batched GEMV otherwise.
+@pytest.mark.parametrize("layer_dtype,n,max_seq", [(Q4_K, 37, 64), (Q8_0, 64, 64), (Q6_K, 1, 64), (Q4_K, 150, 192)])
+def test_runner_prefill_matches_oracle(gpu, layer_dtype, n, max_seq):
+    c = dict(TINY, max_seq_len=max_seq)
+    m = build_tiny(seed=7, layer_dtype=layer_dtype)
+    r = make_runner(m, c)
+    L = A.lib()
+    ocfg = oracle_cfg(c)
+    s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
+    kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), dtype=np.float32)
+    toks = np.random.default_rng(n).integers(0, c["vocab_size"], n).astype(np.int32)
+    try:
+        logits = np.empty(c["vocab_size"], dtype=np.float32)
+        nxt = ctypes.c_int32()
+        A.check(L.aeth_runner_prefill(r, toks.ctypes.data, n, logits.ctypes.data, ctypes.byref(nxt)), "prefill")
+        ref = O.forward_batch(ocfg, m["emb"][toks], m["layers"], [layer_dtype] * 7, m["norms"], m["final"], m["lm"],
+                              m["lm_dtype"], s, co, kv)
+        assert_close(logits, ref, what="prefill n=%d" % n)
+        assert nxt.value == O.argmax(logits)
+        assert L.aeth_runner_seq_len(r) == n
+        kv_dev = np.empty_like(kv)
+        fl = ctypes.c_int32()
+        A.check(L.aeth_runner_kv_to_host(r, kv_dev.ctypes.data, ctypes.byref(fl)))
+        assert fl.value == n
+        assert_close_rows(kv_dev[:, :, :, :n].reshape(-1, c["head_dim"]), kv[:, :, :, :n].reshape(-1, c["head_dim"]),
+                          what="kv after prefill")
+        assert not kv_dev[:, :, :, n:].any()
+        if n < max_seq:  # decoding continues from the prefilled cache
+            tok = O.argmax(ref)
+            A.check(L.aeth_runner_decode(r, tok, n, logits.ctypes.data, None), "decode after prefill")
+            ref2, fill = O.decode_step(ocfg, m["emb"][tok], n, m["layers"], [layer_dtype] * 7, m["norms"], m["final"],
+                                       m["lm"], m["lm_dtype"], s, co, kv, n)
+            assert fill == n + 1 and L.aeth_runner_seq_len(r) == n + 1
+            assert_close(logits, ref2, what="decode after prefill")
+    finally:
+        L.aeth_runner_free(r)
+
+
+def test_runner_prefill_bad_arguments(gpu):
+    m = build_tiny(seed=8)
+    r = make_runner(m)
+    L = A.lib()
+    try:
+        toks = np.zeros(TINY["max_seq_len"] + 1, dtype=np.int32)
+        assert L.aeth_runner_prefill(r, toks.ctypes.data, 0, None, None) == -1
+        assert L.aeth_runner_prefill(r, toks.ctypes.data, TINY["max_seq_len"] + 1, None, None) == -1
+        toks[3] = TINY["vocab_size"]
+        assert L.aeth_runner_prefill(r, toks.ctypes.data, 5, None, None) == -1
     finally:
         L.aeth_runner_free(r)
 

@@ -373,6 +373,45 @@ def test_decode_step_matches_f64_composition():
     np.testing.assert_allclose(kv[0, 0, :, fill], k_, rtol=1e-4, atol=1e-4)
 
 
+def test_forward_batch_matches_sequential_decode_steps():
+    """Batched prefill (forward_batch + attention_batch) of a 2-layer toy model
+    with mixed dtypes equals the prompt fed through the pinned decode step one
+    token at a time from an empty cache: same logits of the last token (up to
+    f32 summation order) and the same K/V in slots 0..n-1. Also a prompt of
+    one token, and the empty prompt is refused."""
+    rng = np.random.default_rng(11)
+    vocab, d, nh, nkv, hd, dff, ms = 96, 256, 4, 2, 64, 512, 24
+    nl = 2
+    cfg = O.LlamaCfg(vocab, d, nl, nh, nkv, hd, dff, ms, 10000.0, 1e-5)
+    shapes = [(nh * hd, d), (nkv * hd, d), (nkv * hd, d), (d, nh * hd), (dff, d), (dff, d), (d, dff)]
+    dts = [[Q4_K] * 7, [Q8_0, Q8_0, Q8_0, Q6_K, Q4_K, Q4_K, Q6_K]]
+    W = []
+    for l in range(nl):
+        row = []
+        for j, (n, k) in enumerate(shapes):
+            be, _ = GEOM[dts[l][j]]
+            row.append(synth_blocks(dts[l][j], n * k // be, 100 * l + j))
+        W.append(row)
+    norms = [[(1 + 0.02 * rng.standard_normal(d)).astype(np.float32) for _ in range(2)] for _ in range(nl)]
+    final = (1 + 0.02 * rng.standard_normal(d)).astype(np.float32)
+    lm = synth_blocks(Q6_K, vocab * d // 256, 99)
+    s, c = O.precompute_rope(ms, hd, 10000.0)
+    for n in (9, 1):
+        X = rng.standard_normal((n, d)).astype(np.float32)
+        kvb = np.zeros((nl, 2, nkv, ms, hd), np.float32)
+        lb = O.forward_batch(cfg, X, W, dts, norms, final, lm, Q6_K, s, c, kvb)
+        kvs = np.zeros_like(kvb)
+        fill = 0
+        for i in range(n):
+            ls, fill = O.decode_step(cfg, X[i], i, W, dts, norms, final, lm, Q6_K, s, c, kvs, fill)
+        assert fill == n
+        np.testing.assert_allclose(lb, ls, rtol=1e-4, atol=1e-4 * np.abs(ls).max())
+        np.testing.assert_allclose(kvb[:, :, :, :n], kvs[:, :, :, :n], rtol=1e-4, atol=1e-4)
+        assert not kvb[:, :, :, n:].any()
+    with pytest.raises(RuntimeError):
+        O.forward_batch(cfg, np.zeros((0, d), np.float32), W, dts, norms, final, lm, Q6_K, s, c, kvb)
+
+
 # ── frozen oracle vectors ────────────────────────────────────────────────
 
 def test_golden_fixture():
