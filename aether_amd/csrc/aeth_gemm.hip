@@ -301,19 +301,21 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     AETH_LAUNCH_CHECK();
     GemmArgs G{Ah, Al, Sh, Sl, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, d_c,
                (flags & AETH_MM_ACCUMULATE) ? 1 : 0};
-    const int64_t tiles128 = aeth_cdiv(w->n, GEMM_BN) * aeth_cdiv(m, 128);
-    // tuning override, read once: AETH_GEMM_D (prefetch distance 1, 2 or 4)
+    // tuning overrides, read once: AETH_GEMM_D (prefetch distance 1, 2 or 4), AETH_GEMM_BM (64 | 128)
     static const int env_d = getenv("AETH_GEMM_D") ? atoi(getenv("AETH_GEMM_D")) : 0;
     static const int env_bm = getenv("AETH_GEMM_BM") ? atoi(getenv("AETH_GEMM_BM")) : 0;
-    if (env_bm != 64 && (env_bm == 128 || tiles128 >= aeth_num_cus())) {
+    // measured at m = 512, n = 4096 / 14336: BM = 64 with a one-step prefetch is
+    // best (two workgroups per CU where the grid allows); AETH_GEMM_BM=128 forces
+    // the 128-row tile
+    if (env_bm == 128) {
         dim3 grid((unsigned)aeth_cdiv(w->n, GEMM_BN), (unsigned)aeth_cdiv(m, 128));
-        if (env_d == 1) hipLaunchKernelGGL((k_gemm_q4k<128, 1>), grid, dim3(256), 0, s, G);
-        else hipLaunchKernelGGL((k_gemm_q4k<128, 2>), grid, dim3(256), 0, s, G);
+        if (env_d == 2) hipLaunchKernelGGL((k_gemm_q4k<128, 2>), grid, dim3(256), 0, s, G);
+        else hipLaunchKernelGGL((k_gemm_q4k<128, 1>), grid, dim3(256), 0, s, G);
     } else {
         dim3 grid((unsigned)aeth_cdiv(w->n, GEMM_BN), (unsigned)aeth_cdiv(m, 64));
-        if (env_d == 1) hipLaunchKernelGGL((k_gemm_q4k<64, 1>), grid, dim3(256), 0, s, G);
-        else if (env_d == 2) hipLaunchKernelGGL((k_gemm_q4k<64, 2>), grid, dim3(256), 0, s, G);
-        else hipLaunchKernelGGL((k_gemm_q4k<64, 4>), grid, dim3(256), 0, s, G);
+        if (env_d == 2) hipLaunchKernelGGL((k_gemm_q4k<64, 2>), grid, dim3(256), 0, s, G);
+        else if (env_d == 4) hipLaunchKernelGGL((k_gemm_q4k<64, 4>), grid, dim3(256), 0, s, G);
+        else hipLaunchKernelGGL((k_gemm_q4k<64, 1>), grid, dim3(256), 0, s, G);
     }
     AETH_LAUNCH_CHECK();
     return AETH_OK;

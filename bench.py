@@ -107,7 +107,7 @@ def bench_gemm(torch, A, n, k, m, steps, warmup, seed=0xAE7E43):
     return {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
 
 
-def bench_decode(torch, A, n_tokens=128, prefilled=2048):
+def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512):
     L = A.lib()
     cfg = A.LlamaConfig(vocab_size=128256, d_model=4096, num_layers=32, num_heads=32, num_kv_heads=8, head_dim=128,
                         d_ff=14336, max_seq_len=4096, rope_base=500000.0, rms_norm_eps=1e-5)
@@ -124,14 +124,25 @@ def bench_decode(torch, A, n_tokens=128, prefilled=2048):
     t0 = time.perf_counter()
     A.check(L.aeth_runner_generate(r, 1, prefilled, n_tokens, toks, 1), "generate")
     dt_s = time.perf_counter() - t0
+    # batched prefill of a 512-token prompt (forward_batch): one warm-up, then timed
+    prompt = (ctypes.c_int32 * prefill_tokens)(*[(7919 * i + 13) % 128256 for i in range(prefill_tokens)])
+    A.check(L.aeth_runner_prefill(r, prompt, prefill_tokens, None, None), "prefill warmup")
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        A.check(L.aeth_runner_prefill(r, prompt, prefill_tokens, None, None), "prefill")
+    pf_s = (time.perf_counter() - t0) / reps
     L.aeth_runner_free(r)
+    layer_weights = 4096 * 4096 * 2 + 1024 * 4096 * 2 + 14336 * 4096 * 3
+    pf_flops = 2.0 * prefill_tokens * 32 * layer_weights + 2.0 * 128256 * 4096
     # weight bytes + f32 KV read (avg over steps) + KV write, per step
     q4 = 32 * (4096 * 16 * 144 * 2 + 1024 * 16 * 144 * 2 + 14336 * 16 * 144 * 2 + 4096 * 56 * 144)
     q6 = 128256 * 16 * 210
     kv_avg = 32 * 2 * 8 * 128 * 4 * (prefilled + 1 + (n_tokens - 1) / 2.0)
     step_bytes = q4 + q6 + kv_avg + (32 * 2 + 1) * 4096 * 4
     return {"tok_s": n_tokens / dt_s, "ms_per_token": dt_s * 1e3 / n_tokens, "setup_s": setup_s,
-            "gbs": step_bytes * n_tokens / dt_s / 1e9, "step_bytes": step_bytes, "first_tokens": list(toks)[:8]}
+            "gbs": step_bytes * n_tokens / dt_s / 1e9, "step_bytes": step_bytes, "first_tokens": list(toks)[:8],
+            "prefill_tok_s": prefill_tokens / pf_s, "prefill_ms": pf_s * 1e3, "prefill_tflops": pf_flops / pf_s / 1e12}
 
 
 def measured_traffic():
@@ -228,6 +239,9 @@ def main():
                                   "GB/s": round(d["gbs"], 1), "frac_hbm": round(d["gbs"] / HBM_PEAK_GBS, 4),
                                   "tokens": 128, "prefilled": 2048, "first_tokens": d["first_tokens"]}
         print("[bench] decode 8B: %s" % extra["decode_8b_q4k"], file=sys.stderr, flush=True)
+        extra["prefill_8b_q4k_512"] = {"tok/s": round(d["prefill_tok_s"], 1), "ms": round(d["prefill_ms"], 2),
+                                       "TFLOP/s": round(d["prefill_tflops"], 2), "tokens": 512}
+        print("[bench] prefill 8B: %s" % extra["prefill_8b_q4k_512"], file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:
