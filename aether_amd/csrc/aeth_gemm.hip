@@ -266,6 +266,331 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs G) {
         }
 }
 
+// ── Ring-buffered variant (the default): A arrives as MFMA fragments, weights as
+// raw quants, both through a 3-stage LDS ring filled by global_load_lds_dwordx4
+// (lane i of a wave writes LDS bytes [16i, 16i+16) of the destination, from any
+// global address), so no VGPR staging and no LDS stores by the waves.
+// Workgroup tile 64 × 128, 4 waves of 32 × 64; one stage = 64 K-positions (a
+// quarter super-block): 16 A fragments (2 m-tiles × 4 k-slices × {hi, lo}),
+// 8 tiles × 512 B of quants, the super-block's headers. Each wave issues the
+// same 6 loads per stage, so a fixed vmcnt marks the arrival of a stage.
+#define G2_BM 64
+#define G2_BN 128
+#define G2_A 16384
+#define G2_B 4096
+#define G2_H 4096  // 2 KiB of headers per stage, each half loaded by two waves
+#define G2_STAGE (G2_A + G2_B + G2_H)
+#define G2_NST 3
+#define G2_LOADS 6
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// positions 1 and 2 of each group of 4 exchanged (an involution)
+__device__ __forceinline__ int perm4(int i) { return (i & ~3) | ((0x3120 >> (4 * (i & 3))) & 3); }
+
+// A (f32 [m][k]) → fragments: fragment (mt, ks, part) = 1 KiB at ((mt·nks + ks)·2 + part)·1024
+// bytes (nks = k/16); lane l holds row 32·mt + l%32 at k-positions 16·ks + 8·(l/32) + perm4(i),
+// i < 8, part 0 = hi, 1 = lo. Rows m..mp-1 are zero. Sh/Sl and escale as k_gemm_prep.
+__global__ void __launch_bounds__(256) k_gemm_prep_frag(const float* __restrict__ A, int m, int k,
+                                                        _Float16* __restrict__ frag, _Float16* __restrict__ Sh,
+                                                        _Float16* __restrict__ Sl, float* __restrict__ escale) {
+    __shared__ float red[4];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const bool live = r < m;
+    const float* a = A + (int64_t)min(r, m - 1) * k;
+    float mx = 0.0f;
+    for (int i = tid; i < k; i += 256) mx = fmaxf(mx, fabsf(a[i]));
+    mx = aeth_wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int E = 0;
+    if (mx > 0.0f && isfinite(mx)) (void)frexpf(mx, &E);
+    const int e = E > 14 ? E - 14 : 0;  // |A·2^-e| < 2^14
+    if (tid == 0) escale[r] = ldexpf(1.0f, e);
+    const int nks = k / 16, mt = r / 32, lr = r % 32;
+    // 8-element groups g; groups 4q..4q+3 form sub-block q (k is a multiple of 256,
+    // so every lane of a wave that enters an iteration has its whole aligned 4-group)
+    for (int g = tid; g < k / 8; g += 256) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = live ? a[8 * g + i] : 0.0f;
+        float fs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) fs += v[i];
+        half8_t hi, lo;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float x = ldexpf(v[perm4(i)], -e);
+            const _Float16 h = (_Float16)x;
+            hi[i] = h;
+            lo[i] = (_Float16)(x - (float)h);
+        }
+        _Float16* dst = frag + ((int64_t)(mt * nks + (g >> 1)) * 2) * 512 + (lr + 32 * (g & 1)) * 8;
+        *(half8_t*)dst = hi;
+        *(half8_t*)(dst + 512) = lo;
+        fs += __shfl_xor(fs, 1, 64);
+        fs += __shfl_xor(fs, 2, 64);
+        if ((g & 3) == 0) {
+            const float sv = ldexpf(fs, -(e + 5));
+            const _Float16 h = (_Float16)sv;
+            Sh[(int64_t)r * (k / 32) + g / 4] = h;
+            Sl[(int64_t)r * (k / 32) + g / 4] = (_Float16)(sv - (float)h);
+        }
+    }
+}
+
+struct Gemm2Args {
+    const uint8_t* frag;
+    const _Float16 *Sh, *Sl;
+    const float* escale;
+    const uint8_t* hdr;
+    const uint8_t* qs;
+    int m, n, k, nb, ntiles;
+    int gm, gn;  // 64-row and 128-column tiles of C
+    float* C;
+    int accumulate;
+};
+
+__device__ __forceinline__ void g_dma(const void* g, char* l) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 16, 0, 0);
+}
+
+// bytes (b0, b1, b2, b3) of w as fp16 pairs (b0, b1) and (b2, b3): (0x64 | b) is 1024 + b
+__device__ __forceinline__ void bytes_to_h2(uint32_t w, half2_t& p01, half2_t& p23) {
+    const half2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    p01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, 0x07010700u)) + k1024;
+    p23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, 0x07030702u)) + k1024;
+}
+
+__device__ __forceinline__ uint32_t pkfma(uint32_t q, half2_t s, half2_t z) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2_t, q), s, z));
+}
+
+// 8 quants (one nibble of 8 bytes) → the B operand, k-order [0, 2, 1, 3] per 4
+__device__ __forceinline__ half8_t dq8(uint2 raw, int nib, half2_t s, half2_t z) {
+    const uint32_t x = raw.x >> (4 * nib), y = raw.y >> (4 * nib);
+    const uint32_t q0 = pkfma((x & 0x000F000Fu) | 0x64006400u, s, z);
+    const uint32_t q1 = pkfma(((x >> 8) & 0x000F000Fu) | 0x64006400u, s, z);
+    const uint32_t q2 = pkfma((y & 0x000F000Fu) | 0x64006400u, s, z);
+    const uint32_t q3 = pkfma(((y >> 8) & 0x000F000Fu) | 0x64006400u, s, z);
+    return __builtin_bit_cast(half8_t, make_uint4(q0, q1, q2, q3));
+}
+
+// LDS reads issued as inline asm: the compiler would otherwise order every LDS
+// read after all outstanding direct-to-LDS loads (vmcnt(0)), since it cannot tell
+// the ring's slots apart. The kernel waits with lgkmcnt itself, then passes each
+// value through pin() so no use is scheduled above its wait.
+typedef __attribute__((address_space(3))) char lds_char;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_char*)p; }
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_b128(uint32_t a) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ half8_t lds_b128h(uint32_t a) {
+    half8_t v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+// two 8-byte reads, at a and a + 256
+__device__ __forceinline__ u32x4 lds_2b64_256(uint32_t a) {
+    u32x4 v;
+    asm volatile("ds_read2_b64 %0, %1 offset1:32" : "=v"(v) : "v"(a));
+    return v;
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (N << 8) | (3 << 14));  // vmcnt, expcnt at their maximum
+}
+template <class T>
+__device__ __forceinline__ void pin(T& v) {
+    asm volatile("" : "+v"(v));
+}
+
+// Workgroup → tile: the 8 XCDs take workgroup ids round-robin; each XCD gets a
+// contiguous run of tiles, ordered in groups of 4 row-tiles so that the
+// workgroups resident on one XCD share A rows and weight tiles in its L2.
+__device__ __forceinline__ void g2_tile(int id, int gm, int gn, int& tm, int& tn) {
+    const int T = gm * gn;
+    if ((T & 7) == 0) id = (id & 7) * (T >> 3) + (id >> 3);
+    const int GM = 4, per = GM * gn, grp = id / per, first = grp * GM, rows = min(GM, gm - first);
+    const int in = id - grp * per;
+    tm = first + in % rows;
+    tn = in / rows;
+}
+
+__global__ void __launch_bounds__(256) k_gemm_q4k_ring(Gemm2Args G) {
+    __shared__ __attribute__((aligned(1024))) char ring[G2_NST * G2_STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    g2_tile(blockIdx.x, G.gm, G.gn, tm, tn);
+    const int n0 = tn * G2_BN, m0 = tm * G2_BM;
+    const int nb = G.nb, nst = 4 * nb, nks = G.k / 16;
+
+    // direct-load sources for stage 0; stage s adds s·8 KiB (A), s·512 B (quants),
+    // (s/4)·256 B (headers). Tiles past the last are clamped (never written back).
+    const uint8_t* a_src[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int f = wave + 4 * j;  // local fragment: m-tile f/8, k-slice (f/2)%4, part f%2
+        a_src[j] = G.frag + ((int64_t)((2 * tm + (f >> 3)) * nks + ((f >> 1) & 3)) * 2 + (f & 1)) * 1024 + lane * 16;
+    }
+    const int bt = min(n0 / 16 + 2 * wave + (lane >> 5), G.ntiles - 1);
+    const uint8_t* b_src = G.qs + (int64_t)bt * nb * 2048 + (lane & 31) * 16;
+    const int ht = min(n0 / 16 + 4 * (wave & 1) + (lane >> 4), G.ntiles - 1);
+    const uint8_t* h_src = G.hdr + ((int64_t)ht * nb * 16 + (lane & 15)) * 16;
+    auto issue = [&](int s, char* st) {
+        s = min(s, nst - 1);  // the ring's tail reloads the last stage into a free buffer
+#pragma unroll
+        for (int j = 0; j < 4; j++) g_dma(a_src[j] + (int64_t)s * 8192, st + (wave + 4 * j) * 1024);
+        g_dma(b_src + (int64_t)s * 512, st + G2_A + wave * 1024);
+        g_dma(h_src + (int64_t)(s >> 2) * 256, st + G2_A + G2_B + wave * 1024);
+    };
+
+    // LDS offsets: A fragment (wm, ks, part) at a_off + (2ks + part)·1024; quants of
+    // column c's tile, lane (n, kg) at b_off[c] + 256·kg; its header at h_off[c]
+    const int a_off = wm * 8192 + lane * 16;
+    int b_off[2], h_off[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const int nc = 64 * wn + 32 * c + (lane & 31), t = nc >> 4, n = nc & 15;
+        b_off[c] = G2_A + t * 512 + n * 16 + 8 * (lane >> 5);
+        h_off[c] = G2_A + G2_B + (t >> 2) * 1024 + ((t & 3) * 16 + n) * 16;
+    }
+    const int srow = min(m0 + 32 * wm + (lane & 31), G.m - 1);
+    const _Float16* s_src = ((lane >> 5) ? G.Sl : G.Sh) + (int64_t)srow * (G.k / 32);
+
+    f32x16 acc[2], part[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        acc[c] = (f32x16){};
+        part[c] = (f32x16){};
+    }
+    u32x4 hd[2] = {};
+    half8_t sv = {};
+
+    issue(0, ring);
+    issue(1, ring + G2_STAGE);
+    const uint32_t ring_lds = lds_addr(ring);
+    int cur = 0;  // ring slot of stage s
+    for (int b = 0; b < nb; b++) {
+#pragma unroll
+        for (int J = 0; J < 4; J++) {
+            const int s = 4 * b + J;
+            const uint32_t st = ring_lds + cur * G2_STAGE;
+            const int nx = cur == 0 ? 2 : cur - 1;  // slot of stage s + 2 (= slot of s - 1)
+            // this wave's loads of stage s have landed (those of s + 1 may be in flight)
+            __builtin_amdgcn_s_waitcnt((G2_LOADS & 15) | (7 << 4) | (15 << 8) | ((G2_LOADS >> 4) << 14));
+            __builtin_amdgcn_s_barrier();  // every wave's part of stage s is in; slot nx is free
+            issue(s + 2, ring + nx * G2_STAGE);
+            cur = cur == 2 ? 0 : cur + 1;
+            if (J == 0) sv = *(const half8_t*)(s_src + b * 8);
+            // LDS reads in one batch, consumed in order under lgkmcnt
+            if (J == 0) {
+                hd[0] = lds_b128<0>(st + h_off[0]);
+                hd[1] = lds_b128<0>(st + h_off[1]);
+            }
+            u32x4 raw[2];  // .xy: k-group 0, .zw: k-group 1 (256 B further)
+            raw[0] = lds_2b64_256(st + b_off[0]);
+            raw[1] = lds_2b64_256(st + b_off[1]);
+            const uint32_t pa = st + a_off;
+            half8_t a[4][2];
+            a[0][0] = lds_b128h<0>(pa);
+            a[0][1] = lds_b128h<1024>(pa);
+            a[1][0] = lds_b128h<2048>(pa);
+            a[1][1] = lds_b128h<3072>(pa);
+            a[2][0] = lds_b128h<4096>(pa);
+            a[2][1] = lds_b128h<5120>(pa);
+            a[3][0] = lds_b128h<6144>(pa);
+            a[3][1] = lds_b128h<7168>(pa);
+            lgkm_wait<6>();
+            pin(hd[0]);
+            pin(hd[1]);
+            pin(raw[0]);
+            pin(raw[1]);
+            pin(a[0][0]);
+            pin(a[0][1]);
+            // scales of sub-blocks 2J (low nibbles) and 2J + 1 (high nibbles), get_scale_min_k4
+            half2_t sn[2][2], zn[2][2];
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const uint32_t y = hd[c].y, w = hd[c].w;
+                const uint32_t sc4 = J < 2 ? (y & 0x3F3F3F3Fu) : ((w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u));
+                half2_t p01, p23;
+                bytes_to_h2(sc4, p01, p23);
+                const half2_t pr = (J & 1) ? p23 : p01;
+                const half2_t m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+                sn[c][0] = __builtin_shufflevector(pr, pr, 0, 0);
+                sn[c][1] = __builtin_shufflevector(pr, pr, 1, 1);
+                zn[c][0] = sn[c][0] * m1024;
+                zn[c][1] = sn[c][1] * m1024;
+            }
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                const int nib = ks >> 1, kg = ks & 1;
+                if (ks == 1) lgkm_wait<4>();
+                if (ks == 2) lgkm_wait<2>();
+                if (ks == 3) lgkm_wait<0>();
+                if (ks > 0) {
+                    pin(a[ks][0]);
+                    pin(a[ks][1]);
+                }
+                half8_t bv[2];
+#pragma unroll
+                for (int c = 0; c < 2; c++) {
+                    const uint2 r2 = kg ? make_uint2(raw[c].z, raw[c].w) : make_uint2(raw[c].x, raw[c].y);
+                    bv[c] = dq8(r2, nib, sn[c][nib], zn[c][nib]);
+                }
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+#pragma unroll
+                    for (int c = 0; c < 2; c++)
+                        part[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks][p], bv[c], part[c], 0, 0, 0);
+            }
+            if (J == 3) {
+                // super-block done: C += d·P − 32·dmin·Σ_s m_s·S_s (S scaled by 2^-(e+5))
+#pragma unroll
+                for (int c = 0; c < 2; c++) {
+                    const float d = aeth_decode_d(hd[c].x), dmin = aeth_decode_d(hd[c].x >> 16);
+                    const uint32_t z = hd[c].z, w = hd[c].w;
+                    half2_t m01, m23, m45, m67;
+                    bytes_to_h2(z & 0x3F3F3F3Fu, m01, m23);
+                    bytes_to_h2(((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u), m45, m67);
+                    const half8_t mv = {m01[0], m01[1], m23[0], m23[1], m45[0], m45[1], m67[0], m67[1]};
+                    const f32x16 q = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv, mv, (f32x16){}, 0, 0, 0);
+                    const float dm = dmin * 32.0f;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[c][r] += d * part[c][r] - dm * q[r];
+                    part[c] = (f32x16){};
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the tail's loads land before the workgroup's LDS is released
+
+    const int lr = lane & 31;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const int col = n0 + 64 * wn + 32 * c + lr;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = m0 + 32 * wm + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+            if (row < G.m && col < G.n) {
+                const float v = acc[c][r] * G.escale[row];
+                float* dst = G.C + (int64_t)row * G.n + col;
+                *dst = G.accumulate ? *dst + v : v;
+            }
+        }
+    }
+}
+
 namespace {
 struct GemmWs {
     void* ptr = nullptr;
@@ -278,9 +603,13 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
                          hipStream_t s) {
     const int k = (int)w->k, nb = (int)w->nb;
     if (k != nb * 256) return aeth_gemv_launch(w, d_a, m, d_c, flags, s);  // ragged K: row-batched GEMV
-    if (m > 65535 * 128) return aeth_set_error(AETH_EINVAL, "gemm: m too large");
-    // workspace: Ah, Al [m][k], Sh, Sl [m][k/32] (fp16), escale [m] (f32)
-    const size_t need = (size_t)m * k * 2 * 2 + (size_t)m * (k / 32) * 2 * 2 + (size_t)m * 4 + 256;
+    // AETH_GEMM_KERNEL=1 selects the register-staged kernel (k_gemm_q4k) instead of the ring
+    static const int env_kernel = getenv("AETH_GEMM_KERNEL") ? atoi(getenv("AETH_GEMM_KERNEL")) : 0;
+    const bool ring = env_kernel != 1;
+    const int64_t mp = ring ? aeth_cdiv(m, G2_BM) * G2_BM : m;  // fragment rows: whole 64-row tiles
+    if (mp > (1LL << 20) || mp * k > (1LL << 30)) return aeth_set_error(AETH_EINVAL, "gemm: m=%lld too large", (long long)m);
+    // workspace: A parts [mp][k] × {hi, lo}, Sh, Sl [mp][k/32] (fp16), escale [mp] (f32)
+    const size_t need = (size_t)mp * k * 2 * 2 + (size_t)mp * (k / 32) * 2 * 2 + (size_t)mp * 4 + 256;
     int dev = 0;
     AETH_HIP_CHECK(hipGetDevice(&dev));
     if (dev < 0 || dev >= 64) return aeth_set_error(AETH_EINVAL, "gemm: device index");
@@ -293,30 +622,32 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
         ws.bytes = need;
     }
     _Float16* Ah = (_Float16*)ws.ptr;
-    _Float16* Al = Ah + (size_t)m * k;
-    _Float16* Sh = Al + (size_t)m * k;
-    _Float16* Sl = Sh + (size_t)m * (k / 32);
-    float* esc = (float*)(Sl + (size_t)m * (k / 32));
+    _Float16* Al = Ah + (size_t)mp * k;
+    _Float16* Sh = Al + (size_t)mp * k;
+    _Float16* Sl = Sh + (size_t)mp * (k / 32);
+    float* esc = (float*)(Sl + (size_t)mp * (k / 32));
+    if (ring) {
+        hipLaunchKernelGGL(k_gemm_prep_frag, dim3((unsigned)mp), dim3(256), 0, s, d_a, (int)m, k, Ah, Sh, Sl, esc);
+        AETH_LAUNCH_CHECK();
+        const int gm = (int)(mp / G2_BM), gn = (int)aeth_cdiv(w->n, G2_BN);
+        Gemm2Args G{(const uint8_t*)Ah, Sh, Sl, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb,
+                    (int)aeth_cdiv(w->n, 16), gm, gn, d_c, (flags & AETH_MM_ACCUMULATE) ? 1 : 0};
+        hipLaunchKernelGGL(k_gemm_q4k_ring, dim3((unsigned)(gm * gn)), dim3(256), 0, s, G);
+        AETH_LAUNCH_CHECK();
+        return AETH_OK;
+    }
     hipLaunchKernelGGL(k_gemm_prep, dim3((unsigned)m), dim3(256), 0, s, d_a, k, Ah, Al, Sh, Sl, esc);
     AETH_LAUNCH_CHECK();
     GemmArgs G{Ah, Al, Sh, Sl, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, d_c,
                (flags & AETH_MM_ACCUMULATE) ? 1 : 0};
-    // tuning overrides, read once: AETH_GEMM_D (prefetch distance 1, 2 or 4), AETH_GEMM_BM (64 | 128)
+    // tuning override, read once: AETH_GEMM_D (prefetch distance 1, 2 or 4)
     static const int env_d = getenv("AETH_GEMM_D") ? atoi(getenv("AETH_GEMM_D")) : 0;
-    static const int env_bm = getenv("AETH_GEMM_BM") ? atoi(getenv("AETH_GEMM_BM")) : 0;
     // measured at m = 512, n = 4096 / 14336: BM = 64 with a one-step prefetch is
-    // best (two workgroups per CU where the grid allows); AETH_GEMM_BM=128 forces
-    // the 128-row tile
-    if (env_bm == 128) {
-        dim3 grid((unsigned)aeth_cdiv(w->n, GEMM_BN), (unsigned)aeth_cdiv(m, 128));
-        if (env_d == 2) hipLaunchKernelGGL((k_gemm_q4k<128, 2>), grid, dim3(256), 0, s, G);
-        else hipLaunchKernelGGL((k_gemm_q4k<128, 1>), grid, dim3(256), 0, s, G);
-    } else {
-        dim3 grid((unsigned)aeth_cdiv(w->n, GEMM_BN), (unsigned)aeth_cdiv(m, 64));
-        if (env_d == 2) hipLaunchKernelGGL((k_gemm_q4k<64, 2>), grid, dim3(256), 0, s, G);
-        else if (env_d == 4) hipLaunchKernelGGL((k_gemm_q4k<64, 4>), grid, dim3(256), 0, s, G);
-        else hipLaunchKernelGGL((k_gemm_q4k<64, 1>), grid, dim3(256), 0, s, G);
-    }
+    // best of this kernel (two workgroups per CU where the grid allows)
+    dim3 grid((unsigned)aeth_cdiv(w->n, GEMM_BN), (unsigned)aeth_cdiv(m, 64));
+    if (env_d == 2) hipLaunchKernelGGL((k_gemm_q4k<64, 2>), grid, dim3(256), 0, s, G);
+    else if (env_d == 4) hipLaunchKernelGGL((k_gemm_q4k<64, 4>), grid, dim3(256), 0, s, G);
+    else hipLaunchKernelGGL((k_gemm_q4k<64, 1>), grid, dim3(256), 0, s, G);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
