@@ -2,9 +2,11 @@
 
 Usage: python -m aether_amd.build   (or aether_amd.build.build())
 """
+import concurrent.futures
 import os
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -29,39 +31,72 @@ def hipcc():
     return "hipcc"
 
 
-def command(out=LIB):
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    return [
-        hipcc(),
-        "-x", "hip",
-        "--offload-arch=" + ARCH,
-        "-O3",
-        "-std=c++17",
-        "-fPIC",
-        "-shared",
-        "-fvisibility=hidden",
-        "-ffp-contract=fast-honor-pragmas",
-        # packed-FP32 VALU forms are kept out of the device code
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-Wall",
-        "-Wno-unused-result",
-        "-Wno-unused-value",
-        "-o", out,
-    ] + srcs
+# per-source device flags: the GEMM keeps its MFMA accumulators in VGPRs (one
+# wave per SIMD leaves room for them), avoiding AGPR→VGPR copies in its epilogue
+EXTRA = {
+    "aeth_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+COMMON = [
+    "-x", "hip",
+    "--offload-arch=" + ARCH,
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-ffp-contract=fast-honor-pragmas",
+    # packed-FP32 VALU forms are kept out of the device code
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-result",
+    "-Wno-unused-value",
+]
 
 
-def build(verbose=True):
-    cmd = command(LIB + ".tmp")
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def compile_command(src, obj, extra=()):
+    """hipcc -c of one source (csrc-relative name or path) into obj."""
+    path = src if os.path.isabs(src) else os.path.join(CSRC, src)
+    return [hipcc()] + COMMON + ["-I", CSRC] + EXTRA.get(os.path.basename(path), []) + list(extra) + \
+        ["-c", "-o", obj, path]
+
+
+def link_command(objs, out):
+    return [hipcc(), "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", out] + list(objs)
+
+
+def _run(cmd):
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
-    if out.strip() and verbose:
-        print(out, flush=True)
-    if r.returncode != 0:
-        raise RuntimeError("hipcc failed (rc=%d)" % r.returncode)
-    os.replace(LIB + ".tmp", LIB)
-    return LIB
+    return r.returncode, out
+
+
+def build(verbose=True, out=LIB, sources=None, extra=()):
+    """Compiles every source (in parallel) and links the shared library at out."""
+    sources = list(sources or SOURCES)
+    with tempfile.TemporaryDirectory(prefix="aeth_build_") as tmp:
+        objs = [os.path.join(tmp, "%02d_%s.o" % (i, os.path.basename(s))) for i, s in enumerate(sources)]
+        cmds = [compile_command(s, o, extra) for s, o in zip(sources, objs)]
+        with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(cmds))) as ex:
+            results = list(ex.map(_run, cmds))
+        failed = False
+        for cmd, (rc, text) in zip(cmds, results):
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            if text.strip() and (verbose or rc):
+                print(text, flush=True)
+            failed |= rc != 0
+        if failed:
+            raise RuntimeError("hipcc failed")
+        cmd = link_command(objs, out + ".tmp")
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        rc, text = _run(cmd)
+        if text.strip():
+            print(text, flush=True)
+        if rc != 0:
+            raise RuntimeError("link failed (rc=%d)" % rc)
+    os.replace(out + ".tmp", out)
+    return out
 
 
 if __name__ == "__main__":

@@ -12,7 +12,7 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import GEOM, Q4_K, Q6_K, Q8_0, assert_close, synth_blocks, weight
+from tests._util import GEOM, Q4_K, Q6_K, Q8_0, assert_close, assert_close_rows, synth_blocks, weight
 
 pytestmark = pytest.mark.gpu
 DTYPES = [Q8_0, Q4_K, Q6_K]
@@ -263,6 +263,37 @@ def test_synthetic_generator_deterministic(gpu):
     assert (d >= 0).all() and 0.004 < d.mean() < 0.012  # |N(0,1)|*0.01 has mean 0.008
     q = blk[:, 16:]
     assert abs(q.mean() - 127.5) < 2.0
+
+
+# The Q4_K GEMM (m > 1): an odd super-block count takes the single-K-group
+# kernel, an even one the split-K kernel; m and n off the 64 × 128 tile grid.
+# Row magnitudes span 2^-12 .. 2^20 (the per-block fp16 exponent), with an
+# all-zero row, and the accumulate epilogue is checked on top.
+@pytest.mark.parametrize("m,n,k", [(70, 130, 768), (65, 300, 1024), (130, 40, 2560), (3, 16, 512)])
+def test_gemm_q4k_tiles_exponents_accumulate(gpu, m, n, k):
+    rng = np.random.default_rng(m * 31 + n * 7 + k)
+    raw = weight(Q4_K, n, k, 3 * n + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    scale = np.ones(m, dtype=np.float32)
+    scale[m // 3] = 2.0 ** 20
+    scale[m // 2] = 2.0 ** -12
+    scale[(2 * m) // 3] = 0.0
+    if m > 40:
+        scale[33:40] = 2.0 ** 15  # a block with values past fp16 range next to ordinary rows
+    x *= scale[:, None]
+    w = make_weight(gpu, Q4_K, n, k, raw)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    got = gemv(gpu, w, x.ravel(), n, m)
+    got_acc = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q4_K, x.ravel(), raw, m, n, k).reshape(m, n)
+    # rows of magnitude 1 take the element-wise bar; the scaled rows a bar
+    # relative to their own magnitude (an f32 sum's error scales with its terms)
+    plain = scale == 1.0
+    assert_close(got[plain], ref[plain], what="gemm m=%d n=%d k=%d" % (m, n, k))
+    assert_close_rows(got, ref, what="gemm (scaled rows) m=%d n=%d k=%d" % (m, n, k))
+    assert_close(got_acc[plain], (ref + y0)[plain], what="gemm accumulate m=%d n=%d k=%d" % (m, n, k))
+    assert np.all(got[(2 * m) // 3] == 0.0)
 
 
 @pytest.mark.parametrize("n", [4096, 14336])
