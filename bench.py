@@ -183,6 +183,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
+    ap.add_argument("--extra", default="q8,q6,gemm,decode",
+                    help="comma-separated extra sections to run: q8, q6, gemm, decode (default: all)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (HBM counter calibration under rocprofv3)")
@@ -218,22 +220,26 @@ def main():
     print("[bench] Q4_K GEMV %dx%d: %.3f us  %.1f GB/s" % (n, k, head["ms"] * 1e3, head["gbs"]), file=sys.stderr,
           flush=True)
     extra = {}
-    if not args.no_extra:
+    sections = set() if args.no_extra else set(x.strip() for x in args.extra.split(",") if x.strip())
+    if "q8" in sections:
         r = bench_gemv(torch, A, 8, 4096, 4096, args.steps, args.warmup, seed=0xAE7E41)
         extra["q8_0_gemv_4096x4096"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),
                                          "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         print("[bench] Q8_0 GEMV: %s" % extra["q8_0_gemv_4096x4096"], file=sys.stderr, flush=True)
+    if "q6" in sections:
         r = bench_gemv(torch, A, 14, 128256, 4096, max(20, args.steps // 4), max(3, args.warmup // 4), copies=2,
                        seed=0xAE7E42)
         extra["q6_k_gemv_128256x4096"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),
                                            "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         print("[bench] Q6_K GEMV: %s" % extra["q6_k_gemv_128256x4096"], file=sys.stderr, flush=True)
         del r
+    if "gemm" in sections:
         for nn in (4096, 14336):
             g = bench_gemm(torch, A, nn, 4096, 512, 5, 2)
             extra["q4_k_gemm_m512_n%d" % nn] = {"TFLOP/s": round(g["tflops"], 2), "ms": round(g["ms"], 4),
                                                  "frac_int8_peak": round(g["tflops"] / INT8_PEAK_TOPS, 4)}
             print("[bench] Q4_K GEMM n=%d: %s" % (nn, extra["q4_k_gemm_m512_n%d" % nn]), file=sys.stderr, flush=True)
+    if "decode" in sections:
         d = bench_decode(torch, A)
         extra["decode_8b_q4k"] = {"tok/s": round(d["tok_s"], 1), "ms_per_token": round(d["ms_per_token"], 4),
                                   "GB/s": round(d["gbs"], 1), "frac_hbm": round(d["gbs"] / HBM_PEAK_GBS, 4),
