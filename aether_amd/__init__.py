@@ -8,7 +8,8 @@ import ctypes
 import os
 
 __all__ = ["lib", "check", "AethError", "LIB_PATH", "DTYPE_Q8_0", "DTYPE_Q4_K", "DTYPE_Q6_K",
-           "LlamaConfig", "header_symbols", "MM_ACCUMULATE", "block_geometry"]
+           "LlamaConfig", "header_symbols", "MM_ACCUMULATE", "block_geometry", "AETH_OK", "AETH_EINVAL",
+           "AETH_EHIP", "AETH_ENOMEM", "AETH_EUNSUPPORTED", "AETH_ESTATE"]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libaether_hip.so")
@@ -16,6 +17,8 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
 DTYPE_Q8_0, DTYPE_Q4_K, DTYPE_Q6_K = 8, 12, 14
 MM_ACCUMULATE = 1
+# return codes (include/aether_hip.h)
+AETH_OK, AETH_EINVAL, AETH_EHIP, AETH_ENOMEM, AETH_EUNSUPPORTED, AETH_ESTATE = 0, -1, -2, -3, -4, -5
 _GEOM = {DTYPE_Q8_0: (32, 34), DTYPE_Q4_K: (256, 144), DTYPE_Q6_K: (256, 210)}
 
 
@@ -46,6 +49,11 @@ _SIGS = {
     "aeth_weight_bytes": (_I64, [_P]),
     "aeth_weight_export_raw": (_INT, [_P, _P, _INT, _P]),
     "aeth_dequant": (_INT, [_INT, _P, _I64, _P, _P]),
+    "aeth_requantize": (_INT, [_INT, _P, _I64, _I64, _P, _P]),
+    "aeth_quantize_activations_q8_0": (_INT, [_P, _I64, _I64, _P, _P]),
+    "aeth_transpose_f32": (_INT, [_P, _I64, _I64, _P, _P]),
+    "aeth_load_quant_ws_bytes": (_I64, [_I64, _I64]),
+    "aeth_load_quant": (_INT, [_INT, _P, _I64, _I64, _P, _P, _P]),
     "aeth_qmatmul": (_INT, [_P, _P, _I64, _P, ctypes.c_uint, _P]),
     "aeth_quantized_matmul_impl": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P]),
     "aeth_matmul_q8_0": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),

@@ -14,6 +14,7 @@ LIB = os.path.join(HERE, "libaether_hip.so")
 SOURCES = [
     "aeth_weights.hip",
     "aeth_dequant.hip",
+    "aeth_quantize.hip",
     "aeth_gemv.hip",
     "aeth_gemm.hip",
     "aeth_decode_ops.hip",

@@ -72,6 +72,32 @@ AETH_API int aeth_weight_export_raw(const aeth_weight* w, void* dst, int dst_is_
  * blocks for the K-quants as the reference does (tail left untouched). */
 AETH_API int aeth_dequant(int dtype, const void* d_raw, int64_t n_elems, float* d_out, void* stream);
 
+/* f32 [rows][cols] → GGUF blocks [rows][ceil(cols/block_elems)], byte-exact
+ * with requantize_q8_0 / requantize_q4_k / requantize_q6_k
+ * (src/quant/matmul/dispatch.rs:139-184, 186-300, 431-537; entry
+ * `requantize` :139-147). d_dst holds rows·ceil(cols/bs)·block_bytes bytes. */
+AETH_API int aeth_requantize(int dtype, const float* d_src, int64_t rows, int64_t cols, void* d_dst,
+                             void* stream);
+
+/* Q8_0 activation blocks, byte-exact with quantize_activations_q8_0[_batched]
+ * (src/quant/matmul/neon.rs:106-155) over quantize_q8_0_block (:45-104):
+ * m rows of k f32 → m·ceil(k/32) blocks of 34 bytes (a partial last block is
+ * zero-padded). */
+AETH_API int aeth_quantize_activations_q8_0(const float* d_a, int64_t m, int64_t k, void* d_dst, void* stream);
+
+/* [rows][cols] f32 → [cols][rows] (the transpose inside transpose_quantized_bytes,
+ * src/inference/model_loader.rs:372-385). d_src and d_dst must not overlap. */
+AETH_API int aeth_transpose_f32(const float* d_src, int64_t rows, int64_t cols, float* d_dst, void* stream);
+
+/* load_quant (src/inference/model_loader.rs:330-386) for a 2-D quantized
+ * tensor on the device: GGUF bytes of shape [k, n] → dequantize → transpose
+ * → requantize, giving [n][k] row blocks in d_dst (n·ceil(k/bs)·block_bytes
+ * bytes, the layout aeth_weight_create takes). d_ws holds
+ * aeth_load_quant_ws_bytes(k, n) bytes. Q8_0, Q4_K and Q6_K. */
+AETH_API int64_t aeth_load_quant_ws_bytes(int64_t k, int64_t n);
+AETH_API int aeth_load_quant(int dtype, const void* d_src, int64_t k, int64_t n, void* d_dst, void* d_ws,
+                             void* stream);
+
 /* C[m×n] = A[m×k] · Wᵀ on the device — QuantKernel::matmul
  * (src/quant/matmul/registry.rs:7-19) / quantized_matmul_impl
  * (src/quant/matmul/dispatch.rs:98-135) with device operands. m == 1 runs the
