@@ -85,6 +85,17 @@ extern "C" AETH_API int aeth_attn_decode(const float* d_q, const float* d_layer_
                             head_dim, max_seq, (float*)ws, d_out, (hipStream_t)stream);
 }
 
+extern "C" AETH_API int aeth_attn_prefill(const float* d_q, int64_t q_stride, const float* d_layer_kv, int64_t n,
+                                          int64_t n_heads, int64_t kv_heads, int64_t head_dim, int64_t max_seq,
+                                          float* d_out, void* stream) {
+    if (!d_q || !d_layer_kv || !d_out || n <= 0 || n > max_seq || kv_heads <= 0 || n_heads <= 0 ||
+        n_heads % kv_heads != 0 || q_stride < n_heads * head_dim || (q_stride & 3))
+        return aeth_set_error(AETH_EINVAL, "aeth_attn_prefill: bad argument (n %lld, max_seq %lld)", (long long)n,
+                              (long long)max_seq);
+    return aeth_attn_prefill_launch(d_q, q_stride, d_layer_kv, n, n_heads, kv_heads, head_dim, max_seq, d_out,
+                                    (hipStream_t)stream);
+}
+
 extern "C" AETH_API int aeth_silu_mul(float* d_gate, const float* d_up, int64_t n, void* stream) {
     if (!d_gate || !d_up || n < 0) return aeth_set_error(AETH_EINVAL, "aeth_silu_mul: bad argument");
     return aeth_silu_mul_launch(d_gate, d_up, n, (hipStream_t)stream);

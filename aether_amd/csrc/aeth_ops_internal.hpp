@@ -31,6 +31,7 @@ int aeth_state_advance_launch(int* st, unsigned long long* amax, int64_t max_seq
 int aeth_embed_rows_launch(const float* table, const int* d_tokens, int64_t n, int64_t d, float* x, hipStream_t s);
 int aeth_prefill_rope_kv_launch(float* qkv, int64_t n, int64_t nh, int64_t nkv, int64_t hd, const float* sin_t,
                                 const float* cos_t, int64_t max_seq, float* layer_kv, hipStream_t s);
-int aeth_attn_prefill_launch(const float* qkv, const float* layer_kv, int64_t n, int64_t nh, int64_t nkv,
-                             int64_t hd, int64_t max_seq, float* out, hipStream_t s);
+// q rows of q_stride floats (the fused projection: (nh + 2·nkv)·hd), head h at column h·hd
+int aeth_attn_prefill_launch(const float* q, int64_t q_stride, const float* layer_kv, int64_t n, int64_t nh,
+                             int64_t nkv, int64_t hd, int64_t max_seq, float* out, hipStream_t s);
 int aeth_silu_pairs_launch(const float* gu, int64_t total, float* h, hipStream_t s);

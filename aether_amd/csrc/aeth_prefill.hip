@@ -6,16 +6,22 @@
 //  * k_embed_rows: token embeddings → rows of x;
 //  * k_prefill_rope_kv: RoPE of q and k at each token's position
 //    (apply_rope_inplace, runner.rs:1886-1909) and the cache writes (:890-906);
-//  * k_attn_prefill: causal attention (attention_batch, runner.rs:1809-1883)
-//    as one flash-style pass per (64-query block, head): online softmax over
-//    64-key blocks in LDS, 4×4 score and 4×8 output register tiles per thread;
+//  * k_attn_prefill_mf: causal attention (attention_batch, runner.rs:1809-1883)
+//    on the f32 matrix cores, flash-style (online softmax over 16-key blocks);
+//    k_attn_prefill, the f32 VALU form (64-query blocks, 4×4 score and 4×8
+//    output register tiles per thread), serves group sizes the MFMA form does
+//    not take;
 //  * k_silu_pairs: h = g·σ(g)·u on the interleaved gate/up GEMM output
 //    (runner.rs:1617-1625 form).
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include "aeth_common.hpp"
 #include "aeth_internal.hpp"
 #include "aeth_ops_internal.hpp"
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(256) k_embed_rows(const float* __restrict__ table, const int* __restrict__ tokens,
                                                     int64_t d, float* __restrict__ x) {
@@ -208,11 +214,178 @@ __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ 
     }
 }
 
-int aeth_attn_prefill_launch(const float* qkv, const float* layer_kv, int64_t n, int64_t nh, int64_t nkv,
-                             int64_t hd, int64_t max_seq, float* out, hipStream_t s) {
+// Causal attention on the f32 matrix cores, v_mfma_f32_16x16x4_f32 (lane l
+// holds A[l%16][l/16] and B[l/16][l%16]; result register r of lane l is
+// D[4(l/16) + r][l%16]). Scores are computed transposed, Sᵀ = K·Qᵀ, so that a
+// lane's accumulator holds 4 keys of one score column; those registers are
+// then directly the B operand of Oᵀ = Vᵀ·Pᵀ (no transposes). The 16 columns
+// are QB = 16/G queries × the G query heads of one KV head (column c: query
+// c/G, head c%G), so every K/V element loaded serves all G heads.
+// K-index maps: in Sᵀ step i, lane group g (= l/16) contracts d = 32g + i;
+// in Oᵀ step j it contracts key t0 + 4g + j (its own score register j), and
+// Oᵀ row m of d-tile dt is d = 8m + dt, so a lane (c, g) ends with d = 32g +
+// 8r + dt of column c.
+// Work: workgroup (KV head, query-block pair {p, nqb−1−p}), which balances the
+// causal triangle; its 4 waves take the 16-key blocks of a query block round
+// robin, each keeping an online softmax, and merge the partials through LDS.
+template <int G>
+__global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict__ qkv, int64_t qkv_stride,
+                                                         const float* __restrict__ layer_kv, int n, int nh, int nkv,
+                                                         int64_t max_seq, float* __restrict__ out) {
+    constexpr int QB = 16 / G, HD = 128, PLD = HD + 4;
+    __shared__ __attribute__((aligned(16))) float po[4][16][PLD];  // per wave: column c, d
+    __shared__ float pm[4][16], pl[4][16];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int c = lane & 15, grp = lane >> 4;
+    const int g = blockIdx.x % nkv, p = blockIdx.x / nkv;
+    const int nqb = (n + QB - 1) / QB;
+    const int head = g * G + c % G;
+    const float* K = layer_kv + (int64_t)g * max_seq * HD;
+    const float* V = layer_kv + (int64_t)(nkv + g) * max_seq * HD;
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (int pass = 0; pass < 2; pass++) {
+        const int qb = pass == 0 ? p : nqb - 1 - p;
+        if (pass == 1 && qb == p) break;  // the middle block of an odd count (uniform)
+        const int q0 = qb * QB, query = q0 + c / G;
+        float qv[32];
+        {
+            const float* src = qkv + (int64_t)min(query, n - 1) * qkv_stride + (int64_t)head * HD + 32 * grp;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 t = *(const float4*)(src + 4 * i);
+                qv[4 * i] = t.x; qv[4 * i + 1] = t.y; qv[4 * i + 2] = t.z; qv[4 * i + 3] = t.w;
+            }
+        }
+        const int kb_end = (min(q0 + QB, n) - 1) / 16;  // last key block, inclusive
+        // loads of one key block: K rows t0 + c (A of Sᵀ), V rows t0 + 4·grp + j,
+        // floats [8c, 8c + 8) (A of Oᵀ); rows past n are clamped and masked
+        float4 kr[8], vr[4][2], krn[8], vrn[4][2];
+        auto load = [&](int kb, float4* kk, float4 (*vv)[2]) {
+            const int t0 = 16 * kb;
+            const float4* ks = (const float4*)(K + (int64_t)min(t0 + c, n - 1) * HD + 32 * grp);
+#pragma unroll
+            for (int i = 0; i < 8; i++) kk[i] = ks[i];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4* vs = (const float4*)(V + (int64_t)min(t0 + 4 * grp + j, n - 1) * HD + 8 * c);
+                vv[j][0] = vs[0];
+                vv[j][1] = vs[1];
+            }
+        };
+        float m = -INFINITY, l = 0.0f;
+        f32x4 o[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o[dt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        if (w <= kb_end) load(w, kr, vr);
+        for (int kb = w; kb <= kb_end; kb += 4) {
+            load(min(kb + 4, kb_end), krn, vrn);  // next block in flight during this one
+            const int t0 = 16 * kb;
+            f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].x, qv[4 * i], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].y, qv[4 * i + 1], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].z, qv[4 * i + 2], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].w, qv[4 * i + 3], s, 0, 0, 0);
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = t0 + 4 * grp + r;
+                s[r] = (t <= query && t < n) ? s[r] * scale : -INFINITY;
+                mx = fmaxf(mx, s[r]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m, mx);
+            const float alpha = m_new == -INFINITY ? 1.0f : expf(m - m_new);
+            float ps = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                s[r] = m_new == -INFINITY ? 0.0f : expf(s[r] - m_new);
+                ps += s[r];
+            }
+            ps += __shfl_xor(ps, 16, 64);
+            ps += __shfl_xor(ps, 32, 64);
+            l = l * alpha + ps;
+            m = m_new;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) o[dt] *= alpha;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float vj[8] = {vr[j][0].x, vr[j][0].y, vr[j][0].z, vr[j][0].w,
+                                     vr[j][1].x, vr[j][1].y, vr[j][1].z, vr[j][1].w};
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vj[dt], s[j], o[dt], 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) kr[i] = krn[i];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                vr[j][0] = vrn[j][0];
+                vr[j][1] = vrn[j][1];
+            }
+        }
+        // this wave's partial: column c, d = 32·grp + 8r + dt
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt += 4)
+                *(float4*)&po[w][c][32 * grp + 8 * r + dt] = make_float4(o[dt][r], o[dt + 1][r], o[dt + 2][r], o[dt + 3][r]);
+        if (grp == 0) {
+            pm[w][c] = m;
+            pl[w][c] = l;
+        }
+        __syncthreads();
+        {  // merge the 4 waves: thread → column tid/16, d [8·(tid%16), +8)
+            const int cc = tid >> 4, d0 = 8 * (tid & 15);
+            float M = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 4; v++) M = fmaxf(M, pm[v][cc]);
+            float wgt[4], L = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                wgt[v] = pm[v][cc] == -INFINITY ? 0.0f : expf(pm[v][cc] - M);
+                L += wgt[v] * pl[v][cc];
+            }
+            float acc[8] = {};
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float4 a = *(const float4*)&po[v][cc][d0];
+                const float4 b = *(const float4*)&po[v][cc][d0 + 4];
+                acc[0] += wgt[v] * a.x; acc[1] += wgt[v] * a.y; acc[2] += wgt[v] * a.z; acc[3] += wgt[v] * a.w;
+                acc[4] += wgt[v] * b.x; acc[5] += wgt[v] * b.y; acc[6] += wgt[v] * b.z; acc[7] += wgt[v] * b.w;
+            }
+            const int qq = q0 + cc / G, hh = g * G + cc % G;
+            if (qq < n) {
+                const float inv = 1.0f / L;
+                float* dst = out + (int64_t)qq * nh * HD + (int64_t)hh * HD + d0;
+                *(float4*)dst = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+                *(float4*)(dst + 4) = make_float4(acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv);
+            }
+        }
+        __syncthreads();  // LDS is reused by the second query block
+    }
+}
+
+int aeth_attn_prefill_launch(const float* qkv, int64_t stride, const float* layer_kv, int64_t n, int64_t nh,
+                             int64_t nkv, int64_t hd, int64_t max_seq, float* out, hipStream_t s) {
     if (n <= 0) return AETH_OK;
     if (hd != 128 || nh % nkv != 0)
         return aeth_set_error(AETH_EUNSUPPORTED, "prefill attention: head_dim %lld (needs 128)", (long long)hd);
+    // AETH_PREFILL_ATTN=valu selects the f32 VALU kernel (comparison, tests)
+    static const bool force_valu = getenv("AETH_PREFILL_ATTN") && !strcmp(getenv("AETH_PREFILL_ATTN"), "valu");
+    const int64_t G = nh / nkv;
+    if (!force_valu && (G == 1 || G == 2 || G == 4 || G == 8)) {
+        const int64_t nqb = aeth_cdiv(n, 16 / G);
+        const dim3 grid((unsigned)(nkv * aeth_cdiv(nqb, 2)));
+        if (G == 1) hipLaunchKernelGGL(k_attn_prefill_mf<1>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
+        else if (G == 2) hipLaunchKernelGGL(k_attn_prefill_mf<2>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
+        else if (G == 4) hipLaunchKernelGGL(k_attn_prefill_mf<4>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
+        else hipLaunchKernelGGL(k_attn_prefill_mf<8>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
+        AETH_LAUNCH_CHECK();
+        return AETH_OK;
+    }
     const size_t lds = sizeof(float) * ((size_t)(PA_BQ + 2 * PA_BK) * (128 + 4) + PA_BQ * (PA_BK + 1) + 3 * PA_BQ);
     static bool opted = false;
     if (!opted) {
@@ -221,7 +394,7 @@ int aeth_attn_prefill_launch(const float* qkv, const float* layer_kv, int64_t n,
         opted = true;
     }
     hipLaunchKernelGGL(k_attn_prefill<128>, dim3((unsigned)aeth_cdiv(n, PA_BQ), (unsigned)nh), dim3(256), lds, s, qkv,
-                       (nh + 2 * nkv) * hd, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
+                       stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }

@@ -271,7 +271,7 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
         if ((rc = aeth_prefill_rope_kv_launch(r->p_qkv, n, nh, nkv, hd, r->rope_sin, r->rope_cos, c.max_seq_len,
                                               lkv, s)))
             return rc;
-        if ((rc = aeth_attn_prefill_launch(r->p_qkv, lkv, n, nh, nkv, hd, c.max_seq_len, r->p_att, s))) return rc;
+        if ((rc = aeth_attn_prefill_launch(r->p_qkv, (nh + 2 * nkv) * hd, lkv, n, nh, nkv, hd, c.max_seq_len, r->p_att, s))) return rc;
         if ((rc = aeth_qmatmul(r->wo[l], r->p_att, n, r->p_x, AETH_MM_ACCUMULATE, s))) return rc;
         if ((rc = aeth_rmsnorm_launch(r->p_x, r->norms + (int64_t)l * 2 * d + d, n, d, c.rms_norm_eps, r->p_n, s)))
             return rc;

@@ -150,6 +150,13 @@ AETH_API int aeth_kv_append(float* d_layer_kv, const float* d_k, const float* d_
  * over positions [0, seq) of one layer slice of the static cache. */
 AETH_API int aeth_attn_decode(const float* d_q, const float* d_layer_kv, int64_t n_heads, int64_t kv_heads,
                               int64_t head_dim, int64_t max_seq, int64_t seq, float* d_out, void* stream);
+/* Causal GQA attention of a prompt batch (attention_batch, runner.rs:1809-1883):
+ * query i (row i of d_q, [n][q_stride] with head h at column h*head_dim, RoPE
+ * already applied) attends to cache slots 0..i of the layer slice d_layer_kv
+ * ([2][kv_heads][max_seq][head_dim]); d_out is [n][n_heads*head_dim]. */
+AETH_API int aeth_attn_prefill(const float* d_q, int64_t q_stride, const float* d_layer_kv, int64_t n,
+                               int64_t n_heads, int64_t kv_heads, int64_t head_dim, int64_t max_seq, float* d_out,
+                               void* stream);
 /* SiLU-MLP glue (runner.rs:1617-1625): g = g * sigmoid(g) * up. */
 AETH_API int aeth_silu_mul(float* d_gate, const float* d_up, int64_t n, void* stream);
 /* Residual add (runner.rs:1609-1611): x += y. */

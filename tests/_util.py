@@ -58,6 +58,27 @@ def assert_close(g, r, tol=1e-3, cos_min=0.9999, what=""):
     assert (cos > cos_min).all(), "%s: row cosine %r <= %r" % (what, cos.min(), cos_min)
 
 
+def assert_close_logits(g, r, tol=1e-3, floor=1e-5, cos_min=0.9999, what=""):
+    """Whole-model logits (a decode step or a prefill through every layer): the
+    element-wise bar of assert_close, where an element may also sit within
+    floor·max|r_row| of the reference. A logit is an f32 sum whose rounding scales
+    with the row's largest terms; in a row spanning ±658 (the Q8_0 test model) the
+    reference's own f32 order and any other exact-f32 order differ by a few 1e-3
+    on its small entries. Kernel-level outputs keep the plain element-wise bar."""
+    g = np.atleast_2d(np.asarray(g, dtype=np.float64))
+    r = np.atleast_2d(np.asarray(r, dtype=np.float64))
+    assert g.shape == r.shape, (g.shape, r.shape)
+    ok = close_mask(g, r, tol) | (np.abs(g - r) <= floor * np.abs(r).max(axis=1, keepdims=True))
+    if not ok.all():
+        i = np.argwhere(~ok)[0]
+        raise AssertionError("%s: %d/%d logits out of tolerance; first at %s: got %r ref %r (row max %r)" %
+                             (what, (~ok).sum(), ok.size, tuple(i), g[tuple(i)], r[tuple(i)], np.abs(r[i[0]]).max()))
+    num = (g * r).sum(axis=1)
+    den = np.sqrt((g * g).sum(axis=1) * (r * r).sum(axis=1))
+    cos = np.where(den > 0, num / np.where(den > 0, den, 1), 1.0)
+    assert (cos > cos_min).all(), "%s: row cosine %r <= %r" % (what, cos.min(), cos_min)
+
+
 def assert_close_rows(g, r, tol=1e-3, what=""):
     """For intermediate state (the KV cache): per row, |g-r| <= tol·max(1, max|r_row|).
     An entry's float error scales with the magnitudes summed into it, i.e. with

@@ -8,7 +8,7 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import Q4_K, Q6_K, Q8_0, assert_close, assert_close_rows, weight
+from tests._util import Q4_K, Q6_K, Q8_0, assert_close, assert_close_logits, assert_close_rows, weight
 
 pytestmark = pytest.mark.gpu
 
@@ -115,14 +115,49 @@ def test_argmax_last_max_wins(gpu):
     assert int(od.cpu()[0]) == 128000 == O.argmax(x)
 
 
+# Prefill attention (attention_batch, runner.rs:1809-1883) against an f64
+# restatement of its formula: s_t = (q·k_t)/√hd for t ≤ i, max-subtracted
+# softmax, Σ p_t v_t. Group sizes 1, 2, 4, 8 take the f32-MFMA kernel, 3 the
+# f32 VALU one; ragged n against the 16-key and query blocks, the 8B shape,
+# and sharp softmaxes (scaled q).
+@pytest.mark.parametrize("n,nh,nkv,max_seq,qs", [(1, 4, 4, 8, 1.0), (70, 8, 2, 96, 1.0), (150, 4, 2, 192, 3.0),
+                                                 (33, 8, 1, 40, 1.0), (64, 6, 2, 64, 1.0), (512, 32, 8, 512, 1.0),
+                                                 (97, 16, 4, 128, 4.0)])
+def test_attn_prefill_matches_f64(gpu, n, nh, nkv, max_seq, qs):
+    torch = gpu
+    hd = 128
+    rng = np.random.default_rng(n * 13 + nh)
+    stride = (nh + 2 * nkv) * hd
+    q = (rng.standard_normal((n, stride)) * qs).astype(np.float32)
+    kv = np.zeros((2, nkv, max_seq, hd), dtype=np.float32)
+    kv[:, :, :n] = rng.standard_normal((2, nkv, n, hd)).astype(np.float32)
+    out = torch.empty(n * nh * hd, dtype=torch.float32, device="cuda")
+    qd, kvd = torch.from_numpy(q).cuda(), torch.from_numpy(kv).cuda()  # kept alive across the launch
+    A.check(A.lib().aeth_attn_prefill(qd.data_ptr(), stride, kvd.data_ptr(), n, nh, nkv, hd, max_seq,
+                                      out.data_ptr(), None), "attn_prefill")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(n, nh, hd)
+    G = nh // nkv
+    ref = np.empty((n, nh, hd))
+    K = kv[0].astype(np.float64)
+    V = kv[1].astype(np.float64)
+    for h in range(nh):
+        qh = q[:, h * hd:(h + 1) * hd].astype(np.float64)
+        sc = qh @ K[h // G, :n].T / np.sqrt(hd)
+        sc[np.triu_indices(n, 1)] = -np.inf
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
+        ref[:, h] = (p / p.sum(axis=1, keepdims=True)) @ V[h // G, :n]
+    assert_close(got.reshape(n, -1), ref.reshape(n, -1), what="attn_prefill n=%d nh=%d nkv=%d" % (n, nh, nkv))
+    assert np.abs(got - ref).max() < 1e-5
+
+
 # ── device LlamaRunner vs the oracle's decode step ───────────────────────
 
 TINY = dict(vocab_size=512, d_model=256, num_layers=2, num_heads=4, num_kv_heads=2, head_dim=128, d_ff=512,
             max_seq_len=64, rope_base=10000.0, rms_norm_eps=1e-5)
 
 
-def build_tiny(seed=1, lm_dtype=Q6_K, layer_dtype=Q4_K):
-    c = TINY
+def build_tiny(seed=1, lm_dtype=Q6_K, layer_dtype=Q4_K, c=TINY):
     rng = np.random.default_rng(seed)
     d, qd, kvd, dff = c["d_model"], c["num_heads"] * c["head_dim"], c["num_kv_heads"] * c["head_dim"], c["d_ff"]
     shapes = [(qd, d), (kvd, d), (kvd, d), (d, qd), (dff, d), (dff, d), (d, dff)]
@@ -170,7 +205,7 @@ def test_runner_decode_matches_oracle(gpu, layer_dtype):
             A.check(L.aeth_runner_decode(r, tok, step, logits.ctypes.data, ctypes.byref(nxt)), "decode")
             ref, fill = O.decode_step(ocfg, m["emb"][tok], step, m["layers"], [layer_dtype] * 7, m["norms"], m["final"],
                                       m["lm"], m["lm_dtype"], s, co, kv, fill)
-            assert_close(logits, ref, what="step %d" % step)
+            assert_close_logits(logits, ref, what="step %d" % step)
             assert nxt.value == O.argmax(logits)
             tok = O.argmax(ref)  # teacher forcing on the CPU's token
         assert L.aeth_runner_seq_len(r) == 6
@@ -202,7 +237,7 @@ def test_runner_prefill_matches_oracle(gpu, layer_dtype, n, max_seq):
         A.check(L.aeth_runner_prefill(r, toks.ctypes.data, n, logits.ctypes.data, ctypes.byref(nxt)), "prefill")
         ref = O.forward_batch(ocfg, m["emb"][toks], m["layers"], [layer_dtype] * 7, m["norms"], m["final"], m["lm"],
                               m["lm_dtype"], s, co, kv)
-        assert_close(logits, ref, what="prefill n=%d" % n)
+        assert_close_logits(logits, ref, what="prefill n=%d" % n)
         assert nxt.value == O.argmax(logits)
         assert L.aeth_runner_seq_len(r) == n
         kv_dev = np.empty_like(kv)
@@ -218,7 +253,30 @@ def test_runner_prefill_matches_oracle(gpu, layer_dtype, n, max_seq):
             ref2, fill = O.decode_step(ocfg, m["emb"][tok], n, m["layers"], [layer_dtype] * 7, m["norms"], m["final"],
                                        m["lm"], m["lm_dtype"], s, co, kv, n)
             assert fill == n + 1 and L.aeth_runner_seq_len(r) == n + 1
-            assert_close(logits, ref2, what="decode after prefill")
+            assert_close_logits(logits, ref2, what="decode after prefill")
+    finally:
+        L.aeth_runner_free(r)
+
+
+# GQA group sizes G = query heads per KV head: the MFMA attention packs 16/G
+# queries × G heads into its 16 score columns (G = 2 is TINY above); n = 70 is
+# ragged against every query block, the 16-key blocks and the block pairs.
+@pytest.mark.parametrize("heads,kv_heads", [(4, 4), (8, 2), (8, 1)])
+def test_runner_prefill_gqa_groups(gpu, heads, kv_heads):
+    c = dict(TINY, num_heads=heads, num_kv_heads=kv_heads, max_seq_len=96)
+    n = 70
+    m = build_tiny(seed=heads * 10 + kv_heads, c=c)
+    r = make_runner(m, c)
+    L = A.lib()
+    s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
+    kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), dtype=np.float32)
+    toks = np.random.default_rng(heads).integers(0, c["vocab_size"], n).astype(np.int32)
+    try:
+        logits = np.empty(c["vocab_size"], dtype=np.float32)
+        A.check(L.aeth_runner_prefill(r, toks.ctypes.data, n, logits.ctypes.data, None), "prefill")
+        ref = O.forward_batch(oracle_cfg(c), m["emb"][toks], m["layers"], [Q4_K] * 7, m["norms"], m["final"], m["lm"],
+                              m["lm_dtype"], s, co, kv)
+        assert_close_logits(logits, ref, what="prefill heads=%d kv_heads=%d" % (heads, kv_heads))
     finally:
         L.aeth_runner_free(r)
 

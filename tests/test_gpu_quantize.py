@@ -55,8 +55,8 @@ def test_requantize_byte_exact(gpu, dtype, rows, cols):
     be, bb = GEOM[dtype]
     nbytes = rows * ((cols + be - 1) // be) * bb
     out = torch.full((nbytes,), 0xA5, dtype=torch.uint8, device="cuda")
-    A.check(A.lib().aeth_requantize(dtype, to_dev(torch, x).data_ptr(), rows, cols, out.data_ptr(), None),
-            "requantize")
+    xd = to_dev(torch, x)  # device copies stay referenced until the kernel has run
+    A.check(A.lib().aeth_requantize(dtype, xd.data_ptr(), rows, cols, out.data_ptr(), None), "requantize")
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     ref = O.requantize(dtype, x.ravel(), rows, cols)
@@ -76,7 +76,8 @@ def test_quantize_activations_q8_0_byte_exact(gpu, m, k):
         a[8, 0] = 127.0
     nbytes = m * ((k + 31) // 32) * 34
     out = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device="cuda")
-    A.check(A.lib().aeth_quantize_activations_q8_0(to_dev(torch, a).data_ptr(), m, k, out.data_ptr(), None), "quant")
+    ad = to_dev(torch, a)
+    A.check(A.lib().aeth_quantize_activations_q8_0(ad.data_ptr(), m, k, out.data_ptr(), None), "quant")
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     ref = O.quantize_activations_q8_0(a.ravel(), m, k)
@@ -93,7 +94,8 @@ def test_q8_0_activation_blocks_feed_the_dotprod_reference(gpu):
     m, n, k = 3, 24, 512
     a = rng.standard_normal((m, k)).astype(np.float32)
     out = torch.empty(m * (k // 32) * 34, dtype=torch.uint8, device="cuda")
-    A.check(A.lib().aeth_quantize_activations_q8_0(to_dev(torch, a).data_ptr(), m, k, out.data_ptr(), None), "quant")
+    ad = to_dev(torch, a)
+    A.check(A.lib().aeth_quantize_activations_q8_0(ad.data_ptr(), m, k, out.data_ptr(), None), "quant")
     torch.cuda.synchronize()
     aq = out.cpu().numpy()
     for dtype in (Q8_0, Q4_K):
@@ -115,7 +117,8 @@ def test_transpose_f32(gpu, rows, cols):
     torch = gpu
     x = np.random.default_rng(rows + cols).standard_normal((rows, cols)).astype(np.float32)
     out = torch.empty(rows * cols, dtype=torch.float32, device="cuda")
-    A.check(A.lib().aeth_transpose_f32(to_dev(torch, x).data_ptr(), rows, cols, out.data_ptr(), None), "transpose")
+    xd = to_dev(torch, x)
+    A.check(A.lib().aeth_transpose_f32(xd.data_ptr(), rows, cols, out.data_ptr(), None), "transpose")
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().reshape(cols, rows), x.T)
 
@@ -138,8 +141,8 @@ def test_load_quant_byte_exact_and_usable(gpu, dtype, k, n):
     raw = synth_blocks(dtype, (k * n + be - 1) // be, 100 + k + n + dtype).ravel()
     ws = torch.empty(L.aeth_load_quant_ws_bytes(k, n), dtype=torch.uint8, device="cuda")
     out = torch.empty(n * ((k + be - 1) // be) * bb, dtype=torch.uint8, device="cuda")
-    A.check(L.aeth_load_quant(dtype, to_dev(torch, raw).data_ptr(), k, n, out.data_ptr(), ws.data_ptr(), None),
-            "load_quant")
+    rawd = to_dev(torch, raw)
+    A.check(L.aeth_load_quant(dtype, rawd.data_ptr(), k, n, out.data_ptr(), ws.data_ptr(), None), "load_quant")
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     ref = load_quant_oracle(dtype, raw, k, n)
@@ -150,7 +153,8 @@ def test_load_quant_byte_exact_and_usable(gpu, dtype, k, n):
     A.check(L.aeth_weight_create(dtype, n, k, out.data_ptr(), 1, None, ctypes.byref(w)), "weight_create")
     x = np.random.default_rng(k).standard_normal(k).astype(np.float32)
     y = torch.empty(n, dtype=torch.float32, device="cuda")
-    A.check(L.aeth_qmatmul(w, to_dev(torch, x).data_ptr(), 1, y.data_ptr(), 0, None), "qmatmul")
+    xd = to_dev(torch, x)
+    A.check(L.aeth_qmatmul(w, xd.data_ptr(), 1, y.data_ptr(), 0, None), "qmatmul")
     torch.cuda.synchronize()
     L.aeth_weight_free(w)
     assert_close(y.cpu().numpy(), O.reference_matmul(dtype, x, ref, 1, n, k)[0], what="load_quant → GEMV")
