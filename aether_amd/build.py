@@ -21,6 +21,7 @@ SOURCES = [
     "aeth_prefill.hip",
     "aeth_host.cpp",
     "aeth_runner.cpp",
+    "aeth_gguf.cpp",
 ]
 ARCH = os.environ.get("AETH_OFFLOAD_ARCH", "gfx950")
 

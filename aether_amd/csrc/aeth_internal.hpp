@@ -49,3 +49,8 @@ int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d
 // Q4_K prefill GEMM (m > 1).
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s);
+
+// GGUF file → runner (aeth_gguf.cpp): LlamaModel::from_gguf on the device load path.
+struct aeth_runner;
+int aeth_gguf_load_runner(const char* path, aeth_runner** out, int* bos, int* eos);
+

@@ -614,21 +614,25 @@ extern "C" AETH_API int aeth_runner_export(const aeth_runner* r, int which, int3
 struct aether_model {
     aeth_runner* runner;
     float frame_budget_ms;
+    int bos_id, eos_id;
 };
 
 extern "C" AETHER_API aether_model* aether_model_from_runner(aeth_runner* r) {
     if (!r) return nullptr;
-    return new aether_model{r, 0.0f};
+    return new aether_model{r, 0.0f, 1, 2};
 }
 
-// GGUF file loading (gguf.rs:297-397) is not part of this build: the two
-// loaders report that through aether_last_error and return NULL.
+// aether_load (c_api.rs:41-74): GGUF file → device runner (aeth_gguf.cpp);
+// NULL with aether_last_error set on failure.
 extern "C" AETHER_API aether_model* aether_load(const char* path) {
-    aeth_set_error(AETH_EUNSUPPORTED, "aether_load(%s): GGUF file loading is not built; use aeth_runner_create",
-                   path ? path : "(null)");
-    return nullptr;
+    aeth_runner* r = nullptr;
+    int bos = 1, eos = 2;
+    if (aeth_gguf_load_runner(path, &r, &bos, &eos) != AETH_OK) return nullptr;
+    return new aether_model{r, 0.0f, bos, eos};
 }
 
+// aether_load_streaming (c_api.rs:76-102) keeps max_hot decoder layers resident on
+// the reference's CPU path; with 288 GB of HBM every layer stays on the device.
 extern "C" AETHER_API aether_model* aether_load_streaming(const char* path, int max_hot) {
     (void)max_hot;
     return aether_load(path);
@@ -644,9 +648,10 @@ extern "C" AETHER_API int aether_vocab_size(const aether_model* m) { return m ? 
 extern "C" AETHER_API int aether_context_len(const aether_model* m) { return m ? m->runner->cfg.max_seq_len : 0; }
 extern "C" AETHER_API int aether_num_layers(const aether_model* m) { return m ? m->runner->cfg.num_layers : 0; }
 extern "C" AETHER_API int aether_d_model(const aether_model* m) { return m ? m->runner->cfg.d_model : 0; }
-// Synthetic models carry no tokenizer metadata: the conventional LLaMA ids.
-extern "C" AETHER_API int aether_eos_id(const aether_model* m) { return m ? 2 : -1; }
-extern "C" AETHER_API int aether_bos_id(const aether_model* m) { return m ? 1 : -1; }
+// tokenizer.ggml.{eos,bos}_token_id of a loaded file (tokenizer/mod.rs:65-66);
+// the conventional LLaMA ids 2 / 1 otherwise.
+extern "C" AETHER_API int aether_eos_id(const aether_model* m) { return m ? m->eos_id : -1; }
+extern "C" AETHER_API int aether_bos_id(const aether_model* m) { return m ? m->bos_id : -1; }
 extern "C" AETHER_API int aether_num_gpu_layers(const aether_model* m) { return m ? m->runner->cfg.num_layers : 0; }
 extern "C" AETHER_API int aether_num_cpu_layers(const aether_model* m) { return m ? 0 : 0; }
 

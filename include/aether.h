@@ -5,9 +5,15 @@
  * Same functions, argument meaning and return codes as the reference:
  * 0 = AETHER_OK, -1 = AETHER_ERR, -2 = AETHER_TIMEOUT; logits buffers hold
  * aether_vocab_size() floats. Differences of this build:
- *   - aether_load / aether_load_streaming: GGUF file parsing is not built;
- *     they return NULL (message in aether_last_error). Models are created
- *     with aeth_runner_create (aether_hip.h) and wrapped by
+ *   - aether_load / aether_load_streaming read a GGUF v3 file (gguf.rs:297-397,
+ *     model_loader.rs:159-386) into the device runner: layer and LM-head
+ *     weights Q8_0 / Q4_K / Q6_K (q/k/v and gate/up sharing a dtype per
+ *     layer), norms F32 / F16, head_dim 128, at most 8 query heads per KV
+ *     head, no sliding window or partial RoPE, and a cache of
+ *     min(context_length, 8192) positions. max_hot is ignored: every layer
+ *     stays in HBM. Other files return NULL with the reason in
+ *     aether_last_error. Models can also be created with
+ *     aeth_runner_create (aether_hip.h) and wrapped by
  *     aether_model_from_runner — no counterpart in the reference.
  *   - aether_encode / aether_decode_token: no tokenizer (NULL).
  *   - aether_sample: greedy only (temperature <= 1e-6 or top_p <= 1e-6).
