@@ -177,6 +177,7 @@ struct GemmArgs {
     int gm, gn;                     // 64-row and 128-column tiles of C
     int a_bytes, q_bytes, h_bytes;  // buffer extents for the buffer-resource loads
     float* C;
+    int64_t ldc;  // row stride of C
     int accumulate;
 };
 
@@ -429,7 +430,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_ring(GemmArgs G) {
             const int row = m0 + 32 * wm + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
             if (row < G.m && col < G.n) {
                 const float v = acc[c][r] * G.escale[row];
-                float* dst = G.C + (int64_t)row * G.n + col;
+                float* dst = G.C + (int64_t)row * G.ldc + col;
                 *dst = G.accumulate ? *dst + v : v;
             }
         }
@@ -679,7 +680,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
                 const float sum = acc[mt][c][r] + red[((mt * 2 + c) * 16 + r) * 64 + lane];
                 if (row < G.m && col < G.n) {
                     const float v = sum * G.escale[row];
-                    float* dst = G.C + (int64_t)row * G.n + col;
+                    float* dst = G.C + (int64_t)row * G.ldc + col;
                     *dst = G.accumulate ? *dst + v : v;
                 }
             }
@@ -695,9 +696,15 @@ GemmWs g_gemm_ws[64];
 }  // namespace
 
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s) {
+                         hipStream_t s, int64_t ldc) {
     const int k = (int)w->k, nb = (int)w->nb;
-    if (k != nb * 256) return aeth_gemv_launch(w, d_a, m, d_c, flags, s);  // ragged K: row-batched GEMV
+    if (ldc <= 0) ldc = w->n;
+    if (k != nb * 256) {  // ragged K: row-batched GEMV
+        GemvEpi e;
+        e.flags = flags;
+        e.ldc = ldc;
+        return aeth_gemv_launch_ex(w, d_a, m, d_c, e, s);
+    }
     const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM;  // fragment rows: whole 64-row tiles
     if (mp > (1LL << 20) || mp * k > (1LL << 29)) return aeth_set_error(AETH_EINVAL, "gemm: m=%lld too large", (long long)m);
     // workspace: fragments [mp][k] × {hi, lo}, Sh, Sl [mp][k/32] (fp16), escale [mp] (f32)
@@ -730,7 +737,7 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     const int64_t qb = ntiles * nb * 2048, hb = ntiles * nb * 256, ab = mp * k * 4;
     GemmArgs G{(const uint8_t*)frag, Sh, Sl, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, (int)ntiles, gm, gn,
                (int)std::min(ab, (int64_t)INT32_MAX), (int)std::min(qb, (int64_t)INT32_MAX),
-               (int)std::min(hb, (int64_t)INT32_MAX), d_c, (flags & AETH_MM_ACCUMULATE) ? 1 : 0};
+               (int)std::min(hb, (int64_t)INT32_MAX), d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0};
     const bool fits32 = qb < INT32_MAX && ab < INT32_MAX;  // buffer offsets are 32-bit
     // AETH_GEMM_KERNEL=2 forces the single-K-group kernel (tuning and tests)
     static const int env_kernel = getenv("AETH_GEMM_KERNEL") ? atoi(getenv("AETH_GEMM_KERNEL")) : 0;

@@ -558,7 +558,7 @@ int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float
     G.x_stride = w->k;
     G.k = (int)w->k;
     G.y = d_y;
-    G.y_stride = e.swiglu ? w->n / 2 : w->n;
+    G.y_stride = e.ldc ? e.ldc : e.swiglu ? w->n / 2 : w->n;
     G.accumulate = (e.flags & AETH_MM_ACCUMULATE) ? 1 : 0;
     G.norm_w = e.norm_w;
     G.eps = e.eps;

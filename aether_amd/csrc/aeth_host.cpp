@@ -44,12 +44,19 @@ int workspace(int use, size_t bytes, void** out) {
 }
 }  // namespace
 
+int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
+                    hipStream_t s) {
+    if (m > 1 && w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
+    GemvEpi e;
+    e.flags = flags;
+    e.ldc = ldc;
+    return aeth_gemv_launch_ex(w, d_a, m, d_c, e, s);
+}
+
 extern "C" AETH_API int aeth_qmatmul(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                                      void* stream) {
     if (!w || !d_a || !d_c || m <= 0) return aeth_set_error(AETH_EINVAL, "aeth_qmatmul: bad argument");
-    hipStream_t s = (hipStream_t)stream;
-    if (m > 1 && w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s);
-    return aeth_gemv_launch(w, d_a, m, d_c, flags, s);
+    return aeth_qmatmul_ld(w, d_a, m, d_c, 0, flags, (hipStream_t)stream);
 }
 
 extern "C" AETH_API int aeth_rmsnorm(const float* d_x, const float* d_w, int64_t rows, int64_t n, float eps,

@@ -39,6 +39,7 @@ struct GemvEpi {
     float eps = 0.0f;
     int swiglu = 0;                       // rows are (gate, up) pairs; y gets n/2 outputs
     unsigned long long* amax = nullptr;   // fused greedy argmax key
+    int64_t ldc = 0;                      // output row stride for m > 1 (0: the output width)
 };
 
 // GEMV on one activation row per launch-row (a: [m][k] f32, c: [m][n]).
@@ -46,9 +47,12 @@ int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float
                         hipStream_t s);
 int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags,
                      hipStream_t s);
-// Q4_K prefill GEMM (m > 1).
+// Q4_K prefill GEMM (m > 1); ldc = output row stride (0: n).
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s);
+                         hipStream_t s, int64_t ldc = 0);
+// aeth_qmatmul with an output row stride (rows of c are ldc floats apart).
+int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
+                    hipStream_t s);
 
 // GGUF file → runner (aeth_gguf.cpp): LlamaModel::from_gguf on the device load path.
 struct aeth_runner;

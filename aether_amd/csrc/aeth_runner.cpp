@@ -26,6 +26,8 @@ struct aeth_runner {
     // per layer: q|k|v rows concatenated; gate and up rows interleaved
     // (row 2i = gate_i, row 2i+1 = up_i) for the fused SwiGLU epilogue
     std::vector<aeth_weight*> wqkv, wo, wgu, wdown;
+    // per layer, set when q/k/v (gate/up) do not share a dtype: the fused weight is then NULL
+    std::vector<aeth_weight*> wq, wk, wv, wg, wu;
     std::vector<int> dtypes;                         // per layer x 7
     aeth_weight* lm_head = nullptr;
     float* norms = nullptr;       // [L][2][d]
@@ -150,6 +152,8 @@ void runner_release(aeth_runner* r) {
     for (auto* w : r->wqkv) aeth_weight_free(w);
     for (auto* w : r->wo) aeth_weight_free(w);
     for (auto* w : r->wgu) aeth_weight_free(w);
+    for (auto* v : {&r->wq, &r->wk, &r->wv, &r->wg, &r->wu})
+        for (auto* w : *v) aeth_weight_free(w);
     for (auto* w : r->wdown) aeth_weight_free(w);
     aeth_weight_free(r->lm_head);
     void* bufs[] = {r->norms, r->final_norm, r->emb, r->rope_sin, r->rope_cos, r->kv, r->x, r->normed, r->qkv,
@@ -178,7 +182,15 @@ int enqueue_layers(aeth_runner* r, int l0, int l1) {
         GemvEpi e1;
         e1.norm_w = r->norms + (int64_t)l * 2 * d;
         e1.eps = c.rms_norm_eps;
-        if ((rc = aeth_gemv_launch_ex(r->wqkv[l], r->x, 1, r->qkv, e1, s))) return rc;
+        if (r->wqkv[l]) {
+            if ((rc = aeth_gemv_launch_ex(r->wqkv[l], r->x, 1, r->qkv, e1, s))) return rc;
+        } else {  // q, k, v of different formats: three GEMVs into the q|k|v vector
+            const int64_t qd = nh * hd, kvd = nkv * hd;
+            if ((rc = aeth_gemv_launch_ex(r->wq[l], r->x, 1, r->qkv, e1, s)) ||
+                (rc = aeth_gemv_launch_ex(r->wk[l], r->x, 1, r->qkv + qd, e1, s)) ||
+                (rc = aeth_gemv_launch_ex(r->wv[l], r->x, 1, r->qkv + qd + kvd, e1, s)))
+                return rc;
+        }
         if ((rc = aeth_attn_launch(nullptr, r->qkv, lkv, r->rope_sin, r->rope_cos, r->st, 0, nh, nkv, hd,
                                    c.max_seq_len, r->attn_ws, r->attn, s)))
             return rc;
@@ -188,8 +200,16 @@ int enqueue_layers(aeth_runner* r, int l0, int l1) {
         GemvEpi e3;
         e3.norm_w = r->norms + (int64_t)l * 2 * d + d;
         e3.eps = c.rms_norm_eps;
-        e3.swiglu = 1;
-        if ((rc = aeth_gemv_launch_ex(r->wgu[l], r->x, 1, r->gu, e3, s))) return rc;
+        if (r->wgu[l]) {
+            e3.swiglu = 1;
+            if ((rc = aeth_gemv_launch_ex(r->wgu[l], r->x, 1, r->gu, e3, s))) return rc;
+        } else {  // gate and up of different formats: g, u, then g·σ(g)·u in place
+            const int64_t dff = c.d_ff;
+            if ((rc = aeth_gemv_launch_ex(r->wg[l], r->x, 1, r->gu, e3, s)) ||
+                (rc = aeth_gemv_launch_ex(r->wu[l], r->x, 1, r->gu + dff, e3, s)) ||
+                (rc = aeth_silu_mul_launch(r->gu, r->gu + dff, dff, s)))
+                return rc;
+        }
         if ((rc = aeth_gemv_launch_ex(r->wdown[l], r->gu, 1, r->x, e2, s))) return rc;
     }
     return AETH_OK;
@@ -267,7 +287,15 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
         float* lkv = r->kv + (int64_t)l * kv_layer_floats(c);
         if ((rc = aeth_rmsnorm_launch(r->p_x, r->norms + (int64_t)l * 2 * d, n, d, c.rms_norm_eps, r->p_n, s)))
             return rc;
-        if ((rc = aeth_qmatmul(r->wqkv[l], r->p_n, n, r->p_qkv, 0, s))) return rc;
+        if (r->wqkv[l]) {
+            if ((rc = aeth_qmatmul(r->wqkv[l], r->p_n, n, r->p_qkv, 0, s))) return rc;
+        } else {  // separate q, k, v into the columns of the [n][q|k|v] rows
+            const int64_t qd = nh * hd, kvd = nkv * hd, ld = qd + 2 * kvd;
+            if ((rc = aeth_qmatmul_ld(r->wq[l], r->p_n, n, r->p_qkv, ld, 0, s)) ||
+                (rc = aeth_qmatmul_ld(r->wk[l], r->p_n, n, r->p_qkv + qd, ld, 0, s)) ||
+                (rc = aeth_qmatmul_ld(r->wv[l], r->p_n, n, r->p_qkv + qd + kvd, ld, 0, s)))
+                return rc;
+        }
         if ((rc = aeth_prefill_rope_kv_launch(r->p_qkv, n, nh, nkv, hd, r->rope_sin, r->rope_cos, c.max_seq_len,
                                               lkv, s)))
             return rc;
@@ -275,9 +303,18 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
         if ((rc = aeth_qmatmul(r->wo[l], r->p_att, n, r->p_x, AETH_MM_ACCUMULATE, s))) return rc;
         if ((rc = aeth_rmsnorm_launch(r->p_x, r->norms + (int64_t)l * 2 * d + d, n, d, c.rms_norm_eps, r->p_n, s)))
             return rc;
-        if ((rc = aeth_qmatmul(r->wgu[l], r->p_n, n, r->p_gu, 0, s))) return rc;
-        if ((rc = aeth_silu_pairs_launch(r->p_gu, n * dff, r->p_h, s))) return rc;
-        if ((rc = aeth_qmatmul(r->wdown[l], r->p_h, n, r->p_x, AETH_MM_ACCUMULATE, s))) return rc;
+        const float* h = r->p_h;
+        if (r->wgu[l]) {
+            if ((rc = aeth_qmatmul(r->wgu[l], r->p_n, n, r->p_gu, 0, s))) return rc;
+            if ((rc = aeth_silu_pairs_launch(r->p_gu, n * dff, r->p_h, s))) return rc;
+        } else {  // g [n][dff], u [n][dff], then g·σ(g)·u in place
+            if ((rc = aeth_qmatmul(r->wg[l], r->p_n, n, r->p_gu, 0, s)) ||
+                (rc = aeth_qmatmul(r->wu[l], r->p_n, n, r->p_gu + n * dff, 0, s)) ||
+                (rc = aeth_silu_mul_launch(r->p_gu, r->p_gu + n * dff, n * dff, s)))
+                return rc;
+            h = r->p_gu;
+        }
+        if ((rc = aeth_qmatmul(r->wdown[l], h, n, r->p_x, AETH_MM_ACCUMULATE, s))) return rc;
     }
     // head on the last row; the state update then leaves pos = fill = n
     AETH_HIP_CHECK(hipMemcpyAsync(r->x, r->p_x + (int64_t)(n - 1) * d, sizeof(float) * d, hipMemcpyDeviceToDevice, s));
@@ -351,16 +388,24 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
         const void* const* W = layer_weights ? layer_weights + (size_t)l * 7 : nullptr;
         auto hw = [&](int j) -> const void* { return W ? W[j] : nullptr; };
         aeth_weight* w = nullptr;
-        if (T[0] != T[1] || T[0] != T[2] || T[4] != T[5]) {
-            runner_release(r);
-            return aeth_set_error(AETH_EUNSUPPORTED, "runner: q/k/v and gate/up must share a dtype per layer");
+        // q|k|v rows fused into one weight, gate/up rows interleaved (SwiGLU epilogue),
+        // when they share a dtype; separate weights otherwise (mixed-format files)
+        for (auto* v : {&r->wqkv, &r->wq, &r->wk, &r->wv, &r->wgu, &r->wg, &r->wu}) v->push_back(nullptr);
+        if (T[0] == T[1] && T[0] == T[2]) {
+            RC(make_concat(T[0], {qd, kvd, kvd}, d, {hw(0), hw(1), hw(2)}, mix(seed, l, 1), s, &r->wqkv[l]));
+        } else {
+            RC(make_weight(T[0], qd, d, hw(0), mix(seed, l, 1), s, &r->wq[l]));
+            RC(make_weight(T[1], kvd, d, hw(1), mix(seed, l, 2), s, &r->wk[l]));
+            RC(make_weight(T[2], kvd, d, hw(2), mix(seed, l, 3), s, &r->wv[l]));
         }
-        RC(make_concat(T[0], {qd, kvd, kvd}, d, {hw(0), hw(1), hw(2)}, mix(seed, l, 1), s, &w));
-        r->wqkv.push_back(w);
         RC(make_weight(T[3], d, qd, hw(3), mix(seed, l, 4), s, &w));
         r->wo.push_back(w);
-        RC(make_interleaved(T[4], dff, d, hw(4), hw(5), mix(seed, l, 5), s, &w));
-        r->wgu.push_back(w);
+        if (T[4] == T[5]) {
+            RC(make_interleaved(T[4], dff, d, hw(4), hw(5), mix(seed, l, 5), s, &r->wgu[l]));
+        } else {
+            RC(make_weight(T[4], dff, d, hw(4), mix(seed, l, 5), s, &r->wg[l]));
+            RC(make_weight(T[5], dff, d, hw(5), mix(seed, l, 6), s, &r->wu[l]));
+        }
         RC(make_weight(T[6], d, dff, hw(6), mix(seed, l, 7), s, &w));
         r->wdown.push_back(w);
     }
@@ -414,7 +459,7 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
     RC(dmalloc(&r->normed, d > dff ? d : dff));
     RC(dmalloc(&r->qkv, qd + 2 * kvd));
     RC(dmalloc(&r->attn, qd));
-    RC(dmalloc(&r->gu, dff));
+    RC(dmalloc(&r->gu, 2 * dff));  // h, or g | u when gate and up are separate
     RC(dmalloc(&r->logits, c.vocab_size));
     RC(dmalloc(&r->attn_ws, aeth_attn_ws_floats(c.num_heads, c.head_dim, c.max_seq_len)));
     if (hipMemset(r->attn_ws, 0, sizeof(float) * aeth_attn_ws_floats(c.num_heads, c.head_dim, c.max_seq_len)) !=
@@ -569,6 +614,11 @@ extern "C" AETH_API int aeth_runner_export(const aeth_runner* r, int which, int3
     AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
     if (which >= 0 && which <= 6) {
         if (l < 0 || l >= c.num_layers) return aeth_set_error(AETH_EINVAL, "export: layer out of range");
+        const aeth_weight* sep[7] = {r->wq[l], r->wk[l], r->wv[l], nullptr, r->wg[l], r->wu[l], nullptr};
+        if (sep[which]) {  // a separately stored weight: its bytes as they are
+            if (host_bytes < sep[which]->bytes) return aeth_set_error(AETH_EINVAL, "export: buffer too small");
+            return aeth_weight_export_raw(sep[which], host, 0, r->stream);
+        }
         const aeth_weight* w = which <= 2 ? r->wqkv[l] : which == 3 ? r->wo[l] : which <= 5 ? r->wgu[l] : r->wdown[l];
         std::vector<uint8_t> all((size_t)w->bytes);
         int rc = aeth_weight_export_raw(w, all.data(), 0, r->stream);

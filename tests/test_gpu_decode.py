@@ -158,23 +158,25 @@ TINY = dict(vocab_size=512, d_model=256, num_layers=2, num_heads=4, num_kv_heads
 
 
 def build_tiny(seed=1, lm_dtype=Q6_K, layer_dtype=Q4_K, c=TINY):
+    """layer_dtype: one format for all seven layer weights, or a list of seven (q k v o gate up down)."""
+    dts = list(layer_dtype) if isinstance(layer_dtype, (list, tuple)) else [layer_dtype] * 7
     rng = np.random.default_rng(seed)
     d, qd, kvd, dff = c["d_model"], c["num_heads"] * c["head_dim"], c["num_kv_heads"] * c["head_dim"], c["d_ff"]
     shapes = [(qd, d), (kvd, d), (kvd, d), (d, qd), (dff, d), (dff, d), (d, dff)]
-    layers = [[weight(layer_dtype, n, k, seed * 100 + l * 7 + j) for j, (n, k) in enumerate(shapes)]
+    layers = [[weight(dts[j], n, k, seed * 100 + l * 7 + j) for j, (n, k) in enumerate(shapes)]
               for l in range(c["num_layers"])]
     norms = [[(1 + 0.02 * rng.standard_normal(d)).astype(np.float32) for _ in range(2)] for _ in range(c["num_layers"])]
     final = (1 + 0.02 * rng.standard_normal(d)).astype(np.float32)
     lm = weight(lm_dtype, c["vocab_size"], d, seed * 31)
     emb = rng.standard_normal((c["vocab_size"], d)).astype(np.float32)
-    return dict(layers=layers, norms=norms, final=final, lm=lm, emb=emb, lm_dtype=lm_dtype, layer_dtype=layer_dtype)
+    return dict(layers=layers, norms=norms, final=final, lm=lm, emb=emb, lm_dtype=lm_dtype, layer_dtype=dts)
 
 
 def make_runner(m, c=TINY):
     cfg = A.LlamaConfig(**c)
     nl = c["num_layers"]
     wp = (ctypes.c_void_p * (nl * 7))(*[m["layers"][l][j].ctypes.data for l in range(nl) for j in range(7)])
-    dt = (ctypes.c_int32 * (nl * 7))(*([m["layer_dtype"]] * nl * 7))
+    dt = (ctypes.c_int32 * (nl * 7))(*(m["layer_dtype"] * nl))
     npp = (ctypes.c_void_p * (nl * 2))(*[m["norms"][l][j].ctypes.data for l in range(nl) for j in range(2)])
     r = ctypes.c_void_p()
     A.check(A.lib().aeth_runner_create(ctypes.byref(cfg), wp, dt, npp, m["final"].ctypes.data, m["lm"].ctypes.data,
@@ -277,6 +279,48 @@ def test_runner_prefill_gqa_groups(gpu, heads, kv_heads):
         ref = O.forward_batch(oracle_cfg(c), m["emb"][toks], m["layers"], [Q4_K] * 7, m["norms"], m["final"], m["lm"],
                               m["lm_dtype"], s, co, kv)
         assert_close_logits(logits, ref, what="prefill heads=%d kv_heads=%d" % (heads, kv_heads))
+    finally:
+        L.aeth_runner_free(r)
+
+
+# Files that mix formats inside a layer (llama.cpp's Q4_K_M keeps attn_v and
+# ffn_down in Q6_K): q/k/v and gate/up of different formats are run as separate
+# weights (three GEMVs into q|k|v, gate and up GEMVs then SiLU·up; strided GEMM
+# columns in prefill). n = 150 takes the Q4_K GEMM with the output row stride.
+MIXED = [[Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K],     # Q4_K_M
+         [Q8_0, Q4_K, Q6_K, Q6_K, Q4_K, Q8_0, Q4_K]]     # every split, GEMV and GEMM columns
+
+
+@pytest.mark.parametrize("mix", [0, 1])
+@pytest.mark.parametrize("n", [1, 23, 150])
+def test_runner_mixed_formats(gpu, mix, n):
+    c = dict(TINY, max_seq_len=192)
+    m = build_tiny(seed=11 + mix, layer_dtype=MIXED[mix], c=c)
+    r = make_runner(m, c)
+    L = A.lib()
+    ocfg = oracle_cfg(c)
+    s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
+    kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), dtype=np.float32)
+    toks = np.random.default_rng(n).integers(0, c["vocab_size"], n).astype(np.int32)
+    try:
+        logits = np.empty(c["vocab_size"], dtype=np.float32)
+        A.check(L.aeth_runner_prefill(r, toks.ctypes.data, n, logits.ctypes.data, None), "prefill")
+        ref = O.forward_batch(ocfg, m["emb"][toks], m["layers"], MIXED[mix], m["norms"], m["final"], m["lm"],
+                              m["lm_dtype"], s, co, kv)
+        assert_close_logits(logits, ref, what="mixed prefill n=%d" % n)
+        fill = n
+        tok = O.argmax(ref)
+        for step in range(2):
+            A.check(L.aeth_runner_decode(r, tok, fill, logits.ctypes.data, None), "mixed decode")
+            ref, fill = O.decode_step(ocfg, m["emb"][tok], fill, m["layers"], MIXED[mix], m["norms"], m["final"],
+                                      m["lm"], m["lm_dtype"], s, co, kv, fill)
+            assert_close_logits(logits, ref, what="mixed decode step %d" % step)
+            tok = O.argmax(ref)
+        # separately stored weights export as they were given
+        for j in range(7):
+            blob = np.empty(m["layers"][1][j].nbytes, dtype=np.uint8)
+            A.check(L.aeth_runner_export(r, j, 1, blob.ctypes.data, blob.nbytes), "export %d" % j)
+            assert np.array_equal(blob, m["layers"][1][j].view(np.uint8).ravel()), "export %d" % j
     finally:
         L.aeth_runner_free(r)
 

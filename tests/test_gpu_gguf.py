@@ -31,6 +31,7 @@ def quant_gguf(dtype, k, n, seed):
 def build_file(path, layer_dtype=Q4_K, lm_dtype=Q6_K, f16_norms=False, context=64, extra_meta=(), drop=None,
                override=None):
     c = CFG
+    dts = list(layer_dtype) if isinstance(layer_dtype, (list, tuple)) else [layer_dtype] * 7
     d, dff, v = c["d_model"], c["d_ff"], c["vocab_size"]
     qd, kvd = c["num_heads"] * c["head_dim"], c["num_kv_heads"] * c["head_dim"]
     rng = np.random.default_rng(5)
@@ -56,8 +57,8 @@ def build_file(path, layer_dtype=Q4_K, lm_dtype=Q6_K, f16_norms=False, context=6
         model["norms"].append([an, fn])
         ws = []
         for j, (n, k) in enumerate(shapes):
-            raw, qw = quant_gguf(layer_dtype, k, n, 1000 + 10 * l + j)
-            tensors.append(("blk.%d.%s.weight" % (l, names[j]), [k, n], layer_dtype, raw))
+            raw, qw = quant_gguf(dts[j], k, n, 1000 + 10 * l + j)
+            tensors.append(("blk.%d.%s.weight" % (l, names[j]), [k, n], dts[j], raw))
             ws.append(qw)
         model["layers"].append(ws)
     model["final"] = norm("output_norm.weight")
@@ -81,7 +82,7 @@ def build_file(path, layer_dtype=Q4_K, lm_dtype=Q6_K, f16_norms=False, context=6
             ("tokenizer.ggml.bos_token_id", U32, 7),
             ("tokenizer.ggml.eos_token_id", U32, 9)] + list(extra_meta)
     write_gguf(str(path), meta, tensors)
-    model["layer_dtype"], model["lm_dtype"] = layer_dtype, lm_dtype
+    model["layer_dtype"], model["lm_dtype"] = dts, lm_dtype
     return model
 
 
@@ -89,7 +90,10 @@ def last_error(L):
     return ctypes.cast(L.aether_last_error(), ctypes.c_char_p).value.decode()
 
 
-@pytest.mark.parametrize("layer_dtype,f16_norms", [(Q4_K, False), (Q8_0, True), (Q6_K, False)])
+Q4_K_M = [Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K]   # llama.cpp's mix: attn_v and ffn_down in Q6_K
+
+
+@pytest.mark.parametrize("layer_dtype,f16_norms", [(Q4_K, False), (Q8_0, True), (Q6_K, False), (Q4_K_M, False)])
 def test_aether_load_prefill_decode_match_oracle(gpu, tmp_path, layer_dtype, f16_norms):
     L = A.lib()
     path = tmp_path / "tiny.gguf"
@@ -108,12 +112,12 @@ def test_aether_load_prefill_decode_match_oracle(gpu, tmp_path, layer_dtype, f16
         toks = np.random.default_rng(3).integers(0, c["vocab_size"], 20).astype(np.int32)
         logits = np.empty(c["vocab_size"], dtype=np.float32)
         assert L.aether_prefill(m, toks.ctypes.data, len(toks), logits.ctypes.data) == 0, last_error(L)
-        ref = O.forward_batch(ocfg, mdl["emb"][toks], mdl["layers"], [layer_dtype] * 7, mdl["norms"], mdl["final"],
+        ref = O.forward_batch(ocfg, mdl["emb"][toks], mdl["layers"], mdl["layer_dtype"], mdl["norms"], mdl["final"],
                               mdl["lm"], mdl["lm_dtype"], s, co, kv)
         assert_close_logits(logits, ref, what="aether_load prefill")
         tok = int(np.argmax(ref))
         assert L.aether_decode(m, tok, len(toks), logits.ctypes.data) == 0, last_error(L)
-        ref2, _ = O.decode_step(ocfg, mdl["emb"][tok], len(toks), mdl["layers"], [layer_dtype] * 7, mdl["norms"],
+        ref2, _ = O.decode_step(ocfg, mdl["emb"][tok], len(toks), mdl["layers"], mdl["layer_dtype"], mdl["norms"],
                                 mdl["final"], mdl["lm"], mdl["lm_dtype"], s, co, kv, len(toks))
         assert_close_logits(logits, ref2, what="aether_load decode")
     finally:
