@@ -43,7 +43,7 @@
 #include <immintrin.h>
 #endif
 
-#define ORC_API __attribute__((visibility("default")))
+#include "oracle.h"
 
 /* ── f16 <-> f32 (third-party `half` 2.7.1, Cargo.lock:926-928) ─────────── */
 
@@ -285,6 +285,21 @@ ORC_API void orc_avx2_matmul_q6_k(const float* a, const uint8_t* b, size_t m, si
 #else
     kquant_avx2_order_scalar(orc_dequant_q6_k_block, 210, a, b, m, n, k, c);
 #endif
+}
+
+/* avx2::matmul_q5_k, avx2.rs:97-131 (dequant_q5_k_block, dequant.rs:542-584). */
+ORC_API void orc_avx2_matmul_q5_k(const float* a, const uint8_t* b, size_t m, size_t n, size_t k,
+                                  float* c) {
+#if defined(__AVX2__)
+    kquant_avx2(orc_dequant_q5_k_block, 176, a, b, m, n, k, c);
+#else
+    kquant_avx2_order_scalar(orc_dequant_q5_k_block, 176, a, b, m, n, k, c);
+#endif
+}
+
+ORC_API void orc_avx2order_scalar_matmul_q5_k(const float* a, const uint8_t* b, size_t m, size_t n,
+                                              size_t k, float* c) {
+    kquant_avx2_order_scalar(orc_dequant_q5_k_block, 176, a, b, m, n, k, c);
 }
 
 ORC_API void orc_avx2order_scalar_matmul_q4_k(const float* a, const uint8_t* b, size_t m, size_t n,
@@ -810,20 +825,28 @@ typedef struct {
     float rope_base, eps;
 } orc_llama_cfg;
 
-enum { ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14 };
+enum { ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14 };
 
-/* quantized_matmul_impl's x86 route (dispatch.rs:98-135 → avx2_dispatch.rs), m rows. */
+/* quantized_matmul_impl's x86 route (dispatch.rs:98-135 → avx2_dispatch.rs), m rows:
+ * Q4_K / Q5_K / Q6_K through the AVX2 f32 pipeline, Q8_0 through its scalar
+ * kernel (the AVX2 one mis-addresses, above), every other format (F32, F16,
+ * Q2_K, Q3_K: weights kept in GGUF [k][n] order) dequantized and multiplied
+ * by matmul_f32_gguf. */
 static void orc_qmatmul_m(int dtype, const float* a, size_t m, const uint8_t* w, size_t n, size_t k, float* c) {
     if (dtype == ORC_Q4_K) orc_avx2_matmul_q4_k(a, w, m, n, k, c);
+    else if (dtype == ORC_Q5_K) orc_avx2_matmul_q5_k(a, w, m, n, k, c);
     else if (dtype == ORC_Q6_K) orc_avx2_matmul_q6_k(a, w, m, n, k, c);
-    else orc_scalar_matmul_q8_0(a, w, n * ((k + 31) / 32) * 34, m, n, k, c);
+    else if (dtype == ORC_Q8_0) orc_scalar_matmul_q8_0(a, w, n * ((k + 31) / 32) * 34, m, n, k, c);
+    else if (orc_gguf_order_matmul(dtype, a, m, w, n, k, c) != 0) memset(c, 0, m * n * sizeof(float));
 }
 
 static void orc_qmatmul(int dtype, const float* a, const uint8_t* w, size_t n, size_t k, float* c) {
     orc_qmatmul_m(dtype, a, 1, w, n, k, c);
 }
 
-/* weights[l*7 + {0..6}] = q,k,v,o,gate,up,down raw row-major [out][in] blocks;
+/* weights[l*7 + {0..6}] = q,k,v,o,gate,up,down: Q8_0/Q4_K/Q5_K/Q6_K as raw
+ * row-major [out][in] blocks (load_quant's transposed form), F32/F16/Q2_K/Q3_K
+ * as the file holds them, GGUF [in][out] order;
  * norms[l*2 + {0,1}] = attn_norm, ffn_norm; kv = StaticKVCache storage
  * [L][2][kv_heads][max_seq][hd] (kv_cache.rs:9-31); *seq_len is the cache's
  * fill and is advanced on return. x holds the token's embedding row. */

@@ -14,15 +14,16 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 _lib = None
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-BLOCK_ELEMS = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
+F32, F16, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 1, 8, 10, 11, 12, 13, 14
+BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+_SOURCES = ("oracle.c", "oracle_formats.c", "oracle.h", "Makefile")
 
 
 def build(force=False):
     """Compile liboracle.so with the committed Makefile (gcc)."""
     if force or not os.path.exists(_LIB_PATH) or (
-        os.path.getmtime(_LIB_PATH) < os.path.getmtime(os.path.join(_HERE, "oracle.c"))
+        os.path.getmtime(_LIB_PATH) < max(os.path.getmtime(os.path.join(_HERE, f)) for f in _SOURCES)
     ):
         subprocess.check_call(["make", "-s", "-B" if force else "-s", "-C", _HERE])
     return _LIB_PATH
@@ -97,6 +98,10 @@ def dequant(dtype, data, n):
         L.orc_dequant_q4_k(_p(data, ctypes.c_uint8), ctypes.c_size_t(n), _p(out, ctypes.c_float))
     elif dtype == Q6_K:
         L.orc_dequant_q6_k(_p(data, ctypes.c_uint8), ctypes.c_size_t(n), _p(out, ctypes.c_float))
+    elif dtype in (F32, F16, Q2_K, Q3_K, Q5_K):
+        if L.orc_dequant_any(ctypes.c_int(dtype), _p(data, ctypes.c_uint8), ctypes.c_size_t(n),
+                             _p(out, ctypes.c_float)) != 0:
+            raise ValueError(dtype)
     else:
         raise ValueError(dtype)
     return out
@@ -121,16 +126,25 @@ def avx2_matmul(dtype, a, b, m, n, k):
     L = lib()
     if dtype == Q4_K:
         return _mm(L.orc_avx2_matmul_q4_k, a, b, m, n, k)
+    if dtype == Q5_K:
+        return _mm(L.orc_avx2_matmul_q5_k, a, b, m, n, k)
     if dtype == Q6_K:
         return _mm(L.orc_avx2_matmul_q6_k, a, b, m, n, k)
     if dtype == Q8_0:
         return _mm(L.orc_avx2_matmul_q8_0, a, b, m, n, k, with_len=True)
+    if dtype == Q2_K:
+        return _mm(L.orc_avx2order_matmul_q2_k, a, b, m, n, k)
+    if dtype == Q3_K:
+        return _mm(L.orc_avx2order_matmul_q3_k, a, b, m, n, k)
+    if dtype == F16:
+        return _mm(L.orc_avx2order_matmul_f16, a, b, m, n, k)
     raise ValueError(dtype)
 
 
 def avx2order_scalar_matmul(dtype, a, b, m, n, k):
     L = lib()
-    fn = {Q4_K: L.orc_avx2order_scalar_matmul_q4_k, Q6_K: L.orc_avx2order_scalar_matmul_q6_k}[dtype]
+    fn = {Q4_K: L.orc_avx2order_scalar_matmul_q4_k, Q5_K: L.orc_avx2order_scalar_matmul_q5_k,
+          Q6_K: L.orc_avx2order_scalar_matmul_q6_k}[dtype]
     return _mm(fn, a, b, m, n, k)
 
 
@@ -142,16 +156,43 @@ def scalar_matmul(dtype, a, b, m, n, k):
         return _mm(L.orc_scalar_matmul_q4_k, a, b, m, n, k)
     if dtype == Q6_K:
         return _mm(L.orc_scalar_matmul_q6_k, a, b, m, n, k)
-    raise ValueError(dtype)
+    fn = {Q5_K: L.orc_scalar_matmul_q5_k, Q2_K: L.orc_scalar_matmul_q2_k, Q3_K: L.orc_scalar_matmul_q3_k,
+          F16: L.orc_scalar_matmul_f16}.get(dtype)
+    if fn is None:
+        raise ValueError(dtype)
+    return _mm(fn, a, b, m, n, k)
 
 
 def reference_matmul(dtype, a, b, m, n, k):
-    """What the reference computes on an x86 AVX2 host for this dtype, except
-    Q8_0, whose AVX2 kernel mis-addresses its quants (see oracle.c); Q8_0 uses
-    the scalar kernel, which is the format's stated semantics."""
+    """What the reference computes on an x86 AVX2 host for this dtype on
+    [n][k] row-major weights (matmul_q*, matmul_f16), except Q8_0, whose AVX2
+    kernel mis-addresses its quants (see oracle.c); Q8_0 uses the scalar
+    kernel, which is the format's stated semantics."""
     if dtype == Q8_0:
         return scalar_matmul(dtype, a, b, m, n, k)
     return avx2_matmul(dtype, a, b, m, n, k)
+
+
+def matmul_f32_gguf(a, b, m, n, k):
+    """matmul_f32_gguf (dispatch.rs:541-574): b is f32 [k][n] (GGUF order)."""
+    a, b = _f32(a), _f32(b)
+    c = np.empty(m * n, dtype=np.float32)
+    lib().orc_matmul_f32_gguf(_p(a, ctypes.c_float), _p(b, ctypes.c_float), ctypes.c_size_t(m),
+                              ctypes.c_size_t(n), ctypes.c_size_t(k), _p(c, ctypes.c_float))
+    return c.reshape(m, n)
+
+
+def gguf_order_matmul(dtype, a, b, m, n, k):
+    """quantized_matmul_impl's fallback for F32/F16/Q2_K/Q3_K weights kept in
+    GGUF [k][n] order: dequantize(b, [k, n]) then matmul_f32_gguf."""
+    a, b = _f32(a), _u8(b)
+    c = np.empty(m * n, dtype=np.float32)
+    rc = lib().orc_gguf_order_matmul(ctypes.c_int(dtype), _p(a, ctypes.c_float), ctypes.c_size_t(m),
+                                     _p(b, ctypes.c_uint8), ctypes.c_size_t(n), ctypes.c_size_t(k),
+                                     _p(c, ctypes.c_float))
+    if rc != 0:
+        raise ValueError(dtype)
+    return c.reshape(m, n)
 
 
 # ── requantize / Q8 activations / dotprod references ────────────────────
@@ -160,7 +201,7 @@ def requantize(dtype, data, rows, cols):
     data = _f32(data)
     be, bb = BLOCK_ELEMS[dtype], BLOCK_BYTES[dtype]
     out = np.zeros(rows * ((cols + be - 1) // be) * bb, dtype=np.uint8)
-    fn = {Q8_0: lib().orc_requantize_q8_0, Q4_K: lib().orc_requantize_q4_k,
+    fn = {Q8_0: lib().orc_requantize_q8_0, Q4_K: lib().orc_requantize_q4_k, Q5_K: lib().orc_requantize_q5_k,
           Q6_K: lib().orc_requantize_q6_k}[dtype]
     fn(_p(data, ctypes.c_float), ctypes.c_size_t(rows), ctypes.c_size_t(cols), _p(out, ctypes.c_uint8))
     return out
@@ -178,7 +219,8 @@ def dotprod_ref(dtype, aq, b, m, n, k):
     aq = _u8(aq)
     b = _u8(b)
     c = np.empty(m * n, dtype=np.float32)
-    fn = {Q8_0: lib().orc_dotprod_ref_q8_0, Q4_K: lib().orc_dotprod_ref_q4_k}[dtype]
+    fn = {Q8_0: lib().orc_dotprod_ref_q8_0, Q4_K: lib().orc_dotprod_ref_q4_k, Q5_K: lib().orc_dotprod_ref_q5_k,
+          Q6_K: lib().orc_dotprod_ref_q6_k}[dtype]
     fn(_p(aq, ctypes.c_uint8), _p(b, ctypes.c_uint8), ctypes.c_size_t(m), ctypes.c_size_t(n),
        ctypes.c_size_t(k), _p(c, ctypes.c_float))
     return c.reshape(m, n)

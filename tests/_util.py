@@ -2,8 +2,9 @@
 and the tolerance rule of the north star."""
 import numpy as np
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-GEOM = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+F32, F16, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 1, 8, 10, 11, 12, 13, 14
+GEOM = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144),
+        Q5_K: (256, 176), Q6_K: (256, 210)}
 
 
 def f16_bytes(v):
@@ -14,14 +15,20 @@ def synth_blocks(dtype, n_blocks, seed):
     """Raw GGUF blocks as BASELINE.json describes the benchmark weights."""
     rng = np.random.default_rng(seed)
     be, bb = GEOM[dtype]
+    if dtype == F16:
+        return (rng.standard_normal(n_blocks) * 0.05).astype(np.float16).view(np.uint8)
+    if dtype == F32:
+        return (rng.standard_normal(n_blocks) * 0.05).astype(np.float32).view(np.uint8)
     raw = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
     scale = lambda: f16_bytes(np.abs(rng.standard_normal(n_blocks)) * 0.01)
     if dtype == Q8_0:
         raw[:, 0:2] = scale()
         raw[:, 2:] = rng.integers(-127, 128, size=(n_blocks, 32)).astype(np.int8).view(np.uint8)
-    elif dtype == Q4_K:
+    elif dtype in (Q4_K, Q5_K, Q2_K):  # d, dmin lead the block
         raw[:, 0:2] = scale()
         raw[:, 2:4] = scale()
+    elif dtype == Q3_K:
+        raw[:, 108:110] = scale()
     else:
         raw[:, 192:208] = rng.integers(-64, 64, size=(n_blocks, 16)).astype(np.int8).view(np.uint8)
         raw[:, 208:210] = scale()
@@ -30,7 +37,7 @@ def synth_blocks(dtype, n_blocks, seed):
 
 def weight(dtype, n, k, seed):
     be, bb = GEOM[dtype]
-    nb = (k + 31) // 32 if dtype == Q8_0 else k // 256
+    nb = (k + 31) // 32 if dtype == Q8_0 else k if be == 1 else k // 256
     return synth_blocks(dtype, n * nb, seed)
 
 
