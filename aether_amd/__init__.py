@@ -7,7 +7,8 @@ path: if the library is missing or no GPU is present, calls raise.
 import ctypes
 import os
 
-__all__ = ["lib", "check", "AethError", "LIB_PATH", "DTYPE_Q8_0", "DTYPE_Q4_K", "DTYPE_Q6_K",
+__all__ = ["lib", "check", "AethError", "LIB_PATH", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q8_0", "DTYPE_Q2_K",
+           "DTYPE_Q3_K", "DTYPE_Q4_K", "DTYPE_Q5_K", "DTYPE_Q6_K",
            "LlamaConfig", "header_symbols", "MM_ACCUMULATE", "block_geometry", "AETH_OK", "AETH_EINVAL",
            "AETH_EHIP", "AETH_ENOMEM", "AETH_EUNSUPPORTED", "AETH_ESTATE"]
 
@@ -15,11 +16,13 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libaether_hip.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
-DTYPE_Q8_0, DTYPE_Q4_K, DTYPE_Q6_K = 8, 12, 14
+DTYPE_F32, DTYPE_F16, DTYPE_Q8_0, DTYPE_Q2_K, DTYPE_Q3_K = 0, 1, 8, 10, 11
+DTYPE_Q4_K, DTYPE_Q5_K, DTYPE_Q6_K = 12, 13, 14
 MM_ACCUMULATE = 1
 # return codes (include/aether_hip.h)
 AETH_OK, AETH_EINVAL, AETH_EHIP, AETH_ENOMEM, AETH_EUNSUPPORTED, AETH_ESTATE = 0, -1, -2, -3, -4, -5
-_GEOM = {DTYPE_Q8_0: (32, 34), DTYPE_Q4_K: (256, 144), DTYPE_Q6_K: (256, 210)}
+_GEOM = {DTYPE_F32: (1, 4), DTYPE_F16: (1, 2), DTYPE_Q8_0: (32, 34), DTYPE_Q2_K: (256, 84), DTYPE_Q3_K: (256, 110),
+         DTYPE_Q4_K: (256, 144), DTYPE_Q5_K: (256, 176), DTYPE_Q6_K: (256, 210)}
 
 
 class AethError(RuntimeError):
@@ -58,6 +61,7 @@ _SIGS = {
     "aeth_quantized_matmul_impl": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P]),
     "aeth_matmul_q8_0": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q4_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
+    "aeth_matmul_q5_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q6_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_register_hip_kernels": (_INT, []),
     "aeth_registered_kernel_name": (_INT, [_INT, ctypes.c_char_p, _INT]),

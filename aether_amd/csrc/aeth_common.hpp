@@ -11,7 +11,10 @@
 #define Q8_BLOCK_ELEMS 32
 #define Q8_BLOCK_BYTES 34
 #define QK_BLOCK_ELEMS 256
+#define Q2K_BLOCK_BYTES 84
+#define Q3K_BLOCK_BYTES 110
 #define Q4K_BLOCK_BYTES 144
+#define Q5K_BLOCK_BYTES 176
 #define Q6K_BLOCK_BYTES 210
 
 // Records a message for aeth_last_error() and returns `code`.

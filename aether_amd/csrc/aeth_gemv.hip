@@ -1,30 +1,36 @@
-// Decode GEMV for Q4_K / Q6_K / Q8_0 weights on the int8 matrix cores of gfx950:
-//   y[r] = Σ_k x[k]·W[r][k]  (avx2::matmul_q4_k / matmul_q6_k, src/quant/avx2.rs:23-94;
-//   scalar matmul_q8_0, src/quant/matmul/q8_0.rs:5-89), one activation row per grid.y.
+// Decode GEMV for Q4_K / Q5_K / Q6_K / Q8_0 weights on the int8 matrix cores of gfx950:
+//   y[r] = Σ_k x[k]·W[r][k]  (avx2::matmul_q4_k / matmul_q6_k / matmul_q5_k,
+//   src/quant/avx2.rs:23-131; scalar matmul_q8_0, src/quant/matmul/q8_0.rs:5-89),
+//   one activation row per grid.y.
 //
 // Exact integer core. Each wave turns its slice of the activation row into an
-// exact integer form: per group of 32 (Q4_K, Q8_0) or 16 (Q6_K) elements,
-// x ≈ x_int·2^-S with |x_int| ≤ 2^22 (22 bits + sign against the group
-// maximum), split into three balanced signed byte digits
-// x_int = d0 + 256·d1 + 65536·d2. The digits are the A operand of
-// v_mfma_i32_16x16x64_i8 — M = 4 output slots × 4 digit rows (the fourth row
-// zero) — and 16 weight rows are the B operand (N). Lane (n, kg) (n = lane % 16,
+// exact integer form: per group of 32 (Q4_K, Q5_K, Q8_0) or 16 (Q6_K) elements,
+// x = x_int·2^-S with |x_int| < 2^30 against the group maximum — every element
+// within 2^7 of the maximum is represented exactly (its 24-bit significand
+// fits), smaller ones to 2^-30 of the maximum — split into four balanced
+// signed byte digits x_int = d0 + 2^8·d1 + 2^16·d2 + 2^24·d3. The digits are
+// the A operand of v_mfma_i32_16x16x64_i8 — M = 4 output slots × 4 digit rows
+// — and 16 weight rows are the B operand (N). Lane (n, kg) (n = lane % 16,
 // kg = lane / 16) supplies 16 k-slots of row n; A lane (m, kg) holds the
 // digits that pair with them, nonzero only where slot m/4 owns those k-slots.
 // One MFMA so returns the exact integer dot of every digit with 64 quants of 16
 // rows, already split by scale group; the output lane (n, g) holds slot g's
-// three digit sums for row n and applies that group's scales in f32.
+// four digit sums for row n (each exact in i32: |Σ q·d| ≤ 32·63·128), pairs
+// them in i32 (d0 + 2^8·d1, d2 + 2^8·d3) and recombines exactly in f64 before
+// one rounding to f32 and the group's scales.
 //
 // Per format ("chunk" = the unit of K a wave steps through):
 //  Q4_K, chunk = super-block (256). Per half h, lane (n, kg) loads
 //    qs[64h + 16kg, +16) of row n: low nibbles are sub-block 4h + 2(kg ≥ 2),
 //    high nibbles the next one. Two MFMAs (low / high nibbles) share one A;
 //    slot g ↔ sub-block 4h + g, the even slots exact in the first result, the
-//    odd ones in the second. |Σ q·x_int| ≤ 32·15·2^22 < 2^31: digits recombine
-//    in i32;  acc += 2^-S·Σq·x_int·d·sc − dmin·m·Σx.
+//    odd ones in the second;  acc += 2^-S·Σq·x_int·d·sc − dmin·m·Σx.
+//  Q5_K, as Q4_K (same quant and header planes) plus a plane of fifth bits:
+//    lane (n, kg) loads 8 bytes, 16 bits per (half, low / high nibbles) for its
+//    16 elements; each bit is spread to 0x10 of its byte before the MFMA.
 //  Q8_0, chunk = 4 blocks (128). MFMA j, lane (n, kg): the 16 raw quant bytes
 //    [16(kg & 1), +16) of block 2j + (kg ≥ 2) — no unpacking; slot g ↔ block g.
-//    acc += 2^-S·(Σ q·x_int)·d (the top digit joins in f32).
+//    acc += 2^-S·(Σ q·x_int)·d.
 //  Q6_K, chunk = super-block. Lane (n, kg) loads the 48 bytes of its 2×16
 //    elements of half h = kg / 2, g' = kg % 2: ql[64h + 16g', +16),
 //    ql[64h + 32 + 16g', +16), qh[32h + 16g', +16), and MFMA v (0..3) takes
@@ -32,8 +38,8 @@
 //    q + 32 ∈ [0, 63]; slot g ↔ lane group kg = g. The offset is removed
 //    exactly per digit (−32·Σ digit) before   acc += 2^-S·Σ(q)·x_int·sc·d.
 //
-// A operands are kept compact in LDS: only the three digit rows, 16-byte
-// vectors indexed (region, kg, slot, digit), 3 bytes per activation element.
+// A operands are kept compact in LDS: only the digit rows, 16-byte vectors
+// indexed (region, kg, slot, digit), 4 bytes per activation element.
 // A lane whose (m, kg) holds no digits for an MFMA reads a 16-byte zero slot
 // instead (one address select per operand read).
 //
@@ -59,7 +65,7 @@
 
 typedef int mq_v4i __attribute__((ext_vector_type(4)));
 
-enum { FQ4K = 0, FQ6K = 1, FQ80 = 2 };
+enum { FQ4K = 0, FQ6K = 1, FQ80 = 2, FQ5K = 3 };
 
 struct MqParams {
     const uint8_t* p0;
@@ -97,26 +103,39 @@ struct MqLane {
     int m, kg, s, d;
 };
 
-template <> struct MF<FQ4K> {
-    static constexpr int CE = 256, AB = 768, MB = 64, GE = 32;
-    struct D { int4 q[2]; uint4 h; };
-    // planes: p0 = headers [tile][sb][16 rows][16 B], p1 = quants [tile][sb][h][64][16 B]
+// Σ q·x_int from its digit pairs lo = Σq·d0 + 2^8·Σq·d1 and hi = Σq·d2 + 2^8·Σq·d3
+// (both exact in i32): exact in f64, rounded once to f32.
+__device__ __forceinline__ float mq_recombine(int lo, int hi) {
+    return (float)fma((double)hi, 65536.0, (double)lo);
+}
+
+// Bit i of b (i < 4) → 0x10 in byte i: the fifth quant bit of four elements.
+__device__ __forceinline__ int mq_spread4(uint32_t b) { return (int)(((b * 0x00204081u) & 0x01010101u) << 4); }
+
+// Q4_K and Q5_K share the chunk, the A layout and the scale handling; Q5_K adds
+// the fifth bits, read per lane as 4 × 16 bits (half h, low / high nibble).
+template <bool Q5> struct MFK {
+    static constexpr int CE = 256, AB = 1024, MB = 64, GE = 32;
+    struct D { int4 q[2]; uint4 h; uint2 qh; };
+    // planes: p0 = headers [tile][sb][16 rows][16 B], p1 = quants [tile][sb][h][64][16 B],
+    //         Q5: p2 = fifth bits [tile][sb][64][8 B]
     __device__ static void load(D& d, const MqParams& G, int64_t c, int lane) {  // c = tile·nc + chunk
         d.q[0] = *(const int4*)(G.p1 + (c * 2) * 1024 + lane * 16);
         d.q[1] = *(const int4*)(G.p1 + (c * 2 + 1) * 1024 + lane * 16);
         d.h = *(const uint4*)(G.p0 + (c * 16 + (lane & 15)) * 16);
+        if (Q5) d.qh = *(const uint2*)(G.p2 + (c * 64 + lane) * 8);
     }
-    // compact A: per half h, vector ((kg·2 + (s & 1))·3 + d), kg ∈ the pair of slot s.
+    // compact A: per half h, vector ((kg·2 + (s & 1))·4 + d), kg ∈ the pair of slot s.
     // byte offset of an octet's digit-0 piece (digit d: +16·d)
     __device__ static int aoff(int ec) {
         const int h = ec >> 7, s = (ec >> 5) & 3, p = ec & 31, kg = 2 * (s >> 1) + (p >> 4);
-        return h * 384 + ((kg * 2 + (s & 1)) * 3) * 16 + (p & 8);
+        return h * 512 + ((kg * 2 + (s & 1)) * 4) * 16 + (p & 8);
     }
     __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
                                 const char* zs) {
         const int g = lane >> 4;
-        const bool va = (L.s >> 1) == (L.kg >> 1) && L.d < 3;
-        const int vo = ((L.kg * 2 + (L.s & 1)) * 3 + L.d) * 16;
+        const bool va = (L.s >> 1) == (L.kg >> 1);
+        const int vo = ((L.kg * 2 + (L.s & 1)) * 4 + L.d) * 16;
         const bool odd = g & 1;
         const mq_v4i zero = {0, 0, 0, 0};
         const float d = aeth_decode_d(dd.h.x), dmin = aeth_decode_d(dd.h.x >> 16);
@@ -133,20 +152,29 @@ template <> struct MF<FQ4K> {
             lo.x = Q.x & 0x0F0F0F0F; lo.y = Q.y & 0x0F0F0F0F; lo.z = Q.z & 0x0F0F0F0F; lo.w = Q.w & 0x0F0F0F0F;
             hi.x = (Q.x >> 4) & 0x0F0F0F0F; hi.y = (Q.y >> 4) & 0x0F0F0F0F;
             hi.z = (Q.z >> 4) & 0x0F0F0F0F; hi.w = (Q.w >> 4) & 0x0F0F0F0F;
-            const mq_v4i a = *(const mq_v4i*)(va ? A + hh * 384 + vo : zs);
+            if (Q5) {  // q = nibble | fifth bit << 4 ∈ [0, 31]
+                const uint32_t hw = hh ? dd.qh.y : dd.qh.x, hl = hw & 0xFFFFu, hu = hw >> 16;
+                lo.x |= mq_spread4(hl & 15u); lo.y |= mq_spread4((hl >> 4) & 15u);
+                lo.z |= mq_spread4((hl >> 8) & 15u); lo.w |= mq_spread4(hl >> 12);
+                hi.x |= mq_spread4(hu & 15u); hi.y |= mq_spread4((hu >> 4) & 15u);
+                hi.z |= mq_spread4((hu >> 8) & 15u); hi.w |= mq_spread4(hu >> 12);
+            }
+            const mq_v4i a = *(const mq_v4i*)(va ? A + hh * 512 + vo : zs);
             const mq_v4i D1 = mq_mfma(a, lo, zero), D2 = mq_mfma(a, hi, zero);
-            const int e0 = odd ? D2.x : D1.x, e1 = odd ? D2.y : D1.y, e2 = odd ? D2.z : D1.z;
-            const int v = e0 + e1 * 256 + e2 * 65536;
+            const mq_v4i E = odd ? D2 : D1;
+            const float v = mq_recombine(E.x + E.y * 256, E.z + E.w * 256);
             const int2 mt = ((const int2*)meta)[4 * hh + g];
-            acc = fmaf(ldexpf((float)v, mt.x), d * sc[hh], acc);
+            acc = fmaf(ldexpf(v, mt.x), d * sc[hh], acc);
             acc = fmaf(-dmin * mn[hh], __int_as_float(mt.y), acc);
         }
         return acc;
     }
 };
+template <> struct MF<FQ4K> : MFK<false> {};
+template <> struct MF<FQ5K> : MFK<true> {};
 
 template <> struct MF<FQ80> {
-    static constexpr int CE = 128, AB = 384, MB = 32, GE = 32;
+    static constexpr int CE = 128, AB = 512, MB = 32, GE = 32;
     struct D { int4 q[2]; uint32_t d; };
     // planes: p0 = quants [tile][group][j][64][16 B], p1 = d [tile][group][4 blocks][16 rows] (f16)
     __device__ static void load(D& d, const MqParams& G, int64_t c, int lane) {
@@ -154,30 +182,29 @@ template <> struct MF<FQ80> {
         d.q[1] = *(const int4*)(G.p0 + (c * 2 + 1) * 1024 + lane * 16);
         d.d = ((const uint16_t*)G.p1)[c * 64 + lane];
     }
-    // compact A: per MFMA j, vector (kg·3 + d) (slot s = 2j + (kg ≥ 2))
+    // compact A: per MFMA j, vector (kg·4 + d) (slot s = 2j + (kg ≥ 2))
     __device__ static int aoff(int ec) {
         const int s = ec >> 5, p = ec & 31, kg = 2 * (s & 1) + (p >> 4);
-        return (s >> 1) * 192 + (kg * 3) * 16 + (p & 8);
+        return (s >> 1) * 256 + (kg * 4) * 16 + (p & 8);
     }
     __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
                                 const char* zs) {
         const int g = lane >> 4;
         const mq_v4i zero = {0, 0, 0, 0};
-        const int vo = (L.kg * 3 + L.d) * 16;
-        const bool v0 = L.s == (L.kg >> 1) && L.d < 3, v1 = L.s == 2 + (L.kg >> 1) && L.d < 3;
-        const mq_v4i a0 = *(const mq_v4i*)(v0 ? A + vo : zs), a1 = *(const mq_v4i*)(v1 ? A + 192 + vo : zs);
+        const int vo = (L.kg * 4 + L.d) * 16;
+        const bool v0 = L.s == (L.kg >> 1), v1 = L.s == 2 + (L.kg >> 1);
+        const mq_v4i a0 = *(const mq_v4i*)(v0 ? A + vo : zs), a1 = *(const mq_v4i*)(v1 ? A + 256 + vo : zs);
         const mq_v4i b0 = {dd.q[0].x, dd.q[0].y, dd.q[0].z, dd.q[0].w};
         const mq_v4i b1 = {dd.q[1].x, dd.q[1].y, dd.q[1].z, dd.q[1].w};
         const mq_v4i D = mq_mfma(a1, b1, mq_mfma(a0, b0, zero));
-        // |Σ q·d_k| ≤ 32·127·128: d0 + 256·d1 exact in i32, the top digit joins in f32
-        const float val = (float)(D.x + D.y * 256) + 65536.0f * (float)D.z;
+        const float val = mq_recombine(D.x + D.y * 256, D.z + D.w * 256);
         const int2 mt = ((const int2*)meta)[g];
         return ldexpf(val, mt.x) * aeth_f16_to_f32(dd.d);  // Q8_0 scales are plain f16 (q8_0.rs)
     }
 };
 
 template <> struct MF<FQ6K> {
-    static constexpr int CE = 256, AB = 768, MB = 256, GE = 16;
+    static constexpr int CE = 256, AB = 1024, MB = 256, GE = 16;
     struct D { int4 a, b, h; uint2 sc; uint32_t d; };
     // planes: p0 = [tile][sb][part A|B|H][64][16 B], p1 = sc [tile][sb][16 rows][16 B],
     //         p2 = d [tile][sb][16 rows] (f16)
@@ -188,16 +215,16 @@ template <> struct MF<FQ6K> {
         d.sc = *(const uint2*)(G.p1 + (c * 16 + (lane & 15)) * 16 + ((lane >> 5) & 1) * 8);
         d.d = ((const uint16_t*)G.p2)[c * 16 + (lane & 15)];
     }
-    // compact A: per MFMA v, vector (kg·3 + d) (slot = kg)
+    // compact A: per MFMA v, vector (kg·4 + d) (slot = kg)
     __device__ static int aoff(int ec) {
         const int h = ec >> 7, r = ec & 127, v = r >> 5, kg = 2 * h + ((r >> 4) & 1);
-        return v * 192 + (kg * 3) * 16 + (r & 8);
+        return v * 256 + (kg * 4) * 16 + (r & 8);
     }
     __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
                                 const char* zs) {
         const int g = lane >> 4;
-        const bool va = L.s == L.kg && L.d < 3;
-        const int vo = (L.kg * 3 + L.d) * 16;
+        const bool va = L.s == L.kg;
+        const int vo = (L.kg * 4 + L.d) * 16;
         const mq_v4i zero = {0, 0, 0, 0};
         const int* Aw = (const int*)&dd.a;
         const int* Bw = (const int*)&dd.b;
@@ -217,12 +244,11 @@ template <> struct MF<FQ6K> {
                 else w = ((Bw[e] >> 4) & 0x0F0F0F0F) | ((Hw[e] >> 2) & 0x30303030);
                 q[e] = w;
             }
-            const mq_v4i a = *(const mq_v4i*)(va ? A + v * 192 + vo : zs);
+            const mq_v4i a = *(const mq_v4i*)(va ? A + v * 256 + vo : zs);
             const mq_v4i Dv = mq_mfma(a, q, zero);
             const int4 mt = ((const int4*)meta)[8 * (g >> 1) + 2 * v + (g & 1)];
-            // stored q + 32 ∈ [0, 63]: subtract 32·Σ digit per digit (exact)
-            const int a0 = Dv.x - mt.y, a1 = Dv.y - mt.z, a2 = Dv.z - mt.w;
-            const float val = ldexpf((float)a2 * 65536.0f + (float)(a0 + a1 * 256), mt.x);
+            // stored q + 32 ∈ [0, 63]: subtract 32·Σ x_int per digit pair (exact in i32)
+            const float val = ldexpf(mq_recombine(Dv.x + Dv.y * 256 - mt.y, Dv.z + Dv.w * 256 - mt.z), mt.x);
             const uint32_t sw = v < 2 ? s01 : s23;
             part += (float)(int8_t)((sw >> (16 * (v & 1))) & 0xFFu) * val;
         }
@@ -251,8 +277,9 @@ __device__ __forceinline__ void mq_load_x(const float* __restrict__ x, int o0, i
 }
 
 // The wave's activation slice → compact A operands (every byte of the slice's
-// regions is written) and per-group meta: Q4_K {−S, Σx}, Q8_0 {−S, 0}, Q6_K
-// {−S, 32·Σd0, 32·Σd1, 32·Σd2}. Written and later read by this wave only.
+// regions is written) and per-group meta: Q4_K / Q5_K {−S, Σx}, Q8_0 {−S, 0},
+// Q6_K {−S, 32·(Σd0 + 2^8·Σd1), 32·(Σd2 + 2^8·Σd3), 0}. Written and later
+// read by this wave only.
 // Returns nonzero (wave-uniform) if the slice holds a NaN or an infinity.
 template <int F, int XO>
 __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase, char* Mbase) {
@@ -282,25 +309,29 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
         const bool use = mx > 0.0f && fin;
         int E = 0;
         if (use) (void)frexpf(mx, &E);
-        const int S = use ? 22 - E : 0;
-        int d0[8], d1[8], d2[8];
-        int s0 = 0, s1 = 0, s2 = 0;
+        const int S = use ? 30 - E : 0;  // max|x| < 2^E, so |x_int| < 2^30
+        int d0[8], d1[8], d2[8], d3[8];
+        int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
         float fs = 0.0f;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const int xi = use ? (int)rintf(ldexpf(v[t], S)) : 0;
-            const int a = (xi << 24) >> 24;
+            const int a = (xi << 24) >> 24;  // balanced digits: each in [−128, 127], d3 in [−64, 64]
             const int r = (xi - a) >> 8;
             const int b = (r << 24) >> 24;
+            const int r2 = (r - b) >> 8;
+            const int c2 = (r2 << 24) >> 24;
             d0[t] = a;
             d1[t] = b;
-            d2[t] = (r - b) >> 8;
+            d2[t] = c2;
+            d3[t] = (r2 - c2) >> 8;
             s0 += a;
             s1 += b;
-            s2 += d2[t];
+            s2 += c2;
+            s3 += d3[t];
             fs += v[t];
         }
-        if (F == FQ4K) {
+        if (F == FQ4K || F == FQ5K) {
             fs += __shfl_xor(fs, 1, 64);
             fs += __shfl_xor(fs, 2, 64);
         }
@@ -308,6 +339,7 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
             s0 += __shfl_xor(s0, 1, 64);
             s1 += __shfl_xor(s1, 1, 64);
             s2 += __shfl_xor(s2, 1, 64);
+            s3 += __shfl_xor(s3, 1, 64);
         }
         if (live) {
             const int c = o / (T::CE / 8), ec = 8 * o - c * T::CE;
@@ -317,10 +349,13 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
                 make_uint2(mq_pack4(d1[0], d1[1], d1[2], d1[3]), mq_pack4(d1[4], d1[5], d1[6], d1[7]));
             *(uint2*)(dst + 32) =
                 make_uint2(mq_pack4(d2[0], d2[1], d2[2], d2[3]), mq_pack4(d2[4], d2[5], d2[6], d2[7]));
+            *(uint2*)(dst + 48) =
+                make_uint2(mq_pack4(d3[0], d3[1], d3[2], d3[3]), mq_pack4(d3[4], d3[5], d3[6], d3[7]));
             char* mb = Mbase + (size_t)c * T::MB;
-            if (F == FQ4K && (ec & 31) == 0) ((int2*)mb)[ec >> 5] = make_int2(-S, __float_as_int(fs));
+            if ((F == FQ4K || F == FQ5K) && (ec & 31) == 0) ((int2*)mb)[ec >> 5] = make_int2(-S, __float_as_int(fs));
             if (F == FQ80 && (ec & 31) == 0) ((int2*)mb)[ec >> 5] = make_int2(-S, 0);
-            if (F == FQ6K && (ec & 15) == 0) ((int4*)mb)[ec >> 4] = make_int4(-S, 32 * s0, 32 * s1, 32 * s2);
+            if (F == FQ6K && (ec & 15) == 0)
+                ((int4*)mb)[ec >> 4] = make_int4(-S, 32 * (s0 + 256 * s1), 32 * (s2 + 256 * s3), 0);
         }
     }
     return __any(bad);
@@ -575,6 +610,7 @@ int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float
     if (!rag && (((uintptr_t)d_x & 15) || (e.norm_w && ((uintptr_t)e.norm_w & 15)) || (m > 1 && (G.k & 3))))
         return aeth_set_error(AETH_EINVAL, "gemv: x rows and the norm weight must be 16-byte aligned");
     if (w->dtype == AETH_DTYPE_Q4_K) return mq_dispatch<FQ4K, false>(G, m, s);
+    if (w->dtype == AETH_DTYPE_Q5_K) return mq_dispatch<FQ5K, false>(G, m, s);
     if (w->dtype == AETH_DTYPE_Q6_K) return mq_dispatch<FQ6K, false>(G, m, s);
     if (q8) return rag ? mq_dispatch<FQ80, true>(G, m, s) : mq_dispatch<FQ80, false>(G, m, s);
     return aeth_set_error(AETH_EUNSUPPORTED, "gemv: dtype %d", w->dtype);

@@ -259,8 +259,10 @@ int load_quant(const Gguf& g, const std::string& name, Staging& st, std::vector<
     if (it == g.tensors.end()) return aeth_set_error(AETH_EINVAL, "Missing tensor: %s", name.c_str());
     const TensorInfo& t = it->second;
     if (t.shape.size() != 2) return aeth_set_error(AETH_EUNSUPPORTED, "tensor %s is not 2-D", name.c_str());
-    if (t.dtype != AETH_DTYPE_Q8_0 && t.dtype != AETH_DTYPE_Q4_K && t.dtype != AETH_DTYPE_Q6_K)
-        return aeth_set_error(AETH_EUNSUPPORTED, "tensor %s: dtype %u is not a format this build runs (Q8_0, Q4_K, Q6_K)",
+    if (t.dtype != AETH_DTYPE_Q8_0 && t.dtype != AETH_DTYPE_Q4_K && t.dtype != AETH_DTYPE_Q5_K &&
+        t.dtype != AETH_DTYPE_Q6_K)
+        return aeth_set_error(AETH_EUNSUPPORTED,
+                              "tensor %s: dtype %u is not a format this build runs (Q8_0, Q4_K, Q5_K, Q6_K)",
                               name.c_str(), t.dtype);
     const int64_t k = (int64_t)t.shape[0], n = (int64_t)t.shape[1];
     int be, bb;
@@ -281,7 +283,7 @@ int load_quant(const Gguf& g, const std::string& name, Staging& st, std::vector<
     return AETH_OK;
 }
 
-// dequantize of an F32 / F16 / Q8_0 / Q4_K / Q6_K tensor to f32 (loader/dequant.rs entry `dequantize`)
+// dequantize of an F32 / F16 / Q8_0 / Q2_K..Q6_K tensor to f32 (loader/dequant.rs entry `dequantize`)
 int dequantize(const TensorInfo& t, const std::string& name, Staging& st, std::vector<float>& out) {
     uint64_t ne = 1;
     for (uint64_t d : t.shape) ne *= d;
@@ -294,7 +296,7 @@ int dequantize(const TensorInfo& t, const std::string& name, Staging& st, std::v
             memcpy(&h, t.data + 2 * i, 2);
             out[i] = half_to_float(h);
         }
-    } else if (t.dtype == AETH_DTYPE_Q8_0 || t.dtype == AETH_DTYPE_Q4_K || t.dtype == AETH_DTYPE_Q6_K) {
+    } else if (t.dtype == AETH_DTYPE_Q8_0 || (t.dtype >= AETH_DTYPE_Q2_K && t.dtype <= AETH_DTYPE_Q6_K)) {
         int rc;
         if ((rc = Staging::grow(&st.src, &st.src_b, t.bytes)) || (rc = Staging::grow(&st.ws, &st.ws_b, ne * 4)))
             return rc;

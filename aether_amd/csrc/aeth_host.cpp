@@ -220,6 +220,7 @@ class HipQuantKernel final : public QuantKernel {
         switch (dtype_) {
             case AETH_DTYPE_Q8_0: return "Q8_0 (hip gfx950)";
             case AETH_DTYPE_Q4_K: return "Q4_K (hip gfx950)";
+            case AETH_DTYPE_Q5_K: return "Q5_K (hip gfx950)";
             default: return "Q6_K (hip gfx950)";
         }
     }
@@ -258,7 +259,7 @@ int dispatch_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_l
 }  // namespace aeth
 
 extern "C" AETH_API int aeth_register_hip_kernels(void) {
-    for (int dt : {AETH_DTYPE_Q8_0, AETH_DTYPE_Q4_K, AETH_DTYPE_Q6_K}) {
+    for (int dt : {AETH_DTYPE_Q8_0, AETH_DTYPE_Q4_K, AETH_DTYPE_Q5_K, AETH_DTYPE_Q6_K}) {
         int rc = aeth::register_kernel(std::unique_ptr<aeth::QuantKernel>(new aeth::HipQuantKernel(dt)));
         if (rc) return rc;
     }
@@ -286,7 +287,7 @@ extern "C" AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, co
     int rc = aeth::dispatch_matmul(a, m, b_raw, b_len, n, k, dtype, c);
     if (rc == 1) return AETH_OK;
     if (rc < 0) return rc;
-    if (dtype != AETH_DTYPE_Q8_0 && dtype != AETH_DTYPE_Q4_K && dtype != AETH_DTYPE_Q6_K)
+    if (dtype != AETH_DTYPE_Q8_0 && dtype != AETH_DTYPE_Q4_K && dtype != AETH_DTYPE_Q5_K && dtype != AETH_DTYPE_Q6_K)
         return aeth_set_error(AETH_EUNSUPPORTED, "quantized_matmul_impl: dtype %d not on the HIP path", dtype);
     return host_matmul(a, m, b_raw, b_len, n, k, dtype, c);
 }
@@ -298,6 +299,10 @@ extern "C" AETH_API int aeth_matmul_q8_0(const float* a, const uint8_t* b, int64
 extern "C" AETH_API int aeth_matmul_q4_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
                                          int64_t k, float* c) {
     return host_matmul(a, m, b, b_len, n, k, AETH_DTYPE_Q4_K, c);
+}
+extern "C" AETH_API int aeth_matmul_q5_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                                         int64_t k, float* c) {
+    return host_matmul(a, m, b, b_len, n, k, AETH_DTYPE_Q5_K, c);
 }
 extern "C" AETH_API int aeth_matmul_q6_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
                                          int64_t k, float* c) {

@@ -1,8 +1,8 @@
 // f32 → GGUF blocks on the device: the load-time re-quantizers and the Q8_0
 // activation quantizer, byte-exact with the reference.
 //
-//  * requantize_{q8_0,q4_k,q6_k} (src/quant/matmul/dispatch.rs:149-184,
-//    186-300, 431-537): f32 rows → blocks, used by load_quant to transpose
+//  * requantize_{q8_0,q4_k,q5_k,q6_k} (src/quant/matmul/dispatch.rs:149-184,
+//    186-300, 302-429, 431-537): f32 rows → blocks, used by load_quant to transpose
 //    quantized weights (model_loader.rs:330-386).
 //  * quantize_q8_0_block / quantize_activations_q8_0[_batched]
 //    (src/quant/matmul/neon.rs:45-155): the Q8_0 activation scheme.
@@ -63,8 +63,14 @@ __global__ void __launch_bounds__(256) k_requant_q8_0(const float* __restrict__ 
 // m_s = |min(min, 0)|, d_s = (max + m_s)/15; d = max_s d_s / 63,
 // dmin = max_s m_s / 63 (1 when 0); sc, m = clamp(round(d_s/d)), clamp(round(m_s/dmin))
 // in [0, 63], packed as get_scale_min_k4 reads them; q = clamp(round((x + dmin·m)/(d·sc)), 0, 15).
-__global__ void __launch_bounds__(256) k_requant_q4_k(const float* __restrict__ src, int64_t rows, int64_t cols,
-                                                      int64_t bpr, uint8_t* __restrict__ out) {
+// Q5 = true: requantize_q5_k, dispatch.rs:302-429 — the same with 31 levels;
+// the low nibbles fill qs (byte 48 on), the fifth bit of element e goes to
+// bit e % 8 of qh[e / 8] (bytes 16..47).
+template <bool Q5>
+__global__ void __launch_bounds__(256) k_requant_qk(const float* __restrict__ src, int64_t rows, int64_t cols,
+                                                    int64_t bpr, uint8_t* __restrict__ out) {
+    constexpr float LV = Q5 ? 31.0f : 15.0f;
+    constexpr int BB = Q5 ? Q5K_BLOCK_BYTES : Q4K_BLOCK_BYTES;
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= rows * bpr) return;
     const int64_t r = b / bpr, blk = b - r * bpr;
@@ -84,7 +90,7 @@ __global__ void __launch_bounds__(256) k_requant_q4_k(const float* __restrict__ 
             }
         }
         msub[sb] = fabsf(fminf(mn, 0.0f));
-        dsub[sb] = (mx + msub[sb]) / 15.0f;
+        dsub[sb] = (mx + msub[sb]) / LV;
     }
     float maxd = 0.0f, maxm = 0.0f;
     for (int sb = 0; sb < 8; sb++) {
@@ -93,7 +99,7 @@ __global__ void __launch_bounds__(256) k_requant_q4_k(const float* __restrict__ 
     }
     const float d = maxd == 0.0f ? 1.0f : maxd / 63.0f;
     const float dmin = maxm == 0.0f ? 1.0f : maxm / 63.0f;
-    uint8_t* o = out + b * 144;
+    uint8_t* o = out + b * BB;
     const uint32_t db = f16_bits(d), dmb = f16_bits(dmin);
     o[0] = (uint8_t)db;
     o[1] = (uint8_t)(db >> 8);
@@ -109,6 +115,7 @@ __global__ void __launch_bounds__(256) k_requant_q4_k(const float* __restrict__ 
         o[8 + q] = (uint8_t)((mm[q] & 63) | ((mm[q + 4] >> 4) << 6));
         o[12 + q] = (uint8_t)((sc[q + 4] & 0x0F) | ((mm[q + 4] & 0x0F) << 4));
     }
+    uint32_t qh[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // Q5: the 256 fifth bits
     for (int ch = 0; ch < 4; ch++) {
         const int is = 2 * ch;
         const float d1 = d * (float)sc[is], m1 = dmin * (float)mm[is];
@@ -116,11 +123,19 @@ __global__ void __launch_bounds__(256) k_requant_q4_k(const float* __restrict__ 
         for (int l = 0; l < 32; l++) {
             const int i0 = is * 32 + l, i1 = (is + 1) * 32 + l;
             uint32_t q0 = 0, q1 = 0;
-            if (i0 < actual && d1 != 0.0f) q0 = (uint32_t)fminf(fmaxf(roundf((x[i0] + m1) / d1), 0.0f), 15.0f);
-            if (i1 < actual && d2 != 0.0f) q1 = (uint32_t)fminf(fmaxf(roundf((x[i1] + m2) / d2), 0.0f), 15.0f);
-            o[16 + ch * 32 + l] = (uint8_t)(q0 | (q1 << 4));
+            if (i0 < actual && d1 != 0.0f) q0 = (uint32_t)fminf(fmaxf(roundf((x[i0] + m1) / d1), 0.0f), LV);
+            if (i1 < actual && d2 != 0.0f) q1 = (uint32_t)fminf(fmaxf(roundf((x[i1] + m2) / d2), 0.0f), LV);
+            if (Q5) {
+                o[48 + ch * 32 + l] = (uint8_t)((q0 & 0x0F) | ((q1 & 0x0F) << 4));
+                qh[i0 >> 5] |= (q0 >> 4) << (i0 & 31);
+                qh[i1 >> 5] |= (q1 >> 4) << (i1 & 31);
+            } else {
+                o[16 + ch * 32 + l] = (uint8_t)(q0 | (q1 << 4));
+            }
         }
     }
+    if (Q5)
+        for (int j = 0; j < 32; j++) o[16 + j] = (uint8_t)(qh[j >> 2] >> (8 * (j & 3)));
 }
 
 // requantize_q6_k, dispatch.rs:431-537: per 16-element sub-block s_max = max|x|;
@@ -240,14 +255,15 @@ static int requant_launch(int dtype, const float* src, int64_t rows, int64_t col
     if (aeth_cdiv(nblk, 256) > 0x7FFFFFFF) return aeth_set_error(AETH_EINVAL, "requantize: too many blocks");
     const dim3 grid((unsigned)aeth_cdiv(nblk, 256));
     if (dtype == AETH_DTYPE_Q8_0) hipLaunchKernelGGL(k_requant_q8_0, grid, dim3(256), 0, s, src, rows, cols, bpr, dst);
-    else if (dtype == AETH_DTYPE_Q4_K) hipLaunchKernelGGL(k_requant_q4_k, grid, dim3(256), 0, s, src, rows, cols, bpr, dst);
+    else if (dtype == AETH_DTYPE_Q4_K) hipLaunchKernelGGL(k_requant_qk<false>, grid, dim3(256), 0, s, src, rows, cols, bpr, dst);
+    else if (dtype == AETH_DTYPE_Q5_K) hipLaunchKernelGGL(k_requant_qk<true>, grid, dim3(256), 0, s, src, rows, cols, bpr, dst);
     else hipLaunchKernelGGL(k_requant_q6_k, grid, dim3(256), 0, s, src, rows, cols, bpr, dst);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
 
 static bool requant_dtype(int dtype) {
-    return dtype == AETH_DTYPE_Q8_0 || dtype == AETH_DTYPE_Q4_K || dtype == AETH_DTYPE_Q6_K;
+    return dtype == AETH_DTYPE_Q8_0 || dtype == AETH_DTYPE_Q4_K || dtype == AETH_DTYPE_Q5_K || dtype == AETH_DTYPE_Q6_K;
 }
 
 extern "C" AETH_API int aeth_requantize(int dtype, const float* d_src, int64_t rows, int64_t cols, void* d_dst,

@@ -47,6 +47,7 @@ extern "C" AETH_API int aeth_block_geometry(int dtype, int* block_elems, int* bl
     switch (dtype) {
         case AETH_DTYPE_Q8_0: e = Q8_BLOCK_ELEMS; b = Q8_BLOCK_BYTES; break;
         case AETH_DTYPE_Q4_K: e = QK_BLOCK_ELEMS; b = Q4K_BLOCK_BYTES; break;
+        case AETH_DTYPE_Q5_K: e = QK_BLOCK_ELEMS; b = Q5K_BLOCK_BYTES; break;
         case AETH_DTYPE_Q6_K: e = QK_BLOCK_ELEMS; b = Q6K_BLOCK_BYTES; break;
         default: return aeth_set_error(AETH_EUNSUPPORTED, "unsupported dtype %d", dtype);
     }
@@ -69,6 +70,10 @@ int64_t aeth_blocks_per_row(int dtype, int64_t k) {
 // contiguously; lane (n, kg) = lane n + 16·kg of a 64-lane wave.
 //  Q4_K: p0 = headers [tile][b][16 rows][16 B]; p1 = quants [tile][b][half h][lane][16 B],
 //        lane (n, kg) = qs[64h + 16kg, +16) of row n (aeth_q4k_*_off).
+//  Q5_K: p0, p1 as Q4_K (header bytes 0..15; qs = bytes 48..175 in Q4_K's qs
+//        order); p2 = fifth bits [tile][b][lane][8 B], lane (n, kg) holding, per
+//        half h, the 16-bit runs of qh for its low-nibble elements
+//        (128h + 64(kg/2) + 16(kg%2) + [0,16)) and high-nibble elements (+32).
 //  Q6_K: p0 = [tile][b][part][lane][16 B], lane (n, kg = 2h + g'): part 0 =
 //        ql[64h + 16g', +16), part 1 = ql[64h + 32 + 16g', +16), part 2 =
 //        qh[32h + 16g', +16); p1 = sc [tile][b][16 rows][16 B]; p2 = d [tile][b][16 rows].
@@ -88,6 +93,18 @@ __device__ __forceinline__ uint8_t* planar_addr(int dtype, int64_t i, int64_t nb
         const int64_t row = blk / nb, b = blk - row * nb;
         if (off < 16) return p0 + aeth_q4k_hdr_off(row, b, nb) + off;
         return p1 + aeth_q4k_qs_off(row, b, off - 16, nb);
+    }
+    if (dtype == AETH_DTYPE_Q5_K) {
+        const int64_t blk = i / Q5K_BLOCK_BYTES;
+        const int off = (int)(i - blk * Q5K_BLOCK_BYTES);
+        const int64_t row = blk / nb, b = blk - row * nb;
+        if (off < 16) return p0 + aeth_q4k_hdr_off(row, b, nb) + off;
+        if (off >= 48) return p1 + aeth_q4k_qs_off(row, b, off - 48, nb);
+        // qh byte q: half q/16, r = q%16 → lane group kg = 2(r/8) + (r/2)%2,
+        // byte 4h + 2·(high nibble: (r%8)/4) + r%2 of the lane's 8
+        const int q = off - 16, h = q >> 4, r = q & 15;
+        const int kg = 2 * (r >> 3) + ((r >> 1) & 1), j = 4 * h + 2 * ((r & 7) >> 2) + (r & 1);
+        return p2 + ((((row >> 4) * nb + b) * 64 + (row & 15) + 16 * kg) * 8 + j);
     }
     if (dtype == AETH_DTYPE_Q6_K) {
         const int64_t blk = i / Q6K_BLOCK_BYTES;
@@ -158,6 +175,7 @@ extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, cons
     int64_t sz[4] = {0, 0, 0, 0};
     const int64_t prow = aeth_cdiv(n, 16) * 16;  // whole 16-row tiles
     if (dtype == AETH_DTYPE_Q4_K) { sz[0] = prow * w->nb * 16; sz[1] = prow * w->nb * 128; }
+    else if (dtype == AETH_DTYPE_Q5_K) { sz[0] = prow * w->nb * 16; sz[1] = prow * w->nb * 128; sz[2] = prow * w->nb * 32; }
     else if (dtype == AETH_DTYPE_Q6_K) { sz[0] = prow * w->nb * 192; sz[1] = prow * w->nb * 16; sz[2] = prow * w->nb * 2; }
     else { const int64_t pb = aeth_cdiv(w->nb, 4) * 4; sz[0] = prow * pb * 32; sz[1] = prow * pb * 2; }
     int64_t off[4], tot = 0;
@@ -270,9 +288,10 @@ __global__ void k_fill_synthetic(int dtype, uint64_t seed, uint8_t* __restrict__
     if (i >= total_bytes) return;
     uint64_t key = splitmix64(seed);
     uint8_t v;
-    if (dtype == AETH_DTYPE_Q4_K) {
-        int64_t blk = i / Q4K_BLOCK_BYTES;
-        int off = (int)(i - blk * Q4K_BLOCK_BYTES);
+    if (dtype == AETH_DTYPE_Q4_K || dtype == AETH_DTYPE_Q5_K) {
+        const int bb = dtype == AETH_DTYPE_Q4_K ? Q4K_BLOCK_BYTES : Q5K_BLOCK_BYTES;
+        int64_t blk = i / bb;
+        int off = (int)(i - blk * bb);
         if (off < 4) {
             uint32_t b = scale_f16_bits(key, (uint64_t)blk, off >> 1);
             v = (uint8_t)((off & 1) ? (b >> 8) : b);

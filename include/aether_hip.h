@@ -30,8 +30,13 @@ extern "C" {
 #define AETH_ESTATE (-5)
 
 /* GGUFDtype discriminants, src/loader/gguf.rs:92-110. */
+#define AETH_DTYPE_F32 0
+#define AETH_DTYPE_F16 1
 #define AETH_DTYPE_Q8_0 8
+#define AETH_DTYPE_Q2_K 10
+#define AETH_DTYPE_Q3_K 11
 #define AETH_DTYPE_Q4_K 12
+#define AETH_DTYPE_Q5_K 13
 #define AETH_DTYPE_Q6_K 14
 
 /* aeth_qmatmul flags */
@@ -66,15 +71,17 @@ AETH_API int aeth_weight_export_raw(const aeth_weight* w, void* dst, int dst_is_
 
 /* ── kernels ───────────────────────────────────────────────────────────── */
 
-/* GGUF blocks → f32, bit-exact with dequant_q8_0 / dequant_q4_k /
- * dequant_q6_k (src/loader/dequant.rs:103-127, 195-227, 301-348).
- * d_raw holds ceil(n/block_elems) raw blocks; n is rounded down to whole
- * blocks for the K-quants as the reference does (tail left untouched). */
+/* GGUF blocks → f32, bit-exact with src/loader/dequant.rs: dequant_f32 /
+ * dequant_f16 (:57-95), dequant_q8_0 (:103-127), dequant_q4_k (:195-227),
+ * dequant_q5_k (:229-285), dequant_q6_k (:301-348), dequant_q2_k (:350-398),
+ * dequant_q3_k (:400-451). d_raw holds ceil(n/block_elems) raw blocks; n is
+ * rounded down to whole blocks for the K-quants as the reference does (tail
+ * left untouched). */
 AETH_API int aeth_dequant(int dtype, const void* d_raw, int64_t n_elems, float* d_out, void* stream);
 
 /* f32 [rows][cols] → GGUF blocks [rows][ceil(cols/block_elems)], byte-exact
- * with requantize_q8_0 / requantize_q4_k / requantize_q6_k
- * (src/quant/matmul/dispatch.rs:139-184, 186-300, 431-537; entry
+ * with requantize_q8_0 / requantize_q4_k / requantize_q5_k / requantize_q6_k
+ * (src/quant/matmul/dispatch.rs:149-184, 186-300, 302-429, 431-537; entry
  * `requantize` :139-147). d_dst holds rows·ceil(cols/bs)·block_bytes bytes. */
 AETH_API int aeth_requantize(int dtype, const float* d_src, int64_t rows, int64_t cols, void* d_dst,
                              void* stream);
@@ -93,7 +100,8 @@ AETH_API int aeth_transpose_f32(const float* d_src, int64_t rows, int64_t cols, 
  * tensor on the device: GGUF bytes of shape [k, n] → dequantize → transpose
  * → requantize, giving [n][k] row blocks in d_dst (n·ceil(k/bs)·block_bytes
  * bytes, the layout aeth_weight_create takes). d_ws holds
- * aeth_load_quant_ws_bytes(k, n) bytes. Q8_0, Q4_K and Q6_K. */
+ * aeth_load_quant_ws_bytes(k, n) bytes. Q8_0, Q4_K, Q5_K and Q6_K (the
+ * formats is_quantized_type_supported names, model_loader.rs:362-367). */
 AETH_API int64_t aeth_load_quant_ws_bytes(int64_t k, int64_t n);
 AETH_API int aeth_load_quant(int dtype, const void* d_src, int64_t k, int64_t n, void* d_dst, void* d_ws,
                              void* stream);
@@ -121,8 +129,11 @@ AETH_API int aeth_matmul_q4_k(const float* a, const uint8_t* b, int64_t b_len, i
                               int64_t k, float* c);
 AETH_API int aeth_matmul_q6_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
                               int64_t k, float* c);
+/* matmul_q5_k (src/quant/matmul/dispatch.rs:15-34, x86: avx2.rs:97-131). */
+AETH_API int aeth_matmul_q5_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                              int64_t k, float* c);
 /* QuantKernel registry (registry.rs:33-63): registers the HIP kernels for
- * Q8_0, Q4_K and Q6_K; a second registration of a dtype fails with
+ * Q8_0, Q4_K, Q5_K and Q6_K; a second registration of a dtype fails with
  * AETH_ESTATE (the reference panics). aeth_dispatch_matmul returns 1 if a
  * registered kernel handled the call, 0 if none is registered for dtype, <0
  * on error. */

@@ -25,10 +25,10 @@ def test_exports_are_exactly_the_declared_ones():
 def test_block_geometry_and_errors_without_gpu():
     L = A.lib()
     e, b = ctypes.c_int(), ctypes.c_int()
-    for dt, geo in ((8, (32, 34)), (12, (256, 144)), (14, (256, 210))):
+    for dt, geo in ((8, (32, 34)), (12, (256, 144)), (13, (256, 176)), (14, (256, 210))):
         assert L.aeth_block_geometry(dt, ctypes.byref(e), ctypes.byref(b)) == 0
         assert (e.value, b.value) == geo
-    assert L.aeth_block_geometry(13, ctypes.byref(e), ctypes.byref(b)) == -4  # Q5_K not on this path
+    assert L.aeth_block_geometry(2, ctypes.byref(e), ctypes.byref(b)) == -4  # Q4_0 is not on this path
     assert "unsupported" in A.last_error()
     # NULL arguments are refused before any device work
     assert L.aeth_weight_create(12, 4, 256, None, 0, None, None) == -1

@@ -8,7 +8,7 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import Q4_K, Q6_K, Q8_0, assert_close, assert_close_logits, assert_close_rows, weight
+from tests._util import Q4_K, Q5_K, Q6_K, Q8_0, assert_close, assert_close_logits, assert_close_rows, weight
 
 pytestmark = pytest.mark.gpu
 
@@ -189,7 +189,7 @@ def oracle_cfg(c=TINY):
                       c["d_ff"], c["max_seq_len"], c["rope_base"], c["rms_norm_eps"])
 
 
-@pytest.mark.parametrize("layer_dtype", [Q4_K, Q8_0, Q6_K])
+@pytest.mark.parametrize("layer_dtype", [Q4_K, Q8_0, Q6_K, Q5_K])
 def test_runner_decode_matches_oracle(gpu, layer_dtype):
     m = build_tiny(seed=2, layer_dtype=layer_dtype)
     r = make_runner(m)
@@ -223,7 +223,8 @@ def test_runner_decode_matches_oracle(gpu, layer_dtype):
 # Batched prefill (forward_batch) against the oracle's restatement: one query /
 # key block (37), a full cache (64), a single token, and several ragged blocks
 # with the GEMM path (150 of 192); GEMM for Q4_K, row-batched GEMV otherwise.
-@pytest.mark.parametrize("layer_dtype,n,max_seq", [(Q4_K, 37, 64), (Q8_0, 64, 64), (Q6_K, 1, 64), (Q4_K, 150, 192)])
+@pytest.mark.parametrize("layer_dtype,n,max_seq", [(Q4_K, 37, 64), (Q8_0, 64, 64), (Q6_K, 1, 64), (Q4_K, 150, 192),
+                                                   (Q5_K, 40, 64)])
 def test_runner_prefill_matches_oracle(gpu, layer_dtype, n, max_seq):
     c = dict(TINY, max_seq_len=max_seq)
     m = build_tiny(seed=7, layer_dtype=layer_dtype)

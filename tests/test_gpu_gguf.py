@@ -11,7 +11,7 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import GEOM, Q4_K, Q6_K, Q8_0, assert_close_logits, synth_blocks
+from tests._util import GEOM, Q4_K, Q5_K, Q6_K, Q8_0, assert_close_logits, synth_blocks
 from tests.gguf_writer import ARR, F32, STR, U32, write_gguf
 
 pytestmark = pytest.mark.gpu
@@ -93,7 +93,11 @@ def last_error(L):
 Q4_K_M = [Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K]   # llama.cpp's mix: attn_v and ffn_down in Q6_K
 
 
-@pytest.mark.parametrize("layer_dtype,f16_norms", [(Q4_K, False), (Q8_0, True), (Q6_K, False), (Q4_K_M, False)])
+Q5_K_M = [Q5_K, Q5_K, Q6_K, Q5_K, Q5_K, Q5_K, Q6_K]
+
+
+@pytest.mark.parametrize("layer_dtype,f16_norms", [(Q4_K, False), (Q8_0, True), (Q6_K, False), (Q4_K_M, False),
+                                                   (Q5_K_M, True)])
 def test_aether_load_prefill_decode_match_oracle(gpu, tmp_path, layer_dtype, f16_norms):
     L = A.lib()
     path = tmp_path / "tiny.gguf"

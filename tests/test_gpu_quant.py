@@ -12,10 +12,12 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import GEOM, Q4_K, Q6_K, Q8_0, assert_close, assert_close_rows, synth_blocks, weight
+from tests._util import (F16, F32, GEOM, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, assert_close, assert_close_rows,
+                         synth_blocks, weight)
 
 pytestmark = pytest.mark.gpu
-DTYPES = [Q8_0, Q4_K, Q6_K]
+DTYPES = [Q8_0, Q4_K, Q5_K, Q6_K]           # the formats with a fused kernel (row-major [n][k] blocks)
+DEQ_DTYPES = DTYPES + [Q2_K, Q3_K, F16, F32]
 
 
 def dev(torch, arr):
@@ -40,7 +42,7 @@ def gemv(torch, w, x, n, m=1, flags=0, y0=None):
 
 # ── dequant: bit-exact ────────────────────────────────────────────────────
 
-@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dtype", DEQ_DTYPES)
 def test_dequant_bit_exact_random_bytes(gpu, dtype):
     """Fully random bytes: f16 scales hit subnormals, NaN and Inf patterns
     (the bits/65536 rule of decode_d, dequant.rs:161-168)."""
@@ -52,6 +54,10 @@ def test_dequant_bit_exact_random_bytes(gpu, dtype):
     if dtype == Q8_0:  # the plain-f16 path: keep finite scales so NaN != NaN does not matter
         rb = raw.reshape(nblk, bb)
         rb[:, 1] &= 0x7B
+    if dtype == F16:
+        raw.reshape(-1, 2)[:, 1] &= 0x7B
+    if dtype == F32:
+        raw.reshape(-1, 4)[:, 3] &= 0x7F
     n = nblk * be
     ref = O.dequant(dtype, raw, n)
     out = torch.full((n,), float("nan"), dtype=torch.float32, device="cuda")
@@ -62,7 +68,7 @@ def test_dequant_bit_exact_random_bytes(gpu, dtype):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dtype", DEQ_DTYPES)
 def test_dequant_bit_exact_benchmark_blocks(gpu, dtype):
     torch = gpu
     be, bb = GEOM[dtype]
@@ -142,7 +148,7 @@ def test_matmul_nonfinite_activation_gives_nan_rows(gpu, dtype):
     assert np.isnan(ref).all() and np.isnan(got).all()
 
 
-@pytest.mark.parametrize("dtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("dtype", [Q4_K, Q5_K, Q6_K])
 def test_matmul_reference_generators(gpu, dtype):
     """The reference's own test inputs (src/quant/matmul/tests.rs:3-17,
     :386-508): a[i] = ((i*17)%100)/50 - 1, b[i] = (i*31)%256 — f16 scales hit
@@ -172,7 +178,8 @@ def test_matmul_accumulate_epilogue(gpu):
     assert_close(got[0], y0 + ref)
 
 
-@pytest.mark.parametrize("dtype,n,k", [(Q8_0, 4096, 4096), (Q4_K, 14336, 4096), (Q6_K, 128256, 4096)])
+@pytest.mark.parametrize("dtype,n,k", [(Q8_0, 4096, 4096), (Q4_K, 14336, 4096), (Q6_K, 128256, 4096),
+                                       (Q5_K, 14336, 4096)])
 def test_benchmark_config_parity(gpu, dtype, n, k):
     """BASELINE configs 1-3 at full size, weights from the device generator
     copied back so oracle and GPU see identical bytes."""
@@ -211,7 +218,8 @@ def test_quantized_matmul_impl_host_slices(gpu):
                                              c.ctypes.data), "quantized_matmul_impl")
         assert_close(c.reshape(m, n), O.reference_matmul(dtype, a, raw, m, n, k))
         c2 = np.full(m * n, np.nan, dtype=np.float32)
-        fn = {Q8_0: L.aeth_matmul_q8_0, Q4_K: L.aeth_matmul_q4_k, Q6_K: L.aeth_matmul_q6_k}[dtype]
+        fn = {Q8_0: L.aeth_matmul_q8_0, Q4_K: L.aeth_matmul_q4_k, Q5_K: L.aeth_matmul_q5_k,
+              Q6_K: L.aeth_matmul_q6_k}[dtype]
         A.check(fn(a.ctypes.data, raw.ctypes.data, raw.size, m, n, k, c2.ctypes.data), "matmul_q*")
         assert np.array_equal(c, c2)
     A.check(L.aeth_weight_cache_clear())

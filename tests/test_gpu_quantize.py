@@ -15,10 +15,10 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import GEOM, Q4_K, Q6_K, Q8_0, assert_close, synth_blocks
+from tests._util import GEOM, Q4_K, Q5_K, Q6_K, Q8_0, assert_close, synth_blocks
 
 pytestmark = pytest.mark.gpu
-DTYPES = [Q8_0, Q4_K, Q6_K]
+DTYPES = [Q8_0, Q4_K, Q5_K, Q6_K]
 
 
 def special_rows(rng, rows, cols, with_nonfinite=True):
