@@ -62,6 +62,9 @@ _SIGS = {
     "aeth_matmul_q8_0": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q4_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q5_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
+    "aeth_matmul_q2_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
+    "aeth_matmul_q3_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
+    "aeth_matmul_f16": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q6_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_register_hip_kernels": (_INT, []),
     "aeth_registered_kernel_name": (_INT, [_INT, ctypes.c_char_p, _INT]),

@@ -16,6 +16,7 @@ SOURCES = [
     "aeth_dequant.hip",
     "aeth_quantize.hip",
     "aeth_gemv.hip",
+    "aeth_gemv_ext.hip",
     "aeth_gemm.hip",
     "aeth_decode_ops.hip",
     "aeth_prefill.hip",

@@ -361,12 +361,6 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
     return __any(bad);
 }
 
-__device__ __forceinline__ unsigned long long mq_amax_key(float v, int64_t row) {
-    const uint32_t f = __float_as_uint(v);
-    const uint32_t o = (f & 0x80000000u) ? ~f : (f | 0x80000000u);
-    return ((unsigned long long)o << 32) | (unsigned long long)(uint32_t)row;
-}
-
 // Fusions:
 //  norm_w    : x ← x / sqrt(Σx²/k + eps) · norm_w first (rmsnorm_inplace, runner.rs:1739-1746);
 //  swiglu    : rows (2i, 2i+1) = (gate_i, up_i); y[i] = g·σ(g)·u (runner.rs:1617-1625);
@@ -492,7 +486,7 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
             const float v = G.accumulate ? yr[row] + sum : sum;
             yr[row] = v;
             if (G.amax) {
-                const unsigned long long kk = mq_amax_key(v, row);
+                const unsigned long long kk = aeth_amax_key(v, row);
                 best = kk > best ? kk : best;
             }
         }
@@ -581,6 +575,7 @@ static int mq_dispatch(MqParams G, int64_t m, hipStream_t s) {
 
 int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, const GemvEpi& e,
                         hipStream_t s) {
+    if (w->order != AETH_ORDER_PLANAR) return aeth_xgemv_launch(w, d_x, m, d_y, e, s);
     if (m > 65535) return aeth_set_error(AETH_EINVAL, "gemv: m=%lld exceeds 65535", (long long)m);
     MqParams G;
     G.p0 = w->p0;

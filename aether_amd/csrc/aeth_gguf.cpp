@@ -252,22 +252,32 @@ struct Staging {
     }
 };
 
-// load_quant (model_loader.rs:330-359): GGUF shape [k, n] → QuantWeight bytes [n][k] (host)
+// load_quant (model_loader.rs:330-359): GGUF shape [k, n] → QuantWeight bytes (host): [n][k]
+// re-quantized rows for the fused formats, the GGUF bytes for the others
 int load_quant(const Gguf& g, const std::string& name, Staging& st, std::vector<uint8_t>& out, int* dtype,
                int64_t* n_out, int64_t* k_out) {
     auto it = g.tensors.find(name);
     if (it == g.tensors.end()) return aeth_set_error(AETH_EINVAL, "Missing tensor: %s", name.c_str());
     const TensorInfo& t = it->second;
     if (t.shape.size() != 2) return aeth_set_error(AETH_EUNSUPPORTED, "tensor %s is not 2-D", name.c_str());
-    if (t.dtype != AETH_DTYPE_Q8_0 && t.dtype != AETH_DTYPE_Q4_K && t.dtype != AETH_DTYPE_Q5_K &&
-        t.dtype != AETH_DTYPE_Q6_K)
-        return aeth_set_error(AETH_EUNSUPPORTED,
-                              "tensor %s: dtype %u is not a format this build runs (Q8_0, Q4_K, Q5_K, Q6_K)",
-                              name.c_str(), t.dtype);
     const int64_t k = (int64_t)t.shape[0], n = (int64_t)t.shape[1];
     int be, bb;
-    int rc = aeth_block_geometry((int)t.dtype, &be, &bb);
-    if (rc) return rc;
+    if (aeth_block_geometry((int)t.dtype, &be, &bb) != AETH_OK)
+        return aeth_set_error(AETH_EUNSUPPORTED,
+                              "tensor %s: dtype %u is not a format this build runs (F32, F16, Q8_0, Q2_K..Q6_K)",
+                              name.c_str(), t.dtype);
+    int rc;
+    if (!aeth_dtype_fused((int)t.dtype)) {  // F32 / F16 / Q2_K / Q3_K: the bytes as the file holds them (:348-350)
+        const int64_t need = aeth_weight_raw_bytes((int)t.dtype, AETH_ORDER_GGUF, n, k);
+        if (need < 0 || (uint64_t)need > t.bytes)
+            return aeth_set_error(AETH_EINVAL, "tensor %s: %llu bytes for [%lld, %lld]", name.c_str(),
+                                  (unsigned long long)t.bytes, (long long)k, (long long)n);
+        out.assign(t.data, t.data + need);
+        *dtype = (int)t.dtype;
+        *n_out = n;
+        *k_out = k;
+        return AETH_OK;
+    }
     const size_t out_b = (size_t)(n * ((k + be - 1) / be) * bb);
     if ((rc = Staging::grow(&st.src, &st.src_b, t.bytes)) || (rc = Staging::grow(&st.dst, &st.dst_b, out_b)) ||
         (rc = Staging::grow(&st.ws, &st.ws_b, (size_t)aeth_load_quant_ws_bytes(k, n))))

@@ -123,21 +123,21 @@ extern "C" AETH_API int aeth_argmax(const float* d_logits, int64_t n, int32_t* d
 
 // ── host-slice path: QuantWeight bytes → cached device weight ────────────
 namespace {
-using WKey = std::tuple<const void*, int64_t, int, int64_t, int64_t, int>;  // ptr, len, dtype, n, k, device
+using WKey = std::tuple<const void*, int64_t, int, int64_t, int64_t, int, int>;  // ptr, len, dtype, n, k, device, order
 std::mutex g_wc_mu;
 std::map<WKey, aeth_weight*> g_wcache;
 
-int cached_weight(const uint8_t* b_raw, int64_t b_len, int dtype, int64_t n, int64_t k, aeth_weight** out) {
+int cached_weight(const uint8_t* b_raw, int64_t b_len, int dtype, int order, int64_t n, int64_t k, aeth_weight** out) {
     int be, bb;
     int rc = aeth_block_geometry(dtype, &be, &bb);
     if (rc) return rc;
-    int64_t need = n * aeth_blocks_per_row(dtype, k) * bb;
+    int64_t need = aeth_weight_raw_bytes(dtype, order, n, k);
     if (b_len < need)
         return aeth_set_error(AETH_EINVAL, "weight bytes %lld < %lld needed for [%lld, %lld] dtype %d",
                               (long long)b_len, (long long)need, (long long)n, (long long)k, dtype);
     int dev = 0;
     AETH_HIP_CHECK(hipGetDevice(&dev));
-    WKey key{b_raw, b_len, dtype, n, k, dev};
+    WKey key{b_raw, b_len, dtype, n, k, dev, order};
     std::lock_guard<std::mutex> lk(g_wc_mu);
     auto it = g_wcache.find(key);
     if (it != g_wcache.end()) {
@@ -145,7 +145,7 @@ int cached_weight(const uint8_t* b_raw, int64_t b_len, int dtype, int64_t n, int
         return AETH_OK;
     }
     aeth_weight* w = nullptr;
-    rc = aeth_weight_create(dtype, n, k, b_raw, 0, nullptr, &w);
+    rc = aeth_weight_create_ex(dtype, order, n, k, b_raw, 0, nullptr, &w);
     if (rc) return rc;
     g_wcache[key] = w;
     *out = w;
@@ -153,9 +153,11 @@ int cached_weight(const uint8_t* b_raw, int64_t b_len, int dtype, int64_t n, int
 }
 
 // One host-slice matmul: H2D a, launch, D2H c (QuantKernel::matmul semantics:
-// c is fully written).
+// c is fully written). order: how b_raw is laid out — the QuantWeight form
+// (planar for the fused formats, GGUF [k][n] for the others) or [n][k] rows.
 int host_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, int64_t n, int64_t k, int dtype,
-                float* c) {
+                float* c, int order = -1) {
+    if (order < 0) order = aeth_dtype_fused(dtype) ? AETH_ORDER_PLANAR : AETH_ORDER_GGUF;
     if (!a || !b_raw || !c || m <= 0 || n <= 0 || k <= 0)
         return aeth_set_error(AETH_EINVAL, "matmul: bad argument (m=%lld n=%lld k=%lld)", (long long)m, (long long)n,
                               (long long)k);
@@ -163,7 +165,7 @@ int host_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, 
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
         return aeth_set_error(AETH_EHIP, "matmul: no HIP device available (no CPU fallback in this library)");
     aeth_weight* w = nullptr;
-    int rc = cached_weight(b_raw, b_len, dtype, n, k, &w);
+    int rc = cached_weight(b_raw, b_len, dtype, order, n, k, &w);
     if (rc) return rc;
     float *da = nullptr, *dc = nullptr;
     AETH_HIP_CHECK(hipMalloc((void**)&da, sizeof(float) * m * k));
@@ -218,6 +220,10 @@ class HipQuantKernel final : public QuantKernel {
     int dtype() const override { return dtype_; }
     const char* name() const override {
         switch (dtype_) {
+            case AETH_DTYPE_F32: return "F32 (hip gfx950)";
+            case AETH_DTYPE_F16: return "F16 (hip gfx950)";
+            case AETH_DTYPE_Q2_K: return "Q2_K (hip gfx950)";
+            case AETH_DTYPE_Q3_K: return "Q3_K (hip gfx950)";
             case AETH_DTYPE_Q8_0: return "Q8_0 (hip gfx950)";
             case AETH_DTYPE_Q4_K: return "Q4_K (hip gfx950)";
             case AETH_DTYPE_Q5_K: return "Q5_K (hip gfx950)";
@@ -259,7 +265,8 @@ int dispatch_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_l
 }  // namespace aeth
 
 extern "C" AETH_API int aeth_register_hip_kernels(void) {
-    for (int dt : {AETH_DTYPE_Q8_0, AETH_DTYPE_Q4_K, AETH_DTYPE_Q5_K, AETH_DTYPE_Q6_K}) {
+    for (int dt : {AETH_DTYPE_F32, AETH_DTYPE_F16, AETH_DTYPE_Q8_0, AETH_DTYPE_Q2_K, AETH_DTYPE_Q3_K, AETH_DTYPE_Q4_K,
+                   AETH_DTYPE_Q5_K, AETH_DTYPE_Q6_K}) {
         int rc = aeth::register_kernel(std::unique_ptr<aeth::QuantKernel>(new aeth::HipQuantKernel(dt)));
         if (rc) return rc;
     }
@@ -281,13 +288,16 @@ extern "C" AETH_API int aeth_dispatch_matmul(const float* a, int64_t m, const ui
 
 // quantized_matmul_impl (dispatch.rs:98-135): registered kernel first; with
 // none registered the supported dtypes still run on the HIP kernels directly
-// (this library has no CPU path).
+// (this library has no CPU path). F32 / F16 / Q2_K / Q3_K bytes are GGUF
+// [k][n], as load_quant leaves them and the reference's dequantize fallback
+// reads them (dispatch.rs:126-133).
 extern "C" AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
                                                    int64_t n, int64_t k, int dtype, float* c) {
     int rc = aeth::dispatch_matmul(a, m, b_raw, b_len, n, k, dtype, c);
     if (rc == 1) return AETH_OK;
     if (rc < 0) return rc;
-    if (dtype != AETH_DTYPE_Q8_0 && dtype != AETH_DTYPE_Q4_K && dtype != AETH_DTYPE_Q5_K && dtype != AETH_DTYPE_Q6_K)
+    int be, bb;
+    if (aeth_block_geometry(dtype, &be, &bb) != AETH_OK)
         return aeth_set_error(AETH_EUNSUPPORTED, "quantized_matmul_impl: dtype %d not on the HIP path", dtype);
     return host_matmul(a, m, b_raw, b_len, n, k, dtype, c);
 }
@@ -303,6 +313,18 @@ extern "C" AETH_API int aeth_matmul_q4_k(const float* a, const uint8_t* b, int64
 extern "C" AETH_API int aeth_matmul_q5_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
                                          int64_t k, float* c) {
     return host_matmul(a, m, b, b_len, n, k, AETH_DTYPE_Q5_K, c);
+}
+extern "C" AETH_API int aeth_matmul_q2_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                                         int64_t k, float* c) {
+    return host_matmul(a, m, b, b_len, n, k, AETH_DTYPE_Q2_K, c, AETH_ORDER_ROWS);
+}
+extern "C" AETH_API int aeth_matmul_q3_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                                         int64_t k, float* c) {
+    return host_matmul(a, m, b, b_len, n, k, AETH_DTYPE_Q3_K, c, AETH_ORDER_ROWS);
+}
+extern "C" AETH_API int aeth_matmul_f16(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                                        int64_t k, float* c) {
+    return host_matmul(a, m, b, b_len, n, k, AETH_DTYPE_F16, c, AETH_ORDER_ROWS);
 }
 extern "C" AETH_API int aeth_matmul_q6_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
                                          int64_t k, float* c) {

@@ -3,10 +3,26 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// Device copy of one QuantWeight in per-field planes, rows in 16-row tiles
-// (layouts in aeth_weights.hip).
+#include "../../include/aether_hip.h"
+
+// How a weight's bytes are held on the device.
+enum {
+    AETH_ORDER_PLANAR = 0,  // Q8_0 / Q4_K / Q5_K / Q6_K: [n][k] row blocks re-laid in per-field planes
+    AETH_ORDER_GGUF = 1,    // F32 / F16 / Q2_K / Q3_K as load_quant keeps them: GGUF [k][n], raw
+    AETH_ORDER_ROWS = 2,    // F16 / Q2_K / Q3_K [n][k] row blocks, raw (matmul_f16 / _q2_k / _q3_k)
+};
+
+// The formats with a fused matrix-core kernel (is_quantized_type_supported,
+// model_loader.rs:362-367): load_quant re-quantizes them into [n][k] rows.
+inline bool aeth_dtype_fused(int dtype) {
+    return dtype == AETH_DTYPE_Q8_0 || dtype == AETH_DTYPE_Q4_K || dtype == AETH_DTYPE_Q5_K || dtype == AETH_DTYPE_Q6_K;
+}
+
+// Device copy of one QuantWeight: planar (row tiles of 16, layouts in
+// aeth_weights.hip) for the fused formats, the raw bytes otherwise.
 struct aeth_weight {
     int dtype;
+    int order;            // AETH_ORDER_*
     int64_t n, k;         // out_features, in_features
     int64_t nb;           // blocks per row
     int64_t nblk;         // n * nb
@@ -18,6 +34,19 @@ struct aeth_weight {
 
 int aeth_num_cus();
 int64_t aeth_blocks_per_row(int dtype, int64_t k);
+// Bytes of a weight's raw form: planar / rows: n·blocks_per_row·block_bytes;
+// GGUF order: (n·k / block_elems)·block_bytes. < 0 on a bad dtype / shape.
+int64_t aeth_weight_raw_bytes(int dtype, int order, int64_t n, int64_t k);
+int aeth_weight_create_ex(int dtype, int order, int64_t n, int64_t k, const void* raw, int raw_is_device,
+                          hipStream_t s, aeth_weight** out);
+
+// Orderable 64-bit key of (value, row) for the fused greedy argmax: a larger
+// value wins, ties go to the larger row (Iterator::max_by, runner.rs:1964-1973).
+__device__ __forceinline__ unsigned long long aeth_amax_key(float v, int64_t row) {
+    const uint32_t f = __float_as_uint(v);
+    const uint32_t o = (f & 0x80000000u) ? ~f : (f | 0x80000000u);
+    return ((unsigned long long)o << 32) | (unsigned long long)(uint32_t)row;
+}
 
 // Q4_K device layout: rows are grouped in tiles of 16 (zero rows pad the last
 // tile) so that one wave load covers 16 rows × 64 quant bytes contiguously.
@@ -40,6 +69,8 @@ struct GemvEpi {
     int swiglu = 0;                       // rows are (gate, up) pairs; y gets n/2 outputs
     unsigned long long* amax = nullptr;   // fused greedy argmax key
     int64_t ldc = 0;                      // output row stride for m > 1 (0: the output width)
+    float* ws = nullptr;                  // GGUF-order weights: scratch of ws_floats floats
+    int64_t ws_floats = 0;                //   (NULL: the library's per-device scratch)
 };
 
 // GEMV on one activation row per launch-row (a: [m][k] f32, c: [m][n]).
@@ -47,6 +78,13 @@ int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float
                         hipStream_t s);
 int aeth_gemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, unsigned flags,
                      hipStream_t s);
+// VALU GEMV for GGUF-order and raw-row weights (aeth_gemv_ext.hip); the same
+// epilogue except SwiGLU (GGUF order: RMSNorm through the scratch, argmax and
+// accumulate in the reduction; raw rows: accumulate only).
+int aeth_xgemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, const GemvEpi& e,
+                      hipStream_t s);
+// Scratch floats a GGUF-order GEMV of m rows needs at most.
+int64_t aeth_xgemv_ws_floats(const aeth_weight* w, int64_t m);
 // Q4_K prefill GEMM (m > 1); ldc = output row stride (0: n).
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s, int64_t ldc = 0);

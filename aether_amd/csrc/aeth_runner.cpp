@@ -10,6 +10,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <chrono>
 #include <mutex>
 #include <vector>
@@ -40,6 +41,8 @@ struct aeth_runner {
     float *x = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
     float* attn_ws = nullptr;
     void* am_ws = nullptr;
+    float* xws = nullptr;    // scratch of the GGUF-order GEMVs (F32 / F16 / Q2_K / Q3_K weights)
+    int64_t xws_floats = 0;
     int* st = nullptr;       // device {token, pos, fill, next token}
     unsigned long long* amax = nullptr;  // fused LM-head argmax key (reset by the state kernel)
     int* tok_out = nullptr;  // unused slot kept for the release list
@@ -84,7 +87,8 @@ int make_weight(int dtype, int64_t n, int64_t k, const void* host_raw, uint64_t 
     int rc = aeth_block_geometry(dtype, &be, &bb);
     if (rc) return rc;
     if (host_raw) return aeth_weight_create(dtype, n, k, host_raw, 0, s, out);
-    int64_t nblk = n * aeth_blocks_per_row(dtype, k);
+    const int order = aeth_dtype_fused(dtype) ? AETH_ORDER_PLANAR : AETH_ORDER_GGUF;
+    const int64_t nblk = aeth_weight_raw_bytes(dtype, order, n, k) / bb;
     void* raw = nullptr;
     AETH_HIP_CHECK(hipMalloc(&raw, (size_t)(nblk * bb)));
     rc = aeth_fill_synthetic_raw(dtype, seed, raw, nblk, s);
@@ -157,7 +161,7 @@ void runner_release(aeth_runner* r) {
     for (auto* w : r->wdown) aeth_weight_free(w);
     aeth_weight_free(r->lm_head);
     void* bufs[] = {r->norms, r->final_norm, r->emb, r->rope_sin, r->rope_cos, r->kv, r->x, r->normed, r->qkv,
-                    r->attn, r->gu, r->logits, r->attn_ws, r->am_ws, r->st, r->tok_out, r->amax,
+                    r->attn, r->gu, r->logits, r->attn_ws, r->am_ws, r->st, r->tok_out, r->amax, r->xws,
                     r->p_x, r->p_n, r->p_qkv, r->p_att, r->p_gu, r->p_h, r->p_tok};
     for (void* b : bufs)
         if (b) hipFree(b);
@@ -172,6 +176,15 @@ void runner_release(aeth_runner* r) {
 //   x   += attn · Woᵀ                              (residual fused)
 //   h    = silu(g)·u, [g|u] = rmsnorm(x, ffn_norm) · Wguᵀ (norm + SwiGLU fused)
 //   x   += h · Wdownᵀ                              (residual fused)
+// A decode-step epilogue carrying the runner's GGUF-order scratch (so no
+// launch allocates, as graph capture requires).
+GemvEpi step_epi(const aeth_runner* r) {
+    GemvEpi e;
+    e.ws = r->xws;
+    e.ws_floats = r->xws_floats;
+    return e;
+}
+
 int enqueue_layers(aeth_runner* r, int l0, int l1) {
     const aeth_llama_config& c = r->cfg;
     hipStream_t s = r->stream;
@@ -179,7 +192,7 @@ int enqueue_layers(aeth_runner* r, int l0, int l1) {
     int rc;
     for (int l = l0; l < l1; l++) {
         float* lkv = r->kv + (int64_t)l * kv_layer_floats(c);
-        GemvEpi e1;
+        GemvEpi e1 = step_epi(r);
         e1.norm_w = r->norms + (int64_t)l * 2 * d;
         e1.eps = c.rms_norm_eps;
         if (r->wqkv[l]) {
@@ -194,10 +207,10 @@ int enqueue_layers(aeth_runner* r, int l0, int l1) {
         if ((rc = aeth_attn_launch(nullptr, r->qkv, lkv, r->rope_sin, r->rope_cos, r->st, 0, nh, nkv, hd,
                                    c.max_seq_len, r->attn_ws, r->attn, s)))
             return rc;
-        GemvEpi e2;
+        GemvEpi e2 = step_epi(r);
         e2.flags = AETH_MM_ACCUMULATE;
         if ((rc = aeth_gemv_launch_ex(r->wo[l], r->attn, 1, r->x, e2, s))) return rc;
-        GemvEpi e3;
+        GemvEpi e3 = step_epi(r);
         e3.norm_w = r->norms + (int64_t)l * 2 * d + d;
         e3.eps = c.rms_norm_eps;
         if (r->wgu[l]) {
@@ -221,7 +234,7 @@ int enqueue_head(aeth_runner* r) {
     const aeth_llama_config& c = r->cfg;
     hipStream_t s = r->stream;
     int rc;
-    GemvEpi e;
+    GemvEpi e = step_epi(r);
     e.norm_w = r->final_norm;
     e.eps = c.rms_norm_eps;
     e.amax = r->amax;
@@ -389,9 +402,10 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
         auto hw = [&](int j) -> const void* { return W ? W[j] : nullptr; };
         aeth_weight* w = nullptr;
         // q|k|v rows fused into one weight, gate/up rows interleaved (SwiGLU epilogue),
-        // when they share a dtype; separate weights otherwise (mixed-format files)
+        // when they share a fused format; separate weights otherwise (mixed-format
+        // files; GGUF-order F32 / F16 / Q2_K / Q3_K weights, whose rows are not [out] rows)
         for (auto* v : {&r->wqkv, &r->wq, &r->wk, &r->wv, &r->wgu, &r->wg, &r->wu}) v->push_back(nullptr);
-        if (T[0] == T[1] && T[0] == T[2]) {
+        if (T[0] == T[1] && T[0] == T[2] && aeth_dtype_fused(T[0])) {
             RC(make_concat(T[0], {qd, kvd, kvd}, d, {hw(0), hw(1), hw(2)}, mix(seed, l, 1), s, &r->wqkv[l]));
         } else {
             RC(make_weight(T[0], qd, d, hw(0), mix(seed, l, 1), s, &r->wq[l]));
@@ -400,7 +414,7 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
         }
         RC(make_weight(T[3], d, qd, hw(3), mix(seed, l, 4), s, &w));
         r->wo.push_back(w);
-        if (T[4] == T[5]) {
+        if (T[4] == T[5] && aeth_dtype_fused(T[4])) {
             RC(make_interleaved(T[4], dff, d, hw(4), hw(5), mix(seed, l, 5), s, &r->wgu[l]));
         } else {
             RC(make_weight(T[4], dff, d, hw(4), mix(seed, l, 5), s, &r->wg[l]));
@@ -410,6 +424,15 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
         r->wdown.push_back(w);
     }
     RC(make_weight(lm_dtype, c.vocab_size, d, lm_head, mix(seed, 1000003, 9), s, &r->lm_head));
+    {  // scratch for the GGUF-order weights' decode GEMVs (one row)
+        int64_t need = aeth_xgemv_ws_floats(r->lm_head, 1);
+        for (auto* v : {&r->wq, &r->wk, &r->wv, &r->wo, &r->wg, &r->wu, &r->wdown})
+            for (auto* w : *v) need = std::max(need, aeth_xgemv_ws_floats(w, 1));
+        if (need > 0) {
+            RC(dmalloc(&r->xws, need));
+            r->xws_floats = need;
+        }
+    }
     RC(dmalloc(&r->norms, (int64_t)c.num_layers * 2 * d));
     RC(dmalloc(&r->final_norm, d));
     RC(dmalloc(&r->emb, (int64_t)c.vocab_size * d));
@@ -614,8 +637,9 @@ extern "C" AETH_API int aeth_runner_export(const aeth_runner* r, int which, int3
     AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
     if (which >= 0 && which <= 6) {
         if (l < 0 || l >= c.num_layers) return aeth_set_error(AETH_EINVAL, "export: layer out of range");
-        const aeth_weight* sep[7] = {r->wq[l], r->wk[l], r->wv[l], nullptr, r->wg[l], r->wu[l], nullptr};
-        if (sep[which]) {  // a separately stored weight: its bytes as they are
+        const aeth_weight* sep[7] = {r->wq[l], r->wk[l], r->wv[l], r->wo[l], r->wg[l], r->wu[l], r->wdown[l]};
+        if (sep[which] && ((which != 3 && which != 6) || sep[which]->order != AETH_ORDER_PLANAR)) {
+            // a separately stored weight (or a raw-order one): its bytes as they are
             if (host_bytes < sep[which]->bytes) return aeth_set_error(AETH_EINVAL, "export: buffer too small");
             return aeth_weight_export_raw(sep[which], host, 0, r->stream);
         }

@@ -45,6 +45,10 @@ extern "C" AETH_API int aeth_init(int device) {
 extern "C" AETH_API int aeth_block_geometry(int dtype, int* block_elems, int* block_bytes) {
     int e, b;
     switch (dtype) {
+        case AETH_DTYPE_F32: e = 1; b = 4; break;
+        case AETH_DTYPE_F16: e = 1; b = 2; break;
+        case AETH_DTYPE_Q2_K: e = QK_BLOCK_ELEMS; b = Q2K_BLOCK_BYTES; break;
+        case AETH_DTYPE_Q3_K: e = QK_BLOCK_ELEMS; b = Q3K_BLOCK_BYTES; break;
         case AETH_DTYPE_Q8_0: e = Q8_BLOCK_ELEMS; b = Q8_BLOCK_BYTES; break;
         case AETH_DTYPE_Q4_K: e = QK_BLOCK_ELEMS; b = Q4K_BLOCK_BYTES; break;
         case AETH_DTYPE_Q5_K: e = QK_BLOCK_ELEMS; b = Q5K_BLOCK_BYTES; break;
@@ -58,10 +62,18 @@ extern "C" AETH_API int aeth_block_geometry(int dtype, int* block_elems, int* bl
 
 // Blocks per row as the reference counts them: Q8_0 rows hold ceil(k/32)
 // blocks (q8_0.rs:16, requantize_q8_0); K-quant kernels read k/256 blocks
-// (avx2.rs:26, q4_k.rs:16).
+// (avx2.rs:26, q4_k.rs:16, q2_k.rs:16); F16 / F32 rows hold k elements.
 int64_t aeth_blocks_per_row(int dtype, int64_t k) {
     if (dtype == AETH_DTYPE_Q8_0) return (k + 31) / 32;
+    if (dtype == AETH_DTYPE_F16 || dtype == AETH_DTYPE_F32) return k;
     return k / 256;
+}
+
+int64_t aeth_weight_raw_bytes(int dtype, int order, int64_t n, int64_t k) {
+    int be, bb;
+    if (aeth_block_geometry(dtype, &be, &bb) != AETH_OK || n <= 0 || k <= 0) return -1;
+    if (order == AETH_ORDER_GGUF) return (n * k / be) * bb;  // dequantize's flat run of whole blocks
+    return n * aeth_blocks_per_row(dtype, k) * bb;
 }
 
 // ── device layout ────────────────────────────────────────────────────────
@@ -152,8 +164,54 @@ static int relayout(aeth_weight* w, uint8_t* d_raw, int to_planar, hipStream_t s
     return AETH_OK;
 }
 
-extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, const void* raw, int raw_is_device,
-                                           void* stream, aeth_weight** out) {
+// Raw (GGUF-order or row) weights: the bytes as given, one allocation.
+static int create_raw(int dtype, int order, int64_t n, int64_t k, const void* raw, int raw_is_device, hipStream_t s,
+                      aeth_weight** out) {
+    const int64_t bytes = aeth_weight_raw_bytes(dtype, order, n, k);
+    const bool kq = dtype == AETH_DTYPE_Q2_K || dtype == AETH_DTYPE_Q3_K;
+    // the GEMV lanes read 4 consecutive elements of one row (and one block)
+    if (order == AETH_ORDER_GGUF && n % 4)
+        return aeth_set_error(AETH_EUNSUPPORTED, "GGUF-order weights need out_features %% 4 == 0 (n=%lld)", (long long)n);
+    if (order == AETH_ORDER_GGUF && kq && (n * k) % 256)
+        return aeth_set_error(AETH_EINVAL, "GGUF-order Q2_K/Q3_K weights need whole blocks (n·k = %lld)",
+                              (long long)(n * k));
+    if (order == AETH_ORDER_ROWS && kq && k < 256)
+        return aeth_set_error(AETH_EINVAL, "aeth_weight_create: K-quant needs k >= 256 (k=%lld)", (long long)k);
+    if (order == AETH_ORDER_ROWS && dtype == AETH_DTYPE_F16 && k % 4)
+        return aeth_set_error(AETH_EUNSUPPORTED, "row-order F16 weights need k %% 4 == 0 (k=%lld)", (long long)k);
+    if (order == AETH_ORDER_ROWS && dtype == AETH_DTYPE_F32)
+        return aeth_set_error(AETH_EUNSUPPORTED, "row-order F32 weights are not a kernel of this build");
+    aeth_weight* w = new aeth_weight();
+    w->dtype = dtype;
+    w->order = order;
+    w->n = n;
+    w->k = k;
+    w->nb = aeth_blocks_per_row(dtype, k);
+    int be, bb;
+    aeth_block_geometry(dtype, &be, &bb);
+    w->block_bytes = bb;
+    w->nblk = bytes / bb;
+    w->bytes = bytes;
+    hipError_t e = hipMalloc((void**)&w->base, (size_t)(bytes > 0 ? bytes : 256));
+    if (e != hipSuccess) {
+        delete w;
+        return aeth_set_error(AETH_ENOMEM, "aeth_weight_create: hipMalloc(%lld) failed: %s", (long long)bytes,
+                              hipGetErrorString(e));
+    }
+    e = hipMemcpyAsync(w->base, raw, (size_t)bytes, raw_is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && !raw_is_device) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        hipFree(w->base);
+        delete w;
+        return aeth_set_error(AETH_EHIP, "aeth_weight_create: copy failed: %s", hipGetErrorString(e));
+    }
+    w->p0 = w->base;
+    *out = w;
+    return AETH_OK;
+}
+
+int aeth_weight_create_ex(int dtype, int order, int64_t n, int64_t k, const void* raw, int raw_is_device,
+                          hipStream_t s, aeth_weight** out) {
     if (!out) return aeth_set_error(AETH_EINVAL, "aeth_weight_create: out is NULL");
     *out = nullptr;
     int be, bb;
@@ -161,12 +219,15 @@ extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, cons
     if (rc) return rc;
     if (n <= 0 || k <= 0) return aeth_set_error(AETH_EINVAL, "aeth_weight_create: bad shape n=%lld k=%lld",
                                                 (long long)n, (long long)k);
+    if (!raw) return aeth_set_error(AETH_EINVAL, "aeth_weight_create: raw is NULL");
+    if (order != AETH_ORDER_PLANAR) return create_raw(dtype, order, n, k, raw, raw_is_device, s, out);
+    if (!aeth_dtype_fused(dtype))
+        return aeth_set_error(AETH_EUNSUPPORTED, "aeth_weight_create: dtype %d has no planar layout", dtype);
     if (dtype != AETH_DTYPE_Q8_0 && k < 256)
         return aeth_set_error(AETH_EINVAL, "aeth_weight_create: K-quant needs k >= 256 (k=%lld)", (long long)k);
-    if (!raw) return aeth_set_error(AETH_EINVAL, "aeth_weight_create: raw is NULL");
-    hipStream_t s = (hipStream_t)stream;
     aeth_weight* w = new aeth_weight();
     w->dtype = dtype;
+    w->order = AETH_ORDER_PLANAR;
     w->n = n;
     w->k = k;
     w->nb = aeth_blocks_per_row(dtype, k);
@@ -234,6 +295,12 @@ extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, cons
     return AETH_OK;
 }
 
+extern "C" AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, const void* raw, int raw_is_device,
+                                           void* stream, aeth_weight** out) {
+    return aeth_weight_create_ex(dtype, aeth_dtype_fused(dtype) ? AETH_ORDER_PLANAR : AETH_ORDER_GGUF, n, k, raw,
+                                 raw_is_device, (hipStream_t)stream, out);
+}
+
 extern "C" AETH_API int aeth_weight_free(aeth_weight* w) {
     if (!w) return AETH_OK;
     if (w->base) AETH_HIP_CHECK(hipFree(w->base));
@@ -246,6 +313,12 @@ extern "C" AETH_API int64_t aeth_weight_bytes(const aeth_weight* w) { return w ?
 extern "C" AETH_API int aeth_weight_export_raw(const aeth_weight* w, void* dst, int dst_is_device, void* stream) {
     if (!w || !dst) return aeth_set_error(AETH_EINVAL, "aeth_weight_export_raw: NULL argument");
     hipStream_t s = (hipStream_t)stream;
+    if (w->order != AETH_ORDER_PLANAR) {
+        AETH_HIP_CHECK(hipMemcpyAsync(dst, w->base, (size_t)w->bytes,
+                                      dst_is_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, s));
+        if (!dst_is_device) AETH_HIP_CHECK(hipStreamSynchronize(s));
+        return AETH_OK;
+    }
     uint8_t* tmp = (uint8_t*)dst;
     if (!dst_is_device) AETH_HIP_CHECK(hipMalloc((void**)&tmp, (size_t)w->bytes));
     int rc = relayout((aeth_weight*)w, tmp, 0, s);
@@ -298,6 +371,24 @@ __global__ void k_fill_synthetic(int dtype, uint64_t seed, uint8_t* __restrict__
         } else {
             v = (uint8_t)splitmix64(key ^ ((uint64_t)i * 0x9E37ull + 0x1234567ull));
         }
+    } else if (dtype == AETH_DTYPE_Q2_K || dtype == AETH_DTYPE_Q3_K) {
+        const int bb = dtype == AETH_DTYPE_Q2_K ? Q2K_BLOCK_BYTES : Q3K_BLOCK_BYTES;
+        const int d0 = dtype == AETH_DTYPE_Q2_K ? 0 : 108;  // Q2_K: d, dmin lead; Q3_K: d last
+        const int nd = dtype == AETH_DTYPE_Q2_K ? 4 : 2;
+        int64_t blk = i / bb;
+        int off = (int)(i - blk * bb);
+        if (off >= d0 && off < d0 + nd) {
+            uint32_t b = scale_f16_bits(key, (uint64_t)blk, (off - d0) >> 1);
+            v = (uint8_t)(((off - d0) & 1) ? (b >> 8) : b);
+        } else {
+            v = (uint8_t)splitmix64(key ^ ((uint64_t)i * 0x9E37ull + 0x2718281ull));
+        }
+    } else if (dtype == AETH_DTYPE_F16 || dtype == AETH_DTYPE_F32) {
+        const int eb = dtype == AETH_DTYPE_F16 ? 2 : 4;
+        const int64_t el = i / eb;
+        const float x = 0.02f * normal_at(key ^ 0xF16F32ull, (uint64_t)el);
+        const uint32_t bits = dtype == AETH_DTYPE_F16 ? (uint32_t)__half_as_ushort(__float2half_rn(x)) : __float_as_uint(x);
+        v = (uint8_t)(bits >> (8 * (int)(i - el * eb)));
     } else if (dtype == AETH_DTYPE_Q6_K) {
         int64_t blk = i / Q6K_BLOCK_BYTES;
         int off = (int)(i - blk * Q6K_BLOCK_BYTES);

@@ -54,12 +54,17 @@ AETH_API int aeth_block_geometry(int dtype, int* block_elems, int* block_bytes);
 
 /* ── device-resident weights ─────────────────────────────────────────────
  * A registered weight is the device copy of one QuantWeight
- * (src/inference/model_loader.rs:88-93): `raw` holds n rows (out_features)
- * of k/block_elems GGUF blocks each, row-major, exactly as QuantWeight.data.
- * On upload it is re-laid into per-field planes (scales / quants split so
- * every wave load is 16-byte aligned and contiguous); aeth_weight_export_raw
- * reproduces the original bytes. The QuantKernel host-slice path registers
- * weights implicitly (see aeth_quantized_matmul_impl). */
+ * (src/inference/model_loader.rs:88-93) of shape [n, k] (out, in), with
+ * `raw` exactly as QuantWeight.data holds it:
+ *   Q8_0 / Q4_K / Q5_K / Q6_K — n rows of k/block_elems GGUF blocks (the
+ *     form load_quant re-quantizes them into, model_loader.rs:344-347);
+ *     re-laid on upload into per-field planes (scales / quants split so every
+ *     wave load is 16-byte aligned and contiguous);
+ *   F32 / F16 / Q2_K / Q3_K — the GGUF tensor as the file holds it, [k][n]
+ *     read as one flat run of elements / blocks (model_loader.rs:348-350);
+ *     kept as is (Q2_K / Q3_K need n % 256 == 0).
+ * aeth_weight_export_raw reproduces the original bytes. The QuantKernel
+ * host-slice path registers weights implicitly (see aeth_quantized_matmul_impl). */
 typedef struct aeth_weight aeth_weight;
 
 AETH_API int aeth_weight_create(int dtype, int64_t n, int64_t k, const void* raw, int raw_is_device,
@@ -109,13 +114,17 @@ AETH_API int aeth_load_quant(int dtype, const void* d_src, int64_t k, int64_t n,
 /* C[m×n] = A[m×k] · Wᵀ on the device — QuantKernel::matmul
  * (src/quant/matmul/registry.rs:7-19) / quantized_matmul_impl
  * (src/quant/matmul/dispatch.rs:98-135) with device operands. m == 1 runs the
- * decode GEMV; m > 1 runs the prefill GEMM (Q4_K: fp16-split MFMA; others:
- * row-batched GEMV). */
+ * decode GEMV; m > 1 runs the prefill GEMM (Q4_K: fp16-split MFMA; other
+ * fused formats: row-batched GEMV). F32 / F16 / Q2_K / Q3_K weights take the
+ * GGUF-order kernel of matmul_f32_gguf (dispatch.rs:541-574), which uses a
+ * per-device scratch buffer of the library: concurrent calls on different
+ * streams of one device must not overlap. */
 AETH_API int aeth_qmatmul(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                           void* stream);
 
 /* Same, on GGUF bytes and host slices: quantized_matmul_impl
- * (dispatch.rs:98-106) with b_shape = [n, k]. The weight bytes are uploaded
+ * (dispatch.rs:98-106) with b_shape = [n, k] — every format above, with the
+ * byte order of aeth_weight_create. The weight bytes are uploaded
  * once and cached by (pointer, length, dtype, n, k) — the bytes must stay
  * immutable while cached, as QuantWeight.data is (gguf.rs:177-277); a, c are
  * copied per call. Fails (no CPU fallback) if no device is usable. */
@@ -132,8 +141,19 @@ AETH_API int aeth_matmul_q6_k(const float* a, const uint8_t* b, int64_t b_len, i
 /* matmul_q5_k (src/quant/matmul/dispatch.rs:15-34, x86: avx2.rs:97-131). */
 AETH_API int aeth_matmul_q5_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
                               int64_t k, float* c);
+/* matmul_q2_k / matmul_q3_k / matmul_f16 (dispatch.rs:37-90; scalar forms
+ * q2_k.rs, q3_k.rs, f16.rs; x86: avx2.rs:210-389): b holds n rows of
+ * k/256 blocks (F16: n rows of k values), row-major [n][k] — unlike
+ * quantized_matmul_impl, which reads these formats in GGUF order. */
+AETH_API int aeth_matmul_q2_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                              int64_t k, float* c);
+AETH_API int aeth_matmul_q3_k(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                              int64_t k, float* c);
+AETH_API int aeth_matmul_f16(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,
+                             int64_t k, float* c);
 /* QuantKernel registry (registry.rs:33-63): registers the HIP kernels for
- * Q8_0, Q4_K, Q5_K and Q6_K; a second registration of a dtype fails with
+ * F32, F16, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K and Q6_K (bytes as
+ * quantized_matmul_impl passes them); a second registration of a dtype fails with
  * AETH_ESTATE (the reference panics). aeth_dispatch_matmul returns 1 if a
  * registered kernel handled the call, 0 if none is registered for dtype, <0
  * on error. */

@@ -65,17 +65,24 @@ def assert_close(g, r, tol=1e-3, cos_min=0.9999, what=""):
     assert (cos > cos_min).all(), "%s: row cosine %r <= %r" % (what, cos.min(), cos_min)
 
 
-def assert_close_logits(g, r, tol=1e-3, floor=1e-5, cos_min=0.9999, what=""):
+def assert_close_logits(g, r, tol=1e-3, floor=1e-5, cos_min=0.9999, what="", exact=None):
     """Whole-model logits (a decode step or a prefill through every layer): the
     element-wise bar of assert_close, where an element may also sit within
     floor·max|r_row| of the reference. A logit is an f32 sum whose rounding scales
     with the row's largest terms; in a row spanning ±658 (the Q8_0 test model) the
     reference's own f32 order and any other exact-f32 order differ by a few 1e-3
-    on its small entries. Kernel-level outputs keep the plain element-wise bar."""
+    on its small entries. With `exact` (the float64 logits of the same model,
+    tests/_model64.py) an element also passes when it is no farther from the
+    exact value than the reference's own f32 result is (plus 1e-6·max|row|):
+    on the random test models the reference's f32 order itself drifts by up to
+    2e-5·max|row|. Kernel-level outputs keep the plain element-wise bar."""
     g = np.atleast_2d(np.asarray(g, dtype=np.float64))
     r = np.atleast_2d(np.asarray(r, dtype=np.float64))
     assert g.shape == r.shape, (g.shape, r.shape)
     ok = close_mask(g, r, tol) | (np.abs(g - r) <= floor * np.abs(r).max(axis=1, keepdims=True))
+    if exact is not None:
+        x = np.atleast_2d(np.asarray(exact, dtype=np.float64))
+        ok |= np.abs(g - x) <= np.abs(r - x) + 1e-6 * np.abs(x).max(axis=1, keepdims=True)
     if not ok.all():
         i = np.argwhere(~ok)[0]
         raise AssertionError("%s: %d/%d logits out of tolerance; first at %s: got %r ref %r (row max %r)" %

@@ -8,7 +8,9 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import Q4_K, Q5_K, Q6_K, Q8_0, assert_close, assert_close_logits, assert_close_rows, weight
+from tests._model64 import logits64
+from tests._util import (F16, F32, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, assert_close, assert_close_logits,
+                         assert_close_rows, weight)
 
 pytestmark = pytest.mark.gpu
 
@@ -324,6 +326,54 @@ def test_runner_mixed_formats(gpu, mix, n):
             assert np.array_equal(blob, m["layers"][1][j].view(np.uint8).ravel()), "export %d" % j
     finally:
         L.aeth_runner_free(r)
+
+
+# Layers and LM heads in the formats the reference keeps in GGUF order (F32 /
+# F16 / Q2_K / Q3_K: dequantize + matmul_f32_gguf, dispatch.rs:126-133), mixed
+# with fused ones: decode steps (eager and replayed as a HIP graph, whose
+# GGUF-order GEMVs use the runner's own scratch) and prefill against the oracle.
+GGUF_MIX = [[F16, Q2_K, Q3_K, F32, Q5_K, Q2_K, Q3_K], [Q3_K, Q3_K, Q3_K, Q2_K, Q2_K, Q2_K, F16]]
+
+
+@pytest.mark.parametrize("mix,lm_dtype", [(0, F16), (1, Q6_K)])
+def test_runner_gguf_order_formats(gpu, mix, lm_dtype):
+    c = dict(TINY, max_seq_len=64)
+    m = build_tiny(seed=21 + mix, layer_dtype=GGUF_MIX[mix], lm_dtype=lm_dtype, c=c)
+    L = A.lib()
+    ocfg = oracle_cfg(c)
+    s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
+    n = 19
+    toks = np.random.default_rng(mix).integers(0, c["vocab_size"], n).astype(np.int32)
+    r = make_runner(m, c)
+    try:
+        kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), dtype=np.float32)
+        logits = np.empty(c["vocab_size"], dtype=np.float32)
+        A.check(L.aeth_runner_prefill(r, toks.ctypes.data, n, logits.ctypes.data, None), "prefill")
+        ref = O.forward_batch(ocfg, m["emb"][toks], m["layers"], GGUF_MIX[mix], m["norms"], m["final"], m["lm"],
+                              lm_dtype, s, co, kv)
+        seq = list(toks)
+        ex = lambda: logits64(c, m["emb"], m["layers"], GGUF_MIX[mix], m["norms"], m["final"], m["lm"], lm_dtype, seq)
+        assert_close_logits(logits, ref, what="gguf-order prefill", exact=ex())
+        tok, fill = O.argmax(ref), n
+        for step in range(2):
+            nxt = ctypes.c_int32()
+            A.check(L.aeth_runner_decode(r, tok, fill, logits.ctypes.data, ctypes.byref(nxt)), "decode")
+            ref, fill = O.decode_step(ocfg, m["emb"][tok], fill, m["layers"], GGUF_MIX[mix], m["norms"], m["final"],
+                                      m["lm"], lm_dtype, s, co, kv, fill)
+            seq.append(tok)
+            assert_close_logits(logits, ref, what="gguf-order decode %d" % step, exact=ex())
+            assert nxt.value == O.argmax(logits)
+            tok = O.argmax(ref)
+    finally:
+        L.aeth_runner_free(r)
+    outs = []
+    for use_graph in (0, 1):
+        r = make_runner(m, c)
+        t = (ctypes.c_int32 * 8)()
+        A.check(L.aeth_runner_generate(r, 1, 0, 8, t, use_graph), "generate")
+        outs.append(list(t))
+        L.aeth_runner_free(r)
+    assert outs[0] == outs[1]
 
 
 def test_runner_prefill_bad_arguments(gpu):

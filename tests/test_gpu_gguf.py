@@ -11,7 +11,8 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import GEOM, Q4_K, Q5_K, Q6_K, Q8_0, assert_close_logits, synth_blocks
+from tests._model64 import logits64
+from tests._util import F16, F32, GEOM, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, assert_close_logits, synth_blocks
 from tests.gguf_writer import ARR, F32, STR, U32, write_gguf
 
 pytestmark = pytest.mark.gpu
@@ -21,9 +22,13 @@ CFG = dict(vocab_size=512, d_model=256, num_layers=2, num_heads=2, num_kv_heads=
 
 
 def quant_gguf(dtype, k, n, seed):
-    """GGUF bytes of a [k, n] tensor and the QuantWeight bytes load_quant makes of them."""
+    """GGUF bytes of a [k, n] tensor and the QuantWeight bytes load_quant makes of them
+    (re-quantized [n][k] rows for Q8_0 / Q4_K / Q5_K / Q6_K, the bytes themselves
+    otherwise, model_loader.rs:344-350)."""
     be = GEOM[dtype][0]
     raw = synth_blocks(dtype, (k * n + be - 1) // be, seed).ravel()
+    if dtype in (F32, F16, Q2_K, Q3_K):
+        return raw, raw
     flat = O.dequant(dtype, raw, k * n)
     return raw, O.requantize(dtype, flat.reshape(k, n).T.ravel(), n, k)
 
@@ -96,12 +101,18 @@ Q4_K_M = [Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K]   # llama.cpp's mix: attn_v 
 Q5_K_M = [Q5_K, Q5_K, Q6_K, Q5_K, Q5_K, Q5_K, Q6_K]
 
 
-@pytest.mark.parametrize("layer_dtype,f16_norms", [(Q4_K, False), (Q8_0, True), (Q6_K, False), (Q4_K_M, False),
-                                                   (Q5_K_M, True)])
-def test_aether_load_prefill_decode_match_oracle(gpu, tmp_path, layer_dtype, f16_norms):
+Q3_K_M = [Q3_K, Q3_K, Q5_K, Q4_K, Q3_K, Q3_K, Q5_K]          # llama.cpp's Q3_K_M mix
+LOW_BIT = [Q2_K, Q2_K, Q3_K, F16, Q2_K, Q2_K, Q3_K]
+
+
+@pytest.mark.parametrize("layer_dtype,f16_norms,lm_dtype", [(Q4_K, False, Q6_K), (Q8_0, True, Q6_K),
+                                                            (Q6_K, False, Q6_K), (Q4_K_M, False, Q6_K),
+                                                            (Q5_K_M, True, Q6_K), (Q3_K_M, False, Q6_K),
+                                                            (LOW_BIT, True, F16)])
+def test_aether_load_prefill_decode_match_oracle(gpu, tmp_path, layer_dtype, f16_norms, lm_dtype):
     L = A.lib()
     path = tmp_path / "tiny.gguf"
-    mdl = build_file(path, layer_dtype=layer_dtype, f16_norms=f16_norms)
+    mdl = build_file(path, layer_dtype=layer_dtype, f16_norms=f16_norms, lm_dtype=lm_dtype)
     m = L.aether_load(str(path).encode())
     assert m, last_error(L)
     try:
@@ -118,12 +129,14 @@ def test_aether_load_prefill_decode_match_oracle(gpu, tmp_path, layer_dtype, f16
         assert L.aether_prefill(m, toks.ctypes.data, len(toks), logits.ctypes.data) == 0, last_error(L)
         ref = O.forward_batch(ocfg, mdl["emb"][toks], mdl["layers"], mdl["layer_dtype"], mdl["norms"], mdl["final"],
                               mdl["lm"], mdl["lm_dtype"], s, co, kv)
-        assert_close_logits(logits, ref, what="aether_load prefill")
+        ex = lambda seq: logits64(dict(c, max_seq_len=64), mdl["emb"], mdl["layers"], mdl["layer_dtype"], mdl["norms"],
+                                  mdl["final"], mdl["lm"], mdl["lm_dtype"], seq)
+        assert_close_logits(logits, ref, what="aether_load prefill", exact=ex(list(toks)))
         tok = int(np.argmax(ref))
         assert L.aether_decode(m, tok, len(toks), logits.ctypes.data) == 0, last_error(L)
         ref2, _ = O.decode_step(ocfg, mdl["emb"][tok], len(toks), mdl["layers"], mdl["layer_dtype"], mdl["norms"],
                                 mdl["final"], mdl["lm"], mdl["lm_dtype"], s, co, kv, len(toks))
-        assert_close_logits(logits, ref2, what="aether_load decode")
+        assert_close_logits(logits, ref2, what="aether_load decode", exact=ex(list(toks) + [tok]))
     finally:
         L.aether_free(m)
 
@@ -140,8 +153,8 @@ def test_aether_load_rejects_bad_files(gpu, tmp_path):
     build_file(p, drop="blk.1.attn_v.weight")
     assert not L.aether_load(str(p).encode())
     assert "blk.1.attn_v.weight" in last_error(L)
-    p = tmp_path / "f16_weight.gguf"
-    build_file(p, override=("blk.0.ffn_up.weight", [256, 512], 1, np.zeros(256 * 512 * 2, dtype=np.uint8)))
+    p = tmp_path / "q4_0_weight.gguf"  # Q4_0 (ggml type 2) is not a format of this build
+    build_file(p, override=("blk.0.ffn_up.weight", [256, 512], 2, np.zeros(256 * 512 // 32 * 18, dtype=np.uint8)))
     assert not L.aether_load(str(p).encode())
     assert "ffn_up" in last_error(L)
     p = tmp_path / "swa.gguf"

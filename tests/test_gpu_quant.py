@@ -241,7 +241,7 @@ def test_registry_dispatch(gpu):
     c = np.zeros(n, dtype=np.float32)
     assert L.aeth_dispatch_matmul(a.ctypes.data, 1, raw.ctypes.data, raw.size, n, k, Q4_K, c.ctypes.data) == 1
     assert_close(c[None], O.reference_matmul(Q4_K, a, raw, 1, n, k))
-    assert L.aeth_dispatch_matmul(a.ctypes.data, 1, raw.ctypes.data, raw.size, n, k, 1, c.ctypes.data) == 0
+    assert L.aeth_dispatch_matmul(a.ctypes.data, 1, raw.ctypes.data, raw.size, n, k, 2, c.ctypes.data) == 0  # Q4_0
     A.check(L.aeth_weight_cache_clear())
 
 
@@ -329,3 +329,123 @@ def test_prefill_gemm_config_parity(gpu, n):
     cols[0], cols[-1] = 0, n - 1
     ref = O.reference_matmul(Q4_K, ad.cpu().numpy(), raw[cols].reshape(-1), m, len(cols), k)
     assert_close(got[:, cols], ref, what="prefill GEMM n=%d" % n)
+
+
+# ── F32 / F16 / Q2_K / Q3_K: GGUF-order and row kernels ───────────────────
+# quantized_matmul_impl keeps these formats in GGUF [k][n] order and multiplies
+# by dequantize + matmul_f32_gguf (dispatch.rs:126-133, 541-574); the
+# standalone matmul_f16 / _q2_k / _q3_k take [n][k] rows (x86: avx2.rs:210-389).
+GGUF_DTYPES = [F32, F16, Q2_K, Q3_K]
+# n = 300 / 128: K-quant blocks straddle the rows of W; k = 37: blocks span rows
+GGUF_SHAPES = [(1, 256, 256), (1, 4096, 1024), (3, 512, 300), (17, 768, 512), (1, 14336, 4096), (9, 256, 37),
+               (2, 300, 512), (1, 128, 1024)]
+
+
+@pytest.mark.parametrize("dtype", GGUF_DTYPES)
+@pytest.mark.parametrize("m,n,k", GGUF_SHAPES)
+def test_gguf_order_matmul_parity(gpu, dtype, m, n, k):
+    torch = gpu
+    L = A.lib()
+    be, bb = GEOM[dtype]
+    rng = np.random.default_rng(n + k + m)
+    raw = synth_blocks(dtype, n * k // be, n + 7 * k + dtype)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    x[rng.integers(0, m * k, 5)] = 0.0  # skipped rows of W (matmul_f32_gguf's a_i == 0 test)
+    w = make_weight(torch, dtype, n, k, raw)
+    back = np.zeros_like(raw)
+    A.check(L.aeth_weight_export_raw(w, back.ctypes.data, 0, None), "export")
+    assert np.array_equal(back, raw) and L.aeth_weight_bytes(w) == raw.size
+    got = gemv(torch, w, x, n, m)
+    y0 = rng.standard_normal(m * n).astype(np.float32)
+    got_acc = gemv(torch, w, x, n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    L.aeth_weight_free(w)
+    ref = O.gguf_order_matmul(dtype, x, raw, m, n, k)
+    assert_close(got, ref, what="gguf-order dtype %d m=%d n=%d k=%d" % (dtype, m, n, k))
+    assert_close(got_acc, ref + y0.reshape(m, n), what="gguf-order accumulate")
+
+
+def test_gguf_order_zero_activation_skips_infinite_weights(gpu):
+    """A zero activation skips its weight row even when that row holds an
+    infinity (0·inf would be NaN): matmul_f32_gguf's `if scale != 0.0`."""
+    n, k = 512, 64
+    w16 = (np.random.default_rng(1).standard_normal((k, n)) * 0.1).astype(np.float16)
+    w16[7] = np.inf
+    x = np.random.default_rng(2).standard_normal(k).astype(np.float32)
+    x[7] = 0.0
+    raw = w16.view(np.uint8).ravel()
+    w = make_weight(gpu, F16, n, k, raw)
+    got = gemv(gpu, w, x, n, 1)
+    A.lib().aeth_weight_free(w)
+    ref = O.gguf_order_matmul(F16, x, raw, 1, n, k)
+    assert np.isfinite(ref).all() and np.isfinite(got).all()
+    assert_close(got, ref)
+
+
+def test_gguf_order_shape_rules(gpu):
+    """GGUF-order weights: lanes read 4 consecutive outputs (n % 4 == 0) and
+    K-quant tensors are whole blocks (n·k % 256 == 0)."""
+    raw = synth_blocks(Q2_K, 302 * 128 // 256, 1)
+    w = ctypes.c_void_p()
+    assert A.lib().aeth_weight_create(Q2_K, 302, 128, raw.ctypes.data, 0, None, ctypes.byref(w)) == A.AETH_EUNSUPPORTED
+    assert "% 4" in A.last_error()
+    assert A.lib().aeth_weight_create(Q3_K, 4, 100, raw.ctypes.data, 0, None, ctypes.byref(w)) == A.AETH_EINVAL
+    assert "whole blocks" in A.last_error()
+
+
+@pytest.mark.parametrize("dtype,m,n,k", [(Q2_K, 1, 40, 512), (Q2_K, 3, 8, 256), (Q3_K, 1, 300, 4096), (Q3_K, 5, 33, 768),
+                                         (F16, 1, 8, 32), (F16, 3, 8, 128), (F16, 2, 70, 100), (F16, 1, 1000, 4096)])
+def test_row_kernels_standalone(gpu, dtype, m, n, k):
+    """matmul_q2_k / matmul_q3_k / matmul_f16 on [n][k] rows against the x86
+    dispatch (AVX2 order) — for F16 also the reference's own k = 32 / 128
+    cases (tests.rs:581-636)."""
+    L = A.lib()
+    be, bb = GEOM[dtype]
+    rng = np.random.default_rng(k * 3 + n)
+    raw = synth_blocks(dtype, n * (k // be), n + k)
+    a = rng.standard_normal(m * k).astype(np.float32)
+    c = np.full(m * n, np.nan, dtype=np.float32)
+    fn = {Q2_K: L.aeth_matmul_q2_k, Q3_K: L.aeth_matmul_q3_k, F16: L.aeth_matmul_f16}[dtype]
+    A.check(fn(a.ctypes.data, raw.ctypes.data, raw.size, m, n, k, c.ctypes.data), "matmul rows")
+    ref = O.reference_matmul(dtype, a, raw, m, n, k)
+    assert_close(c.reshape(m, n), ref, what="rows dtype %d" % dtype)
+    A.check(L.aeth_weight_cache_clear())
+
+
+def test_row_kernels_reference_generators(gpu):
+    """tests.rs:638-826: the reference's own Q2_K / Q3_K inputs (k = 256, n = 8,
+    m in {1, 3}) through the standalone kernels, against its scalar kernels."""
+    L = A.lib()
+    for dtype, fn in ((Q2_K, L.aeth_matmul_q2_k), (Q3_K, L.aeth_matmul_q3_k)):
+        for m in (1, 3):
+            k, n = 256, 8
+            b = ((np.arange(n * GEOM[dtype][1]) * 31) % 256).astype(np.uint8)
+            a = (((np.arange(m * k) * 17) % 100) / 50.0 - 1.0).astype(np.float32)
+            c = np.zeros(m * n, dtype=np.float32)
+            A.check(fn(a.ctypes.data, b.ctypes.data, b.size, m, n, k, c.ctypes.data), "rows")
+            assert_close(c.reshape(m, n), O.scalar_matmul(dtype, a, b, m, n, k), what="ref gen %d m=%d" % (dtype, m))
+    A.check(L.aeth_weight_cache_clear())
+
+
+def test_quantized_matmul_impl_gguf_order_formats(gpu):
+    """quantized_matmul_impl with F32 / F16 / Q2_K / Q3_K bytes in GGUF order
+    (test_asymmetric_gguf_order_f16, tests.rs:704-760, in general form), and
+    the same bytes through a registered kernel."""
+    L = A.lib()
+    A.check(L.aeth_weight_cache_clear())
+    k, n, m = 256, 512, 3
+    rng = np.random.default_rng(9)
+    buf = ctypes.create_string_buffer(64)
+    if L.aeth_registered_kernel_name(Q4_K, buf, 64) == 0:
+        A.check(L.aeth_register_hip_kernels(), "register")
+    for dtype in GGUF_DTYPES:
+        raw = synth_blocks(dtype, k * n // GEOM[dtype][0], 30 + dtype)
+        a = rng.standard_normal(m * k).astype(np.float32)
+        c = np.full(m * n, np.nan, dtype=np.float32)
+        A.check(L.aeth_quantized_matmul_impl(a.ctypes.data, m, raw.ctypes.data, raw.size, n, k, dtype,
+                                             c.ctypes.data), "quantized_matmul_impl")
+        assert_close(c.reshape(m, n), O.gguf_order_matmul(dtype, a, raw, m, n, k), what="qmi dtype %d" % dtype)
+        assert L.aeth_registered_kernel_name(dtype, buf, 64) == 1
+        c2 = np.zeros(m * n, dtype=np.float32)
+        assert L.aeth_dispatch_matmul(a.ctypes.data, m, raw.ctypes.data, raw.size, n, k, dtype, c2.ctypes.data) == 1
+        assert np.array_equal(c, c2)
+    A.check(L.aeth_weight_cache_clear())
