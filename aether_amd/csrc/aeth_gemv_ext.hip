@@ -32,20 +32,29 @@ namespace {
 
 template <int F> struct XU;
 
+// Each format splits into load (the raw words a lane needs, issued for a whole
+// batch of inputs before any is used) and expand (the four f32 weights).
+
 // dequant_q2_k (dequant.rs:350-398): 84-byte block [d][dmin][scales 16][qs 64];
 // element e = 128h + 32t + 16v + i is bits 2t of qs[32h + 16v + i], sub-block
 // 8h + 2t + v. Blocks are 4-byte aligned (84 = 4·21) and so are the lane's 4 qs bytes.
 template <> struct XU<AETH_DTYPE_Q2_K> {
-    __device__ static void decode(const uint8_t* W, int64_t f, float (&w)[4]) {
+    struct Raw { uint32_t dd, sc, q; int t; };
+    __device__ static Raw load(const uint8_t* W, int64_t f) {
         const uint8_t* b = W + (f >> 8) * Q2K_BLOCK_BYTES;
         const int e = (int)(f & 255), h = e >> 7, t = (e >> 5) & 3, v = (e >> 4) & 1;
-        const uint32_t dd = *(const uint32_t*)b;
-        const float d = aeth_decode_d(dd & 0xFFFFu), dmin = aeth_decode_d(dd >> 16);
-        const uint32_t sc = b[4 + 8 * h + 2 * t + v];
-        const uint32_t q = *(const uint32_t*)(b + 20 + 32 * h + 16 * v + (e & 15));
-        const float dl = d * (float)(sc & 0xF), ml = dmin * (float)(sc >> 4);
+        Raw r;
+        r.dd = *(const uint32_t*)b;
+        r.sc = b[4 + 8 * h + 2 * t + v];
+        r.q = *(const uint32_t*)(b + 20 + 32 * h + 16 * v + (e & 15));
+        r.t = t;
+        return r;
+    }
+    __device__ static void expand(const Raw& r, float (&w)[4]) {
+        const float d = aeth_decode_d(r.dd & 0xFFFFu), dmin = aeth_decode_d(r.dd >> 16);
+        const float dl = d * (float)(r.sc & 0xF), ml = dmin * (float)(r.sc >> 4);
 #pragma unroll
-        for (int c = 0; c < 4; c++) w[c] = dl * (float)((q >> (8 * c + 2 * t)) & 3) - ml;
+        for (int c = 0; c < 4; c++) w[c] = dl * (float)((r.q >> (8 * c + 2 * r.t)) & 3) - ml;
     }
 };
 
@@ -55,27 +64,38 @@ template <> struct XU<AETH_DTYPE_Q2_K> {
 // s = 8h + 2t + v (low nibble of scales[s % 8], high pair from scales[8 + s % 4]),
 // q = ql − 4·(1 − hbit), w = (d·(scale − 32))·q.
 template <> struct XU<AETH_DTYPE_Q3_K> {
-    __device__ static void decode(const uint8_t* W, int64_t f, float (&w)[4]) {
+    struct Raw { uint32_t q, hm, lob, hib, d; int e; };
+    __device__ static Raw load(const uint8_t* W, int64_t f) {
         const uint8_t* b = W + (f >> 8) * Q3K_BLOCK_BYTES;
         const int e = (int)(f & 255), h = e >> 7, t = (e >> 5) & 3, v = (e >> 4) & 1, i = e & 15;
         const uint16_t* qp = (const uint16_t*)(b + 32 + 32 * h + 16 * v + i);
         const uint16_t* hp = (const uint16_t*)(b + 16 * v + i);
-        const uint32_t q = (uint32_t)qp[0] | ((uint32_t)qp[1] << 16), hm = (uint32_t)hp[0] | ((uint32_t)hp[1] << 16);
         const int s = 8 * h + 2 * t + v;
-        const uint32_t lob = b[96 + (s & 7)], hib = b[104 + (s & 3)];
-        const int sc = (int)((s < 8 ? (lob & 0xF) : (lob >> 4)) | (((hib >> (2 * (s >> 2))) & 3) << 4)) - 32;
-        const float dl = aeth_decode_d(*(const uint16_t*)(b + 108)) * (float)sc;
+        Raw r;
+        r.q = (uint32_t)qp[0] | ((uint32_t)qp[1] << 16);
+        r.hm = (uint32_t)hp[0] | ((uint32_t)hp[1] << 16);
+        r.lob = b[96 + (s & 7)];
+        r.hib = b[104 + (s & 3)];
+        r.d = *(const uint16_t*)(b + 108);
+        r.e = e;
+        return r;
+    }
+    __device__ static void expand(const Raw& r, float (&w)[4]) {
+        const int h = r.e >> 7, t = (r.e >> 5) & 3, v = (r.e >> 4) & 1, s = 8 * h + 2 * t + v;
+        const int sc = (int)((s < 8 ? (r.lob & 0xF) : (r.lob >> 4)) | (((r.hib >> (2 * (s >> 2))) & 3) << 4)) - 32;
+        const float dl = aeth_decode_d(r.d) * (float)sc;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const int ql = (int)((q >> (8 * c + 2 * t)) & 3), hb = (int)((hm >> (8 * c + 4 * h + t)) & 1);
+            const int ql = (int)((r.q >> (8 * c + 2 * t)) & 3), hb = (int)((r.hm >> (8 * c + 4 * h + t)) & 1);
             w[c] = dl * (float)(ql - ((hb ^ 1) << 2));
         }
     }
 };
 
 template <> struct XU<AETH_DTYPE_F16> {
-    __device__ static void decode(const uint8_t* W, int64_t f, float (&w)[4]) {
-        const uint2 v = *(const uint2*)(W + 2 * f);
+    typedef uint2 Raw;
+    __device__ static Raw load(const uint8_t* W, int64_t f) { return *(const uint2*)(W + 2 * f); }
+    __device__ static void expand(const Raw& v, float (&w)[4]) {
         w[0] = aeth_f16_to_f32(v.x & 0xFFFFu);
         w[1] = aeth_f16_to_f32(v.x >> 16);
         w[2] = aeth_f16_to_f32(v.y & 0xFFFFu);
@@ -84,23 +104,25 @@ template <> struct XU<AETH_DTYPE_F16> {
 };
 
 template <> struct XU<AETH_DTYPE_F32> {
-    __device__ static void decode(const uint8_t* W, int64_t f, float (&w)[4]) {
-        const float4 v = *(const float4*)(W + 4 * f);
+    typedef float4 Raw;
+    __device__ static Raw load(const uint8_t* W, int64_t f) { return *(const float4*)(W + 4 * f); }
+    __device__ static void expand(const Raw& v, float (&w)[4]) {
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
     }
 };
 
-// GGUF order: partials part[s][row][j] of Σ_{i ∈ split s} x[row][i]·W[i][j].
 // GGUF order: partials part[s][row][j] of Σ_{i ∈ split s} x[row][i]·W[i][j]
-// (element (i, j) is flat element i·n + j; n % 4 == 0).
-template <int F, int R>
-__global__ void __launch_bounds__(256) k_col(const uint8_t* __restrict__ W, int64_t n, int64_t k,
-                                             const float* __restrict__ x, int64_t ldx, int m, int S,
-                                             float* __restrict__ part) {
-    __shared__ float4 red[4][R][64];
+// (element (i, j) is flat element i·n + j; n % 4 == 0). NW waves take every
+// NW-th input of the split, NB inputs per batch with all loads issued first.
+template <int F, int R, int NW>
+__global__ void __launch_bounds__(64 * NW) k_col(const uint8_t* __restrict__ W, int64_t n, int64_t k,
+                                                 const float* __restrict__ x, int64_t ldx, int m, int S,
+                                                 float* __restrict__ part) {
+    constexpr int NB = 8;
+    typedef typename XU<F>::Raw Raw;
+    __shared__ float4 red[NW][R][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t j0 = (int64_t)blockIdx.x * 256 + 4 * lane;  // this lane's first output
-    const bool live = j0 < n;
     const int s = blockIdx.y, r0 = blockIdx.z * R;
     const int64_t i0 = k * s / S, i1 = k * (s + 1) / S;
     float acc[R][4];
@@ -111,46 +133,65 @@ __global__ void __launch_bounds__(256) k_col(const uint8_t* __restrict__ W, int6
     const float* xr[R];
 #pragma unroll
     for (int r = 0; r < R; r++) xr[r] = x + (int64_t)min(r0 + r, m - 1) * ldx;
-    const int64_t jl = live ? j0 : n - 4;  // lanes past n read the last valid group, discarded
-#pragma unroll 2
-    for (int64_t i = i0 + wave; i < i1; i += 4) {
-        float w[4];
-        XU<F>::decode(W, i * n + jl, w);
+    const int64_t jl = j0 < n ? j0 : n - 4;  // lanes past n read the last valid group, discarded
+    for (int64_t ib = i0 + wave; ib < i1; ib += NW * NB) {
+        Raw raw[NB];
+        float xv[NB][R];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const float a = xr[r][i];
-            if (a != 0.0f) {  // matmul_f32_gguf skips zero activations (dispatch.rs:548)
+        for (int b = 0; b < NB; b++) {
+            const int64_t i = ib + (int64_t)b * NW, ic = i < i1 ? i : i1 - 1;
+            raw[b] = XU<F>::load(W, ic * n + jl);
 #pragma unroll
-                for (int t = 0; t < 4; t++) acc[r][t] = fmaf(a, w[t], acc[r][t]);
+            for (int r = 0; r < R; r++) xv[b][r] = i < i1 ? xr[r][ic] : 0.0f;  // past the split: skipped as 0
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            float w[4];
+            XU<F>::expand(raw[b], w);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float a = xv[b][r];
+                if (a != 0.0f) {  // matmul_f32_gguf skips zero activations (dispatch.rs:548)
+#pragma unroll
+                    for (int t = 0; t < 4; t++) acc[r][t] = fmaf(a, w[t], acc[r][t]);
+                }
             }
         }
     }
 #pragma unroll
     for (int r = 0; r < R; r++) red[wave][r][lane] = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
     __syncthreads();
-    const int e = threadIdx.x;  // output 256·blockIdx.x + e
-    const int64_t j = (int64_t)blockIdx.x * 256 + e;
-    if (j >= n) return;
     const float* rf = (const float*)red;
+    for (int idx = threadIdx.x; idx < R * 256; idx += 64 * NW) {
+        const int r = idx >> 8, e = idx & 255;
+        const int64_t j = (int64_t)blockIdx.x * 256 + e;
+        if (j >= n || r0 + r >= m) continue;
+        float v = rf[r * 256 + e];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        if (r0 + r >= m) break;
-        const float v = ((rf[(0 * R + r) * 256 + e] + rf[(1 * R + r) * 256 + e]) + rf[(2 * R + r) * 256 + e]) +
-                        rf[(3 * R + r) * 256 + e];
+        for (int wv = 1; wv < NW; wv++) v += rf[(wv * R + r) * 256 + e];
         part[((int64_t)s * m + r0 + r) * n + j] = v;
     }
 }
 
-// Σ over splits in order, then y = (accumulate ? y : 0) + Σ, and the argmax key.
+// Σ over the S splits, then y = (accumulate ? y : 0) + Σ, and the argmax key.
+// G lanes (a power of two ≥ S, at most 64) share one output: lane g loads the
+// partials of splits g, g + G, …, and the G lanes combine in a fixed
+// butterfly, so the result does not depend on scheduling.
+template <int G>
 __global__ void __launch_bounds__(256) k_col_reduce(const float* __restrict__ part, int S, int64_t m, int64_t n,
                                                     float* __restrict__ y, int64_t ldy, int accumulate,
                                                     unsigned long long* __restrict__ amax) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) / G;
+    const int g = threadIdx.x & (G - 1);
+    const bool live = idx < m * n;
+    const int64_t row = live ? idx / n : 0, j = live ? idx - row * n : 0;
+    float v = 0.0f;
+    if (live)
+        for (int s = g; s < S; s += G) v += part[((int64_t)s * m + row) * n + j];
+#pragma unroll
+    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
     unsigned long long best = 0;
-    if (idx < m * n) {
-        const int64_t row = idx / n, j = idx - row * n;
-        float v = part[row * n + j];
-        for (int s = 1; s < S; s++) v += part[((int64_t)s * m + row) * n + j];
+    if (live && g == 0) {
         float* dst = y + row * ldy + j;
         if (accumulate) v = *dst + v;
         *dst = v;
@@ -168,11 +209,13 @@ __global__ void __launch_bounds__(256) k_col_reduce(const float* __restrict__ pa
 
 // Rows: y[row][j] = Σ_e x[row][e]·W[j][e], a wave per output j, R rows.
 // Row j's elements start at flat element j·row_elems (K-quants: k/256 whole
-// blocks per row; F16: k values, k % 4 == 0).
+// blocks per row; F16: k values, k % 4 == 0); NB units per batch, loads first.
 template <int F, int R>
 __global__ void __launch_bounds__(256) k_row(const uint8_t* __restrict__ W, int64_t n, int64_t kr, int64_t row_elems,
                                              const float* __restrict__ x, int64_t ldx, int m, float* __restrict__ y,
                                              int64_t ldy, int accumulate) {
+    constexpr int NB = 4;
+    typedef typename XU<F>::Raw Raw;
     const int lane = threadIdx.x & 63;
     const int64_t j = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r0 = blockIdx.y * R;
@@ -183,17 +226,30 @@ __global__ void __launch_bounds__(256) k_row(const uint8_t* __restrict__ W, int6
     const float* xr[R];
 #pragma unroll
     for (int r = 0; r < R; r++) xr[r] = x + (int64_t)min(r0 + r, m - 1) * ldx;
-#pragma unroll 2
-    for (int64_t e = 4 * lane; e < kr; e += 256) {  // kr = elements read per row (a multiple of 4)
-        float w[4];
-        XU<F>::decode(W, j * row_elems + e, w);
+    for (int64_t eb = 4 * lane; eb < kr + 4 * lane; eb += 256 * NB) {  // kr: elements per row (a multiple of 4)
+        Raw raw[NB];
+        float4 xv[NB][R];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const float4 xv = *(const float4*)(xr[r] + e);
-            acc[r] = fmaf(xv.x, w[0], acc[r]);
-            acc[r] = fmaf(xv.y, w[1], acc[r]);
-            acc[r] = fmaf(xv.z, w[2], acc[r]);
-            acc[r] = fmaf(xv.w, w[3], acc[r]);
+        for (int b = 0; b < NB; b++) {
+            const int64_t e = eb + 256 * b, ec = e < kr ? e : kr - 4;
+            raw[b] = XU<F>::load(W, j * row_elems + ec);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                xv[b][r] = *(const float4*)(xr[r] + ec);
+                if (e >= kr) xv[b][r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            float w[4];
+            XU<F>::expand(raw[b], w);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                acc[r] = fmaf(xv[b][r].x, w[0], acc[r]);
+                acc[r] = fmaf(xv[b][r].y, w[1], acc[r]);
+                acc[r] = fmaf(xv[b][r].z, w[2], acc[r]);
+                acc[r] = fmaf(xv[b][r].w, w[3], acc[r]);
+            }
         }
     }
 #pragma unroll
@@ -216,16 +272,24 @@ template <int F>
 int launch_col(const aeth_weight* w, const float* x, int64_t m, float* y, int64_t ldy, const GemvEpi& e,
                float* part, int S, hipStream_t s) {
     const int64_t units = aeth_cdiv(w->n, 256);
-    const int R = m == 1 ? 1 : 8;
-    const dim3 grid((unsigned)units, (unsigned)S, (unsigned)aeth_cdiv(m, R));
-    if (R == 1)
-        hipLaunchKernelGGL((k_col<F, 1>), grid, dim3(256), 0, s, w->p0, w->n, w->k, x, w->k, (int)m, S, part);
-    else
-        hipLaunchKernelGGL((k_col<F, 8>), grid, dim3(256), 0, s, w->p0, w->n, w->k, x, w->k, (int)m, S, part);
+    if (m == 1) {
+        const dim3 grid((unsigned)units, (unsigned)S, 1);
+        hipLaunchKernelGGL((k_col<F, 1, 8>), grid, dim3(512), 0, s, w->p0, w->n, w->k, x, w->k, 1, S, part);
+    } else {
+        const dim3 grid((unsigned)units, (unsigned)S, (unsigned)aeth_cdiv(m, 8));
+        hipLaunchKernelGGL((k_col<F, 8, 4>), grid, dim3(256), 0, s, w->p0, w->n, w->k, x, w->k, (int)m, S, part);
+    }
     AETH_LAUNCH_CHECK();
     const int64_t tot = m * w->n;
-    hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)aeth_cdiv(tot, 256)), dim3(256), 0, s, part, S, m, w->n, y, ldy,
-                       (e.flags & AETH_MM_ACCUMULATE) ? 1 : 0, e.amax);
+    const int acc = (e.flags & AETH_MM_ACCUMULATE) ? 1 : 0;
+#define AETH_COL_REDUCE(G)                                                                                       \
+    hipLaunchKernelGGL(k_col_reduce<G>, dim3((unsigned)aeth_cdiv(tot * G, 256)), dim3(256), 0, s, part, S, m,   \
+                       w->n, y, ldy, acc, e.amax)
+    if (S <= 1) AETH_COL_REDUCE(1);
+    else if (S <= 4) AETH_COL_REDUCE(4);
+    else if (S <= 16) AETH_COL_REDUCE(16);
+    else AETH_COL_REDUCE(64);
+#undef AETH_COL_REDUCE
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
@@ -248,12 +312,13 @@ int launch_row(const aeth_weight* w, const float* x, int64_t m, float* y, int64_
 }
 
 // Splits of k for a GGUF-order launch: enough workgroups to cover the chip
-// (≈ 8 per CU), at least 16 inputs per wave.
+// (≈ 4 per CU), at least one batch of inputs (8 per wave) per wave.
 int col_splits(const aeth_weight* w, int64_t m) {
-    const int64_t units = aeth_cdiv(w->n, 256), groups = aeth_cdiv(m, m == 1 ? 1 : 8);
-    int64_t S = aeth_cdiv(8LL * aeth_num_cus(), units * groups);
-    S = S < 1 ? 1 : S > 64 ? 64 : S;
-    const int64_t smax = w->k / 64 > 1 ? w->k / 64 : 1;
+    const int64_t units = aeth_cdiv(w->n, 256), groups = m == 1 ? 1 : aeth_cdiv(m, 8);
+    const int64_t per_wave_batch = m == 1 ? 64 : 32;  // NW·NB inputs
+    int64_t S = aeth_cdiv(4LL * aeth_num_cus(), units * groups);
+    const int64_t smax = w->k / per_wave_batch > 1 ? w->k / per_wave_batch : 1;
+    S = S < 1 ? 1 : S > 128 ? 128 : S;
     return (int)(S < smax ? S : smax);
 }
 

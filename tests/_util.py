@@ -72,17 +72,20 @@ def assert_close_logits(g, r, tol=1e-3, floor=1e-5, cos_min=0.9999, what="", exa
     with the row's largest terms; in a row spanning ±658 (the Q8_0 test model) the
     reference's own f32 order and any other exact-f32 order differ by a few 1e-3
     on its small entries. With `exact` (the float64 logits of the same model,
-    tests/_model64.py) an element also passes when it is no farther from the
-    exact value than the reference's own f32 result is (plus 1e-6·max|row|):
-    on the random test models the reference's f32 order itself drifts by up to
-    2e-5·max|row|. Kernel-level outputs keep the plain element-wise bar."""
+    tests/_model64.py) an element also passes when its distance from the exact
+    value is at most twice the largest distance the reference's own f32 result
+    shows on that row (plus 1e-6·max|row|): on the random test models, whose
+    activations reach the hundreds, one f32 evaluation order drifts from the
+    exact logits by up to 2e-5·max|row|, and another order drifts as much in
+    other places. Kernel-level outputs keep the plain element-wise bar."""
     g = np.atleast_2d(np.asarray(g, dtype=np.float64))
     r = np.atleast_2d(np.asarray(r, dtype=np.float64))
     assert g.shape == r.shape, (g.shape, r.shape)
     ok = close_mask(g, r, tol) | (np.abs(g - r) <= floor * np.abs(r).max(axis=1, keepdims=True))
     if exact is not None:
         x = np.atleast_2d(np.asarray(exact, dtype=np.float64))
-        ok |= np.abs(g - x) <= np.abs(r - x) + 1e-6 * np.abs(x).max(axis=1, keepdims=True)
+        band = 2.0 * np.abs(r - x).max(axis=1, keepdims=True) + 1e-6 * np.abs(x).max(axis=1, keepdims=True)
+        ok |= np.abs(g - x) <= band
     if not ok.all():
         i = np.argwhere(~ok)[0]
         raise AssertionError("%s: %d/%d logits out of tolerance; first at %s: got %r ref %r (row max %r)" %
