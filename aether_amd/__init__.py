@@ -9,7 +9,7 @@ import os
 
 __all__ = ["lib", "check", "AethError", "LIB_PATH", "DTYPE_F32", "DTYPE_F16", "DTYPE_Q8_0", "DTYPE_Q2_K",
            "DTYPE_Q3_K", "DTYPE_Q4_K", "DTYPE_Q5_K", "DTYPE_Q6_K",
-           "LlamaConfig", "header_symbols", "MM_ACCUMULATE", "block_geometry", "AETH_OK", "AETH_EINVAL",
+           "LlamaConfig", "header_symbols", "MM_ACCUMULATE", "MM_Q8_ACTIVATIONS", "block_geometry", "AETH_OK", "AETH_EINVAL",
            "AETH_EHIP", "AETH_ENOMEM", "AETH_EUNSUPPORTED", "AETH_ESTATE"]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -18,7 +18,7 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
 DTYPE_F32, DTYPE_F16, DTYPE_Q8_0, DTYPE_Q2_K, DTYPE_Q3_K = 0, 1, 8, 10, 11
 DTYPE_Q4_K, DTYPE_Q5_K, DTYPE_Q6_K = 12, 13, 14
-MM_ACCUMULATE = 1
+MM_ACCUMULATE, MM_Q8_ACTIVATIONS = 1, 2
 # return codes (include/aether_hip.h)
 AETH_OK, AETH_EINVAL, AETH_EHIP, AETH_ENOMEM, AETH_EUNSUPPORTED, AETH_ESTATE = 0, -1, -2, -3, -4, -5
 _GEOM = {DTYPE_F32: (1, 4), DTYPE_F16: (1, 2), DTYPE_Q8_0: (32, 34), DTYPE_Q2_K: (256, 84), DTYPE_Q3_K: (256, 110),
@@ -59,6 +59,7 @@ _SIGS = {
     "aeth_load_quant": (_INT, [_INT, _P, _I64, _I64, _P, _P, _P]),
     "aeth_qmatmul": (_INT, [_P, _P, _I64, _P, ctypes.c_uint, _P]),
     "aeth_quantized_matmul_impl": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P]),
+    "aeth_quantized_matmul_dotprod": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P]),
     "aeth_matmul_q8_0": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q4_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q5_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),

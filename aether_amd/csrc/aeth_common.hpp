@@ -36,6 +36,15 @@ int aeth_set_error(int code, const char* fmt, ...);
                                   hipGetErrorString(_e), __FILE__, __LINE__);         \
     } while (0)
 
+// binary32 → binary16 bits, round to nearest even (the hardware conversion),
+// NaN as sign | 0x7E00 | payload >> 13 (half::f16::from_f32).
+__device__ __forceinline__ uint32_t aeth_f32_to_f16_bits(float f) {
+    const uint32_t x = __float_as_uint(f);
+    if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu))
+        return ((x >> 16) & 0x8000u) | 0x7E00u | ((x & 0x7FFFFFu) >> 13);
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
 // Exact binary16 -> binary32.
 __device__ __forceinline__ float aeth_f16_to_f32(uint32_t bits16) {
     return __half2float(__ushort_as_half((unsigned short)bits16));

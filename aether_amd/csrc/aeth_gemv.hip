@@ -131,6 +131,7 @@ template <bool Q5> struct MFK {
         const int h = ec >> 7, s = (ec >> 5) & 3, p = ec & 31, kg = 2 * (s >> 1) + (p >> 4);
         return h * 512 + ((kg * 2 + (s & 1)) * 4) * 16 + (p & 8);
     }
+    template <bool Q8A>
     __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
                                 const char* zs) {
         const int g = lane >> 4;
@@ -162,10 +163,15 @@ template <bool Q5> struct MFK {
             const mq_v4i a = *(const mq_v4i*)(va ? A + hh * 512 + vo : zs);
             const mq_v4i D1 = mq_mfma(a, lo, zero), D2 = mq_mfma(a, hi, zero);
             const mq_v4i E = odd ? D2 : D1;
-            const float v = mq_recombine(E.x + E.y * 256, E.z + E.w * 256);
             const int2 mt = ((const int2*)meta)[4 * hh + g];
-            acc = fmaf(ldexpf(v, mt.x), d * sc[hh], acc);
-            acc = fmaf(-dmin * mn[hh], __int_as_float(mt.y), acc);
+            if (Q8A) {  // matmul_q4_k / q5_k_dotprod: d_a·(d1·Σq·q_a − m1·Σq_a) (neon.rs:436-437)
+                const float d1 = d * sc[hh], m1 = dmin * mn[hh];
+                acc += __int_as_float(mt.y) * (d1 * (float)E.x - m1 * (float)mt.x);
+            } else {
+                const float v = mq_recombine(E.x + E.y * 256, E.z + E.w * 256);
+                acc = fmaf(ldexpf(v, mt.x), d * sc[hh], acc);
+                acc = fmaf(-dmin * mn[hh], __int_as_float(mt.y), acc);
+            }
         }
         return acc;
     }
@@ -187,6 +193,7 @@ template <> struct MF<FQ80> {
         const int s = ec >> 5, p = ec & 31, kg = 2 * (s & 1) + (p >> 4);
         return (s >> 1) * 256 + (kg * 4) * 16 + (p & 8);
     }
+    template <bool Q8A>
     __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
                                 const char* zs) {
         const int g = lane >> 4;
@@ -197,8 +204,10 @@ template <> struct MF<FQ80> {
         const mq_v4i b0 = {dd.q[0].x, dd.q[0].y, dd.q[0].z, dd.q[0].w};
         const mq_v4i b1 = {dd.q[1].x, dd.q[1].y, dd.q[1].z, dd.q[1].w};
         const mq_v4i D = mq_mfma(a1, b1, mq_mfma(a0, b0, zero));
-        const float val = mq_recombine(D.x + D.y * 256, D.z + D.w * 256);
         const int2 mt = ((const int2*)meta)[g];
+        if (Q8A)  // matmul_q8_0_dotprod: (Σ q_a·q)·(d_a·d) (tests.rs:44-56)
+            return (float)D.x * (__int_as_float(mt.y) * aeth_f16_to_f32(dd.d));
+        const float val = mq_recombine(D.x + D.y * 256, D.z + D.w * 256);
         return ldexpf(val, mt.x) * aeth_f16_to_f32(dd.d);  // Q8_0 scales are plain f16 (q8_0.rs)
     }
 };
@@ -220,6 +229,7 @@ template <> struct MF<FQ6K> {
         const int h = ec >> 7, r = ec & 127, v = r >> 5, kg = 2 * h + ((r >> 4) & 1);
         return v * 256 + (kg * 4) * 16 + (r & 8);
     }
+    template <bool Q8A>
     __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
                                 const char* zs) {
         const int g = lane >> 4;
@@ -247,12 +257,17 @@ template <> struct MF<FQ6K> {
             const mq_v4i a = *(const mq_v4i*)(va ? A + v * 256 + vo : zs);
             const mq_v4i Dv = mq_mfma(a, q, zero);
             const int4 mt = ((const int4*)meta)[8 * (g >> 1) + 2 * v + (g & 1)];
+            const uint32_t sw = v < 2 ? s01 : s23;
+            const float scv = (float)(int8_t)((sw >> (16 * (v & 1))) & 0xFFu);
+            if (Q8A) {  // matmul_q6_k_dotprod: (d·s·d_a)·Σ q_a·(q − 32) (neon.rs / tests.rs:227-237)
+                part += (aeth_decode_d(dd.d) * scv * __int_as_float(mt.y)) * (float)(Dv.x - 32 * mt.x);
+                continue;
+            }
             // stored q + 32 ∈ [0, 63]: subtract 32·Σ x_int per digit pair (exact in i32)
             const float val = ldexpf(mq_recombine(Dv.x + Dv.y * 256 - mt.y, Dv.z + Dv.w * 256 - mt.z), mt.x);
-            const uint32_t sw = v < 2 ? s01 : s23;
-            part += (float)(int8_t)((sw >> (16 * (v & 1))) & 0xFFu) * val;
+            part += scv * val;
         }
-        return aeth_decode_d(dd.d) * part;
+        return Q8A ? part : aeth_decode_d(dd.d) * part;
     }
 };
 
@@ -280,8 +295,14 @@ __device__ __forceinline__ void mq_load_x(const float* __restrict__ x, int o0, i
 // regions is written) and per-group meta: Q4_K / Q5_K {−S, Σx}, Q8_0 {−S, 0},
 // Q6_K {−S, 32·(Σd0 + 2^8·Σd1), 32·(Σd2 + 2^8·Σd3), 0}. Written and later
 // read by this wave only.
+// Q8A (the int8 dot-product path): the slice becomes Q8_0 activation blocks
+// instead, byte for byte as quantize_q8_0_block (neon.rs:45-104) makes them:
+// per 32 elements d = max|x|/127 (a NaN anywhere gives NaN), stored as f16,
+// q = sat_i8(RNE(x·(1/d))) with the f32 d, zeros when d is not > 0; digit 0
+// holds q, the others zero; meta Q4_K / Q5_K {Σq, d_a}, Q8_0 {0, d_a}, Q6_K
+// per 16 elements {Σq, d_a} (d_a = the stored f16 scale as f32).
 // Returns nonzero (wave-uniform) if the slice holds a NaN or an infinity.
-template <int F, int XO>
+template <int F, int XO, bool Q8A>
 __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase, char* Mbase) {
     typedef MF<F> T;
     const int lane = threadIdx.x & 63;
@@ -303,9 +324,38 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
             nan |= v[t] != v[t];
         }
         mx = fmaxf(mx, __shfl_xor(mx, 1, 64));  // the octets of a group are adjacent lanes
-        if (T::GE == 32) mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        if (T::GE == 32 || Q8A) mx = fmaxf(mx, __shfl_xor(mx, 2, 64));  // Q8_0 activation blocks are 32 wide
         const bool fin = isfinite(mx);
         if ((!fin || nan) && live) bad = 1;
+        if (Q8A) {
+            int nb4 = nan ? 1 : 0;
+            nb4 |= __shfl_xor(nb4, 1, 64);
+            nb4 |= __shfl_xor(nb4, 2, 64);
+            const float dq = nb4 ? __int_as_float(0x7FC00000) : mx / 127.0f;
+            const float da = aeth_f16_to_f32(aeth_f32_to_f16_bits(dq));
+            const float inv = 1.0f / dq;
+            int q[8], sq = 0;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float pr = v[t] * inv;
+                q[t] = dq > 0.0f && pr == pr ? max(-128, min(127, (int)rintf(fminf(fmaxf(pr, -256.0f), 256.0f)))) : 0;
+                sq += q[t];
+            }
+            sq += __shfl_xor(sq, 1, 64);
+            if (T::GE == 32) sq += __shfl_xor(sq, 2, 64);
+            if (live) {
+                const int c = o / (T::CE / 8), ec = 8 * o - c * T::CE;
+                char* dst = Abase + (size_t)c * T::AB + T::aoff(ec);
+                *(uint2*)(dst) = make_uint2(mq_pack4(q[0], q[1], q[2], q[3]), mq_pack4(q[4], q[5], q[6], q[7]));
+                *(uint2*)(dst + 16) = make_uint2(0u, 0u);
+                *(uint2*)(dst + 32) = make_uint2(0u, 0u);
+                *(uint2*)(dst + 48) = make_uint2(0u, 0u);
+                char* mb = Mbase + (size_t)c * T::MB;
+                if (F != FQ6K && (ec & 31) == 0) ((int2*)mb)[ec >> 5] = make_int2(F == FQ80 ? 0 : sq, __float_as_int(da));
+                if (F == FQ6K && (ec & 15) == 0) ((int4*)mb)[ec >> 4] = make_int4(sq, __float_as_int(da), 0, 0);
+            }
+            continue;
+        }
         const bool use = mx > 0.0f && fin;
         int E = 0;
         if (use) (void)frexpf(mx, &E);
@@ -369,7 +419,7 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
 //  accumulate: y += result (residual adds, runner.rs:1609-1611, 1629-1631).
 // RING = false: the workgroup's tiles all fit the RD load slots (issued up
 // front); RING = true: the slots are refilled as they are consumed.
-template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG>
+template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG, bool Q8A>
 __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
     typedef MF<F> T;
     typedef typename T::D Dt;
@@ -428,14 +478,15 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
 
     // a NaN or infinity in the slice makes every partial of this wave NaN
     if (lane == 0) *(uint4*)zs = make_uint4(0u, 0u, 0u, 0u);
-    const float poison = mq_build<F, XO>(xv, c0, nbw, G.kx, Abase, Mbase) ? __int_as_float(0x7FC00000) : 0.0f;
+    const float poison = mq_build<F, XO, Q8A>(xv, c0, nbw, G.kx, Abase, Mbase) ? __int_as_float(0x7FC00000) : 0.0f;
 
     auto tile = [&](const Dt (&b)[NBW]) {
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < NBW; i++)
             if (i < nbw)
-                acc += T::dot(b[i], Abase + (size_t)(c0 + i) * T::AB, Mbase + (size_t)(c0 + i) * T::MB, lane, L, zs);
+                acc += T::template dot<Q8A>(b[i], Abase + (size_t)(c0 + i) * T::AB, Mbase + (size_t)(c0 + i) * T::MB,
+                                            lane, L, zs);
         acc += __shfl_xor(acc, 16, 64);
         acc += __shfl_xor(acc, 32, 64);
         return acc + poison;
@@ -510,27 +561,27 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
 
 // ── dispatch ─────────────────────────────────────────────────────────────
 
-template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG>
+template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG, bool Q8A>
 static int mq_launch_k(dim3 grid, size_t lds, hipStream_t s, const MqParams& G) {
     static size_t opted = 64 * 1024;  // dynamic LDS above 64 KiB is opted into per kernel
     if (lds > opted) {
-        AETH_HIP_CHECK(hipFuncSetAttribute((const void*)k_gemv_mf<F, NBW, RD, XO, RING, W, RAG>,
+        AETH_HIP_CHECK(hipFuncSetAttribute((const void*)k_gemv_mf<F, NBW, RD, XO, RING, W, RAG, Q8A>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         opted = lds;
     }
-    hipLaunchKernelGGL((k_gemv_mf<F, NBW, RD, XO, RING, W, RAG>), grid, dim3(64 * W), lds, s, G);
+    hipLaunchKernelGGL((k_gemv_mf<F, NBW, RD, XO, RING, W, RAG, Q8A>), grid, dim3(64 * W), lds, s, G);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
 
-template <int F, int NBW, int RD, int W, bool RAG>
+template <int F, int NBW, int RD, int W, bool RAG, bool Q8A>
 static int mq_launch(dim3 grid, size_t lds, hipStream_t s, const MqParams& G) {
     constexpr int XO = (NBW * MF<F>::CE / 8 + 63) / 64;
-    return G.tpw <= RD ? mq_launch_k<F, NBW, RD, XO, false, W, RAG>(grid, lds, s, G)
-                       : mq_launch_k<F, NBW, RD, XO, true, W, RAG>(grid, lds, s, G);
+    return G.tpw <= RD ? mq_launch_k<F, NBW, RD, XO, false, W, RAG, Q8A>(grid, lds, s, G)
+                       : mq_launch_k<F, NBW, RD, XO, true, W, RAG, Q8A>(grid, lds, s, G);
 }
 
-template <int F, bool RAG>
+template <int F, bool RAG, bool Q8A>
 static int mq_dispatch(MqParams G, int64_t m, hipStream_t s) {
     typedef MF<F> T;
     const int nc = G.nc;
@@ -559,18 +610,18 @@ static int mq_dispatch(MqParams G, int64_t m, hipStream_t s) {
         return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d needs %zu B of LDS (max %d)", G.k, lds, MQ_LDS_MAX);
     const dim3 grid((unsigned)aeth_cdiv(G.ntiles, tpw), (unsigned)m);
     if (W == 16) {
-        if (NBW == 1) return mq_launch<F, 1, 2, 16, RAG>(grid, lds, s, G);
-        if (NBW == 2) return mq_launch<F, 2, 2, 16, RAG>(grid, lds, s, G);
-        if (NBW == 4) return mq_launch<F, 4, 1, 16, RAG>(grid, lds, s, G);
-        return mq_launch<F, 8, 1, 16, RAG>(grid, lds, s, G);
+        if (NBW == 1) return mq_launch<F, 1, 2, 16, RAG, Q8A>(grid, lds, s, G);
+        if (NBW == 2) return mq_launch<F, 2, 2, 16, RAG, Q8A>(grid, lds, s, G);
+        if (NBW == 4) return mq_launch<F, 4, 1, 16, RAG, Q8A>(grid, lds, s, G);
+        return mq_launch<F, 8, 1, 16, RAG, Q8A>(grid, lds, s, G);
     }
-    if (NBW == 1) return mq_launch<F, 1, 2, 8, RAG>(grid, lds, s, G);
-    if (NBW == 2) return mq_launch<F, 2, 2, 8, RAG>(grid, lds, s, G);
+    if (NBW == 1) return mq_launch<F, 1, 2, 8, RAG, Q8A>(grid, lds, s, G);
+    if (NBW == 2) return mq_launch<F, 2, 2, 8, RAG, Q8A>(grid, lds, s, G);
     if (NBW == 4) {
-        if (RD == 2) return mq_launch<F, 4, 2, 8, RAG>(grid, lds, s, G);
-        return mq_launch<F, 4, 1, 8, RAG>(grid, lds, s, G);
+        if (RD == 2) return mq_launch<F, 4, 2, 8, RAG, Q8A>(grid, lds, s, G);
+        return mq_launch<F, 4, 1, 8, RAG, Q8A>(grid, lds, s, G);
     }
-    return mq_launch<F, 8, 1, 8, RAG>(grid, lds, s, G);
+    return mq_launch<F, 8, 1, 8, RAG, Q8A>(grid, lds, s, G);
 }
 
 int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float* d_y, const GemvEpi& e,
@@ -604,10 +655,16 @@ int aeth_gemv_launch_ex(const aeth_weight* w, const float* d_x, int64_t m, float
     const bool rag = (G.kx & 7) != 0;
     if (!rag && (((uintptr_t)d_x & 15) || (e.norm_w && ((uintptr_t)e.norm_w & 15)) || (m > 1 && (G.k & 3))))
         return aeth_set_error(AETH_EINVAL, "gemv: x rows and the norm weight must be 16-byte aligned");
-    if (w->dtype == AETH_DTYPE_Q4_K) return mq_dispatch<FQ4K, false>(G, m, s);
-    if (w->dtype == AETH_DTYPE_Q5_K) return mq_dispatch<FQ5K, false>(G, m, s);
-    if (w->dtype == AETH_DTYPE_Q6_K) return mq_dispatch<FQ6K, false>(G, m, s);
-    if (q8) return rag ? mq_dispatch<FQ80, true>(G, m, s) : mq_dispatch<FQ80, false>(G, m, s);
+    if (e.flags & AETH_MM_Q8_ACTIVATIONS) {  // the int8 dot-product path (a14 activations)
+        if (w->dtype == AETH_DTYPE_Q4_K) return mq_dispatch<FQ4K, false, true>(G, m, s);
+        if (w->dtype == AETH_DTYPE_Q5_K) return mq_dispatch<FQ5K, false, true>(G, m, s);
+        if (w->dtype == AETH_DTYPE_Q6_K) return mq_dispatch<FQ6K, false, true>(G, m, s);
+        if (q8) return rag ? mq_dispatch<FQ80, true, true>(G, m, s) : mq_dispatch<FQ80, false, true>(G, m, s);
+    }
+    if (w->dtype == AETH_DTYPE_Q4_K) return mq_dispatch<FQ4K, false, false>(G, m, s);
+    if (w->dtype == AETH_DTYPE_Q5_K) return mq_dispatch<FQ5K, false, false>(G, m, s);
+    if (w->dtype == AETH_DTYPE_Q6_K) return mq_dispatch<FQ6K, false, false>(G, m, s);
+    if (q8) return rag ? mq_dispatch<FQ80, true, false>(G, m, s) : mq_dispatch<FQ80, false, false>(G, m, s);
     return aeth_set_error(AETH_EUNSUPPORTED, "gemv: dtype %d", w->dtype);
 }
 

@@ -46,7 +46,8 @@ int workspace(int use, size_t bytes, void** out) {
 
 int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
                     hipStream_t s) {
-    if (m > 1 && w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
+    if (m > 1 && w->dtype == AETH_DTYPE_Q4_K && !(flags & AETH_MM_Q8_ACTIVATIONS))
+        return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
     GemvEpi e;
     e.flags = flags;
     e.ldc = ldc;
@@ -156,7 +157,7 @@ int cached_weight(const uint8_t* b_raw, int64_t b_len, int dtype, int order, int
 // c is fully written). order: how b_raw is laid out — the QuantWeight form
 // (planar for the fused formats, GGUF [k][n] for the others) or [n][k] rows.
 int host_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, int64_t n, int64_t k, int dtype,
-                float* c, int order = -1) {
+                float* c, int order = -1, unsigned flags = 0) {
     if (order < 0) order = aeth_dtype_fused(dtype) ? AETH_ORDER_PLANAR : AETH_ORDER_GGUF;
     if (!a || !b_raw || !c || m <= 0 || n <= 0 || k <= 0)
         return aeth_set_error(AETH_EINVAL, "matmul: bad argument (m=%lld n=%lld k=%lld)", (long long)m, (long long)n,
@@ -176,7 +177,7 @@ int host_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, 
     }
     e = hipMemcpy(da, a, sizeof(float) * m * k, hipMemcpyHostToDevice);
     if (e == hipSuccess) {
-        rc = aeth_qmatmul(w, da, m, dc, 0, nullptr);
+        rc = aeth_qmatmul(w, da, m, dc, flags, nullptr);
         if (rc == AETH_OK) {
             e = hipMemcpy(c, dc, sizeof(float) * m * n, hipMemcpyDeviceToHost);
         }
@@ -300,6 +301,16 @@ extern "C" AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, co
     if (aeth_block_geometry(dtype, &be, &bb) != AETH_OK)
         return aeth_set_error(AETH_EUNSUPPORTED, "quantized_matmul_impl: dtype %d not on the HIP path", dtype);
     return host_matmul(a, m, b_raw, b_len, n, k, dtype, c);
+}
+
+// quantized_matmul_impl on an aarch64 host with dotprod: Q8_0 / Q4_K / Q5_K /
+// Q6_K through the int8 dot-product kernels, the other formats as on x86.
+extern "C" AETH_API int aeth_quantized_matmul_dotprod(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
+                                                      int64_t n, int64_t k, int dtype, float* c) {
+    int be, bb;
+    if (aeth_block_geometry(dtype, &be, &bb) != AETH_OK)
+        return aeth_set_error(AETH_EUNSUPPORTED, "quantized_matmul_dotprod: dtype %d not on the HIP path", dtype);
+    return host_matmul(a, m, b_raw, b_len, n, k, dtype, c, -1, AETH_MM_Q8_ACTIVATIONS);
 }
 
 extern "C" AETH_API int aeth_matmul_q8_0(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,

@@ -21,14 +21,7 @@
 
 #pragma clang fp contract(off)
 
-// f32 → binary16 bits, round to nearest even (the hardware conversion), NaN as
-// sign | 0x7E00 | payload >> 13.
-__device__ __forceinline__ uint32_t f16_bits(float f) {
-    const uint32_t x = __float_as_uint(f);
-    if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu))
-        return ((x >> 16) & 0x8000u) | 0x7E00u | ((x & 0x7FFFFFu) >> 13);
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
-}
+__device__ __forceinline__ uint32_t f16_bits(float f) { return aeth_f32_to_f16_bits(f); }
 
 // requantize_q8_0, dispatch.rs:149-184: d = max|x|/127 (1 if the block is 0),
 // q = clamp(round(x/d), −128, 127); a row's last block may be partial (its

@@ -42,6 +42,14 @@ extern "C" {
 /* aeth_qmatmul flags */
 #define AETH_MM_ACCUMULATE 1u /* c += A·Wᵀ instead of c = A·Wᵀ (fused residual add,
                                  runner.rs:1609-1611, 1629-1631) */
+#define AETH_MM_Q8_ACTIVATIONS 2u /* the int8 dot-product path of an aarch64 host with
+                                     dotprod (avx2_dispatch.rs:9-44, dispatch.rs:21-22):
+                                     activations quantized to Q8_0 blocks as
+                                     quantize_activations_q8_0 (neon.rs:106-155) does,
+                                     exact integer dots against the weight quants
+                                     (matmul_q8_0 / q4_k / q5_k / q6_k_dotprod). Q8_0,
+                                     Q4_K, Q5_K, Q6_K weights; ignored for the others,
+                                     which have no such path. */
 
 /* ── runtime ─────────────────────────────────────────────────────────────── */
 
@@ -130,6 +138,12 @@ AETH_API int aeth_qmatmul(const aeth_weight* w, const float* d_a, int64_t m, flo
  * copied per call. Fails (no CPU fallback) if no device is usable. */
 AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
                                         int64_t n, int64_t k, int dtype, float* c);
+/* quantized_matmul_impl as an aarch64 host with dotprod runs it
+ * (avx2_dispatch.rs:9-44, dispatch.rs:21-22): Q8_0 / Q4_K / Q5_K / Q6_K
+ * through the int8 dot-product kernels (AETH_MM_Q8_ACTIVATIONS), the other
+ * formats as aeth_quantized_matmul_impl. Same arguments and caching. */
+AETH_API int aeth_quantized_matmul_dotprod(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
+                                           int64_t n, int64_t k, int dtype, float* c);
 /* matmul_q8_0 / matmul_q4_k / matmul_q6_k(a, b, m, n, k, c)
  * (src/quant/matmul/avx2_dispatch.rs:58-68): argument order as the reference. */
 AETH_API int aeth_matmul_q8_0(const float* a, const uint8_t* b, int64_t b_len, int64_t m, int64_t n,

@@ -431,9 +431,12 @@ ORC_API void orc_requantize_q5_k(const float* data, size_t rows, size_t cols, ui
 
 /* matmul_q5_k_dotprod_reference, tests.rs:254-330: per 32-element
  * sub-block exact i32 dot and Σq_a, acc += d_a·(d1·dot − m1·Σq_a). The
- * activation block of sub-block is of super-block blk is 8·blk + is; the
- * reference's test helper omits the 8·blk term (it only runs k = 256), and
- * its NEON kernel (neon.rs) indexes 8·blk + is as written here. */
+ * activation block of sub-block is of super-block blk is 8·blk + is, as the
+ * Q4_K and Q6_K dot-product kernels index it (neon.rs:392-393, tests.rs:99-103).
+ * The reference's Q5_K test helper and its NEON kernel (neon.rs:1441-1446)
+ * both drop the 8·blk term, so for k > 256 they read the first super-block's
+ * activations for every super-block; at k = 256, the only size the reference
+ * tests, the two forms agree. This restatement keeps the format's semantics. */
 ORC_API void orc_dotprod_ref_q5_k(const uint8_t* aq, const uint8_t* b, size_t m, size_t n, size_t k, float* c) {
     size_t nb = k / 256;
     for (size_t row = 0; row < m; row++)

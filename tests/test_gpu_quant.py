@@ -449,3 +449,79 @@ def test_quantized_matmul_impl_gguf_order_formats(gpu):
         assert L.aeth_dispatch_matmul(a.ctypes.data, m, raw.ctypes.data, raw.size, n, k, dtype, c2.ctypes.data) == 1
         assert np.array_equal(c, c2)
     A.check(L.aeth_weight_cache_clear())
+
+
+# ── the int8 dot-product path (aarch64 dotprod hosts) ────────────────────
+# AETH_MM_Q8_ACTIVATIONS: activations become Q8_0 blocks exactly as
+# quantize_activations_q8_0 makes them (neon.rs:45-155), then exact integer
+# dots against the weight quants (matmul_*_dotprod; their references in
+# tests.rs:28-330). Only the f32 summation order differs from the references.
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m,n,k", [(1, 64, 256), (1, 1000, 4096), (3, 129, 1024), (1, 333, 14336), (2, 48, 2048)])
+def test_dotprod_mode_parity(gpu, dtype, m, n, k):
+    rng = np.random.default_rng(m + n + k + dtype)
+    raw = weight(dtype, n, k, 3 * n + k)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    x[: min(64, k)] *= 50.0  # blocks with a large maximum next to ordinary ones
+    w = make_weight(gpu, dtype, n, k, raw)
+    got = gemv(gpu, w, x, n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    aq = O.quantize_activations_q8_0(x, m, k)
+    ref = O.dotprod_ref(dtype, aq, raw, m, n, k)
+    assert_close(got, ref, what="dotprod dtype %d m=%d n=%d k=%d" % (dtype, m, n, k))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 40, 100), (2, 33, 1000), (3, 16, 4128)])
+def test_dotprod_mode_q8_0_ragged_k(gpu, m, n, k):
+    """Q8_0 rows of ceil(k/32) blocks: the last activation block is zero-padded
+    (quantize_activations_q8_0, neon.rs:115-126)."""
+    rng = np.random.default_rng(k)
+    raw = weight(Q8_0, n, k, n + k)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = make_weight(gpu, Q8_0, n, k, raw)
+    got = gemv(gpu, w, x, n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.dotprod_ref(Q8_0, O.quantize_activations_q8_0(x, m, k), raw, m, n, k)
+    assert_close(got, ref, what="dotprod q8_0 ragged k=%d" % k)
+
+
+def test_dotprod_mode_reference_generators_and_nan(gpu):
+    """The reference's own dotprod inputs (tests.rs:386-570: k = 256, n = 8,
+    m in {1, 3}) for Q4_K / Q5_K / Q6_K, and a NaN activation giving NaN rows
+    (its block scale is NaN, as vmaxq_f32 propagates it)."""
+    for dtype in (Q4_K, Q5_K, Q6_K):
+        for m in (1, 3):
+            k, n = 256, 8
+            b = ((np.arange(n * GEOM[dtype][1]) * 31) % 256).astype(np.uint8)
+            a = (((np.arange(m * k) * 17) % 100) / 50.0 - 1.0).astype(np.float32)
+            w = make_weight(gpu, dtype, n, k, b)
+            got = gemv(gpu, w, a, n, m, flags=A.MM_Q8_ACTIVATIONS)
+            A.lib().aeth_weight_free(w)
+            ref = O.dotprod_ref(dtype, O.quantize_activations_q8_0(a, m, k), b, m, n, k)
+            assert_close(got, ref, what="dotprod ref gen %d m=%d" % (dtype, m))
+    raw = weight(Q4_K, 32, 512, 4)
+    x = np.random.default_rng(2).standard_normal(512).astype(np.float32)
+    x[100] = np.nan
+    w = make_weight(gpu, Q4_K, 32, 512, raw)
+    got = gemv(gpu, w, x, 32, 1, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    assert np.isnan(got).all()
+
+
+def test_quantized_matmul_dotprod_host_slices(gpu):
+    L = A.lib()
+    A.check(L.aeth_weight_cache_clear())
+    n, k, m = 40, 512, 2
+    rng = np.random.default_rng(6)
+    for dtype in DTYPES + [F16, Q2_K]:
+        raw = synth_blocks(dtype, n * k // GEOM[dtype][0], 50 + dtype)
+        a = rng.standard_normal(m * k).astype(np.float32)
+        c = np.full(m * n, np.nan, dtype=np.float32)
+        A.check(L.aeth_quantized_matmul_dotprod(a.ctypes.data, m, raw.ctypes.data, raw.size, n, k, dtype,
+                                                c.ctypes.data), "quantized_matmul_dotprod")
+        if dtype in DTYPES:
+            ref = O.dotprod_ref(dtype, O.quantize_activations_q8_0(a, m, k), raw, m, n, k)
+        else:  # no dot-product kernel: the GGUF-order route as on x86
+            ref = O.gguf_order_matmul(dtype, a, raw, m, n, k)
+        assert_close(c.reshape(m, n), ref, what="dotprod host dtype %d" % dtype)
+    A.check(L.aeth_weight_cache_clear())
