@@ -7,8 +7,9 @@
  * aether_vocab_size() floats. Differences of this build:
  *   - aether_load / aether_load_streaming read a GGUF v3 file (gguf.rs:297-397,
  *     model_loader.rs:159-386) into the device runner: layer and LM-head
- *     weights Q8_0 / Q4_K / Q6_K (any mix across tensors, as in
- *     Q4_K_M files), norms F32 / F16, head_dim 128, at most 8 query heads per KV
+ *     weights F32 / F16 / Q8_0 / Q2_K..Q6_K (any mix across tensors, as in
+ *     Q4_K_M / Q5_K_M / Q3_K_M files; F32 / F16 / Q2_K / Q3_K need
+ *     out_features % 4 == 0), norms F32 / F16, head_dim 128, at most 8 query heads per KV
  *     head, no sliding window or partial RoPE, and a cache of
  *     min(context_length, 8192) positions. max_hot is ignored: every layer
  *     stays in HBM. Other files return NULL with the reason in

@@ -231,8 +231,9 @@ typedef struct aeth_runner aeth_runner;
 
 /* Creates a runner with device weights and a zeroed StaticKVCache of
  * max_seq_len positions. Host buffers: per layer l, layer_weights[l*7+j]
- * for j = q,k,v,o,gate,up,down (raw GGUF blocks, [out][in] as QuantWeight),
- * layer_dtypes likewise; norms[l*2+{0,1}] = attn_norm, ffn_norm (f32);
+ * for j = q,k,v,o,gate,up,down (each as its QuantWeight holds it: [out][in]
+ * row blocks for Q8_0 / Q4_K / Q5_K / Q6_K, the GGUF [in][out] tensor for
+ * F32 / F16 / Q2_K / Q3_K — see aeth_weight_create), layer_dtypes likewise; norms[l*2+{0,1}] = attn_norm, ffn_norm (f32);
  * final_norm (f32, d_model); lm_head (raw, dtype lm_dtype); embeddings
  * f32 [vocab][d_model]. Any pointer may be NULL when `synthetic_seed` is
  * nonzero: the runner then generates that tensor on the device (weights as
