@@ -9,7 +9,9 @@ value = algorithmic bytes per launch / mean launch time over K timed launches
 
 The same JSON line carries the other configs as `extra`: Q8_0 and Q6_K GEMV
 (configs 0, 2), the Q4_K prefill GEMM at M=512 (config 3) and the LLaMA-8B
-shape greedy decode (config 4), plus `roofline` for the headline kernel and
+shape greedy decode (config 4), the Q5_K GEMV and the headline shape on the
+int8 dot-product path (and, on request, GGUF-order F16 / Q2_K GEMVs), plus
+`roofline` for the headline kernel and
 `cpu_baseline`: the oracle's restatement of the reference's AVX2 path on one
 host core over a bounded sample of the same workload.
 """
@@ -30,7 +32,8 @@ FP16_PEAK_TFLOPS = 2500.0
 
 
 def algorithmic_bytes(dtype, n, k):
-    be, bb = {8: (32, 34), 12: (256, 144), 14: (256, 210)}[dtype]
+    be, bb = {1: (1, 2), 8: (32, 34), 10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176),
+              14: (256, 210)}[dtype]
     return n * (k // be) * bb + k * 4 + n * 4
 
 
@@ -69,7 +72,7 @@ def time_launches(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps  # ms per launch
 
 
-def bench_gemv(torch, A, dtype, n, k, steps, warmup, copies=16, seed=0xAE7E40):
+def bench_gemv(torch, A, dtype, n, k, steps, warmup, copies=16, seed=0xAE7E40, flags=0):
     L = A.lib()
     ws, raws = make_weights(torch, A, dtype, n, k, copies, seed)
     x = torch.empty(k, dtype=torch.float32, device="cuda")
@@ -78,7 +81,7 @@ def bench_gemv(torch, A, dtype, n, k, steps, warmup, copies=16, seed=0xAE7E40):
     s = torch.cuda.current_stream().cuda_stream
 
     def step(i):
-        rc = L.aeth_qmatmul(ws[i % copies], x.data_ptr(), 1, y.data_ptr(), 0, s)
+        rc = L.aeth_qmatmul(ws[i % copies], x.data_ptr(), 1, y.data_ptr(), flags, s)
         if rc:
             A.check(rc, "qmatmul")
 
@@ -183,8 +186,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--extra", default="q8,q6,gemm,decode",
-                    help="comma-separated extra sections to run: q8, q6, gemm, decode (default: all)")
+    ap.add_argument("--extra", default="q8,q6,q5,dotprod,gemm,decode",
+                    help="comma-separated extra sections to run: q8, q6, q5, dotprod, gemm, decode (default), "
+                         "f16, q2k (GGUF-order formats, not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (HBM counter calibration under rocprofv3)")
@@ -233,6 +237,23 @@ def main():
                                            "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         print("[bench] Q6_K GEMV: %s" % extra["q6_k_gemv_128256x4096"], file=sys.stderr, flush=True)
         del r
+    if "q5" in sections:
+        r = bench_gemv(torch, A, 13, 14336, 4096, args.steps, args.warmup, seed=0xAE7E44)
+        extra["q5_k_gemv_14336x4096"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),
+                                          "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        print("[bench] Q5_K GEMV: %s" % extra["q5_k_gemv_14336x4096"], file=sys.stderr, flush=True)
+    if "dotprod" in sections:  # the headline shape on the int8 dot-product path (a14 activations)
+        r = bench_gemv(torch, A, 12, n, k, args.steps, args.warmup, seed=0xAE7E45, flags=A.MM_Q8_ACTIVATIONS)
+        extra["q4_k_gemv_14336x4096_dotprod"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),
+                                                  "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        print("[bench] Q4_K GEMV dotprod: %s" % extra["q4_k_gemv_14336x4096_dotprod"], file=sys.stderr, flush=True)
+    for sec, dt, nn, kk in (("f16", 1, 4096, 4096), ("q2k", 10, 4096, 4096)):
+        if sec in sections:  # GGUF-order weights (quantized_matmul_impl's dequantize route)
+            r = bench_gemv(torch, A, dt, nn, kk, args.steps, args.warmup, copies=8, seed=0xAE7E46)
+            key = "%s_gguf_order_gemv_%dx%d" % ({1: "f16", 10: "q2_k"}[dt], nn, kk)
+            extra[key] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),
+                          "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+            print("[bench] %s: %s" % (key, extra[key]), file=sys.stderr, flush=True)
     if "gemm" in sections:
         for nn in (4096, 14336):
             g = bench_gemm(torch, A, nn, 4096, 512, 5, 2)
