@@ -93,6 +93,30 @@ __device__ __forceinline__ mq_v4i mq_mfma(const mq_v4i& a, const mq_v4i& b, cons
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
+// 16 weight bytes, read once per GEMV: a non-temporal (streaming) load, which
+// keeps the weight stream from displacing x and the other operands in L2.
+__device__ __forceinline__ int4 mq_ld16(const uint8_t* p) {
+    const mq_v4i v = __builtin_nontemporal_load((const mq_v4i*)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+
+// v from lane ^ 1 and lane ^ 2 (within a quad of lanes): DPP quad_perm moves.
+__device__ __forceinline__ int mq_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int mq_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ float mq_xor1f(float v) { return __int_as_float(mq_xor1(__float_as_int(v))); }
+__device__ __forceinline__ float mq_xor2f(float v) { return __int_as_float(mq_xor2(__float_as_int(v))); }
+
+// v[l] + v[l ^ 16], then the same across l ^ 32: the four 16-lane rows summed
+// into every lane. gfx950's permlane16/32 swaps exchange whole rows: after the
+// swap of (v, v) one result holds a lane's own value and the other its
+// partner's, so each sum is the pair in either order (addition commutes).
+__device__ __forceinline__ float mq_sum_rows(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // ── per-format traits ────────────────────────────────────────────────────
 // CE: activation elements per chunk; AB: LDS bytes of A operands per chunk;
 // MB: LDS meta bytes per chunk; GE: elements per exponent group.
@@ -120,9 +144,10 @@ template <bool Q5> struct MFK {
     // planes: p0 = headers [tile][sb][16 rows][16 B], p1 = quants [tile][sb][h][64][16 B],
     //         Q5: p2 = fifth bits [tile][sb][64][8 B]
     __device__ static void load(D& d, const MqParams& G, int64_t c, int lane) {  // c = tile·nc + chunk
-        d.q[0] = *(const int4*)(G.p1 + (c * 2) * 1024 + lane * 16);
-        d.q[1] = *(const int4*)(G.p1 + (c * 2 + 1) * 1024 + lane * 16);
-        d.h = *(const uint4*)(G.p0 + (c * 16 + (lane & 15)) * 16);
+        d.q[0] = mq_ld16(G.p1 + (c * 2) * 1024 + lane * 16);
+        d.q[1] = mq_ld16(G.p1 + (c * 2 + 1) * 1024 + lane * 16);
+        const int4 h = mq_ld16(G.p0 + (c * 16 + (lane & 15)) * 16);
+        d.h = make_uint4(h.x, h.y, h.z, h.w);
         if (Q5) d.qh = *(const uint2*)(G.p2 + (c * 64 + lane) * 8);
     }
     // compact A: per half h, vector ((kg·2 + (s & 1))·4 + d), kg ∈ the pair of slot s.
@@ -135,9 +160,13 @@ template <bool Q5> struct MFK {
     __device__ static float dot(const D& dd, const char* A, const char* meta, int lane, const MqLane& L,
                                 const char* zs) {
         const int g = lane >> 4;
+        // A rows of the even slots pair with the low nibbles, of the odd slots
+        // with the high ones: each MFMA reads only its own rows (the others from
+        // the zero slot), so the second accumulates onto the first and every
+        // output lane ends with its slot's four digit sums
         const bool va = (L.s >> 1) == (L.kg >> 1);
+        const bool vlo = va && !(L.s & 1), vhi = va && (L.s & 1);
         const int vo = ((L.kg * 2 + (L.s & 1)) * 4 + L.d) * 16;
-        const bool odd = g & 1;
         const mq_v4i zero = {0, 0, 0, 0};
         const float d = aeth_decode_d(dd.h.x), dmin = aeth_decode_d(dd.h.x >> 16);
         // get_scale_min_k4 (common.rs:29-38) for sub-blocks g and 4 + g
@@ -160,15 +189,18 @@ template <bool Q5> struct MFK {
                 hi.x |= mq_spread4(hu & 15u); hi.y |= mq_spread4((hu >> 4) & 15u);
                 hi.z |= mq_spread4((hu >> 8) & 15u); hi.w |= mq_spread4(hu >> 12);
             }
-            const mq_v4i a = *(const mq_v4i*)(va ? A + hh * 512 + vo : zs);
-            const mq_v4i D1 = mq_mfma(a, lo, zero), D2 = mq_mfma(a, hi, zero);
-            const mq_v4i E = odd ? D2 : D1;
+            const mq_v4i alo = *(const mq_v4i*)(vlo ? A + hh * 512 + vo : zs);
+            const mq_v4i ahi = *(const mq_v4i*)(vhi ? A + hh * 512 + vo : zs);
+            const mq_v4i E = mq_mfma(ahi, hi, mq_mfma(alo, lo, zero));
             const int2 mt = ((const int2*)meta)[4 * hh + g];
             if (Q8A) {  // matmul_q4_k / q5_k_dotprod: d_a·(d1·Σq·q_a − m1·Σq_a) (neon.rs:436-437)
                 const float d1 = d * sc[hh], m1 = dmin * mn[hh];
                 acc += __int_as_float(mt.y) * (d1 * (float)E.x - m1 * (float)mt.x);
             } else {
-                const float v = mq_recombine(E.x + E.y * 256, E.z + E.w * 256);
+                // Q4_K: both pairs fit 24 bits (|Σq·d| ≤ 32·15·128), so one f32
+                // fma rounds the exact sum once, as the f64 form does
+                const float v = Q5 ? mq_recombine(E.x + E.y * 256, E.z + E.w * 256)
+                                   : fmaf((float)(E.z + E.w * 256), 65536.0f, (float)(E.x + E.y * 256));
                 acc = fmaf(ldexpf(v, mt.x), d * sc[hh], acc);
                 acc = fmaf(-dmin * mn[hh], __int_as_float(mt.y), acc);
             }
@@ -184,6 +216,7 @@ template <> struct MF<FQ80> {
     struct D { int4 q[2]; uint32_t d; };
     // planes: p0 = quants [tile][group][j][64][16 B], p1 = d [tile][group][4 blocks][16 rows] (f16)
     __device__ static void load(D& d, const MqParams& G, int64_t c, int lane) {
+        // plain loads: measured faster than streaming ones for this format
         d.q[0] = *(const int4*)(G.p0 + (c * 2) * 1024 + lane * 16);
         d.q[1] = *(const int4*)(G.p0 + (c * 2 + 1) * 1024 + lane * 16);
         d.d = ((const uint16_t*)G.p1)[c * 64 + lane];
@@ -218,9 +251,9 @@ template <> struct MF<FQ6K> {
     // planes: p0 = [tile][sb][part A|B|H][64][16 B], p1 = sc [tile][sb][16 rows][16 B],
     //         p2 = d [tile][sb][16 rows] (f16)
     __device__ static void load(D& d, const MqParams& G, int64_t c, int lane) {
-        d.a = *(const int4*)(G.p0 + (c * 3) * 1024 + lane * 16);
-        d.b = *(const int4*)(G.p0 + (c * 3 + 1) * 1024 + lane * 16);
-        d.h = *(const int4*)(G.p0 + (c * 3 + 2) * 1024 + lane * 16);
+        d.a = mq_ld16(G.p0 + (c * 3) * 1024 + lane * 16);
+        d.b = mq_ld16(G.p0 + (c * 3 + 1) * 1024 + lane * 16);
+        d.h = mq_ld16(G.p0 + (c * 3 + 2) * 1024 + lane * 16);
         d.sc = *(const uint2*)(G.p1 + (c * 16 + (lane & 15)) * 16 + ((lane >> 5) & 1) * 8);
         d.d = ((const uint16_t*)G.p2)[c * 16 + (lane & 15)];
     }
@@ -313,9 +346,11 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
         const int o = o0 + lane + 64 * i;
         const bool live = o < o1;
         float* v = xv[i];
+        if (8 * o1 > kx) {  // the slice runs past k (Q8_0 padding blocks, ragged k): zeros there
 #pragma unroll
-        for (int t = 0; t < 8; t++)
-            if (8 * o + t >= kx) v[t] = 0.0f;  // past k (Q8_0 padding blocks) or past the slice
+            for (int t = 0; t < 8; t++)
+                if (8 * o + t >= kx) v[t] = 0.0f;
+        }
         float mx = 0.0f;
         bool nan = false;  // fmaxf drops NaN operands: test for them explicitly
 #pragma unroll
@@ -323,14 +358,14 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
             mx = fmaxf(mx, fabsf(v[t]));
             nan |= v[t] != v[t];
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));  // the octets of a group are adjacent lanes
-        if (T::GE == 32 || Q8A) mx = fmaxf(mx, __shfl_xor(mx, 2, 64));  // Q8_0 activation blocks are 32 wide
+        mx = fmaxf(mx, mq_xor1f(mx));  // the octets of a group are adjacent lanes
+        if (T::GE == 32 || Q8A) mx = fmaxf(mx, mq_xor2f(mx));  // Q8_0 activation blocks are 32 wide
         const bool fin = isfinite(mx);
         if ((!fin || nan) && live) bad = 1;
         if (Q8A) {
             int nb4 = nan ? 1 : 0;
-            nb4 |= __shfl_xor(nb4, 1, 64);
-            nb4 |= __shfl_xor(nb4, 2, 64);
+            nb4 |= mq_xor1(nb4);
+            nb4 |= mq_xor2(nb4);
             const float dq = nb4 ? __int_as_float(0x7FC00000) : mx / 127.0f;
             const float da = aeth_f16_to_f32(aeth_f32_to_f16_bits(dq));
             const float inv = 1.0f / dq;
@@ -341,8 +376,8 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
                 q[t] = dq > 0.0f && pr == pr ? max(-128, min(127, (int)rintf(fminf(fmaxf(pr, -256.0f), 256.0f)))) : 0;
                 sq += q[t];
             }
-            sq += __shfl_xor(sq, 1, 64);
-            if (T::GE == 32) sq += __shfl_xor(sq, 2, 64);
+            sq += mq_xor1(sq);
+            if (T::GE == 32) sq += mq_xor2(sq);
             if (live) {
                 const int c = o / (T::CE / 8), ec = 8 * o - c * T::CE;
                 char* dst = Abase + (size_t)c * T::AB + T::aoff(ec);
@@ -360,52 +395,57 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
         int E = 0;
         if (use) (void)frexpf(mx, &E);
         const int S = use ? 30 - E : 0;  // max|x| < 2^E, so |x_int| < 2^30
-        int d0[8], d1[8], d2[8], d3[8];
-        int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+        // Balanced digits by one biased add: y = x_int + 0x808080 has bytes
+        // (d0 + 128, d1 + 128, d2 + 128, d3) — each (d + 128) ∈ [0, 255] absorbs
+        // the borrow the balanced split would propagate, and d3 = y >> 24 ∈ [−64, 64].
+        // The bytes are then transposed (element-major → digit-major) and the
+        // bias flipped off with one xor per word (−128 ≡ ^0x80 on a byte).
+        uint32_t y[8];
+        uint32_t sx = 0, sh = 0;  // Q6_K: Σ x_int and Σ (y >> 16), both mod 2^32
         float fs = 0.0f;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const int xi = use ? (int)rintf(ldexpf(v[t], S)) : 0;
-            const int a = (xi << 24) >> 24;  // balanced digits: each in [−128, 127], d3 in [−64, 64]
-            const int r = (xi - a) >> 8;
-            const int b = (r << 24) >> 24;
-            const int r2 = (r - b) >> 8;
-            const int c2 = (r2 << 24) >> 24;
-            d0[t] = a;
-            d1[t] = b;
-            d2[t] = c2;
-            d3[t] = (r2 - c2) >> 8;
-            s0 += a;
-            s1 += b;
-            s2 += c2;
-            s3 += d3[t];
+            y[t] = (uint32_t)xi + 0x00808080u;
+            sx += (uint32_t)xi;
+            sh += (uint32_t)((int)y[t] >> 16);  // (d2 + 128) + 2^8·d3
             fs += v[t];
         }
-        if (F == FQ4K || F == FQ5K) {
-            fs += __shfl_xor(fs, 1, 64);
-            fs += __shfl_xor(fs, 2, 64);
+        uint32_t dg[4][2];  // digit d of elements 4j .. 4j + 3
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t *z = y + 4 * j;
+            const uint32_t l01 = __builtin_amdgcn_perm(z[1], z[0], 0x05010400u);  // z0.b0 z1.b0 z0.b1 z1.b1
+            const uint32_t h01 = __builtin_amdgcn_perm(z[1], z[0], 0x07030602u);  // z0.b2 z1.b2 z0.b3 z1.b3
+            const uint32_t l23 = __builtin_amdgcn_perm(z[3], z[2], 0x05010400u);
+            const uint32_t h23 = __builtin_amdgcn_perm(z[3], z[2], 0x07030602u);
+            dg[0][j] = __builtin_amdgcn_perm(l23, l01, 0x05040100u) ^ 0x80808080u;
+            dg[1][j] = __builtin_amdgcn_perm(l23, l01, 0x07060302u) ^ 0x80808080u;
+            dg[2][j] = __builtin_amdgcn_perm(h23, h01, 0x05040100u) ^ 0x80808080u;
+            dg[3][j] = __builtin_amdgcn_perm(h23, h01, 0x07060302u);
         }
-        if (F == FQ6K) {
-            s0 += __shfl_xor(s0, 1, 64);
-            s1 += __shfl_xor(s1, 1, 64);
-            s2 += __shfl_xor(s2, 1, 64);
-            s3 += __shfl_xor(s3, 1, 64);
+        if (F == FQ4K || F == FQ5K) {
+            fs += mq_xor1f(fs);
+            fs += mq_xor2f(fs);
+        }
+        int slo = 0, shi = 0;
+        if (F == FQ6K) {  // per 16 elements: Σ(d0 + 2^8·d1) and Σ(d2 + 2^8·d3), exact in i32
+            sx += (uint32_t)mq_xor1((int)sx);
+            sh += (uint32_t)mq_xor1((int)sh);
+            shi = (int)(sh - 128u * 16u);
+            slo = (int)(sx - ((uint32_t)shi << 16));
         }
         if (live) {
             const int c = o / (T::CE / 8), ec = 8 * o - c * T::CE;
             char* dst = Abase + (size_t)c * T::AB + T::aoff(ec);
-            *(uint2*)(dst) = make_uint2(mq_pack4(d0[0], d0[1], d0[2], d0[3]), mq_pack4(d0[4], d0[5], d0[6], d0[7]));
-            *(uint2*)(dst + 16) =
-                make_uint2(mq_pack4(d1[0], d1[1], d1[2], d1[3]), mq_pack4(d1[4], d1[5], d1[6], d1[7]));
-            *(uint2*)(dst + 32) =
-                make_uint2(mq_pack4(d2[0], d2[1], d2[2], d2[3]), mq_pack4(d2[4], d2[5], d2[6], d2[7]));
-            *(uint2*)(dst + 48) =
-                make_uint2(mq_pack4(d3[0], d3[1], d3[2], d3[3]), mq_pack4(d3[4], d3[5], d3[6], d3[7]));
+            *(uint2*)(dst) = make_uint2(dg[0][0], dg[0][1]);
+            *(uint2*)(dst + 16) = make_uint2(dg[1][0], dg[1][1]);
+            *(uint2*)(dst + 32) = make_uint2(dg[2][0], dg[2][1]);
+            *(uint2*)(dst + 48) = make_uint2(dg[3][0], dg[3][1]);
             char* mb = Mbase + (size_t)c * T::MB;
             if ((F == FQ4K || F == FQ5K) && (ec & 31) == 0) ((int2*)mb)[ec >> 5] = make_int2(-S, __float_as_int(fs));
             if (F == FQ80 && (ec & 31) == 0) ((int2*)mb)[ec >> 5] = make_int2(-S, 0);
-            if (F == FQ6K && (ec & 15) == 0)
-                ((int4*)mb)[ec >> 4] = make_int4(-S, 32 * (s0 + 256 * s1), 32 * (s2 + 256 * s3), 0);
+            if (F == FQ6K && (ec & 15) == 0) ((int4*)mb)[ec >> 4] = make_int4(-S, 32 * slo, 32 * shi, 0);
         }
     }
     return __any(bad);
@@ -487,9 +527,7 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
             if (i < nbw)
                 acc += T::template dot<Q8A>(b[i], Abase + (size_t)(c0 + i) * T::AB, Mbase + (size_t)(c0 + i) * T::MB,
                                             lane, L, zs);
-        acc += __shfl_xor(acc, 16, 64);
-        acc += __shfl_xor(acc, 32, 64);
-        return acc + poison;
+        return mq_sum_rows(acc) + poison;
     };
     if (!RING) {  // every tile already in flight: no refills
 #pragma unroll
