@@ -117,6 +117,17 @@ __device__ __forceinline__ float mq_sum_rows(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Sum over the wave, the same value in every lane: quad butterflies, then the
+// 8- and 16-lane mirrors (lane i pairs with 7 − i, then 15 − i: both partners
+// add the same two values), then the row swaps.
+__device__ __forceinline__ float mq_wave_sum(float v) {
+    v += mq_xor1f(v);
+    v += mq_xor2f(v);
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
+    return mq_sum_rows(v);
+}
+
 // ── per-format traits ────────────────────────────────────────────────────
 // CE: activation elements per chunk; AB: LDS bytes of A operands per chunk;
 // MB: LDS meta bytes per chunk; GE: elements per exponent group.
@@ -503,17 +514,24 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
 #pragma unroll
             for (int t = 0; t < 8; t++) ss += (o < o1 && 8 * o + t < G.kx) ? xv[i][t] * xv[i][t] : 0.0f;
         }
-        ss = aeth_wave_sum(ss);
+        ss = mq_wave_sum(ss);
         if (lane == 0) ssum[wave] = ss;
         __syncthreads();
         float tot = 0.0f;
 #pragma unroll
         for (int w = 0; w < W; w++) tot += ssum[w];
         const float rms = sqrtf(tot / (float)G.k + G.eps);
+        // x / rms by one correctly rounded reciprocal and a residual step per
+        // element (Markstein: q0 = x·r, q = q0 + (x − q0·rms)·r rounds x / rms
+        // correctly away from overflow and underflow), then · w
+        const float inv = 1.0f / rms;
 #pragma unroll
         for (int i = 0; i < XO; i++)
 #pragma unroll
-            for (int t = 0; t < 8; t++) xv[i][t] = xv[i][t] / rms * wv[i][t];
+            for (int t = 0; t < 8; t++) {
+                const float q0 = xv[i][t] * inv;
+                xv[i][t] = fmaf(fmaf(-q0, rms, xv[i][t]), inv, q0) * wv[i][t];
+            }
     }
 
     // a NaN or infinity in the slice makes every partial of this wave NaN
