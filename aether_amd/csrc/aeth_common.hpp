@@ -59,16 +59,60 @@ __device__ __forceinline__ float aeth_decode_d(uint32_t bits16) {
     return ((bits16 & 0x7C00u) == 0x7C00u) ? alt : f;  // select, not a branch
 }
 
+// Lane exchanges without the LDS crossbar: DPP quad_perm moves (lane ^ 1,
+// lane ^ 2) and row mirrors (lane i of 8 ↔ 7 − i, of 16 ↔ 15 − i), and
+// gfx950's permlane16/32 swaps, which exchange whole 16- and 32-lane rows.
+// Callers keep all 64 lanes of the wave active.
+__device__ __forceinline__ int aeth_dpp_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int aeth_dpp_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ float aeth_dpp_xor1f(float v) { return __int_as_float(aeth_dpp_xor1(__float_as_int(v))); }
+__device__ __forceinline__ float aeth_dpp_xor2f(float v) { return __int_as_float(aeth_dpp_xor2(__float_as_int(v))); }
+__device__ __forceinline__ float aeth_dpp_mirror8f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float aeth_dpp_mirror16f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
+}
+
+// v[l] + v[l ^ 16], then the same across l ^ 32: after a swap of (v, v) one
+// result holds the lane's own value and the other its partner's, so both
+// partners add the same two values and every lane ends with the same sum.
+__device__ __forceinline__ float aeth_sum_rows(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ float aeth_max_rows(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// v[l] + v[l ^ 32] (the two 32-lane halves), the same value in both partners.
+__device__ __forceinline__ float aeth_add_halves(float v) {
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Sum / max over the wave, the same value in every lane (each step adds a
+// lane's value to its partner's, and the partner adds the same pair).
 __device__ __forceinline__ float aeth_wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    v += aeth_dpp_xor1f(v);
+    v += aeth_dpp_xor2f(v);
+    v += aeth_dpp_mirror8f(v);
+    v += aeth_dpp_mirror16f(v);
+    return aeth_sum_rows(v);
 }
 
 __device__ __forceinline__ float aeth_wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    v = fmaxf(v, aeth_dpp_xor1f(v));
+    v = fmaxf(v, aeth_dpp_xor2f(v));
+    v = fmaxf(v, aeth_dpp_mirror8f(v));
+    v = fmaxf(v, aeth_dpp_mirror16f(v));
+    return aeth_max_rows(v);
 }
 
 static inline int64_t aeth_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -240,8 +240,8 @@ __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
                 const float4 qv = *(const float4*)(&qs[g][32 * qd + 4 * i]);
                 a += qv.x * kk[i].x + qv.y * kk[i].y + qv.z * kk[i].z + qv.w * kk[i].w;
             }
-            a += __shfl_xor(a, 1, 64);
-            a += __shfl_xor(a, 2, 64);
+            a += aeth_dpp_xor1f(a);
+            a += aeth_dpp_xor2f(a);
             if (qd == 0) sc[g][sp] = sp < nt ? a * scale : -INFINITY;
         }
     }
@@ -278,10 +278,10 @@ __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
                 o.z += pj * vv[j].z;
                 o.w += pj * vv[j].w;
             }
-            o.x += __shfl_xor(o.x, 32, 64);
-            o.y += __shfl_xor(o.y, 32, 64);
-            o.z += __shfl_xor(o.z, 32, 64);
-            o.w += __shfl_xor(o.w, 32, 64);
+            o.x = aeth_add_halves(o.x);
+            o.y = aeth_add_halves(o.y);
+            o.z = aeth_add_halves(o.z);
+            o.w = aeth_add_halves(o.w);
             if (lane < 32) *(float4*)(&ov[wave][g][4 * vd4]) = o;
         }
     }
@@ -302,12 +302,12 @@ __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
 // out = Σ_c e^{m_c-M} o_c / Σ_c e^{m_c-M} l_c. A separate launch: a kernel
 // boundary makes every chunk's partials visible across the XCDs' L2s, which a
 // device-scope fence inside one kernel would buy with L2 write-backs. Thread d
-// loads its column of up to 32 chunks at a time in one batch; the chunk
+// loads its column of up to 64 chunks at a time in one batch; the chunk
 // statistics are loaded first.
 template <int HD>
 __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
     static_assert(ATTN_MAX_CHUNKS <= HD, "one thread per chunk statistic");
-    constexpr int CB = 32;
+    constexpr int CB = 64;  // one load batch up to seq 4096
     __shared__ float cw[ATTN_MAX_CHUNKS];
     __shared__ float red[HD / 64][2];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

@@ -100,34 +100,6 @@ __device__ __forceinline__ int4 mq_ld16(const uint8_t* p) {
     return make_int4(v.x, v.y, v.z, v.w);
 }
 
-// v from lane ^ 1 and lane ^ 2 (within a quad of lanes): DPP quad_perm moves.
-__device__ __forceinline__ int mq_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
-__device__ __forceinline__ int mq_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
-__device__ __forceinline__ float mq_xor1f(float v) { return __int_as_float(mq_xor1(__float_as_int(v))); }
-__device__ __forceinline__ float mq_xor2f(float v) { return __int_as_float(mq_xor2(__float_as_int(v))); }
-
-// v[l] + v[l ^ 16], then the same across l ^ 32: the four 16-lane rows summed
-// into every lane. gfx950's permlane16/32 swaps exchange whole rows: after the
-// swap of (v, v) one result holds a lane's own value and the other its
-// partner's, so each sum is the pair in either order (addition commutes).
-__device__ __forceinline__ float mq_sum_rows(float v) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-// Sum over the wave, the same value in every lane: quad butterflies, then the
-// 8- and 16-lane mirrors (lane i pairs with 7 − i, then 15 − i: both partners
-// add the same two values), then the row swaps.
-__device__ __forceinline__ float mq_wave_sum(float v) {
-    v += mq_xor1f(v);
-    v += mq_xor2f(v);
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
-    return mq_sum_rows(v);
-}
-
 // ── per-format traits ────────────────────────────────────────────────────
 // CE: activation elements per chunk; AB: LDS bytes of A operands per chunk;
 // MB: LDS meta bytes per chunk; GE: elements per exponent group.
@@ -369,14 +341,14 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
             mx = fmaxf(mx, fabsf(v[t]));
             nan |= v[t] != v[t];
         }
-        mx = fmaxf(mx, mq_xor1f(mx));  // the octets of a group are adjacent lanes
-        if (T::GE == 32 || Q8A) mx = fmaxf(mx, mq_xor2f(mx));  // Q8_0 activation blocks are 32 wide
+        mx = fmaxf(mx, aeth_dpp_xor1f(mx));  // the octets of a group are adjacent lanes
+        if (T::GE == 32 || Q8A) mx = fmaxf(mx, aeth_dpp_xor2f(mx));  // Q8_0 activation blocks are 32 wide
         const bool fin = isfinite(mx);
         if ((!fin || nan) && live) bad = 1;
         if (Q8A) {
             int nb4 = nan ? 1 : 0;
-            nb4 |= mq_xor1(nb4);
-            nb4 |= mq_xor2(nb4);
+            nb4 |= aeth_dpp_xor1(nb4);
+            nb4 |= aeth_dpp_xor2(nb4);
             const float dq = nb4 ? __int_as_float(0x7FC00000) : mx / 127.0f;
             const float da = aeth_f16_to_f32(aeth_f32_to_f16_bits(dq));
             const float inv = 1.0f / dq;
@@ -387,8 +359,8 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
                 q[t] = dq > 0.0f && pr == pr ? max(-128, min(127, (int)rintf(fminf(fmaxf(pr, -256.0f), 256.0f)))) : 0;
                 sq += q[t];
             }
-            sq += mq_xor1(sq);
-            if (T::GE == 32) sq += mq_xor2(sq);
+            sq += aeth_dpp_xor1(sq);
+            if (T::GE == 32) sq += aeth_dpp_xor2(sq);
             if (live) {
                 const int c = o / (T::CE / 8), ec = 8 * o - c * T::CE;
                 char* dst = Abase + (size_t)c * T::AB + T::aoff(ec);
@@ -436,13 +408,13 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
             dg[3][j] = __builtin_amdgcn_perm(h23, h01, 0x07060302u);
         }
         if (F == FQ4K || F == FQ5K) {
-            fs += mq_xor1f(fs);
-            fs += mq_xor2f(fs);
+            fs += aeth_dpp_xor1f(fs);
+            fs += aeth_dpp_xor2f(fs);
         }
         int slo = 0, shi = 0;
         if (F == FQ6K) {  // per 16 elements: Σ(d0 + 2^8·d1) and Σ(d2 + 2^8·d3), exact in i32
-            sx += (uint32_t)mq_xor1((int)sx);
-            sh += (uint32_t)mq_xor1((int)sh);
+            sx += (uint32_t)aeth_dpp_xor1((int)sx);
+            sh += (uint32_t)aeth_dpp_xor1((int)sh);
             shi = (int)(sh - 128u * 16u);
             slo = (int)(sx - ((uint32_t)shi << 16));
         }
@@ -514,7 +486,7 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
 #pragma unroll
             for (int t = 0; t < 8; t++) ss += (o < o1 && 8 * o + t < G.kx) ? xv[i][t] * xv[i][t] : 0.0f;
         }
-        ss = mq_wave_sum(ss);
+        ss = aeth_wave_sum(ss);
         if (lane == 0) ssum[wave] = ss;
         __syncthreads();
         float tot = 0.0f;
@@ -545,7 +517,7 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
             if (i < nbw)
                 acc += T::template dot<Q8A>(b[i], Abase + (size_t)(c0 + i) * T::AB, Mbase + (size_t)(c0 + i) * T::MB,
                                             lane, L, zs);
-        return mq_sum_rows(acc) + poison;
+        return aeth_sum_rows(acc) + poison;
     };
     if (!RING) {  // every tile already in flight: no refills
 #pragma unroll

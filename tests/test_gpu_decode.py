@@ -91,6 +91,29 @@ def test_attention_one_hot(gpu):
         np.testing.assert_allclose(got[h], kv[1, 0, 77], rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("nh,nkv,ms,seq", [(64, 8, 4096, 3000), (8, 8, 512, 300), (16, 2, 8192, 8192),
+                                           (32, 8, 2688, 2600), (4, 1, 256, 1)])
+def test_attention_shapes(gpu, nh, nkv, ms, seq):
+    """Query-head groups of 1, 4 and 8, several chunk-merge batches (seq past
+    2560), the longest cache (128 chunks): back-to-back calls of different
+    shapes share one workspace and its chunk counters."""
+    torch = gpu
+    hd = 128
+    rng = np.random.default_rng(seq + nh)
+    kv = rng.standard_normal((2, nkv, ms, hd)).astype(np.float32)
+    g = nh // nkv
+    for rep in range(2):
+        q = rng.standard_normal(nh * hd).astype(np.float32)
+        s = seq if rep == 0 else max(1, seq // 3)
+        od = torch.empty(nh * hd, dtype=torch.float32, device="cuda")
+        qd, kvd = dev(torch, q), dev(torch, kv)
+        A.check(A.lib().aeth_attn_decode(qd.data_ptr(), kvd.data_ptr(), nh, nkv, hd, ms, s, od.data_ptr(), None))
+        torch.cuda.synchronize()
+        ref = np.concatenate([O.attn_direct(q[h * hd:(h + 1) * hd], kv[0, h // g], kv[1, h // g], s, hd)
+                              for h in range(nh)])
+        assert_close(od.cpu().numpy(), ref, tol=1e-4, what="attn nh=%d nkv=%d seq=%d" % (nh, nkv, s))
+
+
 def test_silu_mul_and_add(gpu):
     torch = gpu
     rng = np.random.default_rng(4)
