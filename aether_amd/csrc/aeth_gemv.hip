@@ -469,7 +469,7 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
 
     float xv[XO][8], wv[XO][8];
     mq_load_x<XO, RAG>(xr, o0, o1, G.kx, xv);
-    mq_load_x<XO, RAG>(G.norm_w ? G.norm_w : xr, o0, o1, G.kx, wv);
+    if (G.norm_w) mq_load_x<XO, RAG>(G.norm_w, o0, o1, G.kx, wv);  // (a uniform branch)
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight stream
     Dt buf[RD][NBW];
 #pragma unroll
