@@ -537,9 +537,13 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
                     const float acc = tile(buf[r]);
                     if (lane < 16) part[(j * W + wave) * 16 + lane] = acc;
                 }
+                // refill with tile j + RD; past the run, the same loads of chunk 0 of tile 0,
+                // which every wave's surplus refills share (so they hit in cache), instead of
+                // re-streaming the last tile (branching around the loads would leave the
+                // compiler's per-tile waits inexact)
 #pragma unroll
                 for (int i = 0; i < NBW; i++)
-                    T::load(buf[r][i], G, (t0 + min(j + RD, ntw - 1)) * nc + c0 + min(i, max(nbw - 1, 0)), lane);
+                    T::load(buf[r][i], G, j + RD < ntw ? (t0 + j + RD) * nc + c0 + min(i, max(nbw - 1, 0)) : 0, lane);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
