@@ -50,10 +50,12 @@
 // after the one barrier the partials are summed in a fixed order
 // (deterministic) and the epilogue (accumulate, SwiGLU, argmax) runs.
 //
-// Every global load is issued unconditionally (out-of-range indices clamped to
-// valid addresses, values discarded): the compiler can then count outstanding
+// Every global load is issued unconditionally (values past a wave's chunks or
+// a workgroup's tiles are discarded): the compiler can then count outstanding
 // loads exactly and wait for each one alone, instead of draining the whole
-// weight stream at the first use of x.
+// weight stream at the first use of x. Surplus loads repeat a load issued in
+// the same batch (still in flight, so they cost no HBM traffic), except the
+// ring's refills past the last tile, which read chunk 0 of tile 0.
 #include <math.h>
 #include <stdlib.h>
 
