@@ -495,20 +495,21 @@ int aeth_embed_launch(const float* table, const int* d_token, int64_t token, int
 // Advances the device decode state {token, pos, fill} after a step:
 // StaticKVCache::advance (kv_cache.rs:67-71) and pos += 1; the next token was
 // written by the argmax.
-__global__ void k_state_advance(int* st, unsigned long long* amax, int64_t max_seq) {
+__global__ void k_state_advance(int* st, unsigned long long* amax, int* hist, int64_t max_seq) {
     if (threadIdx.x == 0 && blockIdx.x == 0) {
         if (amax) {
             st[0] = (int)(uint32_t)(*amax & 0xFFFFFFFFull);
             st[3] = st[0];
             *amax = 0ull;
+            if (hist && st[4] >= 0 && st[4] < max_seq) hist[st[4]++] = st[0];  // the step's token, by step
         }
         st[1] += 1;
         if (st[2] < max_seq) st[2] += 1;
     }
 }
 
-int aeth_state_advance_launch(int* st, unsigned long long* amax, int64_t max_seq, hipStream_t s) {
-    hipLaunchKernelGGL(k_state_advance, dim3(1), dim3(64), 0, s, st, amax, max_seq);
+int aeth_state_advance_launch(int* st, unsigned long long* amax, int* hist, int64_t max_seq, hipStream_t s) {
+    hipLaunchKernelGGL(k_state_advance, dim3(1), dim3(64), 0, s, st, amax, hist, max_seq);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }

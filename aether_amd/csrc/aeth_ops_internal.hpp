@@ -26,7 +26,7 @@ int aeth_embed_launch(const float* table, const int* d_token, int64_t token, int
                       hipStream_t s);
 // After a step: token = argmax key's row (key reset to 0), pos += 1, fill
 // advanced (StaticKVCache::advance).
-int aeth_state_advance_launch(int* st, unsigned long long* amax, int64_t max_seq, hipStream_t s);
+int aeth_state_advance_launch(int* st, unsigned long long* amax, int* hist, int64_t max_seq, hipStream_t s);
 // Batched prefill glue (aeth_prefill.hip).
 int aeth_embed_rows_launch(const float* table, const int* d_tokens, int64_t n, int64_t d, float* x, hipStream_t s);
 int aeth_prefill_rope_kv_launch(float* qkv, int64_t n, int64_t nh, int64_t nkv, int64_t hd, const float* sin_t,

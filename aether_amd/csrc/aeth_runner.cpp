@@ -45,7 +45,7 @@ struct aeth_runner {
     int64_t xws_floats = 0;
     int* st = nullptr;       // device {token, pos, fill, next token}
     unsigned long long* amax = nullptr;  // fused LM-head argmax key (reset by the state kernel)
-    int* tok_out = nullptr;  // unused slot kept for the release list
+    int* tok_out = nullptr;  // [max_seq] greedy tokens of the current generate call, by step
     int fill = 0;           // host mirror of the cache fill
     hipGraphExec_t graph = nullptr;
     // batched prefill buffers (grow-only): rows of x, normed x, q|k|v, attention
@@ -170,7 +170,7 @@ void runner_release(aeth_runner* r) {
 }
 
 // Enqueues layers [l0, l1) of one decode step on r->stream; scalars come
-// from r->st = {token, pos, fill, next token}. Per layer (runner.rs:1557-1632):
+// from r->st = {token, pos, fill, next token, generate step}. Per layer (runner.rs:1557-1632):
 //   qkv  = rmsnorm(x, attn_norm) · Wqkvᵀ          (norm fused into the GEMV)
 //   attn = GQA attention with RoPE + KV append   (one kernel)
 //   x   += attn · Woᵀ                              (residual fused)
@@ -239,7 +239,7 @@ int enqueue_head(aeth_runner* r) {
     e.eps = c.rms_norm_eps;
     e.amax = r->amax;
     if ((rc = aeth_gemv_launch_ex(r->lm_head, r->x, 1, r->logits, e, s))) return rc;
-    return aeth_state_advance_launch(r->st, r->amax, c.max_seq_len, s);
+    return aeth_state_advance_launch(r->st, r->amax, r->tok_out, c.max_seq_len, s);
 }
 
 int enqueue_step(aeth_runner* r) {
@@ -345,7 +345,7 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
 }
 
 int set_state(aeth_runner* r, int token, int pos) {
-    int h[4] = {token, pos, r->fill, token};
+    int h[5] = {token, pos, r->fill, token, 0};  // + the generate step counter
     AETH_HIP_CHECK(hipMemcpyAsync(r->st, h, sizeof(h), hipMemcpyHostToDevice, r->stream));
     return AETH_OK;
 }
@@ -496,8 +496,8 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
         return aeth_set_error(AETH_EHIP, "runner: argmax slot clear failed");
     }
     RC(dmalloc((uint8_t**)&r->am_ws, aeth_argmax_ws_bytes()));
-    RC(dmalloc(&r->st, 4));
-    RC(dmalloc(&r->tok_out, 4));
+    RC(dmalloc(&r->st, 5));
+    RC(dmalloc(&r->tok_out, c.max_seq_len));
     if (hipStreamSynchronize(s) != hipSuccess) {
         runner_release(r);
         return aeth_set_error(AETH_EHIP, "runner: setup sync failed");
@@ -619,11 +619,12 @@ extern "C" AETH_API int aeth_runner_generate(aeth_runner* r, int32_t token, int3
             return aeth_set_error(AETH_EHIP, "graph instantiate failed: %s", hipGetErrorString(e));
         }
     }
-    for (int i = 0; i < n_steps; i++) {
+    for (int i = 0; i < n_steps; i++) {  // each step appends its token to tok_out on the device
         if (use_graph) AETH_HIP_CHECK(hipGraphLaunch(r->graph, r->stream));
         else if ((rc = enqueue_step(r))) return rc;
-        AETH_HIP_CHECK(hipMemcpyAsync(tokens + i, r->st + 3, sizeof(int), hipMemcpyDeviceToHost, r->stream));
     }
+    if (n_steps > 0)
+        AETH_HIP_CHECK(hipMemcpyAsync(tokens, r->tok_out, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, r->stream));
     AETH_HIP_CHECK(hipStreamSynchronize(r->stream));
     r->fill += n_steps;
     return AETH_OK;
