@@ -29,9 +29,56 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
     for (int64_t i = threadIdx.x; i < n; i += 256) o[i] = xr[i] / rms * w[i];
 }
 
+// Rows of n = 1024·V elements with 16-byte aligned x, w and out: one pass, the
+// row held in registers (V float4 per thread, all loads issued up front), and
+// x / rms as one correctly rounded reciprocal with a residual step per element
+// (Markstein's correctly rounded quotient: the same value as the division).
+template <int V>
+__global__ void __launch_bounds__(256) k_rmsnorm_v(const float* __restrict__ x, const float* __restrict__ w,
+                                                   int64_t n, float eps, float* __restrict__ out) {
+    __shared__ float red[4];
+    const float4* xr = (const float4*)(x + (int64_t)blockIdx.x * n);
+    const float4* wr = (const float4*)w;
+    float4* o = (float4*)(out + (int64_t)blockIdx.x * n);
+    float4 v[V], wv[V];
+#pragma unroll
+    for (int j = 0; j < V; j++) v[j] = xr[threadIdx.x + 256 * j];
+#pragma unroll
+    for (int j = 0; j < V; j++) wv[j] = wr[threadIdx.x + 256 * j];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; j++) ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+    ss = aeth_wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rms = sqrtf(tot / (float)n + eps), inv = 1.0f / rms;
+    auto q = [&](float a) { const float q0 = a * inv; return fmaf(fmaf(-q0, rms, a), inv, q0); };
+#pragma unroll
+    for (int j = 0; j < V; j++)
+        o[threadIdx.x + 256 * j] = make_float4(q(v[j].x) * wv[j].x, q(v[j].y) * wv[j].y, q(v[j].z) * wv[j].z,
+                                               q(v[j].w) * wv[j].w);
+}
+
 int aeth_rmsnorm_launch(const float* x, const float* w, int64_t rows, int64_t n, float eps, float* out,
                         hipStream_t s) {
     if (rows <= 0 || n <= 0) return AETH_OK;
+    const bool al16 = (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15) == 0;
+    if (al16 && n % 1024 == 0 && n <= 8192) {
+        const dim3 g((unsigned)rows), b(256);
+        switch (n / 1024) {
+            case 1: hipLaunchKernelGGL(k_rmsnorm_v<1>, g, b, 0, s, x, w, n, eps, out); break;
+            case 2: hipLaunchKernelGGL(k_rmsnorm_v<2>, g, b, 0, s, x, w, n, eps, out); break;
+            case 3: hipLaunchKernelGGL(k_rmsnorm_v<3>, g, b, 0, s, x, w, n, eps, out); break;
+            case 4: hipLaunchKernelGGL(k_rmsnorm_v<4>, g, b, 0, s, x, w, n, eps, out); break;
+            case 5: hipLaunchKernelGGL(k_rmsnorm_v<5>, g, b, 0, s, x, w, n, eps, out); break;
+            case 6: hipLaunchKernelGGL(k_rmsnorm_v<6>, g, b, 0, s, x, w, n, eps, out); break;
+            case 7: hipLaunchKernelGGL(k_rmsnorm_v<7>, g, b, 0, s, x, w, n, eps, out); break;
+            default: hipLaunchKernelGGL(k_rmsnorm_v<8>, g, b, 0, s, x, w, n, eps, out); break;
+        }
+        AETH_LAUNCH_CHECK();
+        return AETH_OK;
+    }
     hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, s, x, w, n, eps, out);
     AETH_LAUNCH_CHECK();
     return AETH_OK;

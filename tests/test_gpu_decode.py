@@ -19,10 +19,12 @@ def dev(torch, arr):
     return torch.from_numpy(np.ascontiguousarray(arr)).cuda()
 
 
-def test_rmsnorm(gpu):
+@pytest.mark.parametrize("n", [4096, 1024, 8192, 4000, 100])
+def test_rmsnorm(gpu, n):
+    """Row lengths of the one-pass register kernel (multiples of 1024) and of
+    the general loop."""
     torch = gpu
     rng = np.random.default_rng(1)
-    n = 4096
     x = rng.standard_normal((3, n)).astype(np.float32) * 3
     w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
     xd, wd = dev(torch, x), dev(torch, w)
