@@ -71,12 +71,68 @@ __global__ void __launch_bounds__(256) k_prefill_rope_kv(float* __restrict__ qkv
     }
 }
 
+// The same for hd % 8 == 0 on 16-byte aligned rows: float4 pieces (four rotation
+// pairs, or four v elements), 4 per thread per batch with every load issued
+// before the first store.
+__global__ void __launch_bounds__(256) k_prefill_rope_kv4(float* __restrict__ qkv, int64_t stride, int nh, int nkv,
+                                                          int hd, const float* __restrict__ sin_t,
+                                                          const float* __restrict__ cos_t, int64_t max_seq,
+                                                          float* __restrict__ layer_kv) {
+    const int64_t i = blockIdx.x;
+    const int half = hd / 2, q4 = half / 4;
+    const int64_t p = i < max_seq ? i : max_seq - 1;
+    float* row = qkv + i * stride;
+    const float* sn = sin_t + p * half;
+    const float* cs = cos_t + p * half;
+    const int64_t hs = max_seq * hd;
+    const int units = (nh + nkv) * q4, vunits = nkv * hd / 4;
+    for (int u0 = 0; u0 < units; u0 += 1024) {
+        float4 a[4], b[4], c[4], t[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int u = min(u0 + (int)threadIdx.x + 256 * k, units - 1), h = u / q4, e = 4 * (u - h * q4);
+            a[k] = *(const float4*)(row + (int64_t)h * hd + e);
+            b[k] = *(const float4*)(row + (int64_t)h * hd + e + half);
+            c[k] = *(const float4*)(cs + e);
+            t[k] = *(const float4*)(sn + e);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int u = u0 + (int)threadIdx.x + 256 * k;
+            if (u < units) {
+                const int h = u / q4, e = 4 * (u - h * q4);
+                const float4 r0 = make_float4(a[k].x * c[k].x - b[k].x * t[k].x, a[k].y * c[k].y - b[k].y * t[k].y,
+                                              a[k].z * c[k].z - b[k].z * t[k].z, a[k].w * c[k].w - b[k].w * t[k].w);
+                const float4 r1 = make_float4(a[k].x * t[k].x + b[k].x * c[k].x, a[k].y * t[k].y + b[k].y * c[k].y,
+                                              a[k].z * t[k].z + b[k].z * c[k].z, a[k].w * t[k].w + b[k].w * c[k].w);
+                *(float4*)(row + (int64_t)h * hd + e) = r0;
+                *(float4*)(row + (int64_t)h * hd + e + half) = r1;
+                if (h >= nh) {
+                    float* kd = layer_kv + (int64_t)(h - nh) * hs + i * hd;
+                    *(float4*)(kd + e) = r0;
+                    *(float4*)(kd + e + half) = r1;
+                }
+            }
+        }
+    }
+    const float* vsrc = row + (int64_t)(nh + nkv) * hd;
+    for (int u = threadIdx.x; u < vunits; u += 256) {
+        const int h = (4 * u) / hd, e = 4 * u - h * hd;
+        *(float4*)(layer_kv + (int64_t)(nkv + h) * hs + i * hd + e) = *(const float4*)(vsrc + 4 * u);
+    }
+}
+
 int aeth_prefill_rope_kv_launch(float* qkv, int64_t n, int64_t nh, int64_t nkv, int64_t hd, const float* sin_t,
                                 const float* cos_t, int64_t max_seq, float* layer_kv, hipStream_t s) {
     if (n <= 0) return AETH_OK;
     if (n > max_seq) return aeth_set_error(AETH_EINVAL, "prefill: %lld tokens exceed the cache", (long long)n);
-    hipLaunchKernelGGL(k_prefill_rope_kv, dim3((unsigned)n), dim3(256), 0, s, qkv, (nh + 2 * nkv) * hd, (int)nh,
-                       (int)nkv, (int)hd, sin_t, cos_t, max_seq, layer_kv);
+    const bool al16 = (((uintptr_t)qkv | (uintptr_t)sin_t | (uintptr_t)cos_t | (uintptr_t)layer_kv) & 15) == 0;
+    if (al16 && hd % 8 == 0)
+        hipLaunchKernelGGL(k_prefill_rope_kv4, dim3((unsigned)n), dim3(256), 0, s, qkv, (nh + 2 * nkv) * hd, (int)nh,
+                           (int)nkv, (int)hd, sin_t, cos_t, max_seq, layer_kv);
+    else
+        hipLaunchKernelGGL(k_prefill_rope_kv, dim3((unsigned)n), dim3(256), 0, s, qkv, (nh + 2 * nkv) * hd, (int)nh,
+                           (int)nkv, (int)hd, sin_t, cos_t, max_seq, layer_kv);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
