@@ -13,7 +13,9 @@ shape greedy decode (config 4), the Q5_K GEMV and the headline shape on the
 int8 dot-product path (and, on request, GGUF-order F16 / Q2_K GEMVs), plus
 `roofline` for the headline kernel and
 `cpu_baseline`: the oracle's restatement of the reference's AVX2 path on one
-host core over a bounded sample of the same workload.
+host core over a bounded sample of the same workload (and, in `extra`, the
+reference's scalar kernel with its output rows spread over up to 16 host
+threads, as its rayon callers spread them).
 """
 import argparse
 import ctypes
@@ -159,6 +161,37 @@ def measured_traffic():
         return None
 
 
+def cpu_rows_parallel(raw, x, n, k, seconds=4.0):
+    """Secondary CPU figure: the reference's scalar Q4_K kernel (q4_k.rs, whose
+    callers spread output rows over cores with rayon) restated in oracle/oracle.c,
+    its output rows split evenly across up to 16 host threads (ctypes releases
+    the GIL during each call)."""
+    import concurrent.futures
+    from oracle import oracle as O
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    row_bytes = (k // 256) * 144
+    parts = [(n * t // threads, n * (t + 1) // threads) for t in range(threads)]
+
+    def run(pr):
+        r0, r1 = pr
+        O.scalar_matmul(12, x, raw[r0 * row_bytes:r1 * row_bytes], 1, r1 - r0, k)
+
+    calls = 0
+    with concurrent.futures.ThreadPoolExecutor(threads) as ex:
+        t0 = time.perf_counter()
+        while True:
+            list(ex.map(run, parts))
+            calls += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+    nbytes = algorithmic_bytes(12, n, k)
+    return {"value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port (scalar kernel, rows over threads)",
+            "sample": "%d full Q4_K GEMVs 14336x4096 in %.1f s" % (calls, el)}
+
+
 def cpu_baseline(raw, x, n, k, seconds=10.0):
     """The oracle's AVX2-path restatement (single thread, as the reference's
     avx2::matmul_q4_k) timed on this host over repeated full GEMVs."""
@@ -274,6 +307,9 @@ def main():
     if not args.no_cpu:
         raw = head["raw0"].cpu().numpy()
         x = head["x"].cpu().numpy()
+        cpu_par = cpu_rows_parallel(raw, x, n, k)  # before the single-core leg pins this process
+        print("[bench] cpu, scalar kernel over threads: %s" % cpu_par, file=sys.stderr, flush=True)
+        extra["cpu_q4_k_gemv_rows_parallel"] = cpu_par
         cpu = cpu_baseline(raw, x, n, k, args.cpu_seconds)
         print("[bench] cpu baseline: %s" % cpu, file=sys.stderr, flush=True)
 
