@@ -17,14 +17,16 @@
 // rows, already split by scale group; the output lane (n, g) holds slot g's
 // four digit sums for row n (each exact in i32: |Σ q·d| ≤ 32·63·128), pairs
 // them in i32 (d0 + 2^8·d1, d2 + 2^8·d3) and recombines exactly in f64 before
-// one rounding to f32 and the group's scales.
+// one rounding to f32 and the group's scales (Q4_K: one f32 fma, exact because
+// both pairs fit 24 bits).
 //
 // Per format ("chunk" = the unit of K a wave steps through):
 //  Q4_K, chunk = super-block (256). Per half h, lane (n, kg) loads
 //    qs[64h + 16kg, +16) of row n: low nibbles are sub-block 4h + 2(kg ≥ 2),
-//    high nibbles the next one. Two MFMAs (low / high nibbles) share one A;
-//    slot g ↔ sub-block 4h + g, the even slots exact in the first result, the
-//    odd ones in the second;  acc += 2^-S·Σq·x_int·d·sc − dmin·m·Σx.
+//    high nibbles the next one. Two chained MFMAs (low, then high nibbles):
+//    the even slots' A rows feed the first, the odd slots' the second (each
+//    reads the zero slot for the other rows), so slot g ↔ sub-block 4h + g
+//    ends complete;  acc += 2^-S·Σq·x_int·d·sc − dmin·m·Σx.
 //  Q5_K, as Q4_K (same quant and header planes) plus a plane of fifth bits:
 //    lane (n, kg) loads 8 bytes, 16 bits per (half, low / high nibbles) for its
 //    16 elements; each bit is spread to 0x10 of its byte before the MFMA.
