@@ -168,22 +168,24 @@ struct AttnArgs {
     float* out;          // [n_heads][hd]
 };
 
-// Thread layout (256 threads, chunk of T = 64 positions, HD = 128):
-//  scores: thread (p = tid/4, quarter qd = tid%4) holds K[p][32qd, +32) and
-//          dots it with every query head of the group; 4-lane reduction.
+// Thread layout (512 threads = 8 waves, two per SIMD; chunk of T = 64
+// positions, HD = 128):
+//  scores: thread (p = tid/8, eighth e = tid%8) holds K[p][16e, +16) and dots
+//          it with every query head of the group; 8-lane reduction.
 //  P·V:    thread (dims 4(tid%32), position group pg = tid/32) holds
-//          V[8pg + j][4(tid%32), +4) for j < 8.
+//          V[4pg + j][4(tid%32), +4) for j < 4; lanes l, l+32 and then the
+//          8 waves are summed.
 // All loads are unconditional (clamped indices) and issued in one batch in
 // the order q/rope inputs → K → V, so each phase waits only for its own data.
 template <int HD>
-__global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
+__global__ void __launch_bounds__(512) k_attn(AttnArgs A) {
     static_assert(HD == 128, "decode attention is laid out for head_dim 128");
-    constexpr int HALF = HD / 2;
+    constexpr int HALF = HD / 2, NWV = 8;
     __shared__ __attribute__((aligned(16))) float qs[ATTN_MAX_GROUPS][HD];
     __shared__ __attribute__((aligned(16))) float knew[HD];
     __shared__ __attribute__((aligned(16))) float vnew[HD];
     __shared__ float sc[ATTN_MAX_GROUPS][ATTN_T];
-    __shared__ __attribute__((aligned(16))) float ov[4][ATTN_MAX_GROUPS][HD];
+    __shared__ __attribute__((aligned(16))) float ov[NWV][ATTN_MAX_GROUPS][HD];
     __shared__ float mstat[ATTN_MAX_GROUPS][2];
     const int kvh = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int groups = A.n_heads / A.kv_heads;
@@ -209,60 +211,54 @@ __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
     if (prow < 0) prow = 0;
     const bool has_new = fused && fill >= t0 && fill < t0 + ATTN_T && fill < A.max_seq;
 
-    // 1. q / rope inputs (rotation pairs (e, e + HD/2); two pairs per thread cover 8
-    // heads). Without the fused path the table and new-k/v pointers alias q so that
-    // the loads stay unconditional; their values are then unused.
+    // 1. q / rope inputs (rotation pairs (e, e + HD/2); one pair per thread covers
+    // 8 heads). Without the fused path the table and new-k/v pointers alias q so
+    // that the loads stay unconditional; their values are then unused.
     const float* qsrc = (fused ? A.qkv : A.q) + (int64_t)kvh * groups * HD;
     const float* sin_t = fused ? A.sin_t : qsrc;
     const float* cos_t = fused ? A.cos_t : qsrc;
     const float* ksrc = fused ? A.qkv + (int64_t)A.n_heads * HD + (int64_t)kvh * HD : qsrc;
     const float* vsrc = fused ? A.qkv + (int64_t)(A.n_heads + A.kv_heads) * HD + (int64_t)kvh * HD : qsrc;
-    float qx0[2], qx1[2], qsn[2], qcs[2];
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-        const int i = min(tid + 256 * r, groups * HALF - 1), g = i / HALF, e = i - g * HALF;
-        qx0[r] = qsrc[g * HD + e];
-        qx1[r] = qsrc[g * HD + e + HALF];
-        qsn[r] = sin_t[prow * HALF + e];
-        qcs[r] = cos_t[prow * HALF + e];
+    float qx0, qx1, qsn, qcs;
+    {
+        const int i = min(tid, groups * HALF - 1), g = i / HALF, e = i - g * HALF;
+        qx0 = qsrc[g * HD + e];
+        qx1 = qsrc[g * HD + e + HALF];
+        qsn = sin_t[prow * HALF + e];
+        qcs = cos_t[prow * HALF + e];
     }
     const float kx0 = ksrc[tid & (HALF - 1)], kx1 = ksrc[(tid & (HALF - 1)) + HALF];
     const float vx = vsrc[tid & (HD - 1)];
     __builtin_amdgcn_sched_barrier(0);  // these small loads go out before the K/V batch
     // 2. K (scores layout) and V (P·V layout) of the chunk, positions past nt clamped
-    const int sp = tid >> 2, qd = tid & 3;
-    float4 kk[8];
+    const int sp = tid >> 3, qe = tid & 7;
+    float4 kk[4];
     {
-        const float4* kr = (const float4*)(K + (t0 + min(sp, nt - 1)) * HD + 32 * qd);
+        const float4* kr = (const float4*)(K + (t0 + min(sp, nt - 1)) * HD + 16 * qe);
 #pragma unroll
-        for (int i = 0; i < 8; i++) kk[i] = kr[i];
+        for (int i = 0; i < 4; i++) kk[i] = kr[i];
     }
     const int vd4 = tid & 31, pg = tid >> 5;
-    float4 vv[8];
+    float4 vv[4];
 #pragma unroll
-    for (int j = 0; j < 8; j++) vv[j] = *(const float4*)(V + (t0 + min(8 * pg + j, nt - 1)) * HD + 4 * vd4);
+    for (int j = 0; j < 4; j++) vv[j] = *(const float4*)(V + (t0 + min(4 * pg + j, nt - 1)) * HD + 4 * vd4);
     // Consume the q / rope inputs here, after the K/V batch is issued: otherwise the
     // compiler sinks their loads into the conditional stores below, behind K and V.
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" : "+v"(qx0[0]), "+v"(qx1[0]), "+v"(qsn[0]), "+v"(qcs[0]), "+v"(qx0[1]), "+v"(qx1[1]),
-                 "+v"(qsn[1]), "+v"(qcs[1]));
+    asm volatile("" : "+v"(qx0), "+v"(qx1), "+v"(qsn), "+v"(qcs));
     float kvx[3] = {kx0, kx1, vx};
     asm volatile("" : "+v"(kvx[0]), "+v"(kvx[1]), "+v"(kvx[2]));
 
     // 3. rotated q (and the new k / v) to LDS
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-        const int i = tid + 256 * r;
-        if (i < groups * HALF) {
-            const int g = i / HALF, e = i - g * HALF;
-            qs[g][e] = fused ? qx0[r] * qcs[r] - qx1[r] * qsn[r] : qx0[r];
-            qs[g][e + HALF] = fused ? qx0[r] * qsn[r] + qx1[r] * qcs[r] : qx1[r];
-        }
+    if (tid < groups * HALF) {
+        const int g = tid / HALF, e = tid - g * HALF;
+        qs[g][e] = fused ? qx0 * qcs - qx1 * qsn : qx0;
+        qs[g][e + HALF] = fused ? qx0 * qsn + qx1 * qcs : qx1;
     }
     if (fused) {
-        if (tid < HALF) {  // pair r = 0 of thread tid < HALF is (head 0, e = tid): same table entries
-            knew[tid] = kvx[0] * qcs[0] - kvx[1] * qsn[0];
-            knew[tid + HALF] = kvx[0] * qsn[0] + kvx[1] * qcs[0];
+        if (tid < HALF) {  // the pair of thread tid < HALF is (head 0, e = tid): same table entries
+            knew[tid] = kvx[0] * qcs - kvx[1] * qsn;
+            knew[tid + HALF] = kvx[0] * qsn + kvx[1] * qcs;
         }
         if (tid < HD) vnew[tid] = kvx[2];
     }
@@ -276,25 +272,27 @@ __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
     const bool knew_here = has_new && t0 + sp == fill;
     if (knew_here) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) kk[i] = *(const float4*)(&knew[32 * qd + 4 * i]);
+        for (int i = 0; i < 4; i++) kk[i] = *(const float4*)(&knew[16 * qe + 4 * i]);
     }
 #pragma unroll
     for (int g = 0; g < ATTN_MAX_GROUPS; g++) {
         if (g < groups) {
             float a = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 qv = *(const float4*)(&qs[g][32 * qd + 4 * i]);
+            for (int i = 0; i < 4; i++) {
+                const float4 qv = *(const float4*)(&qs[g][16 * qe + 4 * i]);
                 a += qv.x * kk[i].x + qv.y * kk[i].y + qv.z * kk[i].z + qv.w * kk[i].w;
             }
             a += aeth_dpp_xor1f(a);
             a += aeth_dpp_xor2f(a);
-            if (qd == 0) sc[g][sp] = sp < nt ? a * scale : -INFINITY;
+            a += aeth_dpp_mirror8f(a);
+            if (qe == 0) sc[g][sp] = sp < nt ? a * scale : -INFINITY;
         }
     }
     __syncthreads();
-    // 5. softmax over the chunk: wave w handles heads w, w+4
-    for (int g = wave; g < groups; g += 4) {
+    // 5. softmax over the chunk: wave w handles head w
+    if (wave < groups) {
+        const int g = wave;
         const float sv = sc[g][lane];
         const float m = aeth_wave_max(sv);
         const float pr = lane < nt ? expf(sv - m) : 0.0f;
@@ -306,20 +304,20 @@ __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
         }
     }
     __syncthreads();
-    // 6. Σ_t p_t v_t: 8 positions per thread, then lanes l / l+32 and the 4 waves
+    // 6. Σ_t p_t v_t: 4 positions per thread, then lanes l / l+32 and the 8 waves
     if (has_new) {
         const float4 nv = *(const float4*)(&vnew[4 * vd4]);
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (t0 + 8 * pg + j == fill) vv[j] = nv;
+        for (int j = 0; j < 4; j++)
+            if (t0 + 4 * pg + j == fill) vv[j] = nv;
     }
 #pragma unroll
     for (int g = 0; g < ATTN_MAX_GROUPS; g++) {
         if (g < groups) {
             float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float pj = sc[g][8 * pg + j];
+            for (int j = 0; j < 4; j++) {
+                const float pj = sc[g][4 * pg + j];
                 o.x += pj * vv[j].x;
                 o.y += pj * vv[j].y;
                 o.z += pj * vv[j].z;
@@ -333,10 +331,11 @@ __global__ void __launch_bounds__(256) k_attn(AttnArgs A) {
         }
     }
     __syncthreads();
-    for (int i = tid; i < groups * HD; i += 256) {
+    for (int i = tid; i < groups * HD; i += 512) {
         const int g = i / HD, d = i - g * HD;
         float* dst = A.ws + ((int64_t)(kvh * groups + g) * A.max_chunks + chunk) * (HD + 2);
-        dst[d] = (ov[0][g][d] + ov[1][g][d]) + (ov[2][g][d] + ov[3][g][d]);
+        dst[d] = ((ov[0][g][d] + ov[1][g][d]) + (ov[2][g][d] + ov[3][g][d])) +
+                 ((ov[4][g][d] + ov[5][g][d]) + (ov[6][g][d] + ov[7][g][d]));
     }
     if (tid < groups) {
         float* dst = A.ws + ((int64_t)(kvh * groups + tid) * A.max_chunks + chunk) * (HD + 2);
@@ -426,7 +425,7 @@ int aeth_attn_launch(const float* q, const float* qkv, float* layer_kv, const fl
     A.out = out;
     const int grid_chunks = d_st ? A.max_chunks : (int)aeth_cdiv(min(seq, max_seq), ATTN_T);
     if (grid_chunks <= 0) return AETH_OK;
-    hipLaunchKernelGGL(k_attn<128>, dim3(grid_chunks, (unsigned)kv_heads), dim3(256), 0, s, A);
+    hipLaunchKernelGGL(k_attn<128>, dim3(grid_chunks, (unsigned)kv_heads), dim3(512), 0, s, A);
     AETH_LAUNCH_CHECK();
     hipLaunchKernelGGL(k_attn_merge<128>, dim3((unsigned)n_heads), dim3(128), 0, s, A);
     AETH_LAUNCH_CHECK();
