@@ -152,6 +152,9 @@ int aeth_kv_append_launch(float* layer_kv, const float* k, const float* v, int64
 #define ATTN_T 64
 #define ATTN_MAX_GROUPS 8
 #define ATTN_MAX_CHUNKS 128  // max_seq <= 8192
+#ifndef ATTN_NT
+#define ATTN_NT 512  // threads of k_attn (512 or 1024; 1024 measured 7 % slower at seq 2049)
+#endif
 
 struct AttnArgs {
     const float* q;      // [n_heads][hd] (already rotated) when qkv == nullptr
@@ -177,10 +180,12 @@ struct AttnArgs {
 //          8 waves are summed.
 // All loads are unconditional (clamped indices) and issued in one batch in
 // the order q/rope inputs → K → V, so each phase waits only for its own data.
-template <int HD>
-__global__ void __launch_bounds__(512) k_attn(AttnArgs A) {
-    static_assert(HD == 128, "decode attention is laid out for head_dim 128");
-    constexpr int HALF = HD / 2, NWV = 8;
+template <int HD, int NT>
+__global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
+    static_assert(HD == 128 && (NT == 512 || NT == 1024), "decode attention is laid out for head_dim 128");
+    constexpr int HALF = HD / 2, NWV = NT / 64;
+    constexpr int LP = NT / 64, KD = HD / LP, K4 = KD / 4;  // scores: lanes per position, dims per lane
+    constexpr int PP = 2048 / NT;                            // P·V: positions per thread
     __shared__ __attribute__((aligned(16))) float qs[ATTN_MAX_GROUPS][HD];
     __shared__ __attribute__((aligned(16))) float knew[HD];
     __shared__ __attribute__((aligned(16))) float vnew[HD];
@@ -231,17 +236,17 @@ __global__ void __launch_bounds__(512) k_attn(AttnArgs A) {
     const float vx = vsrc[tid & (HD - 1)];
     __builtin_amdgcn_sched_barrier(0);  // these small loads go out before the K/V batch
     // 2. K (scores layout) and V (P·V layout) of the chunk, positions past nt clamped
-    const int sp = tid >> 3, qe = tid & 7;
-    float4 kk[4];
+    const int sp = tid / LP, qe = tid % LP;
+    float4 kk[K4];
     {
-        const float4* kr = (const float4*)(K + (t0 + min(sp, nt - 1)) * HD + 16 * qe);
+        const float4* kr = (const float4*)(K + (t0 + min(sp, nt - 1)) * HD + KD * qe);
 #pragma unroll
-        for (int i = 0; i < 4; i++) kk[i] = kr[i];
+        for (int i = 0; i < K4; i++) kk[i] = kr[i];
     }
     const int vd4 = tid & 31, pg = tid >> 5;
-    float4 vv[4];
+    float4 vv[PP];
 #pragma unroll
-    for (int j = 0; j < 4; j++) vv[j] = *(const float4*)(V + (t0 + min(4 * pg + j, nt - 1)) * HD + 4 * vd4);
+    for (int j = 0; j < PP; j++) vv[j] = *(const float4*)(V + (t0 + min(PP * pg + j, nt - 1)) * HD + 4 * vd4);
     // Consume the q / rope inputs here, after the K/V batch is issued: otherwise the
     // compiler sinks their loads into the conditional stores below, behind K and V.
     __builtin_amdgcn_sched_barrier(0);
@@ -272,20 +277,21 @@ __global__ void __launch_bounds__(512) k_attn(AttnArgs A) {
     const bool knew_here = has_new && t0 + sp == fill;
     if (knew_here) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) kk[i] = *(const float4*)(&knew[16 * qe + 4 * i]);
+        for (int i = 0; i < K4; i++) kk[i] = *(const float4*)(&knew[KD * qe + 4 * i]);
     }
 #pragma unroll
     for (int g = 0; g < ATTN_MAX_GROUPS; g++) {
         if (g < groups) {
             float a = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 qv = *(const float4*)(&qs[g][16 * qe + 4 * i]);
+            for (int i = 0; i < K4; i++) {
+                const float4 qv = *(const float4*)(&qs[g][KD * qe + 4 * i]);
                 a += qv.x * kk[i].x + qv.y * kk[i].y + qv.z * kk[i].z + qv.w * kk[i].w;
             }
             a += aeth_dpp_xor1f(a);
             a += aeth_dpp_xor2f(a);
             a += aeth_dpp_mirror8f(a);
+            if (LP == 16) a += aeth_dpp_mirror16f(a);
             if (qe == 0) sc[g][sp] = sp < nt ? a * scale : -INFINITY;
         }
     }
@@ -308,16 +314,16 @@ __global__ void __launch_bounds__(512) k_attn(AttnArgs A) {
     if (has_new) {
         const float4 nv = *(const float4*)(&vnew[4 * vd4]);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (t0 + 4 * pg + j == fill) vv[j] = nv;
+        for (int j = 0; j < PP; j++)
+            if (t0 + PP * pg + j == fill) vv[j] = nv;
     }
 #pragma unroll
     for (int g = 0; g < ATTN_MAX_GROUPS; g++) {
         if (g < groups) {
             float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float pj = sc[g][4 * pg + j];
+            for (int j = 0; j < PP; j++) {
+                const float pj = sc[g][PP * pg + j];
                 o.x += pj * vv[j].x;
                 o.y += pj * vv[j].y;
                 o.z += pj * vv[j].z;
@@ -331,11 +337,17 @@ __global__ void __launch_bounds__(512) k_attn(AttnArgs A) {
         }
     }
     __syncthreads();
-    for (int i = tid; i < groups * HD; i += 512) {
+    for (int i = tid; i < groups * HD; i += NT) {
         const int g = i / HD, d = i - g * HD;
         float* dst = A.ws + ((int64_t)(kvh * groups + g) * A.max_chunks + chunk) * (HD + 2);
-        dst[d] = ((ov[0][g][d] + ov[1][g][d]) + (ov[2][g][d] + ov[3][g][d])) +
-                 ((ov[4][g][d] + ov[5][g][d]) + (ov[6][g][d] + ov[7][g][d]));
+        float t8[NWV];
+#pragma unroll
+        for (int w = 0; w < NWV; w++) t8[w] = ov[w][g][d];
+#pragma unroll
+        for (int h = NWV / 2; h >= 1; h >>= 1)  // pairwise, a fixed order
+#pragma unroll
+            for (int w = 0; w < h; w++) t8[w] += t8[w + h];
+        dst[d] = t8[0];
     }
     if (tid < groups) {
         float* dst = A.ws + ((int64_t)(kvh * groups + tid) * A.max_chunks + chunk) * (HD + 2);
@@ -425,7 +437,7 @@ int aeth_attn_launch(const float* q, const float* qkv, float* layer_kv, const fl
     A.out = out;
     const int grid_chunks = d_st ? A.max_chunks : (int)aeth_cdiv(min(seq, max_seq), ATTN_T);
     if (grid_chunks <= 0) return AETH_OK;
-    hipLaunchKernelGGL(k_attn<128>, dim3(grid_chunks, (unsigned)kv_heads), dim3(512), 0, s, A);
+    hipLaunchKernelGGL((k_attn<128, ATTN_NT>), dim3(grid_chunks, (unsigned)kv_heads), dim3(ATTN_NT), 0, s, A);
     AETH_LAUNCH_CHECK();
     hipLaunchKernelGGL(k_attn_merge<128>, dim3((unsigned)n_heads), dim3(128), 0, s, A);
     AETH_LAUNCH_CHECK();
