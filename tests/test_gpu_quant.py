@@ -203,6 +203,29 @@ def test_benchmark_config_parity(gpu, dtype, n, k):
     assert_close(yd.cpu().numpy(), ref, what="config dtype %d" % dtype)
 
 
+@pytest.mark.parametrize("dtype,n,k", [(Q4_K, 50000, 4096), (Q8_0, 50000, 1024), (Q6_K, 33000, 512)])
+def test_gemv_tall_ragged_parity(gpu, dtype, n, k):
+    """Tall matrices take the refilling ring of tiles; these row counts leave the
+    last workgroup fewer tiles than the others (and fewer than the ring holds),
+    so its surplus loads and the past-the-end refills are exercised."""
+    torch = gpu
+    L = A.lib()
+    be, bb = GEOM[dtype]
+    nb = k // be
+    raw_d = torch.empty(n * nb * bb, dtype=torch.uint8, device="cuda")
+    A.check(L.aeth_fill_synthetic_raw(dtype, 0x7A11 + dtype, raw_d.data_ptr(), n * nb, None), "fill")
+    xd = torch.empty(k, dtype=torch.float32, device="cuda")
+    A.check(L.aeth_fill_normal_f32(0x5EED + n, xd.data_ptr(), k, 0.0, 1.0, None), "fill x")
+    w = ctypes.c_void_p()
+    A.check(L.aeth_weight_create(dtype, n, k, raw_d.data_ptr(), 1, None, ctypes.byref(w)), "create")
+    yd = torch.empty(n, dtype=torch.float32, device="cuda")
+    A.check(L.aeth_qmatmul(w, xd.data_ptr(), 1, yd.data_ptr(), 0, None), "qmatmul")
+    torch.cuda.synchronize()
+    L.aeth_weight_free(w)
+    ref = O.reference_matmul(dtype, xd.cpu().numpy(), raw_d.cpu().numpy(), 1, n, k)
+    assert_close(yd.cpu().numpy(), ref, what="tall dtype %d n=%d" % (dtype, n))
+
+
 # ── host-slice boundary: quantized_matmul_impl / QuantKernel registry ────
 
 def test_quantized_matmul_impl_host_slices(gpu):
