@@ -437,41 +437,60 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_ring(GemmArgs G) {
     }
 }
 
-// ── Split-K variant (the default): the same 64 × 128 workgroup tile, computed
-// by 4 waves as 2 column halves × 2 K halves, each wave a 64 × 64 tile over half
-// of K. Every dequantised weight fragment then feeds 4 MFMAs (2 m-tiles × {hi,
-// lo}) instead of 2, halving the VALU work per MFMA; the two K halves meet in
-// LDS at the end. A stage holds 64 K-positions of both halves (2 × 22 KiB), the
-// ring 3 stages (132 KiB: one workgroup per CU). Per stage and wave: 11 loads
-// through buffer resources (the stage offset is a scalar), 32 MFMAs.
+// ── Split-K variant: the same 64 × 128 workgroup tile, computed by 4 waves as
+// 2 column halves × 2 K halves, each wave a 64 × 64 tile over half of K. Every
+// dequantised weight fragment then feeds 4 MFMAs (2 m-tiles × {hi, lo}) instead
+// of 2, halving the VALU work per MFMA; the two K halves meet in LDS at the end.
+// A stage holds 64 K-positions of both halves (2 × 22 KiB), the ring 3 stages
+// (132 KiB: one workgroup per CU). Per stage and wave: 11 loads through buffer
+// resources (the stage offset is a scalar), 32 MFMAs. The default launches the
+// 8-wave form (k_gemm_q4k_sk8: the two m-tiles on separate waves, two waves per
+// SIMD, 6 loads and 16 MFMAs per stage and wave), measured 2-5 % faster; splitting
+// the columns instead (dequantisation not repeated, A read twice from LDS) gained
+// nothing.
 #define G3_HALF (G2_A + G2_B + 2048)  // one K half: A fragments, quants, headers
 #define G3_STAGE (2 * G3_HALF)
 #define G3_LOADS 11
 
-__global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
+template <int MS>
+__device__ __forceinline__ void gemm_sk_body(const GemmArgs& G) {
+    // MS = 1: 4 waves, each both m-tiles of its (column half, K half).
+    // MS = 2: 8 waves, waves w and w + 4 take m-tile 0 and 1 of the same (column
+    // half, K half), two waves per SIMD, so one wave's dequantisation and LDS
+    // waits overlap the other's MFMAs; the LDS ring is the same.
+    constexpr int NM = 2 / MS;                // m-tiles per wave
+    constexpr int LOADS = MS == 1 ? G3_LOADS : 6;
     __shared__ __attribute__((aligned(1024))) char ring[G2_NST * G3_STAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave & 1, kh = wave >> 1;  // column half, K half
+    const int wq = wave & 3, wn = wave & 1, kh = (wave >> 1) & 1;  // loader slot, column half, K half
+    const int mb = MS == 2 ? wave >> 2 : 0;                      // first m-tile of this wave
     int tm, tn;
     g2_tile(blockIdx.x, G.gm, G.gn, tm, tn);
     const int n0 = tn * G2_BN, m0 = tm * G2_BM;
     const int nb = G.nb, hsb = nb / 2, nst = 4 * hsb, nks = G.k / 16;
 
-    // Direct loads: 44 pieces of 1 KiB per stage, piece w + 4i to wave w (i < 11):
-    // i < 8: A fragment (K half i/4, local fragment w + 4(i%4)); i = 8, 9: quants of
-    // tiles 2w, 2w+1 for K half i-8; i = 10: headers of tiles 4(w%2)..+3 for K half w/2.
-    // Lane offsets are fixed; stage s of K half h adds (h·nst + s)·8 KiB (A),
-    // ·512 B (quants), ((h·nst + s)/4)·256 B (headers).
-    uint32_t a_lo[4];
+    // Direct loads: 44 pieces of 1 KiB per stage. MS = 1: piece w + 4i to wave w
+    // (i < 11): i < 8: A fragment (K half i/4, local fragment w + 4(i%4)); i = 8, 9:
+    // quants of tiles 2w, 2w+1 for K half i-8; i = 10: headers of tiles
+    // 4(w%2)..+3 for K half w/2. MS = 2: wave w takes the A fragments of m-tile
+    // mb (local fragments w%4 + 8mb, w%4 + 8mb + 4, both K halves), the quants of
+    // K half mb and the same header piece as wave w%4 (a duplicate of identical
+    // bytes, so every wave issues 6 loads). Lane offsets are fixed; stage s of K
+    // half h adds (h·nst + s)·8 KiB (A), ·512 B (quants), ((h·nst + s)/4)·256 B
+    // (headers).
+    constexpr int NJ = 4 / MS;
+    uint32_t a_lo[NJ];
+    int a_f[NJ];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int f = wave + 4 * j;  // m-tile f/8, k-slice (f/2)%4, part f%2
+    for (int j = 0; j < NJ; j++) {
+        const int f = wq + 4 * (MS == 2 ? 2 * mb + j : j);  // m-tile f/8, k-slice (f/2)%4, part f%2
+        a_f[j] = f;
         a_lo[j] = (uint32_t)((((2 * tm + (f >> 3)) * nks + ((f >> 1) & 3)) * 2 + (f & 1)) * 1024 + lane * 16);
     }
-    const int bt = min(n0 / 16 + 2 * wave + (lane >> 5), G.ntiles - 1);
+    const int bt = min(n0 / 16 + 2 * wq + (lane >> 5), G.ntiles - 1);
     const uint32_t b_lo = (uint32_t)(bt * nb * 2048 + (lane & 31) * 16);
-    const int ht = min(n0 / 16 + 4 * (wave & 1) + (lane >> 4), G.ntiles - 1);
+    const int ht = min(n0 / 16 + 4 * (wq & 1) + (lane >> 4), G.ntiles - 1);
     const uint32_t h_lo = (uint32_t)((ht * nb * 16 + (lane & 15)) * 16);
     // buffer resources (loads past an extent read zeros); the per-stage offset goes in
     // the scalar offset, so a load needs no vector address arithmetic
@@ -483,22 +502,24 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(st + h * G3_HALF + (wave + 4 * j) * 1024), 16,
+            for (int j = 0; j < NJ; j++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(st + h * G3_HALF + a_f[j] * 1024), 16,
                                                          a_lo[j], (h * nst + s) * 8192, 0, 0);
         }
 #pragma unroll
-        for (int h = 0; h < 2; h++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(st + h * G3_HALF + G2_A + wave * 1024), 16, b_lo,
+        for (int i = 0; i < 2 / MS; i++) {
+            const int h = MS == 1 ? i : mb;  // (no branch around a load: the wait counts stay exact)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(st + h * G3_HALF + G2_A + wq * 1024), 16, b_lo,
                                                      (h * nst + s) * 512, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, (lds_void*)(st + kh * G3_HALF + G2_A + G2_B + (wave & 1) * 1024),
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, (lds_void*)(st + kh * G3_HALF + G2_A + G2_B + (wq & 1) * 1024),
                                                  16, h_lo, ((kh * nst + s) >> 2) * 256, 0, 0);
     };
 
     // LDS offsets within the wave's K half: A fragment (mt, ks, part) at
     // a_off + (8mt + 2ks + part)·1024; column c's quants (lane (n, kg)) at
     // b_off[c] + 256·kg; its header at h_off[c]
-    const int a_off = kh * G3_HALF + lane * 16;
+    const int a_off = kh * G3_HALF + lane * 16 + mb * 8192;
     int b_off[2], h_off[2];
 #pragma unroll
     for (int c = 0; c < 2; c++) {
@@ -506,23 +527,23 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
         b_off[c] = kh * G3_HALF + G2_A + t * 512 + n * 16 + 8 * (lane >> 5);
         h_off[c] = kh * G3_HALF + G2_A + G2_B + t * 256 + n * 16;
     }
-    const _Float16* s_src[2];
+    const _Float16* s_src[NM];
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
-        const int srow = min(m0 + 32 * mt + (lane & 31), G.m - 1);
+    for (int mt = 0; mt < NM; mt++) {
+        const int srow = min(m0 + 32 * (mb + mt) + (lane & 31), G.m - 1);
         s_src[mt] = ((lane >> 5) ? G.Sl : G.Sh) + (int64_t)srow * (G.k / 32) + kh * hsb * 8;
     }
 
-    f32x16 acc[2][2], part[2][2];
+    f32x16 acc[NM][2], part[NM][2];
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int mt = 0; mt < NM; mt++)
 #pragma unroll
         for (int c = 0; c < 2; c++) {
             acc[mt][c] = (f32x16){};
             part[mt][c] = (f32x16){};
         }
     u32x4 hd[2] = {};
-    half8_t sv[2] = {};
+    half8_t sv[NM] = {};
     uint32_t c64;  // 0x64006400 in a VGPR (see dq8)
     asm("v_mov_b32 %0, 0x64006400" : "=v"(c64));
 
@@ -537,15 +558,16 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
             const uint32_t st = ring_lds + cur * G3_STAGE;
             const int nx = cur == 0 ? 2 : cur - 1;  // slot of stage s + 2 (= slot of s - 1)
             // this wave's loads of stage s have landed (those of s + 1 may be in flight)
-            __builtin_amdgcn_s_waitcnt((G3_LOADS & 15) | (7 << 4) | (15 << 8) | ((G3_LOADS >> 4) << 14));
+            __builtin_amdgcn_s_waitcnt((LOADS & 15) | (7 << 4) | (15 << 8) | ((LOADS >> 4) << 14));
             __builtin_amdgcn_s_barrier();  // every wave's part of stage s is in; slot nx is free
             if (J == 0) {
-                sv[0] = *(const half8_t*)(s_src[0] + b * 8);
-                sv[1] = *(const half8_t*)(s_src[1] + b * 8);
+#pragma unroll
+                for (int mt = 0; mt < NM; mt++) sv[mt] = *(const half8_t*)(s_src[mt] + b * 8);
             }
             issue(s + 2, ring + nx * G3_STAGE);
             cur = cur == 2 ? 0 : cur + 1;
             // LDS reads, one k-slice ahead of the MFMAs, consumed under lgkmcnt
+            // (2·NM A reads per k-slice)
             if (J == 0) {
                 hd[0] = lds_b128<0>(st + h_off[0]);
                 hd[1] = lds_b128<0>(st + h_off[1]);
@@ -554,24 +576,30 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
             raw[0] = lds_2b64_256(st + b_off[0]);
             raw[1] = lds_2b64_256(st + b_off[1]);
             const uint32_t pa = st + a_off;
-            half8_t a[4][2][2];  // [ks][mt][part]
+            half8_t a[4][NM][2];  // [ks][mt][part]
             a[0][0][0] = lds_b128h<0>(pa);
             a[0][0][1] = lds_b128h<1024>(pa);
-            a[0][1][0] = lds_b128h<8192>(pa);
-            a[0][1][1] = lds_b128h<9216>(pa);
+            if constexpr (NM == 2) {
+                a[0][NM - 1][0] = lds_b128h<8192>(pa);
+                a[0][NM - 1][1] = lds_b128h<9216>(pa);
+            }
             a[1][0][0] = lds_b128h<2048>(pa);
             a[1][0][1] = lds_b128h<3072>(pa);
-            a[1][1][0] = lds_b128h<10240>(pa);
-            a[1][1][1] = lds_b128h<11264>(pa);
-            lgkm_wait<4>();
+            if constexpr (NM == 2) {
+                a[1][NM - 1][0] = lds_b128h<10240>(pa);
+                a[1][NM - 1][1] = lds_b128h<11264>(pa);
+            }
+            lgkm_wait<2 * NM>();
             pin(hd[0]);
             pin(hd[1]);
             pin(raw[0]);
             pin(raw[1]);
             a[2][0][0] = lds_b128h<4096>(pa);
             a[2][0][1] = lds_b128h<5120>(pa);
-            a[2][1][0] = lds_b128h<12288>(pa);
-            a[2][1][1] = lds_b128h<13312>(pa);
+            if constexpr (NM == 2) {
+                a[2][NM - 1][0] = lds_b128h<12288>(pa);
+                a[2][NM - 1][1] = lds_b128h<13312>(pa);
+            }
             // scales of sub-blocks 2J (low nibbles) and 2J + 1 (high nibbles), get_scale_min_k4:
             // sp = (sc, sc'/16), zp = (−1024·sc, −64·sc'), used as broadcast halves
             half2_t sp[2], zp[2];
@@ -590,16 +618,18 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
             for (int ks = 0; ks < 4; ks++) {
                 const int nib = ks >> 1, kg = ks & 1;
                 if (ks == 1) {
-                    lgkm_wait<4>();
+                    lgkm_wait<2 * NM>();
                     a[3][0][0] = lds_b128h<6144>(pa);
                     a[3][0][1] = lds_b128h<7168>(pa);
-                    a[3][1][0] = lds_b128h<14336>(pa);
-                    a[3][1][1] = lds_b128h<15360>(pa);
+                    if constexpr (NM == 2) {
+                        a[3][NM - 1][0] = lds_b128h<14336>(pa);
+                        a[3][NM - 1][1] = lds_b128h<15360>(pa);
+                    }
                 }
-                if (ks == 2) lgkm_wait<4>();
+                if (ks == 2) lgkm_wait<2 * NM>();
                 if (ks == 3) lgkm_wait<0>();
 #pragma unroll
-                for (int mt = 0; mt < 2; mt++) {
+                for (int mt = 0; mt < NM; mt++) {
                     pin(a[ks][mt][0]);
                     pin(a[ks][mt][1]);
                 }
@@ -617,7 +647,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
 #pragma unroll
                 for (int p = 0; p < 2; p++)
 #pragma unroll
-                    for (int mt = 0; mt < 2; mt++)
+                    for (int mt = 0; mt < NM; mt++)
 #pragma unroll
                         for (int c = 0; c < 2; c++)
                             part[mt][c] =
@@ -626,7 +656,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
 #if AETH_GEMM_IGLP
             // interleave: each MFMA followed by a few VALU ops (next k-slice's dequantisation)
 #pragma unroll
-            for (int i = 0; i < 32; i++) {
+            for (int i = 0; i < 16 * NM; i++) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, AETH_GEMM_IGLP, 0);
             }
@@ -642,7 +672,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
                     bytes_to_h2(((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u), m45, m67);
                     const half8_t mv = {m01[0], m01[1], m23[0], m23[1], m45[0], m45[1], m67[0], m67[1]};
 #pragma unroll
-                    for (int mt = 0; mt < 2; mt++) {
+                    for (int mt = 0; mt < NM; mt++) {
                         const f32x16 q = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv[mt], mv, (f32x16){}, 0, 0, 0);
 #pragma unroll
                         for (int r = 0; r < 16; r++)
@@ -660,24 +690,24 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
     float* red = (float*)ring + wn * 4096;
     if (kh == 1) {
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++)
+        for (int mt = 0; mt < NM; mt++)
 #pragma unroll
             for (int c = 0; c < 2; c++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) red[((mt * 2 + c) * 16 + r) * 64 + lane] = acc[mt][c][r];
+                for (int r = 0; r < 16; r++) red[(((mb + mt) * 2 + c) * 16 + r) * 64 + lane] = acc[mt][c][r];
     }
     __syncthreads();
     if (kh == 1) return;
     const int lr = lane & 31;
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int mt = 0; mt < NM; mt++)
 #pragma unroll
         for (int c = 0; c < 2; c++) {
             const int col = n0 + 64 * wn + 32 * c + lr;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int row = m0 + 32 * mt + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-                const float sum = acc[mt][c][r] + red[((mt * 2 + c) * 16 + r) * 64 + lane];
+                const int row = m0 + 32 * (mb + mt) + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                const float sum = acc[mt][c][r] + red[(((mb + mt) * 2 + c) * 16 + r) * 64 + lane];
                 if (row < G.m && col < G.n) {
                     const float v = sum * G.escale[row];
                     float* dst = G.C + (int64_t)row * G.ldc + col;
@@ -686,6 +716,9 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) {
             }
         }
 }
+
+__global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) { gemm_sk_body<1>(G); }
+__global__ void __launch_bounds__(512) k_gemm_q4k_sk8(GemmArgs G) { gemm_sk_body<2>(G); }
 
 namespace {
 struct GemmWs {
@@ -739,10 +772,12 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
                (int)std::min(ab, (int64_t)INT32_MAX), (int)std::min(qb, (int64_t)INT32_MAX),
                (int)std::min(hb, (int64_t)INT32_MAX), d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0};
     const bool fits32 = qb < INT32_MAX && ab < INT32_MAX;  // buffer offsets are 32-bit
-    // AETH_GEMM_KERNEL=2 forces the single-K-group kernel (tuning and tests)
+    // AETH_GEMM_KERNEL=2 forces the single-K-group kernel, =3 the 4-wave split-K kernel (tuning and tests)
     static const int env_kernel = getenv("AETH_GEMM_KERNEL") ? atoi(getenv("AETH_GEMM_KERNEL")) : 0;
-    if ((nb & 1) == 0 && fits32 && env_kernel != 2)
+    if ((nb & 1) == 0 && fits32 && env_kernel == 3)
         hipLaunchKernelGGL(k_gemm_q4k_sk, dim3((unsigned)(gm * gn)), dim3(256), 0, s, G);
+    else if ((nb & 1) == 0 && fits32 && env_kernel != 2)
+        hipLaunchKernelGGL(k_gemm_q4k_sk8, dim3((unsigned)(gm * gn)), dim3(512), 0, s, G);
     else
         hipLaunchKernelGGL(k_gemm_q4k_ring, dim3((unsigned)(gm * gn)), dim3(256), 0, s, G);
     AETH_LAUNCH_CHECK();
