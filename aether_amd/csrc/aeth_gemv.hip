@@ -626,7 +626,7 @@ static int mq_dispatch(MqParams G, int64_t m, hipStream_t s) {
     // front (short memory queues, so each wave's tiles arrive early and their
     // compute overlaps the stream); one tile per workgroup when there are no
     // more tiles than CUs; taller matrices use the ring with ~2 workgroups per
-    // CU so the per-workgroup activation conversion stays amortised.
+    // CU (Q6_K: ~4) so the per-workgroup activation conversion stays amortised.
     // Tuning overrides, read once: AETH_GEMV_WAVES (8 | 16), AETH_GEMV_TPW.
     static const int env_w = getenv("AETH_GEMV_WAVES") ? atoi(getenv("AETH_GEMV_WAVES")) : 0;
     static const int env_tpw = getenv("AETH_GEMV_TPW") ? atoi(getenv("AETH_GEMV_TPW")) : 0;
@@ -637,7 +637,9 @@ static int mq_dispatch(MqParams G, int64_t m, hipStream_t s) {
     const int NBW = nbw <= 1 ? 1 : nbw <= 2 ? 2 : nbw <= 4 ? 4 : 8;
     if (nbw > 8) return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d is beyond this kernel's range", G.k);
     const int RD = NBW <= 2 || (W == 8 && NBW == 4 && F != FQ6K) ? 2 : 1;
-    int64_t tpw = G.ntiles <= cus ? 1 : G.ntiles <= 8 * cus ? RD : aeth_cdiv(G.ntiles, 2 * cus);
+    // (Q6_K on the ring: ~4 workgroups per CU, measured 1.5 % faster on the 128256-row LM head)
+    const int64_t wpc = F == FQ6K ? 4 : 2;
+    int64_t tpw = G.ntiles <= cus ? 1 : G.ntiles <= 8 * cus ? RD : aeth_cdiv(G.ntiles, wpc * cus);
     if (env_tpw > 0) tpw = env_tpw;
     if (tpw > MQ_TPW_MAX) tpw = MQ_TPW_MAX;
     G.tpw = (int)tpw;
