@@ -71,6 +71,11 @@ _SIGS = {
     "aeth_registered_kernel_name": (_INT, [_INT, ctypes.c_char_p, _INT]),
     "aeth_dispatch_matmul": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P]),
     "aeth_weight_cache_clear": (_INT, []),
+    "aeth_weight_cache_set_limit": (_INT, [_I64]),
+    "aeth_weight_cache_bytes": (_I64, []),
+    "aeth_backend_rms_norm": (_INT, [_P, _P, _I64, _I64, ctypes.c_float, _P]),
+    "aeth_backend_causal_attention": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_float, _P]),
+    "aeth_causal_attention": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_float, _P, _P]),
     "aeth_rmsnorm": (_INT, [_P, _P, _I64, _I64, ctypes.c_float, _P, _P]),
     "aeth_rope": (_INT, [_P, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "aeth_kv_append": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),

@@ -20,6 +20,7 @@ SOURCES = [
     "aeth_gemm.hip",
     "aeth_decode_ops.hip",
     "aeth_prefill.hip",
+    "aeth_backend.hip",
     "aeth_host.cpp",
     "aeth_runner.cpp",
     "aeth_gguf.cpp",

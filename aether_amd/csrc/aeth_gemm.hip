@@ -720,16 +720,14 @@ __device__ __forceinline__ void gemm_sk_body(const GemmArgs& G) {
 __global__ void __launch_bounds__(256) k_gemm_q4k_sk(GemmArgs G) { gemm_sk_body<1>(G); }
 __global__ void __launch_bounds__(512) k_gemm_q4k_sk8(GemmArgs G) { gemm_sk_body<2>(G); }
 
-namespace {
-struct GemmWs {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-GemmWs g_gemm_ws[64];
-}  // namespace
+int64_t aeth_gemm_ws_bytes(int64_t m, int64_t k) {
+    // fragments [mp][k] × {hi, lo}, Sh, Sl [mp][k/32] (fp16), escale [mp] (f32)
+    const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM;
+    return mp * k * 2 * 2 + mp * (k / 32) * 2 * 2 + mp * 4 + 256;
+}
 
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s, int64_t ldc) {
+                         hipStream_t s, int64_t ldc, void* ws, size_t ws_bytes) {
     const int k = (int)w->k, nb = (int)w->nb;
     if (ldc <= 0) ldc = w->n;
     if (k != nb * 256) {  // ragged K: row-batched GEMV
@@ -740,20 +738,14 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     }
     const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM;  // fragment rows: whole 64-row tiles
     if (mp > (1LL << 20) || mp * k > (1LL << 29)) return aeth_set_error(AETH_EINVAL, "gemm: m=%lld too large", (long long)m);
-    // workspace: fragments [mp][k] × {hi, lo}, Sh, Sl [mp][k/32] (fp16), escale [mp] (f32)
-    const size_t need = (size_t)mp * k * 2 * 2 + (size_t)mp * (k / 32) * 2 * 2 + (size_t)mp * 4 + 256;
-    int dev = 0;
-    AETH_HIP_CHECK(hipGetDevice(&dev));
-    if (dev < 0 || dev >= 64) return aeth_set_error(AETH_EINVAL, "gemm: device index");
-    GemmWs& ws = g_gemm_ws[dev];
-    if (ws.bytes < need) {
-        if (ws.ptr) AETH_HIP_CHECK(hipFree(ws.ptr));
-        ws.ptr = nullptr;
-        ws.bytes = 0;
-        AETH_HIP_CHECK(hipMalloc(&ws.ptr, need));
-        ws.bytes = need;
+    const size_t need = (size_t)aeth_gemm_ws_bytes(m, k);
+    if (ws && ws_bytes < need)
+        return aeth_set_error(AETH_EINVAL, "gemm: workspace of %zu bytes < %zu needed", ws_bytes, need);
+    if (!ws) {
+        int rc = aeth_stream_scratch(s, AETH_SCRATCH_GEMM, need, &ws);
+        if (rc) return rc;
     }
-    _Float16* frag = (_Float16*)ws.ptr;
+    _Float16* frag = (_Float16*)ws;
     _Float16* Sh = frag + (size_t)mp * k * 2;
     _Float16* Sl = Sh + (size_t)mp * (k / 32);
     float* esc = (float*)(Sl + (size_t)mp * (k / 32));

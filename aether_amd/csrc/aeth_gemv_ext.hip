@@ -262,12 +262,6 @@ __global__ void __launch_bounds__(256) k_row(const uint8_t* __restrict__ W, int6
     }
 }
 
-struct XWs {
-    float* ptr = nullptr;
-    int64_t floats = 0;
-};
-XWs g_xws[64];
-
 template <int F>
 int launch_col(const aeth_weight* w, const float* x, int64_t m, float* y, int64_t ldy, const GemvEpi& e,
                float* part, int S, hipStream_t s) {
@@ -353,19 +347,11 @@ int aeth_xgemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* 
     if (ws && e.ws_floats < need)
         return aeth_set_error(AETH_EINVAL, "gemv: scratch of %lld floats < %lld needed", (long long)e.ws_floats,
                               (long long)need);
-    if (!ws) {  // the library's per-device scratch (grow-only)
-        int dev = 0;
-        AETH_HIP_CHECK(hipGetDevice(&dev));
-        if (dev < 0 || dev >= 64) return aeth_set_error(AETH_EINVAL, "gemv: device index");
-        XWs& xw = g_xws[dev];
-        if (xw.floats < need) {
-            if (xw.ptr) AETH_HIP_CHECK(hipFree(xw.ptr));
-            xw.ptr = nullptr;
-            xw.floats = 0;
-            AETH_HIP_CHECK(hipMalloc((void**)&xw.ptr, (size_t)need * sizeof(float)));
-            xw.floats = need;
-        }
-        ws = xw.ptr;
+    if (!ws) {  // the library's scratch of this stream
+        void* p = nullptr;
+        int rc = aeth_stream_scratch(s, AETH_SCRATCH_XGEMV, (size_t)need * sizeof(float), &p);
+        if (rc) return rc;
+        ws = (float*)p;
     }
     float* part = ws;
     const float* x = d_x;

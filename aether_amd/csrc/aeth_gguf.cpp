@@ -179,8 +179,13 @@ int gguf_open(const char* path, Gguf& g) {
         uint64_t be, bb, ne = 1;
         if (!dtype_geometry(t.dtype, &be, &bb))
             return aeth_set_error(AETH_EINVAL, "Unknown tensor dtype: %u (%s)", t.dtype, it.first.c_str());
-        for (uint64_t d : t.shape) ne *= d;
-        t.bytes = (ne + be - 1) / be * bb;  // compute_tensor_byte_size, gguf.rs:539-551
+        // every dimension within int32 and the element and byte counts within uint64:
+        // a wrapped product would let a crafted header pass the bounds check below
+        for (uint64_t d : t.shape)
+            if (d > (uint64_t)INT32_MAX || __builtin_mul_overflow(ne, d, &ne))
+                return aeth_set_error(AETH_EINVAL, "Tensor '%s': shape overflows", it.first.c_str());
+        if (__builtin_mul_overflow((ne + be - 1) / be, bb, &t.bytes))  // compute_tensor_byte_size, gguf.rs:539-551
+            return aeth_set_error(AETH_EINVAL, "Tensor '%s': byte size overflows", it.first.c_str());
         const uint64_t off = start + t.offset;
         if (off > g.len || t.bytes > g.len - off)
             return aeth_set_error(AETH_EINVAL, "Tensor '%s' offset out of bounds", it.first.c_str());
@@ -260,7 +265,8 @@ int load_quant(const Gguf& g, const std::string& name, Staging& st, std::vector<
     if (it == g.tensors.end()) return aeth_set_error(AETH_EINVAL, "Missing tensor: %s", name.c_str());
     const TensorInfo& t = it->second;
     if (t.shape.size() != 2) return aeth_set_error(AETH_EUNSUPPORTED, "tensor %s is not 2-D", name.c_str());
-    const int64_t k = (int64_t)t.shape[0], n = (int64_t)t.shape[1];
+    const int64_t k = (int64_t)t.shape[0], n = (int64_t)t.shape[1];  // each <= INT32_MAX (gguf_open)
+    if (k < 1 || n < 1) return aeth_set_error(AETH_EINVAL, "tensor %s has an empty dimension", name.c_str());
     int be, bb;
     if (aeth_block_geometry((int)t.dtype, &be, &bb) != AETH_OK)
         return aeth_set_error(AETH_EUNSUPPORTED,
@@ -278,14 +284,21 @@ int load_quant(const Gguf& g, const std::string& name, Staging& st, std::vector<
         *k_out = k;
         return AETH_OK;
     }
-    const size_t out_b = (size_t)(n * ((k + be - 1) / be) * bb);
-    if ((rc = Staging::grow(&st.src, &st.src_b, t.bytes)) || (rc = Staging::grow(&st.dst, &st.dst_b, out_b)) ||
-        (rc = Staging::grow(&st.ws, &st.ws_b, (size_t)aeth_load_quant_ws_bytes(k, n))))
+    int64_t out_b = 0, kn = 0;
+    const int64_t ws_b = aeth_load_quant_ws_bytes(k, n);
+    if (!aeth_mul_ok(n, aeth_cdiv(k, be) * bb, &out_b) || !aeth_mul_ok(k, n, &kn) || ws_b < 0)
+        return aeth_set_error(AETH_EINVAL, "tensor %s: [%lld, %lld] is too large", name.c_str(), (long long)k,
+                              (long long)n);
+    if ((uint64_t)kn / (uint64_t)be * (uint64_t)bb > t.bytes)
+        return aeth_set_error(AETH_EINVAL, "tensor %s: %llu bytes for [%lld, %lld]", name.c_str(),
+                              (unsigned long long)t.bytes, (long long)k, (long long)n);
+    if ((rc = Staging::grow(&st.src, &st.src_b, t.bytes)) || (rc = Staging::grow(&st.dst, &st.dst_b, (size_t)out_b)) ||
+        (rc = Staging::grow(&st.ws, &st.ws_b, (size_t)ws_b)))
         return rc;
     AETH_HIP_CHECK(hipMemcpyAsync(st.src, t.data, t.bytes, hipMemcpyHostToDevice, st.s));
     if ((rc = aeth_load_quant((int)t.dtype, st.src, k, n, st.dst, st.ws, st.s))) return rc;
-    out.resize(out_b);
-    AETH_HIP_CHECK(hipMemcpyAsync(out.data(), st.dst, out_b, hipMemcpyDeviceToHost, st.s));
+    out.resize((size_t)out_b);
+    AETH_HIP_CHECK(hipMemcpyAsync(out.data(), st.dst, (size_t)out_b, hipMemcpyDeviceToHost, st.s));
     AETH_HIP_CHECK(hipStreamSynchronize(st.s));
     *dtype = (int)t.dtype;
     *n_out = n;
@@ -359,8 +372,17 @@ int aeth_gguf_load_runner(const char* path, aeth_runner** out, int* bos, int* eo
     auto te = g.tensors.find("token_embd.weight");
     if (te == g.tensors.end() || te->second.shape.size() < 2) return aeth_set_error(AETH_EINVAL, "Cannot determine vocab size");
     const int64_t vocab = (int64_t)te->second.shape[1];
-    if (nh <= 0 || d % nh) return aeth_set_error(AETH_EINVAL, "embedding_length %lld is not a multiple of %lld heads",
-                                                 (long long)d, (long long)nh);
+    // every dimension positive and within int32, so that the products below cannot wrap
+    const int64_t dims[] = {d, nl, nh, nkv, dff, vocab};
+    for (int64_t v : dims)
+        if (v <= 0 || v > INT32_MAX)
+            return aeth_set_error(AETH_EINVAL, "GGUF config: a dimension (%lld) is not in [1, 2^31)", (long long)v);
+    if (nl > 65536 || (d % nh)) return aeth_set_error(AETH_EINVAL, "GGUF config: %lld layers, d %lld, %lld heads",
+                                                       (long long)nl, (long long)d, (long long)nh);
+    int64_t vd = 0;
+    if (!aeth_mul_ok(vocab, d, &vd) || vd > (1LL << 40))
+        return aeth_set_error(AETH_EINVAL, "GGUF config: vocab %lld x d %lld is too large", (long long)vocab,
+                              (long long)d);
     const int64_t hd = d / nh;
     if (meta_usize(g, key("rope.dimension_count"), &rope_dim) && rope_dim != hd)
         return aeth_set_error(AETH_EUNSUPPORTED, "partial RoPE (rope.dimension_count %lld of head_dim %lld) is not built",

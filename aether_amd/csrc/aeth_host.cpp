@@ -4,45 +4,70 @@
 // (src/quant/matmul/dispatch.rs:98-135, avx2_dispatch.rs:58-68).
 #include <hip/hip_runtime.h>
 
+#include <string.h>
+
+#include <algorithm>
 #include <map>
 #include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <tuple>
+#include <vector>
 
 #include "aeth_common.hpp"
 #include "aeth_internal.hpp"
 #include "aeth_ops_internal.hpp"
 
-// ── per-device scratch for the standalone decode-op entry points ─────────
-// One buffer per (device, use); calls that overlap on one device (different
-// host threads or streams) share it and race; the runner uses its own.
+// ── library scratch: one grow-only buffer per (device, stream, use) ───────
+// Work enqueued on one stream runs in order, so calls on the same stream can
+// share a buffer; calls on different streams (runners, host threads) get
+// their own. A grow first waits for the stream (the old buffer may still be
+// read by its kernels) and is refused while the stream is being captured.
 namespace {
-struct Workspace {
+struct Scratch {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
-std::mutex g_ws_mu;
-std::map<std::pair<int, int>, Workspace> g_ws;
-enum { WS_ATTN = 0, WS_ARGMAX = 1 };
+std::mutex g_scratch_mu;
+std::map<std::tuple<int, hipStream_t, int>, Scratch> g_scratch;
+}  // namespace
 
-int workspace(int use, size_t bytes, void** out) {
+int aeth_stream_scratch(hipStream_t s, int use, size_t bytes, void** out) {
     int dev = 0;
     AETH_HIP_CHECK(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace& w = g_ws[std::make_pair(dev, use)];
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    Scratch& w = g_scratch[std::make_tuple(dev, s, use)];
     if (w.bytes < bytes) {
-        if (w.ptr) AETH_HIP_CHECK(hipFree(w.ptr));
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        AETH_HIP_CHECK(hipStreamIsCapturing(s, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return aeth_set_error(AETH_ESTATE, "scratch of %zu bytes would have to be allocated during graph capture "
+                                               "(run the call once before capturing)", bytes);
+        if (w.ptr) {
+            AETH_HIP_CHECK(hipStreamSynchronize(s));
+            AETH_HIP_CHECK(hipFree(w.ptr));
+        }
         w.ptr = nullptr;
         w.bytes = 0;
         AETH_HIP_CHECK(hipMalloc(&w.ptr, bytes));
-        AETH_HIP_CHECK(hipMemset(w.ptr, 0, bytes));
         w.bytes = bytes;
     }
     *out = w.ptr;
     return AETH_OK;
 }
-}  // namespace
+
+void aeth_stream_scratch_release(hipStream_t s) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    for (auto it = g_scratch.begin(); it != g_scratch.end();) {
+        if (std::get<1>(it->first) == s) {
+            if (it->second.ptr) hipFree(it->second.ptr);
+            it = g_scratch.erase(it);
+        } else {
+            ++it;
+        }
+    }
+}
 
 int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
                     hipStream_t s) {
@@ -87,7 +112,8 @@ extern "C" AETH_API int aeth_attn_decode(const float* d_q, const float* d_layer_
         return aeth_set_error(AETH_EINVAL, "aeth_attn_decode: bad argument (seq %lld, max_seq %lld)", (long long)seq,
                               (long long)max_seq);
     void* ws = nullptr;
-    int rc = workspace(WS_ATTN, sizeof(float) * aeth_attn_ws_floats(n_heads, head_dim, max_seq), &ws);
+    int rc = aeth_stream_scratch((hipStream_t)stream, AETH_SCRATCH_ATTN,
+                                 sizeof(float) * aeth_attn_ws_floats(n_heads, head_dim, max_seq), &ws);
     if (rc) return rc;
     return aeth_attn_launch(d_q, nullptr, (float*)d_layer_kv, nullptr, nullptr, nullptr, seq, n_heads, kv_heads,
                             head_dim, max_seq, (float*)ws, d_out, (hipStream_t)stream);
@@ -117,84 +143,222 @@ extern "C" AETH_API int aeth_add(float* d_x, const float* d_y, int64_t n, void* 
 extern "C" AETH_API int aeth_argmax(const float* d_logits, int64_t n, int32_t* d_out, void* stream) {
     if (!d_logits || !d_out) return aeth_set_error(AETH_EINVAL, "aeth_argmax: bad argument");
     void* ws = nullptr;
-    int rc = workspace(WS_ARGMAX, (size_t)aeth_argmax_ws_bytes(), &ws);
+    int rc = aeth_stream_scratch((hipStream_t)stream, AETH_SCRATCH_ARGMAX, (size_t)aeth_argmax_ws_bytes(), &ws);
     if (rc) return rc;
     return aeth_argmax_launch(d_logits, n, d_out, nullptr, ws, (hipStream_t)stream);
 }
 
 // ── host-slice path: QuantWeight bytes → cached device weight ────────────
+// A host-slice call (QuantKernel::matmul semantics: borrowed slices, c fully
+// written) uploads the weight once and keeps the device copy in a cache keyed
+// by (pointer, length, dtype, n, k, device, layout). Every call re-checks the
+// bytes against a 64-bit content fingerprint, so a buffer rewritten in place,
+// or freed and reallocated at the same address, is uploaded again. The cache
+// holds at most aeth_weight_cache_set_limit() device bytes (least recently
+// used weights are dropped first). Calls on one device are serialised; they
+// run on a library stream with reused staging buffers for a and c.
 namespace {
 using WKey = std::tuple<const void*, int64_t, int, int64_t, int64_t, int, int>;  // ptr, len, dtype, n, k, device, order
-std::mutex g_wc_mu;
-std::map<WKey, aeth_weight*> g_wcache;
 
-int cached_weight(const uint8_t* b_raw, int64_t b_len, int dtype, int order, int64_t n, int64_t k, aeth_weight** out) {
+// Content fingerprint: four multiply-rotate lanes over 32-byte steps (a
+// 64-bit mix in the style of the xxHash family), the tail byte-wise, then the
+// length. Buffers past 8 MiB are split into 1 MiB chunks hashed by up to 8
+// host threads and the chunk digests folded in order.
+inline uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
+const uint64_t kP1 = 0x9E3779B185EBCA87ull, kP2 = 0xC2B2AE3D27D4EB4Full, kP3 = 0x165667B19E3779F9ull;
+
+uint64_t fp_chunk(const uint8_t* p, size_t n, uint64_t seed) {
+    uint64_t v[4] = {seed + kP1 + kP2, seed + kP2, seed, seed - kP1};
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int l = 0; l < 4; l++) {
+            uint64_t w;
+            memcpy(&w, p + i + 8 * l, 8);
+            v[l] = rotl64(v[l] + w * kP2, 31) * kP1;
+        }
+    uint64_t h = rotl64(v[0], 1) + rotl64(v[1], 7) + rotl64(v[2], 12) + rotl64(v[3], 18);
+    for (; i < n; i++) h = rotl64(h ^ (p[i] * kP3), 11) * kP1;
+    h ^= (uint64_t)n;
+    h ^= h >> 33;
+    h *= kP2;
+    h ^= h >> 29;
+    h *= kP3;
+    return h ^ (h >> 32);
+}
+
+uint64_t fingerprint(const uint8_t* p, size_t n) {
+    const size_t chunk = 1 << 20;
+    if (n <= ((size_t)8 << 20)) return fp_chunk(p, n, 0);
+    const size_t nc = (n + chunk - 1) / chunk;
+    std::vector<uint64_t> d(nc);
+    const unsigned nt = (unsigned)std::min<size_t>(8, nc);
+    std::vector<std::thread> th;
+    for (unsigned t = 0; t < nt; t++)
+        th.emplace_back([&, t] {
+            for (size_t c = t; c < nc; c += nt) d[c] = fp_chunk(p + c * chunk, std::min(chunk, n - c * chunk), c);
+        });
+    for (auto& x : th) x.join();
+    return fp_chunk((const uint8_t*)d.data(), nc * 8, (uint64_t)n);
+}
+
+struct CacheEntry {
+    std::shared_ptr<aeth_weight> w;
+    uint64_t fp = 0;
+    uint64_t tick = 0;
+};
+std::mutex g_wc_mu;
+std::map<WKey, CacheEntry> g_wcache;
+int64_t g_wc_bytes = 0;                  // device bytes held by the cache
+int64_t g_wc_limit = (int64_t)32 << 30;  // eviction bound
+uint64_t g_wc_tick = 0;
+
+std::shared_ptr<aeth_weight> share(aeth_weight* w) {
+    return std::shared_ptr<aeth_weight>(w, [](aeth_weight* p) { aeth_weight_free(p); });
+}
+
+// Drops least recently used entries until `incoming` more bytes fit (a weight in
+// use by another call stays alive until that call releases it).
+void evict_for(int64_t incoming) {
+    while (!g_wcache.empty() && g_wc_bytes + incoming > g_wc_limit) {
+        auto lru = g_wcache.begin();
+        for (auto it = g_wcache.begin(); it != g_wcache.end(); ++it)
+            if (it->second.tick < lru->second.tick) lru = it;
+        g_wc_bytes -= lru->second.w->bytes;
+        g_wcache.erase(lru);
+    }
+}
+
+int cached_weight(const uint8_t* b_raw, int64_t b_len, int dtype, int order, int64_t n, int64_t k,
+                  std::shared_ptr<aeth_weight>* out) {
     int be, bb;
     int rc = aeth_block_geometry(dtype, &be, &bb);
     if (rc) return rc;
     int64_t need = aeth_weight_raw_bytes(dtype, order, n, k);
+    if (need < 0)
+        return aeth_set_error(AETH_EINVAL, "matmul: bad weight shape [%lld, %lld]", (long long)n, (long long)k);
     if (b_len < need)
         return aeth_set_error(AETH_EINVAL, "weight bytes %lld < %lld needed for [%lld, %lld] dtype %d",
                               (long long)b_len, (long long)need, (long long)n, (long long)k, dtype);
     int dev = 0;
     AETH_HIP_CHECK(hipGetDevice(&dev));
-    WKey key{b_raw, b_len, dtype, n, k, dev, order};
-    std::lock_guard<std::mutex> lk(g_wc_mu);
-    auto it = g_wcache.find(key);
-    if (it != g_wcache.end()) {
-        *out = it->second;
-        return AETH_OK;
+    const WKey key{b_raw, b_len, dtype, n, k, dev, order};
+    const uint64_t fp = fingerprint(b_raw, (size_t)need);
+    {
+        std::lock_guard<std::mutex> lk(g_wc_mu);
+        auto it = g_wcache.find(key);
+        if (it != g_wcache.end()) {
+            if (it->second.fp == fp) {
+                it->second.tick = ++g_wc_tick;
+                *out = it->second.w;
+                return AETH_OK;
+            }
+            g_wc_bytes -= it->second.w->bytes;  // the bytes changed: upload again
+            g_wcache.erase(it);
+        }
     }
     aeth_weight* w = nullptr;
     rc = aeth_weight_create_ex(dtype, order, n, k, b_raw, 0, nullptr, &w);
     if (rc) return rc;
-    g_wcache[key] = w;
-    *out = w;
+    std::shared_ptr<aeth_weight> sw = share(w);
+    std::lock_guard<std::mutex> lk(g_wc_mu);
+    auto it = g_wcache.find(key);
+    if (it != g_wcache.end()) {  // another thread uploaded the same bytes meanwhile
+        g_wc_bytes -= it->second.w->bytes;
+        g_wcache.erase(it);
+    }
+    evict_for(sw->bytes);
+    if (sw->bytes <= g_wc_limit) {
+        g_wcache[key] = CacheEntry{sw, fp, ++g_wc_tick};
+        g_wc_bytes += sw->bytes;
+    }
+    *out = sw;
     return AETH_OK;
 }
 
-// One host-slice matmul: H2D a, launch, D2H c (QuantKernel::matmul semantics:
-// c is fully written). order: how b_raw is laid out — the QuantWeight form
-// (planar for the fused formats, GGUF [k][n] for the others) or [n][k] rows.
-int host_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, int64_t n, int64_t k, int dtype,
-                float* c, int order = -1, unsigned flags = 0) {
+// Per-device state of the host-slice calls: a lock, a non-blocking stream and
+// grow-only staging for a and c.
+struct HostDev {
+    std::mutex mu;
+    hipStream_t s = nullptr;
+    float *da = nullptr, *dc = nullptr;
+    int64_t a_cap = 0, c_cap = 0;
+};
+std::mutex g_hd_mu;
+std::map<int, std::unique_ptr<HostDev>> g_hostdev;
+
+HostDev& host_dev(int dev) {
+    std::lock_guard<std::mutex> lk(g_hd_mu);
+    auto& p = g_hostdev[dev];
+    if (!p) p.reset(new HostDev());
+    return *p;
+}
+
+int grow(float** p, int64_t* cap, int64_t floats) {
+    if (floats <= *cap) return AETH_OK;
+    if (*p) AETH_HIP_CHECK(hipFree(*p));
+    *p = nullptr;
+    *cap = 0;
+    AETH_HIP_CHECK(hipMalloc((void**)p, sizeof(float) * (size_t)floats));
+    *cap = floats;
+    return AETH_OK;
+}
+
+// One host-slice matmul: H2D a, launch, D2H c. order: how b_raw is laid out —
+// the QuantWeight form (planar for the fused formats, GGUF [k][n] for the
+// others) or [n][k] rows.
+int host_matmul_impl(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, int64_t n, int64_t k, int dtype,
+                     float* c, int order, unsigned flags) {
     if (order < 0) order = aeth_dtype_fused(dtype) ? AETH_ORDER_PLANAR : AETH_ORDER_GGUF;
-    if (!a || !b_raw || !c || m <= 0 || n <= 0 || k <= 0)
+    int64_t mk = 0, mn = 0;
+    if (!a || !b_raw || !c || m <= 0 || n <= 0 || k <= 0 || !aeth_mul_ok(m, k, &mk) || !aeth_mul_ok(m, n, &mn))
         return aeth_set_error(AETH_EINVAL, "matmul: bad argument (m=%lld n=%lld k=%lld)", (long long)m, (long long)n,
                               (long long)k);
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
         return aeth_set_error(AETH_EHIP, "matmul: no HIP device available (no CPU fallback in this library)");
-    aeth_weight* w = nullptr;
+    std::shared_ptr<aeth_weight> w;
     int rc = cached_weight(b_raw, b_len, dtype, order, n, k, &w);
     if (rc) return rc;
-    float *da = nullptr, *dc = nullptr;
-    AETH_HIP_CHECK(hipMalloc((void**)&da, sizeof(float) * m * k));
-    hipError_t e = hipMalloc((void**)&dc, sizeof(float) * m * n);
-    if (e != hipSuccess) {
-        hipFree(da);
-        return aeth_set_error(AETH_ENOMEM, "matmul: hipMalloc failed: %s", hipGetErrorString(e));
+    int dev = 0;
+    AETH_HIP_CHECK(hipGetDevice(&dev));
+    HostDev& h = host_dev(dev);
+    std::lock_guard<std::mutex> lk(h.mu);
+    if (!h.s) AETH_HIP_CHECK(hipStreamCreateWithFlags(&h.s, hipStreamNonBlocking));
+    if ((rc = grow(&h.da, &h.a_cap, mk)) || (rc = grow(&h.dc, &h.c_cap, mn))) return rc;
+    AETH_HIP_CHECK(hipMemcpyAsync(h.da, a, sizeof(float) * (size_t)mk, hipMemcpyHostToDevice, h.s));
+    if ((rc = aeth_qmatmul(w.get(), h.da, m, h.dc, flags, h.s))) {
+        hipStreamSynchronize(h.s);
+        return rc;
     }
-    e = hipMemcpy(da, a, sizeof(float) * m * k, hipMemcpyHostToDevice);
-    if (e == hipSuccess) {
-        rc = aeth_qmatmul(w, da, m, dc, flags, nullptr);
-        if (rc == AETH_OK) {
-            e = hipMemcpy(c, dc, sizeof(float) * m * n, hipMemcpyDeviceToHost);
-        }
-    }
-    hipFree(da);
-    hipFree(dc);
-    if (rc) return rc;
-    if (e != hipSuccess) return aeth_set_error(AETH_EHIP, "matmul: copy failed: %s", hipGetErrorString(e));
+    AETH_HIP_CHECK(hipMemcpyAsync(c, h.dc, sizeof(float) * (size_t)mn, hipMemcpyDeviceToHost, h.s));
+    AETH_HIP_CHECK(hipStreamSynchronize(h.s));
     return AETH_OK;
+}
+
+int host_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, int64_t n, int64_t k, int dtype,
+                float* c, int order = -1, unsigned flags = 0) {
+    return aeth_guard("matmul", [&] { return host_matmul_impl(a, m, b_raw, b_len, n, k, dtype, c, order, flags); });
 }
 }  // namespace
 
 extern "C" AETH_API int aeth_weight_cache_clear(void) {
     std::lock_guard<std::mutex> lk(g_wc_mu);
-    for (auto& kv : g_wcache) aeth_weight_free(kv.second);
-    g_wcache.clear();
+    g_wcache.clear();  // weights still in use by a running call are freed when it ends
+    g_wc_bytes = 0;
     return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_weight_cache_set_limit(int64_t max_bytes) {
+    if (max_bytes < 0) return aeth_set_error(AETH_EINVAL, "aeth_weight_cache_set_limit: negative limit");
+    std::lock_guard<std::mutex> lk(g_wc_mu);
+    g_wc_limit = max_bytes;
+    evict_for(0);
+    return AETH_OK;
+}
+
+extern "C" AETH_API int64_t aeth_weight_cache_bytes(void) {
+    std::lock_guard<std::mutex> lk(g_wc_mu);
+    return g_wc_bytes;
 }
 
 // ── QuantKernel registry (registry.rs:7-63) ──────────────────────────────
@@ -266,12 +430,14 @@ int dispatch_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_l
 }  // namespace aeth
 
 extern "C" AETH_API int aeth_register_hip_kernels(void) {
-    for (int dt : {AETH_DTYPE_F32, AETH_DTYPE_F16, AETH_DTYPE_Q8_0, AETH_DTYPE_Q2_K, AETH_DTYPE_Q3_K, AETH_DTYPE_Q4_K,
-                   AETH_DTYPE_Q5_K, AETH_DTYPE_Q6_K}) {
-        int rc = aeth::register_kernel(std::unique_ptr<aeth::QuantKernel>(new aeth::HipQuantKernel(dt)));
-        if (rc) return rc;
-    }
-    return AETH_OK;
+    return aeth_guard("aeth_register_hip_kernels", [] {
+        for (int dt : {AETH_DTYPE_F32, AETH_DTYPE_F16, AETH_DTYPE_Q8_0, AETH_DTYPE_Q2_K, AETH_DTYPE_Q3_K,
+                       AETH_DTYPE_Q4_K, AETH_DTYPE_Q5_K, AETH_DTYPE_Q6_K}) {
+            int rc = aeth::register_kernel(std::unique_ptr<aeth::QuantKernel>(new aeth::HipQuantKernel(dt)));
+            if (rc) return rc;
+        }
+        return (int)AETH_OK;
+    });
 }
 
 extern "C" AETH_API int aeth_registered_kernel_name(int dtype, char* buf, int buf_len) {
@@ -284,7 +450,7 @@ extern "C" AETH_API int aeth_registered_kernel_name(int dtype, char* buf, int bu
 
 extern "C" AETH_API int aeth_dispatch_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, int64_t n,
                                              int64_t k, int dtype, float* c) {
-    return aeth::dispatch_matmul(a, m, b_raw, b_len, n, k, dtype, c);
+    return aeth_guard("aeth_dispatch_matmul", [&] { return aeth::dispatch_matmul(a, m, b_raw, b_len, n, k, dtype, c); });
 }
 
 // quantized_matmul_impl (dispatch.rs:98-135): registered kernel first; with
@@ -294,7 +460,7 @@ extern "C" AETH_API int aeth_dispatch_matmul(const float* a, int64_t m, const ui
 // reads them (dispatch.rs:126-133).
 extern "C" AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
                                                    int64_t n, int64_t k, int dtype, float* c) {
-    int rc = aeth::dispatch_matmul(a, m, b_raw, b_len, n, k, dtype, c);
+    int rc = aeth_guard("quantized_matmul_impl", [&] { return aeth::dispatch_matmul(a, m, b_raw, b_len, n, k, dtype, c); });
     if (rc == 1) return AETH_OK;
     if (rc < 0) return rc;
     int be, bb;

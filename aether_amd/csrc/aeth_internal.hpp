@@ -3,7 +3,36 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <exception>
+#include <new>
+
 #include "../../include/aether_hip.h"
+
+int aeth_set_error(int code, const char* fmt, ...);
+
+// Runs an entry point's body so that no C++ exception crosses the C ABI: an
+// allocation failure of the host containers becomes AETH_ENOMEM, anything
+// else AETH_EINVAL, with the message in aeth_last_error().
+template <class F>
+int aeth_guard(const char* what, F&& body) noexcept {
+    try {
+        return body();
+    } catch (const std::bad_alloc&) {
+        return aeth_set_error(AETH_ENOMEM, "%s: out of host memory", what);
+    } catch (const std::exception& e) {
+        return aeth_set_error(AETH_EINVAL, "%s: %s", what, e.what());
+    } catch (...) {
+        return aeth_set_error(AETH_EINVAL, "%s: unexpected exception", what);
+    }
+}
+
+// a·b for non-negative sizes; false (and *out untouched) on overflow of int64.
+inline bool aeth_mul_ok(int64_t a, int64_t b, int64_t* out) {
+    int64_t r;
+    if (a < 0 || b < 0 || __builtin_mul_overflow(a, b, &r)) return false;
+    *out = r;
+    return true;
+}
 
 // How a weight's bytes are held on the device.
 enum {
@@ -70,7 +99,7 @@ struct GemvEpi {
     unsigned long long* amax = nullptr;   // fused greedy argmax key
     int64_t ldc = 0;                      // output row stride for m > 1 (0: the output width)
     float* ws = nullptr;                  // GGUF-order weights: scratch of ws_floats floats
-    int64_t ws_floats = 0;                //   (NULL: the library's per-device scratch)
+    int64_t ws_floats = 0;                //   (NULL: the library's scratch of the launch stream)
 };
 
 // GEMV on one activation row per launch-row (a: [m][k] f32, c: [m][n]).
@@ -87,10 +116,21 @@ int aeth_xgemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* 
 int64_t aeth_xgemv_ws_floats(const aeth_weight* w, int64_t m);
 // Q4_K prefill GEMM (m > 1); ldc = output row stride (0: n).
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s, int64_t ldc = 0);
+                         hipStream_t s, int64_t ldc = 0, void* ws = nullptr, size_t ws_bytes = 0);
 // aeth_qmatmul with an output row stride (rows of c are ldc floats apart).
 int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
                     hipStream_t s);
+
+// Library scratch (aeth_host.cpp): a grow-only device buffer per (device,
+// stream, use) for calls that bring no workspace of their own. Calls on one
+// stream share it (their kernels run in order); a grow waits for the stream
+// and is refused during graph capture.
+enum { AETH_SCRATCH_GEMM = 0, AETH_SCRATCH_XGEMV = 1, AETH_SCRATCH_ATTN = 2, AETH_SCRATCH_ARGMAX = 3 };
+int aeth_stream_scratch(hipStream_t s, int use, size_t bytes, void** out);
+// Frees every scratch buffer of stream s (before the stream is destroyed).
+void aeth_stream_scratch_release(hipStream_t s);
+// Bytes of GEMM scratch (A fragments, sub-block sums, row scales) for m rows of k.
+int64_t aeth_gemm_ws_bytes(int64_t m, int64_t k);
 
 // GGUF file → runner (aeth_gguf.cpp): LlamaModel::from_gguf on the device load path.
 struct aeth_runner;

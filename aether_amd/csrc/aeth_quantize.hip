@@ -293,7 +293,9 @@ extern "C" AETH_API int aeth_transpose_f32(const float* d_src, int64_t rows, int
 
 extern "C" AETH_API int64_t aeth_load_quant_ws_bytes(int64_t k, int64_t n) {
     if (k <= 0 || n <= 0) return 0;
-    return 2 * k * n * (int64_t)sizeof(float);
+    int64_t kn = 0;
+    if (!aeth_mul_ok(k, n, &kn) || kn > INT64_MAX / 8) return -1;  // too large for any device
+    return 2 * kn * (int64_t)sizeof(float);
 }
 
 // load_quant for a 2-D quantized tensor, model_loader.rs:330-386: GGUF shape

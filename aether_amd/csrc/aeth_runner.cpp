@@ -152,6 +152,7 @@ uint64_t mix(uint64_t seed, uint64_t a, uint64_t b) {
 
 void runner_release(aeth_runner* r) {
     if (!r) return;
+    if (r->stream) hipStreamSynchronize(r->stream);  // nothing in flight reads what is freed below
     if (r->graph) hipGraphExecDestroy(r->graph);
     for (auto* w : r->wqkv) aeth_weight_free(w);
     for (auto* w : r->wo) aeth_weight_free(w);
@@ -165,7 +166,10 @@ void runner_release(aeth_runner* r) {
                     r->p_x, r->p_n, r->p_qkv, r->p_att, r->p_gu, r->p_h, r->p_tok};
     for (void* b : bufs)
         if (b) hipFree(b);
-    if (r->stream) hipStreamDestroy(r->stream);
+    if (r->stream) {
+        aeth_stream_scratch_release(r->stream);  // the GEMM / GGUF-order scratch of this runner's stream
+        hipStreamDestroy(r->stream);
+    }
     delete r;
 }
 
@@ -361,10 +365,18 @@ int check_step_args(aeth_runner* r, int token, int pos) {
 
 }  // namespace
 
-extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const void* const* layer_weights,
-                                           const int32_t* layer_dtypes, const float* const* norms,
-                                           const float* final_norm, const void* lm_head, int32_t lm_dtype,
-                                           const float* embeddings, uint64_t seed, aeth_runner** out) {
+namespace {
+// Releases a half-built runner on every early return or exception.
+struct RunnerHold {
+    aeth_runner* r = nullptr;
+    ~RunnerHold() {
+        if (r) runner_release(r);
+    }
+};
+
+int runner_create_impl(const aeth_llama_config* cfg, const void* const* layer_weights, const int32_t* layer_dtypes,
+                       const float* const* norms, const float* final_norm, const void* lm_head, int32_t lm_dtype,
+                       const float* embeddings, uint64_t seed, aeth_runner** out) {
     if (!cfg || !out || !layer_dtypes) return aeth_set_error(AETH_EINVAL, "aeth_runner_create: NULL argument");
     *out = nullptr;
     const aeth_llama_config& c = *cfg;
@@ -378,20 +390,18 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
     bool need_seed = !lm_head || !embeddings || !final_norm || !layer_weights || !norms;
     if (need_seed && seed == 0)
         return aeth_set_error(AETH_EINVAL, "aeth_runner_create: missing tensors need a nonzero synthetic_seed");
-    aeth_runner* r = new aeth_runner();
+    RunnerHold hold;
+    aeth_runner* r = hold.r = new aeth_runner();
     r->cfg = c;
     int rc = AETH_OK;
 #define RC(expr)                        \
     do {                                \
         if ((rc = (expr)) != AETH_OK) { \
-            runner_release(r);          \
             return rc;                  \
         }                               \
     } while (0)
-    if (hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking) != hipSuccess) {
-        delete r;
+    if (hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking) != hipSuccess)
         return aeth_set_error(AETH_EHIP, "aeth_runner_create: stream creation failed");
-    }
     hipStream_t s = r->stream;
     (void)aeth_num_cus();  // cache the device query outside any graph capture
     const int64_t d = c.d_model, qd = (int64_t)c.num_heads * c.head_dim, kvd = kKvd(c), dff = c.d_ff;
@@ -441,7 +451,6 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
             for (int j = 0; j < 2; j++)
                 if (hipMemcpy(r->norms + ((int64_t)l * 2 + j) * d, norms[l * 2 + j], sizeof(float) * d,
                               hipMemcpyHostToDevice) != hipSuccess) {
-                    runner_release(r);
                     return aeth_set_error(AETH_EHIP, "runner: norm upload failed");
                 }
     } else {
@@ -449,7 +458,6 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
     }
     if (final_norm) {
         if (hipMemcpy(r->final_norm, final_norm, sizeof(float) * d, hipMemcpyHostToDevice) != hipSuccess) {
-            runner_release(r);
             return aeth_set_error(AETH_EHIP, "runner: final norm upload failed");
         }
     } else {
@@ -458,7 +466,6 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
     if (embeddings) {
         if (hipMemcpy(r->emb, embeddings, sizeof(float) * (size_t)c.vocab_size * d, hipMemcpyHostToDevice) !=
             hipSuccess) {
-            runner_release(r);
             return aeth_set_error(AETH_EHIP, "runner: embedding upload failed");
         }
     } else {
@@ -470,12 +477,10 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
     RC(dmalloc(&r->rope_cos, (int64_t)rcs.size()));
     if (hipMemcpy(r->rope_sin, rs.data(), rs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(r->rope_cos, rcs.data(), rcs.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
-        runner_release(r);
         return aeth_set_error(AETH_EHIP, "runner: rope upload failed");
     }
     RC(dmalloc(&r->kv, (int64_t)c.num_layers * kv_layer_floats(c)));
     if (hipMemsetAsync(r->kv, 0, sizeof(float) * (size_t)c.num_layers * kv_layer_floats(c), s) != hipSuccess) {
-        runner_release(r);
         return aeth_set_error(AETH_EHIP, "runner: kv clear failed");
     }
     RC(dmalloc(&r->x, d));
@@ -487,24 +492,33 @@ extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const v
     RC(dmalloc(&r->attn_ws, aeth_attn_ws_floats(c.num_heads, c.head_dim, c.max_seq_len)));
     if (hipMemset(r->attn_ws, 0, sizeof(float) * aeth_attn_ws_floats(c.num_heads, c.head_dim, c.max_seq_len)) !=
         hipSuccess) {
-        runner_release(r);
         return aeth_set_error(AETH_EHIP, "runner: workspace clear failed");
     }
     RC(dmalloc(&r->amax, 1));
     if (hipMemset(r->amax, 0, sizeof(unsigned long long)) != hipSuccess) {
-        runner_release(r);
         return aeth_set_error(AETH_EHIP, "runner: argmax slot clear failed");
     }
     RC(dmalloc((uint8_t**)&r->am_ws, aeth_argmax_ws_bytes()));
     RC(dmalloc(&r->st, 5));
     RC(dmalloc(&r->tok_out, c.max_seq_len));
     if (hipStreamSynchronize(s) != hipSuccess) {
-        runner_release(r);
         return aeth_set_error(AETH_EHIP, "runner: setup sync failed");
     }
 #undef RC
+    hold.r = nullptr;
     *out = r;
     return AETH_OK;
+}
+}  // namespace
+
+extern "C" AETH_API int aeth_runner_create(const aeth_llama_config* cfg, const void* const* layer_weights,
+                                           const int32_t* layer_dtypes, const float* const* norms,
+                                           const float* final_norm, const void* lm_head, int32_t lm_dtype,
+                                           const float* embeddings, uint64_t seed, aeth_runner** out) {
+    return aeth_guard("aeth_runner_create", [&] {
+        return runner_create_impl(cfg, layer_weights, layer_dtypes, norms, final_norm, lm_head, lm_dtype, embeddings,
+                                  seed, out);
+    });
 }
 
 extern "C" AETH_API int aeth_runner_free(aeth_runner* r) {
@@ -630,7 +644,7 @@ extern "C" AETH_API int aeth_runner_generate(aeth_runner* r, int32_t token, int3
     return AETH_OK;
 }
 
-extern "C" AETH_API int aeth_runner_export(const aeth_runner* r, int which, int32_t l, void* host, int64_t host_bytes) {
+static int runner_export_impl(const aeth_runner* r, int which, int32_t l, void* host, int64_t host_bytes) {
     if (!r || !host) return aeth_set_error(AETH_EINVAL, "aeth_runner_export: NULL");
     const aeth_llama_config& c = r->cfg;
     const int64_t d = c.d_model, qd = (int64_t)c.num_heads * c.head_dim, kvd = kKvd(c), dff = c.d_ff;
@@ -684,6 +698,10 @@ extern "C" AETH_API int aeth_runner_export(const aeth_runner* r, int which, int3
     return AETH_OK;
 }
 
+extern "C" AETH_API int aeth_runner_export(const aeth_runner* r, int which, int32_t l, void* host, int64_t host_bytes) {
+    return aeth_guard("aeth_runner_export", [&] { return runner_export_impl(r, which, l, host, host_bytes); });
+}
+
 // ── aether.h C ABI (src/c_api.rs) over the device runner ─────────────────
 
 struct aether_model {
@@ -694,7 +712,9 @@ struct aether_model {
 
 extern "C" AETHER_API aether_model* aether_model_from_runner(aeth_runner* r) {
     if (!r) return nullptr;
-    return new aether_model{r, 0.0f, 1, 2};
+    aether_model* m = new (std::nothrow) aether_model{r, 0.0f, 1, 2};
+    if (!m) aeth_set_error(AETH_ENOMEM, "aether_model_from_runner: out of host memory");
+    return m;
 }
 
 // aether_load (c_api.rs:41-74): GGUF file → device runner (aeth_gguf.cpp);
@@ -702,8 +722,14 @@ extern "C" AETHER_API aether_model* aether_model_from_runner(aeth_runner* r) {
 extern "C" AETHER_API aether_model* aether_load(const char* path) {
     aeth_runner* r = nullptr;
     int bos = 1, eos = 2;
-    if (aeth_gguf_load_runner(path, &r, &bos, &eos) != AETH_OK) return nullptr;
-    return new aether_model{r, 0.0f, bos, eos};
+    if (aeth_guard("aether_load", [&] { return aeth_gguf_load_runner(path, &r, &bos, &eos); }) != AETH_OK)
+        return nullptr;
+    aether_model* m = new (std::nothrow) aether_model{r, 0.0f, bos, eos};
+    if (!m) {
+        aeth_runner_free(r);
+        aeth_set_error(AETH_ENOMEM, "aether_load: out of host memory");
+    }
+    return m;
 }
 
 // aether_load_streaming (c_api.rs:76-102) keeps max_hot decoder layers resident on

@@ -71,7 +71,9 @@ int64_t aeth_blocks_per_row(int dtype, int64_t k) {
 
 int64_t aeth_weight_raw_bytes(int dtype, int order, int64_t n, int64_t k) {
     int be, bb;
-    if (aeth_block_geometry(dtype, &be, &bb) != AETH_OK || n <= 0 || k <= 0) return -1;
+    // n, k within int32 (the kernels index rows and columns in 32 bits) and no product past int64
+    if (aeth_block_geometry(dtype, &be, &bb) != AETH_OK || n <= 0 || k <= 0 || n > INT32_MAX || k > INT32_MAX)
+        return -1;
     if (order == AETH_ORDER_GGUF) return (n * k / be) * bb;  // dequantize's flat run of whole blocks
     return n * aeth_blocks_per_row(dtype, k) * bb;
 }
@@ -181,7 +183,10 @@ static int create_raw(int dtype, int order, int64_t n, int64_t k, const void* ra
         return aeth_set_error(AETH_EUNSUPPORTED, "row-order F16 weights need k %% 4 == 0 (k=%lld)", (long long)k);
     if (order == AETH_ORDER_ROWS && dtype == AETH_DTYPE_F32)
         return aeth_set_error(AETH_EUNSUPPORTED, "row-order F32 weights are not a kernel of this build");
-    aeth_weight* w = new aeth_weight();
+    if (bytes < 0) return aeth_set_error(AETH_EINVAL, "aeth_weight_create: bad shape n=%lld k=%lld", (long long)n,
+                                         (long long)k);
+    aeth_weight* w = new (std::nothrow) aeth_weight();
+    if (!w) return aeth_set_error(AETH_ENOMEM, "aeth_weight_create: out of host memory");
     w->dtype = dtype;
     w->order = order;
     w->n = n;
@@ -225,7 +230,11 @@ int aeth_weight_create_ex(int dtype, int order, int64_t n, int64_t k, const void
         return aeth_set_error(AETH_EUNSUPPORTED, "aeth_weight_create: dtype %d has no planar layout", dtype);
     if (dtype != AETH_DTYPE_Q8_0 && k < 256)
         return aeth_set_error(AETH_EINVAL, "aeth_weight_create: K-quant needs k >= 256 (k=%lld)", (long long)k);
-    aeth_weight* w = new aeth_weight();
+    if (n > INT32_MAX || k > INT32_MAX)
+        return aeth_set_error(AETH_EINVAL, "aeth_weight_create: shape n=%lld k=%lld beyond int32", (long long)n,
+                              (long long)k);
+    aeth_weight* w = new (std::nothrow) aeth_weight();
+    if (!w) return aeth_set_error(AETH_ENOMEM, "aeth_weight_create: out of host memory");
     w->dtype = dtype;
     w->order = AETH_ORDER_PLANAR;
     w->n = n;

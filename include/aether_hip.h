@@ -113,7 +113,8 @@ AETH_API int aeth_transpose_f32(const float* d_src, int64_t rows, int64_t cols, 
  * tensor on the device: GGUF bytes of shape [k, n] → dequantize → transpose
  * → requantize, giving [n][k] row blocks in d_dst (n·ceil(k/bs)·block_bytes
  * bytes, the layout aeth_weight_create takes). d_ws holds
- * aeth_load_quant_ws_bytes(k, n) bytes. Q8_0, Q4_K, Q5_K and Q6_K (the
+ * aeth_load_quant_ws_bytes(k, n) bytes (-1 when k·n is too large to size).
+ * Q8_0, Q4_K, Q5_K and Q6_K (the
  * formats is_quantized_type_supported names, model_loader.rs:362-367). */
 AETH_API int64_t aeth_load_quant_ws_bytes(int64_t k, int64_t n);
 AETH_API int aeth_load_quant(int dtype, const void* d_src, int64_t k, int64_t n, void* d_dst, void* d_ws,
@@ -124,18 +125,21 @@ AETH_API int aeth_load_quant(int dtype, const void* d_src, int64_t k, int64_t n,
  * (src/quant/matmul/dispatch.rs:98-135) with device operands. m == 1 runs the
  * decode GEMV; m > 1 runs the prefill GEMM (Q4_K: fp16-split MFMA; other
  * fused formats: row-batched GEMV). F32 / F16 / Q2_K / Q3_K weights take the
- * GGUF-order kernel of matmul_f32_gguf (dispatch.rs:541-574), which uses a
- * per-device scratch buffer of the library: concurrent calls on different
- * streams of one device must not overlap. */
+ * GGUF-order kernel of matmul_f32_gguf (dispatch.rs:541-574). The Q4_K GEMM
+ * and the GGUF-order kernel use a scratch buffer the library keeps per
+ * (device, stream): calls on different streams never share it, calls on one
+ * stream run in order. It grows on first use of a larger shape (a grow waits
+ * for the stream and fails with AETH_ESTATE during graph capture: run the
+ * shape once before capturing). Several host threads enqueueing on the same
+ * stream at once must serialise their calls. */
 AETH_API int aeth_qmatmul(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                           void* stream);
 
 /* Same, on GGUF bytes and host slices: quantized_matmul_impl
  * (dispatch.rs:98-106) with b_shape = [n, k] — every format above, with the
- * byte order of aeth_weight_create. The weight bytes are uploaded
- * once and cached by (pointer, length, dtype, n, k) — the bytes must stay
- * immutable while cached, as QuantWeight.data is (gguf.rs:177-277); a, c are
- * copied per call. Fails (no CPU fallback) if no device is usable. */
+ * byte order of aeth_weight_create. The weight bytes are uploaded once and
+ * cached (see aeth_weight_cache_clear); a and c are copied per call. Calls on
+ * one device are serialised. Fails (no CPU fallback) if no device is usable. */
 AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
                                         int64_t n, int64_t k, int dtype, float* c);
 /* quantized_matmul_impl as an aarch64 host with dotprod runs it
@@ -175,8 +179,17 @@ AETH_API int aeth_register_hip_kernels(void);
 AETH_API int aeth_registered_kernel_name(int dtype, char* buf, int buf_len);
 AETH_API int aeth_dispatch_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, int64_t n,
                                   int64_t k, int dtype, float* c);
-/* Drops every cached host-slice weight (frees device memory). */
+/* The host-slice weight cache (no counterpart in the reference, whose
+ * QuantKernel::matmul reads b_raw on every call): entries are keyed by
+ * (pointer, length, dtype, n, k, device) and every hit is re-checked against a
+ * 64-bit fingerprint of the bytes, so a buffer rewritten in place or
+ * reallocated at the same address is uploaded again. clear drops every entry;
+ * set_limit bounds the device bytes held (least recently used entries go
+ * first; default 32 GiB; a weight larger than the limit is not kept);
+ * cache_bytes reports the bytes held. */
 AETH_API int aeth_weight_cache_clear(void);
+AETH_API int aeth_weight_cache_set_limit(int64_t max_bytes);
+AETH_API int64_t aeth_weight_cache_bytes(void);
 
 /* rmsnorm_inplace (runner.rs:1739-1746) on `rows` rows of n: out = x/rms*w. */
 AETH_API int aeth_rmsnorm(const float* d_x, const float* d_w, int64_t rows, int64_t n, float eps,
@@ -209,6 +222,28 @@ AETH_API int aeth_add(float* d_x, const float* d_y, int64_t n, void* stream);
 /* Greedy sample (runner.rs:1964-1973; aether_argmax c_api.rs:384-396):
  * index of the maximum, the LAST one on ties; result written to d_out. */
 AETH_API int aeth_argmax(const float* d_logits, int64_t n, int32_t* d_out, void* stream);
+
+/* ── device trait Backend (src/backend/mod.rs:12-218) ─────────────────────
+ * The decode-path ops of the reference's Backend, which a Rust
+ * `impl Backend for HipBackend` binds (its execute() matches Op::RmsNorm and
+ * Op::CausalAttention and returns an error for every other op — there is no
+ * CPU fallback, unlike CudaBackend::execute, src/backend/cuda.rs:60-64).
+ * Host slices in and out (Tensor data), synchronous. */
+/* Backend::rms_norm → Op::RmsNorm { epsilon } (cpu.rs:514-545): x holds
+ * rows·last_dim f32 ([..., last_dim] flattened), w last_dim; per row
+ * out = (x / sqrt(Σx²/last_dim + eps)) · w. */
+AETH_API int aeth_backend_rms_norm(const float* x, const float* w, int64_t rows, int64_t last_dim, float eps,
+                                   float* out);
+/* Backend::causal_attention → Op::CausalAttention { scale, num_heads }
+ * (mod.rs:209-218, cpu.rs:1660-1727): q, k, v, out are [batch][seq][d] f32;
+ * head h owns columns [h·hd, (h+1)·hd), hd = d / num_heads (columns past
+ * num_heads·hd are 0); query i attends to keys 0..i with softmax((q·k)·scale).
+ * head_dim up to 256; num_heads == 0 is AETH_EINVAL (the reference panics). */
+AETH_API int aeth_backend_causal_attention(const float* q, const float* k, const float* v, int64_t batch,
+                                           int64_t seq, int64_t d, int64_t num_heads, float scale, float* out);
+/* The same attention on device pointers, asynchronous on `stream`. */
+AETH_API int aeth_causal_attention(const float* d_q, const float* d_k, const float* d_v, int64_t batch, int64_t seq,
+                                   int64_t d, int64_t num_heads, float scale, float* d_out, void* stream);
 
 /* ── synthetic inputs (generated on the device, counter-based, seeded) ───
  * Raw GGUF blocks as the benchmark configs describe them:

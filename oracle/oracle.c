@@ -850,17 +850,36 @@ static void orc_qmatmul(int dtype, const float* a, const uint8_t* w, size_t n, s
  * norms[l*2 + {0,1}] = attn_norm, ffn_norm; kv = StaticKVCache storage
  * [L][2][kv_heads][max_seq][hd] (kv_cache.rs:9-31); *seq_len is the cache's
  * fill and is advanced on return. x holds the token's embedding row. */
+ORC_API int orc_decode_step_from(const orc_llama_cfg* cfg, const float* x_embed, int32_t pos, int32_t start_layer,
+                                 const uint8_t* const* weights, const int32_t* wdtype,
+                                 const float* const* norms, const float* final_norm,
+                                 const uint8_t* lm_head, int32_t lm_dtype, const float* rope_sin,
+                                 const float* rope_cos, float* kv, int32_t* seq_len, float* logits);
+
 ORC_API int orc_decode_step(const orc_llama_cfg* cfg, const float* x_embed, int32_t pos,
                             const uint8_t* const* weights, const int32_t* wdtype,
                             const float* const* norms, const float* final_norm,
                             const uint8_t* lm_head, int32_t lm_dtype, const float* rope_sin,
                             const float* rope_cos, float* kv, int32_t* seq_len, float* logits) {
+    return orc_decode_step_from(cfg, x_embed, pos, 0, weights, wdtype, norms, final_norm, lm_head, lm_dtype,
+                                rope_sin, rope_cos, kv, seq_len, logits);
+}
+
+/* The same step entered at layer start_layer with x = the residual stream
+ * after the layers before it: the resume of a budgeted decode
+ * (forward_one_internal's start_layer = completed + 1 with the saved
+ * partial.x, runner.rs:1201-1217). start_layer 0 is the plain step. */
+ORC_API int orc_decode_step_from(const orc_llama_cfg* cfg, const float* x_embed, int32_t pos, int32_t start_layer,
+                                 const uint8_t* const* weights, const int32_t* wdtype,
+                                 const float* const* norms, const float* final_norm,
+                                 const uint8_t* lm_head, int32_t lm_dtype, const float* rope_sin,
+                                 const float* rope_cos, float* kv, int32_t* seq_len, float* logits) {
     size_t d = (size_t)cfg->d_model, hd = (size_t)cfg->head_dim, nh = (size_t)cfg->n_heads;
     size_t nkv = (size_t)cfg->n_kv_heads, dff = (size_t)cfg->d_ff, ms = (size_t)cfg->max_seq;
     size_t kvd = nkv * hd;
     /* the reference's append() refuses a full cache and attn_direct would then
      * index past max_seq (a panic in Rust); report it instead. */
-    if (*seq_len < 0 || (size_t)*seq_len >= ms) return -2;
+    if (*seq_len < 0 || (size_t)*seq_len >= ms || start_layer < 0) return -2;
     float* x = malloc(d * 4);
     float* normed = malloc(d * 4);
     float* q = malloc(nh * hd * 4);
@@ -874,7 +893,7 @@ ORC_API int orc_decode_step(const orc_llama_cfg* cfg, const float* x_embed, int3
     if (!x || !normed || !q || !kk || !vv || !attn || !proj || !gate || !up || !scores) return -1;
     memcpy(x, x_embed, d * 4);
     size_t head_stride = ms * hd, layer_stride = 2 * nkv * head_stride;
-    for (int32_t l = 0; l < cfg->n_layers; l++) {
+    for (int32_t l = start_layer; l < cfg->n_layers; l++) {
         const uint8_t* const* W = weights + (size_t)l * 7;
         const int32_t* T = wdtype + (size_t)l * 7;
         orc_rmsnorm(x, norms[l * 2], d, cfg->eps, normed);

@@ -17,7 +17,7 @@ _lib = None
 F32, F16, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 1, 8, 10, 11, 12, 13, 14
 BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
 BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
-_SOURCES = ("oracle.c", "oracle_formats.c", "oracle.h", "Makefile")
+_SOURCES = ("oracle.c", "oracle_formats.c", "oracle_backend.c", "oracle.h", "Makefile")
 
 
 def build(force=False):
@@ -47,6 +47,8 @@ def lib():
         L.orc_argmax.restype = ctypes.c_int32
         L.orc_argmax.argtypes = [f32p, sz]
         L.orc_decode_step.restype = ctypes.c_int
+        L.orc_decode_step_from.restype = ctypes.c_int
+        L.orc_causal_attention.restype = ctypes.c_int
         L.orc_forward_batch.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -277,10 +279,12 @@ class LlamaCfg(ctypes.Structure):
 
 
 def decode_step(cfg, x_embed, pos, layer_weights, layer_dtypes, norms, final_norm, lm_head, lm_dtype,
-                rope_sin, rope_cos, kv, seq_len):
+                rope_sin, rope_cos, kv, seq_len, start_layer=0):
     """One CPU decode step (runner.rs:1557-1646). layer_weights: list over layers
     of 7 uint8 arrays (q,k,v,o,gate,up,down); norms: list over layers of
-    (attn_norm, ffn_norm). kv is updated in place. Returns (logits, seq_len)."""
+    (attn_norm, ffn_norm). kv is updated in place. Returns (logits, seq_len).
+    start_layer > 0 enters the step there with x_embed as the residual stream
+    (the resume of a budgeted decode, runner.rs:1201-1217)."""
     L = lib()
     nl = cfg.n_layers
     keep = []
@@ -305,7 +309,8 @@ def decode_step(cfg, x_embed, pos, layer_weights, layer_dtypes, norms, final_nor
     assert kv.dtype == np.float32 and kv.flags.c_contiguous
     sl = ctypes.c_int32(seq_len)
     logits = np.empty(cfg.vocab, dtype=np.float32)
-    rc_ = L.orc_decode_step(ctypes.byref(cfg), _p(x, ctypes.c_float), ctypes.c_int32(pos), wp, wt, npp,
+    rc_ = L.orc_decode_step_from(ctypes.byref(cfg), _p(x, ctypes.c_float), ctypes.c_int32(pos),
+                                 ctypes.c_int32(start_layer), wp, wt, npp,
                             _p(fn_, ctypes.c_float), _p(lm, ctypes.c_uint8), ctypes.c_int32(lm_dtype),
                             _p(rs, ctypes.c_float), _p(rc, ctypes.c_float), _p(kv, ctypes.c_float),
                             ctypes.byref(sl), _p(logits, ctypes.c_float))
@@ -355,3 +360,30 @@ def forward_batch(cfg, x_embeds, layer_weights, layer_dtypes, norms, final_norm,
         raise RuntimeError("orc_forward_batch failed: %d" % rc_)
     del keep
     return logits
+
+
+# ── Backend trait ops (src/backend/cpu.rs) ───────────────────────────────
+
+def backend_rms_norm(x, w, eps):
+    """Op::RmsNorm (cpu.rs:514-545) over the rows of x ([..., last_dim])."""
+    x, w = _f32(x), _f32(w)
+    last = w.size
+    out = np.empty_like(x)
+    lib().orc_backend_rms_norm(_p(x, ctypes.c_float), _p(w, ctypes.c_float), ctypes.c_size_t(x.size // last),
+                               ctypes.c_size_t(last), ctypes.c_float(eps), _p(out, ctypes.c_float))
+    return out
+
+
+def causal_attention(q, k, v, num_heads, scale):
+    """Op::CausalAttention (cpu.rs:1660-1727) on [batch][seq][d] arrays."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    b, s, d = q.shape
+    out = np.empty_like(q)
+    scratch = np.empty(max(1, s), dtype=np.float32)
+    rc = lib().orc_causal_attention(_p(q, ctypes.c_float), _p(k, ctypes.c_float), _p(v, ctypes.c_float),
+                                    ctypes.c_size_t(b), ctypes.c_size_t(s), ctypes.c_size_t(d),
+                                    ctypes.c_size_t(num_heads), ctypes.c_float(scale), _p(scratch, ctypes.c_float),
+                                    _p(out, ctypes.c_float))
+    if rc != 0:
+        raise ValueError("causal_attention: num_heads must be positive")
+    return out

@@ -463,3 +463,102 @@ def test_c_api_surface(gpu):
         assert L.aether_load(b"/nonexistent.gguf") is None
     finally:
         L.aether_free(model)
+
+
+def test_decode_budgeted_timeout_and_resume(gpu):
+    """aether_decode_budgeted (c_api.rs:324-355 → decode_step_budgeted,
+    runner.rs:1201-1282) forced from the host: a budget of 1e-9 ms has expired
+    at the first layer check, so the call returns AETHER_TIMEOUT (-2) without
+    logits and records completed_layer = 0 (the reference's
+    layer_idx.saturating_sub(1) at layer 0); a retry with the same (token, pos)
+    resumes at layer 1 with the saved residual stream — i.e. layer 0 is skipped,
+    exactly as the reference does — and, given time, completes. The oracle enters
+    its decode step at layer 1 with x = the embedding (orc_decode_step_from). A
+    retry with another (token, pos) drops the partial state and runs every layer."""
+    L = A.lib()
+    m = build_tiny(seed=6)
+    r = make_runner(m)
+    model = L.aether_model_from_runner(r)
+    c = TINY
+    ocfg = oracle_cfg()
+    s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
+    kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), dtype=np.float32)
+    try:
+        toks = np.array([3, 17, 29], np.int32)
+        logits = np.full(c["vocab_size"], np.nan, np.float32)
+        assert L.aether_prefill(model, toks.ctypes.data, 3, logits.ctypes.data) == 0
+        O.forward_batch(ocfg, m["emb"][toks], m["layers"], [Q4_K] * 7, m["norms"], m["final"], m["lm"],
+                        m["lm_dtype"], s, co, kv)
+        tok = 41
+        L.aether_set_frame_budget(model, 1e-9)
+        sentinel = np.full(c["vocab_size"], 7.0, np.float32)
+        for _ in range(2):  # expires before layer 0, then again right at the resume layer
+            assert L.aether_decode_budgeted(model, tok, 3, sentinel.ctypes.data) == -2
+            assert (sentinel == 7.0).all()  # no logits written on a timeout
+            assert L.aeth_runner_seq_len(r) == 3
+        L.aether_set_frame_budget(model, 1e6)
+        assert L.aether_decode_budgeted(model, tok, 3, logits.ctypes.data) == 0
+        assert L.aeth_runner_seq_len(r) == 4
+        ref, fill = O.decode_step(ocfg, m["emb"][tok], 3, m["layers"], [Q4_K] * 7, m["norms"], m["final"], m["lm"],
+                                  m["lm_dtype"], s, co, kv, 3, start_layer=1)
+        assert fill == 4
+        assert_close_logits(logits, ref, what="resumed at layer 1")
+        # a timed-out attempt for (tok2, 4), then a different token at pos 4: fresh step
+        L.aether_set_frame_budget(model, 1e-9)
+        assert L.aether_decode_budgeted(model, 55, 4, sentinel.ctypes.data) == -2
+        L.aether_set_frame_budget(model, 1e6)
+        assert L.aether_decode_budgeted(model, 56, 4, logits.ctypes.data) == 0
+        ref, fill = O.decode_step(ocfg, m["emb"][56], 4, m["layers"], [Q4_K] * 7, m["norms"], m["final"], m["lm"],
+                                  m["lm_dtype"], s, co, kv, 4)
+        assert_close_logits(logits, ref, what="fresh step after a dropped partial")
+        kv_dev = np.empty_like(kv)
+        fl = ctypes.c_int32()
+        A.check(L.aeth_runner_kv_to_host(r, kv_dev.ctypes.data, ctypes.byref(fl)))
+        assert fl.value == 5
+        assert_close_rows(kv_dev[:, :, :, :5].reshape(-1, c["head_dim"]), kv[:, :, :, :5].reshape(-1, c["head_dim"]),
+                          what="kv after budgeted steps")
+        # budget <= 0: the plain decode
+        L.aether_set_frame_budget(model, 0.0)
+        assert L.aether_decode_budgeted(model, 57, 5, logits.ctypes.data) == 0
+        ref, fill = O.decode_step(ocfg, m["emb"][57], 5, m["layers"], [Q4_K] * 7, m["norms"], m["final"], m["lm"],
+                                  m["lm_dtype"], s, co, kv, 5)
+        assert_close_logits(logits, ref, what="unbudgeted")
+    finally:
+        L.aether_free(model)
+
+
+def test_runners_prefill_concurrently(gpu):
+    """Two runners prefilling from two host threads at once (each on its own
+    stream, with the GEMM's scratch per stream) give exactly their serial
+    results; the Q4_K GEMM runs for n = 150."""
+    import threading
+
+    L = A.lib()
+    c = dict(TINY, max_seq_len=192)
+    models = [build_tiny(seed=40 + i, c=c) for i in range(2)]
+    toks = [np.random.default_rng(60 + i).integers(0, c["vocab_size"], 150).astype(np.int32) for i in range(2)]
+
+    def prefill(r, t, out):
+        A.check(L.aeth_runner_prefill(r, t.ctypes.data, t.size, out.ctypes.data, None), "prefill")
+
+    serial = []
+    for i in range(2):
+        r = make_runner(models[i], c)
+        out = np.empty(c["vocab_size"], np.float32)
+        prefill(r, toks[i], out)
+        serial.append(out)
+        L.aeth_runner_free(r)
+    runners = [make_runner(models[i], c) for i in range(2)]
+    try:
+        for rep in range(3):
+            outs = [np.empty(c["vocab_size"], np.float32) for _ in range(2)]
+            th = [threading.Thread(target=prefill, args=(runners[i], toks[i], outs[i])) for i in range(2)]
+            for t in th:
+                t.start()
+            for t in th:
+                t.join()
+            for i in range(2):
+                assert np.array_equal(outs[i], serial[i]), "runner %d rep %d" % (i, rep)
+    finally:
+        for r in runners:
+            L.aeth_runner_free(r)

@@ -1,0 +1,117 @@
+"""The decode step at the LLaMA-8B widths of BASELINE config 4 (d 4096, 32/8
+heads of 128, d_ff 14336, vocab 128256, RoPE θ 500000, KV prefilled to 2048
+positions) — the shapes where the fused kernels of the benchmark run:
+  * the 6144-row q|k|v GEMV with the attention RMSNorm fused,
+  * the 28672-row interleaved gate|up GEMV with RMSNorm and SwiGLU fused,
+  * the k = 14336 down GEMV accumulating into the residual,
+  * the 128256-row Q6_K LM head on the refilling ring with the final RMSNorm
+    and the 64-bit atomicMax greedy argmax fused.
+A 2-layer model of those widths is built on the device from a seed, exported
+through aeth_runner_export and run teacher-forced against the oracle's decode
+step (runner.rs:1557-1646); the full 32-layer model is checked by properties
+(graph replay = eager, finite logits, fused argmax = host argmax)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import aether_amd as A
+from oracle import oracle as O
+from tests._util import Q4_K, Q6_K, assert_close_logits, assert_close_rows
+
+pytestmark = pytest.mark.gpu
+
+C8B = dict(vocab_size=128256, d_model=4096, num_layers=2, num_heads=32, num_kv_heads=8, head_dim=128, d_ff=14336,
+           max_seq_len=4096, rope_base=500000.0, rms_norm_eps=1e-5)
+PREFILLED = 2048
+
+
+def synthetic_runner(c, seed):
+    cfg = A.LlamaConfig(**c)
+    nl = c["num_layers"]
+    dt = (ctypes.c_int32 * (nl * 7))(*([Q4_K] * (nl * 7)))
+    r = ctypes.c_void_p()
+    A.check(A.lib().aeth_runner_create(ctypes.byref(cfg), None, dt, None, None, None, Q6_K, None, seed,
+                                       ctypes.byref(r)), "runner_create")
+    return r
+
+
+def export(r, which, l, nbytes, dtype=np.uint8):
+    buf = np.empty(nbytes // np.dtype(dtype).itemsize, dtype=dtype)
+    A.check(A.lib().aeth_runner_export(r, which, l, buf.ctypes.data, nbytes), "export %d/%d" % (which, l))
+    return buf
+
+
+def test_decode_8b_widths_match_oracle(gpu):
+    c = C8B
+    L = A.lib()
+    d, dff, kvd, V = c["d_model"], c["d_ff"], c["num_kv_heads"] * c["head_dim"], c["vocab_size"]
+    r = synthetic_runner(c, 0x8B8B8B)
+    try:
+        A.check(L.aeth_runner_fill_kv(r, 0x4B56, PREFILLED), "fill_kv")
+        rowb = lambda k: (k // 256) * 144
+        sizes = [d * rowb(d), kvd * rowb(d), kvd * rowb(d), d * rowb(d), dff * rowb(d), dff * rowb(d), d * rowb(dff)]
+        layers = [[export(r, j, l, sizes[j]) for j in range(7)] for l in range(c["num_layers"])]
+        norms = [[export(r, 7 + j, l, d * 4, np.float32) for j in range(2)] for l in range(c["num_layers"])]
+        final = export(r, 9, 0, d * 4, np.float32)
+        lm = export(r, 10, 0, V * 16 * 210)
+        kv = np.empty((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), np.float32)
+        fl = ctypes.c_int32()
+        A.check(L.aeth_runner_kv_to_host(r, kv.ctypes.data, ctypes.byref(fl)), "kv_to_host")
+        assert fl.value == PREFILLED
+        s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
+        assert np.array_equal(export(r, 12, 0, s.nbytes, np.float32), s)  # the runner's RoPE table is the oracle's
+        ocfg = O.LlamaCfg(V, d, c["num_layers"], c["num_heads"], c["num_kv_heads"], c["head_dim"], dff,
+                          c["max_seq_len"], c["rope_base"], c["rms_norm_eps"])
+        tok, fill = 1, PREFILLED
+        logits = np.empty(V, np.float32)
+        for step in range(3):
+            print("8B-width decode step %d (token %d, pos %d)" % (step, tok, fill), flush=True)
+            nxt = ctypes.c_int32()
+            A.check(L.aeth_runner_decode(r, tok, fill, logits.ctypes.data, ctypes.byref(nxt)), "decode")
+            emb = export(r, 11, tok, d * 4, np.float32)
+            ref, fill = O.decode_step(ocfg, emb, fill, layers, [Q4_K] * 7, norms, final, lm, Q6_K, s, co, kv, fill)
+            assert np.isfinite(logits).all()
+            assert_close_logits(logits, ref, what="8B-width step %d" % step)
+            assert nxt.value == O.argmax(logits), (nxt.value, O.argmax(logits))  # fused argmax = host argmax
+            tok = O.argmax(ref)
+        kv_dev = np.empty_like(kv)
+        A.check(L.aeth_runner_kv_to_host(r, kv_dev.ctypes.data, ctypes.byref(fl)), "kv_to_host")
+        assert fl.value == PREFILLED + 3
+        new = slice(PREFILLED, PREFILLED + 3)
+        assert_close_rows(kv_dev[:, :, :, new].reshape(-1, c["head_dim"]), kv[:, :, :, new].reshape(-1, c["head_dim"]),
+                          what="kv slots written by the steps")
+        assert np.array_equal(kv_dev[:, :, :, :PREFILLED], kv[:, :, :, :PREFILLED])
+    finally:
+        L.aeth_runner_free(r)
+
+
+def test_decode_8b_full_depth_graph_equals_eager(gpu):
+    """32 layers: eager steps (logits back each step) and the captured HIP graph
+    (greedy on the device) give the same tokens; logits are finite and the
+    fused LM-head argmax is the host argmax of the logits returned."""
+    c = dict(C8B, num_layers=32)
+    L = A.lib()
+    r = synthetic_runner(c, 0x8B8B8B)
+    n = 8
+    try:
+        A.check(L.aeth_runner_fill_kv(r, 0x4B56, PREFILLED), "fill_kv")
+        eager = []
+        tok = 1
+        logits = np.empty(c["vocab_size"], np.float32)
+        for step in range(n):
+            nxt = ctypes.c_int32()
+            A.check(L.aeth_runner_decode(r, tok, PREFILLED + step, logits.ctypes.data, ctypes.byref(nxt)), "decode")
+            assert np.isfinite(logits).all(), step
+            assert nxt.value == O.argmax(logits), step
+            eager.append(nxt.value)
+            tok = nxt.value
+        print("32-layer eager tokens", eager, flush=True)
+        for rep in range(2):
+            A.check(L.aeth_runner_fill_kv(r, 0x4B56, PREFILLED), "fill_kv")
+            toks = (ctypes.c_int32 * n)()
+            A.check(L.aeth_runner_generate(r, 1, PREFILLED, n, toks, 1), "generate (graph)")
+            assert list(toks) == eager, (rep, list(toks), eager)
+            assert L.aeth_runner_seq_len(r) == PREFILLED + n
+    finally:
+        L.aeth_runner_free(r)

@@ -169,3 +169,32 @@ def test_requantize_and_load_quant_bad_arguments(gpu):
     assert L.aeth_load_quant(Q4_K, None, 256, 4, None, None, None) == A.AETH_EINVAL
     assert L.aeth_load_quant(16, None, 256, 4, None, None, None) == A.AETH_EUNSUPPORTED
     assert L.aeth_load_quant_ws_bytes(256, 4) == 2 * 256 * 4 * 4
+
+
+def test_requantize_hand_blocks(gpu):
+    """The device re-quantizers on the hand blocks of tests/requant_hand_cases.py:
+    halves round away from zero and quants divide by the f32 scale, not the
+    stored f16 one — literal expected bytes, not the oracle's output."""
+    from tests import requant_hand_cases as H
+
+    torch = gpu
+
+    def dev_requant(dtype, x, cols):
+        be, bb = GEOM[dtype]
+        out = torch.full((bb * (cols // be),), 0xA5, dtype=torch.uint8, device="cuda")
+        xd = to_dev(torch, x)
+        A.check(A.lib().aeth_requantize(dtype, xd.data_ptr(), 1, cols, out.data_ptr(), None), "requantize")
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    for make in (H.q8_0_ties, H.q8_0_f32_scale):
+        x, expect = make()
+        H.check_bytes(dev_requant(Q8_0, x, 32), expect, make.__name__)
+    for make in (H.q4_k_ties, H.q4_k_f32_scale):
+        x, expect = make()
+        H.check_bytes(dev_requant(Q4_K, x, 256), expect, make.__name__)
+    for x, dbits, sc0, deq in H.q6_k_cases():
+        b = dev_requant(Q6_K, x, 256)
+        assert int(b[208]) | (int(b[209]) << 8) == dbits
+        assert int(b[192]) == sc0
+        assert list(O.dequant(Q6_K, b, 256)[:len(deq)]) == deq

@@ -424,3 +424,21 @@ def test_golden_fixture():
         assert np.array_equal(O.dequant(dt, raw, n * k).view(np.uint32), g[name + "_deq"].view(np.uint32))
         out = O.reference_matmul(dt, g["a"][:k], raw, 1, n, k)
         assert np.array_equal(out.view(np.uint32), g[name + "_mm"].view(np.uint32))
+
+
+# ── re-quantizer rounding, pinned by hand blocks (tests/requant_hand_cases.py) ──
+
+def test_requantize_hand_blocks_round_half_away_with_f32_scale():
+    from tests import requant_hand_cases as H
+
+    for make in (H.q8_0_ties, H.q8_0_f32_scale):
+        x, expect = make()
+        H.check_bytes(O.requantize(Q8_0, x, 1, 32), expect, make.__name__)
+    for make in (H.q4_k_ties, H.q4_k_f32_scale):
+        x, expect = make()
+        H.check_bytes(O.requantize(Q4_K, x, 1, 256), expect, make.__name__)
+    for x, dbits, sc0, deq in H.q6_k_cases():
+        b = O.requantize(Q6_K, x, 1, 256)
+        assert int(b[208]) | (int(b[209]) << 8) == dbits
+        assert int(b[192]) == sc0
+        assert list(O.dequant(Q6_K, b, 256)[:len(deq)]) == deq
