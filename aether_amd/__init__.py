@@ -80,6 +80,7 @@ _SIGS = {
     "aeth_rope": (_INT, [_P, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "aeth_kv_append": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_attn_decode": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
+    "aeth_attn_decode_noalloc": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "aeth_attn_prefill": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "aeth_silu_mul": (_INT, [_P, _P, _I64, _P]),
     "aeth_add": (_INT, [_P, _P, _I64, _P]),

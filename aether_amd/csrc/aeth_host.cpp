@@ -119,6 +119,58 @@ extern "C" AETH_API int aeth_attn_decode(const float* d_q, const float* d_layer_
                             head_dim, max_seq, (float*)ws, d_out, (hipStream_t)stream);
 }
 
+// ── decode attention without allocation ───────────────────────────────────
+// For callers that cannot allocate (code under HIP graph capture, tight serving
+// loops): the chunk partials live in a file-scope device array, `scratch`, of
+// kNoAllocFloats floats (4 MiB) that every GPU the library runs on holds until
+// the process ends. Host code never passes the array's name (a host-side
+// stand-in): it uses the per-device address hipGetSymbolAddress returns.
+// Nothing in it has to start at zero (each chunk's partial is written before the
+// merge reads it). Calls that overlap on one GPU share the array and race.
+namespace {
+constexpr int64_t kNoAllocFloats = (int64_t)1 << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+float* g_noalloc_ptr[kMaxDevices] = {};
+}  // namespace
+
+static __device__ __align__(256) float scratch[kNoAllocFloats];
+
+// Resolves this device's copy of `scratch` (the device must be current).
+int aeth_noalloc_setup(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return aeth_set_error(AETH_EINVAL, "no-alloc scratch: device %d", dev);
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (g_noalloc_ptr[dev]) return AETH_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return aeth_set_error(AETH_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                              hipGetErrorString(e));
+    g_noalloc_ptr[dev] = (float*)p;
+    return AETH_OK;
+}
+
+extern "C" AETH_API int aeth_attn_decode_noalloc(const float* d_q, const float* d_layer_kv, int64_t n_heads,
+                                                 int64_t kv_heads, int64_t head_dim, int64_t max_seq, int64_t seq,
+                                                 float* d_out, void* stream) {
+    if (!d_q || !d_layer_kv || !d_out || seq <= 0 || seq > max_seq || n_heads <= 0 || head_dim <= 0 ||
+        n_heads > 65536 || head_dim > 65536 || max_seq > INT32_MAX)
+        return aeth_set_error(AETH_EINVAL, "aeth_attn_decode_noalloc: bad argument (seq %lld, max_seq %lld)",
+                              (long long)seq, (long long)max_seq);
+    const int64_t need = aeth_attn_ws_floats(n_heads, head_dim, max_seq);
+    if (need > kNoAllocFloats)
+        return aeth_set_error(AETH_EINVAL,
+                              "aeth_attn_decode_noalloc: %lld scratch floats needed (n_heads x ceil(max_seq/64) x "
+                              "(head_dim+2)), more than the %lld the library holds",
+                              (long long)need, (long long)kNoAllocFloats);
+    int dev = 0;
+    AETH_HIP_CHECK(hipGetDevice(&dev));
+    int rc = aeth_noalloc_setup(dev);
+    if (rc) return rc;
+    return aeth_attn_launch(d_q, nullptr, (float*)d_layer_kv, nullptr, nullptr, nullptr, seq, n_heads, kv_heads,
+                            head_dim, max_seq, g_noalloc_ptr[dev], d_out, (hipStream_t)stream);
+}
+
 extern "C" AETH_API int aeth_attn_prefill(const float* d_q, int64_t q_stride, const float* d_layer_kv, int64_t n,
                                           int64_t n_heads, int64_t kv_heads, int64_t head_dim, int64_t max_seq,
                                           float* d_out, void* stream) {

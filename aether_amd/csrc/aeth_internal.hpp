@@ -129,6 +129,9 @@ enum { AETH_SCRATCH_GEMM = 0, AETH_SCRATCH_XGEMV = 1, AETH_SCRATCH_ATTN = 2, AET
 int aeth_stream_scratch(hipStream_t s, int use, size_t bytes, void** out);
 // Frees every scratch buffer of stream s (before the stream is destroyed).
 void aeth_stream_scratch_release(hipStream_t s);
+// Resolves the device address of the no-allocation entry point's static
+// scratch on device dev (current); called by aeth_init and on first use.
+int aeth_noalloc_setup(int dev);
 // Bytes of GEMM scratch (A fragments, sub-block sums, row scales) for m rows of k.
 int64_t aeth_gemm_ws_bytes(int64_t m, int64_t k);
 

@@ -39,7 +39,7 @@ extern "C" AETH_API int aeth_init(int device) {
         return aeth_set_error(AETH_EINVAL, "aeth_init: device %d out of range (%d devices)", device, count);
     AETH_HIP_CHECK(hipSetDevice(device));
     (void)aeth_num_cus();
-    return AETH_OK;
+    return aeth_noalloc_setup(device);
 }
 
 extern "C" AETH_API int aeth_block_geometry(int dtype, int* block_elems, int* block_bytes) {

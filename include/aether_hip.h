@@ -208,6 +208,15 @@ AETH_API int aeth_kv_append(float* d_layer_kv, const float* d_k, const float* d_
  * over positions [0, seq) of one layer slice of the static cache. */
 AETH_API int aeth_attn_decode(const float* d_q, const float* d_layer_kv, int64_t n_heads, int64_t kv_heads,
                               int64_t head_dim, int64_t max_seq, int64_t seq, float* d_out, void* stream);
+/* No counterpart in the reference: aeth_attn_decode for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments and results; the chunk partials go to a
+ * static device array of 4 MiB (1,048,576 floats) per GPU instead of a
+ * library allocation, so n_heads·ceil(max_seq/64)·(head_dim+2) must not exceed
+ * 1,048,576 (AETH_EINVAL otherwise). Calls that overlap on one GPU share that
+ * array and race: serialise them (one stream, or one caller at a time). */
+AETH_API int aeth_attn_decode_noalloc(const float* d_q, const float* d_layer_kv, int64_t n_heads, int64_t kv_heads,
+                                      int64_t head_dim, int64_t max_seq, int64_t seq, float* d_out, void* stream);
 /* Causal GQA attention of a prompt batch (attention_batch, runner.rs:1809-1883):
  * query i (row i of d_q, [n][q_stride] with head h at column h*head_dim, RoPE
  * already applied) attends to cache slots 0..i of the layer slice d_layer_kv
