@@ -60,6 +60,8 @@ _SIGS = {
     "aeth_qmatmul": (_INT, [_P, _P, _I64, _P, ctypes.c_uint, _P]),
     "aeth_quantized_matmul_impl": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P]),
     "aeth_quantized_matmul_dotprod": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P]),
+    "aeth_quantized_matmul_impl_cached": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P, _P]),
+    "aeth_stream_read": (_INT, [_P, _I64, _P, _I64, _P]),
     "aeth_matmul_q8_0": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q4_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q5_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),

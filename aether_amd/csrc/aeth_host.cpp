@@ -521,6 +521,18 @@ extern "C" AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, co
     return host_matmul(a, m, b_raw, b_len, n, k, dtype, c);
 }
 
+// quantized_matmul_impl with b_f32_cache (dispatch.rs:113-117): the cached f32
+// weight, GGUF [k][n], multiplied by the F32 GGUF-order kernel of matmul_f32_gguf.
+extern "C" AETH_API int aeth_quantized_matmul_impl_cached(const float* a, int64_t m, const uint8_t* b_raw,
+                                                          int64_t b_len, int64_t n, int64_t k, int dtype, float* c,
+                                                          const float* b_f32_cache) {
+    if (!b_f32_cache) return aeth_quantized_matmul_impl(a, m, b_raw, b_len, n, k, dtype, c);
+    int64_t kn = 0;
+    if (!aeth_mul_ok(k, n, &kn) || kn > INT64_MAX / 4)
+        return aeth_set_error(AETH_EINVAL, "quantized_matmul_impl: bad shape [%lld, %lld]", (long long)n, (long long)k);
+    return host_matmul(a, m, (const uint8_t*)b_f32_cache, kn * 4, n, k, AETH_DTYPE_F32, c, AETH_ORDER_GGUF);
+}
+
 // quantized_matmul_impl on an aarch64 host with dotprod: Q8_0 / Q4_K / Q5_K /
 // Q6_K through the int8 dot-product kernels, the other formats as on x86.
 extern "C" AETH_API int aeth_quantized_matmul_dotprod(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,

@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "aeth_common.hpp"
 #include "aeth_internal.hpp"
 
@@ -448,6 +450,46 @@ extern "C" AETH_API int aeth_fill_normal_f32(uint64_t seed, float* d_out, int64_
     if (n == 0) return AETH_OK;
     hipLaunchKernelGGL(k_fill_normal, dim3((unsigned)aeth_cdiv(n, 256)), dim3(256), 0, (hipStream_t)stream, seed,
                        d_out, n, mean, stdv);
+    AETH_LAUNCH_CHECK();
+    return AETH_OK;
+}
+
+// ── measurement: a plain streaming read ──────────────────────────────────
+// Reads every 16-byte word of [src, src + bytes) once (non-temporal loads,
+// eight in flight per thread before any is used) and folds them into one
+// word per thread, stored only if it equals a value no input makes likely,
+// so the loads cannot be dropped. The benchmark times it on the GEMV's weight
+// copies: the HBM floor a single launch of that size can show.
+typedef uint32_t sr_u4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(512) k_stream_read(const sr_u4* __restrict__ src, int64_t n16,
+                                                     uint32_t* __restrict__ sink) {
+    constexpr int U = 8;
+    const int64_t per_block = (int64_t)512 * U;
+    uint32_t acc = 0;
+    for (int64_t base = (int64_t)blockIdx.x * per_block; base < n16; base += (int64_t)gridDim.x * per_block) {
+        sr_u4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t i = base + (int64_t)u * 512 + threadIdx.x;
+            v[u] = i < n16 ? __builtin_nontemporal_load(src + i) : sr_u4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9E3779B9u) sink[blockIdx.x * 512 + threadIdx.x] = acc;
+}
+
+extern "C" AETH_API int aeth_stream_read(const void* d_src, int64_t bytes, uint32_t* d_sink, int64_t sink_words,
+                                         void* stream) {
+    if (!d_src || !d_sink || bytes < 16 || (bytes & 15) || ((uintptr_t)d_src & 15))
+        return aeth_set_error(AETH_EINVAL, "aeth_stream_read: bad argument");
+    const int64_t n16 = bytes / 16, per_block = 512 * 8;
+    const int64_t blocks = std::min<int64_t>(aeth_cdiv(n16, per_block), sink_words / 512);
+    if (blocks <= 0) return aeth_set_error(AETH_EINVAL, "aeth_stream_read: sink of %lld words < 512",
+                                           (long long)sink_words);
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)blocks), dim3(512), 0, (hipStream_t)stream, (const sr_u4*)d_src,
+                       n16, d_sink);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }

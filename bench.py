@@ -60,12 +60,18 @@ def make_weights(torch, A, dtype, n, k, copies, seed):
 
 
 def time_launches(torch, fn, steps, warmup):
+    """Mean ms per launch of `steps` back-to-back launches on the current stream,
+    bracketed by HIP events on that stream. A bounded spin kernel (torch's
+    clock-based _sleep, ~5 ms) is queued first so that every timed launch is
+    already enqueued when the start event fires: the figure is the GPU's, not
+    the rate at which Python can enqueue."""
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2.4e9 * max(0.005, steps * 30e-6)))
     e0.record(stream)
     for i in range(steps):
         fn(i)
@@ -94,25 +100,42 @@ def bench_gemv(torch, A, dtype, n, k, steps, warmup, copies=16, seed=0xAE7E40, f
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "raw0": raws[0], "x": x}
 
 
-def bench_gemm(torch, A, n, k, m, steps, warmup, seed=0xAE7E43):
+def bench_read_floor(torch, A, nbytes, steps, warmup, copies=16):
+    """The plain streaming read (aeth_stream_read) of nbytes, rotated over as
+    many device buffers as the GEMV's weight copies: what one launch of that
+    size can stream from HBM on this box."""
+    L = A.lib()
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    sink = torch.zeros(1 << 20, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+
+    def step(i):
+        A.check(L.aeth_stream_read(bufs[i % copies].data_ptr(), nbytes, sink.data_ptr(), sink.numel(), s), "read")
+
+    ms = time_launches(torch, step, steps, warmup)
+    del bufs
+    return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9}
+
+
+def bench_gemm(torch, A, n, k, m, steps, warmup, seed=0xAE7E43, flags=0):
     L = A.lib()
     copies = 2
-    ws, _ = make_weights(torch, A, 12, n, k, copies, seed)
+    ws, raws = make_weights(torch, A, 12, n, k, copies, seed)
     a = torch.empty(m * k, dtype=torch.float32, device="cuda")
     A.check(L.aeth_fill_normal_f32(seed ^ 0x77, a.data_ptr(), m * k, 0.0, 1.0, None))
     c = torch.empty(m * n, dtype=torch.float32, device="cuda")
     s = torch.cuda.current_stream().cuda_stream
 
     def step(i):
-        A.check(L.aeth_qmatmul(ws[i % copies], a.data_ptr(), m, c.data_ptr(), 0, s), "gemm")
+        A.check(L.aeth_qmatmul(ws[i % copies], a.data_ptr(), m, c.data_ptr(), flags, s), "gemm")
 
     ms = time_launches(torch, step, steps, warmup)
     for w in ws:
         L.aeth_weight_free(w)
-    return {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+    return {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "raw0": raws[0], "a": a}
 
 
-def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512):
+def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512, want_cpu=False):
     L = A.lib()
     cfg = A.LlamaConfig(vocab_size=128256, d_model=4096, num_layers=32, num_heads=32, num_kv_heads=8, head_dim=128,
                         d_ff=14336, max_seq_len=4096, rope_base=500000.0, rms_norm_eps=1e-5)
@@ -137,6 +160,7 @@ def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512):
     for _ in range(reps):
         A.check(L.aeth_runner_prefill(r, prompt, prefill_tokens, None, None), "prefill")
     pf_s = (time.perf_counter() - t0) / reps
+    cpu_model = export_decode_model(A, r, cfg, prefilled, [1] + list(toks)[:7]) if want_cpu else None
     L.aeth_runner_free(r)
     layer_weights = 4096 * 4096 * 2 + 1024 * 4096 * 2 + 14336 * 4096 * 3
     pf_flops = 2.0 * prefill_tokens * 32 * layer_weights + 2.0 * 128256 * 4096
@@ -147,7 +171,44 @@ def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512):
     step_bytes = q4 + q6 + kv_avg + (32 * 2 + 1) * 4096 * 4
     return {"tok_s": n_tokens / dt_s, "ms_per_token": dt_s * 1e3 / n_tokens, "setup_s": setup_s,
             "gbs": step_bytes * n_tokens / dt_s / 1e9, "step_bytes": step_bytes, "first_tokens": list(toks)[:8],
-            "prefill_tok_s": prefill_tokens / pf_s, "prefill_ms": pf_s * 1e3, "prefill_tflops": pf_flops / pf_s / 1e12}
+            "prefill_tok_s": prefill_tokens / pf_s, "prefill_ms": pf_s * 1e3, "prefill_tflops": pf_flops / pf_s / 1e12,
+            "cpu_model": cpu_model}
+
+
+def export_decode_model(A, r, cfg, prefilled, tokens):
+    """Host copies of what the CPU decode step reads: every layer weight (raw
+    GGUF row blocks), the norms, the LM head, the KV cache refilled to
+    `prefilled` positions, and the embedding rows of `tokens` (the GPU's greedy
+    tokens, so both sides decode the same sequence)."""
+    import numpy as np
+
+    L = A.lib()
+
+    def ex(which, l, nbytes, dt=np.uint8):
+        buf = np.empty(nbytes // np.dtype(dt).itemsize, dtype=dt)
+        A.check(L.aeth_runner_export(r, which, l, buf.ctypes.data, nbytes), "export")
+        return buf
+
+    d, dff, kvd, nl = cfg.d_model, cfg.d_ff, cfg.num_kv_heads * cfg.head_dim, cfg.num_layers
+    rowb = lambda k: (k // 256) * 144
+    sizes = [d * rowb(d), kvd * rowb(d), kvd * rowb(d), d * rowb(d), dff * rowb(d), dff * rowb(d), d * rowb(dff)]
+    A.check(L.aeth_runner_fill_kv(r, 0x4B56, prefilled), "fill_kv")
+    kv = np.empty((nl, 2, cfg.num_kv_heads, cfg.max_seq_len, cfg.head_dim), np.float32)
+    fill = ctypes.c_int32()
+    A.check(L.aeth_runner_kv_to_host(r, kv.ctypes.data, ctypes.byref(fill)), "kv_to_host")
+    return {"cfg": cfg, "layers": [[ex(j, l, sizes[j]) for j in range(7)] for l in range(nl)],
+            "norms": [[ex(7 + j, l, d * 4, np.float32) for j in range(2)] for l in range(nl)],
+            "final": ex(9, 0, d * 4, np.float32), "lm": ex(10, 0, cfg.vocab_size * 16 * 210), "kv": kv,
+            "prefilled": prefilled, "tokens": tokens, "emb": [ex(11, t, d * 4, np.float32) for t in tokens]}
+
+
+def profile_traffic(name):
+    """HBM bytes per dispatch recorded in profiles/<name>_traffic.json, or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", name + "_traffic.json")) as f:
+            return json.load(f)["traffic_bytes_per_dispatch"]
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def measured_traffic():
@@ -192,6 +253,88 @@ def cpu_rows_parallel(raw, x, n, k, seconds=4.0):
             "sample": "%d full Q4_K GEMVs 14336x4096 in %.1f s" % (calls, el)}
 
 
+def cpu_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_median(fn, runs):
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], ts
+
+
+def cpu_configs(q8, q6, gemm, dec):
+    """CPU figures beside the other configs, on one pinned core (the reference's
+    AVX2 kernels are single-threaded): C1 the scalar Q8_0 kernel q8_0.rs (the
+    reference's AVX2 Q8_0 kernel mis-addresses its quants, avx2.rs:163), median
+    of 5; C3 avx2::matmul_q6_k, median of 5; C4 one m = 512 avx2::matmul_q4_k
+    call per N; C5 the CPU decode step (forward_one_internal's CPU branch,
+    runner.rs:1557-1646) per token over 8 steps of the GPU's greedy sequence."""
+    from oracle import oracle as O
+
+    out = {}
+    host = cpu_name()
+    if q8 is not None:
+        raw, x = q8
+        med, ts = cpu_median(lambda: O.scalar_matmul(8, x, raw, 1, 4096, 4096), 5)
+        out["q8_0_gemv_4096x4096"] = {"value": round(algorithmic_bytes(8, 4096, 4096) / med / 1e9, 3), "unit": "GB/s",
+                                      "cores": 1, "kind": "port", "cpu": host,
+                                      "sample": "median of 5 full GEMVs (scalar q8_0.rs restated): %.2f ms" % (med * 1e3)}
+        print("[bench] cpu C1: %s" % out["q8_0_gemv_4096x4096"], file=sys.stderr, flush=True)
+    if q6 is not None:
+        raw, x = q6
+        med, ts = cpu_median(lambda: O.avx2_matmul(14, x, raw, 1, 128256, 4096), 5)
+        out["q6_k_gemv_128256x4096"] = {"value": round(algorithmic_bytes(14, 128256, 4096) / med / 1e9, 3),
+                                        "unit": "GB/s", "cores": 1, "kind": "port", "cpu": host,
+                                        "sample": "median of 5 full GEMVs (avx2::matmul_q6_k restated): %.1f ms"
+                                                  % (med * 1e3)}
+        print("[bench] cpu C3: %s" % out["q6_k_gemv_128256x4096"], file=sys.stderr, flush=True)
+    for nn, (raw, a) in sorted(gemm.items()):
+        t0 = time.perf_counter()
+        O.avx2_matmul(12, a, raw, 512, nn, 4096)
+        el = time.perf_counter() - t0
+        out["q4_k_gemm_m512_n%d" % nn] = {"value": round(2.0 * 512 * nn * 4096 / el / 1e9, 3), "unit": "GFLOP/s",
+                                          "cores": 1, "kind": "port", "cpu": host,
+                                          "sample": "one m=512 call of avx2::matmul_q4_k restated: %.2f s" % el}
+        print("[bench] cpu C4 n=%d: %s" % (nn, out["q4_k_gemm_m512_n%d" % nn]), file=sys.stderr, flush=True)
+    if dec is not None:
+        import numpy as np
+
+        c = dec["cfg"]
+        ocfg = O.LlamaCfg(c.vocab_size, c.d_model, c.num_layers, c.num_heads, c.num_kv_heads, c.head_dim, c.d_ff,
+                          c.max_seq_len, c.rope_base, c.rms_norm_eps)
+        s_, co = O.precompute_rope(c.max_seq_len, c.head_dim, c.rope_base)
+        fill = dec["prefilled"]
+        ts = []
+        agree = 0
+        for i, tok in enumerate(dec["tokens"]):
+            t0 = time.perf_counter()
+            logits, fill = O.decode_step(ocfg, dec["emb"][i], fill, dec["layers"], [12] * 7, dec["norms"],
+                                         dec["final"], dec["lm"], 14, s_, co, dec["kv"], fill)
+            ts.append(time.perf_counter() - t0)
+            if i + 1 < len(dec["tokens"]):
+                agree += int(O.argmax(logits) == dec["tokens"][i + 1])
+        mean = sum(ts) / len(ts)
+        out["decode_8b_q4k"] = {"value": round(1.0 / mean, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+                                "cpu": host,
+                                "sample": "%d CPU decode steps of the 32-layer model after 2048 positions, mean %.2f s "
+                                          "per token; greedy tokens equal to the GPU's on %d of %d steps"
+                                          % (len(ts), mean, agree, len(ts) - 1)}
+        print("[bench] cpu C5: %s" % out["decode_8b_q4k"], file=sys.stderr, flush=True)
+    return out
+
+
 def cpu_baseline(raw, x, n, k, seconds=10.0):
     """The oracle's AVX2-path restatement (single thread, as the reference's
     avx2::matmul_q4_k) timed on this host over repeated full GEMVs."""
@@ -219,9 +362,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--extra", default="q8,q6,q5,dotprod,gemm,decode",
-                    help="comma-separated extra sections to run: q8, q6, q5, dotprod, gemm, decode (default), "
-                         "f16, q2k (GGUF-order formats, not run by default)")
+    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,gemm,gemm_q8,decode",
+                    help="comma-separated extra sections to run: floor, q8, q6, q5, dotprod, gemm, gemm_q8, decode "
+                         "(default), f16, q2k (GGUF-order formats, not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (HBM counter calibration under rocprofv3)")
@@ -258,17 +401,36 @@ def main():
           flush=True)
     extra = {}
     sections = set() if args.no_extra else set(x.strip() for x in args.extra.split(",") if x.strip())
+    want_cpu = not args.no_cpu
+    cpu_in = {"q8": None, "q6": None, "gemm": {}, "dec": None}
+    if "floor" in sections:  # the plain read of the headline's weight bytes over 16 rotated buffers
+        wbytes = n * (k // 256) * 144
+        f = bench_read_floor(torch, A, wbytes, args.steps, args.warmup)
+        extra["read_floor_33MB"] = {"GB/s": round(f["gbs"], 1), "us": round(f["ms"] * 1e3, 3),
+                                    "frac_hbm": round(f["gbs"] / HBM_PEAK_GBS, 4), "bytes": wbytes,
+                                    "headline_over_floor": round(head["ms"] / f["ms"], 4)}
+        print("[bench] read floor: %s" % extra["read_floor_33MB"], file=sys.stderr, flush=True)
     if "q8" in sections:
         r = bench_gemv(torch, A, 8, 4096, 4096, args.steps, args.warmup, seed=0xAE7E41)
         extra["q8_0_gemv_4096x4096"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),
-                                         "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+                                         "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                                         "traffic": profile_traffic("q8_0_gemv_4096x4096"),
+                                         "parity": "scalar q8_0.rs (the reference's x86 AVX2 Q8_0 kernel reads "
+                                                   "quants 16-23 for elements 8-15 and past the last block, "
+                                                   "avx2.rs:163; its outputs differ from these)"}
         print("[bench] Q8_0 GEMV: %s" % extra["q8_0_gemv_4096x4096"], file=sys.stderr, flush=True)
+        if want_cpu:
+            cpu_in["q8"] = (r["raw0"].cpu().numpy(), r["x"].cpu().numpy())
+        del r
     if "q6" in sections:
         r = bench_gemv(torch, A, 14, 128256, 4096, max(20, args.steps // 4), max(3, args.warmup // 4), copies=2,
                        seed=0xAE7E42)
         extra["q6_k_gemv_128256x4096"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),
-                                           "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+                                           "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                                           "traffic": profile_traffic("q6_k_gemv_128256x4096")}
         print("[bench] Q6_K GEMV: %s" % extra["q6_k_gemv_128256x4096"], file=sys.stderr, flush=True)
+        if want_cpu:
+            cpu_in["q6"] = (r["raw0"].cpu().numpy(), r["x"].cpu().numpy())
         del r
     if "q5" in sections:
         r = bench_gemv(torch, A, 13, 14336, 4096, args.steps, args.warmup, seed=0xAE7E44)
@@ -288,13 +450,30 @@ def main():
                           "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
             print("[bench] %s: %s" % (key, extra[key]), file=sys.stderr, flush=True)
     if "gemm" in sections:
+        gsteps, gwarm = max(3, min(args.steps, 50)), max(1, min(args.warmup, 5))
         for nn in (4096, 14336):
-            g = bench_gemm(torch, A, nn, 4096, 512, 5, 2)
+            g = bench_gemm(torch, A, nn, 4096, 512, gsteps, gwarm)
             extra["q4_k_gemm_m512_n%d" % nn] = {"TFLOP/s": round(g["tflops"], 2), "ms": round(g["ms"], 4),
-                                                 "frac_int8_peak": round(g["tflops"] / INT8_PEAK_TOPS, 4)}
+                                                 "frac_int8_peak": round(g["tflops"] / INT8_PEAK_TOPS, 4),
+                                                 "frac_fp16_peak": round(g["tflops"] / FP16_PEAK_TFLOPS, 4),
+                                                 "steps": gsteps, "mode": "exact (f32 activations)"}
             print("[bench] Q4_K GEMM n=%d: %s" % (nn, extra["q4_k_gemm_m512_n%d" % nn]), file=sys.stderr, flush=True)
+            if want_cpu:
+                cpu_in["gemm"][nn] = (g["raw0"].cpu().numpy(), g["a"].cpu().numpy())
+            del g
+    if "gemm_q8" in sections:  # the dot-product mode's GEMM: a14 Q8_0 activation blocks
+        gsteps, gwarm = max(3, min(args.steps, 50)), max(1, min(args.warmup, 5))
+        for nn in (4096, 14336):
+            g = bench_gemm(torch, A, nn, 4096, 512, gsteps, gwarm, flags=A.MM_Q8_ACTIVATIONS)
+            extra["q4_k_gemm_m512_n%d_q8act" % nn] = {"TFLOP/s": round(g["tflops"], 2), "ms": round(g["ms"], 4),
+                                                       "frac_int8_peak": round(g["tflops"] / INT8_PEAK_TOPS, 4),
+                                                       "steps": gsteps, "mode": "q8 (Q8_0 activation blocks)"}
+            print("[bench] Q4_K GEMM q8 n=%d: %s" % (nn, extra["q4_k_gemm_m512_n%d_q8act" % nn]), file=sys.stderr,
+                  flush=True)
+            del g
     if "decode" in sections:
-        d = bench_decode(torch, A)
+        d = bench_decode(torch, A, want_cpu=want_cpu)
+        cpu_in["dec"] = d.pop("cpu_model")
         extra["decode_8b_q4k"] = {"tok/s": round(d["tok_s"], 1), "ms_per_token": round(d["ms_per_token"], 4),
                                   "GB/s": round(d["gbs"], 1), "frac_hbm": round(d["gbs"] / HBM_PEAK_GBS, 4),
                                   "tokens": 128, "prefilled": 2048, "first_tokens": d["first_tokens"]}
@@ -310,8 +489,10 @@ def main():
         cpu_par = cpu_rows_parallel(raw, x, n, k)  # before the single-core leg pins this process
         print("[bench] cpu, scalar kernel over threads: %s" % cpu_par, file=sys.stderr, flush=True)
         extra["cpu_q4_k_gemv_rows_parallel"] = cpu_par
-        cpu = cpu_baseline(raw, x, n, k, args.cpu_seconds)
+        cpu = cpu_baseline(raw, x, n, k, args.cpu_seconds)  # pins this process to one core
         print("[bench] cpu baseline: %s" % cpu, file=sys.stderr, flush=True)
+        for key, val in cpu_configs(cpu_in["q8"], cpu_in["q6"], cpu_in["gemm"], cpu_in["dec"]).items():
+            extra.setdefault(key, {})["cpu_baseline"] = val
 
     out = {
         "metric": "Q4_K GEMV HBM GB/s (% peak); prefill GEMM TFLOP/s; 8B-shape decode tok/s",

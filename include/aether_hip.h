@@ -146,6 +146,12 @@ AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, const uint8_t
  * (avx2_dispatch.rs:9-44, dispatch.rs:21-22): Q8_0 / Q4_K / Q5_K / Q6_K
  * through the int8 dot-product kernels (AETH_MM_Q8_ACTIVATIONS), the other
  * formats as aeth_quantized_matmul_impl. Same arguments and caching. */
+/* quantized_matmul_impl with its b_f32_cache argument (dispatch.rs:98-117):
+ * when b_f32_cache is non-NULL it holds the weight dequantized to f32 in GGUF
+ * [k][n] order (k·n floats) and c = matmul_f32_gguf(a, cache) — b_raw is then
+ * not read; with NULL this is aeth_quantized_matmul_impl. Same caching. */
+AETH_API int aeth_quantized_matmul_impl_cached(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
+                                               int64_t n, int64_t k, int dtype, float* c, const float* b_f32_cache);
 AETH_API int aeth_quantized_matmul_dotprod(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
                                            int64_t n, int64_t k, int dtype, float* c);
 /* matmul_q8_0 / matmul_q4_k / matmul_q6_k(a, b, m, n, k, c)
@@ -263,6 +269,13 @@ AETH_API int aeth_causal_attention(const float* d_q, const float* d_k, const flo
 AETH_API int aeth_fill_synthetic_raw(int dtype, uint64_t seed, void* d_raw, int64_t n_blocks, void* stream);
 /* out[i] = mean + std * N(0,1) from (seed, i). */
 AETH_API int aeth_fill_normal_f32(uint64_t seed, float* d_out, int64_t n, float mean, float std, void* stream);
+
+/* Measurement kernel, no counterpart in the reference: reads `bytes`
+ * (a multiple of 16, 16-byte aligned) once with streaming loads, the plain
+ * HBM read a single launch of that size achieves (the benchmark's floor for
+ * the GEMVs). d_sink holds sink_words >= 512 words; a word is written only if
+ * the fold of the input hits one fixed value. */
+AETH_API int aeth_stream_read(const void* d_src, int64_t bytes, uint32_t* d_sink, int64_t sink_words, void* stream);
 
 /* ── LlamaRunner (src/inference/runner.rs) on the device ─────────────────
  * Model shape = LlamaConfig (model_loader.rs:71-84). */

@@ -278,6 +278,13 @@ class LlamaCfg(ctypes.Structure):
                 ("eps", ctypes.c_float)]
 
 
+def _dtype_of(layer_dtypes, l, j):
+    """layer_dtypes: seven formats for every layer, or one list of seven per layer."""
+    if isinstance(layer_dtypes[0], (list, tuple)):
+        return layer_dtypes[l][j]
+    return layer_dtypes[j]
+
+
 def decode_step(cfg, x_embed, pos, layer_weights, layer_dtypes, norms, final_norm, lm_head, lm_dtype,
                 rope_sin, rope_cos, kv, seq_len, start_layer=0):
     """One CPU decode step (runner.rs:1557-1646). layer_weights: list over layers
@@ -295,7 +302,7 @@ def decode_step(cfg, x_embed, pos, layer_weights, layer_dtypes, norms, final_nor
             arr = _u8(layer_weights[l][j])
             keep.append(arr)
             wp[l * 7 + j] = _p(arr, ctypes.c_uint8)
-            wt[l * 7 + j] = layer_dtypes[l][j] if isinstance(layer_dtypes[l], (list, tuple)) else layer_dtypes[j]
+            wt[l * 7 + j] = _dtype_of(layer_dtypes, l, j)
     npp = (ctypes.POINTER(ctypes.c_float) * (nl * 2))()
     for l in range(nl):
         for j in range(2):
@@ -329,7 +336,7 @@ def _model_ptrs(cfg, layer_weights, layer_dtypes, norms):
             arr = _u8(layer_weights[l][j])
             keep.append(arr)
             wp[l * 7 + j] = _p(arr, ctypes.c_uint8)
-            wt[l * 7 + j] = layer_dtypes[l][j] if isinstance(layer_dtypes[l], (list, tuple)) else layer_dtypes[j]
+            wt[l * 7 + j] = _dtype_of(layer_dtypes, l, j)
     npp = (ctypes.POINTER(ctypes.c_float) * (nl * 2))()
     for l in range(nl):
         for j in range(2):

@@ -102,3 +102,38 @@ def test_concurrent_host_threads(gpu):
     for (dt, a, raw, m), got in zip(jobs, out):
         assert_close(got, O.reference_matmul(dt, a, raw, m, n, k), what="thread dtype %d" % dt)
     A.check(L.aeth_weight_cache_clear())
+
+
+@pytest.mark.parametrize("m", [1, 5])
+def test_quantized_matmul_impl_b_f32_cache(gpu, m):
+    """quantized_matmul_impl's b_f32_cache branch (dispatch.rs:113-117): the
+    cached f32 weight in GGUF [k][n] order is multiplied by matmul_f32_gguf and
+    b_raw is ignored; without a cache the raw bytes are used."""
+    L = A.lib()
+    n, k = 64, 512
+    raw = weight(Q4_K, n, k, 77)
+    # the cache a LayerCache would hold: the weight dequantized, GGUF [in][out] order
+    cache = np.ascontiguousarray(O.dequant(Q4_K, raw, n * k).reshape(n, k).T)
+    a = np.random.default_rng(m).standard_normal(m * k).astype(np.float32)
+    c = np.full(m * n, np.nan, np.float32)
+    junk = np.zeros_like(raw)  # not read when the cache is given
+    A.check(L.aeth_quantized_matmul_impl_cached(a.ctypes.data, m, junk.ctypes.data, junk.size, n, k, Q4_K,
+                                                c.ctypes.data, cache.ctypes.data), "impl_cached")
+    assert_close(c.reshape(m, n), O.matmul_f32_gguf(a, cache, m, n, k))
+    c2 = np.full(m * n, np.nan, np.float32)
+    A.check(L.aeth_quantized_matmul_impl_cached(a.ctypes.data, m, raw.ctypes.data, raw.size, n, k, Q4_K,
+                                                c2.ctypes.data, None), "impl_cached (no cache)")
+    assert_close(c2.reshape(m, n), O.reference_matmul(Q4_K, a, raw, m, n, k))
+    A.check(L.aeth_weight_cache_clear())
+
+
+def test_stream_read_arguments(gpu):
+    torch = gpu
+    L = A.lib()
+    src = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    A.check(L.aeth_stream_read(src.data_ptr(), src.numel(), sink.data_ptr(), sink.numel(), None), "stream_read")
+    torch.cuda.synchronize()
+    assert not sink.any()
+    assert L.aeth_stream_read(src.data_ptr(), 15, sink.data_ptr(), sink.numel(), None) == A.AETH_EINVAL
+    assert L.aeth_stream_read(src.data_ptr(), src.numel(), sink.data_ptr(), 100, None) == A.AETH_EINVAL
