@@ -104,8 +104,17 @@ __global__ void __launch_bounds__(256) k_gemm_rowscale(const float* __restrict__
 //    16·ks + 8·(l/32) + perm4(i), i < 8, of A·2^-e, part 0 = hi, 1 = lo;
 //  * Sh/Sl [row][k/32] = Σ of each 32-element sub-block of A·2^-(e+5), hi/lo.
 // Thread (row lr = tid/8, sub-block q = tid%8) converts 32 elements.
+//
+// Q8 = true (AETH_MM_Q8_ACTIVATIONS, the dot-product mode): each 32-element
+// sub-block is first replaced by its Q8_0 activation block, dequantized —
+// quantize_q8_0_block (neon.rs:45-104): d = max|x|/127 (NaN-propagating max),
+// q = sat_i8(RNE(x·(1/d))) with the f32 d, and the value q·f16(d) the integer
+// dot of the reference scales with (d_a = the stored f16 d). q·f16(d) has at
+// most 18 significant bits, so it is exact in f32 and in the hi/lo split: the
+// GEMM then computes Σ (q_a·d_a)·(q·sc·d) exactly per product, i.e. the
+// reference's per-term d_a·(d1·Σ q·q_a − m1·Σ q_a) up to f32 summation order.
 #define GF_LD 260  // LDS row stride in floats
-template <bool AL16>
+template <bool AL16, bool Q8>
 __global__ void __launch_bounds__(256) k_gemm_frag(const float* __restrict__ A, int m, int k,
                                                    const float* __restrict__ escale, _Float16* __restrict__ frag,
                                                    _Float16* __restrict__ Sh, _Float16* __restrict__ Sl) {
@@ -139,6 +148,24 @@ __global__ void __launch_bounds__(256) k_gemm_frag(const float* __restrict__ A, 
         v[4 * i + 1] = t.y;
         v[4 * i + 2] = t.z;
         v[4 * i + 3] = t.w;
+    }
+    if (Q8) {
+        bool nan = false;
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            nan |= v[i] != v[i];
+            mx = fmaxf(mx, fabsf(v[i]));
+        }
+        const float d = nan ? __uint_as_float(0x7FC00000u) : mx / 127.0f;
+        const float da = aeth_f16_to_f32(aeth_f32_to_f16_bits(d));  // d_a as the block stores it
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const float p = v[i] * id;  // RNE with saturation, NaN → 0 (vcvtnq_s32_f32, sqxtn)
+            const float q = p != p ? 0.0f : fminf(fmaxf(rintf(p), -128.0f), 127.0f);
+            v[i] = d > 0.0f ? q * da : (d == 0.0f ? 0.0f : da);  // a NaN block dequantizes to NaN
+        }
     }
     float sum = 0.0f;
 #pragma unroll
@@ -754,8 +781,11 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     if (al16) hipLaunchKernelGGL(k_gemm_rowscale<true>, rg, dim3(256), 0, s, d_a, (int)m, (int)mp, k, esc);
     else hipLaunchKernelGGL(k_gemm_rowscale<false>, rg, dim3(256), 0, s, d_a, (int)m, (int)mp, k, esc);
     AETH_LAUNCH_CHECK();
-    if (al16) hipLaunchKernelGGL(k_gemm_frag<true>, fg, dim3(256), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
-    else hipLaunchKernelGGL(k_gemm_frag<false>, fg, dim3(256), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
+    const bool q8 = (flags & AETH_MM_Q8_ACTIVATIONS) != 0;
+    if (al16 && q8) hipLaunchKernelGGL((k_gemm_frag<true, true>), fg, dim3(256), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
+    else if (q8) hipLaunchKernelGGL((k_gemm_frag<false, true>), fg, dim3(256), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
+    else if (al16) hipLaunchKernelGGL((k_gemm_frag<true, false>), fg, dim3(256), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
+    else hipLaunchKernelGGL((k_gemm_frag<false, false>), fg, dim3(256), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
     AETH_LAUNCH_CHECK();
     const int gm = (int)(mp / G2_BM), gn = (int)aeth_cdiv(w->n, G2_BN);
     const int64_t ntiles = aeth_cdiv(w->n, 16);

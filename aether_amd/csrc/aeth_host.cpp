@@ -71,8 +71,7 @@ void aeth_stream_scratch_release(hipStream_t s) {
 
 int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
                     hipStream_t s) {
-    if (m > 1 && w->dtype == AETH_DTYPE_Q4_K && !(flags & AETH_MM_Q8_ACTIVATIONS))
-        return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
+    if (m > 1 && w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
     GemvEpi e;
     e.flags = flags;
     e.ldc = ldc;

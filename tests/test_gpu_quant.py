@@ -548,3 +548,31 @@ def test_quantized_matmul_dotprod_host_slices(gpu):
             ref = O.gguf_order_matmul(dtype, a, raw, m, n, k)
         assert_close(c.reshape(m, n), ref, what="dotprod host dtype %d" % dtype)
     A.check(L.aeth_weight_cache_clear())
+
+
+# The dot-product mode at m > 1 runs the Q4_K prefill GEMM with Q8_0 activation
+# blocks (each 32-element block quantised as quantize_q8_0_block, neon.rs:45-104,
+# then used as q·d_a): odd super-block counts (the single-K-group kernel), ragged
+# m, both column extents, and a NaN row among finite ones.
+@pytest.mark.parametrize("m,n,k", [(64, 256, 4096), (150, 4096, 4096), (512, 256, 4096), (70, 512, 1280),
+                                   (33, 128, 14336)])
+def test_dotprod_mode_gemm(gpu, m, n, k):
+    rng = np.random.default_rng(m * 7 + n + k)
+    raw = weight(Q4_K, n, k, m + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1, :64] *= 300.0      # a block maximum far above its neighbours
+    x[2] *= 2.0 ** -12      # tiny blocks (f16 scales near the subnormal range)
+    x[3, 5:37] = 0.0        # a straddled zero block: d = 0 → zero quants
+    if m > 4:
+        x[4, 7] = np.nan
+    w = make_weight(gpu, Q4_K, n, k, raw)
+    got = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    aq = O.quantize_activations_q8_0(x.ravel(), m, k)
+    ref = O.dotprod_ref(Q4_K, aq, raw, m, n, k)
+    if m > 4:
+        assert np.isnan(got[4]).all() and np.isnan(ref[4]).all()
+        keep = np.arange(m) != 4
+        got, ref = got[keep], ref[keep]
+    assert np.isfinite(got).all()
+    assert_close(got, ref, what="dotprod GEMM m=%d n=%d k=%d" % (m, n, k))
