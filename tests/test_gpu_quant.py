@@ -300,8 +300,11 @@ def test_synthetic_generator_deterministic(gpu):
 # kernel, an even one the split-K kernel; m and n off the 64 × 128 tile grid.
 # Row magnitudes span 2^-12 .. 2^20 (the per-block fp16 exponent), with an
 # all-zero row, and the accumulate epilogue is checked on top.
-@pytest.mark.parametrize("m,n,k", [(70, 130, 768), (65, 300, 1024), (130, 40, 2560), (3, 16, 512)])
+@pytest.mark.parametrize("m,n,k", [(70, 130, 768), (65, 300, 1024), (130, 40, 2560), (3, 16, 512), (45, 48, 16384),
+                                   (34, 64, 20480)])
 def test_gemm_q4k_tiles_exponents_accumulate(gpu, m, n, k):
+    """Ragged tiles, per-row exponents (2^20, 2^-12, zero rows, a block past
+    fp16 range) and accumulate, up to rows of 16384 and 20480 elements."""
     rng = np.random.default_rng(m * 31 + n * 7 + k)
     raw = weight(Q4_K, n, k, 3 * n + k)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -576,3 +579,42 @@ def test_dotprod_mode_gemm(gpu, m, n, k):
         got, ref = got[keep], ref[keep]
     assert np.isfinite(got).all()
     assert_close(got, ref, what="dotprod GEMM m=%d n=%d k=%d" % (m, n, k))
+
+
+GEMM_KERNEL_SCRIPT = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, %r)
+import aether_amd as A
+from oracle import oracle as O
+from tests._util import weight, assert_close
+A.check(A.lib().aeth_init(0))
+for m, n, k in ((130, 200, 1024), (64, 128, 2048), (70, 48, 1280)):
+    raw = weight(12, n, k, m + n)
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    w = __import__("ctypes").c_void_p()
+    rawd = torch.from_numpy(raw).cuda()
+    A.check(A.lib().aeth_weight_create(12, n, k, rawd.data_ptr(), 1, None, __import__("ctypes").byref(w)))
+    xd = torch.from_numpy(x).cuda()
+    y = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    A.check(A.lib().aeth_qmatmul(w, xd.data_ptr(), m, y.data_ptr(), 0, None))
+    torch.cuda.synchronize()
+    assert_close(y.cpu().numpy().reshape(m, n), O.reference_matmul(12, x.ravel(), raw, m, n, k), what="kernel")
+    A.lib().aeth_weight_free(w)
+print("ok")
+"""
+
+
+@pytest.mark.parametrize("kernel", ["2", "3"])
+def test_gemm_alternate_kernels(gpu, kernel):
+    """The GEMM kernels the default never picks for even super-block counts:
+    AETH_GEMM_KERNEL=2 (the single-K-group ring kernel) and =3 (the 4-wave
+    split-K kernel), read once per process, so each runs in a fresh process."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, AETH_GEMM_KERNEL=kernel)
+    r = subprocess.run([sys.executable, "-c", GEMM_KERNEL_SCRIPT % root], env=env, cwd=root, timeout=240,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:]
