@@ -22,6 +22,7 @@ SOURCES = [
     "aeth_prefill.hip",
     "aeth_backend.hip",
     "aeth_host.cpp",
+    "aeth_blas.cpp",
     "aeth_runner.cpp",
     "aeth_gguf.cpp",
 ]
@@ -64,8 +65,13 @@ def compile_command(src, obj, extra=()):
         ["-c", "-o", obj, path]
 
 
+ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+
+
 def link_command(objs, out):
-    return [hipcc(), "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", out] + list(objs)
+    # rocBLAS serves the plain f32 GEMMs of the formats without a GEMM kernel of their own
+    return [hipcc(), "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", out] + list(objs) + \
+        ["-L" + ROCM_LIB, "-lrocblas", "-Wl,-rpath," + ROCM_LIB]
 
 
 def _run(cmd):

@@ -58,6 +58,7 @@ int aeth_stream_scratch(hipStream_t s, int use, size_t bytes, void** out) {
 }
 
 void aeth_stream_scratch_release(hipStream_t s) {
+    aeth_blas_release_stream(s);
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     for (auto it = g_scratch.begin(); it != g_scratch.end();) {
         if (std::get<1>(it->first) == s) {
@@ -69,9 +70,25 @@ void aeth_stream_scratch_release(hipStream_t s) {
     }
 }
 
+namespace {
+constexpr int64_t kDequantGemmRows = 16;
+}
+
 int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
                     hipStream_t s) {
+    const bool kquant = w->dtype == AETH_DTYPE_Q4_K || w->dtype == AETH_DTYPE_Q5_K || w->dtype == AETH_DTYPE_Q6_K;
+    // the dot-product mode's batched K-quant kernels index activation rows (k/256)·8 blocks
+    // apart; for k % 256 != 0 only the dequantized product reproduces that (aeth_blas.cpp)
+    if (m > 1 && (flags & AETH_MM_Q8_ACTIVATIONS) && kquant && (w->k % 256) != 0)
+        return aeth_dequant_gemm_launch(w, d_a, m, d_c, ldc, flags, s);
     if (m > 1 && w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
+    // the other block formats from 16 rows on: dequantized once, one SGEMM (instead
+    // of the weight streamed once per row by the batched GEMV). Their dequantized
+    // weights are finite (K-quant scales go through decode_d), so the SGEMM's
+    // 0·w terms equal matmul_f32_gguf's skipped rows; F32 / F16 weights, which may
+    // hold infinities, keep the kernels that skip zero activations as the reference does.
+    if (m >= kDequantGemmRows && w->dtype != AETH_DTYPE_F32 && w->dtype != AETH_DTYPE_F16)
+        return aeth_dequant_gemm_launch(w, d_a, m, d_c, ldc, flags, s);
     GemvEpi e;
     e.flags = flags;
     e.ldc = ldc;

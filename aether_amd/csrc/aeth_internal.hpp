@@ -125,13 +125,27 @@ int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_
 // stream, use) for calls that bring no workspace of their own. Calls on one
 // stream share it (their kernels run in order); a grow waits for the stream
 // and is refused during graph capture.
-enum { AETH_SCRATCH_GEMM = 0, AETH_SCRATCH_XGEMV = 1, AETH_SCRATCH_ATTN = 2, AETH_SCRATCH_ARGMAX = 3 };
+enum {
+    AETH_SCRATCH_GEMM = 0,
+    AETH_SCRATCH_XGEMV = 1,
+    AETH_SCRATCH_ATTN = 2,
+    AETH_SCRATCH_ARGMAX = 3,
+    AETH_SCRATCH_DEQ = 4,   // dequantized f32 weight of a batched product (aeth_blas.cpp)
+    AETH_SCRATCH_QACT = 5,  // Q8_0 activation blocks and their f32 values (same)
+};
 int aeth_stream_scratch(hipStream_t s, int use, size_t bytes, void** out);
 // Frees every scratch buffer of stream s (before the stream is destroyed).
 void aeth_stream_scratch_release(hipStream_t s);
 // Resolves the device address of the no-allocation entry point's static
 // scratch on device dev (current); called by aeth_init and on first use.
 int aeth_noalloc_setup(int dev);
+// Batched product (m > 1) through a dequantized f32 weight and one rocBLAS
+// SGEMM (aeth_blas.cpp), for the formats without a matrix-core GEMM; rows of c
+// are ldc floats apart (0: n). Handles are per (device, stream);
+// aeth_blas_release_stream drops those of a stream.
+int aeth_dequant_gemm_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc,
+                             unsigned flags, hipStream_t s);
+void aeth_blas_release_stream(hipStream_t s);
 // Bytes of GEMM scratch (A fragments, sub-block sums, row scales) for m rows of k.
 int64_t aeth_gemm_ws_bytes(int64_t m, int64_t k);
 

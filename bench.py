@@ -135,6 +135,23 @@ def bench_gemm(torch, A, n, k, m, steps, warmup, seed=0xAE7E43, flags=0):
     return {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "raw0": raws[0], "a": a}
 
 
+def bench_batched(torch, A, dtype, n, k, m, steps, warmup, seed=0xAE7E47):
+    L = A.lib()
+    ws, _ = make_weights(torch, A, dtype, n, k, 2, seed)
+    a = torch.empty(m * k, dtype=torch.float32, device="cuda")
+    A.check(L.aeth_fill_normal_f32(seed ^ 0x77, a.data_ptr(), m * k, 0.0, 1.0, None))
+    c = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+
+    def step(i):
+        A.check(L.aeth_qmatmul(ws[i % 2], a.data_ptr(), m, c.data_ptr(), 0, s), "batched")
+
+    ms = time_launches(torch, step, steps, warmup)
+    for w in ws:
+        L.aeth_weight_free(w)
+    return {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+
+
 def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512, want_cpu=False):
     L = A.lib()
     cfg = A.LlamaConfig(vocab_size=128256, d_model=4096, num_layers=32, num_heads=32, num_kv_heads=8, head_dim=128,
@@ -362,9 +379,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,gemm,gemm_q8,decode",
-                    help="comma-separated extra sections to run: floor, q8, q6, q5, dotprod, gemm, gemm_q8, decode "
-                         "(default), f16, q2k (GGUF-order formats, not run by default)")
+    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,gemm,gemm_q8,gemm_q6k,decode",
+                    help="comma-separated extra sections to run: floor, q8, q6, q5, dotprod, gemm, gemm_q8, gemm_q6k, "
+                         "decode (default), f16, q2k (GGUF-order formats, not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (HBM counter calibration under rocprofv3)")
@@ -471,6 +488,11 @@ def main():
             print("[bench] Q4_K GEMM q8 n=%d: %s" % (nn, extra["q4_k_gemm_m512_n%d_q8act" % nn]), file=sys.stderr,
                   flush=True)
             del g
+    if "gemm_q6k" in sections:  # batched Q6_K (dequantized once, one SGEMM): a Q4_K_M file's attn_v / ffn_down
+        r = bench_batched(torch, A, 14, 4096, 4096, 512, max(3, min(args.steps, 20)), 2)
+        extra["q6_k_batched_m512_n4096"] = {"TFLOP/s": round(r["tflops"], 2), "ms": round(r["ms"], 4),
+                                             "path": "dequantized once, widened to f64, one rocBLAS DGEMM"}
+        print("[bench] Q6_K batched m=512: %s" % extra["q6_k_batched_m512_n4096"], file=sys.stderr, flush=True)
     if "decode" in sections:
         d = bench_decode(torch, A, want_cpu=want_cpu)
         cpu_in["dec"] = d.pop("cpu_model")

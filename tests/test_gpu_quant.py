@@ -419,7 +419,8 @@ def test_gguf_order_shape_rules(gpu):
 
 
 @pytest.mark.parametrize("dtype,m,n,k", [(Q2_K, 1, 40, 512), (Q2_K, 3, 8, 256), (Q3_K, 1, 300, 4096), (Q3_K, 5, 33, 768),
-                                         (F16, 1, 8, 32), (F16, 3, 8, 128), (F16, 2, 70, 100), (F16, 1, 1000, 4096)])
+                                         (F16, 1, 8, 32), (F16, 3, 8, 128), (F16, 2, 70, 100), (F16, 1, 1000, 4096),
+                                         (Q2_K, 20, 64, 512), (Q3_K, 40, 48, 1024), (F16, 24, 64, 256)])
 def test_row_kernels_standalone(gpu, dtype, m, n, k):
     """matmul_q2_k / matmul_q3_k / matmul_f16 on [n][k] rows against the x86
     dispatch (AVX2 order) — for F16 also the reference's own k = 32 / 128
@@ -618,3 +619,56 @@ def test_gemm_alternate_kernels(gpu, kernel):
     r = subprocess.run([sys.executable, "-c", GEMM_KERNEL_SCRIPT % root], env=env, cwd=root, timeout=240,
                        stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:]
+
+
+# Batched products of the block formats without a GEMM kernel of their own
+# (m >= 16): the weight is dequantized once and multiplied by one SGEMM —
+# planar Q8_0 / Q5_K / Q6_K rows (including Q8_0's ragged k and K-quant rows
+# whose tail past k/256 blocks the reference ignores), GGUF-order Q2_K / Q3_K,
+# accumulate, and the dot-product mode's Q8_0 activation blocks.
+@pytest.mark.parametrize("dtype,m,n,k", [(Q8_0, 16, 300, 1000), (Q8_0, 150, 512, 4096), (Q5_K, 70, 256, 2048),
+                                         (Q6_K, 150, 1024, 4096), (Q6_K, 33, 96, 14336), (Q5_K, 20, 64, 600)])
+def test_batched_dequant_gemm(gpu, dtype, m, n, k):
+    rng = np.random.default_rng(m + n + k + dtype)
+    raw = weight(dtype, n, k, 5 * n + k)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = make_weight(gpu, dtype, n, k, raw)
+    got = gemv(gpu, w, x, n, m)
+    y0 = rng.standard_normal(m * n).astype(np.float32)
+    got_acc = gemv(gpu, w, x, n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    got_q8 = gemv(gpu, w, x, n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(dtype, x, raw, m, n, k)
+    assert_close(got, ref, what="batched dtype %d m=%d n=%d k=%d" % (dtype, m, n, k))
+    assert_close(got_acc, ref + y0.reshape(m, n), what="batched accumulate")
+    ref_q8 = O.dotprod_ref(dtype, O.quantize_activations_q8_0(x, m, k), raw, m, n, k)
+    assert_close(got_q8, ref_q8, what="batched dot-product mode")
+
+
+@pytest.mark.parametrize("dtype,m,n,k", [(Q2_K, 40, 512, 1024), (Q3_K, 16, 768, 512), (Q3_K, 64, 300, 512)])
+def test_batched_dequant_gemm_gguf_order(gpu, dtype, m, n, k):
+    rng = np.random.default_rng(n + k + m)
+    raw = synth_blocks(dtype, n * k // 256, n + 3 * k + dtype)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    x[rng.integers(0, m * k, 9)] = 0.0
+    w = make_weight(gpu, dtype, n, k, raw)
+    got = gemv(gpu, w, x, n, m)
+    A.lib().aeth_weight_free(w)
+    assert_close(got, O.gguf_order_matmul(dtype, x, raw, m, n, k), what="batched gguf-order %d" % dtype)
+
+
+@pytest.mark.parametrize("dtype,m,n,k", [(Q4_K, 3, 40, 600), (Q6_K, 2, 48, 1000), (Q5_K, 20, 33, 300),
+                                         (Q4_K, 40, 64, 1300)])
+def test_dotprod_mode_batched_ragged_k(gpu, dtype, m, n, k):
+    """The reference's batched K-quant dotprod kernels read row r's activation
+    blocks from r·(k/256)·8 on (neon.rs:517-518, :994) while the quantizer lays
+    rows ceil(k/32) blocks apart: for k % 256 != 0 rows past the first see a
+    shifted window. The oracle restates that indexing; the device matches it."""
+    rng = np.random.default_rng(m + n + k)
+    raw = weight(dtype, n, k, 7 * n + k)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = make_weight(gpu, dtype, n, k, raw)
+    got = gemv(gpu, w, x, n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.dotprod_ref(dtype, O.quantize_activations_q8_0(x, m, k), raw, m, n, k)
+    assert_close(got, ref, what="batched ragged dotprod %d m=%d k=%d" % (dtype, m, k))
