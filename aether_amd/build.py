@@ -18,6 +18,7 @@ SOURCES = [
     "aeth_gemv.hip",
     "aeth_gemv_ext.hip",
     "aeth_gemm.hip",
+    "aeth_gemm_kq.hip",
     "aeth_decode_ops.hip",
     "aeth_prefill.hip",
     "aeth_backend.hip",
@@ -36,10 +37,11 @@ def hipcc():
     return "hipcc"
 
 
-# per-source device flags: the GEMM keeps its MFMA accumulators in VGPRs (one
-# wave per SIMD leaves room for them), avoiding AGPR→VGPR copies in its epilogue
+# per-source device flags: the GEMMs keep their MFMA accumulators in VGPRs, where
+# the per-super-block epilogues operate on them without AGPR→VGPR copies
 EXTRA = {
     "aeth_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "aeth_gemm_kq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 COMMON = [

@@ -1,0 +1,122 @@
+// Shared pieces of the Q4_K prefill GEMM kernels (aeth_gemm.hip, aeth_gemm_kq.hip):
+// operand types, the packed-fp16 weight dequantisation, LDS reads under manual
+// lgkmcnt and the XCD-aware tile order.
+#pragma once
+#include <stdint.h>
+
+#include "aeth_common.hpp"
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) char lds_char;
+
+// positions 1 and 2 of each group of 4 exchanged (an involution)
+__device__ __forceinline__ int perm4(int i) { return (i & ~3) | ((0x3120 >> (4 * (i & 3))) & 3); }
+
+// bytes (b0, b1, b2, b3) of w as fp16 pairs (b0, b1) and (b2, b3): (0x64 | b) is 1024 + b
+__device__ __forceinline__ void bytes_to_h2(uint32_t w, half2_t& p01, half2_t& p23) {
+    const half2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    p01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, 0x07010700u)) + k1024;
+    p23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, 0x07030702u)) + k1024;
+}
+
+__device__ __forceinline__ uint32_t pkfma(uint32_t q, half2_t s, half2_t z) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2_t, q), s, z));
+}
+
+// Eight quants of (x, y) → an fp16 MFMA operand (k-order [0, 2, 1, 3] per 4).
+// The nibble pairs come from one v_and_or_b32 each: MASK 0x000F000F keeps the
+// low nibbles of bytes (0, 2) as halves 1024 + q (scales s = sc, z = −1024·sc),
+// MASK 0x00F000F0 the high nibbles as 1024 + 16q (s = sc/16, z = −64·sc); bytes
+// (1, 3) after a shift by 8 (x8, y8). c64 holds 0x64006400 in a VGPR, so that
+// the OR's constant does not need a second scalar operand (VOP3 takes one).
+// Every result q·sc ≤ 945 is an exact fp16 integer (the fused product is exact).
+template <uint32_t MASK>
+__device__ __forceinline__ half8_t dq8s(uint32_t x, uint32_t y, uint32_t x8, uint32_t y8, uint32_t c64, half2_t s,
+                                        half2_t z) {
+    const uint32_t q0 = pkfma((x & MASK) | c64, s, z);
+    const uint32_t q1 = pkfma((x8 & MASK) | c64, s, z);
+    const uint32_t q2 = pkfma((y & MASK) | c64, s, z);
+    const uint32_t q3 = pkfma((y8 & MASK) | c64, s, z);
+    return __builtin_bit_cast(half8_t, make_uint4(q0, q1, q2, q3));
+}
+template <uint32_t MASK>
+__device__ __forceinline__ half8_t dq8(uint32_t x, uint32_t y, uint32_t c64, half2_t s, half2_t z) {
+    return dq8s<MASK>(x, y, x >> 8, y >> 8, c64, s, z);
+}
+
+// LDS reads issued as inline asm: the compiler would otherwise order every LDS
+// read after all outstanding direct-to-LDS loads (vmcnt(0)), since it cannot
+// tell the ring's slots apart. Kernels wait with lgkmcnt themselves, then pass
+// each value through pin() so no use is scheduled above its wait.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_char*)p; }
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_b128(uint32_t a) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ half8_t lds_b128h(uint32_t a) {
+    half8_t v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_b64(uint32_t a) {
+    u32x2 v;
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+// two 8-byte reads, at a and a + 256
+__device__ __forceinline__ u32x4 lds_2b64_256(uint32_t a) {
+    u32x4 v;
+    asm volatile("ds_read2_b64 %0, %1 offset1:32" : "=v"(v) : "v"(a));
+    return v;
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (N << 8) | (3 << 14));  // vmcnt, expcnt at their maximum
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));  // lgkmcnt at its maximum
+}
+template <class T>
+__device__ __forceinline__ void pin(T& v) {
+    asm volatile("" : "+v"(v));
+}
+
+// Workgroup → tile: the 8 XCDs take workgroup ids round-robin; each XCD gets a
+// contiguous run of tiles, ordered in groups of 4 row-tiles so that the
+// workgroups resident on one XCD share A rows and weight tiles in its L2.
+__device__ __forceinline__ void g2_tile(int id, int gm, int gn, int& tm, int& tn) {
+    const int T = gm * gn;
+    if ((T & 7) == 0) id = (id & 7) * (T >> 3) + (id >> 3);
+    const int GM = 4, per = GM * gn, grp = id / per, first = grp * GM, rows = min(GM, gm - first);
+    const int in = id - grp * per;
+    tm = first + in % rows;
+    tn = in / rows;
+}
+
+// Arguments of the K-split GEMM kernel (aeth_gemm_kq.hip).
+struct KqArgs {
+    const uint8_t* frag;   // A·2^-e as fp16 MFMA fragments: ((mt·(k/16) + ks)·2 + part)·1 KiB (k_gemm_prep)
+    const uint8_t* sums;   // sub-block sums of A·2^-(e+5): hi [mp][k/32] then lo [mp][k/32] (fp16)
+    const float* escale;   // [mp]: 2^e
+    const uint8_t* hdr;    // Q4_K tile layout (aeth_q4k_hdr_off)
+    const uint8_t* qs;     // Q4_K tile layout (aeth_q4k_qs_off)
+    int m, n, k, nb, ntiles, mp;
+    int gm, gn;            // 64-row and 128-column tiles of C
+    int a_bytes, s_bytes, q_bytes, h_bytes;  // buffer extents (each < 2^31)
+    float* C;
+    int64_t ldc;
+    int accumulate;
+};
+int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s);

@@ -1,0 +1,324 @@
+// Q4_K prefill GEMM, K-split form (m > 1):  C[m][n] = Σ_k A[m][k]·W[n][k]
+// (avx2::matmul_q4_k with m rows, src/quant/avx2.rs:23-57; quantized_matmul_impl).
+//
+// Operands as in the exact mode of aeth_gemm.hip: A·2^-e split into fp16 hi/lo
+// MFMA fragments (k_gemm_prep), weights as exact fp16 integers q·sc, f32
+// accumulation on v_mfma_f32_32x32x16_f16; the mins enter per super-block through
+// the sub-block sums S (one more MFMA, k = 8 sub-blocks × {hi, lo}).
+//
+// Work split. A workgroup owns a 64 × 128 tile of C and has 8 waves, two per
+// SIMD; wave w computes the whole tile over the w-th eighth of the super-blocks.
+// A wave so holds 2 m-tiles × 4 column tiles of accumulators: every A fragment it
+// reads feeds 4 MFMAs and every dequantised weight fragment 4 (2 m-tiles × {hi,
+// lo}). The waves share no data: each streams its own A fragments, quants,
+// headers and sub-block sums into a private LDS ring with direct-to-LDS buffer
+// loads and waits for them with its own vmcnt, so the main loop has no barrier;
+// the two waves of a SIMD cover each other's waits. The eight partial tiles meet
+// in LDS at the end and are summed in a fixed order (deterministic).
+//
+// One accumulator per output. A column's contribution of super-block b is
+// d_b·P_b − 32·dmin_b·Q_b (P_b = Σ A·(q·sc) from the MFMAs, Q_b = Σ_s m_s·S_s).
+// Instead of a separate P_b per super-block the accumulator U holds the running
+// sum in units of the current scale D_b (= d_b; a zero d_b keeps the previous
+// scale and zeroes the super-block's weight operands): entering b, U ← U·D_{b-1}/D_b
+// (one multiply per output), the MFMAs then add P_b in place, and leaving b,
+// U ← U + (−32·dmin_b/D_b)·Q_b; the result is D_last·U. The rescaling rounds once
+// per super-block, at the level of the running sum, like the f32 sum it replaces.
+//
+// Ring. A slice is 16 K positions: 4 A fragments of 1 KiB (2 m-tiles × {hi, lo}).
+// Two consecutive slices read the low and the high nibbles of the same quant
+// bytes qs[32J + 16kg, +16) (128 rows × 16 B = 2 KiB, loaded with the first).
+// A super-block's first slice also loads its headers (128 × 16 B) and the 64
+// rows' sub-block sums (2 KiB), which the wave copies to registers when it starts
+// the super-block. Per wave: 3 A slots, 2 quant slots, 1 header slot (20 KiB);
+// slice s + 2 is issued before slice s is computed.
+#include <math.h>
+#include <stdint.h>
+
+#include "aeth_common.hpp"
+#include "aeth_gemm_common.hpp"
+#include "aeth_internal.hpp"
+
+#define K8_A 4096                                       // A fragments of a slice
+#define K8_NA 3                                         // A slots
+#define K8_B 2048                                       // quants of a slice pair
+#define K8_HS 4096                                      // headers + sub-block sums of a super-block
+#define K8_BOFF (K8_NA * K8_A)                          // quant slots
+#define K8_HOFF (K8_BOFF + 2 * K8_B)                    // header slot
+#define K8_WAVE (K8_HOFF + K8_HS)                       // LDS per wave: 20 KiB
+#define K8_W 8                                          // waves
+
+// buffer loads issued for slice s (s = position in the wave's run)
+__host__ __device__ constexpr int k8_loads(int s) { return 4 + ((s & 1) == 0 ? 2 : 0) + ((s & 15) == 0 ? 4 : 0); }
+
+__global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
+    __shared__ __attribute__((aligned(1024))) char smem[K8_W * K8_WAVE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tm, tn;
+    g2_tile(blockIdx.x, G.gm, G.gn, tm, tn);
+    const int n0 = tn * 128, m0 = tm * 64, t0 = n0 >> 4;
+    const int nb = G.nb, nks = G.k >> 4, ksb = G.k >> 5;
+    const int sb0 = nb * wave / K8_W, nsb = nb * (wave + 1) / K8_W - sb0, ns = 16 * nsb;
+    char* wl = smem + wave * K8_WAVE;
+    const uint32_t wl_lds = lds_addr(wl);
+
+    // buffer resources; per-lane offsets are fixed, per-slice offsets go in the scalar offset
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)G.frag, (short)0, G.a_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc((void*)G.sums, (short)0, G.s_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rQ = __builtin_amdgcn_make_buffer_rsrc((void*)G.qs, (short)0, G.q_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rH = __builtin_amdgcn_make_buffer_rsrc((void*)G.hdr, (short)0, G.h_bytes, 0x00020000);
+    // DMA piece i (i = 0, 1) of quants / headers: lane → row tile 4i + lane/16 of the workgroup's 8, row lane%16
+    uint32_t q_v[2], h_v[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int t = min(t0 + 4 * i + (lane >> 4), G.ntiles - 1);  // tiles past the last: clamped, never stored
+        q_v[i] = (uint32_t)(t * nb * 2048 + (lane & 15) * 16);
+        h_v[i] = (uint32_t)(t * nb * 256 + (lane & 15) * 16);
+    }
+    // sub-block sums of m-tile mt: lane → row m0 + 32mt + lane%32, hi (lane < 32) or lo
+    uint32_t s_v[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        const int row = min(m0 + 32 * mt + (lane & 31), G.mp - 1);
+        s_v[mt] = (uint32_t)(((lane >> 5) * G.mp * ksb + row * ksb) * 2);
+    }
+    const uint32_t a_v = (uint32_t)(lane * 16);
+
+    // Slice s of this wave. Slices past the run (the ring's tail) repeat the last
+    // slice's data into free slots, so every slice issues the loads k8_loads(s) counts.
+    auto issue = [&](int s) {
+        const int se = min(s, ns - 1);
+        const int b = sb0 + (se >> 4), J = (se >> 2) & 3, kg = (se >> 1) & 1, nib = se & 1;
+        const int ks = 16 * b + 4 * J + 2 * nib + kg;
+        char* sa = wl + (s % K8_NA) * K8_A;
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void*)(sa + (mt * 2 + p) * 1024), 16, a_v,
+                                                         (((2 * tm + mt) * nks + ks) * 2 + p) * 1024, 0, 0);
+        if ((s & 1) == 0) {
+            char* sq = wl + K8_BOFF + ((s >> 1) & 1) * K8_B;
+            const int qoff = b * 2048 + (J >> 1) * 1024 + (2 * (J & 1) + kg) * 256;
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void*)(sq + i * 1024), 16, q_v[i], qoff, 0, 0);
+        }
+        if ((s & 15) == 0) {
+            char* hs = wl + K8_HOFF;
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rH, (lds_void*)(hs + i * 1024), 16, h_v[i], b * 256, 0, 0);
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(hs + 2048 + mt * 1024), 16, s_v[mt], b * 16, 0,
+                                                         0);
+        }
+    };
+
+    // LDS offsets of column tile c: quants of lane (col, k-group lane/32), header of col
+    int b_off[4], h_off[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int col = 32 * c + (lane & 31);
+        b_off[c] = (col >> 4) * 256 + (col & 15) * 16 + 8 * (lane >> 5);
+        h_off[c] = (col >> 4) * 256 + (col & 15) * 16;
+    }
+
+    f32x16 U[2][4];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) U[mt][c] = (f32x16){};
+    float D[4] = {1.0f, 1.0f, 1.0f, 1.0f};  // current scale of column tile c (this lane's column)
+    u32x4 hd[4] = {};
+    half8_t sv[2] = {};
+    half2_t sp[4] = {}, zp[4] = {};
+    u32x2 raw[4] = {};
+    uint32_t x8[4] = {}, y8[4] = {};
+    uint32_t c64;  // 0x64006400 in a VGPR (see dq8s)
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(c64));
+
+    if (ns > 0) {
+        issue(0);
+        issue(1);
+    }
+    for (int bi = 0; bi < nsb; bi++) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int s = 16 * bi + j;
+            const int nib = j & 1;
+            // slice s has landed when only slice s + 1's loads are outstanding
+            const int nxt = k8_loads(j + 1);  // 4, 6 or 10 (folded: j is unrolled)
+            if (nxt == 10) vm_wait<10>();
+            else if (nxt == 6) vm_wait<6>();
+            else vm_wait<4>();
+            issue(s + 2);
+            const uint32_t sa = wl_lds + (s % K8_NA) * K8_A;
+            const uint32_t sq = wl_lds + K8_BOFF + ((j >> 1) & 1) * K8_B;
+            if (j == 0) {
+                const uint32_t hs = wl_lds + K8_HOFF;
+#pragma unroll
+                for (int c = 0; c < 4; c++) hd[c] = lds_b128<0>(hs + h_off[c]);
+                sv[0] = lds_b128h<2048>(hs + a_v);
+                sv[1] = lds_b128h<3072>(hs + a_v);
+            }
+            if (nib == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) raw[c] = lds_b64<0>(sq + b_off[c]);
+            }
+            half8_t a[2][2];  // [mt][part]
+            a[0][0] = lds_b128h<0>(sa + a_v);
+            a[0][1] = lds_b128h<1024>(sa + a_v);
+            a[1][0] = lds_b128h<2048>(sa + a_v);
+            a[1][1] = lds_b128h<3072>(sa + a_v);
+            lgkm_wait<4>();  // all but the A fragments
+            if (j == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) pin(hd[c]);
+                pin(sv[0]);
+                pin(sv[1]);
+                // entering the super-block: rescale U to this block's d (a zero d keeps the scale;
+                // its weights are zeroed through the scales below)
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float d = aeth_decode_d(hd[c][0]);
+                    const float Dn = d != 0.0f ? d : D[c];
+                    if (bi > 0) {
+                        const float r = D[c] / Dn;
+#pragma unroll
+                        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                            for (int q = 0; q < 16; q++) U[mt][c][q] *= r;
+                    }
+                    D[c] = Dn;
+                }
+            }
+            if ((j & 3) == 0) {
+                // scales of sub-blocks 2J (low nibbles) and 2J + 1 (high nibbles), get_scale_min_k4
+                // (common.rs:29-38): sp = (sc, sc'/16), zp = (−1024·sc, −64·sc'), used as broadcast
+                // halves; all zero when the block's d is zero
+                const int J = j >> 2;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const uint32_t y = hd[c][1], w = hd[c][3];
+                    uint32_t sc4 = J < 2 ? (y & 0x3F3F3F3Fu) : ((w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u));
+                    if ((hd[c][0] & 0x7FFFu) == 0u) sc4 = 0u;  // d = ±0
+                    half2_t p01, p23;
+                    bytes_to_h2(sc4, p01, p23);
+                    const half2_t pr = (J & 1) ? p23 : p01;
+                    const half2_t k_s = {(_Float16)1.0f, (_Float16)0.0625f};
+                    const half2_t k_z = {(_Float16)-1024.0f, (_Float16)-64.0f};
+                    sp[c] = pr * k_s;
+                    zp[c] = pr * k_z;
+                }
+            }
+            if (nib == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    pin(raw[c]);
+                    x8[c] = raw[c][0] >> 8;
+                    y8[c] = raw[c][1] >> 8;
+                }
+            }
+            half8_t bv[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                if (nib == 0)
+                    bv[c] = dq8s<0x000F000Fu>(raw[c][0], raw[c][1], x8[c], y8[c], c64,
+                                              __builtin_shufflevector(sp[c], sp[c], 0, 0),
+                                              __builtin_shufflevector(zp[c], zp[c], 0, 0));
+                else
+                    bv[c] = dq8s<0x00F000F0u>(raw[c][0], raw[c][1], x8[c], y8[c], c64,
+                                              __builtin_shufflevector(sp[c], sp[c], 1, 1),
+                                              __builtin_shufflevector(zp[c], zp[c], 1, 1));
+            }
+            lgkm_wait<0>();
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                pin(a[mt][0]);
+                pin(a[mt][1]);
+            }
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        U[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt][p], bv[c], U[mt][c], 0, 0, 0);
+            if (j == 15) {
+                // leaving the super-block: U += (−32·dmin/D)·Σ_s m_s·S_s (S carries 2^-(e+5))
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float ndm = -32.0f * aeth_decode_d(hd[c][0] >> 16) / D[c];
+                    const uint32_t z = hd[c][2], w = hd[c][3];
+                    half2_t m01, m23, m45, m67;
+                    bytes_to_h2(z & 0x3F3F3F3Fu, m01, m23);
+                    bytes_to_h2(((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u), m45, m67);
+                    const half8_t mv = {m01[0], m01[1], m23[0], m23[1], m45[0], m45[1], m67[0], m67[1]};
+#pragma unroll
+                    for (int mt = 0; mt < 2; mt++) {
+                        const f32x16 q = __builtin_amdgcn_mfma_f32_32x32x16_f16(sv[mt], mv, (f32x16){}, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) U[mt][c][r] = fmaf(ndm, q[r], U[mt][c][r]);
+                    }
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the tail's loads have landed
+    __syncthreads();                // and every wave is done with its ring
+
+    // The eight K-eighth tiles meet in LDS. Round 1: waves 4..7 hand theirs to
+    // waves 0..3 (slot [w - 4]); round 2: waves 0..3 write the pair sums and wave w
+    // (0..7) sums (mt, c) = (w / 4, w % 4) over them in order and stores it.
+    float* red = (float*)smem;  // [4][2][4][16][64] floats = 128 KiB
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) U[mt][c][r] *= D[c];
+    if (wave >= 4) {
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) red[((((wave - 4) * 2 + mt) * 4 + c) * 16 + r) * 64 + lane] = U[mt][c][r];
+    }
+    __syncthreads();
+    if (wave < 4) {
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int i = (((wave * 2 + mt) * 4 + c) * 16 + r) * 64 + lane;
+                    red[i] = U[mt][c][r] + red[i];
+                }
+    }
+    __syncthreads();
+    const int mt = wave >> 2, c = wave & 3, lr = lane & 31;
+    const int col = n0 + 32 * c + lr;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        float sum = red[(((0 * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < 4; w++) sum += red[(((w * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
+        const int row = m0 + 32 * mt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < G.m && col < G.n) {
+            const float v = sum * G.escale[row];
+            float* dst = G.C + (int64_t)row * G.ldc + col;
+            *dst = G.accumulate ? *dst + v : v;
+        }
+    }
+}
+
+int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s) {
+    hipLaunchKernelGGL(k_gemm_q4k_kq, dim3((unsigned)(G.gm * G.gn)), dim3(64 * K8_W), 0, s, G);
+    AETH_LAUNCH_CHECK();
+    return AETH_OK;
+}

@@ -335,7 +335,10 @@ def test_runner_mixed_formats(gpu, mix, n):
         A.check(L.aeth_runner_prefill(r, toks.ctypes.data, n, logits.ctypes.data, None), "prefill")
         ref = O.forward_batch(ocfg, m["emb"][toks], m["layers"], MIXED[mix], m["norms"], m["final"], m["lm"],
                               m["lm_dtype"], s, co, kv)
-        assert_close_logits(logits, ref, what="mixed prefill n=%d" % n)
+        # anchored on the float64 evaluation: at n = 150 the reference's own f32 logits
+        # drift from it by 1.8e-5·max|row|, past the plain floor
+        exact = logits64(c, m["emb"], m["layers"], MIXED[mix], m["norms"], m["final"], m["lm"], m["lm_dtype"], toks)
+        assert_close_logits(logits, ref, what="mixed prefill n=%d" % n, exact=exact)
         fill = n
         tok = O.argmax(ref)
         for step in range(2):
