@@ -62,6 +62,7 @@ _SIGS = {
     "aeth_quantized_matmul_dotprod": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P]),
     "aeth_quantized_matmul_impl_cached": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _INT, _P, _P]),
     "aeth_stream_read": (_INT, [_P, _I64, _P, _I64, _P]),
+    "aeth_mfma_rate": (_INT, [_INT, _INT, _INT, _P, _P]),
     "aeth_matmul_q8_0": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q4_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "aeth_matmul_q5_k": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P]),

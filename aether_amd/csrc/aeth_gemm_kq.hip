@@ -85,27 +85,30 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
     }
     const uint32_t a_v = (uint32_t)(lane * 16);
 
-    // Slice s of this wave. Slices past the run (the ring's tail) repeat the last
-    // slice's data into free slots, so every slice issues the loads k8_loads(s) counts.
-    auto issue = [&](int s) {
-        const int se = min(s, ns - 1);
-        const int b = sb0 + (se >> 4), J = (se >> 2) & 3, kg = (se >> 1) & 1, nib = se & 1;
-        const int ks = 16 * b + 4 * J + 2 * nib + kg;
-        char* sa = wl + (s % K8_NA) * K8_A;
+    // Loads of slice s = 16·(b − sb0) + jl of this wave, into A slot sa (a byte
+    // offset in the wave's LDS). Offsets are a per-super-block scalar base plus
+    // constants (jl is known at compile time). Slices past the run (the ring's
+    // tail) read whatever lies beyond it: the next K range's data, or zeros past
+    // a buffer's extent (buffer loads check it); their slots are never read.
+    const int aB0 = 2 * tm * nks * 2048, aB1 = (2 * tm + 1) * nks * 2048;  // A fragments of the two m-tiles
+    auto issue = [&](int b, int jl, int sa) {
+        const int J = jl >> 2, kg = (jl >> 1) & 1, nib = jl & 1;
+        const int kso = b * 32768 + (4 * J + 2 * nib + kg) * 2048;
+        char* st = wl + sa;
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
             for (int p = 0; p < 2; p++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void*)(sa + (mt * 2 + p) * 1024), 16, a_v,
-                                                         (((2 * tm + mt) * nks + ks) * 2 + p) * 1024, 0, 0);
-        if ((s & 1) == 0) {
-            char* sq = wl + K8_BOFF + ((s >> 1) & 1) * K8_B;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void*)(st + (mt * 2 + p) * 1024), 16, a_v,
+                                                         (mt ? aB1 : aB0) + kso + p * 1024, 0, 0);
+        if ((jl & 1) == 0) {
+            char* sq = wl + K8_BOFF + ((jl >> 1) & 1) * K8_B;
             const int qoff = b * 2048 + (J >> 1) * 1024 + (2 * (J & 1) + kg) * 256;
 #pragma unroll
             for (int i = 0; i < 2; i++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void*)(sq + i * 1024), 16, q_v[i], qoff, 0, 0);
         }
-        if ((s & 15) == 0) {
+        if (jl == 0) {
             char* hs = wl + K8_HOFF;
 #pragma unroll
             for (int i = 0; i < 2; i++)
@@ -141,21 +144,27 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
     asm("v_mov_b32 %0, 0x64006400" : "=v"(c64));
 
     if (ns > 0) {
-        issue(0);
-        issue(1);
+        issue(sb0, 0, 0);
+        issue(sb0, 1, K8_A);
     }
+    int s3 = 0;  // (16·bi) mod 3: slice 16·bi + j uses A slot (s3 + j) mod 3
     for (int bi = 0; bi < nsb; bi++) {
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            const int s = 16 * bi + j;
             const int nib = j & 1;
             // slice s has landed when only slice s + 1's loads are outstanding
             const int nxt = k8_loads(j + 1);  // 4, 6 or 10 (folded: j is unrolled)
             if (nxt == 10) vm_wait<10>();
             else if (nxt == 6) vm_wait<6>();
             else vm_wait<4>();
-            issue(s + 2);
-            const uint32_t sa = wl_lds + (s % K8_NA) * K8_A;
+            {
+                int sl = s3 + (j + 2) % 3;
+                sl = sl >= 3 ? sl - 3 : sl;
+                issue(sb0 + bi + (j + 2) / 16, (j + 2) & 15, sl * K8_A);
+            }
+            int sc3 = s3 + j % 3;
+            sc3 = sc3 >= 3 ? sc3 - 3 : sc3;
+            const uint32_t sa = wl_lds + sc3 * K8_A;
             const uint32_t sq = wl_lds + K8_BOFF + ((j >> 1) & 1) * K8_B;
             if (j == 0) {
                 const uint32_t hs = wl_lds + K8_HOFF;
@@ -186,7 +195,7 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
                     const float d = aeth_decode_d(hd[c][0]);
                     const float Dn = d != 0.0f ? d : D[c];
                     if (bi > 0) {
-                        const float r = D[c] / Dn;
+                        const float r = D[c] * __builtin_amdgcn_rcpf(Dn);  // one rounding per block
 #pragma unroll
                         for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -251,7 +260,7 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
                 // leaving the super-block: U += (−32·dmin/D)·Σ_s m_s·S_s (S carries 2^-(e+5))
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    const float ndm = -32.0f * aeth_decode_d(hd[c][0] >> 16) / D[c];
+                    const float ndm = -32.0f * aeth_decode_d(hd[c][0] >> 16) * __builtin_amdgcn_rcpf(D[c]);
                     const uint32_t z = hd[c][2], w = hd[c][3];
                     half2_t m01, m23, m45, m67;
                     bytes_to_h2(z & 0x3F3F3F3Fu, m01, m23);
@@ -266,6 +275,7 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
                 }
             }
         }
+        s3 = s3 == 2 ? 0 : s3 + 1;
     }
     __builtin_amdgcn_s_waitcnt(0);  // the tail's loads have landed
     __syncthreads();                // and every wave is done with its ring

@@ -493,3 +493,52 @@ extern "C" AETH_API int aeth_stream_read(const void* d_src, int64_t bytes, uint3
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
+
+// Matrix-core rate of this GPU (measurement kernel): every wave issues `iters`
+// rounds of 8 independent MFMAs — kind 0: v_mfma_f32_32x32x16_f16 (32768
+// flops each), kind 1: v_mfma_i32_32x32x32_i8 (65536 ops each) — on register
+// operands, one wave per SIMD (256 threads per workgroup). The MFMA peak the
+// GEMM's fraction is quoted against, as the box sustains it.
+typedef _Float16 mr_h8 __attribute__((ext_vector_type(8)));
+typedef float mr_f16x __attribute__((ext_vector_type(16)));
+typedef int mr_i16x __attribute__((ext_vector_type(16)));
+typedef int mr_i4 __attribute__((ext_vector_type(4)));
+template <int KIND>
+__global__ void __launch_bounds__(256) k_mfma_rate(int iters, float* __restrict__ sink) {
+    mr_h8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = (_Float16)(threadIdx.x * 0.001f + i);
+        b[i] = (_Float16)(i * 0.5f);
+    }
+    const mr_i4 ai = {(int)threadIdx.x, 1, 2, 3}, bi = {3, 2, 1, (int)threadIdx.x};
+    mr_f16x acc[8];
+    mr_i16x iacc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        acc[j] = (mr_f16x){};
+        iacc[j] = (mr_i16x){};
+    }
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (KIND == 0) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[j], 0, 0, 0);
+            else iacc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ai, bi, iacc[j], 0, 0, 0);
+        }
+    }
+    float t = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) t += acc[j][0] + (float)iacc[j][0];
+    if (t == 12345.0f) sink[blockIdx.x * 256 + threadIdx.x] = t;
+}
+
+extern "C" AETH_API int aeth_mfma_rate(int kind, int iters, int workgroups, float* d_sink, void* stream) {
+    if ((kind != 0 && kind != 1) || iters <= 0 || workgroups <= 0 || !d_sink)
+        return aeth_set_error(AETH_EINVAL, "aeth_mfma_rate: bad argument");
+    if (kind == 0)
+        hipLaunchKernelGGL(k_mfma_rate<0>, dim3((unsigned)workgroups), dim3(256), 0, (hipStream_t)stream, iters, d_sink);
+    else
+        hipLaunchKernelGGL(k_mfma_rate<1>, dim3((unsigned)workgroups), dim3(256), 0, (hipStream_t)stream, iters, d_sink);
+    AETH_LAUNCH_CHECK();
+    return AETH_OK;
+}

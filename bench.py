@@ -117,6 +117,22 @@ def bench_read_floor(torch, A, nbytes, steps, warmup, copies=16):
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9}
 
 
+def bench_mfma_rate(torch, A, kind, iters=2000, workgroups=256):
+    """Matrix-core rate the box sustains (aeth_mfma_rate): kind 0 fp16
+    v_mfma_f32_32x32x16_f16, kind 1 int8 v_mfma_i32_32x32x32_i8, one wave per
+    SIMD of independent MFMAs on register operands; TFLOP/s or TOP/s."""
+    L = A.lib()
+    sink = torch.empty(workgroups * 256, dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+
+    def step(i):
+        A.check(L.aeth_mfma_rate(kind, iters, workgroups, sink.data_ptr(), s), "mfma_rate")
+
+    ms = time_launches(torch, step, 5, 2)
+    ops = (32768 if kind == 0 else 65536) * 8 * iters * workgroups * 4
+    return ops / (ms * 1e-3) / 1e12
+
+
 def bench_gemm(torch, A, n, k, m, steps, warmup, seed=0xAE7E43, flags=0):
     L = A.lib()
     copies = 2
@@ -379,7 +395,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,gemm,gemm_q8,gemm_q6k,decode",
+    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,decode",
                     help="comma-separated extra sections to run: floor, q8, q6, q5, dotprod, gemm, gemm_q8, gemm_q6k, "
                          "decode (default), f16, q2k (GGUF-order formats, not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -466,6 +482,14 @@ def main():
             extra[key] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),
                           "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
             print("[bench] %s: %s" % (key, extra[key]), file=sys.stderr, flush=True)
+    mfma = None
+    if "mfma" in sections:  # the matrix-core rates this box sustains (the GEMM's measured roofline)
+        mfma = {"fp16_TFLOP/s": round(bench_mfma_rate(torch, A, 0), 1),
+                "int8_TOP/s": round(bench_mfma_rate(torch, A, 1), 1)}
+        mfma["frac_of_spec"] = {"fp16": round(mfma["fp16_TFLOP/s"] / FP16_PEAK_TFLOPS, 4),
+                                "int8": round(mfma["int8_TOP/s"] / INT8_PEAK_TOPS, 4)}
+        extra["mfma_rate_measured"] = mfma
+        print("[bench] MFMA rate: %s" % mfma, file=sys.stderr, flush=True)
     if "gemm" in sections:
         gsteps, gwarm = max(3, min(args.steps, 50)), max(1, min(args.warmup, 5))
         for nn in (4096, 14336):
@@ -474,6 +498,9 @@ def main():
                                                  "frac_int8_peak": round(g["tflops"] / INT8_PEAK_TOPS, 4),
                                                  "frac_fp16_peak": round(g["tflops"] / FP16_PEAK_TFLOPS, 4),
                                                  "steps": gsteps, "mode": "exact (f32 activations)"}
+            if mfma:  # the exact mode runs two fp16 MFMA passes per product: its ceiling is half the fp16 rate
+                extra["q4_k_gemm_m512_n%d" % nn]["frac_exact_mode_ceiling"] = round(
+                    g["tflops"] / (mfma["fp16_TFLOP/s"] / 2), 4)
             print("[bench] Q4_K GEMM n=%d: %s" % (nn, extra["q4_k_gemm_m512_n%d" % nn]), file=sys.stderr, flush=True)
             if want_cpu:
                 cpu_in["gemm"][nn] = (g["raw0"].cpu().numpy(), g["a"].cpu().numpy())

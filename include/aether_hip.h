@@ -276,6 +276,13 @@ AETH_API int aeth_fill_normal_f32(uint64_t seed, float* d_out, int64_t n, float 
  * the GEMVs). d_sink holds sink_words >= 512 words; a word is written only if
  * the fold of the input hits one fixed value. */
 AETH_API int aeth_stream_read(const void* d_src, int64_t bytes, uint32_t* d_sink, int64_t sink_words, void* stream);
+/* Measurement kernel, no counterpart in the reference: `workgroups` × 4 waves
+ * each issue iters × 8 independent matrix-core instructions on register
+ * operands — kind 0: v_mfma_f32_32x32x16_f16 (32768 flops each), kind 1:
+ * v_mfma_i32_32x32x32_i8 (65536 ops each): the rate the box sustains (the
+ * GEMM's second roofline). d_sink holds workgroups × 256 floats; a value is
+ * written only if a fold of the results hits one fixed value. */
+AETH_API int aeth_mfma_rate(int kind, int iters, int workgroups, float* d_sink, void* stream);
 
 /* ── LlamaRunner (src/inference/runner.rs) on the device ─────────────────
  * Model shape = LlamaConfig (model_loader.rs:71-84). */
