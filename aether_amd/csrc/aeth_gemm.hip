@@ -61,13 +61,15 @@
 //    (nks = k/16): lane l holds row 32·mt + l%32 at k-positions
 //    16·ks + 8·(l/32) + perm4(i), i < 8, of A·2^-e, part 0 = hi, 1 = lo;
 //  * Sh/Sl [row][k/32] = Σ of each 32-element sub-block of A·2^-(e+5), hi/lo.
-// Workgroup = 4 rows, one wave per row (512 rows: 128 workgroups). The row is read in
+// Workgroup = 2 rows, one wave per row (512 rows: 256 workgroups, one per CU;
+// 1 and 4 rows per workgroup measured slower). The row is read in
 // chunks of 4096 elements with every load of a chunk in flight; pass 2 converts
 // a row of one chunk from registers and re-reads longer rows (from cache). Lane
 // l converts the 8-element groups gi = l + 64·it, group gi being (k-slice gi/2,
 // k-group gi%2) of the row's fragment lane; a step's pieces go through LDS so
-// that each store writes the 4 rows' pieces of a fragment as 64 contiguous bytes. A 32-element sub-block is the groups of four adjacent lanes; its
-// sums (and its Q8_0 block) meet by DPP.
+// that each store writes the 2 rows' pieces of a fragment as 32 contiguous
+// bytes. A 32-element sub-block is the groups of four adjacent lanes; its sums
+// (and its Q8_0 block) meet by DPP.
 //
 // Q8 = true (AETH_MM_Q8_ACTIVATIONS, the dot-product mode): each 32-element
 // sub-block is first replaced by its Q8_0 activation block, dequantized —
@@ -102,7 +104,7 @@ __device__ __forceinline__ void prep_load_chunk(const float* __restrict__ a, int
     }
 }
 
-#define PREP_ROWS 4
+#define PREP_ROWS 2
 #define PREP_LD 5  // LDS stride in 16-byte pieces between groups (5: lanes spread over the banks)
 template <bool AL16, bool Q8>
 __global__ void __launch_bounds__(64 * PREP_ROWS) k_gemm_prep(const float* __restrict__ A, int m, int k,
