@@ -55,21 +55,27 @@
 #define G2_LOADS 6
 
 // ── activation prep (f32 A [m][k]; rows m..mp-1 read as zero). Writes
-//  * escale[r] = 2^e, e ≥ 0 the least with |A[r]·2^-e| < 2^14 (pass 1: the row
-//    maximum, 16 loads per lane in flight);
+//  * escale[r] = 2^e, e ≥ 0 the least with |A[r]·2^-e| < 2^14;
 //  * fragment (mt, ks, part) = 1 KiB at ((mt·nks + ks)·2 + part)·1024 bytes
 //    (nks = k/16): lane l holds row 32·mt + l%32 at k-positions
 //    16·ks + 8·(l/32) + perm4(i), i < 8, of A·2^-e, part 0 = hi, 1 = lo;
 //  * Sh/Sl [row][k/32] = Σ of each 32-element sub-block of A·2^-(e+5), hi/lo.
-// Workgroup = 2 rows, one wave per row (512 rows: 256 workgroups, one per CU;
-// 1 and 4 rows per workgroup measured slower). The row is read in
-// chunks of 4096 elements with every load of a chunk in flight; pass 2 converts
-// a row of one chunk from registers and re-reads longer rows (from cache). Lane
-// l converts the 8-element groups gi = l + 64·it, group gi being (k-slice gi/2,
-// k-group gi%2) of the row's fragment lane; a step's pieces go through LDS so
-// that each store writes the 2 rows' pieces of a fragment as 32 contiguous
-// bytes. A 32-element sub-block is the groups of four adjacent lanes; its sums
-// (and its Q8_0 block) meet by DPP.
+// A may be produced here from the previous op's output (GemmIn): the RMSNorm
+// of the row (runner.rs:1739-1746, the element formula of k_rmsnorm_v), or
+// h = g·σ(g)·u over the interleaved gate/up pairs (the formula of k_silu_pairs),
+// so the GEMM reads the producer's input and the normalised / gated rows never
+// go through memory.
+//
+// Workgroup = 2 rows × WK K-parts, one wave per (row, part): wave (ri, j) takes
+// the steps [S·j/WK, S·(j+1)/WK) of its row (a step = 64 groups of 8 elements,
+// S = ⌈k/512⌉), all of its loads in flight at once (SPW steps in registers;
+// longer rows of the plain input are read in chunks and re-read for the
+// conversion). The row's sum of squares and maximum meet in LDS. Lane l of a
+// step converts group gi = 64·step + l, group gi being (k-slice gi/2, k-group
+// gi%2) of the row's fragment lane; a step's pieces go through LDS so that each
+// store writes the 2 rows' pieces of a fragment as 32 contiguous bytes. A
+// 32-element sub-block is the groups of four adjacent lanes; its sums (and its
+// Q8_0 block) meet by DPP.
 //
 // Q8 = true (AETH_MM_Q8_ACTIVATIONS, the dot-product mode): each 32-element
 // sub-block is first replaced by its Q8_0 activation block, dequantized —
@@ -79,66 +85,127 @@
 // most 18 significant bits, so it is exact in f32 and in the hi/lo split: the
 // GEMM then computes Σ (q_a·d_a)·(q·sc·d) exactly per product, i.e. the
 // reference's per-term d_a·(d1·Σ q·q_a − m1·Σ q_a) up to f32 summation order.
-// Lane l holds the 8-element groups gi = l + 64·it (it < 8) of a 4096-element
-// chunk of the row: elements [8gi, 8gi + 8), read with every load in flight.
+#define PREP_ROWS 2
+#define PREP_LD 3  // LDS stride in 16-byte pieces between groups (odd: lanes spread over the banks)
+
+struct PrepArgs {
+    const float* A;       // [m][k], or [m][2k] (g, u) pairs for PREP_SWIGLU
+    const float* norm_w;  // [k] for PREP_RMSNORM
+    float eps;
+    int m, k;
+    float* escale;
+    _Float16 *frag, *Sh, *Sl;
+};
+
+// 8 consecutive floats at p (16-byte aligned when AL16)
 template <bool AL16>
-__device__ __forceinline__ void prep_load_chunk(const float* __restrict__ a, int ng, int g0, bool live,
-                                                float (&v)[8][8]) {
-    const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void prep_ld8(const float* __restrict__ p, float* v) {
+    if (AL16) {
+        const float4 x0 = *(const float4*)p, x1 = *(const float4*)(p + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    } else {
 #pragma unroll
-    for (int it = 0; it < 8; it++) {
-        const int gi = g0 + lane + 64 * it;
-        if (live && gi < ng) {
-            if (AL16) {
-                const float4 x0 = *(const float4*)(a + 8 * gi), x1 = *(const float4*)(a + 8 * gi + 4);
-                v[it][0] = x0.x; v[it][1] = x0.y; v[it][2] = x0.z; v[it][3] = x0.w;
-                v[it][4] = x1.x; v[it][5] = x1.y; v[it][6] = x1.z; v[it][7] = x1.w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) v[it][i] = a[8 * gi + i];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[it][i] = 0.0f;
-        }
+        for (int i = 0; i < 8; i++) v[i] = p[i];
     }
 }
 
-#define PREP_ROWS 2
-#define PREP_LD 5  // LDS stride in 16-byte pieces between groups (5: lanes spread over the banks)
-template <bool AL16, bool Q8>
-__global__ void __launch_bounds__(64 * PREP_ROWS) k_gemm_prep(const float* __restrict__ A, int m, int k,
-                                                               float* __restrict__ escale, _Float16* __restrict__ frag,
-                                                               _Float16* __restrict__ Sh, _Float16* __restrict__ Sl) {
-    // staging of one chunk step: [part][group][row] 16-byte pieces
-    __shared__ __attribute__((aligned(16))) uint4 stage[2 * 64 * PREP_LD];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, r0 = blockIdx.x * PREP_ROWS, r = r0 + wv;
-    const bool live = r < m;
-    const float* a = A + (int64_t)min(r, m - 1) * k;
-    const int ng = k / 8, nks = k / 16, mt = r0 >> 5, rr0 = r0 & 31;
-    float v[8][8];
+template <bool AL16, bool Q8, int MODE, int WK>
+__global__ void __launch_bounds__(64 * PREP_ROWS * WK) k_gemm_prep(PrepArgs P) {
+    constexpr int SPW = 32 / WK;  // steps a wave holds in registers (k ≤ 16384 in one chunk)
+    __shared__ __attribute__((aligned(16))) uint4 stage[WK][2][64][PREP_LD];  // [part j][hi/lo][group][row]
+    __shared__ float red[2][PREP_ROWS * WK];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, ri = wv & 1, j = wv >> 1;
+    const int r0 = blockIdx.x * PREP_ROWS, r = r0 + ri;
+    const bool live = r < P.m;
+    const int k = P.k, ng = k / 8, nks = k / 16, mt = r0 >> 5, rr0 = r0 & 31;
+    const int S = (ng + 63) / 64, s0 = S * j / WK, ns = S * (j + 1) / WK - s0, nsmax = (S + WK - 1) / WK;
+    const float* a = P.A + (int64_t)min(r, P.m - 1) * (MODE == PREP_SWIGLU ? 2 * k : k);
+    float v[SPW][8], v2[SPW][8];
+    // loads of the SPW steps from step t0 of this part (every load issued before any use)
+    auto load = [&](int t0) {
+#pragma unroll
+        for (int t = 0; t < SPW; t++) {
+            const int gi = 64 * (s0 + t0 + t) + lane;
+            const bool ok = live && t0 + t < ns && gi < ng;
+            if (ok) {
+                if (MODE == PREP_SWIGLU) {
+                    prep_ld8<AL16>(a + 16 * gi, v[t]);
+                    prep_ld8<AL16>(a + 16 * gi + 8, v2[t]);
+                } else {
+                    prep_ld8<AL16>(a + 8 * gi, v[t]);
+                    if (MODE == PREP_RMSNORM) prep_ld8<AL16>(P.norm_w + 8 * gi, v2[t]);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[t][i] = v2[t][i] = 0.0f;
+            }
+        }
+        if (MODE == PREP_SWIGLU) {  // (g, u) pairs → g·σ(g)·u, in k order
+#pragma unroll
+            for (int t = 0; t < SPW; t++) {
+                float h[8];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float g0 = v[t][2 * i], u0 = v[t][2 * i + 1], g1 = v2[t][2 * i], u1 = v2[t][2 * i + 1];
+                    h[i] = g0 * (1.0f / (1.0f + expf(-g0))) * u0;
+                    h[4 + i] = g1 * (1.0f / (1.0f + expf(-g1))) * u1;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[t][i] = h[i];
+            }
+        }
+    };
+    const int nck = (nsmax + SPW - 1) / SPW;  // chunks (1 unless a plain row is longer than 16384)
     float mx = 0.0f;
-    for (int g0 = 0; g0 < ng; g0 += 512) {  // pass 1: the row maximum, a chunk at a time
-        prep_load_chunk<AL16>(a, ng, g0, live, v);
+    for (int c = 0; c < nck; c++) {
+        load(c * SPW);
+        if (MODE == PREP_RMSNORM) {  // rms = sqrt(Σx²/k + eps); x ← (x / rms)·w (one chunk: k ≤ 16384)
+            float ss = 0.0f;
 #pragma unroll
-        for (int it = 0; it < 8; it++)
+            for (int t = 0; t < SPW; t++)
 #pragma unroll
-            for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[it][i]));
+                for (int i = 0; i < 8; i++) ss += v[t][i] * v[t][i];
+            ss = aeth_wave_sum(ss);
+            if (lane == 0) red[0][wv] = ss;
+            __syncthreads();
+            float tot = 0.0f;
+#pragma unroll
+            for (int q = 0; q < WK; q++) tot += red[0][2 * q + ri];
+            const float rms = sqrtf(tot / (float)k + P.eps), inv = 1.0f / rms;
+#pragma unroll
+            for (int t = 0; t < SPW; t++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float x = v[t][i], q0 = x * inv;  // the correctly rounded x / rms
+                    v[t][i] = fmaf(fmaf(-q0, rms, x), inv, q0) * v2[t][i];
+                }
+        }
+#pragma unroll
+        for (int t = 0; t < SPW; t++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[t][i]));
     }
     mx = aeth_wave_max(mx);
+    if (lane == 0) red[1][wv] = mx;
+    __syncthreads();
+    mx = 0.0f;
+#pragma unroll
+    for (int q = 0; q < WK; q++) mx = fmaxf(mx, red[1][2 * q + ri]);
     int E = 0;
     if (mx > 0.0f && isfinite(mx)) (void)frexpf(mx, &E);
     const float esc = ldexpf(1.0f, E > 14 ? E - 14 : 0);
-    if (lane == 0) escale[r] = esc;
+    if (j == 0 && lane == 0) P.escale[r] = esc;
     const float inv = 1.0f / esc;  // a power of two: the products below are exact scalings
-    for (int g0 = 0; g0 < ng; g0 += 512) {  // pass 2 (a row of one chunk is still in registers)
-        if (ng > 512) prep_load_chunk<AL16>(a, ng, g0, live, v);
+    const int tp = tid & 127;      // thread of the part's wave pair
+    for (int c = 0; c < nck; c++) {
+        if (nck > 1) load(c * SPW);  // (one chunk: still in registers)
 #pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int gb = g0 + 64 * it;  // first group of this step
-            if (gb >= ng) break;          // uniform
-            const int gi = gb + lane;
-            float* x = v[it];
+        for (int t = 0; t < SPW; t++) {
+            if (c * SPW + t >= nsmax) break;  // uniform
+            const int gb = 64 * (s0 + c * SPW + t), gi = gb + lane;
+            const bool sl = c * SPW + t < ns;  // this part has the step (uniform per wave)
+            float* x = v[t];
             if (Q8) {  // quantize_q8_0_block (neon.rs:45-104), then the value q·f16(d)
                 int nan = 0;
                 float bm = 0.0f;
@@ -169,34 +236,32 @@ __global__ void __launch_bounds__(64 * PREP_ROWS) k_gemm_prep(const float* __res
             half8_t hi, lo;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const float t = x[perm4(i)] * inv;
-                const _Float16 th = (_Float16)t;
+                const float tv = x[perm4(i)] * inv;
+                const _Float16 th = (_Float16)tv;
                 hi[i] = th;
-                lo[i] = (_Float16)(t - (float)th);
+                lo[i] = (_Float16)(tv - (float)th);
             }
-            const bool gl = gi < ng;  // uniform per block of four lanes (ng is a multiple of 32)
-            if (gl && (lane & 3) == 0) {
+            if (sl && gi < ng && (lane & 3) == 0) {  // gi < ng is uniform per four lanes (ng % 32 == 0)
                 const float sv = sum * inv * 0.03125f;
                 const _Float16 sh = (_Float16)sv;
-                Sh[(int64_t)r * (k / 32) + (gi >> 2)] = sh;
-                Sl[(int64_t)r * (k / 32) + (gi >> 2)] = (_Float16)(sv - (float)sh);
+                P.Sh[(int64_t)r * (k / 32) + (gi >> 2)] = sh;
+                P.Sl[(int64_t)r * (k / 32) + (gi >> 2)] = (_Float16)(sv - (float)sh);
             }
             __syncthreads();  // the previous step's pieces have been stored
-            stage[(0 * 64 + lane) * PREP_LD + wv] = __builtin_bit_cast(uint4, hi);
-            stage[(1 * 64 + lane) * PREP_LD + wv] = __builtin_bit_cast(uint4, lo);
+            stage[j][0][lane][ri] = __builtin_bit_cast(uint4, hi);
+            stage[j][1][lane][ri] = __builtin_bit_cast(uint4, lo);
             __syncthreads();
-            // piece P = (part, group, row): PREP_ROWS consecutive threads store one group's rows,
-            // 16·PREP_ROWS contiguous bytes of fragment (mt, group/2, part) at lane rows rr0..,
-            // k-group group%2
+            // piece (part, group, row) = (Q / 128, (Q / 2) % 64, Q % 2): two consecutive threads
+            // store one group's two rows, 32 contiguous bytes of fragment (mt, group/2, part)
+            // at lane rows rr0, rr0 + 1, k-group group%2
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                const int P = threadIdx.x + 64 * PREP_ROWS * h, i = P % PREP_ROWS, g = (P / PREP_ROWS) & 63;
-                const int part = P / (64 * PREP_ROWS);
-                if (gb + g < ng) {
+                const int Q = tp + 128 * h, i = Q & 1, g = (Q >> 1) & 63, part = Q >> 7;
+                if (sl && gb + g < ng) {
                     const int gg = gb + g;
-                    uint4* dst = (uint4*)(frag + ((int64_t)(mt * nks + (gg >> 1)) * 2 + part) * 512) +
+                    uint4* dst = (uint4*)(P.frag + ((int64_t)(mt * nks + (gg >> 1)) * 2 + part) * 512) +
                                  rr0 + i + 32 * (gg & 1);
-                    *dst = stage[(part * 64 + g) * PREP_LD + i];
+                    *dst = stage[j][part][g][i];
                 }
             }
         }
@@ -405,10 +470,28 @@ int64_t aeth_gemm_ws_bytes(int64_t m, int64_t k) {
     return mp * k * 2 * 2 + mp * (k / 32) * 2 * 2 + mp * 4 + 256;
 }
 
+template <bool AL16, bool Q8, int MODE>
+static void prep_launch(int wk, unsigned grid, hipStream_t s, const PrepArgs& P) {
+    if (wk == 8) hipLaunchKernelGGL((k_gemm_prep<AL16, Q8, MODE, 8>), dim3(grid), dim3(64 * PREP_ROWS * 8), 0, s, P);
+    else hipLaunchKernelGGL((k_gemm_prep<AL16, Q8, MODE, 4>), dim3(grid), dim3(64 * PREP_ROWS * 4), 0, s, P);
+}
+
+bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {
+    if (!w || w->dtype != AETH_DTYPE_Q4_K || w->order != AETH_ORDER_PLANAR || m <= 1) return false;
+    if (mode == PREP_PLAIN) return true;
+    if (w->k != w->nb * 256) return false;  // ragged K goes to the row-batched GEMV
+    if (w->k > 16384 || ((uintptr_t)d_a & 15)) return false;  // one chunk of registers per wave, float4 loads
+    if (mode == PREP_RMSNORM) return norm_w && ((uintptr_t)norm_w & 15) == 0;
+    return mode == PREP_SWIGLU;
+}
+
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s, int64_t ldc, void* ws, size_t ws_bytes) {
+                         hipStream_t s, int64_t ldc, void* ws, size_t ws_bytes, const GemmIn* in) {
     const int k = (int)w->k, nb = (int)w->nb;
+    const int mode = in ? in->mode : PREP_PLAIN;
     if (ldc <= 0) ldc = w->n;
+    if (mode != PREP_PLAIN && !aeth_gemm_fuses(w, m, mode, d_a, in->norm_w))
+        return aeth_set_error(AETH_EINVAL, "gemm: fused producer %d not available for k=%d", mode, k);
     if (k != nb * 256) {  // ragged K: row-batched GEMV
         GemvEpi e;
         e.flags = flags;
@@ -430,11 +513,21 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     float* esc = (float*)(Sl + (size_t)mp * (k / 32));
     const bool al16 = ((uintptr_t)d_a & 15) == 0;
     const bool q8 = (flags & AETH_MM_Q8_ACTIVATIONS) != 0;
-    const dim3 pg((unsigned)(mp / PREP_ROWS));
-    if (al16 && q8) hipLaunchKernelGGL((k_gemm_prep<true, true>), pg, dim3(64 * PREP_ROWS), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
-    else if (q8) hipLaunchKernelGGL((k_gemm_prep<false, true>), pg, dim3(64 * PREP_ROWS), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
-    else if (al16) hipLaunchKernelGGL((k_gemm_prep<true, false>), pg, dim3(64 * PREP_ROWS), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
-    else hipLaunchKernelGGL((k_gemm_prep<false, false>), pg, dim3(64 * PREP_ROWS), 0, s, d_a, (int)m, k, esc, frag, Sh, Sl);
+    // K-parts per row: 4 (measured against 8 on the prefill shapes); AETH_PREP_WK overrides (tests, tuning)
+    static const int env_wk = getenv("AETH_PREP_WK") ? atoi(getenv("AETH_PREP_WK")) : 0;
+    const int wk = env_wk == 8 ? 8 : 4;
+    const PrepArgs P{d_a, in ? in->norm_w : nullptr, in ? in->eps : 0.0f, (int)m, k, esc, frag, Sh, Sl};
+    const unsigned pg = (unsigned)(mp / PREP_ROWS);
+    if (mode == PREP_RMSNORM) {
+        if (q8) prep_launch<true, true, PREP_RMSNORM>(wk, pg, s, P);
+        else prep_launch<true, false, PREP_RMSNORM>(wk, pg, s, P);
+    } else if (mode == PREP_SWIGLU) {
+        if (q8) prep_launch<true, true, PREP_SWIGLU>(wk, pg, s, P);
+        else prep_launch<true, false, PREP_SWIGLU>(wk, pg, s, P);
+    } else if (al16 && q8) prep_launch<true, true, PREP_PLAIN>(wk, pg, s, P);
+    else if (q8) prep_launch<false, true, PREP_PLAIN>(wk, pg, s, P);
+    else if (al16) prep_launch<true, false, PREP_PLAIN>(wk, pg, s, P);
+    else prep_launch<false, false, PREP_PLAIN>(wk, pg, s, P);
     AETH_LAUNCH_CHECK();
     const int gm = (int)(mp / G2_BM), gn = (int)aeth_cdiv(w->n, G2_BN);
     const int64_t ntiles = aeth_cdiv(w->n, 16);

@@ -114,9 +114,26 @@ int aeth_xgemv_launch(const aeth_weight* w, const float* d_x, int64_t m, float* 
                       hipStream_t s);
 // Scratch floats a GGUF-order GEMV of m rows needs at most.
 int64_t aeth_xgemv_ws_floats(const aeth_weight* w, int64_t m);
-// Q4_K prefill GEMM (m > 1); ldc = output row stride (0: n).
+// The op whose output the Q4_K GEMM takes as A, run inside its activation prep:
+// A itself, the RMSNorm of A's rows with weight norm_w (k_rmsnorm_v's formula),
+// or h = g·σ(g)·u over A's interleaved (g, u) pairs (A has 2k columns;
+// k_silu_pairs's formula).
+enum { PREP_PLAIN = 0, PREP_RMSNORM = 1, PREP_SWIGLU = 2 };
+struct GemmIn {
+    int mode = PREP_PLAIN;
+    const float* norm_w = nullptr;
+    float eps = 0.0f;
+};
+// Whether aeth_gemm_q4k_launch runs producer `mode` for this weight and A (else
+// the caller runs the producer itself): a planar Q4_K weight, m > 1, and for
+// the RMSNorm and SwiGLU producers whole super-blocks, k ≤ 16384 and 16-byte
+// aligned A (and norm weight).
+bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w);
+// Q4_K prefill GEMM (m > 1); ldc = output row stride (0: n); in = the fused
+// producer (nullptr: plain A; any other mode must pass aeth_gemm_fuses).
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s, int64_t ldc = 0, void* ws = nullptr, size_t ws_bytes = 0);
+                         hipStream_t s, int64_t ldc = 0, void* ws = nullptr, size_t ws_bytes = 0,
+                         const GemmIn* in = nullptr);
 // aeth_qmatmul with an output row stride (rows of c are ldc floats apart).
 int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
                     hipStream_t s);

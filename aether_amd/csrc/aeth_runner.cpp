@@ -302,36 +302,60 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
     if ((rc = aeth_embed_rows_launch(r->emb, r->p_tok, n, d, r->p_x, s))) return rc;
     for (int l = 0; l < c.num_layers; l++) {
         float* lkv = r->kv + (int64_t)l * kv_layer_floats(c);
-        if ((rc = aeth_rmsnorm_launch(r->p_x, r->norms + (int64_t)l * 2 * d, n, d, c.rms_norm_eps, r->p_n, s)))
-            return rc;
-        if (r->wqkv[l]) {
-            if ((rc = aeth_qmatmul(r->wqkv[l], r->p_n, n, r->p_qkv, 0, s))) return rc;
-        } else {  // separate q, k, v into the columns of the [n][q|k|v] rows
-            const int64_t qd = nh * hd, kvd = nkv * hd, ld = qd + 2 * kvd;
-            if ((rc = aeth_qmatmul_ld(r->wq[l], r->p_n, n, r->p_qkv, ld, 0, s)) ||
-                (rc = aeth_qmatmul_ld(r->wk[l], r->p_n, n, r->p_qkv + qd, ld, 0, s)) ||
-                (rc = aeth_qmatmul_ld(r->wv[l], r->p_n, n, r->p_qkv + qd + kvd, ld, 0, s)))
-                return rc;
+        const float* attn_norm = r->norms + (int64_t)l * 2 * d;
+        const float* ffn_norm = attn_norm + d;
+        // Q4_K GEMMs take the RMSNorm (and the SwiGLU below) inside their activation prep
+        GemmIn nin;
+        nin.mode = PREP_RMSNORM;
+        nin.eps = c.rms_norm_eps;
+        nin.norm_w = attn_norm;
+        if (r->wqkv[l] && aeth_gemm_fuses(r->wqkv[l], n, PREP_RMSNORM, r->p_x, attn_norm)) {
+            if ((rc = aeth_gemm_q4k_launch(r->wqkv[l], r->p_x, n, r->p_qkv, 0, s, 0, nullptr, 0, &nin))) return rc;
+        } else {
+            if ((rc = aeth_rmsnorm_launch(r->p_x, attn_norm, n, d, c.rms_norm_eps, r->p_n, s))) return rc;
+            if (r->wqkv[l]) {
+                if ((rc = aeth_qmatmul(r->wqkv[l], r->p_n, n, r->p_qkv, 0, s))) return rc;
+            } else {  // separate q, k, v into the columns of the [n][q|k|v] rows
+                const int64_t qd = nh * hd, kvd = nkv * hd, ld = qd + 2 * kvd;
+                if ((rc = aeth_qmatmul_ld(r->wq[l], r->p_n, n, r->p_qkv, ld, 0, s)) ||
+                    (rc = aeth_qmatmul_ld(r->wk[l], r->p_n, n, r->p_qkv + qd, ld, 0, s)) ||
+                    (rc = aeth_qmatmul_ld(r->wv[l], r->p_n, n, r->p_qkv + qd + kvd, ld, 0, s)))
+                    return rc;
+            }
         }
         if ((rc = aeth_prefill_rope_kv_launch(r->p_qkv, n, nh, nkv, hd, r->rope_sin, r->rope_cos, c.max_seq_len,
                                               lkv, s)))
             return rc;
         if ((rc = aeth_attn_prefill_launch(r->p_qkv, (nh + 2 * nkv) * hd, lkv, n, nh, nkv, hd, c.max_seq_len, r->p_att, s))) return rc;
         if ((rc = aeth_qmatmul(r->wo[l], r->p_att, n, r->p_x, AETH_MM_ACCUMULATE, s))) return rc;
-        if ((rc = aeth_rmsnorm_launch(r->p_x, r->norms + (int64_t)l * 2 * d + d, n, d, c.rms_norm_eps, r->p_n, s)))
-            return rc;
         const float* h = r->p_h;
+        GemmIn din;  // the down GEMM's producer
         if (r->wgu[l]) {
-            if ((rc = aeth_qmatmul(r->wgu[l], r->p_n, n, r->p_gu, 0, s))) return rc;
-            if ((rc = aeth_silu_pairs_launch(r->p_gu, n * dff, r->p_h, s))) return rc;
+            nin.norm_w = ffn_norm;
+            if (aeth_gemm_fuses(r->wgu[l], n, PREP_RMSNORM, r->p_x, ffn_norm)) {
+                if ((rc = aeth_gemm_q4k_launch(r->wgu[l], r->p_x, n, r->p_gu, 0, s, 0, nullptr, 0, &nin))) return rc;
+            } else if ((rc = aeth_rmsnorm_launch(r->p_x, ffn_norm, n, d, c.rms_norm_eps, r->p_n, s)) ||
+                       (rc = aeth_qmatmul(r->wgu[l], r->p_n, n, r->p_gu, 0, s))) {
+                return rc;
+            }
+            if (aeth_gemm_fuses(r->wdown[l], n, PREP_SWIGLU, r->p_gu, nullptr)) {  // h = g·σ(g)·u in the prep
+                din.mode = PREP_SWIGLU;
+                h = r->p_gu;
+            } else if ((rc = aeth_silu_pairs_launch(r->p_gu, n * dff, r->p_h, s))) {
+                return rc;
+            }
         } else {  // g [n][dff], u [n][dff], then g·σ(g)·u in place
-            if ((rc = aeth_qmatmul(r->wg[l], r->p_n, n, r->p_gu, 0, s)) ||
+            if ((rc = aeth_rmsnorm_launch(r->p_x, ffn_norm, n, d, c.rms_norm_eps, r->p_n, s)) ||
+                (rc = aeth_qmatmul(r->wg[l], r->p_n, n, r->p_gu, 0, s)) ||
                 (rc = aeth_qmatmul(r->wu[l], r->p_n, n, r->p_gu + n * dff, 0, s)) ||
                 (rc = aeth_silu_mul_launch(r->p_gu, r->p_gu + n * dff, n * dff, s)))
                 return rc;
             h = r->p_gu;
         }
-        if ((rc = aeth_qmatmul(r->wdown[l], h, n, r->p_x, AETH_MM_ACCUMULATE, s))) return rc;
+        rc = din.mode == PREP_SWIGLU
+                 ? aeth_gemm_q4k_launch(r->wdown[l], h, n, r->p_x, AETH_MM_ACCUMULATE, s, 0, nullptr, 0, &din)
+                 : aeth_qmatmul(r->wdown[l], h, n, r->p_x, AETH_MM_ACCUMULATE, s);
+        if (rc) return rc;
     }
     // head on the last row; the state update then leaves pos = fill = n
     AETH_HIP_CHECK(hipMemcpyAsync(r->x, r->p_x + (int64_t)(n - 1) * d, sizeof(float) * d, hipMemcpyDeviceToDevice, s));

@@ -590,7 +590,7 @@ import aether_amd as A
 from oracle import oracle as O
 from tests._util import weight, assert_close
 A.check(A.lib().aeth_init(0))
-for m, n, k in ((130, 200, 1024), (64, 128, 2048), (70, 48, 1280)):
+for m, n, k in ((130, 200, 1024), (64, 128, 2048), (70, 48, 1280), (33, 96, 14336), (34, 64, 20480)):
     raw = weight(12, n, k, m + n)
     x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
     w = __import__("ctypes").c_void_p()
@@ -606,17 +606,18 @@ print("ok")
 """
 
 
-@pytest.mark.parametrize("kernel", ["2"])
-def test_gemm_alternate_kernels(gpu, kernel):
-    """The GEMM kernel the default picks only for buffers past 2 GiB:
-    AETH_GEMM_KERNEL=2 (the single-K-group ring kernel), read once per process,
-    so it runs in a fresh process."""
+@pytest.mark.parametrize("var,val", [("AETH_GEMM_KERNEL", "2"), ("AETH_PREP_WK", "8")])
+def test_gemm_alternate_kernels(gpu, var, val):
+    """Variants the default does not pick, each read once per process, so each
+    runs in a fresh process: AETH_GEMM_KERNEL=2, the single-K-group ring kernel
+    (the default only for buffers past 2 GiB); AETH_PREP_WK=8, the activation
+    prep with 8 K-parts per row (one and two chunks of registers per wave)."""
     import os
     import subprocess
     import sys
 
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    env = dict(os.environ, AETH_GEMM_KERNEL=kernel)
+    env = dict(os.environ, **{var: val})
     r = subprocess.run([sys.executable, "-c", GEMM_KERNEL_SCRIPT % root], env=env, cwd=root, timeout=240,
                        stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:]
