@@ -122,25 +122,31 @@ __global__ void __launch_bounds__(64 * PREP_ROWS * WK) k_gemm_prep(PrepArgs P) {
     const int S = (ng + 63) / 64, s0 = S * j / WK, ns = S * (j + 1) / WK - s0, nsmax = (S + WK - 1) / WK;
     const float* a = P.A + (int64_t)min(r, P.m - 1) * (MODE == PREP_SWIGLU ? 2 * k : k);
     float v[SPW][8], v2[SPW][8];
-    // loads of the SPW steps from step t0 of this part (every load issued before any use)
+    // loads of the SPW steps from step t0 of this part. Every load is issued, from a clamped
+    // address, and values outside the row, the part or the live rows are zeroed afterwards: a
+    // load under a branch would make the compiler wait for it at the branch's end, one round
+    // trip per load.
     auto load = [&](int t0) {
+        bool ok[SPW];
 #pragma unroll
         for (int t = 0; t < SPW; t++) {
-            const int gi = 64 * (s0 + t0 + t) + lane;
-            const bool ok = live && t0 + t < ns && gi < ng;
-            if (ok) {
-                if (MODE == PREP_SWIGLU) {
-                    prep_ld8<AL16>(a + 16 * gi, v[t]);
-                    prep_ld8<AL16>(a + 16 * gi + 8, v2[t]);
-                } else {
-                    prep_ld8<AL16>(a + 8 * gi, v[t]);
-                    if (MODE == PREP_RMSNORM) prep_ld8<AL16>(P.norm_w + 8 * gi, v2[t]);
-                }
+            const int gi = 64 * (s0 + t0 + t) + lane, gc = min(gi, ng - 1);
+            ok[t] = live && t0 + t < ns && gi < ng;
+            if (MODE == PREP_SWIGLU) {
+                prep_ld8<AL16>(a + 16 * gc, v[t]);
+                prep_ld8<AL16>(a + 16 * gc + 8, v2[t]);
             } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) v[t][i] = v2[t][i] = 0.0f;
+                prep_ld8<AL16>(a + 8 * gc, v[t]);
+                if (MODE == PREP_RMSNORM) prep_ld8<AL16>(P.norm_w + 8 * gc, v2[t]);
             }
         }
+#pragma unroll
+        for (int t = 0; t < SPW; t++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                v[t][i] = ok[t] ? v[t][i] : 0.0f;
+                v2[t][i] = ok[t] ? v2[t][i] : 0.0f;
+            }
         if (MODE == PREP_SWIGLU) {  // (g, u) pairs → g·σ(g)·u, in k order
 #pragma unroll
             for (int t = 0; t < SPW; t++) {
