@@ -203,11 +203,13 @@ def test_benchmark_config_parity(gpu, dtype, n, k):
     assert_close(yd.cpu().numpy(), ref, what="config dtype %d" % dtype)
 
 
-@pytest.mark.parametrize("dtype,n,k", [(Q4_K, 50000, 4096), (Q8_0, 50000, 1024), (Q6_K, 33000, 512)])
+@pytest.mark.parametrize("dtype,n,k", [(Q4_K, 50000, 4096), (Q8_0, 50000, 1024), (Q6_K, 33000, 512),
+                                       (Q4_K, 20000, 4096), (Q5_K, 28700, 2048), (Q8_0, 30000, 512)])
 def test_gemv_tall_ragged_parity(gpu, dtype, n, k):
-    """Tall matrices take the refilling ring of tiles; these row counts leave the
-    last workgroup fewer tiles than the others (and fewer than the ring holds),
-    so its surplus loads and the past-the-end refills are exercised."""
+    """Tall matrices take the refilling ring of tiles (4 to 8 tiles per CU: one
+    workgroup per CU, 5 to 8 tiles each); these row counts leave the last
+    workgroup fewer tiles than the others (and fewer than the ring holds), so
+    its surplus loads and the past-the-end refills are exercised."""
     torch = gpu
     L = A.lib()
     be, bb = GEOM[dtype]
