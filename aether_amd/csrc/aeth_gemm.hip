@@ -66,16 +66,18 @@
 // so the GEMM reads the producer's input and the normalised / gated rows never
 // go through memory.
 //
-// Workgroup = 2 rows × WK K-parts, one wave per (row, part): wave (ri, j) takes
-// the steps [S·j/WK, S·(j+1)/WK) of its row (a step = 64 groups of 8 elements,
-// S = ⌈k/512⌉), all of its loads in flight at once (SPW steps in registers;
-// longer rows of the plain input are read in chunks and re-read for the
-// conversion). The row's sum of squares and maximum meet in LDS. Lane l of a
-// step converts group gi = 64·step + l, group gi being (k-slice gi/2, k-group
-// gi%2) of the row's fragment lane; a step's pieces go through LDS so that each
-// store writes the 2 rows' pieces of a fragment as 32 contiguous bytes. A
-// 32-element sub-block is the groups of four adjacent lanes; its sums (and its
-// Q8_0 block) meet by DPP.
+// Workgroup = 4 rows (2 for the RMSNorm / SwiGLU producers holding 8 steps of
+// inputs) × 4 K-parts, one wave per (row, part): wave (ri, j) takes
+// the steps [S·j/4, S·(j+1)/4) of its row (a step = 64 groups of 8 elements,
+// S = ⌈k/512⌉), all of its loads in flight at once (SPW steps in registers,
+// sized to the share; longer rows of the plain input are read in chunks and
+// re-read for the conversion). The row's sum of squares and maximum meet in LDS.
+// Lane l of a step converts group gi = 64·step + l, group gi being (k-slice
+// gi/2, k-group gi%2) of the row's fragment lane; a step's pieces go through LDS
+// so that each store writes the 4 rows' pieces of a fragment as 64 contiguous
+// bytes (measured at k = 4096: 2 rows 6.8 µs, 4 rows 5.7 µs, 8 rows 7.5 µs — 64
+// workgroups for m = 512). A 32-element sub-block is the groups of four
+// adjacent lanes; its sums (and its Q8_0 block) meet by DPP.
 //
 // Q8 = true (AETH_MM_Q8_ACTIVATIONS, the dot-product mode): each 32-element
 // sub-block is first replaced by its Q8_0 activation block, dequantized —
@@ -85,8 +87,8 @@
 // most 18 significant bits, so it is exact in f32 and in the hi/lo split: the
 // GEMM then computes Σ (q_a·d_a)·(q·sc·d) exactly per product, i.e. the
 // reference's per-term d_a·(d1·Σ q·q_a − m1·Σ q_a) up to f32 summation order.
-#define PREP_ROWS 2
-#define PREP_LD 3  // LDS stride in 16-byte pieces between groups (odd: lanes spread over the banks)
+#define PREP_WK 4    // K-parts per row (one wave each)
+#define PREP_LD 5    // LDS stride in 16-byte pieces between groups (odd: lanes spread over the banks)
 
 struct PrepArgs {
     const float* A;       // [m][k], or [m][2k] (g, u) pairs for PREP_SWIGLU
@@ -110,12 +112,15 @@ __device__ __forceinline__ void prep_ld8(const float* __restrict__ p, float* v) 
     }
 }
 
-template <bool AL16, bool Q8, int MODE, int WK>
-__global__ void __launch_bounds__(64 * PREP_ROWS * WK) k_gemm_prep(PrepArgs P) {
-    constexpr int SPW = 32 / WK;  // steps a wave holds in registers (k ≤ 16384 in one chunk)
+// SPW: steps a wave holds in registers, at least its share ⌈S/4⌉ (1, 2, 4 or 8: k ≤ 16384 in one chunk).
+// PREP_ROWS: rows per workgroup, 4 (2 where the producer's 8 steps of inputs need more than the
+// 128 registers of a 16-wave workgroup).
+template <bool AL16, bool Q8, int MODE, int SPW, int PREP_ROWS>
+__global__ void __launch_bounds__(64 * PREP_ROWS * PREP_WK) k_gemm_prep(PrepArgs P) {
+    constexpr int WK = PREP_WK;
     __shared__ __attribute__((aligned(16))) uint4 stage[WK][2][64][PREP_LD];  // [part j][hi/lo][group][row]
     __shared__ float red[2][PREP_ROWS * WK];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, ri = wv & 1, j = wv >> 1;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, ri = wv % PREP_ROWS, j = wv / PREP_ROWS;
     const int r0 = blockIdx.x * PREP_ROWS, r = r0 + ri;
     const bool live = r < P.m;
     const int k = P.k, ng = k / 8, nks = k / 16, mt = r0 >> 5, rr0 = r0 & 31;
@@ -177,7 +182,7 @@ __global__ void __launch_bounds__(64 * PREP_ROWS * WK) k_gemm_prep(PrepArgs P) {
             __syncthreads();
             float tot = 0.0f;
 #pragma unroll
-            for (int q = 0; q < WK; q++) tot += red[0][2 * q + ri];
+            for (int q = 0; q < WK; q++) tot += red[0][PREP_ROWS * q + ri];
             const float rms = sqrtf(tot / (float)k + P.eps), inv = 1.0f / rms;
 #pragma unroll
             for (int t = 0; t < SPW; t++)
@@ -197,13 +202,13 @@ __global__ void __launch_bounds__(64 * PREP_ROWS * WK) k_gemm_prep(PrepArgs P) {
     __syncthreads();
     mx = 0.0f;
 #pragma unroll
-    for (int q = 0; q < WK; q++) mx = fmaxf(mx, red[1][2 * q + ri]);
+    for (int q = 0; q < WK; q++) mx = fmaxf(mx, red[1][PREP_ROWS * q + ri]);
     int E = 0;
     if (mx > 0.0f && isfinite(mx)) (void)frexpf(mx, &E);
     const float esc = ldexpf(1.0f, E > 14 ? E - 14 : 0);
     if (j == 0 && lane == 0) P.escale[r] = esc;
     const float inv = 1.0f / esc;  // a power of two: the products below are exact scalings
-    const int tp = tid & 127;      // thread of the part's wave pair
+    const int tp = tid % (64 * PREP_ROWS);  // thread of the part's PREP_ROWS waves
     for (int c = 0; c < nck; c++) {
         if (nck > 1) load(c * SPW);  // (one chunk: still in registers)
 #pragma unroll
@@ -257,12 +262,13 @@ __global__ void __launch_bounds__(64 * PREP_ROWS * WK) k_gemm_prep(PrepArgs P) {
             stage[j][0][lane][ri] = __builtin_bit_cast(uint4, hi);
             stage[j][1][lane][ri] = __builtin_bit_cast(uint4, lo);
             __syncthreads();
-            // piece (part, group, row) = (Q / 128, (Q / 2) % 64, Q % 2): two consecutive threads
-            // store one group's two rows, 32 contiguous bytes of fragment (mt, group/2, part)
-            // at lane rows rr0, rr0 + 1, k-group group%2
+            // piece (part, group, row) = (Q / 64R, (Q / R) % 64, Q % R), R = PREP_ROWS: R consecutive
+            // threads store one group's R rows, 16·R contiguous bytes of fragment (mt, group/2, part)
+            // at lane rows rr0 .. rr0 + R − 1, k-group group%2
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                const int Q = tp + 128 * h, i = Q & 1, g = (Q >> 1) & 63, part = Q >> 7;
+                const int Q = tp + 64 * PREP_ROWS * h, i = Q % PREP_ROWS, g = (Q / PREP_ROWS) & 63;
+                const int part = Q / (64 * PREP_ROWS);
                 if (sl && gb + g < ng) {
                     const int gg = gb + g;
                     uint4* dst = (uint4*)(P.frag + ((int64_t)(mt * nks + (gg >> 1)) * 2 + part) * 512) +
@@ -476,10 +482,17 @@ int64_t aeth_gemm_ws_bytes(int64_t m, int64_t k) {
     return mp * k * 2 * 2 + mp * (k / 32) * 2 * 2 + mp * 4 + 256;
 }
 
+template <bool AL16, bool Q8, int MODE, int SPW>
+static void prep_launch_r(unsigned mp, hipStream_t s, const PrepArgs& P) {
+    constexpr int R = SPW == 8 && MODE != PREP_PLAIN ? 2 : 4;
+    hipLaunchKernelGGL((k_gemm_prep<AL16, Q8, MODE, SPW, R>), dim3(mp / R), dim3(64 * R * PREP_WK), 0, s, P);
+}
 template <bool AL16, bool Q8, int MODE>
-static void prep_launch(int wk, unsigned grid, hipStream_t s, const PrepArgs& P) {
-    if (wk == 8) hipLaunchKernelGGL((k_gemm_prep<AL16, Q8, MODE, 8>), dim3(grid), dim3(64 * PREP_ROWS * 8), 0, s, P);
-    else hipLaunchKernelGGL((k_gemm_prep<AL16, Q8, MODE, 4>), dim3(grid), dim3(64 * PREP_ROWS * 4), 0, s, P);
+static void prep_launch(int spw, unsigned mp, hipStream_t s, const PrepArgs& P) {
+    if (spw == 1) prep_launch_r<AL16, Q8, MODE, 1>(mp, s, P);
+    else if (spw == 2) prep_launch_r<AL16, Q8, MODE, 2>(mp, s, P);
+    else if (spw == 4) prep_launch_r<AL16, Q8, MODE, 4>(mp, s, P);
+    else prep_launch_r<AL16, Q8, MODE, 8>(mp, s, P);
 }
 
 bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {
@@ -519,21 +532,21 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     float* esc = (float*)(Sl + (size_t)mp * (k / 32));
     const bool al16 = ((uintptr_t)d_a & 15) == 0;
     const bool q8 = (flags & AETH_MM_Q8_ACTIVATIONS) != 0;
-    // K-parts per row: 4 (measured against 8 on the prefill shapes); AETH_PREP_WK overrides (tests, tuning)
-    static const int env_wk = getenv("AETH_PREP_WK") ? atoi(getenv("AETH_PREP_WK")) : 0;
-    const int wk = env_wk == 8 ? 8 : 4;
+    // registers per wave: its share of the row's steps, rounded up to 1, 2, 4 or 8 (past 8: chunks)
+    const int share = (int)aeth_cdiv(aeth_cdiv(k, 512), PREP_WK);
+    const int spw = share <= 1 ? 1 : share <= 2 ? 2 : share <= 4 ? 4 : 8;
     const PrepArgs P{d_a, in ? in->norm_w : nullptr, in ? in->eps : 0.0f, (int)m, k, esc, frag, Sh, Sl};
-    const unsigned pg = (unsigned)(mp / PREP_ROWS);
+    const unsigned pg = (unsigned)mp;  // fragment rows (whole 64-row tiles)
     if (mode == PREP_RMSNORM) {
-        if (q8) prep_launch<true, true, PREP_RMSNORM>(wk, pg, s, P);
-        else prep_launch<true, false, PREP_RMSNORM>(wk, pg, s, P);
+        if (q8) prep_launch<true, true, PREP_RMSNORM>(spw, pg, s, P);
+        else prep_launch<true, false, PREP_RMSNORM>(spw, pg, s, P);
     } else if (mode == PREP_SWIGLU) {
-        if (q8) prep_launch<true, true, PREP_SWIGLU>(wk, pg, s, P);
-        else prep_launch<true, false, PREP_SWIGLU>(wk, pg, s, P);
-    } else if (al16 && q8) prep_launch<true, true, PREP_PLAIN>(wk, pg, s, P);
-    else if (q8) prep_launch<false, true, PREP_PLAIN>(wk, pg, s, P);
-    else if (al16) prep_launch<true, false, PREP_PLAIN>(wk, pg, s, P);
-    else prep_launch<false, false, PREP_PLAIN>(wk, pg, s, P);
+        if (q8) prep_launch<true, true, PREP_SWIGLU>(spw, pg, s, P);
+        else prep_launch<true, false, PREP_SWIGLU>(spw, pg, s, P);
+    } else if (al16 && q8) prep_launch<true, true, PREP_PLAIN>(spw, pg, s, P);
+    else if (q8) prep_launch<false, true, PREP_PLAIN>(spw, pg, s, P);
+    else if (al16) prep_launch<true, false, PREP_PLAIN>(spw, pg, s, P);
+    else prep_launch<false, false, PREP_PLAIN>(spw, pg, s, P);
     AETH_LAUNCH_CHECK();
     const int gm = (int)(mp / G2_BM), gn = (int)aeth_cdiv(w->n, G2_BN);
     const int64_t ntiles = aeth_cdiv(w->n, 16);

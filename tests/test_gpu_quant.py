@@ -304,10 +304,11 @@ def test_synthetic_generator_deterministic(gpu):
 # Row magnitudes span 2^-12 .. 2^20 (the per-block fp16 exponent), with an
 # all-zero row, and the accumulate epilogue is checked on top.
 @pytest.mark.parametrize("m,n,k", [(70, 130, 768), (65, 300, 1024), (130, 40, 2560), (3, 16, 512), (45, 48, 16384),
-                                   (34, 64, 20480)])
+                                   (34, 64, 20480), (37, 96, 8192)])
 def test_gemm_q4k_tiles_exponents_accumulate(gpu, m, n, k):
     """Ragged tiles, per-row exponents (2^20, 2^-12, zero rows, a block past
-    fp16 range) and accumulate, up to rows of 16384 and 20480 elements."""
+    fp16 range) and accumulate, up to rows of 16384 and 20480 elements (the
+    prep holds 1, 2, 4 or 8 steps of a row per wave, 20480 in two chunks)."""
     rng = np.random.default_rng(m * 31 + n * 7 + k)
     raw = weight(Q4_K, n, k, 3 * n + k)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -608,12 +609,11 @@ print("ok")
 """
 
 
-@pytest.mark.parametrize("var,val", [("AETH_GEMM_KERNEL", "2"), ("AETH_PREP_WK", "8")])
+@pytest.mark.parametrize("var,val", [("AETH_GEMM_KERNEL", "2")])
 def test_gemm_alternate_kernels(gpu, var, val):
-    """Variants the default does not pick, each read once per process, so each
-    runs in a fresh process: AETH_GEMM_KERNEL=2, the single-K-group ring kernel
-    (the default only for buffers past 2 GiB); AETH_PREP_WK=8, the activation
-    prep with 8 K-parts per row (one and two chunks of registers per wave)."""
+    """The GEMM kernel the default picks only for buffers past 2 GiB:
+    AETH_GEMM_KERNEL=2 (the single-K-group ring kernel), read once per process,
+    so it runs in a fresh process."""
     import os
     import subprocess
     import sys
