@@ -440,13 +440,16 @@ __device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase
 
 // Fusions:
 //  norm_w    : x ← x / sqrt(Σx²/k + eps) · norm_w first (rmsnorm_inplace, runner.rs:1739-1746);
+//              exact path: (W·(x·norm_w)) / rms, the epilogue divides; Q8A: x / rms · norm_w, then quantized;
 //  swiglu    : rows (2i, 2i+1) = (gate_i, up_i); y[i] = g·σ(g)·u (runner.rs:1617-1625);
 //  amax      : 64-bit atomic max of (orderable(y) << 32 | row) — ties → last row
 //              (Iterator::max_by, runner.rs:1964-1973);
 //  accumulate: y += result (residual adds, runner.rs:1609-1611, 1629-1631).
 // RING = false: the workgroup's tiles all fit the RD load slots (issued up
 // front); RING = true: the slots are refilled as they are consumed.
-template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG, bool Q8A>
+// NORM: the exact path's fused RMSNorm, with the division moved to the epilogue (G.norm_w set,
+// !Q8A); other instances apply a G.norm_w to the row first.
+template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG, bool Q8A, bool NORM>
 __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
     typedef MF<F> T;
     typedef typename T::D Dt;
@@ -473,7 +476,7 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
 
     float xv[XO][8], wv[XO][8];
     mq_load_x<XO, RAG>(xr, o0, o1, G.kx, xv);
-    if (G.norm_w) mq_load_x<XO, RAG>(G.norm_w, o0, o1, G.kx, wv);  // (a uniform branch)
+    if (NORM || G.norm_w) mq_load_x<XO, RAG>(G.norm_w, o0, o1, G.kx, wv);  // (a uniform branch)
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight stream
     Dt buf[RD][NBW];
 #pragma unroll
@@ -482,7 +485,29 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
         for (int i = 0; i < NBW; i++)
             T::load(buf[r][i], G, (t0 + min(r, ntw - 1)) * nc + c0 + min(i, max(nbw - 1, 0)), lane);
 
-    if (G.norm_w) {  // fused RMSNorm: the waves' slices tile the row; one barrier
+    if (NORM) {
+        // fused RMSNorm, exact dots: 1/rms is one factor of every output, so the slice
+        // becomes x·w at once and each output row is divided by rms in the epilogue, after
+        // the barrier that is there anyway — no wave waits for the others before its first
+        // dot; each wave leaves its slice's Σx² (the slices tile the row)
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XO; i++) {
+            const int o = o0 + lane + 64 * i;
+#pragma unroll
+            for (int t = 0; t < 8; t++) ss += (o < o1 && 8 * o + t < G.kx) ? xv[i][t] * xv[i][t] : 0.0f;
+        }
+        ss = aeth_wave_sum(ss);
+        if (lane == 0) ssum[wave] = ss;
+#pragma unroll
+        for (int i = 0; i < XO; i++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) xv[i][t] *= wv[i][t];
+    } else if (G.norm_w) {
+        // fused RMSNorm applied to the row first — the dot-product mode, whose Q8_0
+        // activation blocks are made from the normalised row itself (byte for byte as the
+        // reference quantizes it): one barrier for Σx², then x / rms · w. (The exact-path
+        // instances carry this block too; it keeps their measured code layout.)
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < XO; i++) {
@@ -554,6 +579,14 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
     }
     __syncthreads();
 
+    float rms = 1.0f;  // the exact path's fused RMSNorm: rms = sqrt(Σx²/k + eps), the waves' slices in order
+    constexpr bool div_rms = NORM;
+    if (div_rms) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) tot += ssum[w];
+        rms = sqrtf(tot / (float)G.k + G.eps);
+    }
     unsigned long long best = 0;
     for (int idx = threadIdx.x; idx < ntw * 16; idx += 64 * W) {
         const int jt = idx >> 4, nn = idx & 15;
@@ -562,11 +595,13 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
         float sum = 0.0f;
 #pragma unroll
         for (int w = 0; w < W; w++) sum += part[(jt * W + w) * 16 + nn];
+        if (div_rms) sum = sum / rms;
         if (G.swiglu) {
             if ((nn & 1) == 0) {
                 float up = 0.0f;
 #pragma unroll
                 for (int w = 0; w < W; w++) up += part[(jt * W + w) * 16 + nn + 1];
+                if (div_rms) up = up / rms;
                 yr[row >> 1] = sum * (1.0f / (1.0f + expf(-sum))) * up;
             }
         } else {
@@ -597,15 +632,15 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
 
 // ── dispatch ─────────────────────────────────────────────────────────────
 
-template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG, bool Q8A>
+template <int F, int NBW, int RD, int XO, bool RING, int W, bool RAG, bool Q8A, bool NORM>
 static int mq_launch_k(dim3 grid, size_t lds, hipStream_t s, const MqParams& G) {
     static size_t opted = 64 * 1024;  // dynamic LDS above 64 KiB is opted into per kernel
     if (lds > opted) {
-        AETH_HIP_CHECK(hipFuncSetAttribute((const void*)k_gemv_mf<F, NBW, RD, XO, RING, W, RAG, Q8A>,
+        AETH_HIP_CHECK(hipFuncSetAttribute((const void*)k_gemv_mf<F, NBW, RD, XO, RING, W, RAG, Q8A, NORM>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         opted = lds;
     }
-    hipLaunchKernelGGL((k_gemv_mf<F, NBW, RD, XO, RING, W, RAG, Q8A>), grid, dim3(64 * W), lds, s, G);
+    hipLaunchKernelGGL((k_gemv_mf<F, NBW, RD, XO, RING, W, RAG, Q8A, NORM>), grid, dim3(64 * W), lds, s, G);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
@@ -613,8 +648,11 @@ static int mq_launch_k(dim3 grid, size_t lds, hipStream_t s, const MqParams& G) 
 template <int F, int NBW, int RD, int W, bool RAG, bool Q8A>
 static int mq_launch(dim3 grid, size_t lds, hipStream_t s, const MqParams& G) {
     constexpr int XO = (NBW * MF<F>::CE / 8 + 63) / 64;
-    return G.tpw <= RD ? mq_launch_k<F, NBW, RD, XO, false, W, RAG, Q8A>(grid, lds, s, G)
-                       : mq_launch_k<F, NBW, RD, XO, true, W, RAG, Q8A>(grid, lds, s, G);
+    if (!RAG && !Q8A && G.norm_w)  // (a fused RMSNorm needs whole 256-element rows: never ragged)
+        return G.tpw <= RD ? mq_launch_k<F, NBW, RD, XO, false, W, RAG, Q8A, !RAG && !Q8A>(grid, lds, s, G)
+                           : mq_launch_k<F, NBW, RD, XO, true, W, RAG, Q8A, !RAG && !Q8A>(grid, lds, s, G);
+    return G.tpw <= RD ? mq_launch_k<F, NBW, RD, XO, false, W, RAG, Q8A, false>(grid, lds, s, G)
+                       : mq_launch_k<F, NBW, RD, XO, true, W, RAG, Q8A, false>(grid, lds, s, G);
 }
 
 template <int F, bool RAG, bool Q8A>
