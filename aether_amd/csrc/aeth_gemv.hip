@@ -477,6 +477,11 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
     float xv[XO][8], wv[XO][8];
     mq_load_x<XO, RAG>(xr, o0, o1, G.kx, xv);
     if (NORM || G.norm_w) mq_load_x<XO, RAG>(G.norm_w, o0, o1, G.kx, wv);  // (a uniform branch)
+    // the residual this thread adds in the epilogue (row t0·16 + thread, the epilogue's first
+    // pass), loaded now so that its latency hides behind the weight stream; unconditional, from
+    // x when there is none to add (a load under a branch would be waited for at its end)
+    const float* yp = G.accumulate && !G.swiglu ? yr + min(t0 * 16 + (int64_t)threadIdx.x, G.n - 1) : xr;
+    const float yprev = *yp;
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight stream
     Dt buf[RD][NBW];
 #pragma unroll
@@ -605,7 +610,7 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
                 yr[row >> 1] = sum * (1.0f / (1.0f + expf(-sum))) * up;
             }
         } else {
-            const float v = G.accumulate ? yr[row] + sum : sum;
+            const float v = G.accumulate ? (idx == (int)threadIdx.x ? yprev : yr[row]) + sum : sum;
             yr[row] = v;
             if (G.amax) {
                 const unsigned long long kk = aeth_amax_key(v, row);
