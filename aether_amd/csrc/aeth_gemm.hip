@@ -79,7 +79,7 @@
 // workgroups for m = 512). A 32-element sub-block is the groups of four
 // adjacent lanes; its sums (and its Q8_0 block) meet by DPP.
 //
-// Q8 = true (AETH_MM_Q8_ACTIVATIONS, the dot-product mode): each 32-element
+// Q8 = true (AETH_MM_Q8_ACTIVATIONS, the dot-product mode; plain input only): each 32-element
 // sub-block is first replaced by its Q8_0 activation block, dequantized —
 // quantize_q8_0_block (neon.rs:45-104): d = max|x|/127 (NaN-propagating max),
 // q = sat_i8(RNE(x·(1/d))) with the f32 d, and the value q·f16(d) the integer
@@ -117,6 +117,7 @@ __device__ __forceinline__ void prep_ld8(const float* __restrict__ p, float* v) 
 // 128 registers of a 16-wave workgroup).
 template <bool AL16, bool Q8, int MODE, int SPW, int PREP_ROWS>
 __global__ void __launch_bounds__(64 * PREP_ROWS * PREP_WK) k_gemm_prep(PrepArgs P) {
+    static_assert(!Q8 || MODE == PREP_PLAIN, "the producers feed the exact mode");
     constexpr int WK = PREP_WK;
     __shared__ __attribute__((aligned(16))) uint4 stage[WK][2][64][PREP_LD];  // [part j][hi/lo][group][row]
     __shared__ float red[2][PREP_ROWS * WK];
@@ -511,6 +512,8 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     if (ldc <= 0) ldc = w->n;
     if (mode != PREP_PLAIN && !aeth_gemm_fuses(w, m, mode, d_a, in->norm_w))
         return aeth_set_error(AETH_EINVAL, "gemm: fused producer %d not available for k=%d", mode, k);
+    if (mode != PREP_PLAIN && (flags & AETH_MM_Q8_ACTIVATIONS))  // the producers feed the exact (f32) mode only
+        return aeth_set_error(AETH_EINVAL, "gemm: fused producer %d with Q8 activations", mode);
     if (k != nb * 256) {  // ragged K: row-batched GEMV
         GemvEpi e;
         e.flags = flags;
@@ -537,13 +540,9 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     const int spw = share <= 1 ? 1 : share <= 2 ? 2 : share <= 4 ? 4 : 8;
     const PrepArgs P{d_a, in ? in->norm_w : nullptr, in ? in->eps : 0.0f, (int)m, k, esc, frag, Sh, Sl};
     const unsigned pg = (unsigned)mp;  // fragment rows (whole 64-row tiles)
-    if (mode == PREP_RMSNORM) {
-        if (q8) prep_launch<true, true, PREP_RMSNORM>(spw, pg, s, P);
-        else prep_launch<true, false, PREP_RMSNORM>(spw, pg, s, P);
-    } else if (mode == PREP_SWIGLU) {
-        if (q8) prep_launch<true, true, PREP_SWIGLU>(spw, pg, s, P);
-        else prep_launch<true, false, PREP_SWIGLU>(spw, pg, s, P);
-    } else if (al16 && q8) prep_launch<true, true, PREP_PLAIN>(spw, pg, s, P);
+    if (mode == PREP_RMSNORM) prep_launch<true, false, PREP_RMSNORM>(spw, pg, s, P);
+    else if (mode == PREP_SWIGLU) prep_launch<true, false, PREP_SWIGLU>(spw, pg, s, P);
+    else if (al16 && q8) prep_launch<true, true, PREP_PLAIN>(spw, pg, s, P);
     else if (q8) prep_launch<false, true, PREP_PLAIN>(spw, pg, s, P);
     else if (al16) prep_launch<true, false, PREP_PLAIN>(spw, pg, s, P);
     else prep_launch<false, false, PREP_PLAIN>(spw, pg, s, P);

@@ -86,43 +86,61 @@ def test_decode_8b_widths_match_oracle(gpu):
         L.aeth_runner_free(r)
 
 
-def test_prefill_8b_widths_match_oracle(gpu):
-    """Batched prefill (forward_batch, runner.rs:833-993) of 70 tokens at the
-    8B widths: the Q4_K GEMMs with the RMSNorm (q|k|v, gate|up at k = 4096)
-    and the SwiGLU (down, k = 14336) run inside their activation prep; 70 rows
-    leave 58 rows of the last 64-row tile empty."""
-    c = dict(C8B, max_seq_len=256)
+# Prefill widths: the Q4_K GEMMs' activation prep holds each wave's share of a row's ⌈k/512⌉ steps
+# (4 waves per row) in registers, rounded up to 1, 2, 4 or 8 steps, and instantiates the RMSNorm
+# producer at k = d_model and the SwiGLU producer at k = d_ff for each. (overrides of C8B, steps per
+# wave for RMSNorm / SwiGLU)
+WIDTHS = {
+    "8b": (dict(), "2 / 8"),
+    "d6144_ff8192": (dict(vocab_size=4096, d_model=6144, num_layers=1, num_heads=48, num_kv_heads=12, d_ff=8192),
+                     "4 / 4"),
+    "d9216_ff3072": (dict(vocab_size=4096, d_model=9216, num_layers=1, num_heads=72, num_kv_heads=9, d_ff=3072),
+                     "8 (18 steps: 5 5 4 4) / 2"),
+    "d2048_ff5632": (dict(vocab_size=4096, d_model=2048, num_layers=1, num_heads=16, num_kv_heads=4, d_ff=5632),
+                     "1 / 4 (11 steps: 2 3 3 3)"),
+}
+
+
+@pytest.mark.parametrize("width", list(WIDTHS))
+def test_prefill_8b_widths_match_oracle(gpu, width):
+    """Batched prefill (forward_batch, runner.rs:833-993) of 70 tokens: the
+    Q4_K GEMMs with the RMSNorm (q|k|v, gate|up at k = d_model) and the
+    SwiGLU (down, k = d_ff) run inside their activation prep; 70 rows leave
+    58 rows of the last 64-row tile empty. The 8B widths and three others
+    that reach the prep's other register shares."""
+    c = dict(C8B, max_seq_len=256, **WIDTHS[width][0])
     L = A.lib()
-    d, dff, kvd, V = c["d_model"], c["d_ff"], c["num_kv_heads"] * c["head_dim"], c["vocab_size"]
+    d, dff, V = c["d_model"], c["d_ff"], c["vocab_size"]
+    qd, kvd = c["num_heads"] * c["head_dim"], c["num_kv_heads"] * c["head_dim"]
     n = 70
     r = synthetic_runner(c, 0x8B8B8C)
     try:
         rowb = lambda k: (k // 256) * 144
-        sizes = [d * rowb(d), kvd * rowb(d), kvd * rowb(d), d * rowb(d), dff * rowb(d), dff * rowb(d), d * rowb(dff)]
+        sizes = [qd * rowb(d), kvd * rowb(d), kvd * rowb(d), d * rowb(qd), dff * rowb(d), dff * rowb(d), d * rowb(dff)]
         layers = [[export(r, j, l, sizes[j]) for j in range(7)] for l in range(c["num_layers"])]
         norms = [[export(r, 7 + j, l, d * 4, np.float32) for j in range(2)] for l in range(c["num_layers"])]
         final = export(r, 9, 0, d * 4, np.float32)
-        lm = export(r, 10, 0, V * 16 * 210)
+        lm = export(r, 10, 0, V * (d // 256) * 210)
         toks = np.random.default_rng(n).integers(0, V, n).astype(np.int32)
         emb = np.stack([export(r, 11, int(t), d * 4, np.float32) for t in toks])
         s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
         ocfg = O.LlamaCfg(V, d, c["num_layers"], c["num_heads"], c["num_kv_heads"], c["head_dim"], dff,
                           c["max_seq_len"], c["rope_base"], c["rms_norm_eps"])
-        print("8B-width prefill of %d tokens" % n, flush=True)
+        print("prefill of %d tokens, %s (prep steps per wave %s)" % (n, width, WIDTHS[width][1]), flush=True)
         logits = np.empty(V, np.float32)
         nxt = ctypes.c_int32()
         A.check(L.aeth_runner_prefill(r, toks.ctypes.data, n, logits.ctypes.data, ctypes.byref(nxt)), "prefill")
         kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), np.float32)
         ref = O.forward_batch(ocfg, emb, layers, [Q4_K] * 7, norms, final, lm, Q6_K, s, co, kv)
         assert np.isfinite(logits).all()
-        assert_close_logits(logits, ref, what="8B-width prefill")
+        assert_close_logits(logits, ref, what="%s prefill" % width)
         assert nxt.value == O.argmax(logits)
         kv_dev = np.empty_like(kv)
         fl = ctypes.c_int32()
         A.check(L.aeth_runner_kv_to_host(r, kv_dev.ctypes.data, ctypes.byref(fl)), "kv_to_host")
         assert fl.value == n
         assert_close_rows(kv_dev[:, :, :, :n].reshape(-1, c["head_dim"]), kv[:, :, :, :n].reshape(-1, c["head_dim"]),
-                          what="kv after the 8B-width prefill")
+                          what="kv after the %s prefill" % width)
     finally:
         L.aeth_runner_free(r)
 
