@@ -293,6 +293,7 @@ struct GemmArgs {
     float* C;
     int64_t ldc;  // row stride of C
     int accumulate;
+    int swiglu;   // C[row][col/2] = g·σ(g)·u over the (g, u) column pairs
 };
 
 // ── Single-K-group kernel (buffers past 2 GiB; the default is the K-split kernel
@@ -462,18 +463,26 @@ __global__ void __launch_bounds__(256) k_gemm_q4k_ring(GemmArgs G) {
     __builtin_amdgcn_s_waitcnt(0);  // the tail's loads land before the workgroup's LDS is released
 
     const int lr = lane & 31;
+    int rows[16];
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-        const int col = n0 + 64 * wn + 32 * c + lr;
+    for (int r = 0; r < 16; r++) rows[r] = m0 + 32 * wm + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+    G2Epi E[2];
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int row = m0 + 32 * wm + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-            if (row < G.m && col < G.n) {
-                const float v = acc[c][r] * G.escale[row];
-                float* dst = G.C + (int64_t)row * G.ldc + col;
-                *dst = G.accumulate ? *dst + v : v;
-            }
-        }
+    for (int c = 0; c < 2; c++)
+        g2_epi_load(E[c], G.escale, G.C, G.ldc, G.m, G.n, rows, n0 + 64 * wn + 32 * c + lr, G.accumulate);
+    if (G.swiglu) {
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2)
+                g2_store_swiglu(E[c], r, G.C, G.ldc, G.m, G.n, rows[r], n0 + 64 * wn + 32 * c + lr, acc[c][r],
+                                acc[c][r + 1]);
+    } else {
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                g2_store(E[c], r, G.C, G.ldc, G.m, G.n, rows[r], n0 + 64 * wn + 32 * c + lr, acc[c][r], G.accumulate);
     }
 }
 
@@ -505,15 +514,23 @@ bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a
     return mode == PREP_SWIGLU;
 }
 
+bool aeth_gemm_swiglu_out(const aeth_weight* w, int64_t m) {
+    return w && w->dtype == AETH_DTYPE_Q4_K && w->order == AETH_ORDER_PLANAR && m > 1 && w->k == w->nb * 256 &&
+           (w->n & 1) == 0;
+}
+
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s, int64_t ldc, void* ws, size_t ws_bytes, const GemmIn* in) {
     const int k = (int)w->k, nb = (int)w->nb;
     const int mode = in ? in->mode : PREP_PLAIN;
-    if (ldc <= 0) ldc = w->n;
+    const bool swo = in && in->swiglu_out;
+    if (ldc <= 0) ldc = swo ? w->n / 2 : w->n;
     if (mode != PREP_PLAIN && !aeth_gemm_fuses(w, m, mode, d_a, in->norm_w))
         return aeth_set_error(AETH_EINVAL, "gemm: fused producer %d not available for k=%d", mode, k);
     if (mode != PREP_PLAIN && (flags & AETH_MM_Q8_ACTIVATIONS))  // the producers feed the exact (f32) mode only
         return aeth_set_error(AETH_EINVAL, "gemm: fused producer %d with Q8 activations", mode);
+    if (swo && (!aeth_gemm_swiglu_out(w, m) || (flags & AETH_MM_ACCUMULATE)))
+        return aeth_set_error(AETH_EINVAL, "gemm: SwiGLU output needs whole super-blocks, even n, no accumulate");
     if (k != nb * 256) {  // ragged K: row-batched GEMV
         GemvEpi e;
         e.flags = flags;
@@ -552,7 +569,7 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     const int64_t qb = ntiles * nb * 2048, hb = ntiles * nb * 256, ab = mp * k * 4;
     GemmArgs G{(const uint8_t*)frag, Sh, Sl, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, (int)ntiles, gm, gn,
                (int)std::min(ab, (int64_t)INT32_MAX), (int)std::min(qb, (int64_t)INT32_MAX),
-               (int)std::min(hb, (int64_t)INT32_MAX), d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0};
+               (int)std::min(hb, (int64_t)INT32_MAX), d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0};
     const bool fits32 = qb < INT32_MAX && ab < INT32_MAX;  // buffer offsets are 32-bit
     // The K-split kernel (aeth_gemm_kq.hip); the single-K-group kernel serves buffers past the 32-bit
     // offsets of the buffer loads, and AETH_GEMM_KERNEL=2 forces it (tests)
@@ -560,7 +577,7 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     if (fits32 && env_kernel != 2) {
         KqArgs Q{(const uint8_t*)frag, (const uint8_t*)Sh, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, (int)ntiles,
                  (int)mp, gm, gn, (int)ab, (int)(mp * (k / 32) * 4), (int)qb, (int)std::min(hb, (int64_t)INT32_MAX),
-                 d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0};
+                 d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0};
         return aeth_gemm_kq_launch(Q, s);
     }
     hipLaunchKernelGGL(k_gemm_q4k_ring, dim3((unsigned)(gm * gn)), dim3(256), 0, s, G);

@@ -105,6 +105,44 @@ __device__ __forceinline__ void g2_tile(int id, int gm, int gn, int& tm, int& tn
     tn = in / rows;
 }
 
+// Epilogue of one lane: 16 outputs at rows row(r) (r < 16, each < mp) of column col.
+// g2_epi_load fetches the rows' scales 2^e and, with accumulate, C's previous values
+// (from clamped addresses, so every load is issued) before the first store: a store to C
+// may alias them, so a load after one waits for it, one round trip per output.
+struct G2Epi {
+    float es[16], pv[16];
+};
+__device__ __forceinline__ void g2_epi_load(G2Epi& E, const float* escale, const float* C, int64_t ldc, int m, int n,
+                                            const int* row, int col, int accumulate) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) E.es[r] = escale[row[r]];
+    if (accumulate) {
+        const int cc = min(col, n - 1);
+#pragma unroll
+        for (int r = 0; r < 16; r++) E.pv[r] = C[(int64_t)min(row[r], m - 1) * ldc + cc];
+    }
+}
+// Store of output r: C[row][col] = sum·2^e (+ the previous value with accumulate).
+__device__ __forceinline__ void g2_store(const G2Epi& E, int r, float* C, int64_t ldc, int m, int n, int row, int col,
+                                         float sum, int accumulate) {
+    const float v = sum * E.es[r];
+    if (row < m && col < n) C[(int64_t)row * ldc + col] = accumulate ? E.pv[r] + v : v;
+}
+// SwiGLU store of outputs r and r + 1 (r even: rows row0 and row0 + 1; columns = (g, u)
+// pairs, lane l holding column col and lane l ^ 1 its neighbour; every lane calls it): after
+// one lane swap the even lane of a pair holds (g, u) of row row0 and the odd lane those of
+// row0 + 1, and each stores h = g·σ(g)·u at C[row][col/2] (σ(g) = 1/(1 + e^-g) with the
+// reciprocal instruction).
+__device__ __forceinline__ void g2_store_swiglu(const G2Epi& E, int r, float* C, int64_t ldc, int m, int n, int row0,
+                                                int col, float sum0, float sum1) {
+    const float v0 = sum0 * E.es[r], v1 = sum1 * E.es[r + 1];
+    const int odd = col & 1;
+    const float y = __shfl_xor(odd ? v0 : v1, 1);
+    const float g = odd ? y : v0, u = odd ? v1 : y;
+    const int row = row0 + odd;
+    if (row < m && col < n) C[(int64_t)row * ldc + (col >> 1)] = g * __builtin_amdgcn_rcpf(1.0f + expf(-g)) * u;
+}
+
 // Arguments of the K-split GEMM kernel (aeth_gemm_kq.hip).
 struct KqArgs {
     const uint8_t* frag;   // A·2^-e as fp16 MFMA fragments: ((mt·(k/16) + ks)·2 + part)·1 KiB (k_gemm_prep)
@@ -118,5 +156,6 @@ struct KqArgs {
     float* C;
     int64_t ldc;
     int accumulate;
+    int swiglu;            // C[row][col/2] = g·σ(g)·u over the (g, u) column pairs
 };
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s);

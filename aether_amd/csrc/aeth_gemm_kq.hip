@@ -284,6 +284,13 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
     // waves 0..3 (slot [w - 4]); round 2: waves 0..3 write the pair sums and wave w
     // (0..7) sums (mt, c) = (w / 4, w % 4) over them in order and stores it.
     float* red = (float*)smem;  // [4][2][4][16][64] floats = 128 KiB
+    const int mt = wave >> 2, c = wave & 3, lr = lane & 31;
+    const int col = n0 + 32 * c + lr;
+    int rows[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) rows[r] = m0 + 32 * mt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    G2Epi E;  // in flight during the reduction
+    g2_epi_load(E, G.escale, G.C, G.ldc, G.m, G.n, rows, col, G.accumulate);
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -311,19 +318,19 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
                 }
     }
     __syncthreads();
-    const int mt = wave >> 2, c = wave & 3, lr = lane & 31;
-    const int col = n0 + 32 * c + lr;
+    float sum[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-        float sum = red[(((0 * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
+        sum[r] = red[(((0 * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
 #pragma unroll
-        for (int w = 1; w < 4; w++) sum += red[(((w * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
-        const int row = m0 + 32 * mt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < G.m && col < G.n) {
-            const float v = sum * G.escale[row];
-            float* dst = G.C + (int64_t)row * G.ldc + col;
-            *dst = G.accumulate ? *dst + v : v;
-        }
+        for (int w = 1; w < 4; w++) sum[r] += red[(((w * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
+    }
+    if (G.swiglu) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) g2_store_swiglu(E, r, G.C, G.ldc, G.m, G.n, rows[r], col, sum[r], sum[r + 1]);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; r++) g2_store(E, r, G.C, G.ldc, G.m, G.n, rows[r], col, sum[r], G.accumulate);
     }
 }
 

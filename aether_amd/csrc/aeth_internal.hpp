@@ -123,12 +123,18 @@ struct GemmIn {
     int mode = PREP_PLAIN;
     const float* norm_w = nullptr;
     float eps = 0.0f;
+    // the output's columns are interleaved (g, u) pairs (the gate|up weight): C receives
+    // h = g·σ(g)·u, n/2 columns per row (σ through the reciprocal instruction), instead of the pairs
+    bool swiglu_out = false;
 };
 // Whether aeth_gemm_q4k_launch runs producer `mode` for this weight and A (else
 // the caller runs the producer itself): a planar Q4_K weight, m > 1, and for
 // the RMSNorm and SwiGLU producers whole super-blocks, k ≤ 16384 and 16-byte
 // aligned A (and norm weight).
 bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w);
+// Whether aeth_gemm_q4k_launch can apply GemmIn::swiglu_out for this weight: a planar
+// Q4_K weight of even n and whole super-blocks, m > 1 (no accumulate).
+bool aeth_gemm_swiglu_out(const aeth_weight* w, int64_t m);
 // Q4_K prefill GEMM (m > 1); ldc = output row stride (0: n); in = the fused
 // producer (nullptr: plain A; any other mode must pass aeth_gemm_fuses).
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,

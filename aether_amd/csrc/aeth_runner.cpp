@@ -304,7 +304,7 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
         float* lkv = r->kv + (int64_t)l * kv_layer_floats(c);
         const float* attn_norm = r->norms + (int64_t)l * 2 * d;
         const float* ffn_norm = attn_norm + d;
-        // Q4_K GEMMs take the RMSNorm (and the SwiGLU below) inside their activation prep
+        // Q4_K GEMMs take the RMSNorm inside their activation prep (the SwiGLU: below)
         GemmIn nin;
         nin.mode = PREP_RMSNORM;
         nin.eps = c.rms_norm_eps;
@@ -331,14 +331,25 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
         const float* h = r->p_h;
         GemmIn din;  // the down GEMM's producer
         if (r->wgu[l]) {
-            nin.norm_w = ffn_norm;
+            // a Q4_K gate|up GEMM writes h = g·σ(g)·u from its epilogue (n·d_ff floats instead of the
+            // 2·n·d_ff pairs); otherwise the pairs go to p_gu and the down GEMM's prep (or
+            // k_silu_pairs) gates them
+            GemmIn gin = nin;
+            gin.norm_w = ffn_norm;
+            gin.swiglu_out = aeth_gemm_swiglu_out(r->wgu[l], n);
+            float* gu = gin.swiglu_out ? r->p_h : r->p_gu;
             if (aeth_gemm_fuses(r->wgu[l], n, PREP_RMSNORM, r->p_x, ffn_norm)) {
-                if ((rc = aeth_gemm_q4k_launch(r->wgu[l], r->p_x, n, r->p_gu, 0, s, 0, nullptr, 0, &nin))) return rc;
-            } else if ((rc = aeth_rmsnorm_launch(r->p_x, ffn_norm, n, d, c.rms_norm_eps, r->p_n, s)) ||
-                       (rc = aeth_qmatmul(r->wgu[l], r->p_n, n, r->p_gu, 0, s))) {
-                return rc;
+                if ((rc = aeth_gemm_q4k_launch(r->wgu[l], r->p_x, n, gu, 0, s, 0, nullptr, 0, &gin))) return rc;
+            } else {
+                if ((rc = aeth_rmsnorm_launch(r->p_x, ffn_norm, n, d, c.rms_norm_eps, r->p_n, s))) return rc;
+                gin.mode = PREP_PLAIN;
+                rc = gin.swiglu_out ? aeth_gemm_q4k_launch(r->wgu[l], r->p_n, n, gu, 0, s, 0, nullptr, 0, &gin)
+                                    : aeth_qmatmul(r->wgu[l], r->p_n, n, gu, 0, s);
+                if (rc) return rc;
             }
-            if (aeth_gemm_fuses(r->wdown[l], n, PREP_SWIGLU, r->p_gu, nullptr)) {  // h = g·σ(g)·u in the prep
+            if (gin.swiglu_out) {
+                h = r->p_h;
+            } else if (aeth_gemm_fuses(r->wdown[l], n, PREP_SWIGLU, r->p_gu, nullptr)) {  // in the down prep
                 din.mode = PREP_SWIGLU;
                 h = r->p_gu;
             } else if ((rc = aeth_silu_pairs_launch(r->p_gu, n * dff, r->p_h, s))) {

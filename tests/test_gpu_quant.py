@@ -605,6 +605,21 @@ for m, n, k in ((130, 200, 1024), (64, 128, 2048), (70, 48, 1280), (33, 96, 1433
     torch.cuda.synchronize()
     assert_close(y.cpu().numpy().reshape(m, n), O.reference_matmul(12, x.ravel(), raw, m, n, k), what="kernel")
     A.lib().aeth_weight_free(w)
+# a prefill: the fused RMSNorm / SwiGLU producers and the gate|up GEMM's SwiGLU epilogue on this kernel
+from tests.test_gpu_decode import TINY, build_tiny, make_runner, oracle_cfg
+from tests._util import Q4_K, assert_close_logits
+c = dict(TINY, max_seq_len=192)
+md = build_tiny(seed=21, c=c)
+r = make_runner(md, c)
+s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
+kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), dtype=np.float32)
+toks = np.random.default_rng(5).integers(0, c["vocab_size"], 150).astype(np.int32)
+logits = np.empty(c["vocab_size"], dtype=np.float32)
+A.check(A.lib().aeth_runner_prefill(r, toks.ctypes.data, 150, logits.ctypes.data, None), "prefill")
+ref = O.forward_batch(oracle_cfg(c), md["emb"][toks], md["layers"], [Q4_K] * 7, md["norms"], md["final"], md["lm"],
+                      md["lm_dtype"], s, co, kv)
+assert_close_logits(logits, ref, what="prefill")
+A.lib().aeth_runner_free(r)
 print("ok")
 """
 
@@ -613,7 +628,8 @@ print("ok")
 def test_gemm_alternate_kernels(gpu, var, val):
     """The GEMM kernel the default picks only for buffers past 2 GiB:
     AETH_GEMM_KERNEL=2 (the single-K-group ring kernel), read once per process,
-    so it runs in a fresh process."""
+    so it runs in a fresh process: plain products, then a runner prefill (its
+    fused producers and the gate|up GEMM's SwiGLU epilogue) against the oracle."""
     import os
     import subprocess
     import sys
