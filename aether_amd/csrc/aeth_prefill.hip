@@ -284,11 +284,45 @@ __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ 
 // Work: workgroup (KV head, query-block pair {p, nqb−1−p}), which balances the
 // causal triangle; its 4 waves take the 16-key blocks of a query block round
 // robin, each keeping an online softmax, and merge the partials through LDS.
+// Per key block the softmax runs in log2 units (v_exp_f32) and rescales the
+// partials only when some column's running max grows by more than 2^8: below
+// that the probabilities are taken against the stale max (at most 2^8 each;
+// the result o / l does not depend on which max is used). K and V are read as
+// buffers of the n filled rows, so the loads of rows ≥ n (the last block's
+// tail) return zeros; those keys are masked. Two register sets alternate, the
+// next block's loads in flight during the current block.
+// Max / sum of a value over the lane pairs (l, l ^ 16) and (l, l ^ 32): v_permlane16_swap and
+// v_permlane32_swap with the same register as both operands leave each lane of a pair the
+// lower lane's value in the first result and the upper lane's in the second (register moves,
+// no LDS round trip); both lanes then compute lower ∘ upper, the same bits.
+__device__ __forceinline__ float pa_max16(float a) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pa_max32(float a) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pa_sum16(float a) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pa_sum32(float a) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float4 pa_ld4(__amdgpu_buffer_rsrc_t r, int off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+}
+
 template <int G>
-__global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict__ qkv, int64_t qkv_stride,
+__global__ void __launch_bounds__(256, 2) k_attn_prefill_mf(const float* __restrict__ qkv, int64_t qkv_stride,
                                                          const float* __restrict__ layer_kv, int n, int nh, int nkv,
                                                          int64_t max_seq, float* __restrict__ out) {
     constexpr int QB = 16 / G, HD = 128, PLD = HD + 4;
+    constexpr float TH = 8.0f;  // log2 units a running max may grow before the partials are rescaled
     __shared__ __attribute__((aligned(16))) float po[4][16][PLD];  // per wave: column c, d
     __shared__ float pm[4][16], pl[4][16];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -298,7 +332,9 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict
     const int head = g * G + c % G;
     const float* K = layer_kv + (int64_t)g * max_seq * HD;
     const float* V = layer_kv + (int64_t)(nkv + g) * max_seq * HD;
-    const float scale = 1.0f / sqrtf((float)HD);
+    const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, n * HD * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, n * HD * 4, 0x00020000);
+    const float sl2 = 1.4426950408889634f / sqrtf((float)HD);  // scale · log2(e)
     for (int pass = 0; pass < 2; pass++) {
         const int qb = pass == 0 ? p : nqb - 1 - p;
         if (pass == 1 && qb == p) break;  // the middle block of an odd count (uniform)
@@ -314,59 +350,62 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict
         }
         const int kb_end = (min(q0 + QB, n) - 1) / 16;  // last key block, inclusive
         // loads of one key block: K rows t0 + c (A of Sᵀ), V rows t0 + 4·grp + j,
-        // floats [8c, 8c + 8) (A of Oᵀ); rows past n are clamped and masked
-        float4 kr[8], vr[4][2], krn[8], vrn[4][2];
+        // floats [8c, 8c + 8) (A of Oᵀ)
         auto load = [&](int kb, float4* kk, float4 (*vv)[2]) {
-            const int t0 = 16 * kb;
-            const float4* ks = (const float4*)(K + (int64_t)min(t0 + c, n - 1) * HD + 32 * grp);
+            const int ko = ((16 * kb + c) * HD + 32 * grp) * 4, vo = ((16 * kb + 4 * grp) * HD + 8 * c) * 4;
 #pragma unroll
-            for (int i = 0; i < 8; i++) kk[i] = ks[i];
+            for (int i = 0; i < 8; i++) kk[i] = pa_ld4(rK, ko + 16 * i);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float4* vs = (const float4*)(V + (int64_t)min(t0 + 4 * grp + j, n - 1) * HD + 8 * c);
-                vv[j][0] = vs[0];
-                vv[j][1] = vs[1];
+                vv[j][0] = pa_ld4(rV, vo + j * HD * 4);
+                vv[j][1] = pa_ld4(rV, vo + j * HD * 4 + 16);
             }
         };
         float m = -INFINITY, l = 0.0f;
         f32x4 o[8];
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) o[dt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        if (w <= kb_end) load(w, kr, vr);
-        for (int kb = w; kb <= kb_end; kb += 4) {
-            load(min(kb + 4, kb_end), krn, vrn);  // next block in flight during this one
+        auto step = [&](int kb, const float4* kr, const float4 (*vr)[2]) {
             const int t0 = 16 * kb;
-            f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+            // four independent chains of 8 MFMAs (d ≡ i mod 4 of each lane group's 32), summed
+            f32x4 s4[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) s4[u] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].x, qv[4 * i], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].y, qv[4 * i + 1], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].z, qv[4 * i + 2], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].w, qv[4 * i + 3], s, 0, 0, 0);
+                s4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].x, qv[4 * i], s4[0], 0, 0, 0);
+                s4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].y, qv[4 * i + 1], s4[1], 0, 0, 0);
+                s4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].z, qv[4 * i + 2], s4[2], 0, 0, 0);
+                s4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].w, qv[4 * i + 3], s4[3], 0, 0, 0);
             }
-            float mx = -INFINITY;
+            f32x4 s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+            if (t0 + 15 <= q0 && t0 + 15 < n) {  // no key of the block passes a query or n (uniform)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int t = t0 + 4 * grp + r;
-                s[r] = (t <= query && t < n) ? s[r] * scale : -INFINITY;
-                mx = fmaxf(mx, s[r]);
+                for (int r = 0; r < 4; r++) s[r] *= sl2;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int t = t0 + 4 * grp + r;
+                    s[r] = (t <= query && t < n) ? s[r] * sl2 : -INFINITY;
+                }
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m, mx);
-            const float alpha = m_new == -INFINITY ? 1.0f : expf(m - m_new);
+            float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+            mx = pa_max32(pa_max16(mx));
+            if (__any(mx > m + TH)) {  // uniform
+                const float m_new = fmaxf(m, mx);
+                const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+                l *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) o[dt] *= alpha;
+                m = m_new;
+            }
             float ps = 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                s[r] = m_new == -INFINITY ? 0.0f : expf(s[r] - m_new);
+                s[r] = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[r] - m);
                 ps += s[r];
             }
-            ps += __shfl_xor(ps, 16, 64);
-            ps += __shfl_xor(ps, 32, 64);
-            l = l * alpha + ps;
-            m = m_new;
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) o[dt] *= alpha;
+            l += pa_sum32(pa_sum16(ps));
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const float vj[8] = {vr[j][0].x, vr[j][0].y, vr[j][0].z, vr[j][0].w,
@@ -374,13 +413,15 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict
 #pragma unroll
                 for (int dt = 0; dt < 8; dt++) o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vj[dt], s[j], o[dt], 0, 0, 0);
             }
-#pragma unroll
-            for (int i = 0; i < 8; i++) kr[i] = krn[i];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                vr[j][0] = vrn[j][0];
-                vr[j][1] = vrn[j][1];
-            }
+        };
+        float4 ka[8], va[4][2], kn[8], vn[4][2];
+        if (w <= kb_end) load(w, ka, va);
+        for (int kb = w; kb <= kb_end; kb += 8) {  // two blocks per trip, the register sets alternating
+            load(min(kb + 4, kb_end), kn, vn);
+            step(kb, ka, va);
+            if (kb + 4 > kb_end) break;
+            load(min(kb + 8, kb_end), ka, va);
+            step(kb + 4, kn, vn);
         }
         // this wave's partial: column c, d = 32·grp + 8r + dt
 #pragma unroll
@@ -401,7 +442,7 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict
             float wgt[4], L = 0.0f;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                wgt[v] = pm[v][cc] == -INFINITY ? 0.0f : expf(pm[v][cc] - M);
+                wgt[v] = pm[v][cc] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pm[v][cc] - M);
                 L += wgt[v] * pl[v][cc];
             }
             float acc[8] = {};
