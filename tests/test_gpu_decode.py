@@ -145,11 +145,14 @@ def test_argmax_last_max_wins(gpu):
 # Prefill attention (attention_batch, runner.rs:1809-1883) against an f64
 # restatement of its formula: s_t = (q·k_t)/√hd for t ≤ i, max-subtracted
 # softmax, Σ p_t v_t. Group sizes 1, 2, 4, 8 take the f32-MFMA kernel, 3 the
-# f32 VALU one; ragged n against the 16-key and query blocks, the 8B shape,
-# and sharp softmaxes (scaled q).
+# f32 VALU one; ragged n against the 16-key and query blocks, n = max_seq with
+# a partial last key block (the MFMA kernel's range-checked loads read its rows
+# past n as zeros), the 8B shape, and sharp softmaxes (scaled q: the running
+# max grows by more than the kernel's rescale threshold).
 @pytest.mark.parametrize("n,nh,nkv,max_seq,qs", [(1, 4, 4, 8, 1.0), (70, 8, 2, 96, 1.0), (150, 4, 2, 192, 3.0),
                                                  (33, 8, 1, 40, 1.0), (64, 6, 2, 64, 1.0), (512, 32, 8, 512, 1.0),
-                                                 (97, 16, 4, 128, 4.0)])
+                                                 (97, 16, 4, 128, 4.0), (37, 16, 2, 37, 2.0), (45, 4, 4, 45, 1.0),
+                                                 (130, 8, 2, 160, 12.0)])
 def test_attn_prefill_matches_f64(gpu, n, nh, nkv, max_seq, qs):
     torch = gpu
     hd = 128
