@@ -34,7 +34,9 @@
 // address): A as MFMA fragments written by the prep kernel in operand order (so
 // every operand read is one contiguous ds_read_b128), the raw Q4_K quants of the
 // 16-row tile layout, and the tiles' headers. The waves dequantise their own B
-// operands from the raw bytes in LDS straight into registers.
+// operands from the raw bytes in LDS straight into registers. Their epilogue
+// (aeth_gemm_common.hpp) stores C, adds it to C (accumulate), or for a gate|up
+// weight of interleaved (g, u) rows stores h = g·σ(g)·u (GemmIn::swiglu_out).
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
