@@ -208,6 +208,30 @@ def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512, wan
             "cpu_model": cpu_model}
 
 
+def bench_decode_eager(torch, A, n_tokens=128, prefilled=2048):
+    """The decode step of bench_decode's model without the HIP graph: each token's
+    kernels are launched one by one (aeth_runner_generate with use_graph = 0).
+    Not in the default sections; its launches carry no graph, so per-dispatch
+    counters (rocprofv3 --pmc) can be collected over it."""
+    L = A.lib()
+    cfg = A.LlamaConfig(vocab_size=128256, d_model=4096, num_layers=32, num_heads=32, num_kv_heads=8, head_dim=128,
+                        d_ff=14336, max_seq_len=4096, rope_base=500000.0, rms_norm_eps=1e-5)
+    dt = (ctypes.c_int32 * (32 * 7))(*([12] * (32 * 7)))
+    r = ctypes.c_void_p()
+    A.check(L.aeth_runner_create(ctypes.byref(cfg), None, dt, None, None, None, 14, None, 0x8B8B8B,
+                                 ctypes.byref(r)), "runner_create")
+    toks = (ctypes.c_int32 * n_tokens)()
+    A.check(L.aeth_runner_fill_kv(r, 0x4B56, prefilled), "fill_kv")
+    A.check(L.aeth_runner_generate(r, 1, prefilled, 2, toks, 0), "warmup generate")
+    A.check(L.aeth_runner_fill_kv(r, 0x4B56, prefilled), "fill_kv")
+    t0 = time.perf_counter()
+    A.check(L.aeth_runner_generate(r, 1, prefilled, n_tokens, toks, 0), "generate (eager)")
+    dt_s = time.perf_counter() - t0
+    L.aeth_runner_free(r)
+    return {"tok_s": n_tokens / dt_s, "ms_per_token": dt_s * 1e3 / n_tokens, "tokens": n_tokens,
+            "first_tokens": list(toks)[:8]}
+
+
 def export_decode_model(A, r, cfg, prefilled, tokens):
     """Host copies of what the CPU decode step reads: every layer weight (raw
     GGUF row blocks), the norms, the LM head, the KV cache refilled to
@@ -397,7 +421,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,decode",
                     help="comma-separated extra sections to run: floor, q8, q6, q5, dotprod, gemm, gemm_q8, gemm_q6k, "
-                         "decode (default), f16, q2k (GGUF-order formats, not run by default)")
+                         "decode (default), f16, q2k (GGUF-order formats), decode_eager (the decode step "
+                         "without its HIP graph; these three not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (HBM counter calibration under rocprofv3)")
@@ -530,6 +555,12 @@ def main():
         extra["prefill_8b_q4k_512"] = {"tok/s": round(d["prefill_tok_s"], 1), "ms": round(d["prefill_ms"], 2),
                                        "TFLOP/s": round(d["prefill_tflops"], 2), "tokens": 512}
         print("[bench] prefill 8B: %s" % extra["prefill_8b_q4k_512"], file=sys.stderr, flush=True)
+
+    if "decode_eager" in sections:  # not a default section: the same decode without the HIP graph
+        d = bench_decode_eager(torch, A, n_tokens=max(2, min(args.steps, 128)))
+        extra["decode_8b_q4k_eager"] = {"tok/s": round(d["tok_s"], 1), "ms_per_token": round(d["ms_per_token"], 4),
+                                        "tokens": d["tokens"], "prefilled": 2048, "first_tokens": d["first_tokens"]}
+        print("[bench] decode 8B eager: %s" % extra["decode_8b_q4k_eager"], file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:
