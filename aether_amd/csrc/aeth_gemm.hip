@@ -507,8 +507,16 @@ static void prep_launch(int spw, unsigned mp, hipStream_t s, const PrepArgs& P) 
     else prep_launch_r<AL16, Q8, MODE, 8>(mp, s, P);
 }
 
+bool aeth_q4k_gemm_rows(const aeth_weight* w, int64_t m) {
+    // measured (prep + GEMM against the row-batched GEMV, weights from HBM): 14336 × 4096 at m = 2 / 4 / 8:
+    // 35.8 / 35.1 / 35.3 µs against 13.3 / 22.0 / 37.5; 4096 × 4096 at m = 2 / 8 / 12: 30.5 / 30.9 / 30.9
+    // against 5.8 / 15.1 / 20.9
+    return m >= 16 || (m >= 8 && w->n > 8192);
+}
+
 bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {
     if (!w || w->dtype != AETH_DTYPE_Q4_K || w->order != AETH_ORDER_PLANAR || m <= 1) return false;
+    if (!aeth_q4k_gemm_rows(w, m)) return false;  // the runner takes the GEMV path and its own producers
     if (mode == PREP_PLAIN) return true;
     if (w->k != w->nb * 256) return false;  // ragged K goes to the row-batched GEMV
     if (w->k > 16384 || ((uintptr_t)d_a & 15)) return false;  // one chunk of registers per wave, float4 loads
@@ -518,7 +526,7 @@ bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a
 
 bool aeth_gemm_swiglu_out(const aeth_weight* w, int64_t m) {
     return w && w->dtype == AETH_DTYPE_Q4_K && w->order == AETH_ORDER_PLANAR && m > 1 && w->k == w->nb * 256 &&
-           (w->n & 1) == 0;
+           (w->n & 1) == 0 && aeth_q4k_gemm_rows(w, m);
 }
 
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,

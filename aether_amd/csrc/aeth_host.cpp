@@ -81,7 +81,7 @@ int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_
     // apart; for k % 256 != 0 only the dequantized product reproduces that (aeth_blas.cpp)
     if (m > 1 && (flags & AETH_MM_Q8_ACTIVATIONS) && kquant && (w->k % 256) != 0)
         return aeth_dequant_gemm_launch(w, d_a, m, d_c, ldc, flags, s);
-    if (m > 1 && w->dtype == AETH_DTYPE_Q4_K && w->order == AETH_ORDER_PLANAR)
+    if (m > 1 && w->dtype == AETH_DTYPE_Q4_K && w->order == AETH_ORDER_PLANAR && aeth_q4k_gemm_rows(w, m))
         return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
     // the other block formats from 16 rows on: dequantized once, one SGEMM (instead
     // of the weight streamed once per row by the batched GEMV). Their dequantized

@@ -303,7 +303,7 @@ def test_synthetic_generator_deterministic(gpu):
 # leaves waves idle); m and n off the 64 × 128 tile grid.
 # Row magnitudes span 2^-12 .. 2^20 (the per-block fp16 exponent), with an
 # all-zero row, and the accumulate epilogue is checked on top.
-@pytest.mark.parametrize("m,n,k", [(70, 130, 768), (65, 300, 1024), (130, 40, 2560), (3, 16, 512), (45, 48, 16384),
+@pytest.mark.parametrize("m,n,k", [(70, 130, 768), (65, 300, 1024), (130, 40, 2560), (16, 16, 512), (45, 48, 16384),
                                    (34, 64, 20480), (37, 96, 8192)])
 def test_gemm_q4k_tiles_exponents_accumulate(gpu, m, n, k):
     """Ragged tiles, per-row exponents (2^20, 2^-12, zero rows, a block past
@@ -332,6 +332,28 @@ def test_gemm_q4k_tiles_exponents_accumulate(gpu, m, n, k):
     assert_close_rows(got, ref, what="gemm (scaled rows) m=%d n=%d k=%d" % (m, n, k))
     assert_close(got_acc[plain], (ref + y0)[plain], what="gemm accumulate m=%d n=%d k=%d" % (m, n, k))
     assert np.all(got[(2 * m) // 3] == 0.0)
+
+
+# Small batches of Q4_K rows: up to 15 rows (7 when n > 8192) take the row-batched
+# GEMV, more the GEMM (aeth_q4k_gemm_rows); both sides of each boundary, plain,
+# accumulate and the dot-product mode (a14 activation blocks).
+@pytest.mark.parametrize("m,n", [(2, 4096), (7, 14336), (8, 14336), (12, 6144), (15, 8192), (16, 4096)])
+def test_q4k_small_batches(gpu, m, n):
+    k = 4096
+    rng = np.random.default_rng(m * 101 + n)
+    raw = weight(Q4_K, n, k, 5 * n + m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = make_weight(gpu, Q4_K, n, k, raw)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    got = gemv(gpu, w, x.ravel(), n, m)
+    got_acc = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    got_q8 = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q4_K, x.ravel(), raw, m, n, k).reshape(m, n)
+    assert_close(got, ref, what="q4_k m=%d n=%d" % (m, n))
+    assert_close(got_acc, ref + y0, what="q4_k accumulate m=%d n=%d" % (m, n))
+    ref_q8 = O.dotprod_ref(Q4_K, O.quantize_activations_q8_0(x.ravel(), m, k), raw, m, n, k).reshape(m, n)
+    assert_close(got_q8, ref_q8, what="q4_k dot-product mode m=%d n=%d" % (m, n))
 
 
 @pytest.mark.parametrize("n", [4096, 14336])
