@@ -1,4 +1,4 @@
-// Batched products (m ≥ 16) for the block formats without a matrix-core GEMM
+// Batched products (from a few hundred rows, per format: aeth_host.cpp) for the block formats without a matrix-core GEMM
 // of their own: Q8_0, Q5_K and Q6_K rows, and Q2_K / Q3_K (GGUF order or
 // rows). The weight is dequantized once per call (bit-exact with
 // src/loader/dequant.rs), weight and activations are widened to f64, and one

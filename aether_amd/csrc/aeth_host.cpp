@@ -71,8 +71,20 @@ void aeth_stream_scratch_release(hipStream_t s) {
 }
 
 namespace {
-constexpr int64_t kDequantGemmRows = 16;
+// Rows from which a block format's product is dequantized once and run as one DGEMM
+// (aeth_blas.cpp) instead of the row-batched GEMV: the DGEMM costs about the same for
+// any m up to 512 (≈ 0.5 ms at 4096 × 4096, 2.7 ms at 4096 × 14336), the GEMV adds
+// 1.5–2.6 µs per row at 4096 × 4096. Measured crossovers at 4096 × 4096 (HIP events,
+// rotated weight copies): Q8_0 ≈ 380 rows, Q5_K ≈ 290, Q6_K and Q2_K ≈ 256, Q3_K ≈ 190.
+int64_t dequant_gemm_rows(int dtype) {
+    switch (dtype) {
+        case AETH_DTYPE_Q8_0: return 384;
+        case AETH_DTYPE_Q5_K: return 288;
+        case AETH_DTYPE_Q3_K: return 192;
+        default: return 256;
+    }
 }
+}  // namespace
 
 int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
                     hipStream_t s) {
@@ -83,12 +95,12 @@ int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_
         return aeth_dequant_gemm_launch(w, d_a, m, d_c, ldc, flags, s);
     if (m > 1 && w->dtype == AETH_DTYPE_Q4_K && w->order == AETH_ORDER_PLANAR && aeth_q4k_gemm_rows(w, m))
         return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
-    // the other block formats from 16 rows on: dequantized once, one SGEMM (instead
+    // the other block formats from a few hundred rows on: dequantized once, one DGEMM (instead
     // of the weight streamed once per row by the batched GEMV). Their dequantized
     // weights are finite (K-quant scales go through decode_d), so the SGEMM's
     // 0·w terms equal matmul_f32_gguf's skipped rows; F32 / F16 weights, which may
     // hold infinities, keep the kernels that skip zero activations as the reference does.
-    if (m >= kDequantGemmRows && w->dtype != AETH_DTYPE_F32 && w->dtype != AETH_DTYPE_F16)
+    if (m >= dequant_gemm_rows(w->dtype) && w->dtype != AETH_DTYPE_F32 && w->dtype != AETH_DTYPE_F16)
         return aeth_dequant_gemm_launch(w, d_a, m, d_c, ldc, flags, s);
     GemvEpi e;
     e.flags = flags;

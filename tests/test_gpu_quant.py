@@ -663,13 +663,15 @@ def test_gemm_alternate_kernels(gpu, var, val):
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:]
 
 
-# Batched products of the block formats without a GEMM kernel of their own
-# (m >= 16): the weight is dequantized once and multiplied by one SGEMM —
-# planar Q8_0 / Q5_K / Q6_K rows (including Q8_0's ragged k and K-quant rows
-# whose tail past k/256 blocks the reference ignores), GGUF-order Q2_K / Q3_K,
-# accumulate, and the dot-product mode's Q8_0 activation blocks.
-@pytest.mark.parametrize("dtype,m,n,k", [(Q8_0, 16, 300, 1000), (Q8_0, 150, 512, 4096), (Q5_K, 70, 256, 2048),
-                                         (Q6_K, 150, 1024, 4096), (Q6_K, 33, 96, 14336), (Q5_K, 20, 64, 600)])
+# Batched products of the block formats without a GEMM kernel of their own:
+# below a per-format row count (Q8_0 384, Q5_K 288, Q6_K 256) the row-batched
+# GEMV, from it the weight dequantized once and one DGEMM — planar Q8_0 / Q5_K /
+# Q6_K rows (including Q8_0's ragged k and K-quant rows whose tail past k/256
+# blocks the reference ignores), accumulate, and the dot-product mode's Q8_0
+# activation blocks, on both paths.
+@pytest.mark.parametrize("dtype,m,n,k", [(Q8_0, 16, 300, 1000), (Q8_0, 400, 128, 1000), (Q8_0, 150, 512, 4096),
+                                         (Q5_K, 70, 256, 2048), (Q5_K, 300, 64, 2048), (Q6_K, 150, 1024, 4096),
+                                         (Q6_K, 260, 96, 4096), (Q6_K, 33, 96, 14336), (Q5_K, 20, 64, 600)])
 def test_batched_dequant_gemm(gpu, dtype, m, n, k):
     rng = np.random.default_rng(m + n + k + dtype)
     raw = weight(dtype, n, k, 5 * n + k)
@@ -687,7 +689,9 @@ def test_batched_dequant_gemm(gpu, dtype, m, n, k):
     assert_close(got_q8, ref_q8, what="batched dot-product mode")
 
 
-@pytest.mark.parametrize("dtype,m,n,k", [(Q2_K, 40, 512, 1024), (Q3_K, 16, 768, 512), (Q3_K, 64, 300, 512)])
+# GGUF-order Q2_K / Q3_K: the row-batched GEMV, and from 256 / 192 rows the dequantized DGEMM.
+@pytest.mark.parametrize("dtype,m,n,k", [(Q2_K, 40, 512, 1024), (Q2_K, 260, 64, 1024), (Q3_K, 16, 768, 512),
+                                         (Q3_K, 64, 300, 512), (Q3_K, 200, 96, 512)])
 def test_batched_dequant_gemm_gguf_order(gpu, dtype, m, n, k):
     rng = np.random.default_rng(n + k + m)
     raw = synth_blocks(dtype, n * k // 256, n + 3 * k + dtype)
