@@ -31,13 +31,16 @@ __global__ void k_widen(const float* __restrict__ src, int64_t rows, int64_t col
     }
 }
 
-// c = (float)p, or c + (float)p with accumulate (the reference adds the f32 product)
-__global__ void k_narrow(const double* __restrict__ p, int64_t m, int64_t n, float* __restrict__ c, int64_t ldc,
-                         int accumulate) {
+// c = (float)p, or c + (float)p with accumulate (the reference adds the f32 product); p is
+// the sum, in order, of `parts` K-range products m·n apart
+__global__ void k_narrow(const double* __restrict__ p, int64_t m, int64_t n, int parts, float* __restrict__ c,
+                         int64_t ldc, int accumulate) {
     const int64_t total = m * n;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = i / n, j = i - r * n;
-        const float v = (float)p[i];
+        double sum = p[i];
+        for (int q = 1; q < parts; q++) sum += p[(int64_t)q * total + i];
+        const float v = (float)sum;
         float* dst = c + r * ldc + j;
         *dst = accumulate ? *dst + v : v;
     }
@@ -99,12 +102,19 @@ int aeth_dequant_gemm_launch(const aeth_weight* w, const float* d_a, int64_t m, 
     const int64_t wf_b = aeth_cdiv(wfloats * 4, 256) * 256, raw_b = planar ? aeth_cdiv(w->bytes, 256) * 256 : 0;
     const int64_t w64_b = aeth_cdiv(n * kx * 8, 256) * 256, a64_b = aeth_cdiv(m * kx * 8, 256) * 256;
     const int64_t kb = aeth_cdiv(k, 32);
+    // K split into `parts` ranges, one batch of the DGEMM each, when its 128 × 128 tiles would leave
+    // CUs idle (m = 512, n = 4096: 128 tiles): the f64 partial products are summed in order after
+    int parts = 1;
+    {
+        const int64_t tiles = aeth_cdiv(n, 128) * aeth_cdiv(m, 128), cus = aeth_num_cus();
+        while (parts < 4 && tiles * parts * 2 <= cus && kx % (parts * 2) == 0 && kx / (parts * 2) >= 512) parts *= 2;
+    }
     // the int8 dot-product path exists for Q8_0 / Q4_K / Q5_K / Q6_K only (the flag is ignored otherwise)
     const bool q8 = (flags & AETH_MM_Q8_ACTIVATIONS) && aeth_dtype_fused(w->dtype);
     const int64_t q_b = q8 ? aeth_cdiv(m * kb * 34, 256) * 256 + m * kb * 32 * 4 : 0;
     void* ws = nullptr;
-    if ((rc = aeth_stream_scratch(s, AETH_SCRATCH_DEQ, (size_t)(wf_b + raw_b + w64_b + a64_b + m * n * 8 + q_b + 256),
-                                  &ws)))
+    if ((rc = aeth_stream_scratch(s, AETH_SCRATCH_DEQ,
+                                  (size_t)(wf_b + raw_b + w64_b + a64_b + parts * m * n * 8 + q_b + 256), &ws)))
         return rc;
     uint8_t* base = (uint8_t*)ws;
     float* Wf = (float*)base;
@@ -112,7 +122,7 @@ int aeth_dequant_gemm_launch(const aeth_weight* w, const float* d_a, int64_t m, 
     double* W64 = (double*)(tmp + raw_b);
     double* A64 = (double*)((uint8_t*)W64 + w64_b);
     double* P64 = (double*)((uint8_t*)A64 + a64_b);
-    uint8_t* qbuf = (uint8_t*)(P64 + m * n);
+    uint8_t* qbuf = (uint8_t*)(P64 + parts * m * n);
     const void* raw = w->base;
     if (planar) {  // back to GGUF row blocks, then dequantize
         if ((rc = aeth_weight_export_raw(w, tmp, 1, s))) return rc;
@@ -141,13 +151,16 @@ int aeth_dequant_gemm_launch(const aeth_weight* w, const float* d_a, int64_t m, 
     AETH_LAUNCH_CHECK();
     rocblas_handle h = nullptr;
     if ((rc = blas_handle(s, &h))) return rc;
-    // column-major view: Pᵀ (n × m, ld n) = Wop (n × kx) · A64ᵀ (kx × m, ld kx)
+    // column-major view: Pᵀ (n × m, ld n) = Wop (n × kx) · A64ᵀ (kx × m, ld kx); batch q takes the
+    // K range [q·kc, (q + 1)·kc): kc columns of A64ᵀ's rows and of Wop's (rows of W64 for [n][k]
+    // weights, kc·n elements on for GGUF [k][n]), into its own n × m product
     const double alpha = 1.0, beta = 0.0;
-    const rocblas_status st =
-        rocblas_dgemm(h, rows ? rocblas_operation_transpose : rocblas_operation_none, rocblas_operation_none, (int)n,
-                      (int)m, (int)kx, &alpha, W64, rows ? (int)kx : (int)n, A64, (int)kx, &beta, P64, (int)n);
+    const int64_t kc = kx / parts;
+    const rocblas_status st = rocblas_dgemm_strided_batched(
+        h, rows ? rocblas_operation_transpose : rocblas_operation_none, rocblas_operation_none, (int)n, (int)m, (int)kc,
+        &alpha, W64, rows ? (int)kx : (int)n, rows ? kc : kc * n, A64, (int)kx, kc, &beta, P64, (int)n, m * n, parts);
     if (st != rocblas_status_success) return aeth_set_error(AETH_EHIP, "rocblas_dgemm failed (status %d)", (int)st);
-    hipLaunchKernelGGL(k_narrow, dim3(grid_for(m * n)), dim3(256), 0, s, P64, m, n, d_c, ldc,
+    hipLaunchKernelGGL(k_narrow, dim3(grid_for(m * n)), dim3(256), 0, s, P64, m, n, parts, d_c, ldc,
                        (flags & AETH_MM_ACCUMULATE) ? 1 : 0);
     AETH_LAUNCH_CHECK();
     return AETH_OK;

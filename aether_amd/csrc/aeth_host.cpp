@@ -72,16 +72,18 @@ void aeth_stream_scratch_release(hipStream_t s) {
 
 namespace {
 // Rows from which a block format's product is dequantized once and run as one DGEMM
-// (aeth_blas.cpp) instead of the row-batched GEMV: the DGEMM costs about the same for
-// any m up to 512 (≈ 0.5 ms at 4096 × 4096, 2.7 ms at 4096 × 14336), the GEMV adds
-// 1.5–2.6 µs per row at 4096 × 4096. Measured crossovers at 4096 × 4096 (HIP events,
-// rotated weight copies): Q8_0 ≈ 380 rows, Q5_K ≈ 290, Q6_K and Q2_K ≈ 256, Q3_K ≈ 190.
+// (aeth_blas.cpp, its K range split over batches until the tiles fill the chip) instead
+// of the row-batched GEMV: the DGEMM costs about the same for any m up to a few hundred
+// (4096 × 4096: 0.15 ms, 4096 × 14336: 0.73 ms), the GEMV grows with m (≈ 2 µs per row
+// at 4096 × 4096). Measured crossovers (HIP events, rotated weight copies): Q6_K 4096 ×
+// 4096 ≈ 64 rows, 4096 × 14336 ≈ 80, 1024 × 4096 ≈ 136; Q8_0 ≈ 112; Q5_K ≈ 80; Q2_K ≈ 40
+// and Q3_K ≈ 32 (GGUF order).
 int64_t dequant_gemm_rows(int dtype) {
     switch (dtype) {
-        case AETH_DTYPE_Q8_0: return 384;
-        case AETH_DTYPE_Q5_K: return 288;
-        case AETH_DTYPE_Q3_K: return 192;
-        default: return 256;
+        case AETH_DTYPE_Q8_0: return 112;
+        case AETH_DTYPE_Q2_K: return 40;
+        case AETH_DTYPE_Q3_K: return 32;
+        default: return 80;  // Q5_K, Q6_K
     }
 }
 }  // namespace

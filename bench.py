@@ -543,7 +543,7 @@ def main():
     if "gemm_q6k" in sections:  # batched Q6_K (dequantized once, one SGEMM): a Q4_K_M file's attn_v / ffn_down
         r = bench_batched(torch, A, 14, 4096, 4096, 512, max(3, min(args.steps, 20)), 2)
         extra["q6_k_batched_m512_n4096"] = {"TFLOP/s": round(r["tflops"], 2), "ms": round(r["ms"], 4),
-                                             "path": "dequantized once, widened to f64, one rocBLAS DGEMM"}
+                                             "path": "dequantized once, widened to f64, rocBLAS DGEMM split over K"}
         print("[bench] Q6_K batched m=512: %s" % extra["q6_k_batched_m512_n4096"], file=sys.stderr, flush=True)
     if "decode" in sections:
         d = bench_decode(torch, A, want_cpu=want_cpu)

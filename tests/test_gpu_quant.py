@@ -664,7 +664,7 @@ def test_gemm_alternate_kernels(gpu, var, val):
 
 
 # Batched products of the block formats without a GEMM kernel of their own:
-# below a per-format row count (Q8_0 384, Q5_K 288, Q6_K 256) the row-batched
+# below a per-format row count (Q8_0 112, Q5_K and Q6_K 80) the row-batched
 # GEMV, from it the weight dequantized once and one DGEMM — planar Q8_0 / Q5_K /
 # Q6_K rows (including Q8_0's ragged k and K-quant rows whose tail past k/256
 # blocks the reference ignores), accumulate, and the dot-product mode's Q8_0
@@ -689,9 +689,9 @@ def test_batched_dequant_gemm(gpu, dtype, m, n, k):
     assert_close(got_q8, ref_q8, what="batched dot-product mode")
 
 
-# GGUF-order Q2_K / Q3_K: the row-batched GEMV, and from 256 / 192 rows the dequantized DGEMM.
-@pytest.mark.parametrize("dtype,m,n,k", [(Q2_K, 40, 512, 1024), (Q2_K, 260, 64, 1024), (Q3_K, 16, 768, 512),
-                                         (Q3_K, 64, 300, 512), (Q3_K, 200, 96, 512)])
+# GGUF-order Q2_K / Q3_K: the row-batched GEMV, and from 40 / 32 rows the dequantized DGEMM.
+@pytest.mark.parametrize("dtype,m,n,k", [(Q2_K, 24, 512, 1024), (Q2_K, 40, 512, 1024), (Q2_K, 260, 64, 1024),
+                                         (Q3_K, 16, 768, 512), (Q3_K, 64, 300, 512), (Q3_K, 200, 96, 512)])
 def test_batched_dequant_gemm_gguf_order(gpu, dtype, m, n, k):
     rng = np.random.default_rng(n + k + m)
     raw = synth_blocks(dtype, n * k // 256, n + 3 * k + dtype)
