@@ -19,6 +19,7 @@ SOURCES = [
     "aeth_gemv_ext.hip",
     "aeth_gemm.hip",
     "aeth_gemm_kq.hip",
+    "aeth_gemm_q6k.hip",
     "aeth_decode_ops.hip",
     "aeth_prefill.hip",
     "aeth_backend.hip",
@@ -42,6 +43,7 @@ def hipcc():
 EXTRA = {
     "aeth_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "aeth_gemm_kq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "aeth_gemm_q6k.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 COMMON = [

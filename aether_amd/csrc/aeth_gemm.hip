@@ -507,6 +507,41 @@ static void prep_launch(int spw, unsigned mp, hipStream_t s, const PrepArgs& P) 
     else prep_launch_r<AL16, Q8, MODE, 8>(mp, s, P);
 }
 
+// The activation prep of the Q4_K and Q6_K GEMMs: A (or, with `in`, its producer's input) into
+// hi/lo fp16 MFMA fragments, sub-block sums and row scales in ws (the stream's scratch when null).
+static int gemm_prep(const float* d_a, int64_t m, int k, unsigned flags, const GemmIn* in, hipStream_t s, void* ws,
+                     size_t ws_bytes, _Float16*& frag, _Float16*& Sh, float*& esc) {
+    const int mode = in ? in->mode : PREP_PLAIN;
+    const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM;  // fragment rows: whole 64-row tiles
+    if (mp > (1LL << 20) || mp * k > (1LL << 29)) return aeth_set_error(AETH_EINVAL, "gemm: m=%lld too large", (long long)m);
+    const size_t need = (size_t)aeth_gemm_ws_bytes(m, k);
+    if (ws && ws_bytes < need)
+        return aeth_set_error(AETH_EINVAL, "gemm: workspace of %zu bytes < %zu needed", ws_bytes, need);
+    if (!ws) {
+        int rc = aeth_stream_scratch(s, AETH_SCRATCH_GEMM, need, &ws);
+        if (rc) return rc;
+    }
+    frag = (_Float16*)ws;
+    Sh = frag + (size_t)mp * k * 2;
+    _Float16* Sl = Sh + (size_t)mp * (k / 32);
+    esc = (float*)(Sl + (size_t)mp * (k / 32));
+    const bool al16 = ((uintptr_t)d_a & 15) == 0;
+    const bool q8 = (flags & AETH_MM_Q8_ACTIVATIONS) != 0;
+    // registers per wave: its share of the row's steps, rounded up to 1, 2, 4 or 8 (past 8: chunks)
+    const int share = (int)aeth_cdiv(aeth_cdiv(k, 512), PREP_WK);
+    const int spw = share <= 1 ? 1 : share <= 2 ? 2 : share <= 4 ? 4 : 8;
+    const PrepArgs P{d_a, in ? in->norm_w : nullptr, in ? in->eps : 0.0f, (int)m, k, esc, frag, Sh, Sl};
+    const unsigned pg = (unsigned)mp;  // fragment rows (whole 64-row tiles)
+    if (mode == PREP_RMSNORM) prep_launch<true, false, PREP_RMSNORM>(spw, pg, s, P);
+    else if (mode == PREP_SWIGLU) prep_launch<true, false, PREP_SWIGLU>(spw, pg, s, P);
+    else if (al16 && q8) prep_launch<true, true, PREP_PLAIN>(spw, pg, s, P);
+    else if (q8) prep_launch<false, true, PREP_PLAIN>(spw, pg, s, P);
+    else if (al16) prep_launch<true, false, PREP_PLAIN>(spw, pg, s, P);
+    else prep_launch<false, false, PREP_PLAIN>(spw, pg, s, P);
+    AETH_LAUNCH_CHECK();
+    return AETH_OK;
+}
+
 bool aeth_q4k_gemm_rows(const aeth_weight* w, int64_t m) {
     // measured (prep + GEMM against the row-batched GEMV, weights from HBM): 14336 × 4096 at m = 2 / 4 / 8:
     // 35.8 / 35.1 / 35.3 µs against 13.3 / 22.0 / 37.5; 4096 × 4096 at m = 2 / 8 / 12: 30.5 / 30.9 / 30.9
@@ -548,32 +583,11 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
         return aeth_gemv_launch_ex(w, d_a, m, d_c, e, s);
     }
     const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM;  // fragment rows: whole 64-row tiles
-    if (mp > (1LL << 20) || mp * k > (1LL << 29)) return aeth_set_error(AETH_EINVAL, "gemm: m=%lld too large", (long long)m);
-    const size_t need = (size_t)aeth_gemm_ws_bytes(m, k);
-    if (ws && ws_bytes < need)
-        return aeth_set_error(AETH_EINVAL, "gemm: workspace of %zu bytes < %zu needed", ws_bytes, need);
-    if (!ws) {
-        int rc = aeth_stream_scratch(s, AETH_SCRATCH_GEMM, need, &ws);
-        if (rc) return rc;
-    }
-    _Float16* frag = (_Float16*)ws;
-    _Float16* Sh = frag + (size_t)mp * k * 2;
-    _Float16* Sl = Sh + (size_t)mp * (k / 32);
-    float* esc = (float*)(Sl + (size_t)mp * (k / 32));
-    const bool al16 = ((uintptr_t)d_a & 15) == 0;
-    const bool q8 = (flags & AETH_MM_Q8_ACTIVATIONS) != 0;
-    // registers per wave: its share of the row's steps, rounded up to 1, 2, 4 or 8 (past 8: chunks)
-    const int share = (int)aeth_cdiv(aeth_cdiv(k, 512), PREP_WK);
-    const int spw = share <= 1 ? 1 : share <= 2 ? 2 : share <= 4 ? 4 : 8;
-    const PrepArgs P{d_a, in ? in->norm_w : nullptr, in ? in->eps : 0.0f, (int)m, k, esc, frag, Sh, Sl};
-    const unsigned pg = (unsigned)mp;  // fragment rows (whole 64-row tiles)
-    if (mode == PREP_RMSNORM) prep_launch<true, false, PREP_RMSNORM>(spw, pg, s, P);
-    else if (mode == PREP_SWIGLU) prep_launch<true, false, PREP_SWIGLU>(spw, pg, s, P);
-    else if (al16 && q8) prep_launch<true, true, PREP_PLAIN>(spw, pg, s, P);
-    else if (q8) prep_launch<false, true, PREP_PLAIN>(spw, pg, s, P);
-    else if (al16) prep_launch<true, false, PREP_PLAIN>(spw, pg, s, P);
-    else prep_launch<false, false, PREP_PLAIN>(spw, pg, s, P);
-    AETH_LAUNCH_CHECK();
+    _Float16 *frag, *Sh;
+    float* esc;
+    int rc = gemm_prep(d_a, m, k, flags, in, s, ws, ws_bytes, frag, Sh, esc);
+    if (rc) return rc;
+    const _Float16* Sl = Sh + (size_t)mp * (k / 32);
     const int gm = (int)(mp / G2_BM), gn = (int)aeth_cdiv(w->n, G2_BN);
     const int64_t ntiles = aeth_cdiv(w->n, 16);
     const int64_t qb = ntiles * nb * 2048, hb = ntiles * nb * 256, ab = mp * k * 4;
@@ -593,4 +607,46 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     hipLaunchKernelGGL(k_gemm_q4k_ring, dim3((unsigned)(gm * gn)), dim3(256), 0, s, G);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
+}
+
+bool aeth_q6k_gemm_rows(const aeth_weight* w, int64_t m) {
+    if (!w || w->dtype != AETH_DTYPE_Q6_K || w->order != AETH_ORDER_PLANAR || w->k != w->nb * 256) return false;
+    const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM, ntiles = aeth_cdiv(w->n, 16);
+    // buffer offsets are 32-bit (the larger products take the dequantized DGEMM)
+    if (ntiles * w->nb * 3072 >= INT32_MAX || mp * w->k * 4 >= INT32_MAX || mp > (1LL << 20)) return false;
+    // AETH_Q6K_GEMM_ROWS=r takes the GEMM from r rows whatever the weight's size (tests; read once)
+    static const int64_t env_rows = getenv("AETH_Q6K_GEMM_ROWS") ? atoll(getenv("AETH_Q6K_GEMM_ROWS")) : 0;
+    if (env_rows > 0) return m >= env_rows;
+    // The row-batched GEMV streams the weight once per row; the GEMM costs a near-constant
+    // ≈ 31 µs (k = 4096) to 45 µs (k = 14336) up to 64 rows. Measured crossovers (HIP events,
+    // rotated weight copies): 1024 × 4096 ≈ 53 rows, 4096 × 4096 ≈ 13, 4096 × 14336 and
+    // 14336 × 4096 ≈ 5, i.e. where m · (weight bytes) reaches ≈ 200 MB.
+    return m * w->nb * w->n * 210 >= 200000000LL;
+}
+
+int aeth_gemm_q6k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
+                         hipStream_t s, int64_t ldc) {
+    if (!aeth_q6k_gemm_rows(w, m)) return aeth_set_error(AETH_EINVAL, "gemm q6_k: shape not taken (m=%lld)", (long long)m);
+    const int k = (int)w->k, nb = (int)w->nb;
+    if (ldc <= 0) ldc = w->n;
+    const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM;
+    _Float16 *frag, *Sh;
+    float* esc;
+    int rc = gemm_prep(d_a, m, k, flags, nullptr, s, nullptr, 0, frag, Sh, esc);
+    if (rc) return rc;
+    const int64_t ntiles = aeth_cdiv(w->n, 16), gm = mp / G2_BM, gn = aeth_cdiv(w->n, G2_BN);
+    // fewer tiles than CUs: split K over workgroups too (each wave keeps at least one super-block)
+    const int ksplit = (int)std::max<int64_t>(1, std::min<int64_t>(aeth_cdiv(aeth_num_cus(), gm * gn), nb / 8));
+    float* part = nullptr;
+    if (ksplit > 1) {
+        void* p = nullptr;
+        rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)ksplit * mp * gn * G2_BN * sizeof(float), &p);
+        if (rc) return rc;
+        part = (float*)p;
+    }
+    Q6Args Q{(const uint8_t*)frag, esc, w->p0, w->p1, w->p2, (int)m, (int)w->n, k, nb, (int)ntiles, (int)mp,
+             (int)gm, (int)gn, (int)(mp * k * 4), (int)(ntiles * nb * 3072), (int)(ntiles * nb * 256),
+             (int)(ntiles * nb * 32), d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, 0,
+             ksplit, part, (int)(gn * G2_BN)};
+    return aeth_gemm_q6k_kq_launch(Q, s);
 }

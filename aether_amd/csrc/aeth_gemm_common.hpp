@@ -159,3 +159,27 @@ struct KqArgs {
     int swiglu;            // C[row][col/2] = g·σ(g)·u over the (g, u) column pairs
 };
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s);
+
+// Arguments of the Q6_K GEMM kernel (aeth_gemm_q6k.hip): A as for KqArgs, the Q6_K weight
+// planes (aeth_weights.hip).
+struct Q6Args {
+    const uint8_t* frag;   // A·2^-e as fp16 MFMA fragments (k_gemm_prep)
+    const float* escale;   // [mp]: 2^e
+    const uint8_t* q;      // [tile][b][part 3][lane][16 B]
+    const uint8_t* sc;     // [tile][b][16 rows][16 B]
+    const uint8_t* dd;     // [tile][b][16 rows] (f16)
+    int m, n, k, nb, ntiles, mp;
+    int gm, gn;            // 64-row and 128-column tiles of C
+    int a_bytes, q_bytes, s_bytes, d_bytes;  // buffer extents (each < 2^31)
+    float* C;
+    int64_t ldc;
+    int accumulate;
+    int swiglu;
+    // K split over workgroups: ksplit > 1 runs ksplit workgroups per tile, each over its share
+    // of the super-blocks, writing its tile's sum to part[split][row][col] (rows mp, pld = 128·gn
+    // columns); a second kernel adds the splits in order and applies the epilogue
+    int ksplit;
+    float* part;
+    int pld;
+};
+int aeth_gemm_q6k_kq_launch(const Q6Args& G, hipStream_t s);

@@ -77,7 +77,8 @@ namespace {
 // (4096 × 4096: 0.15 ms, 4096 × 14336: 0.73 ms), the GEMV grows with m (≈ 2 µs per row
 // at 4096 × 4096). Measured crossovers (HIP events, rotated weight copies): Q6_K 4096 ×
 // 4096 ≈ 64 rows, 4096 × 14336 ≈ 80, 1024 × 4096 ≈ 136; Q8_0 ≈ 112; Q5_K ≈ 80; Q2_K ≈ 40
-// and Q3_K ≈ 32 (GGUF order).
+// and Q3_K ≈ 32 (GGUF order). Q6_K rows of whole super-blocks take the Q6_K GEMM
+// (aeth_gemm_q6k.hip) instead, from the row count aeth_q6k_gemm_rows gives.
 int64_t dequant_gemm_rows(int dtype) {
     switch (dtype) {
         case AETH_DTYPE_Q8_0: return 112;
@@ -97,6 +98,7 @@ int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_
         return aeth_dequant_gemm_launch(w, d_a, m, d_c, ldc, flags, s);
     if (m > 1 && w->dtype == AETH_DTYPE_Q4_K && w->order == AETH_ORDER_PLANAR && aeth_q4k_gemm_rows(w, m))
         return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
+    if (m > 1 && aeth_q6k_gemm_rows(w, m)) return aeth_gemm_q6k_launch(w, d_a, m, d_c, flags, s, ldc);  // Q6_K
     // the other block formats from a few hundred rows on: dequantized once, one DGEMM (instead
     // of the weight streamed once per row by the batched GEMV). Their dequantized
     // weights are finite (K-quant scales go through decode_d), so the SGEMM's

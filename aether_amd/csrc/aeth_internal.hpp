@@ -145,6 +145,13 @@ bool aeth_gemm_swiglu_out(const aeth_weight* w, int64_t m);
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s, int64_t ldc = 0, void* ws = nullptr, size_t ws_bytes = 0,
                          const GemmIn* in = nullptr);
+// Whether m activation rows against Q6_K weight w take the Q6_K GEMM (aeth_gemm_q6k.hip):
+// planar whole super-blocks within the kernel's 32-bit buffer offsets, from 16 rows.
+bool aeth_q6k_gemm_rows(const aeth_weight* w, int64_t m);
+// Q6_K prefill GEMM (the exact mode of the Q4_K GEMM; AETH_MM_ACCUMULATE and the Q8
+// activation blocks as aeth_gemm_q4k_launch); requires aeth_q6k_gemm_rows.
+int aeth_gemm_q6k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
+                         hipStream_t s, int64_t ldc = 0);
 // aeth_qmatmul with an output row stride (rows of c are ldc floats apart).
 int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
                     hipStream_t s);
@@ -160,6 +167,7 @@ enum {
     AETH_SCRATCH_ARGMAX = 3,
     AETH_SCRATCH_DEQ = 4,   // dequantized f32 weight of a batched product (aeth_blas.cpp)
     AETH_SCRATCH_QACT = 5,  // Q8_0 activation blocks and their f32 values (same)
+    AETH_SCRATCH_SPLIT = 6, // partial output tiles of a GEMM split over K across workgroups (aeth_gemm.hip)
 };
 int aeth_stream_scratch(hipStream_t s, int use, size_t bytes, void** out);
 // Frees every scratch buffer of stream s (before the stream is destroyed).

@@ -12,8 +12,8 @@ import pytest
 
 import aether_amd as A
 from oracle import oracle as O
-from tests._util import (F16, F32, GEOM, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, assert_close, assert_close_rows,
-                         synth_blocks, weight)
+from tests._util import (F16, F32, GEOM, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, assert_close, assert_close_logits,
+                         assert_close_rows, synth_blocks, weight)
 
 pytestmark = pytest.mark.gpu
 DTYPES = [Q8_0, Q4_K, Q5_K, Q6_K]           # the formats with a fused kernel (row-major [n][k] blocks)
@@ -152,8 +152,8 @@ def test_matmul_nonfinite_activation_gives_nan_rows(gpu, dtype):
 def test_matmul_reference_generators(gpu, dtype):
     """The reference's own test inputs (src/quant/matmul/tests.rs:3-17,
     :386-508): a[i] = ((i*17)%100)/50 - 1, b[i] = (i*31)%256 — f16 scales hit
-    NaN/Inf patterns, so outputs reach ~1e7."""
-    for m in (1, 3):
+    NaN/Inf patterns, so outputs reach ~1e7. m = 20 takes the Q4_K and Q6_K GEMMs."""
+    for m in (1, 3, 20):
         k, n = 256, 8
         bb = GEOM[dtype][1]
         b = ((np.arange(n * (k // 256) * bb) * 31) % 256).astype(np.uint8)
@@ -354,6 +354,90 @@ def test_q4k_small_batches(gpu, m, n):
     assert_close(got_acc, ref + y0, what="q4_k accumulate m=%d n=%d" % (m, n))
     ref_q8 = O.dotprod_ref(Q4_K, O.quantize_activations_q8_0(x.ravel(), m, k), raw, m, n, k).reshape(m, n)
     assert_close(got_q8, ref_q8, what="q4_k dot-product mode m=%d n=%d" % (m, n))
+
+
+def check_q6k_gemm(torch, m, n, k):
+    """Q6_K product of m rows against the oracle: per-row exponents (2^20, 2^-12, a zero
+    row, a block of 2^15 rows past fp16 range when m > 40), plain, accumulate and the
+    dot-product mode; the weights carry the scale extremes -128 and 127 (16·hi + lo with
+    hi = -8 and 7) and super-blocks whose d is zero.
+
+    With those scales and k up to 20480 a row's outputs reach several thousand, and the
+    reference's own f32 sums then sit up to 7e-3 from the float64 product of the same
+    operands (k = 16384: median 2.8e-4, max 6.9e-3), past the element-wise bar on small
+    entries. Rows of magnitude 1 are therefore also anchored on that float64 product: an
+    element passes the element-wise bar against the reference, or sits within twice the
+    reference's largest distance from the float64 product on its row (assert_close_logits
+    with exact, no floor)."""
+    rng = np.random.default_rng(m * 37 + n * 11 + k)
+    raw = weight(Q6_K, n, k, 9 * n + k).reshape(-1, 210)
+    nblk = raw.shape[0]
+    pick = rng.integers(0, nblk, max(2, nblk // 16))
+    raw[pick[0::2], 192:208] = np.int8(-128).view(np.uint8)
+    raw[pick[1::2], 192:208] = np.int8(127).view(np.uint8)
+    raw[rng.integers(0, nblk, max(1, nblk // 20)), 208:210] = 0
+    raw = raw.reshape(-1)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    scale = np.ones(m, dtype=np.float32)
+    scale[m // 3] = 2.0 ** 20
+    scale[m // 2] = 2.0 ** -12
+    scale[(2 * m) // 3] = 0.0
+    if m > 40:
+        scale[33:40] = 2.0 ** 15
+    x *= scale[:, None]
+    w = make_weight(torch, Q6_K, n, k, raw)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    got = gemv(torch, w, x.ravel(), n, m)
+    got_acc = gemv(torch, w, x.ravel(), n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    got_q8 = gemv(torch, w, x.ravel(), n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q6_K, x.ravel(), raw, m, n, k).reshape(m, n)
+    plain = scale == 1.0
+    w64 = O.dequant(Q6_K, raw, n * k).reshape(n, k).astype(np.float64)
+    ex = x[plain].astype(np.float64) @ w64.T
+    what = "q6_k m=%d n=%d k=%d" % (m, n, k)
+    assert_close_logits(got[plain], ref[plain], floor=0.0, exact=ex, what=what)
+    assert_close_rows(got, ref, what=what + " (scaled rows)")
+    assert_close_logits(got_acc[plain], (ref + y0)[plain], floor=0.0, exact=ex + y0[plain], what=what + " accumulate")
+    assert np.all(got[(2 * m) // 3] == 0.0)
+    aq = O.quantize_activations_q8_0(x.ravel(), m, k)
+    ref_q8 = O.dotprod_ref(Q6_K, aq, raw, m, n, k).reshape(m, n)
+    ex_q8 = O.dequant(Q8_0, aq, m * k).reshape(m, k)[plain].astype(np.float64) @ w64.T
+    assert_close_rows(got_q8, ref_q8, what=what + " dot-product mode")
+    assert_close_logits(got_q8[plain], ref_q8[plain], floor=0.0, exact=ex_q8, what=what + " dot-product mode")
+
+
+# The Q6_K GEMM (planar Q6_K, whole super-blocks, m · weight bytes >= 200 MB): super-block
+# counts that split unevenly over its 8 waves (2, 3, 4, 8, 10, 16, 24, 32, 56, 64, 80), K
+# also split over 2, 3, 4, 7, 8 and 10 workgroups per tile where the tiles are fewer than
+# the CUs, m and n off the 64 × 128 tile grid.
+@pytest.mark.parametrize("m,n,k", [(70, 4600, 768), (16, 30000, 512), (65, 3700, 1024), (130, 1900, 2560),
+                                   (45, 2200, 16384), (37, 1100, 8192), (200, 100, 14336), (34, 400, 20480),
+                                   (17, 7100, 2048), (30, 2000, 4096), (25, 1700, 6144)])
+def test_gemm_q6k_tiles_exponents_accumulate(gpu, m, n, k):
+    check_q6k_gemm(gpu, m, n, k)
+
+
+# Small batches of Q6_K rows: the row-batched GEMV until m · (weight bytes) reaches 200 MB,
+# then the GEMM (aeth_q6k_gemm_rows); both sides of the boundary at three weight sizes, plain,
+# accumulate and the dot-product mode.
+@pytest.mark.parametrize("m,n,k", [(4, 4096, 14336), (5, 4096, 14336), (14, 4096, 4096), (15, 4096, 4096),
+                                   (58, 1024, 4096), (59, 1024, 4096)])
+def test_q6k_small_batches(gpu, m, n, k):
+    rng = np.random.default_rng(m * 103 + n + k)
+    raw = weight(Q6_K, n, k, 3 * n + m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = make_weight(gpu, Q6_K, n, k, raw)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    got = gemv(gpu, w, x.ravel(), n, m)
+    got_acc = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    got_q8 = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q6_K, x.ravel(), raw, m, n, k).reshape(m, n)
+    assert_close(got, ref, what="q6_k m=%d n=%d k=%d" % (m, n, k))
+    assert_close(got_acc, ref + y0, what="q6_k accumulate m=%d n=%d k=%d" % (m, n, k))
+    ref_q8 = O.dotprod_ref(Q6_K, O.quantize_activations_q8_0(x.ravel(), m, k), raw, m, n, k).reshape(m, n)
+    assert_close(got_q8, ref_q8, what="q6_k dot-product mode m=%d n=%d k=%d" % (m, n, k))
 
 
 @pytest.mark.parametrize("n", [4096, 14336])
@@ -663,15 +747,52 @@ def test_gemm_alternate_kernels(gpu, var, val):
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:]
 
 
-# Batched products of the block formats without a GEMM kernel of their own:
+Q6K_GEMM_SCRIPT = r"""
+import sys, torch
+sys.path.insert(0, %r)
+import aether_amd as A
+A.check(A.lib().aeth_init(0))
+from tests.test_gpu_quant import check_q6k_gemm
+for m, n, k in ((70, 130, 768), (16, 16, 512), (3, 48, 1024), (65, 300, 1024), (33, 96, 14336), (200, 64, 14336),
+                (34, 64, 20480)):
+    check_q6k_gemm(torch, m, n, k)
+from tests.test_gpu_decode import test_runner_mixed_formats
+for mix in (0, 1):
+    for n in (23, 150):
+        test_runner_mixed_formats(torch, mix, n)
+print("ok")
+"""
+
+
+def test_q6k_gemm_small_weights(gpu):
+    """The Q6_K GEMM on weights too small for the default to pick it (AETH_Q6K_GEMM_ROWS=2,
+    read once per process, so in a fresh process): ragged tiles from 3 rows, K split over up
+    to 10 workgroups, and runner prefills of mixed-format layers, where the Q6_K v projection
+    writes its columns of q|k|v with the output row stride and the Q6_K down projection adds
+    the residual."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, AETH_Q6K_GEMM_ROWS="2")
+    r = subprocess.run([sys.executable, "-c", Q6K_GEMM_SCRIPT % root], env=env, cwd=root, timeout=240,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:]
+
+
+# Batched products of the block formats without a GEMM kernel of their own (and
+# Q6_K rows the Q6_K GEMM does not take: k not a whole number of super-blocks):
 # below a per-format row count (Q8_0 112, Q5_K and Q6_K 80) the row-batched
 # GEMV, from it the weight dequantized once and one DGEMM — planar Q8_0 / Q5_K /
 # Q6_K rows (including Q8_0's ragged k and K-quant rows whose tail past k/256
 # blocks the reference ignores), accumulate, and the dot-product mode's Q8_0
-# activation blocks, on both paths.
+# activation blocks, on both paths. Q6_K with whole super-blocks takes the Q6_K GEMM
+# once m · weight bytes reaches 200 MB (the 150-row case here), else the GEMV.
 @pytest.mark.parametrize("dtype,m,n,k", [(Q8_0, 16, 300, 1000), (Q8_0, 400, 128, 1000), (Q8_0, 150, 512, 4096),
                                          (Q5_K, 70, 256, 2048), (Q5_K, 300, 64, 2048), (Q6_K, 150, 1024, 4096),
-                                         (Q6_K, 260, 96, 4096), (Q6_K, 33, 96, 14336), (Q5_K, 20, 64, 600)])
+                                         (Q6_K, 260, 96, 4096), (Q6_K, 33, 96, 14336), (Q5_K, 20, 64, 600),
+                                         (Q6_K, 100, 200, 1100), (Q6_K, 40, 64, 1300)])
 def test_batched_dequant_gemm(gpu, dtype, m, n, k):
     rng = np.random.default_rng(m + n + k + dtype)
     raw = weight(dtype, n, k, 5 * n + k)
