@@ -254,10 +254,8 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
             // this slice's operands: B1 = lo·(q − 32), B2 = 16·hi·(q − 32) for sub-block s, k-order
             // [0, 2, 1, 3] per 4 (the pairs of bytes (0, 2) and (1, 3) of each dword, as the prep
             // orders A); 0x64 | q is the half 1024 + q
-            half8_t b1[4], b2[4];
             const half2_t k1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
+            auto build = [&](int c, half8_t& b1, half8_t& b2) {
                 const int sc = (int)(int8_t)((scr[c][s >> 2] >> (8 * (s & 3))) & 0xFFu);
                 const int lo = sc & 15;
                 const _Float16 flo = (_Float16)(float)lo, fhi = (_Float16)(float)(sc - lo);
@@ -279,12 +277,17 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const half2_t y1 = x[i] * slo, y2 = x[i] * shi;
-                    b1[c][2 * i] = y1[0];
-                    b1[c][2 * i + 1] = y1[1];
-                    b2[c][2 * i] = y2[0];
-                    b2[c][2 * i + 1] = y2[1];
+                    b1[2 * i] = y1[0];
+                    b1[2 * i + 1] = y1[1];
+                    b2[2 * i] = y2[0];
+                    b2[2 * i + 1] = y2[1];
                 }
-            }
+            };
+            // Column groups in turn: group c's eight MFMAs are issued between the VALU
+            // instructions that build group c + 1's operands, so the dequantisation runs in the
+            // shadow of the matrix core (the scheduling groups fix that interleave)
+            half8_t b1[4], b2[4];
+            build(0, b1[0], b2[0]);
             lgkm_wait<0>();
 #pragma unroll
             for (int mt = 0; mt < 2; mt++) {
@@ -292,15 +295,23 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
                 pin(a[mt][1]);
             }
 #pragma unroll
-            for (int pa = 0; pa < 2; pa++)
+            for (int c = 0; c < 4; c++) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (c < 3) build(c + 1, b1[c + 1], b2[c + 1]);
 #pragma unroll
-                for (int h2 = 0; h2 < 2; h2++)
+                for (int pa = 0; pa < 2; pa++)
 #pragma unroll
-                    for (int mt = 0; mt < 2; mt++)
+                    for (int h2 = 0; h2 < 2; h2++)
 #pragma unroll
-                        for (int c = 0; c < 4; c++)
+                        for (int mt = 0; mt < 2; mt++)
                             U[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt][pa], h2 ? b2[c] : b1[c], U[mt][c],
                                                                               0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+                }
+            }
         }
         s3 = s3 == 2 ? 0 : s3 + 1;
     }
