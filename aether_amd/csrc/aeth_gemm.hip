@@ -624,15 +624,29 @@ bool aeth_q6k_gemm_rows(const aeth_weight* w, int64_t m) {
     return m * w->nb * w->n * 210 >= 200000000LL;
 }
 
+bool aeth_q6k_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {
+    if (m <= 1 || !aeth_q6k_gemm_rows(w, m)) return false;
+    if (mode == PREP_PLAIN) return true;
+    if (w->k > 16384 || ((uintptr_t)d_a & 15)) return false;  // one chunk of registers per wave, float4 loads
+    if (mode == PREP_RMSNORM) return norm_w && ((uintptr_t)norm_w & 15) == 0;
+    return mode == PREP_SWIGLU;
+}
+
 int aeth_gemm_q6k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s, int64_t ldc) {
+                         hipStream_t s, int64_t ldc, const GemmIn* in) {
     if (!aeth_q6k_gemm_rows(w, m)) return aeth_set_error(AETH_EINVAL, "gemm q6_k: shape not taken (m=%lld)", (long long)m);
+    const int mode = in ? in->mode : PREP_PLAIN;
+    if (in && in->swiglu_out) return aeth_set_error(AETH_EINVAL, "gemm q6_k: no SwiGLU output");
+    if (mode != PREP_PLAIN && !aeth_q6k_gemm_fuses(w, m, mode, d_a, in->norm_w))
+        return aeth_set_error(AETH_EINVAL, "gemm q6_k: fused producer %d not available", mode);
+    if (mode != PREP_PLAIN && (flags & AETH_MM_Q8_ACTIVATIONS))  // the producers feed the exact (f32) mode only
+        return aeth_set_error(AETH_EINVAL, "gemm q6_k: fused producer %d with Q8 activations", mode);
     const int k = (int)w->k, nb = (int)w->nb;
     if (ldc <= 0) ldc = w->n;
     const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM;
     _Float16 *frag, *Sh;
     float* esc;
-    int rc = gemm_prep(d_a, m, k, flags, nullptr, s, nullptr, 0, frag, Sh, esc);
+    int rc = gemm_prep(d_a, m, k, flags, in, s, nullptr, 0, frag, Sh, esc);
     if (rc) return rc;
     const int64_t ntiles = aeth_cdiv(w->n, 16), gm = mp / G2_BM, gn = aeth_cdiv(w->n, G2_BN);
     // fewer tiles than CUs: split K over workgroups too (each wave keeps at least one super-block)

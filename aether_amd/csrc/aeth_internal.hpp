@@ -146,12 +146,16 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
                          hipStream_t s, int64_t ldc = 0, void* ws = nullptr, size_t ws_bytes = 0,
                          const GemmIn* in = nullptr);
 // Whether m activation rows against Q6_K weight w take the Q6_K GEMM (aeth_gemm_q6k.hip):
-// planar whole super-blocks within the kernel's 32-bit buffer offsets, from 16 rows.
+// planar whole super-blocks within the kernel's 32-bit buffer offsets, once m · (weight
+// bytes) reaches 200 MB (the row-batched GEMV below).
 bool aeth_q6k_gemm_rows(const aeth_weight* w, int64_t m);
+// aeth_gemm_fuses for the Q6_K GEMM (its prep is the Q4_K GEMM's).
+bool aeth_q6k_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w);
 // Q6_K prefill GEMM (the exact mode of the Q4_K GEMM; AETH_MM_ACCUMULATE and the Q8
-// activation blocks as aeth_gemm_q4k_launch); requires aeth_q6k_gemm_rows.
+// activation blocks as aeth_gemm_q4k_launch); requires aeth_q6k_gemm_rows, and a producer
+// in `in` aeth_q6k_gemm_fuses (no SwiGLU output).
 int aeth_gemm_q6k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s, int64_t ldc = 0);
+                         hipStream_t s, int64_t ldc = 0, const GemmIn* in = nullptr);
 // aeth_qmatmul with an output row stride (rows of c are ldc floats apart).
 int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, int64_t ldc, unsigned flags,
                     hipStream_t s);

@@ -29,6 +29,9 @@ struct aeth_runner {
     std::vector<aeth_weight*> wqkv, wo, wgu, wdown;
     // per layer, set when q/k/v (gate/up) do not share a dtype: the fused weight is then NULL
     std::vector<aeth_weight*> wq, wk, wv, wg, wu;
+    // per layer, set when q and k share a fused dtype and v does not (llama.cpp's Q4_K_M keeps
+    // attn_v in Q6_K): q|k rows concatenated, v in wv, wq / wk NULL
+    std::vector<aeth_weight*> wqk;
     std::vector<int> dtypes;                         // per layer x 7
     aeth_weight* lm_head = nullptr;
     float* norms = nullptr;       // [L][2][d]
@@ -157,7 +160,7 @@ void runner_release(aeth_runner* r) {
     for (auto* w : r->wqkv) aeth_weight_free(w);
     for (auto* w : r->wo) aeth_weight_free(w);
     for (auto* w : r->wgu) aeth_weight_free(w);
-    for (auto* v : {&r->wq, &r->wk, &r->wv, &r->wg, &r->wu})
+    for (auto* v : {&r->wq, &r->wk, &r->wv, &r->wg, &r->wu, &r->wqk})
         for (auto* w : *v) aeth_weight_free(w);
     for (auto* w : r->wdown) aeth_weight_free(w);
     aeth_weight_free(r->lm_head);
@@ -201,6 +204,10 @@ int enqueue_layers(aeth_runner* r, int l0, int l1) {
         e1.eps = c.rms_norm_eps;
         if (r->wqkv[l]) {
             if ((rc = aeth_gemv_launch_ex(r->wqkv[l], r->x, 1, r->qkv, e1, s))) return rc;
+        } else if (r->wqk[l]) {  // q|k, then v of another format
+            if ((rc = aeth_gemv_launch_ex(r->wqk[l], r->x, 1, r->qkv, e1, s)) ||
+                (rc = aeth_gemv_launch_ex(r->wv[l], r->x, 1, r->qkv + (nh + nkv) * hd, e1, s)))
+                return rc;
         } else {  // q, k, v of different formats: three GEMVs into the q|k|v vector
             const int64_t qd = nh * hd, kvd = nkv * hd;
             if ((rc = aeth_gemv_launch_ex(r->wq[l], r->x, 1, r->qkv, e1, s)) ||
@@ -309,18 +316,30 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
         nin.mode = PREP_RMSNORM;
         nin.eps = c.rms_norm_eps;
         nin.norm_w = attn_norm;
-        if (r->wqkv[l] && aeth_gemm_fuses(r->wqkv[l], n, PREP_RMSNORM, r->p_x, attn_norm)) {
-            if ((rc = aeth_gemm_q4k_launch(r->wqkv[l], r->p_x, n, r->p_qkv, 0, s, 0, nullptr, 0, &nin))) return rc;
-        } else {
-            if ((rc = aeth_rmsnorm_launch(r->p_x, attn_norm, n, d, c.rms_norm_eps, r->p_n, s))) return rc;
+        {
+            // each projection into its columns of the [n][q|k|v] rows: a Q4_K or Q6_K GEMM that
+            // takes the RMSNorm in its prep reads x; any other reads rmsnorm(x), formed once
+            const int64_t qd = nh * hd, kvd = nkv * hd, ld = qd + 2 * kvd;
+            bool normed = false;
+            auto proj = [&](const aeth_weight* w, float* out) -> int {
+                if (aeth_gemm_fuses(w, n, PREP_RMSNORM, r->p_x, attn_norm))
+                    return aeth_gemm_q4k_launch(w, r->p_x, n, out, 0, s, ld, nullptr, 0, &nin);
+                if (w->dtype == AETH_DTYPE_Q6_K && aeth_q6k_gemm_fuses(w, n, PREP_RMSNORM, r->p_x, attn_norm))
+                    return aeth_gemm_q6k_launch(w, r->p_x, n, out, 0, s, ld, &nin);
+                if (!normed) {
+                    int e = aeth_rmsnorm_launch(r->p_x, attn_norm, n, d, c.rms_norm_eps, r->p_n, s);
+                    if (e) return e;
+                    normed = true;
+                }
+                return aeth_qmatmul_ld(w, r->p_n, n, out, ld, 0, s);
+            };
             if (r->wqkv[l]) {
-                if ((rc = aeth_qmatmul(r->wqkv[l], r->p_n, n, r->p_qkv, 0, s))) return rc;
-            } else {  // separate q, k, v into the columns of the [n][q|k|v] rows
-                const int64_t qd = nh * hd, kvd = nkv * hd, ld = qd + 2 * kvd;
-                if ((rc = aeth_qmatmul_ld(r->wq[l], r->p_n, n, r->p_qkv, ld, 0, s)) ||
-                    (rc = aeth_qmatmul_ld(r->wk[l], r->p_n, n, r->p_qkv + qd, ld, 0, s)) ||
-                    (rc = aeth_qmatmul_ld(r->wv[l], r->p_n, n, r->p_qkv + qd + kvd, ld, 0, s)))
-                    return rc;
+                if ((rc = proj(r->wqkv[l], r->p_qkv))) return rc;
+            } else if (r->wqk[l]) {
+                if ((rc = proj(r->wqk[l], r->p_qkv)) || (rc = proj(r->wv[l], r->p_qkv + qd + kvd))) return rc;
+            } else if ((rc = proj(r->wq[l], r->p_qkv)) || (rc = proj(r->wk[l], r->p_qkv + qd)) ||
+                       (rc = proj(r->wv[l], r->p_qkv + qd + kvd))) {
+                return rc;
             }
         }
         if ((rc = aeth_prefill_rope_kv_launch(r->p_qkv, n, nh, nkv, hd, r->rope_sin, r->rope_cos, c.max_seq_len,
@@ -449,9 +468,12 @@ int runner_create_impl(const aeth_llama_config* cfg, const void* const* layer_we
         // q|k|v rows fused into one weight, gate/up rows interleaved (SwiGLU epilogue),
         // when they share a fused format; separate weights otherwise (mixed-format
         // files; GGUF-order F32 / F16 / Q2_K / Q3_K weights, whose rows are not [out] rows)
-        for (auto* v : {&r->wqkv, &r->wq, &r->wk, &r->wv, &r->wgu, &r->wg, &r->wu}) v->push_back(nullptr);
+        for (auto* v : {&r->wqkv, &r->wq, &r->wk, &r->wv, &r->wgu, &r->wg, &r->wu, &r->wqk}) v->push_back(nullptr);
         if (T[0] == T[1] && T[0] == T[2] && aeth_dtype_fused(T[0])) {
             RC(make_concat(T[0], {qd, kvd, kvd}, d, {hw(0), hw(1), hw(2)}, mix(seed, l, 1), s, &r->wqkv[l]));
+        } else if (T[0] == T[1] && aeth_dtype_fused(T[0])) {
+            RC(make_concat(T[0], {qd, kvd}, d, {hw(0), hw(1)}, mix(seed, l, 1), s, &r->wqk[l]));
+            RC(make_weight(T[2], kvd, d, hw(2), mix(seed, l, 3), s, &r->wv[l]));
         } else {
             RC(make_weight(T[0], qd, d, hw(0), mix(seed, l, 1), s, &r->wq[l]));
             RC(make_weight(T[1], kvd, d, hw(1), mix(seed, l, 2), s, &r->wk[l]));
@@ -693,7 +715,8 @@ static int runner_export_impl(const aeth_runner* r, int which, int32_t l, void* 
             if (host_bytes < sep[which]->bytes) return aeth_set_error(AETH_EINVAL, "export: buffer too small");
             return aeth_weight_export_raw(sep[which], host, 0, r->stream);
         }
-        const aeth_weight* w = which <= 2 ? r->wqkv[l] : which == 3 ? r->wo[l] : which <= 5 ? r->wgu[l] : r->wdown[l];
+        const aeth_weight* w = which <= 2 ? (r->wqkv[l] ? r->wqkv[l] : r->wqk[l])
+                               : which == 3 ? r->wo[l] : which <= 5 ? r->wgu[l] : r->wdown[l];
         std::vector<uint8_t> all((size_t)w->bytes);
         int rc = aeth_weight_export_raw(w, all.data(), 0, r->stream);
         if (rc) return rc;

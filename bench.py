@@ -10,7 +10,8 @@ value = algorithmic bytes per launch / mean launch time over K timed launches
 The same JSON line carries the other configs as `extra`: Q8_0 and Q6_K GEMV
 (configs 0, 2), the Q4_K prefill GEMM at M=512 (config 3) and the LLaMA-8B
 shape greedy decode (config 4), the Q5_K GEMV and the headline shape on the
-int8 dot-product path (and, on request, GGUF-order F16 / Q2_K GEMVs), plus
+int8 dot-product path, the Q6_K GEMM at M=512 and the 8B shape with the
+Q4_K_M format mix (and, on request, GGUF-order F16 / Q2_K GEMVs), plus
 `roofline` for the headline kernel and
 `cpu_baseline`: the oracle's restatement of the reference's AVX2 path on one
 host core over a bounded sample of the same workload (and, in `extra`, the
@@ -206,6 +207,42 @@ def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512, wan
             "gbs": step_bytes * n_tokens / dt_s / 1e9, "step_bytes": step_bytes, "first_tokens": list(toks)[:8],
             "prefill_tok_s": prefill_tokens / pf_s, "prefill_ms": pf_s * 1e3, "prefill_tflops": pf_flops / pf_s / 1e12,
             "cpu_model": cpu_model}
+
+
+def bench_q4_k_m(torch, A, n_tokens=64, prefilled=2048, prefill_tokens=512):
+    """bench_decode's model with llama.cpp's Q4_K_M mix: attn_v and ffn_down in Q6_K, the
+    other five layer weights Q4_K. Those layers run q / k / v and gate / up as separate
+    products (no fused q|k|v or gate|up weight), and in prefill the Q6_K projections take
+    the Q6_K GEMM."""
+    L = A.lib()
+    cfg = A.LlamaConfig(vocab_size=128256, d_model=4096, num_layers=32, num_heads=32, num_kv_heads=8, head_dim=128,
+                        d_ff=14336, max_seq_len=4096, rope_base=500000.0, rms_norm_eps=1e-5)
+    dt = (ctypes.c_int32 * (32 * 7))(*([12, 12, 14, 12, 12, 12, 14] * 32))
+    r = ctypes.c_void_p()
+    A.check(L.aeth_runner_create(ctypes.byref(cfg), None, dt, None, None, None, 14, None, 0x8B8B8B,
+                                 ctypes.byref(r)), "runner_create")
+    toks = (ctypes.c_int32 * n_tokens)()
+    A.check(L.aeth_runner_fill_kv(r, 0x4B56, prefilled), "fill_kv")
+    A.check(L.aeth_runner_generate(r, 1, prefilled, 2, toks, 1), "warmup generate")
+    A.check(L.aeth_runner_fill_kv(r, 0x4B56, prefilled), "fill_kv")
+    t0 = time.perf_counter()
+    A.check(L.aeth_runner_generate(r, 1, prefilled, n_tokens, toks, 1), "generate")
+    dt_s = time.perf_counter() - t0
+    prompt = (ctypes.c_int32 * prefill_tokens)(*[(7919 * i + 13) % 128256 for i in range(prefill_tokens)])
+    A.check(L.aeth_runner_prefill(r, prompt, prefill_tokens, None, None), "prefill warmup")
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        A.check(L.aeth_runner_prefill(r, prompt, prefill_tokens, None, None), "prefill")
+    pf_s = (time.perf_counter() - t0) / reps
+    L.aeth_runner_free(r)
+    layer_weights = 4096 * 4096 * 2 + 1024 * 4096 * 2 + 14336 * 4096 * 3
+    pf_flops = 2.0 * prefill_tokens * 32 * layer_weights + 2.0 * 128256 * 4096
+    return {"decode_tok_s": round(n_tokens / dt_s, 1), "ms_per_token": round(dt_s * 1e3 / n_tokens, 4),
+            "prefill_tok_s": round(prefill_tokens / pf_s, 1), "prefill_ms": round(pf_s * 1e3, 3),
+            "prefill_TFLOP/s": round(pf_flops / pf_s / 1e12, 1), "prefill_tokens": prefill_tokens,
+            "decode_tokens": n_tokens, "prefilled": prefilled,
+            "mix": "Q4_K_M: attn_v, ffn_down Q6_K; q, k, o, gate, up Q4_K; LM head Q6_K"}
 
 
 def bench_decode_eager(torch, A, n_tokens=128, prefilled=2048):
@@ -419,9 +456,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,decode",
+    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,decode,q4_k_m",
                     help="comma-separated extra sections to run: floor, q8, q6, q5, dotprod, gemm, gemm_q8, gemm_q6k, "
-                         "decode (default), f16, q2k (GGUF-order formats), decode_eager (the decode step "
+                         "decode, q4_k_m (default), f16, q2k (GGUF-order formats), decode_eager (the decode step "
                          "without its HIP graph; these three not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -540,11 +577,18 @@ def main():
             print("[bench] Q4_K GEMM q8 n=%d: %s" % (nn, extra["q4_k_gemm_m512_n%d_q8act" % nn]), file=sys.stderr,
                   flush=True)
             del g
-    if "gemm_q6k" in sections:  # batched Q6_K (dequantized once, one SGEMM): a Q4_K_M file's attn_v / ffn_down
-        r = bench_batched(torch, A, 14, 4096, 4096, 512, max(3, min(args.steps, 20)), 2)
-        extra["q6_k_batched_m512_n4096"] = {"TFLOP/s": round(r["tflops"], 2), "ms": round(r["ms"], 4),
-                                             "path": "dequantized once, widened to f64, rocBLAS DGEMM split over K"}
-        print("[bench] Q6_K batched m=512: %s" % extra["q6_k_batched_m512_n4096"], file=sys.stderr, flush=True)
+    if "gemm_q6k" in sections:  # the Q6_K GEMM at a Q4_K_M file's attn_v / ffn_down shapes (and 4096 × 4096)
+        for nn, kk in ((4096, 4096), (4096, 14336), (1024, 4096)):
+            r = bench_batched(torch, A, 14, nn, kk, 512, max(3, min(args.steps, 20)), 2)
+            key = "q6_k_gemm_m512_n%d_k%d" % (nn, kk)
+            extra[key] = {"TFLOP/s": round(r["tflops"], 2), "ms": round(r["ms"], 4),
+                          "path": "Q6_K GEMM: exact mode, four fp16 MFMA passes per product"}
+            if mfma:  # four passes: the ceiling is a quarter of the fp16 rate
+                extra[key]["frac_exact_mode_ceiling"] = round(r["tflops"] / (mfma["fp16_TFLOP/s"] / 4), 4)
+            print("[bench] Q6_K GEMM m=512 n=%d k=%d: %s" % (nn, kk, extra[key]), file=sys.stderr, flush=True)
+    if "q4_k_m" in sections:
+        extra["q4_k_m_decode_prefill_8b"] = bench_q4_k_m(torch, A)
+        print("[bench] Q4_K_M 8B: %s" % extra["q4_k_m_decode_prefill_8b"], file=sys.stderr, flush=True)
     if "decode" in sections:
         d = bench_decode(torch, A, want_cpu=want_cpu)
         cpu_in["dec"] = d.pop("cpu_model")
