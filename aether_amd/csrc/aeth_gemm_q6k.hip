@@ -1,13 +1,15 @@
 // Q6_K prefill GEMM (m rows from aeth_q6k_gemm_rows on):  C[m][n] = Σ_k A[m][k]·W[n][k]
 // (avx2::matmul_q6_k with m rows, src/quant/avx2.rs:60-94; quantized_matmul_impl).
 //
-// Exact mode as the Q4_K GEMM: A·2^-e split into fp16 hi/lo MFMA fragments (k_gemm_prep in
-// aeth_gemm.hip), f32 accumulation on v_mfma_f32_32x32x16_f16. A Q6_K weight is
+// The exact mode of the Q4_K GEMM: A·2^-e split into fp16 hi/lo MFMA fragments (k_gemm_prep
+// in aeth_gemm.hip), f32 accumulation on v_mfma_f32_32x32x16_f16. A Q6_K weight is
 // w = d·sc_s·(q − 32): d (f16) per 256-element super-block, sc_s (int8) per 16-element
-// sub-block s, q ∈ [0, 63]. sc·(q − 32) needs 13 bits, more than an fp16 integer holds, so it
-// enters as two exact fp16 operands B1 = lo·(q − 32) and B2 = 16·hi·(q − 32), sc = 16·hi + lo
-// (lo ∈ [0, 15], hi ∈ [−8, 7]; |B1| ≤ 480, B2 a multiple of 16 of at most 4096): every
-// product A_part·B_part is exact, and four MFMA passes (A hi/lo × B1/B2) make one product.
+// sub-block s, q ∈ [0, 63]. sc·(q − 32) needs 13 bits, more than an fp16 integer holds, so
+// against A_hi it enters as two exact fp16 operands B1 = lo·(q − 32) and B2 = 16·hi·(q − 32),
+// sc = 16·hi + lo (lo ∈ [0, 15], hi ∈ [−8, 7]; |B1| ≤ 480, B2 a multiple of 16 of at most
+// 4096), and against A_lo (≤ 2^-11·|A|) as one operand Bs = fp16(sc·(q − 32)) (relative
+// rounding ≤ 2^-11): three MFMA passes per product, each product within 2^-22·|A·w| of exact
+// beyond the hi/lo split's own 2^-22.
 // d enters per super-block through the rescaled accumulator of aeth_gemm_kq.hip: entering
 // super-block b, U ← U·D_{b−1}/D_b (a zero d keeps the scale and zeroes the block's
 // operands); the result is D_last·U. There is no min term.
@@ -255,11 +257,11 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
             // [0, 2, 1, 3] per 4 (the pairs of bytes (0, 2) and (1, 3) of each dword, as the prep
             // orders A); 0x64 | q is the half 1024 + q
             const half2_t k1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-            auto build = [&](int c, half8_t& b1, half8_t& b2) {
+            auto build = [&](int c, half8_t& b1, half8_t& b2, half8_t& bs) {
                 const int sc = (int)(int8_t)((scr[c][s >> 2] >> (8 * (s & 3))) & 0xFFu);
                 const int lo = sc & 15;
-                const _Float16 flo = (_Float16)(float)lo, fhi = (_Float16)(float)(sc - lo);
-                const half2_t slo = {flo, flo}, shi = {fhi, fhi};
+                const _Float16 flo = (_Float16)(float)lo, fhi = (_Float16)(float)(sc - lo), fsc = (_Float16)(float)sc;
+                const half2_t slo = {flo, flo}, shi = {fhi, fhi}, ssc = {fsc, fsc};
                 const u32x2 P = (v & 1) ? rp1[c] : rp0[c];
                 uint32_t w[2];
 #pragma unroll
@@ -276,18 +278,20 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
                 x[3] = __builtin_bit_cast(half2_t, ((w[1] >> 8) & 0x00FF00FFu) | c64) + k1056;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const half2_t y1 = x[i] * slo, y2 = x[i] * shi;
+                    const half2_t y1 = x[i] * slo, y2 = x[i] * shi, y3 = x[i] * ssc;
                     b1[2 * i] = y1[0];
                     b1[2 * i + 1] = y1[1];
                     b2[2 * i] = y2[0];
                     b2[2 * i + 1] = y2[1];
+                    bs[2 * i] = y3[0];
+                    bs[2 * i + 1] = y3[1];
                 }
             };
             // Column groups in turn: group c's eight MFMAs are issued between the VALU
             // instructions that build group c + 1's operands, so the dequantisation runs in the
             // shadow of the matrix core (the scheduling groups fix that interleave)
-            half8_t b1[4], b2[4];
-            build(0, b1[0], b2[0]);
+            half8_t b1[4], b2[4], bs[4];
+            build(0, b1[0], b2[0], bs[0]);
             lgkm_wait<0>();
 #pragma unroll
             for (int mt = 0; mt < 2; mt++) {
@@ -297,19 +301,17 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 __builtin_amdgcn_sched_barrier(0);
-                if (c < 3) build(c + 1, b1[c + 1], b2[c + 1]);
+                if (c < 3) build(c + 1, b1[c + 1], b2[c + 1], bs[c + 1]);
 #pragma unroll
-                for (int pa = 0; pa < 2; pa++)
+                for (int h = 0; h < 3; h++)
 #pragma unroll
-                    for (int h2 = 0; h2 < 2; h2++)
+                    for (int mt = 0; mt < 2; mt++)
+                        U[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt][h == 2], h == 0 ? b1[c] : h == 1 ? b2[c] : bs[c],
+                                                                          U[mt][c], 0, 0, 0);
 #pragma unroll
-                        for (int mt = 0; mt < 2; mt++)
-                            U[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt][pa], h2 ? b2[c] : b1[c], U[mt][c],
-                                                                              0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
+                for (int i = 0; i < 6; i++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
                 }
             }
         }
