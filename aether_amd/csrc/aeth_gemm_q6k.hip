@@ -253,9 +253,9 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
                 }
                 issueSD(min(b + 1, nb - 1));  // the slots are read: the next super-block's scales and d
             }
-            // this slice's operands: B1 = lo·(q − 32), B2 = 16·hi·(q − 32) for sub-block s, k-order
-            // [0, 2, 1, 3] per 4 (the pairs of bytes (0, 2) and (1, 3) of each dword, as the prep
-            // orders A); 0x64 | q is the half 1024 + q
+            // this slice's operands: B1 = lo·(q − 32), B2 = 16·hi·(q − 32), Bs = fp16(sc·(q − 32))
+            // for sub-block s, k-order [0, 2, 1, 3] per 4 (the pairs of bytes (0, 2) and (1, 3) of
+            // each dword, as the prep orders A); 0x64 | q is the half 1024 + q
             const half2_t k1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
             auto build = [&](int c, half8_t& b1, half8_t& b2, half8_t& bs) {
                 const int sc = (int)(int8_t)((scr[c][s >> 2] >> (8 * (s & 3))) & 0xFFu);
