@@ -543,10 +543,16 @@ static int gemm_prep(const float* d_a, int64_t m, int k, unsigned flags, const G
 }
 
 bool aeth_q4k_gemm_rows(const aeth_weight* w, int64_t m) {
-    // measured (prep + GEMM against the row-batched GEMV, weights from HBM): 14336 × 4096 at m = 2 / 4 / 8:
-    // 35.8 / 35.1 / 35.3 µs against 13.3 / 22.0 / 37.5; 4096 × 4096 at m = 2 / 8 / 12: 30.5 / 30.9 / 30.9
-    // against 5.8 / 15.1 / 20.9
-    return m >= 16 || (m >= 8 && w->n > 8192);
+    // AETH_Q4K_GEMM_ROWS=r takes the GEMM from r rows (tests and measurements; read once)
+    static const int64_t env_rows = getenv("AETH_Q4K_GEMM_ROWS") ? atoll(getenv("AETH_Q4K_GEMM_ROWS")) : 0;
+    if (env_rows > 0) return m >= env_rows;
+    // The row-batched GEMV streams the weight once per row; the GEMM (its K split over workgroups
+    // while its tiles are at most half the CUs) costs a near-constant 24 µs (k = 4096) to 42 µs
+    // (28672 × 4096) up to 64 rows. Measured crossovers (prep + GEMM against the GEMV, rotated
+    // weight copies): 4096 × 4096 ≈ 13 rows, 6144 × 4096 ≈ 12, 4096 × 14336, 14336 × 4096 and
+    // 28672 × 4096 ≈ 5, i.e. where m · (weight bytes) reaches ≈ 150 MB; from 16 rows the GEMM
+    // takes any weight (a 1024 × 4096 one would gain from the GEMV up to ≈ 50 rows).
+    return m >= 16 || (m >= 5 && m * w->nb * w->n * 144 >= 150000000LL);
 }
 
 bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {
@@ -599,9 +605,20 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     // offsets of the buffer loads, and AETH_GEMM_KERNEL=2 forces it (tests)
     static const int env_kernel = getenv("AETH_GEMM_KERNEL") ? atoi(getenv("AETH_GEMM_KERNEL")) : 0;
     if (fits32 && env_kernel != 2) {
+        // at most half as many tiles as CUs: K split over workgroups too, as many splits as fit in one
+        // round of workgroups (each wave keeps at least one super-block), the partial tiles in the
+        // stream's scratch (not with a caller's workspace)
+        const int ksplit = ws ? 1 : (int)std::max<int64_t>(1, std::min<int64_t>(aeth_num_cus() / ((int64_t)gm * gn), nb / 8));
+        float* part = nullptr;
+        if (ksplit > 1) {
+            void* p = nullptr;
+            rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)ksplit * mp * gn * G2_BN * sizeof(float), &p);
+            if (rc) return rc;
+            part = (float*)p;
+        }
         KqArgs Q{(const uint8_t*)frag, (const uint8_t*)Sh, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, (int)ntiles,
                  (int)mp, gm, gn, (int)ab, (int)(mp * (k / 32) * 4), (int)qb, (int)std::min(hb, (int64_t)INT32_MAX),
-                 d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0};
+                 d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0, ksplit, part, gn * G2_BN};
         return aeth_gemm_kq_launch(Q, s);
     }
     hipLaunchKernelGGL(k_gemm_q4k_ring, dim3((unsigned)(gm * gn)), dim3(256), 0, s, G);
@@ -649,8 +666,9 @@ int aeth_gemm_q6k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     int rc = gemm_prep(d_a, m, k, flags, in, s, nullptr, 0, frag, Sh, esc);
     if (rc) return rc;
     const int64_t ntiles = aeth_cdiv(w->n, 16), gm = mp / G2_BM, gn = aeth_cdiv(w->n, G2_BN);
-    // fewer tiles than CUs: split K over workgroups too (each wave keeps at least one super-block)
-    const int ksplit = (int)std::max<int64_t>(1, std::min<int64_t>(aeth_cdiv(aeth_num_cus(), gm * gn), nb / 8));
+    // at most half as many tiles as CUs: split K over workgroups too, as many splits as fit in one
+    // round of workgroups (each wave keeps at least one super-block)
+    const int ksplit = (int)std::max<int64_t>(1, std::min<int64_t>(aeth_num_cus() / (gm * gn), nb / 8));
     float* part = nullptr;
     if (ksplit > 1) {
         void* p = nullptr;

@@ -157,8 +157,26 @@ struct KqArgs {
     int64_t ldc;
     int accumulate;
     int swiglu;            // C[row][col/2] = g·σ(g)·u over the (g, u) column pairs
+    // K split over workgroups (ksplit > 1): as Q6Args
+    int ksplit;
+    float* part;
+    int pld;
 };
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s);
+
+// The second kernel of a GEMM split over K across workgroups (aeth_gemm_q6k.hip): the splits'
+// tile sums part[split][row][col] (rows mp, pld columns) added in split order, then the
+// epilogue: C[row][col] = Σ·2^e (+ C with accumulate), or with swiglu h = g·σ(g)·u of the
+// (g, u) column pairs at C[row][col/2].
+struct SplitSum {
+    const float* part;
+    int ksplit, mp, pld;
+    const float* escale;
+    float* C;
+    int64_t ldc;
+    int m, n, accumulate, swiglu;
+};
+int aeth_gemm_split_sum_launch(const SplitSum& S, hipStream_t s);
 
 // Arguments of the Q6_K GEMM kernel (aeth_gemm_q6k.hip): A as for KqArgs, the Q6_K weight
 // planes (aeth_weights.hip).

@@ -55,11 +55,15 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
     __shared__ __attribute__((aligned(1024))) char smem[K8_W * K8_WAVE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // workgroup → (K split ks, tile): splits of one tile are T workgroups apart, so each keeps
+    // the tile's XCD when T is a multiple of 8
+    const int T = G.gm * G.gn, ks = (int)blockIdx.x / T;
     int tm, tn;
-    g2_tile(blockIdx.x, G.gm, G.gn, tm, tn);
+    g2_tile((int)blockIdx.x - ks * T, G.gm, G.gn, tm, tn);
     const int n0 = tn * 128, m0 = tm * 64, t0 = n0 >> 4;
     const int nb = G.nb, nks = G.k >> 4, ksb = G.k >> 5;
-    const int sb0 = nb * wave / K8_W, nsb = nb * (wave + 1) / K8_W - sb0, ns = 16 * nsb;
+    const int lo = nb * ks / G.ksplit, len = nb * (ks + 1) / G.ksplit - lo;  // this split's super-blocks
+    const int sb0 = lo + len * wave / K8_W, nsb = lo + len * (wave + 1) / K8_W - sb0, ns = 16 * nsb;
     char* wl = smem + wave * K8_WAVE;
     const uint32_t wl_lds = lds_addr(wl);
 
@@ -290,7 +294,7 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
 #pragma unroll
     for (int r = 0; r < 16; r++) rows[r] = m0 + 32 * mt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
     G2Epi E;  // in flight during the reduction
-    g2_epi_load(E, G.escale, G.C, G.ldc, G.m, G.n, rows, col, G.accumulate);
+    if (G.ksplit == 1) g2_epi_load(E, G.escale, G.C, G.ldc, G.m, G.n, rows, col, G.accumulate);
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -325,7 +329,11 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
 #pragma unroll
         for (int w = 1; w < 4; w++) sum[r] += red[(((w * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
     }
-    if (G.swiglu) {
+    if (G.ksplit > 1) {  // the split's partial tile (rows < mp, columns < pld: no bounds to check)
+        float* P = G.part + (int64_t)ks * G.mp * G.pld + col;
+#pragma unroll
+        for (int r = 0; r < 16; r++) P[(int64_t)rows[r] * G.pld] = sum[r];
+    } else if (G.swiglu) {
 #pragma unroll
         for (int r = 0; r < 16; r += 2) g2_store_swiglu(E, r, G.C, G.ldc, G.m, G.n, rows[r], col, sum[r], sum[r + 1]);
     } else {
@@ -335,7 +343,9 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
 }
 
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s) {
-    hipLaunchKernelGGL(k_gemm_q4k_kq, dim3((unsigned)(G.gm * G.gn)), dim3(64 * K8_W), 0, s, G);
+    hipLaunchKernelGGL(k_gemm_q4k_kq, dim3((unsigned)(G.gm * G.gn * G.ksplit)), dim3(64 * K8_W), 0, s, G);
     AETH_LAUNCH_CHECK();
-    return AETH_OK;
+    if (G.ksplit == 1) return AETH_OK;
+    const SplitSum S{G.part, G.ksplit, G.mp, G.pld, G.escale, G.C, G.ldc, G.m, G.n, G.accumulate, G.swiglu};
+    return aeth_gemm_split_sum_launch(S, s);
 }

@@ -377,10 +377,8 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
     }
 }
 
-// Sum of the K splits, in split order, and the epilogue: C[row][col] = Σ_s part[s][row][col]·2^e
-// (+ C with accumulate), or with swiglu h = g·σ(g)·u of the (g, u) column pairs at C[row][col/2].
-// One thread per 4 columns of a row.
-__global__ void __launch_bounds__(256) k_gemm_split_sum(Q6Args G) {
+// Sum of the K splits, in split order, and the epilogue (SplitSum). One thread per 4 columns of a row.
+__global__ void __launch_bounds__(256) k_gemm_split_sum(SplitSum G) {
     const int q4 = G.pld >> 2;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (int64_t)G.m * q4) return;
@@ -410,13 +408,17 @@ __global__ void __launch_bounds__(256) k_gemm_split_sum(Q6Args G) {
     }
 }
 
+int aeth_gemm_split_sum_launch(const SplitSum& S, hipStream_t s) {
+    const int64_t threads = (int64_t)S.m * (S.pld / 4);
+    hipLaunchKernelGGL(k_gemm_split_sum, dim3((unsigned)aeth_cdiv(threads, 256)), dim3(256), 0, s, S);
+    AETH_LAUNCH_CHECK();
+    return AETH_OK;
+}
+
 int aeth_gemm_q6k_kq_launch(const Q6Args& G, hipStream_t s) {
     hipLaunchKernelGGL(k_gemm_q6k_kq, dim3((unsigned)(G.gm * G.gn * G.ksplit)), dim3(64 * K6_W), 0, s, G);
     AETH_LAUNCH_CHECK();
-    if (G.ksplit > 1) {
-        const int64_t threads = (int64_t)G.m * (G.pld / 4);
-        hipLaunchKernelGGL(k_gemm_split_sum, dim3((unsigned)aeth_cdiv(threads, 256)), dim3(256), 0, s, G);
-        AETH_LAUNCH_CHECK();
-    }
-    return AETH_OK;
+    if (G.ksplit == 1) return AETH_OK;
+    const SplitSum S{G.part, G.ksplit, G.mp, G.pld, G.escale, G.C, G.ldc, G.m, G.n, G.accumulate, G.swiglu};
+    return aeth_gemm_split_sum_launch(S, s);
 }

@@ -128,9 +128,9 @@ struct GemmIn {
     bool swiglu_out = false;
 };
 // Whether m activation rows against planar Q4_K weight w go to the prefill GEMM
-// (else the row-batched GEMV): from 16 rows, or 8 when n > 8192. Below that the
-// GEMM's 64-row tile idles most of its MFMA work and its n/128 workgroups leave
-// most CUs empty, while the GEMV streams the weight once per row.
+// (else the row-batched GEMV): from 16 rows, or from 5 once m · (weight bytes) reaches
+// 150 MB. Below that the GEMM's near-constant cost (its 64-row tile idles most of its
+// MFMA work) exceeds the GEMV's, which streams the weight once per row.
 bool aeth_q4k_gemm_rows(const aeth_weight* w, int64_t m);
 // Whether aeth_gemm_q4k_launch runs producer `mode` for this weight and A (else
 // the caller runs the producer itself): a planar Q4_K weight, m > 1, and for

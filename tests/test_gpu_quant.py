@@ -334,13 +334,15 @@ def test_gemm_q4k_tiles_exponents_accumulate(gpu, m, n, k):
     assert np.all(got[(2 * m) // 3] == 0.0)
 
 
-# Small batches of Q4_K rows: up to 15 rows (7 when n > 8192) take the row-batched
-# GEMV, more the GEMM (aeth_q4k_gemm_rows); both sides of each boundary, plain,
-# accumulate and the dot-product mode (a14 activation blocks).
-@pytest.mark.parametrize("m,n", [(2, 4096), (7, 14336), (8, 14336), (12, 6144), (15, 8192), (16, 4096)])
-def test_q4k_small_batches(gpu, m, n):
-    k = 4096
-    rng = np.random.default_rng(m * 101 + n)
+# Small batches of Q4_K rows: the row-batched GEMV below 16 rows unless m · (weight
+# bytes) reaches 150 MB from 5 rows, else the GEMM (aeth_q4k_gemm_rows; its K split over
+# up to 8 workgroups at these m); both sides of each boundary, plain, accumulate and the
+# dot-product mode (a14 activation blocks).
+@pytest.mark.parametrize("m,n,k", [(2, 4096, 4096), (15, 4096, 4096), (16, 4096, 4096), (10, 6144, 4096),
+                                   (11, 6144, 4096), (4, 14336, 4096), (5, 14336, 4096), (4, 4096, 14336),
+                                   (5, 4096, 14336), (4, 28672, 4096), (5, 28672, 4096)])
+def test_q4k_small_batches(gpu, m, n, k):
+    rng = np.random.default_rng(m * 101 + n + k)
     raw = weight(Q4_K, n, k, 5 * n + m)
     x = rng.standard_normal((m, k)).astype(np.float32)
     w = make_weight(gpu, Q4_K, n, k, raw)
@@ -350,10 +352,10 @@ def test_q4k_small_batches(gpu, m, n):
     got_q8 = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_Q8_ACTIVATIONS)
     A.lib().aeth_weight_free(w)
     ref = O.reference_matmul(Q4_K, x.ravel(), raw, m, n, k).reshape(m, n)
-    assert_close(got, ref, what="q4_k m=%d n=%d" % (m, n))
-    assert_close(got_acc, ref + y0, what="q4_k accumulate m=%d n=%d" % (m, n))
+    assert_close(got, ref, what="q4_k m=%d n=%d k=%d" % (m, n, k))
+    assert_close(got_acc, ref + y0, what="q4_k accumulate m=%d n=%d k=%d" % (m, n, k))
     ref_q8 = O.dotprod_ref(Q4_K, O.quantize_activations_q8_0(x.ravel(), m, k), raw, m, n, k).reshape(m, n)
-    assert_close(got_q8, ref_q8, what="q4_k dot-product mode m=%d n=%d" % (m, n))
+    assert_close(got_q8, ref_q8, what="q4_k dot-product mode m=%d n=%d k=%d" % (m, n, k))
 
 
 def check_q6k_gemm(torch, m, n, k):
