@@ -194,6 +194,13 @@ def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512, wan
     for _ in range(reps):
         A.check(L.aeth_runner_prefill(r, prompt, prefill_tokens, None, None), "prefill")
     pf_s = (time.perf_counter() - t0) / reps
+    # a short prompt: 32 tokens, where the GEMMs' tiles are fewer than the CUs (K split over workgroups)
+    short = (ctypes.c_int32 * 32)(*[(7919 * i + 13) % 128256 for i in range(32)])
+    A.check(L.aeth_runner_prefill(r, short, 32, None, None), "short prefill warmup")
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        A.check(L.aeth_runner_prefill(r, short, 32, None, None), "short prefill")
+    pf32_s = (time.perf_counter() - t0) / reps
     cpu_model = export_decode_model(A, r, cfg, prefilled, [1] + list(toks)[:7]) if want_cpu else None
     L.aeth_runner_free(r)
     layer_weights = 4096 * 4096 * 2 + 1024 * 4096 * 2 + 14336 * 4096 * 3
@@ -206,6 +213,7 @@ def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512, wan
     return {"tok_s": n_tokens / dt_s, "ms_per_token": dt_s * 1e3 / n_tokens, "setup_s": setup_s,
             "gbs": step_bytes * n_tokens / dt_s / 1e9, "step_bytes": step_bytes, "first_tokens": list(toks)[:8],
             "prefill_tok_s": prefill_tokens / pf_s, "prefill_ms": pf_s * 1e3, "prefill_tflops": pf_flops / pf_s / 1e12,
+            "prefill32_ms": pf32_s * 1e3,
             "cpu_model": cpu_model}
 
 
@@ -599,6 +607,9 @@ def main():
         extra["prefill_8b_q4k_512"] = {"tok/s": round(d["prefill_tok_s"], 1), "ms": round(d["prefill_ms"], 2),
                                        "TFLOP/s": round(d["prefill_tflops"], 2), "tokens": 512}
         print("[bench] prefill 8B: %s" % extra["prefill_8b_q4k_512"], file=sys.stderr, flush=True)
+        extra["prefill_8b_q4k_32"] = {"tok/s": round(32 / d["prefill32_ms"] * 1e3, 1), "ms": round(d["prefill32_ms"], 3),
+                                      "tokens": 32}
+        print("[bench] prefill 8B, 32 tokens: %s" % extra["prefill_8b_q4k_32"], file=sys.stderr, flush=True)
 
     if "decode_eager" in sections:  # not a default section: the same decode without the HIP graph
         d = bench_decode_eager(torch, A, n_tokens=max(2, min(args.steps, 128)))
