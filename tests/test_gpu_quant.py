@@ -308,7 +308,12 @@ def test_synthetic_generator_deterministic(gpu):
 def test_gemm_q4k_tiles_exponents_accumulate(gpu, m, n, k):
     """Ragged tiles, per-row exponents (2^20, 2^-12, zero rows, a block past
     fp16 range) and accumulate, up to rows of 16384 and 20480 elements (the
-    prep holds 1, 2, 4 or 8 steps of a row per wave, 20480 in two chunks)."""
+    prep holds 1, 2, 4 or 8 steps of a row per wave, 20480 in two chunks); K
+    split over 8, 10 and 4 workgroups for the last three shapes."""
+    check_q4k_gemm(gpu, m, n, k)
+
+
+def check_q4k_gemm(gpu, m, n, k):
     rng = np.random.default_rng(m * 31 + n * 7 + k)
     raw = weight(Q4_K, n, k, 3 * n + k)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -754,10 +759,12 @@ import sys, torch
 sys.path.insert(0, %r)
 import aether_amd as A
 A.check(A.lib().aeth_init(0))
-from tests.test_gpu_quant import check_q6k_gemm
+from tests.test_gpu_quant import check_q4k_gemm, check_q6k_gemm
 for m, n, k in ((70, 130, 768), (16, 16, 512), (3, 48, 1024), (65, 300, 1024), (33, 96, 14336), (200, 64, 14336),
                 (34, 64, 20480)):
     check_q6k_gemm(torch, m, n, k)
+for m, n, k in ((3, 48, 1024), (4, 300, 4096), (6, 64, 14336)):  # the Q4_K GEMM below its 16-row floor
+    check_q4k_gemm(torch, m, n, k)
 from tests.test_gpu_decode import test_runner_mixed_formats
 for mix in (0, 1):
     for n in (23, 150):
@@ -771,13 +778,13 @@ def test_q6k_gemm_small_weights(gpu):
     read once per process, so in a fresh process): ragged tiles from 3 rows, K split over up
     to 10 workgroups, and runner prefills of mixed-format layers, where the Q6_K v projection
     writes its columns of q|k|v with the output row stride and the Q6_K down projection adds
-    the residual."""
+    the residual; and the Q4_K GEMM at 3 to 6 rows (AETH_Q4K_GEMM_ROWS=2)."""
     import os
     import subprocess
     import sys
 
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    env = dict(os.environ, AETH_Q6K_GEMM_ROWS="2")
+    env = dict(os.environ, AETH_Q6K_GEMM_ROWS="2", AETH_Q4K_GEMM_ROWS="2")
     r = subprocess.run([sys.executable, "-c", Q6K_GEMM_SCRIPT % root], env=env, cwd=root, timeout=240,
                        stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:]
