@@ -525,6 +525,7 @@ static int gemm_prep(const float* d_a, int64_t m, int k, unsigned flags, const G
     Sh = frag + (size_t)mp * k * 2;
     _Float16* Sl = Sh + (size_t)mp * (k / 32);
     esc = (float*)(Sl + (size_t)mp * (k / 32));
+    if (in && in->prepared) return AETH_OK;
     const bool al16 = ((uintptr_t)d_a & 15) == 0;
     const bool q8 = (flags & AETH_MM_Q8_ACTIVATIONS) != 0;
     // registers per wave: its share of the row's steps, rounded up to 1, 2, 4 or 8 (past 8: chunks)

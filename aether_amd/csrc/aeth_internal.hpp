@@ -126,6 +126,9 @@ struct GemmIn {
     // the output's columns are interleaved (g, u) pairs (the gate|up weight): C receives
     // h = g·σ(g)·u, n/2 columns per row (σ through the reciprocal instruction), instead of the pairs
     bool swiglu_out = false;
+    // the stream's GEMM scratch already holds this A's prep (the same d_a, m, k, mode and
+    // flags, run by the GEMM launched just before on the stream): the prep launch is skipped
+    bool prepared = false;
 };
 // Whether m activation rows against planar Q4_K weight w go to the prefill GEMM
 // (else the row-batched GEMV): from 16 rows, or from 5 once m · (weight bytes) reaches

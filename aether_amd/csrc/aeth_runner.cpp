@@ -321,17 +321,22 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
             // takes the RMSNorm in its prep reads x; any other reads rmsnorm(x), formed once
             const int64_t qd = nh * hd, kvd = nkv * hd, ld = qd + 2 * kvd;
             bool normed = false;
+            GemmIn pin = nin;  // after the first fused GEMM the stream's scratch holds the prep of x
             auto proj = [&](const aeth_weight* w, float* out) -> int {
-                if (aeth_gemm_fuses(w, n, PREP_RMSNORM, r->p_x, attn_norm))
-                    return aeth_gemm_q4k_launch(w, r->p_x, n, out, 0, s, ld, nullptr, 0, &nin);
-                if (w->dtype == AETH_DTYPE_Q6_K && aeth_q6k_gemm_fuses(w, n, PREP_RMSNORM, r->p_x, attn_norm))
-                    return aeth_gemm_q6k_launch(w, r->p_x, n, out, 0, s, ld, &nin);
-                if (!normed) {
-                    int e = aeth_rmsnorm_launch(r->p_x, attn_norm, n, d, c.rms_norm_eps, r->p_n, s);
-                    if (e) return e;
-                    normed = true;
+                int e;
+                if (aeth_gemm_fuses(w, n, PREP_RMSNORM, r->p_x, attn_norm)) {
+                    e = aeth_gemm_q4k_launch(w, r->p_x, n, out, 0, s, ld, nullptr, 0, &pin);
+                } else if (w->dtype == AETH_DTYPE_Q6_K && aeth_q6k_gemm_fuses(w, n, PREP_RMSNORM, r->p_x, attn_norm)) {
+                    e = aeth_gemm_q6k_launch(w, r->p_x, n, out, 0, s, ld, &pin);
+                } else {
+                    if (!normed) {
+                        if ((e = aeth_rmsnorm_launch(r->p_x, attn_norm, n, d, c.rms_norm_eps, r->p_n, s))) return e;
+                        normed = true;
+                    }
+                    return aeth_qmatmul_ld(w, r->p_n, n, out, ld, 0, s);
                 }
-                return aeth_qmatmul_ld(w, r->p_n, n, out, ld, 0, s);
+                pin.prepared = e == AETH_OK;
+                return e;
             };
             if (r->wqkv[l]) {
                 if ((rc = proj(r->wqkv[l], r->p_qkv))) return rc;
