@@ -116,7 +116,7 @@ __device__ __forceinline__ void prep_ld8(const float* __restrict__ p, float* v) 
 
 // SPW: steps a wave holds in registers, at least its share ⌈S/4⌉ (1, 2, 4 or 8: k ≤ 16384 in one chunk).
 // PREP_ROWS: rows per workgroup, 4 (2 where the producer's 8 steps of inputs need more than the
-// 128 registers of a 16-wave workgroup).
+// 128 registers of a 16-wave workgroup; 1 for at most 128 rows, which then take more CUs).
 template <bool AL16, bool Q8, int MODE, int SPW, int PREP_ROWS>
 __global__ void __launch_bounds__(64 * PREP_ROWS * PREP_WK) k_gemm_prep(PrepArgs P) {
     static_assert(!Q8 || MODE == PREP_PLAIN, "the producers feed the exact mode");
@@ -497,7 +497,10 @@ int64_t aeth_gemm_ws_bytes(int64_t m, int64_t k) {
 template <bool AL16, bool Q8, int MODE, int SPW>
 static void prep_launch_r(unsigned mp, hipStream_t s, const PrepArgs& P) {
     constexpr int R = SPW == 8 && MODE != PREP_PLAIN ? 2 : 4;
-    hipLaunchKernelGGL((k_gemm_prep<AL16, Q8, MODE, SPW, R>), dim3(mp / R), dim3(64 * R * PREP_WK), 0, s, P);
+    if (mp <= 128)  // few rows: one row per workgroup, so that they spread over more CUs
+        hipLaunchKernelGGL((k_gemm_prep<AL16, Q8, MODE, SPW, 1>), dim3(mp), dim3(64 * PREP_WK), 0, s, P);
+    else
+        hipLaunchKernelGGL((k_gemm_prep<AL16, Q8, MODE, SPW, R>), dim3(mp / R), dim3(64 * R * PREP_WK), 0, s, P);
 }
 template <bool AL16, bool Q8, int MODE>
 static void prep_launch(int spw, unsigned mp, hipStream_t s, const PrepArgs& P) {
