@@ -20,6 +20,7 @@ SOURCES = [
     "aeth_gemm.hip",
     "aeth_gemm_kq.hip",
     "aeth_gemm_q6k.hip",
+    "aeth_gemm_q80.hip",
     "aeth_decode_ops.hip",
     "aeth_prefill.hip",
     "aeth_backend.hip",
@@ -44,6 +45,7 @@ EXTRA = {
     "aeth_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "aeth_gemm_kq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "aeth_gemm_q6k.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "aeth_gemm_q80.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 COMMON = [

@@ -686,3 +686,40 @@ int aeth_gemm_q6k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
              ksplit, part, (int)(gn * G2_BN)};
     return aeth_gemm_q6k_kq_launch(Q, s);
 }
+
+bool aeth_q80_gemm_rows(const aeth_weight* w, int64_t m) {
+    if (!w || w->dtype != AETH_DTYPE_Q8_0 || w->order != AETH_ORDER_PLANAR || w->k != w->nb * 32 || m <= 1) return false;
+    const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM, ntiles = aeth_cdiv(w->n, 16), ngr = aeth_cdiv(w->nb, 4);
+    if (ntiles * ngr * 2048 >= INT32_MAX || mp * w->k * 4 >= INT32_MAX || mp > (1LL << 20)) return false;
+    // AETH_Q80_GEMM_ROWS=r takes the GEMM from r rows (tests and measurements; read once)
+    static const int64_t env_rows = getenv("AETH_Q80_GEMM_ROWS") ? atoll(getenv("AETH_Q80_GEMM_ROWS")) : 0;
+    if (env_rows > 0) return m >= env_rows;
+    return m >= 16 || (m >= 5 && m * w->nb * w->n * 34 >= 150000000LL);
+}
+
+int aeth_gemm_q80_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
+                         hipStream_t s, int64_t ldc) {
+    if (!aeth_q80_gemm_rows(w, m)) return aeth_set_error(AETH_EINVAL, "gemm q8_0: shape not taken (m=%lld)", (long long)m);
+    const int k = (int)w->k, nb = (int)w->nb;
+    if (ldc <= 0) ldc = w->n;
+    const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM;
+    _Float16 *frag, *Sh;
+    float* esc;
+    int rc = gemm_prep(d_a, m, k, flags, nullptr, s, nullptr, 0, frag, Sh, esc);
+    if (rc) return rc;
+    const int64_t ntiles = aeth_cdiv(w->n, 16), ngr = aeth_cdiv(nb, 4), gm = mp / G2_BM, gn = aeth_cdiv(w->n, G2_BN);
+    // at most half as many tiles as CUs: K split over workgroups too (each wave keeps 8 blocks at least,
+    // the 256 elements of a K-quant super-block)
+    const int ksplit = (int)std::max<int64_t>(1, std::min<int64_t>(aeth_num_cus() / (gm * gn), nb / 64));
+    float* part = nullptr;
+    if (ksplit > 1) {
+        void* p = nullptr;
+        rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)ksplit * mp * gn * G2_BN * sizeof(float), &p);
+        if (rc) return rc;
+        part = (float*)p;
+    }
+    Q80Args Q{(const uint8_t*)frag, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, (int)ngr, (int)ntiles, (int)mp,
+              (int)gm, (int)gn, (int)(mp * k * 4), (int)(ntiles * ngr * 2048), (int)(ntiles * ngr * 128), d_c, ldc,
+              (flags & AETH_MM_ACCUMULATE) ? 1 : 0, 0, ksplit, part, (int)(gn * G2_BN)};
+    return aeth_gemm_q80_kq_launch(Q, s);
+}

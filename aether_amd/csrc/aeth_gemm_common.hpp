@@ -201,3 +201,23 @@ struct Q6Args {
     int pld;
 };
 int aeth_gemm_q6k_kq_launch(const Q6Args& G, hipStream_t s);
+
+// Arguments of the Q8_0 GEMM kernel (aeth_gemm_q80.hip): A as for KqArgs, the Q8_0 weight planes
+// (aeth_weights.hip: blocks in groups of 4 per row).
+struct Q80Args {
+    const uint8_t* frag;   // A·2^-e as fp16 MFMA fragments (k_gemm_prep)
+    const float* escale;   // [mp]: 2^e
+    const uint8_t* q;      // [tile][group][pair 2][lane][16 B]
+    const uint8_t* dd;     // [tile][group][4 blocks][16 rows] (f16)
+    int m, n, k, nb, ngr, ntiles, mp;
+    int gm, gn;            // 64-row and 128-column tiles of C
+    int a_bytes, q_bytes, d_bytes;  // buffer extents (each < 2^31)
+    float* C;
+    int64_t ldc;
+    int accumulate;
+    int swiglu;
+    int ksplit;            // K split over workgroups: as Q6Args
+    float* part;
+    int pld;
+};
+int aeth_gemm_q80_kq_launch(const Q80Args& G, hipStream_t s);

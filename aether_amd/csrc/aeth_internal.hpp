@@ -148,6 +148,14 @@ bool aeth_gemm_swiglu_out(const aeth_weight* w, int64_t m);
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s, int64_t ldc = 0, void* ws = nullptr, size_t ws_bytes = 0,
                          const GemmIn* in = nullptr);
+// Whether m activation rows against planar Q8_0 weight w take the Q8_0 GEMM (aeth_gemm_q80.hip):
+// whole blocks (k = 32·nb) within the kernel's 32-bit buffer offsets, from 16 rows, or from 5
+// once m · (weight bytes) reaches 150 MB.
+bool aeth_q80_gemm_rows(const aeth_weight* w, int64_t m);
+// Q8_0 prefill GEMM (AETH_MM_ACCUMULATE and the Q8 activation blocks as aeth_gemm_q4k_launch);
+// requires aeth_q80_gemm_rows.
+int aeth_gemm_q80_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
+                         hipStream_t s, int64_t ldc = 0);
 // Whether m activation rows against Q6_K weight w take the Q6_K GEMM (aeth_gemm_q6k.hip):
 // planar whole super-blocks within the kernel's 32-bit buffer offsets, once m · (weight
 // bytes) reaches 200 MB (the row-batched GEMV below).

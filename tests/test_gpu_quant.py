@@ -425,6 +425,57 @@ def test_gemm_q6k_tiles_exponents_accumulate(gpu, m, n, k):
     check_q6k_gemm(gpu, m, n, k)
 
 
+def check_q80_gemm(torch, m, n, k):
+    """Q8_0 product of m rows against the oracle, as check_q6k_gemm: per-row exponents, plain,
+    accumulate and the dot-product mode; the weights carry quants −128 and 127 and blocks whose
+    d is zero. Rows of magnitude 1 are anchored on the float64 product of the same operands."""
+    rng = np.random.default_rng(m * 41 + n * 13 + k)
+    raw = weight(Q8_0, n, k, 11 * n + k).reshape(-1, 34)
+    nblk = raw.shape[0]
+    pick = rng.integers(0, nblk, max(2, nblk // 16))
+    raw[pick[0::2], 2:34] = np.int8(-128).view(np.uint8)
+    raw[pick[1::2], 2:34] = np.int8(127).view(np.uint8)
+    raw[rng.integers(0, nblk, max(1, nblk // 20)), 0:2] = 0
+    raw = raw.reshape(-1)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    scale = np.ones(m, dtype=np.float32)
+    scale[m // 3] = 2.0 ** 20
+    scale[m // 2] = 2.0 ** -12
+    scale[(2 * m) // 3] = 0.0
+    if m > 40:
+        scale[33:40] = 2.0 ** 15
+    x *= scale[:, None]
+    w = make_weight(torch, Q8_0, n, k, raw)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    got = gemv(torch, w, x.ravel(), n, m)
+    got_acc = gemv(torch, w, x.ravel(), n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    got_q8 = gemv(torch, w, x.ravel(), n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q8_0, x.ravel(), raw, m, n, k).reshape(m, n)
+    plain = scale == 1.0
+    w64 = O.dequant(Q8_0, raw, n * k).reshape(n, k).astype(np.float64)
+    ex = x[plain].astype(np.float64) @ w64.T
+    what = "q8_0 m=%d n=%d k=%d" % (m, n, k)
+    assert_close_logits(got[plain], ref[plain], floor=0.0, exact=ex, what=what)
+    assert_close_rows(got, ref, what=what + " (scaled rows)")
+    assert_close_logits(got_acc[plain], (ref + y0)[plain], floor=0.0, exact=ex + y0[plain], what=what + " accumulate")
+    assert np.all(got[(2 * m) // 3] == 0.0)
+    aq = O.quantize_activations_q8_0(x.ravel(), m, k)
+    ref_q8 = O.dotprod_ref(Q8_0, aq, raw, m, n, k).reshape(m, n)
+    ex_q8 = O.dequant(Q8_0, aq, m * k).reshape(m, k)[plain].astype(np.float64) @ w64.T
+    assert_close_rows(got_q8, ref_q8, what=what + " dot-product mode")
+    assert_close_logits(got_q8[plain], ref_q8[plain], floor=0.0, exact=ex_q8, what=what + " dot-product mode")
+
+
+# The Q8_0 GEMM (planar Q8_0, k a multiple of 32, from 16 rows): block counts that split
+# unevenly over the 8 waves or leave waves idle (4, 25 — not whole groups of 4 — 40, 64, 128,
+# 448), K split over 2 and 7 workgroups, m and n off the tile grid.
+@pytest.mark.parametrize("m,n,k", [(70, 130, 128), (16, 16, 800), (65, 300, 1280), (130, 40, 4096),
+                                   (45, 48, 14336), (200, 64, 4096), (17, 700, 2048), (512, 256, 4096)])
+def test_gemm_q80_tiles_exponents_accumulate(gpu, m, n, k):
+    check_q80_gemm(gpu, m, n, k)
+
+
 # Small batches of Q6_K rows: the row-batched GEMV until m · (weight bytes) reaches 200 MB,
 # then the GEMM (aeth_q6k_gemm_rows); both sides of the boundary at three weight sizes, plain,
 # accumulate and the dot-product mode.
@@ -759,12 +810,14 @@ import sys, torch
 sys.path.insert(0, %r)
 import aether_amd as A
 A.check(A.lib().aeth_init(0))
-from tests.test_gpu_quant import check_q4k_gemm, check_q6k_gemm
+from tests.test_gpu_quant import check_q4k_gemm, check_q6k_gemm, check_q80_gemm
 for m, n, k in ((70, 130, 768), (16, 16, 512), (3, 48, 1024), (65, 300, 1024), (33, 96, 14336), (200, 64, 14336),
                 (34, 64, 20480)):
     check_q6k_gemm(torch, m, n, k)
 for m, n, k in ((3, 48, 1024), (4, 300, 4096), (6, 64, 14336)):  # the Q4_K GEMM below its 16-row floor
     check_q4k_gemm(torch, m, n, k)
+for m, n, k in ((3, 48, 1024), (6, 64, 14336)):  # and the Q8_0 GEMM
+    check_q80_gemm(torch, m, n, k)
 from tests.test_gpu_decode import test_runner_mixed_formats
 for mix in (0, 1):
     for n in (23, 150):
@@ -778,13 +831,14 @@ def test_q6k_gemm_small_weights(gpu):
     read once per process, so in a fresh process): ragged tiles from 3 rows, K split over up
     to 10 workgroups, and runner prefills of mixed-format layers, where the Q6_K v projection
     writes its columns of q|k|v with the output row stride and the Q6_K down projection adds
-    the residual; and the Q4_K GEMM at 3 to 6 rows (AETH_Q4K_GEMM_ROWS=2)."""
+    the residual; and the Q4_K and Q8_0 GEMMs at 3 to 6 rows (AETH_Q4K_GEMM_ROWS=2,
+    AETH_Q80_GEMM_ROWS=2)."""
     import os
     import subprocess
     import sys
 
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    env = dict(os.environ, AETH_Q6K_GEMM_ROWS="2", AETH_Q4K_GEMM_ROWS="2")
+    env = dict(os.environ, AETH_Q6K_GEMM_ROWS="2", AETH_Q4K_GEMM_ROWS="2", AETH_Q80_GEMM_ROWS="2")
     r = subprocess.run([sys.executable, "-c", Q6K_GEMM_SCRIPT % root], env=env, cwd=root, timeout=240,
                        stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:]
