@@ -77,8 +77,9 @@ namespace {
 // (4096 × 4096: 0.15 ms, 4096 × 14336: 0.73 ms), the GEMV grows with m (≈ 2 µs per row
 // at 4096 × 4096). Measured crossovers (HIP events, rotated weight copies): Q6_K 4096 ×
 // 4096 ≈ 64 rows, 4096 × 14336 ≈ 80, 1024 × 4096 ≈ 136; Q8_0 ≈ 112; Q5_K ≈ 80; Q2_K ≈ 40
-// and Q3_K ≈ 32 (GGUF order). Q6_K rows of whole super-blocks take the Q6_K GEMM
-// (aeth_gemm_q6k.hip) instead, from the row count aeth_q6k_gemm_rows gives.
+// and Q3_K ≈ 32 (GGUF order). Q6_K rows of whole super-blocks and Q8_0 rows of whole blocks take
+// the Q6_K / Q8_0 GEMMs (aeth_gemm_q6k.hip, aeth_gemm_q80.hip) instead, from the row counts
+// aeth_q6k_gemm_rows / aeth_q80_gemm_rows give.
 int64_t dequant_gemm_rows(int dtype) {
     switch (dtype) {
         case AETH_DTYPE_Q8_0: return 112;

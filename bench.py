@@ -10,7 +10,7 @@ value = algorithmic bytes per launch / mean launch time over K timed launches
 The same JSON line carries the other configs as `extra`: Q8_0 and Q6_K GEMV
 (configs 0, 2), the Q4_K prefill GEMM at M=512 (config 3) and the LLaMA-8B
 shape greedy decode (config 4), the Q5_K GEMV and the headline shape on the
-int8 dot-product path, the Q6_K GEMM at M=512 and the 8B shape with the
+int8 dot-product path, the Q6_K and Q8_0 GEMMs at M=512 and the 8B shape with the
 Q4_K_M format mix (and, on request, GGUF-order F16 / Q2_K GEMVs), plus
 `roofline` for the headline kernel and
 `cpu_baseline`: the oracle's restatement of the reference's AVX2 path on one
@@ -464,8 +464,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,decode,q4_k_m",
+    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,gemm_q80,decode,q4_k_m",
                     help="comma-separated extra sections to run: floor, q8, q6, q5, dotprod, gemm, gemm_q8, gemm_q6k, "
+                         "gemm_q80, "
                          "decode, q4_k_m (default), f16, q2k (GGUF-order formats), decode_eager (the decode step "
                          "without its HIP graph; these three not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -594,6 +595,15 @@ def main():
             if mfma:  # three passes: the ceiling is a third of the fp16 rate
                 extra[key]["frac_exact_mode_ceiling"] = round(r["tflops"] / (mfma["fp16_TFLOP/s"] / 3), 4)
             print("[bench] Q6_K GEMM m=512 n=%d k=%d: %s" % (nn, kk, extra[key]), file=sys.stderr, flush=True)
+    if "gemm_q80" in sections:  # the Q8_0 GEMM (a Q8_0 file's prefill projections)
+        for nn, kk in ((4096, 4096), (4096, 14336)):
+            r = bench_batched(torch, A, 8, nn, kk, 512, max(3, min(args.steps, 20)), 2)
+            key = "q8_0_gemm_m512_n%d_k%d" % (nn, kk)
+            extra[key] = {"TFLOP/s": round(r["tflops"], 2), "ms": round(r["ms"], 4),
+                          "path": "Q8_0 GEMM: exact mode, two fp16 MFMA passes per product"}
+            if mfma:
+                extra[key]["frac_exact_mode_ceiling"] = round(r["tflops"] / (mfma["fp16_TFLOP/s"] / 2), 4)
+            print("[bench] Q8_0 GEMM m=512 n=%d k=%d: %s" % (nn, kk, extra[key]), file=sys.stderr, flush=True)
     if "q4_k_m" in sections:
         extra["q4_k_m_decode_prefill_8b"] = bench_q4_k_m(torch, A)
         print("[bench] Q4_K_M 8B: %s" % extra["q4_k_m_decode_prefill_8b"], file=sys.stderr, flush=True)
