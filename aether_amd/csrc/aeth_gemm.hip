@@ -697,15 +697,31 @@ bool aeth_q80_gemm_rows(const aeth_weight* w, int64_t m) {
     return m >= 16 || (m >= 5 && m * w->nb * w->n * 34 >= 150000000LL);
 }
 
+bool aeth_q80_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {
+    if (!aeth_q80_gemm_rows(w, m)) return false;
+    if (mode == PREP_PLAIN) return true;
+    if (w->k > 16384 || ((uintptr_t)d_a & 15)) return false;  // one chunk of registers per wave, float4 loads
+    if (mode == PREP_RMSNORM) return norm_w && ((uintptr_t)norm_w & 15) == 0;
+    return mode == PREP_SWIGLU;
+}
+
 int aeth_gemm_q80_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s, int64_t ldc) {
+                         hipStream_t s, int64_t ldc, const GemmIn* in) {
     if (!aeth_q80_gemm_rows(w, m)) return aeth_set_error(AETH_EINVAL, "gemm q8_0: shape not taken (m=%lld)", (long long)m);
+    const int mode = in ? in->mode : PREP_PLAIN;
+    const bool swo = in && in->swiglu_out;
+    if (mode != PREP_PLAIN && !aeth_q80_gemm_fuses(w, m, mode, d_a, in->norm_w))
+        return aeth_set_error(AETH_EINVAL, "gemm q8_0: fused producer %d not available", mode);
+    if (mode != PREP_PLAIN && (flags & AETH_MM_Q8_ACTIVATIONS))  // the producers feed the exact (f32) mode only
+        return aeth_set_error(AETH_EINVAL, "gemm q8_0: fused producer %d with Q8 activations", mode);
+    if (swo && ((w->n & 1) || (flags & AETH_MM_ACCUMULATE)))
+        return aeth_set_error(AETH_EINVAL, "gemm q8_0: SwiGLU output needs even n, no accumulate");
     const int k = (int)w->k, nb = (int)w->nb;
-    if (ldc <= 0) ldc = w->n;
+    if (ldc <= 0) ldc = swo ? w->n / 2 : w->n;
     const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM;
     _Float16 *frag, *Sh;
     float* esc;
-    int rc = gemm_prep(d_a, m, k, flags, nullptr, s, nullptr, 0, frag, Sh, esc);
+    int rc = gemm_prep(d_a, m, k, flags, in, s, nullptr, 0, frag, Sh, esc);
     if (rc) return rc;
     const int64_t ntiles = aeth_cdiv(w->n, 16), ngr = aeth_cdiv(nb, 4), gm = mp / G2_BM, gn = aeth_cdiv(w->n, G2_BN);
     // at most half as many tiles as CUs: K split over workgroups too (each wave keeps 8 blocks at least,
@@ -720,6 +736,28 @@ int aeth_gemm_q80_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     }
     Q80Args Q{(const uint8_t*)frag, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, (int)ngr, (int)ntiles, (int)mp,
               (int)gm, (int)gn, (int)(mp * k * 4), (int)(ntiles * ngr * 2048), (int)(ntiles * ngr * 128), d_c, ldc,
-              (flags & AETH_MM_ACCUMULATE) ? 1 : 0, 0, ksplit, part, (int)(gn * G2_BN)};
+              (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0, ksplit, part, (int)(gn * G2_BN)};
     return aeth_gemm_q80_kq_launch(Q, s);
+}
+
+bool aeth_gemm_fused_ok(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {
+    if (!w) return false;
+    if (w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_fuses(w, m, mode, d_a, norm_w);
+    if (w->dtype == AETH_DTYPE_Q6_K) return aeth_q6k_gemm_fuses(w, m, mode, d_a, norm_w);
+    if (w->dtype == AETH_DTYPE_Q8_0) return aeth_q80_gemm_fuses(w, m, mode, d_a, norm_w);
+    return false;
+}
+
+bool aeth_gemm_swo_ok(const aeth_weight* w, int64_t m) {
+    if (!w) return false;
+    if (w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_swiglu_out(w, m);
+    return w->dtype == AETH_DTYPE_Q8_0 && (w->n & 1) == 0 && aeth_q80_gemm_rows(w, m);
+}
+
+int aeth_gemm_fused_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
+                           hipStream_t s, int64_t ldc, const GemmIn* in) {
+    if (w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc, nullptr, 0, in);
+    if (w->dtype == AETH_DTYPE_Q6_K) return aeth_gemm_q6k_launch(w, d_a, m, d_c, flags, s, ldc, in);
+    if (w->dtype == AETH_DTYPE_Q8_0) return aeth_gemm_q80_launch(w, d_a, m, d_c, flags, s, ldc, in);
+    return aeth_set_error(AETH_EINVAL, "gemm: no fused GEMM for dtype %d", w->dtype);
 }

@@ -152,10 +152,19 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
 // whole blocks (k = 32·nb) within the kernel's 32-bit buffer offsets, from 16 rows, or from 5
 // once m · (weight bytes) reaches 150 MB.
 bool aeth_q80_gemm_rows(const aeth_weight* w, int64_t m);
-// Q8_0 prefill GEMM (AETH_MM_ACCUMULATE and the Q8 activation blocks as aeth_gemm_q4k_launch);
-// requires aeth_q80_gemm_rows.
+// aeth_gemm_fuses for the Q8_0 GEMM (its prep is the Q4_K GEMM's).
+bool aeth_q80_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w);
+// Q8_0 prefill GEMM (AETH_MM_ACCUMULATE, the Q8 activation blocks, the fused producers and the
+// SwiGLU output as aeth_gemm_q4k_launch); requires aeth_q80_gemm_rows, and a producer in `in`
+// aeth_q80_gemm_fuses.
 int aeth_gemm_q80_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
-                         hipStream_t s, int64_t ldc = 0);
+                         hipStream_t s, int64_t ldc = 0, const GemmIn* in = nullptr);
+// The runner's view of the three GEMMs: whether weight w takes producer `mode` in a GEMM
+// (Q4_K, Q6_K, Q8_0), whether its GEMM writes the SwiGLU output (Q4_K, Q8_0), and the launch.
+bool aeth_gemm_fused_ok(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w);
+bool aeth_gemm_swo_ok(const aeth_weight* w, int64_t m);
+int aeth_gemm_fused_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
+                           hipStream_t s, int64_t ldc, const GemmIn* in);
 // Whether m activation rows against Q6_K weight w take the Q6_K GEMM (aeth_gemm_q6k.hip):
 // planar whole super-blocks within the kernel's 32-bit buffer offsets, once m · (weight
 // bytes) reaches 200 MB (the row-batched GEMV below).

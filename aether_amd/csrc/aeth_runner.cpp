@@ -311,7 +311,7 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
         float* lkv = r->kv + (int64_t)l * kv_layer_floats(c);
         const float* attn_norm = r->norms + (int64_t)l * 2 * d;
         const float* ffn_norm = attn_norm + d;
-        // Q4_K GEMMs take the RMSNorm inside their activation prep (the SwiGLU: below)
+        // the Q4_K, Q6_K and Q8_0 GEMMs take the RMSNorm inside their activation prep (the SwiGLU: below)
         GemmIn nin;
         nin.mode = PREP_RMSNORM;
         nin.eps = c.rms_norm_eps;
@@ -324,10 +324,8 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
             GemmIn pin = nin;  // after the first fused GEMM the stream's scratch holds the prep of x
             auto proj = [&](const aeth_weight* w, float* out) -> int {
                 int e;
-                if (aeth_gemm_fuses(w, n, PREP_RMSNORM, r->p_x, attn_norm)) {
-                    e = aeth_gemm_q4k_launch(w, r->p_x, n, out, 0, s, ld, nullptr, 0, &pin);
-                } else if (w->dtype == AETH_DTYPE_Q6_K && aeth_q6k_gemm_fuses(w, n, PREP_RMSNORM, r->p_x, attn_norm)) {
-                    e = aeth_gemm_q6k_launch(w, r->p_x, n, out, 0, s, ld, &pin);
+                if (aeth_gemm_fused_ok(w, n, PREP_RMSNORM, r->p_x, attn_norm)) {
+                    e = aeth_gemm_fused_launch(w, r->p_x, n, out, 0, s, ld, &pin);
                 } else {
                     if (!normed) {
                         if ((e = aeth_rmsnorm_launch(r->p_x, attn_norm, n, d, c.rms_norm_eps, r->p_n, s))) return e;
@@ -355,25 +353,25 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
         const float* h = r->p_h;
         GemmIn din;  // the down GEMM's producer
         if (r->wgu[l]) {
-            // a Q4_K gate|up GEMM writes h = g·σ(g)·u from its epilogue (n·d_ff floats instead of the
+            // a Q4_K or Q8_0 gate|up GEMM writes h = g·σ(g)·u from its epilogue (n·d_ff floats instead of the
             // 2·n·d_ff pairs); otherwise the pairs go to p_gu and the down GEMM's prep (or
             // k_silu_pairs) gates them
             GemmIn gin = nin;
             gin.norm_w = ffn_norm;
-            gin.swiglu_out = aeth_gemm_swiglu_out(r->wgu[l], n);
+            gin.swiglu_out = aeth_gemm_swo_ok(r->wgu[l], n);
             float* gu = gin.swiglu_out ? r->p_h : r->p_gu;
-            if (aeth_gemm_fuses(r->wgu[l], n, PREP_RMSNORM, r->p_x, ffn_norm)) {
-                if ((rc = aeth_gemm_q4k_launch(r->wgu[l], r->p_x, n, gu, 0, s, 0, nullptr, 0, &gin))) return rc;
+            if (aeth_gemm_fused_ok(r->wgu[l], n, PREP_RMSNORM, r->p_x, ffn_norm)) {
+                if ((rc = aeth_gemm_fused_launch(r->wgu[l], r->p_x, n, gu, 0, s, 0, &gin))) return rc;
             } else {
                 if ((rc = aeth_rmsnorm_launch(r->p_x, ffn_norm, n, d, c.rms_norm_eps, r->p_n, s))) return rc;
                 gin.mode = PREP_PLAIN;
-                rc = gin.swiglu_out ? aeth_gemm_q4k_launch(r->wgu[l], r->p_n, n, gu, 0, s, 0, nullptr, 0, &gin)
+                rc = gin.swiglu_out ? aeth_gemm_fused_launch(r->wgu[l], r->p_n, n, gu, 0, s, 0, &gin)
                                     : aeth_qmatmul(r->wgu[l], r->p_n, n, gu, 0, s);
                 if (rc) return rc;
             }
             if (gin.swiglu_out) {
                 h = r->p_h;
-            } else if (aeth_gemm_fuses(r->wdown[l], n, PREP_SWIGLU, r->p_gu, nullptr)) {  // in the down prep
+            } else if (aeth_gemm_fused_ok(r->wdown[l], n, PREP_SWIGLU, r->p_gu, nullptr)) {  // in the down prep
                 din.mode = PREP_SWIGLU;
                 h = r->p_gu;
             } else if ((rc = aeth_silu_pairs_launch(r->p_gu, n * dff, r->p_h, s))) {
@@ -387,9 +385,8 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
                 return rc;
             h = r->p_gu;
         }
-        rc = din.mode == PREP_SWIGLU
-                 ? aeth_gemm_q4k_launch(r->wdown[l], h, n, r->p_x, AETH_MM_ACCUMULATE, s, 0, nullptr, 0, &din)
-                 : aeth_qmatmul(r->wdown[l], h, n, r->p_x, AETH_MM_ACCUMULATE, s);
+        rc = din.mode == PREP_SWIGLU ? aeth_gemm_fused_launch(r->wdown[l], h, n, r->p_x, AETH_MM_ACCUMULATE, s, 0, &din)
+                                     : aeth_qmatmul(r->wdown[l], h, n, r->p_x, AETH_MM_ACCUMULATE, s);
         if (rc) return rc;
     }
     // head on the last row; the state update then leaves pos = fill = n
