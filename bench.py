@@ -217,15 +217,15 @@ def bench_decode(torch, A, n_tokens=128, prefilled=2048, prefill_tokens=512, wan
             "cpu_model": cpu_model}
 
 
-def bench_q4_k_m(torch, A, n_tokens=64, prefilled=2048, prefill_tokens=512):
+def bench_q4_k_m(torch, A, n_tokens=64, prefilled=2048, prefill_tokens=512, layer_dtypes=(12, 12, 14, 12, 12, 12, 14),
+                 mix="Q4_K_M: attn_v, ffn_down Q6_K; q, k, o, gate, up Q4_K; LM head Q6_K"):
     """bench_decode's model with llama.cpp's Q4_K_M mix: attn_v and ffn_down in Q6_K, the
-    other five layer weights Q4_K. Those layers run q / k / v and gate / up as separate
-    products (no fused q|k|v or gate|up weight), and in prefill the Q6_K projections take
-    the Q6_K GEMM."""
+    other five layer weights Q4_K (q|k one weight, v another; in prefill the Q6_K projections
+    take the Q6_K GEMM), or another per-layer mix (`layer_dtypes`: q k v o gate up down)."""
     L = A.lib()
     cfg = A.LlamaConfig(vocab_size=128256, d_model=4096, num_layers=32, num_heads=32, num_kv_heads=8, head_dim=128,
                         d_ff=14336, max_seq_len=4096, rope_base=500000.0, rms_norm_eps=1e-5)
-    dt = (ctypes.c_int32 * (32 * 7))(*([12, 12, 14, 12, 12, 12, 14] * 32))
+    dt = (ctypes.c_int32 * (32 * 7))(*(list(layer_dtypes) * 32))
     r = ctypes.c_void_p()
     A.check(L.aeth_runner_create(ctypes.byref(cfg), None, dt, None, None, None, 14, None, 0x8B8B8B,
                                  ctypes.byref(r)), "runner_create")
@@ -249,8 +249,7 @@ def bench_q4_k_m(torch, A, n_tokens=64, prefilled=2048, prefill_tokens=512):
     return {"decode_tok_s": round(n_tokens / dt_s, 1), "ms_per_token": round(dt_s * 1e3 / n_tokens, 4),
             "prefill_tok_s": round(prefill_tokens / pf_s, 1), "prefill_ms": round(pf_s * 1e3, 3),
             "prefill_TFLOP/s": round(pf_flops / pf_s / 1e12, 1), "prefill_tokens": prefill_tokens,
-            "decode_tokens": n_tokens, "prefilled": prefilled,
-            "mix": "Q4_K_M: attn_v, ffn_down Q6_K; q, k, o, gate, up Q4_K; LM head Q6_K"}
+            "decode_tokens": n_tokens, "prefilled": prefilled, "mix": mix}
 
 
 def bench_decode_eager(torch, A, n_tokens=128, prefilled=2048):
@@ -464,10 +463,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,gemm_q80,decode,q4_k_m",
+    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,gemm_q80,decode,q4_k_m,q8_0_model",
                     help="comma-separated extra sections to run: floor, q8, q6, q5, dotprod, gemm, gemm_q8, gemm_q6k, "
                          "gemm_q80, "
-                         "decode, q4_k_m (default), f16, q2k (GGUF-order formats), decode_eager (the decode step "
+                         "decode, q4_k_m, q8_0_model (default), f16, q2k (GGUF-order formats), decode_eager (the decode step "
                          "without its HIP graph; these three not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -607,6 +606,10 @@ def main():
     if "q4_k_m" in sections:
         extra["q4_k_m_decode_prefill_8b"] = bench_q4_k_m(torch, A)
         print("[bench] Q4_K_M 8B: %s" % extra["q4_k_m_decode_prefill_8b"], file=sys.stderr, flush=True)
+    if "q8_0_model" in sections:  # every layer weight Q8_0 (prefill on the Q8_0 GEMM, decode on the Q8_0 GEMV)
+        extra["q8_0_decode_prefill_8b"] = bench_q4_k_m(torch, A, layer_dtypes=(8,) * 7,
+                                                       mix="Q8_0 layer weights; LM head Q6_K")
+        print("[bench] Q8_0 8B: %s" % extra["q8_0_decode_prefill_8b"], file=sys.stderr, flush=True)
     if "decode" in sections:
         d = bench_decode(torch, A, want_cpu=want_cpu)
         cpu_in["dec"] = d.pop("cpu_model")
