@@ -164,21 +164,18 @@ __global__ void __launch_bounds__(64 * K0_W) k_gemm_q80_kq(Q80Args G) {
                 }
             }
             // operands q as exact halves, k-order [0, 2, 1, 3] per 4 (bytes (0, 2) and (1, 3) of each
-            // dword, as the prep orders A): q + 128 as 0x64 | byte is the half 1152 + q
+            // dword, as the prep orders A): q + 128 as 0x64 | byte is the half 1152 + q; a zero-d block's
+            // quants are masked to 0 first (byte 0x80 after the flip, the half 0)
             auto build = [&](int c, half8_t& bq) {
-                half2_t x[4];
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
-                    const uint32_t w = qw[c][e] ^ 0x80808080u;
-                    x[2 * e] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(c64, w, 0x04020400u)) + k1152;
-                    x[2 * e + 1] = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(c64, w, 0x04030401u)) + k1152;
-                }
-                const half2_t zero = {(_Float16)0.0f, (_Float16)0.0f};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const half2_t y = zm[c] ? zero : x[i];
-                    bq[2 * i] = y[0];
-                    bq[2 * i + 1] = y[1];
+                    const uint32_t w = (qw[c][e] & ~zm[c]) ^ 0x80808080u;
+                    const half2_t x0 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(c64, w, 0x04020400u)) + k1152;
+                    const half2_t x1 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(c64, w, 0x04030401u)) + k1152;
+                    bq[4 * e] = x0[0];
+                    bq[4 * e + 1] = x0[1];
+                    bq[4 * e + 2] = x1[0];
+                    bq[4 * e + 3] = x1[1];
                 }
             };
             half8_t bq[4];
@@ -201,7 +198,7 @@ __global__ void __launch_bounds__(64 * K0_W) k_gemm_q80_kq(Q80Args G) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
                 }
             }
         }
