@@ -33,7 +33,11 @@ class LlamaConfig(ctypes.Structure):
     _fields_ = [("vocab_size", ctypes.c_int32), ("d_model", ctypes.c_int32), ("num_layers", ctypes.c_int32),
                 ("num_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
                 ("d_ff", ctypes.c_int32), ("max_seq_len", ctypes.c_int32), ("rope_base", ctypes.c_float),
-                ("rms_norm_eps", ctypes.c_float)]
+                ("rms_norm_eps", ctypes.c_float), ("sliding_window", ctypes.c_int32), ("flags", ctypes.c_int32)]
+
+
+CFG_FULL_CONTEXT = 1  # aeth_llama_config.flags: keep max_seq_len past 4096 (up to 8192)
+RUNNER_MAX_SEQ = 4096  # the cache length cap of LlamaRunner::new (runner.rs:225)
 
 
 _lib = None
@@ -76,6 +80,7 @@ _SIGS = {
     "aeth_weight_cache_clear": (_INT, []),
     "aeth_weight_cache_set_limit": (_INT, [_I64]),
     "aeth_weight_cache_bytes": (_I64, []),
+    "aeth_weight_fingerprint": (_INT, [_P, _I64, _P]),
     "aeth_backend_rms_norm": (_INT, [_P, _P, _I64, _I64, ctypes.c_float, _P]),
     "aeth_backend_causal_attention": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_float, _P]),
     "aeth_causal_attention": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_float, _P, _P]),

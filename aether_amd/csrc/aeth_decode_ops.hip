@@ -149,6 +149,9 @@ int aeth_kv_append_launch(float* layer_kv, const float* k, const float* v, int64
 // rotated here with the table row min(pos, max_seq-1), and the new token is
 // position `fill` (the cache fill before this step; seq = fill + 1). The
 // chunk holding it reads k/v from registers and stores them in the cache.
+// A sliding window w (attn_direct's sliding_window, runner.rs:1768-1777)
+// masks the positions before seq - w: chunks wholly before it return at
+// once, and the merge leaves them out.
 #define ATTN_T 64
 #define ATTN_MAX_GROUPS 8
 #define ATTN_MAX_CHUNKS 128  // max_seq <= 8192
@@ -166,6 +169,7 @@ struct AttnArgs {
     int64_t seq_host;    // seq when st == nullptr
     int n_heads, kv_heads, head_dim;
     int64_t max_seq;
+    int64_t window;      // sliding window (0: none)
     float* ws;           // [n_heads][max_chunks][hd + 2]
     int max_chunks;
     float* out;          // [n_heads][hd]
@@ -204,7 +208,8 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
     }
     if (seq > A.max_seq) seq = A.max_seq;
     const int64_t t0 = (int64_t)chunk * ATTN_T;
-    if (t0 >= seq) return;
+    const int64_t wstart = A.window > 0 && seq > A.window ? seq - A.window : 0;  // first visible position
+    if (t0 >= seq || t0 + ATTN_T <= wstart) return;
     const int nt = (int)min((int64_t)ATTN_T, seq - t0);
     const int64_t hs = A.max_seq * HD;
     float* K = A.layer_kv + (int64_t)kvh * hs;
@@ -292,7 +297,7 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
             a += aeth_dpp_xor2f(a);
             a += aeth_dpp_mirror8f(a);
             if (LP == 16) a += aeth_dpp_mirror16f(a);
-            if (qe == 0) sc[g][sp] = sp < nt ? a * scale : -INFINITY;
+            if (qe == 0) sc[g][sp] = sp < nt && t0 + sp >= wstart ? a * scale : -INFINITY;
         }
     }
     __syncthreads();
@@ -372,9 +377,10 @@ __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
     int64_t seq = A.st ? (int64_t)A.st[2] + 1 : A.seq_host;
     if (seq > A.max_seq) seq = A.max_seq;
     const int nch = (int)((seq + ATTN_T - 1) / ATTN_T);
+    const int c_lo = A.window > 0 && seq > A.window ? (int)((seq - A.window) / ATTN_T) : 0;  // chunks before: none
     const float* base = A.ws + (int64_t)h * A.max_chunks * (HD + 2);
     float mc = -INFINITY, lc = 0.0f;
-    if (tid < nch) {
+    if (tid >= c_lo && tid < nch) {
         mc = base[(int64_t)tid * (HD + 2) + HD];
         lc = base[(int64_t)tid * (HD + 2) + HD + 1];
     }
@@ -387,7 +393,7 @@ __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
     M = red[0][0];
 #pragma unroll
     for (int w = 1; w < HD / 64; w++) M = fmaxf(M, red[w][0]);
-    const float wgt = tid < nch ? expf(mc - M) : 0.0f;
+    const float wgt = tid >= c_lo && tid < nch ? expf(mc - M) : 0.0f;
     float L = aeth_wave_sum(wgt * lc);
     if (lane == 0) red[wave][1] = L;
     if (tid < nch) cw[tid] = wgt;
@@ -403,7 +409,7 @@ __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
         }
 #pragma unroll
         for (int j = 0; j < CB; j++)
-            if (c0 + j < nch) acc += cw[c0 + j] * v[j];
+            if (c0 + j >= c_lo && c0 + j < nch) acc += cw[c0 + j] * v[j];
     }
     A.out[(int64_t)h * HD + tid] = acc / L;
 }
@@ -415,7 +421,7 @@ int64_t aeth_attn_ws_floats(int64_t n_heads, int64_t head_dim, int64_t max_seq) 
 // ws: aeth_attn_ws_floats(...) floats of chunk partials.
 int aeth_attn_launch(const float* q, const float* qkv, float* layer_kv, const float* sin_t, const float* cos_t,
                      const int* d_st, int64_t seq, int64_t n_heads, int64_t kv_heads, int64_t head_dim,
-                     int64_t max_seq, float* ws, float* out, hipStream_t s) {
+                     int64_t max_seq, int64_t window, float* ws, float* out, hipStream_t s) {
     if (kv_heads <= 0 || n_heads % kv_heads != 0 || n_heads / kv_heads > ATTN_MAX_GROUPS || head_dim != 128 ||
         kv_heads > 64 || aeth_cdiv(max_seq, ATTN_T) > ATTN_MAX_CHUNKS)
         return aeth_set_error(AETH_EUNSUPPORTED, "attn: unsupported heads=%lld kv_heads=%lld head_dim=%lld max_seq=%lld",
@@ -432,6 +438,7 @@ int aeth_attn_launch(const float* q, const float* qkv, float* layer_kv, const fl
     A.kv_heads = (int)kv_heads;
     A.head_dim = (int)head_dim;
     A.max_seq = max_seq;
+    A.window = window > 0 ? window : 0;
     A.max_chunks = (int)aeth_cdiv(max_seq, ATTN_T);
     A.ws = ws;
     A.out = out;

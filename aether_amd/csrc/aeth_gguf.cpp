@@ -15,6 +15,7 @@
 #include <string.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -387,10 +388,15 @@ int aeth_gguf_load_runner(const char* path, aeth_runner** out, int* bos, int* eo
     if (meta_usize(g, key("rope.dimension_count"), &rope_dim) && rope_dim != hd)
         return aeth_set_error(AETH_EUNSUPPORTED, "partial RoPE (rope.dimension_count %lld of head_dim %lld) is not built",
                               (long long)rope_dim, (long long)hd);
-    if (meta_usize(g, key("attention.sliding_window_length"), &sw))
-        return aeth_set_error(AETH_EUNSUPPORTED, "sliding-window attention is not built");
-    // the device attention handles caches of up to 8192 positions
-    const int64_t max_seq = ctx < 1 ? 2048 : (ctx > 8192 ? 8192 : ctx);
+    // ArchConfig::sliding_window (model_loader.rs:286): None when the key is absent
+    const bool has_sw = meta_usize(g, key("attention.sliding_window_length"), &sw);
+    if (has_sw && sw < 1)  // attn_direct would mask every position (NaN logits); refused instead
+        return aeth_set_error(AETH_EUNSUPPORTED, "attention.sliding_window_length %lld masks every position",
+                              (long long)sw);
+    if (ctx < 1) return aeth_set_error(AETH_EINVAL, "GGUF config: context_length %lld", (long long)ctx);
+    // LlamaConfig::max_seq_len = context_length (default 2048, model_loader.rs:280); the runner then
+    // holds min(max_seq_len, 4096) positions (runner.rs:225, :339)
+    const int64_t max_seq = ctx > INT32_MAX ? INT32_MAX : ctx;
     int64_t bv = 1, ev = 2;
     meta_usize(g, "tokenizer.ggml.bos_token_id", &bv);
     meta_usize(g, "tokenizer.ggml.eos_token_id", &ev);
@@ -398,7 +404,8 @@ int aeth_gguf_load_runner(const char* path, aeth_runner** out, int* bos, int* eo
     if (eos) *eos = (int)ev;
 
     aeth_llama_config cfg{(int32_t)vocab, (int32_t)d, (int32_t)nl, (int32_t)nh, (int32_t)nkv, (int32_t)hd,
-                          (int32_t)dff, (int32_t)max_seq, rope_base, eps};
+                          (int32_t)dff, (int32_t)max_seq, rope_base, eps,
+                          has_sw ? (int32_t)std::min<int64_t>(sw, INT32_MAX) : 0, 0};
     Staging st;
     AETH_HIP_CHECK(hipStreamCreate(&st.s));
     // token embeddings: [d_model][vocab] as the reference reads them → [vocab][d_model] (model_loader.rs:174-188)

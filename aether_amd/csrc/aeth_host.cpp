@@ -7,6 +7,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
+#include <condition_variable>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -151,7 +153,7 @@ extern "C" AETH_API int aeth_attn_decode(const float* d_q, const float* d_layer_
                                  sizeof(float) * aeth_attn_ws_floats(n_heads, head_dim, max_seq), &ws);
     if (rc) return rc;
     return aeth_attn_launch(d_q, nullptr, (float*)d_layer_kv, nullptr, nullptr, nullptr, seq, n_heads, kv_heads,
-                            head_dim, max_seq, (float*)ws, d_out, (hipStream_t)stream);
+                            head_dim, max_seq, 0, (float*)ws, d_out, (hipStream_t)stream);
 }
 
 // ── decode attention without allocation ───────────────────────────────────
@@ -203,7 +205,7 @@ extern "C" AETH_API int aeth_attn_decode_noalloc(const float* d_q, const float* 
     int rc = aeth_noalloc_setup(dev);
     if (rc) return rc;
     return aeth_attn_launch(d_q, nullptr, (float*)d_layer_kv, nullptr, nullptr, nullptr, seq, n_heads, kv_heads,
-                            head_dim, max_seq, g_noalloc_ptr[dev], d_out, (hipStream_t)stream);
+                            head_dim, max_seq, 0, g_noalloc_ptr[dev], d_out, (hipStream_t)stream);
 }
 
 extern "C" AETH_API int aeth_attn_prefill(const float* d_q, int64_t q_stride, const float* d_layer_kv, int64_t n,
@@ -213,7 +215,7 @@ extern "C" AETH_API int aeth_attn_prefill(const float* d_q, int64_t q_stride, co
         n_heads % kv_heads != 0 || q_stride < n_heads * head_dim || (q_stride & 3))
         return aeth_set_error(AETH_EINVAL, "aeth_attn_prefill: bad argument (n %lld, max_seq %lld)", (long long)n,
                               (long long)max_seq);
-    return aeth_attn_prefill_launch(d_q, q_stride, d_layer_kv, n, n_heads, kv_heads, head_dim, max_seq, d_out,
+    return aeth_attn_prefill_launch(d_q, q_stride, d_layer_kv, n, n_heads, kv_heads, head_dim, max_seq, 0, d_out,
                                     (hipStream_t)stream);
 }
 
@@ -249,8 +251,9 @@ using WKey = std::tuple<const void*, int64_t, int, int64_t, int64_t, int, int>; 
 
 // Content fingerprint: four multiply-rotate lanes over 32-byte steps (a
 // 64-bit mix in the style of the xxHash family), the tail byte-wise, then the
-// length. Buffers past 8 MiB are split into 1 MiB chunks hashed by up to 8
-// host threads and the chunk digests folded in order.
+// length. Buffers past 8 MiB are split into 1 MiB chunks hashed by a
+// persistent pool of host threads (the caller and up to 7 workers, started
+// once) and the chunk digests folded in order.
 inline uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
 const uint64_t kP1 = 0x9E3779B185EBCA87ull, kP2 = 0xC2B2AE3D27D4EB4Full, kP3 = 0x165667B19E3779F9ull;
 
@@ -273,18 +276,77 @@ uint64_t fp_chunk(const uint8_t* p, size_t n, uint64_t seed) {
     return h ^ (h >> 32);
 }
 
+// Workers that hash the chunks of one buffer at a time: a job is published
+// under the pool lock with a generation number, chunks are claimed through an
+// atomic counter (the caller claims too), and the caller waits until every
+// worker has left the job. The pool lives for the process (never destroyed,
+// so no thread is joined during static destruction); one job at a time.
+class HashPool {
+  public:
+    static HashPool& get() {
+        static HashPool* pool = new HashPool();
+        return *pool;
+    }
+    void run(const uint8_t* p, size_t n, size_t chunk, uint64_t* d) {
+        std::lock_guard<std::mutex> job(job_mu_);
+        const size_t nc = (n + chunk - 1) / chunk;
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            p_ = p;
+            n_ = n;
+            chunk_ = chunk;
+            d_ = d;
+            nc_ = nc;
+            next_.store(0);
+            busy_ = (int)workers_.size();
+            gen_++;
+        }
+        cv_.notify_all();
+        work();
+        std::unique_lock<std::mutex> lk(mu_);
+        done_cv_.wait(lk, [&] { return busy_ == 0; });
+    }
+
+  private:
+    HashPool() {
+        const unsigned hc = std::thread::hardware_concurrency();
+        const unsigned nw = std::min(7u, hc > 1 ? hc - 1 : 0u);
+        for (unsigned i = 0; i < nw; i++) workers_.emplace_back([this] { loop(); });
+    }
+    void work() {
+        for (size_t c; (c = next_.fetch_add(1)) < nc_;)
+            d_[c] = fp_chunk(p_ + c * chunk_, std::min(chunk_, n_ - c * chunk_), c);
+    }
+    void loop() {
+        uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return gen_ != seen; });
+                seen = gen_;
+            }
+            work();
+            std::lock_guard<std::mutex> lk(mu_);
+            if (--busy_ == 0) done_cv_.notify_one();
+        }
+    }
+    std::mutex job_mu_, mu_;
+    std::condition_variable cv_, done_cv_;
+    std::vector<std::thread> workers_;
+    const uint8_t* p_ = nullptr;
+    size_t n_ = 0, chunk_ = 1, nc_ = 0;
+    uint64_t* d_ = nullptr;
+    std::atomic<size_t> next_{0};
+    int busy_ = 0;
+    uint64_t gen_ = 0;
+};
+
 uint64_t fingerprint(const uint8_t* p, size_t n) {
     const size_t chunk = 1 << 20;
     if (n <= ((size_t)8 << 20)) return fp_chunk(p, n, 0);
     const size_t nc = (n + chunk - 1) / chunk;
     std::vector<uint64_t> d(nc);
-    const unsigned nt = (unsigned)std::min<size_t>(8, nc);
-    std::vector<std::thread> th;
-    for (unsigned t = 0; t < nt; t++)
-        th.emplace_back([&, t] {
-            for (size_t c = t; c < nc; c += nt) d[c] = fp_chunk(p + c * chunk, std::min(chunk, n - c * chunk), c);
-        });
-    for (auto& x : th) x.join();
+    HashPool::get().run(p, n, chunk, d.data());
     return fp_chunk((const uint8_t*)d.data(), nc * 8, (uint64_t)n);
 }
 
@@ -427,6 +489,12 @@ int host_matmul(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len, 
     return aeth_guard("matmul", [&] { return host_matmul_impl(a, m, b_raw, b_len, n, k, dtype, c, order, flags); });
 }
 }  // namespace
+
+extern "C" AETH_API int aeth_weight_fingerprint(const void* host, int64_t bytes, uint64_t* out) {
+    if (!host || bytes < 0 || !out) return aeth_set_error(AETH_EINVAL, "aeth_weight_fingerprint: bad argument");
+    *out = fingerprint((const uint8_t*)host, (size_t)bytes);
+    return AETH_OK;
+}
 
 extern "C" AETH_API int aeth_weight_cache_clear(void) {
     std::lock_guard<std::mutex> lk(g_wc_mu);

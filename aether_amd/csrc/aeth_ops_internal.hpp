@@ -15,9 +15,10 @@ int64_t aeth_attn_ws_floats(int64_t n_heads, int64_t head_dim, int64_t max_seq);
 // Decode attention over one layer slice of the cache. Either q (rotated, with
 // seq given) or qkv (fused projection output: RoPE of q/k and the KV append
 // of the new token happen here, scalars from d_st = {token, pos, fill}).
+// window > 0: sliding-window attention over the last `window` positions.
 int aeth_attn_launch(const float* q, const float* qkv, float* layer_kv, const float* sin_t, const float* cos_t,
                      const int* d_st, int64_t seq, int64_t n_heads, int64_t kv_heads, int64_t head_dim,
-                     int64_t max_seq, float* ws, float* out, hipStream_t s);
+                     int64_t max_seq, int64_t window, float* ws, float* out, hipStream_t s);
 int aeth_silu_mul_launch(float* g, const float* up, int64_t n, hipStream_t s);
 int aeth_add_launch(float* x, const float* y, int64_t n, hipStream_t s);
 int64_t aeth_argmax_ws_bytes();
@@ -31,7 +32,8 @@ int aeth_state_advance_launch(int* st, unsigned long long* amax, int* hist, int6
 int aeth_embed_rows_launch(const float* table, const int* d_tokens, int64_t n, int64_t d, float* x, hipStream_t s);
 int aeth_prefill_rope_kv_launch(float* qkv, int64_t n, int64_t nh, int64_t nkv, int64_t hd, const float* sin_t,
                                 const float* cos_t, int64_t max_seq, float* layer_kv, hipStream_t s);
-// q rows of q_stride floats (the fused projection: (nh + 2·nkv)·hd), head h at column h·hd
+// q rows of q_stride floats (the fused projection: (nh + 2·nkv)·hd), head h at column h·hd;
+// window > 0: query i sees keys max(0, i - window + 1) ..= i
 int aeth_attn_prefill_launch(const float* q, int64_t q_stride, const float* layer_kv, int64_t n, int64_t nh,
-                             int64_t nkv, int64_t hd, int64_t max_seq, float* out, hipStream_t s);
+                             int64_t nkv, int64_t hd, int64_t max_seq, int64_t window, float* out, hipStream_t s);
 int aeth_silu_pairs_launch(const float* gu, int64_t total, float* h, hipStream_t s);

@@ -13,6 +13,7 @@
 //    not take;
 //  * k_silu_pairs: h = g·σ(g)·u on the interleaved gate/up GEMM output
 //    (runner.rs:1617-1625 form).
+#include <limits.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -141,11 +142,12 @@ int aeth_prefill_rope_kv_launch(float* qkv, int64_t n, int64_t nh, int64_t nkv, 
 #define PA_BK 64
 
 // Causal attention of queries [64·blockIdx.x, +64) of head blockIdx.y over keys
-// 0..i of the layer cache (slots written by k_prefill_rope_kv).
+// 0..i of the layer cache (slots written by k_prefill_rope_kv); with a sliding
+// window w > 0, keys i - w + 1 ..= i (attention_batch, runner.rs:1825-1845).
 template <int HD>
 __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ qkv, int64_t qkv_stride,
                                                       const float* __restrict__ layer_kv, int n, int nh, int nkv,
-                                                      int64_t max_seq, float* __restrict__ out) {
+                                                      int64_t max_seq, int window, float* __restrict__ out) {
     constexpr int LD = HD + 4;  // row stride (floats): 16-byte aligned rows
     extern __shared__ __attribute__((aligned(16))) float sm[];
     float* Qs = sm;
@@ -179,7 +181,8 @@ __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ 
 #pragma unroll
         for (int e = 0; e < 8; e++) o[a][e] = 0.0f;
     const int nkb = (min(q0 + PA_BQ, n) - 1) / PA_BK + 1;
-    for (int kb = 0; kb < nkb; kb++) {
+    const int kb0 = window > 0 ? max(0, q0 - window + 1) / PA_BK : 0;  // blocks before every query's window: none
+    for (int kb = kb0; kb < nkb; kb++) {
         const int k0 = kb * PA_BK;
         __syncthreads();  // the previous block's K/V/P are no longer read
         for (int idx = tid; idx < PA_BK * HD / 4; idx += 256) {
@@ -211,7 +214,8 @@ __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ 
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 const int qi = q0 + 4 * qq + a, kj = k0 + 4 * kq + b;
-                Ps[(4 * qq + a) * (PA_BK + 1) + 4 * kq + b] = (kj <= qi && kj < n) ? sacc[a][b] * scale : -INFINITY;
+                Ps[(4 * qq + a) * (PA_BK + 1) + 4 * kq + b] =
+                    (kj <= qi && kj < n && (window <= 0 || kj > qi - window)) ? sacc[a][b] * scale : -INFINITY;
             }
         __syncthreads();
         {  // online softmax: 4 threads per query row, 16 keys each
@@ -290,7 +294,10 @@ __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ 
 // the result o / l does not depend on which max is used). K and V are read as
 // buffers of the n filled rows, so the loads of rows ≥ n (the last block's
 // tail) return zeros; those keys are masked. Two register sets alternate, the
-// next block's loads in flight during the current block.
+// next block's loads in flight during the current block. With a sliding window
+// w > 0 (attention_batch, runner.rs:1825-1845) query i sees keys i - w + 1 ..= i:
+// the waves start at the first key block some query of the block sees, and the
+// keys before a query's window are masked like those past it.
 // Max / sum of a value over the lane pairs (l, l ^ 16) and (l, l ^ 32): v_permlane16_swap and
 // v_permlane32_swap with the same register as both operands leave each lane of a pair the
 // lower lane's value in the first result and the upper lane's in the second (register moves,
@@ -320,7 +327,7 @@ __device__ __forceinline__ float4 pa_ld4(__amdgpu_buffer_rsrc_t r, int off) {
 template <int G>
 __global__ void __launch_bounds__(256, 2) k_attn_prefill_mf(const float* __restrict__ qkv, int64_t qkv_stride,
                                                          const float* __restrict__ layer_kv, int n, int nh, int nkv,
-                                                         int64_t max_seq, float* __restrict__ out) {
+                                                         int64_t max_seq, int window, float* __restrict__ out) {
     constexpr int QB = 16 / G, HD = 128, PLD = HD + 4;
     constexpr float TH = 8.0f;  // log2 units a running max may grow before the partials are rescaled
     __shared__ __attribute__((aligned(16))) float po[4][16][PLD];  // per wave: column c, d
@@ -349,6 +356,9 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_mf(const float* __restr
             }
         }
         const int kb_end = (min(q0 + QB, n) - 1) / 16;  // last key block, inclusive
+        const int kb_beg = window > 0 ? max(0, q0 - window + 1) / 16 : 0;  // first key block any query sees
+        // keys t with t > query - window are visible: t ≥ lo_all for every query of the block
+        const int lo_all = window > 0 ? q0 + QB - window : INT_MIN;
         // loads of one key block: K rows t0 + c (A of Sᵀ), V rows t0 + 4·grp + j,
         // floats [8c, 8c + 8) (A of Oᵀ)
         auto load = [&](int kb, float4* kk, float4 (*vv)[2]) {
@@ -379,14 +389,14 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_mf(const float* __restr
                 s4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[i].w, qv[4 * i + 3], s4[3], 0, 0, 0);
             }
             f32x4 s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-            if (t0 + 15 <= q0 && t0 + 15 < n) {  // no key of the block passes a query or n (uniform)
+            if (t0 + 15 <= q0 && t0 + 15 < n && t0 >= lo_all) {  // no key of the block is masked (uniform)
 #pragma unroll
                 for (int r = 0; r < 4; r++) s[r] *= sl2;
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int t = t0 + 4 * grp + r;
-                    s[r] = (t <= query && t < n) ? s[r] * sl2 : -INFINITY;
+                    s[r] = (t <= query && t < n && (window <= 0 || t > query - window)) ? s[r] * sl2 : -INFINITY;
                 }
             }
             float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
@@ -415,8 +425,8 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_mf(const float* __restr
             }
         };
         float4 ka[8], va[4][2], kn[8], vn[4][2];
-        if (w <= kb_end) load(w, ka, va);
-        for (int kb = w; kb <= kb_end; kb += 8) {  // two blocks per trip, the register sets alternating
+        if (kb_beg + w <= kb_end) load(kb_beg + w, ka, va);
+        for (int kb = kb_beg + w; kb <= kb_end; kb += 8) {  // two blocks per trip, the register sets alternating
             load(min(kb + 4, kb_end), kn, vn);
             step(kb, ka, va);
             if (kb + 4 > kb_end) break;
@@ -466,8 +476,9 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_mf(const float* __restr
 }
 
 int aeth_attn_prefill_launch(const float* qkv, int64_t stride, const float* layer_kv, int64_t n, int64_t nh,
-                             int64_t nkv, int64_t hd, int64_t max_seq, float* out, hipStream_t s) {
+                             int64_t nkv, int64_t hd, int64_t max_seq, int64_t window, float* out, hipStream_t s) {
     if (n <= 0) return AETH_OK;
+    const int win = window > 0 && window < n ? (int)window : 0;  // a window reaching back past key 0 masks nothing
     if (hd != 128 || nh % nkv != 0)
         return aeth_set_error(AETH_EUNSUPPORTED, "prefill attention: head_dim %lld (needs 128)", (long long)hd);
     // AETH_PREFILL_ATTN=valu selects the f32 VALU kernel (comparison, tests)
@@ -476,10 +487,10 @@ int aeth_attn_prefill_launch(const float* qkv, int64_t stride, const float* laye
     if (!force_valu && (G == 1 || G == 2 || G == 4 || G == 8)) {
         const int64_t nqb = aeth_cdiv(n, 16 / G);
         const dim3 grid((unsigned)(nkv * aeth_cdiv(nqb, 2)));
-        if (G == 1) hipLaunchKernelGGL(k_attn_prefill_mf<1>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
-        else if (G == 2) hipLaunchKernelGGL(k_attn_prefill_mf<2>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
-        else if (G == 4) hipLaunchKernelGGL(k_attn_prefill_mf<4>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
-        else hipLaunchKernelGGL(k_attn_prefill_mf<8>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
+        if (G == 1) hipLaunchKernelGGL(k_attn_prefill_mf<1>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, win, out);
+        else if (G == 2) hipLaunchKernelGGL(k_attn_prefill_mf<2>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, win, out);
+        else if (G == 4) hipLaunchKernelGGL(k_attn_prefill_mf<4>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, win, out);
+        else hipLaunchKernelGGL(k_attn_prefill_mf<8>, grid, dim3(256), 0, s, qkv, stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, win, out);
         AETH_LAUNCH_CHECK();
         return AETH_OK;
     }
@@ -491,7 +502,7 @@ int aeth_attn_prefill_launch(const float* qkv, int64_t stride, const float* laye
         opted = true;
     }
     hipLaunchKernelGGL(k_attn_prefill<128>, dim3((unsigned)aeth_cdiv(n, PA_BQ), (unsigned)nh), dim3(256), lds, s, qkv,
-                       stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, out);
+                       stride, layer_kv, (int)n, (int)nh, (int)nkv, max_seq, win, out);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }

@@ -216,7 +216,7 @@ int enqueue_layers(aeth_runner* r, int l0, int l1) {
                 return rc;
         }
         if ((rc = aeth_attn_launch(nullptr, r->qkv, lkv, r->rope_sin, r->rope_cos, r->st, 0, nh, nkv, hd,
-                                   c.max_seq_len, r->attn_ws, r->attn, s)))
+                                   c.max_seq_len, c.sliding_window, r->attn_ws, r->attn, s)))
             return rc;
         GemvEpi e2 = step_epi(r);
         e2.flags = AETH_MM_ACCUMULATE;
@@ -348,7 +348,9 @@ int runner_prefill_locked(aeth_runner* r, const int32_t* tokens, int32_t n, floa
         if ((rc = aeth_prefill_rope_kv_launch(r->p_qkv, n, nh, nkv, hd, r->rope_sin, r->rope_cos, c.max_seq_len,
                                               lkv, s)))
             return rc;
-        if ((rc = aeth_attn_prefill_launch(r->p_qkv, (nh + 2 * nkv) * hd, lkv, n, nh, nkv, hd, c.max_seq_len, r->p_att, s))) return rc;
+        if ((rc = aeth_attn_prefill_launch(r->p_qkv, (nh + 2 * nkv) * hd, lkv, n, nh, nkv, hd, c.max_seq_len,
+                                           c.sliding_window, r->p_att, s)))
+            return rc;
         if ((rc = aeth_qmatmul(r->wo[l], r->p_att, n, r->p_x, AETH_MM_ACCUMULATE, s))) return rc;
         const float* h = r->p_h;
         GemmIn din;  // the down GEMM's producer
@@ -435,7 +437,7 @@ int runner_create_impl(const aeth_llama_config* cfg, const void* const* layer_we
                        const float* embeddings, uint64_t seed, aeth_runner** out) {
     if (!cfg || !out || !layer_dtypes) return aeth_set_error(AETH_EINVAL, "aeth_runner_create: NULL argument");
     *out = nullptr;
-    const aeth_llama_config& c = *cfg;
+    aeth_llama_config c = *cfg;
     if (c.num_layers <= 0 || c.d_model <= 0 || c.num_heads <= 0 || c.num_kv_heads <= 0 || c.head_dim <= 0 ||
         c.d_ff <= 0 || c.vocab_size <= 0 || c.max_seq_len <= 0 || c.num_heads % c.num_kv_heads != 0 ||
         c.head_dim % 2 != 0)
@@ -443,6 +445,16 @@ int runner_create_impl(const aeth_llama_config* cfg, const void* const* layer_we
     if (c.head_dim != 128 || c.num_heads / c.num_kv_heads > 8)
         return aeth_set_error(AETH_EUNSUPPORTED, "aeth_runner_create: the attention kernel needs head_dim 128 and "
                                                  "at most 8 query heads per KV head");
+    if (c.sliding_window < 0 || (c.flags & ~AETH_CFG_FULL_CONTEXT))
+        return aeth_set_error(AETH_EINVAL, "aeth_runner_create: sliding_window %d / flags %d", c.sliding_window, c.flags);
+    // LlamaRunner::new and new_streaming size the cache and the RoPE table at
+    // min(max_seq_len, 4096) (runner.rs:225, :339); a longer cache is an opt-in
+    const int32_t eff_seq = (c.flags & AETH_CFG_FULL_CONTEXT) ? c.max_seq_len
+                                                             : std::min<int32_t>(c.max_seq_len, AETH_RUNNER_MAX_SEQ);
+    if (eff_seq > 8192)
+        return aeth_set_error(AETH_EUNSUPPORTED, "aeth_runner_create: a cache of %d positions (the decode attention "
+                                                 "holds up to 8192)", eff_seq);
+    c.max_seq_len = eff_seq;
     bool need_seed = !lm_head || !embeddings || !final_norm || !layer_weights || !norms;
     if (need_seed && seed == 0)
         return aeth_set_error(AETH_EINVAL, "aeth_runner_create: missing tensors need a nonzero synthetic_seed");

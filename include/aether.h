@@ -10,8 +10,10 @@
  *     weights F32 / F16 / Q8_0 / Q2_K..Q6_K (any mix across tensors, as in
  *     Q4_K_M / Q5_K_M / Q3_K_M files; F32 / F16 / Q2_K / Q3_K need
  *     out_features % 4 == 0), norms F32 / F16, head_dim 128, at most 8 query heads per KV
- *     head, no sliding window or partial RoPE, and a cache of
- *     min(context_length, 8192) positions. max_hot is ignored: every layer
+ *     head, no partial RoPE; attention.sliding_window_length is honoured
+ *     (ArchConfig::sliding_window) and the cache holds min(context_length,
+ *     4096) positions, as LlamaRunner::new sizes it (runner.rs:225), and
+ *     aether_context_len reports that. max_hot is ignored: every layer
  *     stays in HBM. Other files return NULL with the reason in
  *     aether_last_error. Models can also be created with
  *     aeth_runner_create (aether_hip.h) and wrapped by

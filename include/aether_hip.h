@@ -122,16 +122,27 @@ AETH_API int aeth_load_quant(int dtype, const void* d_src, int64_t k, int64_t n,
 
 /* C[m×n] = A[m×k] · Wᵀ on the device — QuantKernel::matmul
  * (src/quant/matmul/registry.rs:7-19) / quantized_matmul_impl
- * (src/quant/matmul/dispatch.rs:98-135) with device operands. m == 1 runs the
- * decode GEMV; m > 1 runs the prefill GEMM (Q4_K: fp16-split MFMA; other
- * fused formats: row-batched GEMV). F32 / F16 / Q2_K / Q3_K weights take the
- * GGUF-order kernel of matmul_f32_gguf (dispatch.rs:541-574). The Q4_K GEMM
- * and the GGUF-order kernel use a scratch buffer the library keeps per
- * (device, stream): calls on different streams never share it, calls on one
- * stream run in order. It grows on first use of a larger shape (a grow waits
- * for the stream and fails with AETH_ESTATE during graph capture: run the
- * shape once before capturing). Several host threads enqueueing on the same
- * stream at once must serialise their calls. */
+ * (src/quant/matmul/dispatch.rs:98-135) with device operands. Routing:
+ *   - m == 1: the matrix-core decode GEMV (Q8_0, Q4_K, Q5_K, Q6_K rows);
+ *   - m > 1, Q4_K / Q6_K / Q8_0 rows: the exact-mode fp16 MFMA GEMMs from 16
+ *     rows (from 5 once m · weight bytes reaches 150 MB, 200 MB for Q6_K),
+ *     the row-batched GEMV below that; Q6_K / Q8_0 products the GEMMs do not
+ *     take (k not whole super-blocks / blocks, buffers past 32-bit offsets)
+ *     run the row-batched GEMV up to 80 / 112 rows, then the DGEMM below;
+ *   - m > 1, Q5_K rows and GGUF-order Q2_K / Q3_K: the row-batched GEMV up to
+ *     a per-format row count (Q5_K 80, Q2_K 40, Q3_K 32), then the weight
+ *     dequantized once and one rocBLAS f64 DGEMM (also every K-quant product
+ *     of the dot-product mode with k not a multiple of 256);
+ *   - F32 / F16 / Q2_K / Q3_K in GGUF order: the kernel of matmul_f32_gguf
+ *     (dispatch.rs:541-574) for the rows not sent to the DGEMM.
+ * Stream scratch: the GEMMs' activation fragments and split-K partials, the
+ * GGUF-order kernel's partials, and the DGEMM's dequantized weight, f64
+ * operands and partials live in buffers the library keeps per (device,
+ * stream), as do the rocBLAS handles: calls on different streams never share
+ * them, calls on one stream run in order. A buffer grows on first use of a
+ * larger shape (a grow waits for the stream and fails with AETH_ESTATE during
+ * graph capture: run every shape once before capturing). Several host
+ * threads enqueueing on the same stream at once must serialise their calls. */
 AETH_API int aeth_qmatmul(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                           void* stream);
 
@@ -142,16 +153,16 @@ AETH_API int aeth_qmatmul(const aeth_weight* w, const float* d_a, int64_t m, flo
  * one device are serialised. Fails (no CPU fallback) if no device is usable. */
 AETH_API int aeth_quantized_matmul_impl(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
                                         int64_t n, int64_t k, int dtype, float* c);
-/* quantized_matmul_impl as an aarch64 host with dotprod runs it
- * (avx2_dispatch.rs:9-44, dispatch.rs:21-22): Q8_0 / Q4_K / Q5_K / Q6_K
- * through the int8 dot-product kernels (AETH_MM_Q8_ACTIVATIONS), the other
- * formats as aeth_quantized_matmul_impl. Same arguments and caching. */
 /* quantized_matmul_impl with its b_f32_cache argument (dispatch.rs:98-117):
  * when b_f32_cache is non-NULL it holds the weight dequantized to f32 in GGUF
  * [k][n] order (k·n floats) and c = matmul_f32_gguf(a, cache) — b_raw is then
  * not read; with NULL this is aeth_quantized_matmul_impl. Same caching. */
 AETH_API int aeth_quantized_matmul_impl_cached(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
                                                int64_t n, int64_t k, int dtype, float* c, const float* b_f32_cache);
+/* quantized_matmul_impl as an aarch64 host with dotprod runs it
+ * (avx2_dispatch.rs:9-44, dispatch.rs:21-22): Q8_0 / Q4_K / Q5_K / Q6_K
+ * through the int8 dot-product kernels (AETH_MM_Q8_ACTIVATIONS), the other
+ * formats as aeth_quantized_matmul_impl. Same arguments and caching. */
 AETH_API int aeth_quantized_matmul_dotprod(const float* a, int64_t m, const uint8_t* b_raw, int64_t b_len,
                                            int64_t n, int64_t k, int dtype, float* c);
 /* matmul_q8_0 / matmul_q4_k / matmul_q6_k(a, b, m, n, k, c)
@@ -196,6 +207,9 @@ AETH_API int aeth_dispatch_matmul(const float* a, int64_t m, const uint8_t* b_ra
 AETH_API int aeth_weight_cache_clear(void);
 AETH_API int aeth_weight_cache_set_limit(int64_t max_bytes);
 AETH_API int64_t aeth_weight_cache_bytes(void);
+/* The fingerprint a host-slice call computes over the weight bytes (the
+ * per-call cost of the check above; exported to time it). */
+AETH_API int aeth_weight_fingerprint(const void* host, int64_t bytes, uint64_t* out);
 
 /* rmsnorm_inplace (runner.rs:1739-1746) on `rows` rows of n: out = x/rms*w. */
 AETH_API int aeth_rmsnorm(const float* d_x, const float* d_w, int64_t rows, int64_t n, float eps,
@@ -285,16 +299,27 @@ AETH_API int aeth_stream_read(const void* d_src, int64_t bytes, uint32_t* d_sink
 AETH_API int aeth_mfma_rate(int kind, int iters, int workgroups, float* d_sink, void* stream);
 
 /* ── LlamaRunner (src/inference/runner.rs) on the device ─────────────────
- * Model shape = LlamaConfig (model_loader.rs:71-84). */
+ * Model shape = LlamaConfig (model_loader.rs:71-84). sliding_window is
+ * ArchConfig::sliding_window (model_loader.rs:62-67; 0 = None): decode and
+ * prefill attention see the last sliding_window positions only
+ * (runner.rs:1768-1777, :1825-1845). As LlamaRunner::new / new_streaming do
+ * (runner.rs:225, :339), the runner's cache and RoPE table hold
+ * min(max_seq_len, 4096) positions; flags AETH_CFG_FULL_CONTEXT keeps
+ * max_seq_len instead (up to 8192, the decode attention's limit) — an
+ * opt-in with no counterpart in the reference. */
 typedef struct aeth_llama_config {
     int32_t vocab_size, d_model, num_layers, num_heads, num_kv_heads, head_dim, d_ff, max_seq_len;
     float rope_base, rms_norm_eps;
+    int32_t sliding_window;
+    int32_t flags;
 } aeth_llama_config;
+#define AETH_CFG_FULL_CONTEXT 1
+#define AETH_RUNNER_MAX_SEQ 4096
 
 typedef struct aeth_runner aeth_runner;
 
 /* Creates a runner with device weights and a zeroed StaticKVCache of
- * max_seq_len positions. Host buffers: per layer l, layer_weights[l*7+j]
+ * min(max_seq_len, 4096) positions (max_seq_len with AETH_CFG_FULL_CONTEXT). Host buffers: per layer l, layer_weights[l*7+j]
  * for j = q,k,v,o,gate,up,down (each as its QuantWeight holds it: [out][in]
  * row blocks for Q8_0 / Q4_K / Q5_K / Q6_K, the GGUF [in][out] tensor for
  * F32 / F16 / Q2_K / Q3_K — see aeth_weight_create), layer_dtypes likewise; norms[l*2+{0,1}] = attn_norm, ffn_norm (f32);

@@ -820,9 +820,14 @@ ORC_API int32_t orc_argmax(const float* logits, size_t n) {
 
 /* ── One decode step, CPU branch of forward_one_internal (runner.rs:1557-1646) */
 
+/* LlamaConfig (model_loader.rs:71-84) as the runner uses it: max_seq is the
+ * runner's cache length (min(max_seq_len, 4096), runner.rs:225 / :339);
+ * sliding_window is ArchConfig::sliding_window (model_loader.rs:62-67, read
+ * from attention.sliding_window_length :286), 0 for None. */
 typedef struct {
     int32_t vocab, d_model, n_layers, n_heads, n_kv_heads, head_dim, d_ff, max_seq;
     float rope_base, eps;
+    int32_t sliding_window;
 } orc_llama_cfg;
 
 enum { ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14 };
@@ -915,7 +920,8 @@ ORC_API int orc_decode_step_from(const orc_llama_cfg* cfg, const float* x_embed,
         for (size_t h = 0; h < nh; h++) {
             size_t kvh = h / groups;
             orc_attn_direct(q + h * hd, lb + kvh * head_stride, lb + nkv * head_stride + kvh * head_stride,
-                            seq, hd, 0, scores, attn + h * hd);
+                            seq, hd, (size_t)(cfg->sliding_window > 0 ? cfg->sliding_window : 0), scores,
+                            attn + h * hd);
         }
         orc_qmatmul(T[3], attn, W[3], d, nh * hd, proj);
         for (size_t i = 0; i < d; i++) x[i] += proj[i];
@@ -938,18 +944,22 @@ ORC_API int orc_decode_step_from(const orc_llama_cfg* cfg, const float* x_embed,
  * All n prompt tokens in one pass: token i at position i, its K/V at cache
  * slot i (the cache is written from slot 0; LlamaRunner::prefill then sets
  * seq_len = n, runner.rs:695-704), batched matmuls with m = n, causal
- * attention_batch (runner.rs:1809-1883, no sliding window), logits of the
- * last token only. x_embeds holds the n embedding rows. */
+ * attention_batch (runner.rs:1809-1883; with a sliding window w query i sees
+ * keys max(0, i - w + 1) ..= i, :1825-1845), logits of the last token only.
+ * x_embeds holds the n embedding rows. window 0 = none. */
 static void orc_attention_batch(const float* q, const float* k, const float* v, size_t n, size_t nh, size_t nkv,
-                                size_t hd, float* out, float* scores) {
+                                size_t hd, size_t window, float* out, float* scores) {
     float scale = 1.0f / sqrtf((float)hd);
     size_t groups = nh / nkv, q_stride = nh * hd, kv_stride = nkv * hd;
+    if (window == 0) window = (size_t)-1; /* sliding_window.unwrap_or(usize::MAX) */
     for (size_t h = 0; h < nh; h++) {
         size_t kvh = h / groups;
         for (size_t i = 0; i < n; i++) {
             const float* qr = q + i * q_stride + h * hd;
             float* row = scores + i * n;
-            for (size_t j = 0; j <= i; j++) {
+            size_t win_start = i >= window ? i - window + 1 : 0;
+            for (size_t j = 0; j < win_start; j++) row[j] = -INFINITY;
+            for (size_t j = win_start; j <= i; j++) {
                 const float* kr = k + j * kv_stride + kvh * hd;
                 float dot = 0.0f;
                 for (size_t e = 0; e < hd; e++) dot += qr[e] * kr[e];
@@ -1022,7 +1032,8 @@ ORC_API int orc_forward_batch(const orc_llama_cfg* cfg, const float* x_embeds, i
                 memcpy(lb + h * head_stride + i * hd, K + (i * nkv + h) * hd, hd * 4);
                 memcpy(lb + nkv * head_stride + h * head_stride + i * hd, V + (i * nkv + h) * hd, hd * 4);
             }
-        orc_attention_batch(Q, K, V, n, nh, nkv, hd, A, S);
+        orc_attention_batch(Q, K, V, n, nh, nkv, hd, (size_t)(cfg->sliding_window > 0 ? cfg->sliding_window : 0), A,
+                            S);
         orc_qmatmul_m(T[3], A, n, W[3], d, qd, P);
         for (size_t i = 0; i < n * d; i++) X[i] += P[i];
         for (size_t i = 0; i < n; i++) orc_rmsnorm(X + i * d, norms[l * 2 + 1], d, cfg->eps, N + i * d);

@@ -275,7 +275,7 @@ class LlamaCfg(ctypes.Structure):
     _fields_ = [("vocab", ctypes.c_int32), ("d_model", ctypes.c_int32), ("n_layers", ctypes.c_int32),
                 ("n_heads", ctypes.c_int32), ("n_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
                 ("d_ff", ctypes.c_int32), ("max_seq", ctypes.c_int32), ("rope_base", ctypes.c_float),
-                ("eps", ctypes.c_float)]
+                ("eps", ctypes.c_float), ("sliding_window", ctypes.c_int32)]
 
 
 def _dtype_of(layer_dtypes, l, j):

@@ -17,9 +17,11 @@ def _deq(dtype, raw, n, k):
 
 
 def logits64(c, emb, layers, dtypes, norms, final, lm, lm_dtype, tokens):
-    """c: config dict (TINY form); layers[l][j] raw bytes of q,k,v,o,gate,up,down;
+    """c: config dict (TINY form; an optional sliding_window w > 0 lets query i
+    see keys i-w+1 ..= i only); layers[l][j] raw bytes of q,k,v,o,gate,up,down;
     dtypes: 7 formats (or one per layer as a list of lists); tokens at
-    positions 0..len-1. Returns float64 logits of the last position."""
+    positions 0..len-1 (positions past the RoPE table clamp to its last row).
+    Returns float64 logits of the last position."""
     d, nh, nkv, hd, dff = c["d_model"], c["num_heads"], c["num_kv_heads"], c["head_dim"], c["d_ff"]
     ms, eps = c["max_seq_len"], c["rms_norm_eps"]
     shapes = [(nh * hd, d), (nkv * hd, d), (nkv * hd, d), (d, nh * hd), (dff, d), (dff, d), (d, dff)]
@@ -31,9 +33,14 @@ def logits64(c, emb, layers, dtypes, norms, final, lm, lm_dtype, tokens):
     def rms(v, w):
         return v / np.sqrt((v * v).sum(-1, keepdims=True) / v.shape[-1] + eps) * w.astype(np.float64)
 
+    rows = np.minimum(np.arange(n), ms - 1)
+    w = c.get("sliding_window", 0)
+    i_, j_ = np.arange(n)[:, None], np.arange(n)[None, :]
+    visible = (j_ <= i_) & ((j_ > i_ - w) if w > 0 else True)
+
     def rope(v):  # v [n][heads][hd], position = row
         a, b = v[..., :hd // 2].copy(), v[..., hd // 2:].copy()
-        cc, ss = C[:n, None, :], S[:n, None, :]
+        cc, ss = C[rows][:, None, :], S[rows][:, None, :]
         return np.concatenate([a * cc - b * ss, a * ss + b * cc], axis=-1)
 
     x = np.asarray(emb, dtype=np.float64)[np.asarray(tokens)]
@@ -48,7 +55,7 @@ def logits64(c, emb, layers, dtypes, norms, final, lm, lm_dtype, tokens):
         g = nh // nkv
         for hh in range(nh):
             sc = q[:, hh] @ k[:, hh // g].T / np.sqrt(hd)
-            sc = np.where(np.tril(np.ones((n, n), bool)), sc, -np.inf)
+            sc = np.where(visible, sc, -np.inf)
             p = np.exp(sc - sc.max(axis=1, keepdims=True))
             att[:, hh] = (p / p.sum(axis=1, keepdims=True)) @ v[:, hh // g]
         x = x + att.reshape(n, -1) @ W[3].T

@@ -65,21 +65,24 @@ def assert_close(g, r, tol=1e-3, cos_min=0.9999, what=""):
     assert (cos > cos_min).all(), "%s: row cosine %r <= %r" % (what, cos.min(), cos_min)
 
 
-def assert_close_logits(g, r, tol=1e-3, floor=1e-5, cos_min=0.9999, what="", exact=None):
+def assert_close_logits(g, r, tol=1e-3, floor=0.0, cos_min=0.9999, what="", exact=None):
     """Whole-model logits (a decode step or a prefill through every layer): the
-    element-wise bar of assert_close, where an element may also sit within
-    floor·max|r_row| of the reference. A logit is an f32 sum whose rounding scales
-    with the row's largest terms; in a row spanning ±658 (the Q8_0 test model) the
-    reference's own f32 order and any other exact-f32 order differ by a few 1e-3
-    on its small entries. With `exact` (the float64 logits of the same model,
-    tests/_model64.py) an element also passes when its distance from the exact
-    value is at most twice the largest distance the reference's own f32 result
-    shows on that row (plus 1e-6·max|row|): on the random test models, whose
-    activations reach the hundreds, one f32 evaluation order drifts from the
-    exact logits by up to 2e-5·max|row|, and another order drifts as much in
-    other places. Kernel-level outputs keep the plain element-wise bar, except
-    where the reference's own f32 sums miss it (the Q6_K GEMM's long rows of
-    magnitude in the thousands: floor 0, exact = the float64 product)."""
+    element-wise bar of assert_close and per-row cosine > cos_min. Two
+    widenings, each used only where a test passes it:
+      * `exact` (the float64 logits of the same model, tests/_model64.py): an
+        element also passes when its distance from the exact value is at most
+        twice the largest distance the reference's own f32 result shows on that
+        row (plus 1e-6·max|row|). A logit is an f32 sum whose rounding scales
+        with the row's largest terms: on some test models (the GGUF-order Q2_K /
+        Q3_K model, logits to ±572) the reference's own f32 result misses the
+        plain bar against the exact logits (test_oracle.py,
+        test_reference_f32_logits_miss_the_plain_bar_on_a_test_model), so no
+        other f32 order can be held to it against the reference there;
+      * `floor`: an element also passes within floor·max|r_row| of the
+        reference (0 unless given).
+    Kernel-level outputs keep the plain element-wise bar, except where the
+    reference's own f32 sums miss it (the Q6_K and Q8_0 GEMMs' long rows of
+    magnitude in the thousands: exact = the float64 product)."""
     g = np.atleast_2d(np.asarray(g, dtype=np.float64))
     r = np.atleast_2d(np.asarray(r, dtype=np.float64))
     assert g.shape == r.shape, (g.shape, r.shape)

@@ -43,3 +43,37 @@ def test_header_is_plain_c():
     r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", inc, "-x", "c", "-", "-o", "/dev/null"],
                        input=src, text=True, stderr=subprocess.PIPE)
     assert r.returncode == 0, r.stderr
+
+
+def test_weight_fingerprint_sees_every_byte():
+    """The content check of the host-slice weight cache (CPU only): the same bytes
+    give the same fingerprint from any thread; one byte changed at the start, in
+    the middle or at the end of a 40 MiB buffer (hashed in 1 MiB chunks by the
+    library's persistent host thread pool) or of a small one changes it."""
+    import threading
+
+    import numpy as np
+
+    L = A.lib()
+
+    def fp(buf):
+        out = ctypes.c_uint64()
+        assert L.aeth_weight_fingerprint(buf.ctypes.data, buf.nbytes, ctypes.byref(out)) == 0
+        return out.value
+
+    for size in (40 << 20, 4096 + 7):
+        buf = np.random.default_rng(size).integers(0, 256, size, dtype=np.uint8)
+        base = fp(buf)
+        seen = []
+        th = [threading.Thread(target=lambda: seen.append(fp(buf))) for _ in range(4)]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        assert seen == [base] * 4
+        for pos in (0, size // 2, size - 1, (1 << 20) + 3 if size > (1 << 21) else 1):
+            buf[pos] ^= 1
+            assert fp(buf) != base, pos
+            buf[pos] ^= 1
+        assert fp(buf) == base
+        assert fp(buf[:-1]) != base  # the length enters the fingerprint

@@ -8,8 +8,9 @@ positions) — the shapes where the fused kernels of the benchmark run:
     and the 64-bit atomicMax greedy argmax fused.
 A 2-layer model of those widths is built on the device from a seed, exported
 through aeth_runner_export and run teacher-forced against the oracle's decode
-step (runner.rs:1557-1646); the full 32-layer model is checked by properties
-(graph replay = eager, finite logits, fused argmax = host argmax)."""
+step (runner.rs:1557-1646); the full 32-layer model is run teacher-forced
+against the oracle for two steps and checked by properties (graph replay =
+eager, finite logits, fused argmax = host argmax)."""
 import ctypes
 
 import numpy as np
@@ -141,6 +142,54 @@ def test_prefill_8b_widths_match_oracle(gpu, width):
         assert fl.value == n
         assert_close_rows(kv_dev[:, :, :, :n].reshape(-1, c["head_dim"]), kv[:, :, :, :n].reshape(-1, c["head_dim"]),
                           what="kv after the %s prefill" % width)
+    finally:
+        L.aeth_runner_free(r)
+
+
+def test_decode_8b_full_depth_matches_oracle(gpu):
+    """BASELINE config 4 itself: all 32 layers, KV prefilled to 2048 positions,
+    two teacher-forced steps against the oracle's decode step
+    (forward_one_internal, runner.rs:1557-1646) — logits (element-wise bar and
+    cosine > 0.9999), the fused greedy argmax, and the K/V slots the steps write.
+    About 4 s of single-thread CPU per oracle step."""
+    c = dict(C8B, num_layers=32)
+    L = A.lib()
+    d, dff, kvd, V = c["d_model"], c["d_ff"], c["num_kv_heads"] * c["head_dim"], c["vocab_size"]
+    r = synthetic_runner(c, 0x8B8B8B)
+    try:
+        A.check(L.aeth_runner_fill_kv(r, 0x4B56, PREFILLED), "fill_kv")
+        rowb = lambda k: (k // 256) * 144
+        sizes = [d * rowb(d), kvd * rowb(d), kvd * rowb(d), d * rowb(d), dff * rowb(d), dff * rowb(d), d * rowb(dff)]
+        layers = [[export(r, j, l, sizes[j]) for j in range(7)] for l in range(c["num_layers"])]
+        norms = [[export(r, 7 + j, l, d * 4, np.float32) for j in range(2)] for l in range(c["num_layers"])]
+        final = export(r, 9, 0, d * 4, np.float32)
+        lm = export(r, 10, 0, V * 16 * 210)
+        kv = np.empty((c["num_layers"], 2, c["num_kv_heads"], c["max_seq_len"], c["head_dim"]), np.float32)
+        fl = ctypes.c_int32()
+        A.check(L.aeth_runner_kv_to_host(r, kv.ctypes.data, ctypes.byref(fl)), "kv_to_host")
+        assert fl.value == PREFILLED
+        s, co = O.precompute_rope(c["max_seq_len"], c["head_dim"], c["rope_base"])
+        ocfg = O.LlamaCfg(V, d, c["num_layers"], c["num_heads"], c["num_kv_heads"], c["head_dim"], dff,
+                          c["max_seq_len"], c["rope_base"], c["rms_norm_eps"])
+        tok, fill = 1, PREFILLED
+        logits = np.empty(V, np.float32)
+        for step in range(2):
+            print("32-layer decode step %d (token %d, pos %d)" % (step, tok, fill), flush=True)
+            nxt = ctypes.c_int32()
+            A.check(L.aeth_runner_decode(r, tok, fill, logits.ctypes.data, ctypes.byref(nxt)), "decode")
+            emb = export(r, 11, tok, d * 4, np.float32)
+            ref, fill = O.decode_step(ocfg, emb, fill, layers, [Q4_K] * 7, norms, final, lm, Q6_K, s, co, kv, fill)
+            print("  oracle step done; logits span %.1f" % np.abs(ref).max(), flush=True)
+            assert_close_logits(logits, ref, what="32-layer step %d" % step)
+            assert nxt.value == O.argmax(logits), (nxt.value, O.argmax(logits))
+            tok = O.argmax(ref)
+        kv_dev = np.empty_like(kv)
+        A.check(L.aeth_runner_kv_to_host(r, kv_dev.ctypes.data, ctypes.byref(fl)), "kv_to_host")
+        assert fl.value == PREFILLED + 2
+        new = slice(PREFILLED, PREFILLED + 2)
+        assert_close_rows(kv_dev[:, :, :, new].reshape(-1, c["head_dim"]), kv[:, :, :, new].reshape(-1, c["head_dim"]),
+                          what="kv slots written by the 32-layer steps")
+        assert np.array_equal(kv_dev[:, :, :, :PREFILLED], kv[:, :, :, :PREFILLED])
     finally:
         L.aeth_runner_free(r)
 

@@ -157,13 +157,54 @@ def test_aether_load_rejects_bad_files(gpu, tmp_path):
     build_file(p, override=("blk.0.ffn_up.weight", [256, 512], 2, np.zeros(256 * 512 // 32 * 18, dtype=np.uint8)))
     assert not L.aether_load(str(p).encode())
     assert "ffn_up" in last_error(L)
-    p = tmp_path / "swa.gguf"
-    build_file(p, extra_meta=[("llama.attention.sliding_window_length", U32, 16)])
+    p = tmp_path / "swa0.gguf"  # a window of 0 would mask every position: refused
+    build_file(p, extra_meta=[("llama.attention.sliding_window_length", U32, 0)])
     assert not L.aether_load(str(p).encode())
-    assert "sliding" in last_error(L)
+    assert "sliding_window" in last_error(L)
     p = tmp_path / "long.gguf"
     build_file(p, context=131072)
     m = L.aether_load_streaming(str(p).encode(), 2)
     assert m, last_error(L)
-    assert L.aether_context_len(m) == 8192
+    assert L.aether_context_len(m) == 4096  # min(context_length, 4096), c_api.rs:123-127
     L.aether_free(m)
+
+
+def test_aether_load_sliding_window_and_context_cap(gpu, tmp_path):
+    """A file with attention.sliding_window_length 3 (ArchConfig::sliding_window,
+    model_loader.rs:286) and context_length 8192: the runner holds 4096 positions
+    (runner.rs:225; aether_context_len 4096), prefill and decode attend over the
+    last 3 positions, and a decode at position 5000 takes RoPE row 4095 — each
+    against the oracle with the same window and a 4096-row table."""
+    L = A.lib()
+    path = tmp_path / "swa.gguf"
+    mdl = build_file(path, layer_dtype=Q4_K_M, context=8192,
+                     extra_meta=[("llama.attention.sliding_window_length", U32, 3)])
+    m = L.aether_load(str(path).encode())
+    assert m, last_error(L)
+    try:
+        c = dict(CFG, max_seq_len=4096, sliding_window=3)
+        assert L.aether_context_len(m) == 4096
+        ocfg = O.LlamaCfg(c["vocab_size"], c["d_model"], c["num_layers"], c["num_heads"], c["num_kv_heads"],
+                          c["head_dim"], c["d_ff"], 4096, c["rope_base"], c["rms_norm_eps"], 3)
+        s, co = O.precompute_rope(4096, c["head_dim"], c["rope_base"])
+        kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], 4096, c["head_dim"]), dtype=np.float32)
+        toks = np.random.default_rng(8).integers(0, c["vocab_size"], 20).astype(np.int32)
+        logits = np.empty(c["vocab_size"], dtype=np.float32)
+        assert L.aether_prefill(m, toks.ctypes.data, len(toks), logits.ctypes.data) == 0, last_error(L)
+        ref = O.forward_batch(ocfg, mdl["emb"][toks], mdl["layers"], mdl["layer_dtype"], mdl["norms"], mdl["final"],
+                              mdl["lm"], mdl["lm_dtype"], s, co, kv)
+        ex = logits64(c, mdl["emb"], mdl["layers"], mdl["layer_dtype"], mdl["norms"], mdl["final"], mdl["lm"],
+                      mdl["lm_dtype"], list(toks))
+        assert_close_logits(logits, ref, what="windowed aether_load prefill", exact=ex)
+        unwindowed = O.forward_batch(O.LlamaCfg(*[getattr(ocfg, f) for f, _ in ocfg._fields_[:-1]]), mdl["emb"][toks],
+                                     mdl["layers"], mdl["layer_dtype"], mdl["norms"], mdl["final"], mdl["lm"],
+                                     mdl["lm_dtype"], s, co, np.zeros_like(kv))
+        assert np.abs(unwindowed - ref).max() > 1e-2 * np.abs(ref).max()  # the window matters here
+        tok = int(np.argmax(ref))
+        assert L.aether_decode(m, tok, 5000, logits.ctypes.data) == 0, last_error(L)
+        ref2, fill = O.decode_step(ocfg, mdl["emb"][tok], 5000, mdl["layers"], mdl["layer_dtype"], mdl["norms"],
+                                   mdl["final"], mdl["lm"], mdl["lm_dtype"], s, co, kv, len(toks))
+        assert fill == 21
+        assert_close_logits(logits, ref2, what="windowed decode at position 5000")
+    finally:
+        L.aether_free(m)

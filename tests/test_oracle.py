@@ -275,6 +275,47 @@ def test_dotprod_reference_is_integer_exact():
     assert (np.abs(got - exact) <= 1e-5 * scale + 1e-6).all()
 
 
+def test_dotprod_q8_0_reference_is_integer_exact():
+    """matmul_q8_0_dotprod_reference (tests.rs:28-60) against the float64 product
+    of the dequantized Q8_0 activation blocks and weights: per block an exact i32
+    sum times d_a·d_b, so only f32 rounding separates them. k = 200 is ragged
+    (blocks_per_row = div_ceil(k, 32) = 7, the last activation block zero-padded
+    by the quantizer)."""
+    rng = np.random.default_rng(23)
+    for m, n, k in ((3, 24, 512), (2, 8, 200)):
+        nb = (k + 31) // 32
+        a = rng.standard_normal(m * k).astype(np.float32) * 3
+        aq = O.quantize_activations_q8_0(a, m, k)
+        b = synth_blocks(Q8_0, n * nb, 3)
+        got = O.dotprod_ref(Q8_0, aq, b, m, n, k)
+        ad = O.dequant(Q8_0, aq, m * nb * 32).reshape(m, nb * 32).astype(np.float64)
+        w = O.dequant(Q8_0, b, n * nb * 32).reshape(n, nb * 32).astype(np.float64)
+        assert not ad[:, k:].any()  # the padded tail of the last block holds zeros
+        exact = ad @ w.T
+        scale = np.abs(ad) @ np.abs(w).T
+        assert (np.abs(got - exact) <= 1e-6 * scale + 1e-7).all()
+
+
+def _q8_block(d, q):
+    return np.concatenate([np.array([d], np.float32).astype(np.float16).view(np.uint8),
+                           np.asarray(q, np.int8).view(np.uint8)])
+
+
+def test_dotprod_q8_0_reference_hand_blocks():
+    """Two blocks per row with distinct scales on both sides, exact in f32:
+    block 0 contributes (Σ i·1)·(d_a·d_b) and block 1 (Σ 2·q_b)·(d_a·d_b). A
+    block index off by one, a scale paired with the wrong block or a wrong row
+    of activations changes the sums (140, 316, ... instead of 252 and 318)."""
+    i = np.arange(32)
+    qb1 = np.where(i < 16, 3, -1)
+    a = np.concatenate([_q8_block(1.0, i), _q8_block(0.5, np.full(32, 2)),    # row 0
+                        _q8_block(0.5, i), _q8_block(1.0, np.full(32, 2))])   # row 1: scales swapped
+    b = np.concatenate([_q8_block(0.25, np.ones(32)), _q8_block(4.0, qb1)])
+    got = O.dotprod_ref(Q8_0, a, b, 2, 1, 64)
+    # row 0: 496·(1·0.25) + 64·(0.5·4) = 124 + 128; row 1: 496·(0.5·0.25) + 64·(1·4) = 62 + 256
+    assert got.ravel().tolist() == [252.0, 318.0]
+
+
 # ── decode-step math ─────────────────────────────────────────────────────
 
 def test_rmsnorm_constant_vector():
@@ -371,6 +412,171 @@ def test_decode_step_matches_f64_composition():
     ref = lmw @ rms(x, final)
     np.testing.assert_allclose(logits, ref, rtol=1e-4, atol=1e-3 * np.abs(ref).max())
     np.testing.assert_allclose(kv[0, 0, :, fill], k_, rtol=1e-4, atol=1e-4)
+
+
+def _toy_model(nl, seed, dts=None):
+    rng = np.random.default_rng(seed)
+    vocab, d, nh, nkv, hd, dff, ms = 64, 256, 4, 2, 64, 512, 16
+    shapes = [(nh * hd, d), (nkv * hd, d), (nkv * hd, d), (d, nh * hd), (dff, d), (dff, d), (d, dff)]
+    dts = dts or [Q4_K] * 7
+    W = [[synth_blocks(dts[j], n * k // GEOM[dts[j]][0], seed * 1000 + 10 * l + j) for j, (n, k) in enumerate(shapes)]
+         for l in range(nl)]
+    norms = [[(1 + 0.02 * rng.standard_normal(d)).astype(np.float32) for _ in range(2)] for _ in range(nl)]
+    final = (1 + 0.02 * rng.standard_normal(d)).astype(np.float32)
+    lm = synth_blocks(Q6_K, vocab * d // 256, seed + 99)
+    return dict(vocab=vocab, d=d, nh=nh, nkv=nkv, hd=hd, dff=dff, ms=ms, W=W, norms=norms, final=final, lm=lm,
+                dts=dts, rng=rng)
+
+
+def test_decode_step_resume_at_the_last_layer_is_the_head():
+    """orc_decode_step_from entered at start_layer = n_layers (a budgeted decode
+    whose every layer completed, runner.rs:1201-1217) runs no layer: its logits
+    are the final RMSNorm and the LM head of x — bit for bit the pinned rmsnorm
+    and LM-head matmul, and the float64 composition — the cache is not written
+    and its fill still advances (StaticKVCache::advance)."""
+    t = _toy_model(2, 31)
+    cfg = O.LlamaCfg(t["vocab"], t["d"], 2, t["nh"], t["nkv"], t["hd"], t["dff"], t["ms"], 10000.0, 1e-5)
+    s, c = O.precompute_rope(t["ms"], t["hd"], 10000.0)
+    x = (t["rng"].standard_normal(t["d"]) * 4).astype(np.float32)
+    kv = t["rng"].standard_normal((2, 2, t["nkv"], t["ms"], t["hd"])).astype(np.float32)
+    kv0 = kv.copy()
+    logits, fill = O.decode_step(cfg, x, 5, t["W"], t["dts"], t["norms"], t["final"], t["lm"], Q6_K, s, c, kv, 5,
+                                 start_layer=2)
+    assert fill == 6 and np.array_equal(kv, kv0)
+    head = O.reference_matmul(Q6_K, O.rmsnorm(x, t["final"], 1e-5), t["lm"], 1, t["vocab"], t["d"])[0]
+    assert np.array_equal(logits.view(np.uint32), head.view(np.uint32))
+    x64 = x.astype(np.float64)
+    h = x64 / np.sqrt((x64 * x64).mean() + 1e-5) * t["final"]
+    lmw = O.dequant(Q6_K, t["lm"], t["vocab"] * t["d"]).reshape(t["vocab"], t["d"]).astype(np.float64)
+    ref = lmw @ h
+    np.testing.assert_allclose(logits, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+
+
+def test_decode_step_resume_at_layer_one():
+    """Entered at layer 1 of a 2-layer model with x as the residual stream after
+    layer 0, the step equals a 1-layer model made of layer 1 alone (its
+    weights, norms and cache layer) — logits and written K/V bit for bit —
+    whatever layer 0's weights and cache hold, and it leaves layer 0's cache
+    untouched. Resuming one layer early or late, or indexing the weights,
+    norms or cache by the wrong layer, changes the result."""
+    t = _toy_model(2, 37)
+    cfg2 = O.LlamaCfg(t["vocab"], t["d"], 2, t["nh"], t["nkv"], t["hd"], t["dff"], t["ms"], 10000.0, 1e-5)
+    cfg1 = O.LlamaCfg(t["vocab"], t["d"], 1, t["nh"], t["nkv"], t["hd"], t["dff"], t["ms"], 10000.0, 1e-5)
+    s, c = O.precompute_rope(t["ms"], t["hd"], 10000.0)
+    x = (t["rng"].standard_normal(t["d"]) * 2).astype(np.float32)
+    kv = np.zeros((2, 2, t["nkv"], t["ms"], t["hd"]), np.float32)
+    kv[:, :, :, :4] = t["rng"].standard_normal((2, 2, t["nkv"], 4, t["hd"]))
+    pos, fill = 4, 4
+    runs = []
+    for garbage_seed in (1, 2):
+        g = _toy_model(1, 500 + garbage_seed)  # layer 0 replaced by unrelated weights, norms and cache
+        W = [g["W"][0], t["W"][1]]
+        norms = [g["norms"][0], t["norms"][1]]
+        k2 = kv.copy()
+        k2[0] = g["rng"].standard_normal(k2[0].shape)
+        k2_l0 = k2[0].copy()
+        lg, f2 = O.decode_step(cfg2, x, pos, W, t["dts"], norms, t["final"], t["lm"], Q6_K, s, c, k2, fill,
+                               start_layer=1)
+        assert f2 == fill + 1 and np.array_equal(k2[0], k2_l0)
+        runs.append((lg, k2[1].copy()))
+    assert np.array_equal(runs[0][0], runs[1][0]) and np.array_equal(runs[0][1], runs[1][1])
+    k1 = kv[1:2].copy()
+    l1, f1 = O.decode_step(cfg1, x, pos, [t["W"][1]], t["dts"], [t["norms"][1]], t["final"], t["lm"], Q6_K, s, c, k1,
+                           fill)
+    assert f1 == fill + 1
+    assert np.array_equal(runs[0][0].view(np.uint32), l1.view(np.uint32))
+    assert np.array_equal(runs[0][1], k1[0])
+    assert not np.array_equal(k1[0], kv[1])  # the step wrote slot 4 of layer 1
+    # entering at layer 0 (the whole step) or at layer 2 (the head alone) gives other logits
+    for other in (0, 2):
+        lo, _ = O.decode_step(cfg2, x, pos, [t["W"][0], t["W"][1]], t["dts"], t["norms"], t["final"], t["lm"], Q6_K, s,
+                              c, kv.copy(), fill, start_layer=other)
+        assert np.abs(lo - l1).max() > 1e-2 * np.abs(l1).max()
+
+
+def test_attn_direct_sliding_window_is_attention_over_the_last_w_keys():
+    """attn_direct with sliding_window w < seq (runner.rs:1768-1777) masks the
+    keys before seq - w: the result equals plain attention over the last w
+    positions (float64 as well); w >= seq is no window at all."""
+    hd, seq = 128, 45
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.standard_normal((seq, hd)).astype(np.float32)
+    v = rng.standard_normal((seq, hd)).astype(np.float32)
+    full = O.attn_direct(q, k, v, seq, hd)
+    for w in (1, 7, 44):
+        got = O.attn_direct(q, k, v, seq, hd, window=w)
+        tail = O.attn_direct(q, k[seq - w:], v[seq - w:], w, hd)
+        np.testing.assert_allclose(got, tail, rtol=1e-6, atol=1e-6)
+        sc = k[seq - w:].astype(np.float64) @ q / np.sqrt(hd)
+        p = np.exp(sc - sc.max())
+        np.testing.assert_allclose(got, (p / p.sum()) @ v[seq - w:], rtol=1e-5, atol=1e-5)
+        assert np.abs(got - full).max() > 1e-3
+    assert np.array_equal(O.attn_direct(q, k, v, seq, hd, window=seq), full)
+    assert np.array_equal(O.attn_direct(q, k, v, seq, hd, window=1000), full)
+    np.testing.assert_allclose(O.attn_direct(q, k, v, seq, hd, window=1), v[seq - 1], rtol=1e-6, atol=1e-6)
+
+
+def test_sliding_window_prefill_and_decode():
+    """The window in both CPU paths: forward_batch's attention_batch (query i
+    sees keys max(0, i - w + 1) ..= i, runner.rs:1825-1845) and the decode
+    step's attn_direct (keys seq - w .. seq) agree token by token, match the
+    float64 model with the same mask, differ from the unwindowed model, and a
+    window at least the prompt length changes nothing."""
+    from tests._model64 import logits64
+
+    t = _toy_model(2, 41, dts=[Q4_K, Q8_0, Q6_K, Q4_K, Q4_K, Q8_0, Q6_K])
+    n, ms = 13, 16
+    emb = t["rng"].standard_normal((t["vocab"], t["d"])).astype(np.float32)
+    toks = t["rng"].integers(0, t["vocab"], n)
+    s, c = O.precompute_rope(ms, t["hd"], 10000.0)
+    res = {}
+    for w in (0, 5, 13):
+        cfg = O.LlamaCfg(t["vocab"], t["d"], 2, t["nh"], t["nkv"], t["hd"], t["dff"], ms, 10000.0, 1e-5, w)
+        kvb = np.zeros((2, 2, t["nkv"], ms, t["hd"]), np.float32)
+        lb = O.forward_batch(cfg, emb[toks], t["W"], t["dts"], t["norms"], t["final"], t["lm"], Q6_K, s, c, kvb)
+        kvs = np.zeros_like(kvb)
+        fill = 0
+        for i in range(n):
+            ls, fill = O.decode_step(cfg, emb[toks[i]], i, t["W"], t["dts"], t["norms"], t["final"], t["lm"], Q6_K, s,
+                                     c, kvs, fill)
+        np.testing.assert_allclose(lb, ls, rtol=1e-4, atol=1e-4 * np.abs(ls).max())
+        np.testing.assert_allclose(kvb, kvs, rtol=1e-4, atol=1e-4)
+        cd = dict(vocab_size=t["vocab"], d_model=t["d"], num_heads=t["nh"], num_kv_heads=t["nkv"], head_dim=t["hd"],
+                  d_ff=t["dff"], max_seq_len=ms, rope_base=10000.0, rms_norm_eps=1e-5, sliding_window=w)
+        ex = logits64(cd, emb, t["W"], t["dts"], t["norms"], t["final"], t["lm"], Q6_K, list(toks))
+        np.testing.assert_allclose(lb, ex, rtol=1e-4, atol=1e-4 * np.abs(ex).max())
+        res[w] = lb
+    assert np.abs(res[5] - res[0]).max() > 1e-2 * np.abs(res[0]).max()
+    assert np.array_equal(res[13], res[0])
+
+
+def test_reference_f32_logits_miss_the_plain_bar_on_a_test_model():
+    """Why model-level logits are anchored on the float64 model: on the
+    GGUF-order test model (Q3_K / Q2_K layers, an F16 down projection, Q6_K
+    head; 19-token prompt, logits up to ±572) the reference's own f32 result —
+    batched prefill and token-by-token decode alike — sits more than
+    1e-3·max(1, |r|) from the exact logits on some entries (e.g. 3.2e-3 on a
+    logit of -1.8). No other f32 evaluation order can be held to the plain
+    element-wise bar against it there; the GPU tests of such models measure
+    both against the float64 value instead (assert_close_logits' `exact`)."""
+    from tests._model64 import logits64
+    from tests._models import TINY, build_tiny, oracle_cfg
+    from tests._util import F16, Q2_K, Q3_K, close_mask
+
+    dts = [Q3_K, Q3_K, Q3_K, Q2_K, Q2_K, Q2_K, F16]
+    c = dict(TINY, max_seq_len=64)
+    m = build_tiny(seed=22, layer_dtype=dts, c=c)
+    s, co = O.precompute_rope(64, c["head_dim"], c["rope_base"])
+    toks = np.random.default_rng(1).integers(0, c["vocab_size"], 19)
+    kv = np.zeros((2, 2, c["num_kv_heads"], 64, c["head_dim"]), np.float32)
+    ref = O.forward_batch(oracle_cfg(c), m["emb"][toks], m["layers"], dts, m["norms"], m["final"], m["lm"], Q6_K, s,
+                          co, kv)
+    ex = logits64(c, m["emb"], m["layers"], dts, m["norms"], m["final"], m["lm"], Q6_K, list(toks))
+    bad = ~close_mask(ref, ex)
+    assert bad.sum() >= 2 and np.abs(ex).max() > 500
+    assert (np.abs(ex[bad]) < 10).all()  # moderate logits, far below the row's maximum
+    assert np.abs(ref - ex).max() <= 2.5e-5 * np.abs(ex).max()
 
 
 def test_forward_batch_matches_sequential_decode_steps():
