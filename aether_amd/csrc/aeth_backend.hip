@@ -22,6 +22,8 @@ constexpr int CA_MAXD = 256;  // head_dim limit: four dims per lane
 // One wave per query i: keys in chunks of 64 (lane ↔ key), the chunk's scores
 // (q·k)·scale with online-softmax rescaling of the running (max, sum, out);
 // each lane accumulates dims lane + 64t of the output, V rows read coalesced.
+// Scores of -inf carry no weight and a row whose scores are all -inf is 0
+// (the reference skips such scores).
 template <bool VEC4>
 __global__ void __launch_bounds__(256) k_causal_attn_bsd(const float* __restrict__ q, const float* __restrict__ k,
                                                          const float* __restrict__ v, int seq, int d, int hd,
@@ -52,7 +54,9 @@ __global__ void __launch_bounds__(256) k_causal_attn_bsd(const float* __restrict
             s = dot * scale;
         }
         const float m_new = fmaxf(m, aeth_wave_max(s));
-        const float p = j <= i ? expf(s - m_new) : 0.0f;
+        // a -inf score (masked, or q·k overflowing to -inf) gets no weight, as cpu.rs:1705-1721
+        // skips it: exp(-inf - m_new) would be NaN while m_new is still -inf
+        const float p = j <= i && s != -INFINITY ? expf(s - m_new) : 0.0f;
         const float alpha = m == -INFINITY ? 0.0f : expf(m - m_new);
         l = l * alpha + aeth_wave_sum(p);
         m = m_new;
@@ -73,7 +77,8 @@ __global__ void __launch_bounds__(256) k_causal_attn_bsd(const float* __restrict
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const int e = lane + 64 * t;
-        if (e < hd) out[base + (int64_t)i * d + e] = acc[t] * inv;
+        // every score -inf: the reference sums nothing and leaves the row 0
+        if (e < hd) out[base + (int64_t)i * d + e] = l == 0.0f ? 0.0f : acc[t] * inv;
     }
 }
 

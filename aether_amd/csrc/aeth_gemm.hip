@@ -689,6 +689,10 @@ int aeth_gemm_q6k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
 
 bool aeth_q80_gemm_rows(const aeth_weight* w, int64_t m) {
     if (!w || w->dtype != AETH_DTYPE_Q8_0 || w->order != AETH_ORDER_PLANAR || w->k != w->nb * 32 || m <= 1) return false;
+    // a NaN or infinite block scale: the rescaled accumulator (U ← U·d_old/d_new) cannot carry
+    // it (entering an infinite d zeroes U, the next one makes Inf·0 = NaN); q8_0.rs adds d·Σ per
+    // block, as the GEMV does, so such weights stay on the GEMV
+    if (w->special_scales) return false;
     const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM, ntiles = aeth_cdiv(w->n, 16), ngr = aeth_cdiv(w->nb, 4);
     if (ntiles * ngr * 2048 >= INT32_MAX || mp * w->k * 4 >= INT32_MAX || mp > (1LL << 20)) return false;
     // AETH_Q80_GEMM_ROWS=r takes the GEMM from r rows (tests and measurements; read once)

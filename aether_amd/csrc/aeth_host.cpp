@@ -108,7 +108,10 @@ int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_
     // weights are finite (K-quant scales go through decode_d), so the SGEMM's
     // 0·w terms equal matmul_f32_gguf's skipped rows; F32 / F16 weights, which may
     // hold infinities, keep the kernels that skip zero activations as the reference does.
-    if (m >= dequant_gemm_rows(w->dtype) && w->dtype != AETH_DTYPE_F32 && w->dtype != AETH_DTYPE_F16)
+    // (a Q8_0 weight with a NaN or infinite block scale stays on the GEMV: dequantized, its
+    // q = 0 entries become 0·Inf = NaN, where q8_0.rs multiplies the block's sum by d)
+    if (m >= dequant_gemm_rows(w->dtype) && w->dtype != AETH_DTYPE_F32 && w->dtype != AETH_DTYPE_F16 &&
+        !(w->dtype == AETH_DTYPE_Q8_0 && w->special_scales))
         return aeth_dequant_gemm_launch(w, d_a, m, d_c, ldc, flags, s);
     GemvEpi e;
     e.flags = flags;

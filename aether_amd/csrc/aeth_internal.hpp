@@ -59,6 +59,9 @@ struct aeth_weight {
     int64_t bytes;        // nblk * block_bytes
     uint8_t* base;
     uint8_t *p0, *p1, *p2, *p3;
+    // planar weights: some block scale (Q8_0 d; Q4_K / Q5_K d or dmin; Q6_K d) has the f16
+    // exponent 31 (NaN / infinity bits), found when the bytes are laid out
+    int special_scales = 0;
 };
 
 int aeth_num_cus();

@@ -148,22 +148,38 @@ __device__ __forceinline__ uint8_t* planar_addr(int dtype, int64_t i, int64_t nb
     return p0 + ((tg * 2 + (s >> 1)) * 64 + n + 16 * kg) * 16 + (p & 15);
 }
 
+// True when raw byte i is the high byte of an f16 block scale: Q8_0 d (bytes 0-1), Q4_K / Q5_K
+// d and dmin (0-3), Q6_K d (208-209).
+__device__ __forceinline__ bool scale_high_byte(int dtype, int64_t i) {
+    if (dtype == AETH_DTYPE_Q4_K) { const int o = (int)(i % Q4K_BLOCK_BYTES); return o == 1 || o == 3; }
+    if (dtype == AETH_DTYPE_Q5_K) { const int o = (int)(i % Q5K_BLOCK_BYTES); return o == 1 || o == 3; }
+    if (dtype == AETH_DTYPE_Q6_K) return i % Q6K_BLOCK_BYTES == 209;
+    return i % Q8_BLOCK_BYTES == 1;
+}
+
+// to_planar: raw → planes, and *special set if a block scale has the f16 exponent 31
+// (bits 2-6 of its high byte all set); otherwise planes → raw.
 __global__ void k_relayout(int dtype, int64_t nb, uint8_t* __restrict__ raw, uint8_t* __restrict__ p0,
                            uint8_t* __restrict__ p1, uint8_t* __restrict__ p2, uint8_t* __restrict__ p3,
-                           int64_t total_bytes, int to_planar) {
+                           int64_t total_bytes, int to_planar, int* special) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total_bytes) return;
     uint8_t* dst = planar_addr(dtype, i, nb, p0, p1, p2, p3);
-    if (to_planar) *dst = raw[i];
-    else raw[i] = *dst;
+    if (to_planar) {
+        const uint8_t b = raw[i];
+        *dst = b;
+        if ((b & 0x7C) == 0x7C && scale_high_byte(dtype, i)) atomicOr(special, 1);
+    } else {
+        raw[i] = *dst;
+    }
 }
 
-static int relayout(aeth_weight* w, uint8_t* d_raw, int to_planar, hipStream_t s) {
+static int relayout(aeth_weight* w, uint8_t* d_raw, int to_planar, hipStream_t s, int* d_special = nullptr) {
     int64_t total = w->nblk * w->block_bytes;
     if (total == 0) return AETH_OK;
     int64_t grid = aeth_cdiv(total, 256);
     hipLaunchKernelGGL(k_relayout, dim3((unsigned)grid), dim3(256), 0, s, w->dtype, w->nb, d_raw, w->p0, w->p1,
-                       w->p2, w->p3, total, to_planar);
+                       w->p2, w->p3, total, to_planar, d_special);
     AETH_LAUNCH_CHECK();
     return AETH_OK;
 }
@@ -253,7 +269,9 @@ int aeth_weight_create_ex(int dtype, int order, int64_t n, int64_t k, const void
     int64_t off[4], tot = 0;
     for (int i = 0; i < 4; i++) { off[i] = tot; tot += align256(sz[i]); }
     w->bytes = w->nblk * bb;
-    hipError_t e = hipMalloc((void**)&w->base, (size_t)(tot > 0 ? tot : 256));
+    const int64_t flag_off = tot;  // one int after the planes: the special-scale flag
+    tot += 256;
+    hipError_t e = hipMalloc((void**)&w->base, (size_t)tot);
     if (e != hipSuccess) {
         delete w;
         return aeth_set_error(AETH_ENOMEM, "aeth_weight_create: hipMalloc(%lld) failed: %s", (long long)tot,
@@ -290,13 +308,16 @@ int aeth_weight_create_ex(int dtype, int order, int64_t n, int64_t k, const void
             return aeth_set_error(AETH_EHIP, "aeth_weight_create: H2D copy failed: %s", hipGetErrorString(e));
         }
     }
-    rc = relayout(w, staging, 1, s);
-    if (!raw_is_device) {
-        hipError_t e2 = hipStreamSynchronize(s);
-        hipFree(staging);
-        if (rc == AETH_OK && e2 != hipSuccess)
+    rc = relayout(w, staging, 1, s, (int*)(w->base + flag_off));
+    int special = 0;
+    if (rc == AETH_OK) {
+        hipError_t e2 = hipMemcpyAsync(&special, w->base + flag_off, sizeof(int), hipMemcpyDeviceToHost, s);
+        if (e2 == hipSuccess) e2 = hipStreamSynchronize(s);
+        if (e2 != hipSuccess)
             rc = aeth_set_error(AETH_EHIP, "aeth_weight_create: sync failed: %s", hipGetErrorString(e2));
     }
+    w->special_scales = special;
+    if (!raw_is_device) hipFree(staging);
     if (rc) {
         hipFree(w->base);
         delete w;
@@ -456,39 +477,44 @@ extern "C" AETH_API int aeth_fill_normal_f32(uint64_t seed, float* d_out, int64_
 
 // ── measurement: a plain streaming read ──────────────────────────────────
 // Reads every 16-byte word of [src, src + bytes) once (non-temporal loads,
-// eight in flight per thread before any is used) and folds them into one
-// word per thread, stored only if it equals a value no input makes likely,
-// so the loads cannot be dropped. The benchmark times it on the GEMV's weight
-// copies: the HBM floor a single launch of that size can show.
+// four in flight per thread before any is used) and folds them into one word
+// per thread, stored only if it equals a value no input makes likely, so the
+// loads cannot be dropped. The benchmark times it on the GEMV's weight copies:
+// the HBM floor a single launch of that size can show. Shape (a sweep of 256 /
+// 512 / 1024 threads, 4 / 8 / 16 loads per thread, 256 … 26307 workgroups,
+// non-temporal or plain loads, measured on the headline's 33 MB and the LM
+// head's 431 MB): 256 threads × 4 loads, one workgroup per 16 KiB up to 2048
+// workgroups, else 512 workgroups looping over the buffer — 6.10 µs for 33 MB,
+// 61.5 µs for 431 MB (7.0 TB/s); non-temporal loads beat plain ones by 4-9 %.
 typedef uint32_t sr_u4 __attribute__((ext_vector_type(4)));
 
-__global__ void __launch_bounds__(512) k_stream_read(const sr_u4* __restrict__ src, int64_t n16,
+__global__ void __launch_bounds__(256) k_stream_read(const sr_u4* __restrict__ src, int64_t n16,
                                                      uint32_t* __restrict__ sink) {
-    constexpr int U = 8;
-    const int64_t per_block = (int64_t)512 * U;
+    constexpr int U = 4;
+    const int64_t per_block = (int64_t)256 * U;
     uint32_t acc = 0;
     for (int64_t base = (int64_t)blockIdx.x * per_block; base < n16; base += (int64_t)gridDim.x * per_block) {
         sr_u4 v[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int64_t i = base + (int64_t)u * 512 + threadIdx.x;
+            const int64_t i = base + (int64_t)u * 256 + threadIdx.x;
             v[u] = i < n16 ? __builtin_nontemporal_load(src + i) : sr_u4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
-    if (acc == 0x9E3779B9u) sink[blockIdx.x * 512 + threadIdx.x] = acc;
+    if (acc == 0x9E3779B9u) sink[blockIdx.x * 256 + threadIdx.x] = acc;
 }
 
 extern "C" AETH_API int aeth_stream_read(const void* d_src, int64_t bytes, uint32_t* d_sink, int64_t sink_words,
                                          void* stream) {
     if (!d_src || !d_sink || bytes < 16 || (bytes & 15) || ((uintptr_t)d_src & 15))
         return aeth_set_error(AETH_EINVAL, "aeth_stream_read: bad argument");
-    const int64_t n16 = bytes / 16, per_block = 512 * 8;
-    const int64_t blocks = std::min<int64_t>(aeth_cdiv(n16, per_block), sink_words / 512);
-    if (blocks <= 0) return aeth_set_error(AETH_EINVAL, "aeth_stream_read: sink of %lld words < 512",
+    const int64_t n16 = bytes / 16, per_block = 256 * 4, full = aeth_cdiv(n16, per_block);
+    const int64_t blocks = std::min<int64_t>(full <= 2048 ? full : 512, sink_words / 256);
+    if (blocks <= 0) return aeth_set_error(AETH_EINVAL, "aeth_stream_read: sink of %lld words < 256",
                                            (long long)sink_words);
-    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)blocks), dim3(512), 0, (hipStream_t)stream, (const sr_u4*)d_src,
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (const sr_u4*)d_src,
                        n16, d_sink);
     AETH_LAUNCH_CHECK();
     return AETH_OK;

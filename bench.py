@@ -350,8 +350,41 @@ def cpu_rows_parallel(raw, x, n, k, seconds=4.0):
                 break
     nbytes = algorithmic_bytes(12, n, k)
     return {"value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port (scalar kernel, rows over threads)",
+            "kind": "port (scalar kernel, rows over threads)", "cpu": cpu_name(), "nproc": os.cpu_count(),
             "sample": "%d full Q4_K GEMVs 14336x4096 in %.1f s" % (calls, el)}
+
+
+def bench_boundary(torch, A, dtype, n, k, raw_dev, device_us, calls=20):
+    """The plugin boundary (QuantKernel::matmul, registry.rs:7-19, reached from
+    quantized_matmul_impl, dispatch.rs:120): aeth_quantized_matmul_impl on host
+    slices — a f32[k] and c f32[n] in pageable host memory, the weight bytes in
+    host memory and already in the library's device cache (one warm-up call
+    uploads them). Per call: the content fingerprint of the whole weight (the
+    cache's check that the slice was not rewritten), the copy of a to the
+    device, the GEMV, the copy of c back and the stream synchronisation.
+    Wall-clock median over `calls` calls; the fingerprint is also timed alone."""
+    import numpy as np
+
+    L = A.lib()
+    raw = raw_dev.cpu().numpy()
+    a = np.random.default_rng(5).standard_normal(k).astype(np.float32)
+    c = np.empty(n, np.float32)
+
+    def call():
+        A.check(L.aeth_quantized_matmul_impl(a.ctypes.data, 1, raw.ctypes.data, raw.nbytes, n, k, dtype,
+                                             c.ctypes.data), "quantized_matmul_impl")
+
+    call()  # uploads the weight into the cache
+    med, _ = cpu_median(call, calls)
+    fpv = ctypes.c_uint64()
+    fmed, _ = cpu_median(lambda: A.check(L.aeth_weight_fingerprint(raw.ctypes.data, raw.nbytes, ctypes.byref(fpv))),
+                         calls)
+    return {"us_per_call": round(med * 1e6, 1), "device_gemv_us": round(device_us, 3),
+            "fingerprint_us": round(fmed * 1e6, 1), "fingerprint_GB/s": round(raw.nbytes / fmed / 1e9, 2),
+            "weight_bytes": int(raw.nbytes), "copies_bytes": int(4 * (k + n)),
+            "host_threads": min(8, os.cpu_count() or 1),
+            "note": "median wall-clock of %d host-slice calls, weight cached on the device; "
+                    "fingerprint = hash of every weight byte per call" % calls}
 
 
 def cpu_name():
@@ -390,14 +423,14 @@ def cpu_configs(q8, q6, gemm, dec):
         raw, x = q8
         med, ts = cpu_median(lambda: O.scalar_matmul(8, x, raw, 1, 4096, 4096), 5)
         out["q8_0_gemv_4096x4096"] = {"value": round(algorithmic_bytes(8, 4096, 4096) / med / 1e9, 3), "unit": "GB/s",
-                                      "cores": 1, "kind": "port", "cpu": host,
+                                      "cores": 1, "kind": "port", "cpu": host, "nproc": os.cpu_count(),
                                       "sample": "median of 5 full GEMVs (scalar q8_0.rs restated): %.2f ms" % (med * 1e3)}
         print("[bench] cpu C1: %s" % out["q8_0_gemv_4096x4096"], file=sys.stderr, flush=True)
     if q6 is not None:
         raw, x = q6
         med, ts = cpu_median(lambda: O.avx2_matmul(14, x, raw, 1, 128256, 4096), 5)
         out["q6_k_gemv_128256x4096"] = {"value": round(algorithmic_bytes(14, 128256, 4096) / med / 1e9, 3),
-                                        "unit": "GB/s", "cores": 1, "kind": "port", "cpu": host,
+                                        "unit": "GB/s", "cores": 1, "kind": "port", "cpu": host, "nproc": os.cpu_count(),
                                         "sample": "median of 5 full GEMVs (avx2::matmul_q6_k restated): %.1f ms"
                                                   % (med * 1e3)}
         print("[bench] cpu C3: %s" % out["q6_k_gemv_128256x4096"], file=sys.stderr, flush=True)
@@ -406,7 +439,7 @@ def cpu_configs(q8, q6, gemm, dec):
         O.avx2_matmul(12, a, raw, 512, nn, 4096)
         el = time.perf_counter() - t0
         out["q4_k_gemm_m512_n%d" % nn] = {"value": round(2.0 * 512 * nn * 4096 / el / 1e9, 3), "unit": "GFLOP/s",
-                                          "cores": 1, "kind": "port", "cpu": host,
+                                          "cores": 1, "kind": "port", "cpu": host, "nproc": os.cpu_count(),
                                           "sample": "one m=512 call of avx2::matmul_q4_k restated: %.2f s" % el}
         print("[bench] cpu C4 n=%d: %s" % (nn, out["q4_k_gemm_m512_n%d" % nn]), file=sys.stderr, flush=True)
     if dec is not None:
@@ -428,7 +461,7 @@ def cpu_configs(q8, q6, gemm, dec):
                 agree += int(O.argmax(logits) == dec["tokens"][i + 1])
         mean = sum(ts) / len(ts)
         out["decode_8b_q4k"] = {"value": round(1.0 / mean, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-                                "cpu": host,
+                                "cpu": host, "nproc": os.cpu_count(),
                                 "sample": "%d CPU decode steps of the 32-layer model after 2048 positions, mean %.2f s "
                                           "per token; greedy tokens equal to the GPU's on %d of %d steps"
                                           % (len(ts), mean, agree, len(ts) - 1)}
@@ -452,8 +485,9 @@ def cpu_baseline(raw, x, n, k, seconds=10.0):
             break
     nbytes = algorithmic_bytes(12, n, k)
     return {"value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": "%d full Q4_K GEMVs 14336x4096 (avx2::matmul_q4_k restated, oracle/oracle.c) in %.1f s on %s"
-                      % (calls, el, platform.processor() or platform.machine())}
+            "cpu": cpu_name(), "nproc": os.cpu_count(),
+            "sample": "%d full Q4_K GEMVs 14336x4096 (avx2::matmul_q4_k restated, oracle/oracle.c) in %.1f s on one "
+                      "pinned core of a %d-thread host" % (calls, el, os.cpu_count() or 0)}
 
 
 def main():
@@ -463,9 +497,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--extra", default="floor,q8,q6,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,gemm_q80,decode,q4_k_m,q8_0_model",
-                    help="comma-separated extra sections to run: floor, q8, q6, q5, dotprod, gemm, gemm_q8, gemm_q6k, "
-                         "gemm_q80, "
+    ap.add_argument("--extra",
+                    default="floor,q8,q6,boundary,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,gemm_q80,decode,q4_k_m,q8_0_model",
+                    help="comma-separated extra sections to run: floor, q8, q6, boundary (host-slice calls; after q6), "
+                         "q5, dotprod, gemm, gemm_q8, gemm_q6k, gemm_q80, "
                          "decode, q4_k_m, q8_0_model (default), f16, q2k (GGUF-order formats), decode_eager (the decode step "
                          "without its HIP graph; these three not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -506,6 +541,7 @@ def main():
     sections = set() if args.no_extra else set(x.strip() for x in args.extra.split(",") if x.strip())
     want_cpu = not args.no_cpu
     cpu_in = {"q8": None, "q6": None, "gemm": {}, "dec": None}
+    q6_raw, q6_us = None, None
     if "floor" in sections:  # the plain read of the headline's weight bytes over 16 rotated buffers
         wbytes = n * (k // 256) * 144
         f = bench_read_floor(torch, A, wbytes, args.steps, args.warmup)
@@ -513,6 +549,11 @@ def main():
                                     "frac_hbm": round(f["gbs"] / HBM_PEAK_GBS, 4), "bytes": wbytes,
                                     "headline_over_floor": round(head["ms"] / f["ms"], 4)}
         print("[bench] read floor: %s" % extra["read_floor_33MB"], file=sys.stderr, flush=True)
+        lbytes = 128256 * 16 * 210  # the LM head's weight bytes (C3), two rotated buffers as its GEMV
+        f = bench_read_floor(torch, A, lbytes, max(20, args.steps // 4), max(3, args.warmup // 4), copies=2)
+        extra["read_floor_431MB"] = {"GB/s": round(f["gbs"], 1), "us": round(f["ms"] * 1e3, 3),
+                                     "frac_hbm": round(f["gbs"] / HBM_PEAK_GBS, 4), "bytes": lbytes}
+        print("[bench] read floor 431 MB: %s" % extra["read_floor_431MB"], file=sys.stderr, flush=True)
     if "q8" in sections:
         r = bench_gemv(torch, A, 8, 4096, 4096, args.steps, args.warmup, seed=0xAE7E41)
         extra["q8_0_gemv_4096x4096"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),
@@ -534,7 +575,17 @@ def main():
         print("[bench] Q6_K GEMV: %s" % extra["q6_k_gemv_128256x4096"], file=sys.stderr, flush=True)
         if want_cpu:
             cpu_in["q6"] = (r["raw0"].cpu().numpy(), r["x"].cpu().numpy())
+        q6_raw, q6_us = r["raw0"], r["ms"] * 1e3
         del r
+    if "boundary" in sections:  # host-slice calls through the plugin boundary, C2 and C3
+        b2 = bench_boundary(torch, A, 12, n, k, head["raw0"], head["ms"] * 1e3)
+        extra["boundary_q4_k_14336x4096"] = b2
+        print("[bench] boundary C2: %s" % b2, file=sys.stderr, flush=True)
+        if q6_raw is not None:
+            b3 = bench_boundary(torch, A, 14, 128256, 4096, q6_raw, q6_us, calls=10)
+            extra["boundary_q6_k_128256x4096"] = b3
+            print("[bench] boundary C3: %s" % b3, file=sys.stderr, flush=True)
+        A.lib().aeth_weight_cache_clear()
     if "q5" in sections:
         r = bench_gemv(torch, A, 13, 14336, 4096, args.steps, args.warmup, seed=0xAE7E44)
         extra["q5_k_gemv_14336x4096"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3),

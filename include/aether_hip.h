@@ -287,8 +287,9 @@ AETH_API int aeth_fill_normal_f32(uint64_t seed, float* d_out, int64_t n, float 
 /* Measurement kernel, no counterpart in the reference: reads `bytes`
  * (a multiple of 16, 16-byte aligned) once with streaming loads, the plain
  * HBM read a single launch of that size achieves (the benchmark's floor for
- * the GEMVs). d_sink holds sink_words >= 512 words; a word is written only if
- * the fold of the input hits one fixed value. */
+ * the GEMVs). d_sink holds sink_words >= 256 words (256 per workgroup used,
+ * up to 2048 workgroups); a word is written only if the fold of the input
+ * hits one fixed value. */
 AETH_API int aeth_stream_read(const void* d_src, int64_t bytes, uint32_t* d_sink, int64_t sink_words, void* stream);
 /* Measurement kernel, no counterpart in the reference: `workgroups` × 4 waves
  * each issue iters × 8 independent matrix-core instructions on register

@@ -45,6 +45,29 @@ def test_backend_causal_attention(gpu, b, s, d, heads):
     assert_close(out.reshape(b * s, d), ref.reshape(b * s, d), tol=1e-4, what="causal_attention")
 
 
+def test_backend_causal_attention_nonfinite_scores(gpu):
+    """Scores of -inf (q·k overflowing in f32) carry no weight, as the
+    reference's `row[j] != -inf` skip (cpu.rs:1705-1721) gives them: a query
+    whose early keys all overflow to -inf — a whole 64-key chunk of them, then
+    finite keys — still gets a finite row; one whose every key overflows gets
+    0; +inf scores give NaN rows on both sides."""
+    b, s, d, heads = 1, 150, 128, 1
+    rng = np.random.default_rng(9)
+    q, k, v = (rng.standard_normal((b, s, d)).astype(np.float32) for _ in range(3))
+    q[0, :, :] = np.abs(q[0]) + 1.0
+    k[0, :70, :] = -3e37   # every dot with these keys is -inf in f32 (q > 0)
+    k[0, 120, :] = 3e37    # +inf for queries 120 and later
+    scale = float(1.0 / np.sqrt(d))
+    out = np.full((b, s, d), 7.0, np.float32)
+    A.check(A.lib().aeth_backend_causal_attention(ptr(q), ptr(k), ptr(v), b, s, d, heads, scale, ptr(out)),
+            "backend_causal_attention")
+    ref = O.causal_attention(q, k, v, heads, scale)
+    assert (ref[0, :70] == 0).all() and np.isfinite(ref[0, 70:120]).all() and np.isnan(ref[0, 120:]).all()
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    fin = np.isfinite(ref)
+    assert_close(out[fin][None, :], ref[fin][None, :], tol=1e-4, what="causal_attention with -inf scores")
+
+
 def test_backend_causal_attention_errors(gpu):
     L = A.lib()
     q = np.zeros((1, 4, 8), np.float32)

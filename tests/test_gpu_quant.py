@@ -476,6 +476,36 @@ def test_gemm_q80_tiles_exponents_accumulate(gpu, m, n, k):
     check_q80_gemm(gpu, m, n, k)
 
 
+# Q8_0 block scales that are NaN or infinite (q8_0.rs decodes d as a plain f16 and adds d·Σ per
+# block): +Inf, −Inf and NaN scales in several blocks of some rows, at batch sizes that would
+# otherwise take the Q8_0 GEMM (20, 64 rows) or the dequantized DGEMM (150 rows), and one row:
+# every element equals the scalar reference's class (NaN, ±Inf) and the finite rows stay
+# within the bar.
+@pytest.mark.parametrize("m", [1, 20, 64, 150])
+def test_q80_nonfinite_block_scales(gpu, m):
+    n, k = 96, 1024
+    rng = np.random.default_rng(m + 5)
+    raw = weight(Q8_0, n, k, 77).reshape(n, k // 32, 34)
+    h = lambda bits: np.array([bits], np.uint16).view(np.uint8)
+    raw[3, 5, 0:2] = h(0x7C00)                                  # +Inf
+    raw[3, 20, 0:2] = h(0x7C00)                                 # two in one row (the rescale's Inf·0 case)
+    raw[7, 1, 0:2] = h(0xFC00)                                  # −Inf
+    raw[7, 30, 0:2] = h(0x7C00)                                 # mixed signs
+    raw[11, 9, 0:2] = h(0x7E00)                                 # NaN
+    raw[40, 2, 0:2], raw[40, 3, 0:2], raw[40, 31, 0:2] = h(0x7C00), h(0x7C00), h(0xFC00)
+    raw = raw.reshape(-1)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = make_weight(gpu, Q8_0, n, k, raw)
+    got = gemv(gpu, w, x.ravel(), n, m)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q8_0, x.ravel(), raw, m, n, k).reshape(m, n)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN pattern m=%d" % m
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref)) and np.array_equal(np.isneginf(got), np.isneginf(ref))
+    assert np.isnan(ref).any() and np.isinf(ref).any()  # the cases occur
+    fin = np.isfinite(ref)
+    assert_close(got[fin], ref[fin], what="finite entries m=%d" % m)
+
+
 # Small batches of Q6_K rows: the row-batched GEMV until m · (weight bytes) reaches 200 MB,
 # then the GEMM (aeth_q6k_gemm_rows); both sides of the boundary at three weight sizes, plain,
 # accumulate and the dot-product mode.
