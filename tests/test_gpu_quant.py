@@ -476,6 +476,33 @@ def test_gemm_q80_tiles_exponents_accumulate(gpu, m, n, k):
     check_q80_gemm(gpu, m, n, k)
 
 
+# Q4_K / Q5_K / Q6_K scales with the f16 exponent 31 (decode_d's rule, dequant.rs:161-168: such
+# bits are read as bits / 65536): a weight holding a few of them takes the GEMV instance with the
+# rule, the same weight without them the one with a plain f16 conversion; both against the oracle.
+@pytest.mark.parametrize("dtype", [Q4_K, Q5_K, Q6_K])
+@pytest.mark.parametrize("special", [False, True])
+def test_gemv_exponent31_scales(gpu, dtype, special):
+    n, k = 300, 1024
+    raw = weight(dtype, n, k, 91).reshape(n * k // 256, -1)
+    if special:
+        pats = np.array([0x7C00, 0xFC00, 0x7E01, 0x7FFF], np.uint16).view(np.uint8).reshape(4, 2)
+        rows = [3, 77, 150, 299]
+        for i, r in enumerate(rows):
+            blk = r * (k // 256) + i % (k // 256)
+            if dtype == Q6_K:
+                raw[blk, 208:210] = pats[i]
+            else:
+                raw[blk, 2 * (i & 1):2 * (i & 1) + 2] = pats[i]  # d, then dmin
+    raw = raw.reshape(-1)
+    x = np.random.default_rng(5).standard_normal(k).astype(np.float32)
+    w = make_weight(gpu, dtype, n, k, raw)
+    got = gemv(gpu, w, x, n)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(dtype, x, raw, 1, n, k)
+    assert np.isfinite(ref).all()
+    assert_close(got, ref, what="dtype %d special scales %s" % (dtype, special))
+
+
 # Q8_0 block scales that are NaN or infinite (q8_0.rs decodes d as a plain f16 and adds d·Σ per
 # block): +Inf, −Inf and NaN scales in several blocks of some rows, at batch sizes that would
 # otherwise take the Q8_0 GEMM (20, 64 rows) or the dequantized DGEMM (150 rows), and one row:
