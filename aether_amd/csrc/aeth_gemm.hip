@@ -559,9 +559,29 @@ bool aeth_q4k_gemm_rows(const aeth_weight* w, int64_t m) {
     return m >= 16 || (m >= 5 && m * w->nb * w->n * 144 >= 150000000LL);
 }
 
+bool aeth_q5k_gemm_rows(const aeth_weight* w, int64_t m) {
+    if (!w || w->dtype != AETH_DTYPE_Q5_K || w->order != AETH_ORDER_PLANAR || w->k != w->nb * 256 || m <= 1)
+        return false;
+    const int64_t mp = aeth_cdiv(m, G2_BM) * G2_BM, ntiles = aeth_cdiv(w->n, 16);
+    // buffer offsets are 32-bit (larger products take the dequantized product)
+    if (ntiles * w->nb * 2048 >= INT32_MAX || mp * w->k * 4 >= INT32_MAX || mp > (1LL << 20)) return false;
+    // AETH_Q5K_GEMM_ROWS=r takes the GEMM from r rows (tests and measurements; read once)
+    static const int64_t env_rows = getenv("AETH_Q5K_GEMM_ROWS") ? atoll(getenv("AETH_Q5K_GEMM_ROWS")) : 0;
+    if (env_rows > 0) return m >= env_rows;
+    return m >= 16 || (m >= 5 && m * w->nb * w->n * 176 >= 150000000LL);
+}
+
+// planar Q4_K or Q5_K weights at m rows that the K-split GEMM takes
+static bool kq_gemm_rows(const aeth_weight* w, int64_t m) {
+    if (!w || w->order != AETH_ORDER_PLANAR) return false;
+    if (w->dtype == AETH_DTYPE_Q4_K) return aeth_q4k_gemm_rows(w, m);
+    return aeth_q5k_gemm_rows(w, m);
+}
+
 bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {
-    if (!w || w->dtype != AETH_DTYPE_Q4_K || w->order != AETH_ORDER_PLANAR || m <= 1) return false;
-    if (!aeth_q4k_gemm_rows(w, m)) return false;  // the runner takes the GEMV path and its own producers
+    if (!w || (w->dtype != AETH_DTYPE_Q4_K && w->dtype != AETH_DTYPE_Q5_K) || w->order != AETH_ORDER_PLANAR || m <= 1)
+        return false;
+    if (!kq_gemm_rows(w, m)) return false;  // the runner takes the GEMV path and its own producers
     if (mode == PREP_PLAIN) return true;
     if (w->k != w->nb * 256) return false;  // ragged K goes to the row-batched GEMV
     if (w->k > 16384 || ((uintptr_t)d_a & 15)) return false;  // one chunk of registers per wave, float4 loads
@@ -570,8 +590,8 @@ bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a
 }
 
 bool aeth_gemm_swiglu_out(const aeth_weight* w, int64_t m) {
-    return w && w->dtype == AETH_DTYPE_Q4_K && w->order == AETH_ORDER_PLANAR && m > 1 && w->k == w->nb * 256 &&
-           (w->n & 1) == 0 && aeth_q4k_gemm_rows(w, m);
+    return w && (w->dtype == AETH_DTYPE_Q4_K || w->dtype == AETH_DTYPE_Q5_K) && w->order == AETH_ORDER_PLANAR &&
+           m > 1 && w->k == w->nb * 256 && (w->n & 1) == 0 && kq_gemm_rows(w, m);
 }
 
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
@@ -586,6 +606,9 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
         return aeth_set_error(AETH_EINVAL, "gemm: fused producer %d with Q8 activations", mode);
     if (swo && (!aeth_gemm_swiglu_out(w, m) || (flags & AETH_MM_ACCUMULATE)))
         return aeth_set_error(AETH_EINVAL, "gemm: SwiGLU output needs whole super-blocks, even n, no accumulate");
+    const bool q5 = w->dtype == AETH_DTYPE_Q5_K;
+    if (q5 && !aeth_q5k_gemm_rows(w, m))
+        return aeth_set_error(AETH_EINVAL, "gemm q5_k: shape not taken (m=%lld)", (long long)m);
     if (k != nb * 256) {  // ragged K: row-batched GEMV
         GemvEpi e;
         e.flags = flags;
@@ -608,7 +631,7 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     // The K-split kernel (aeth_gemm_kq.hip); the single-K-group kernel serves buffers past the 32-bit
     // offsets of the buffer loads, and AETH_GEMM_KERNEL=2 forces it (tests)
     static const int env_kernel = getenv("AETH_GEMM_KERNEL") ? atoi(getenv("AETH_GEMM_KERNEL")) : 0;
-    if (fits32 && env_kernel != 2) {
+    if (fits32 && (env_kernel != 2 || q5)) {
         // at most half as many tiles as CUs: K split over workgroups too, as many splits as fit in one
         // round of workgroups (each wave keeps at least one super-block), the partial tiles in the
         // stream's scratch (not with a caller's workspace)
@@ -622,7 +645,8 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
         }
         KqArgs Q{(const uint8_t*)frag, (const uint8_t*)Sh, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, (int)ntiles,
                  (int)mp, gm, gn, (int)ab, (int)(mp * (k / 32) * 4), (int)qb, (int)std::min(hb, (int64_t)INT32_MAX),
-                 d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0, ksplit, part, gn * G2_BN};
+                 d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0, ksplit, part, gn * G2_BN,
+                 q5 ? w->p3 : nullptr, q5 ? (int)(ntiles * nb * 512) : 0};
         return aeth_gemm_kq_launch(Q, s);
     }
     hipLaunchKernelGGL(k_gemm_q4k_ring, dim3((unsigned)(gm * gn)), dim3(256), 0, s, G);
@@ -746,7 +770,7 @@ int aeth_gemm_q80_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
 
 bool aeth_gemm_fused_ok(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {
     if (!w) return false;
-    if (w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_fuses(w, m, mode, d_a, norm_w);
+    if (w->dtype == AETH_DTYPE_Q4_K || w->dtype == AETH_DTYPE_Q5_K) return aeth_gemm_fuses(w, m, mode, d_a, norm_w);
     if (w->dtype == AETH_DTYPE_Q6_K) return aeth_q6k_gemm_fuses(w, m, mode, d_a, norm_w);
     if (w->dtype == AETH_DTYPE_Q8_0) return aeth_q80_gemm_fuses(w, m, mode, d_a, norm_w);
     return false;
@@ -754,13 +778,14 @@ bool aeth_gemm_fused_ok(const aeth_weight* w, int64_t m, int mode, const float* 
 
 bool aeth_gemm_swo_ok(const aeth_weight* w, int64_t m) {
     if (!w) return false;
-    if (w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_swiglu_out(w, m);
+    if (w->dtype == AETH_DTYPE_Q4_K || w->dtype == AETH_DTYPE_Q5_K) return aeth_gemm_swiglu_out(w, m);
     return w->dtype == AETH_DTYPE_Q8_0 && (w->n & 1) == 0 && aeth_q80_gemm_rows(w, m);
 }
 
 int aeth_gemm_fused_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                            hipStream_t s, int64_t ldc, const GemmIn* in) {
-    if (w->dtype == AETH_DTYPE_Q4_K) return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc, nullptr, 0, in);
+    if (w->dtype == AETH_DTYPE_Q4_K || w->dtype == AETH_DTYPE_Q5_K)
+        return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc, nullptr, 0, in);
     if (w->dtype == AETH_DTYPE_Q6_K) return aeth_gemm_q6k_launch(w, d_a, m, d_c, flags, s, ldc, in);
     if (w->dtype == AETH_DTYPE_Q8_0) return aeth_gemm_q80_launch(w, d_a, m, d_c, flags, s, ldc, in);
     return aeth_set_error(AETH_EINVAL, "gemm: no fused GEMM for dtype %d", w->dtype);

@@ -44,6 +44,21 @@ __device__ __forceinline__ half8_t dq8s(uint32_t x, uint32_t y, uint32_t x8, uin
     const uint32_t q3 = pkfma((y8 & MASK) | c64, s, z);
     return __builtin_bit_cast(half8_t, make_uint4(q0, q1, q2, q3));
 }
+// dq8s for Q5_K: q gains its fifth bit, 16 (low nibbles, MASK 0x000F000F: bit 4 of each half,
+// M5 = 0x00100010) or 256 in the in-place high nibble's units (MASK 0x00F000F0: bit 8, M5 =
+// 0x01000100), so the halves are 1024 + q5 or 1024 + 16·q5 and every result q5·sc ≤ 1953 is
+// exact. P holds the eight fifth bits of this slice's pair of sub-blocks (bits 0-3: the four
+// dwords' first halves of the low-nibble sub-block, 4-7 the high-nibble one's; bits 16-23 the
+// second halves): dword i takes its bits shifted left by 4 − i.
+template <uint32_t MASK, uint32_t M5>
+__device__ __forceinline__ half8_t dq8s5(uint32_t x, uint32_t y, uint32_t x8, uint32_t y8, uint32_t P, uint32_t c64,
+                                         half2_t s, half2_t z) {
+    const uint32_t q0 = pkfma((x & MASK) | (((P << 4) & M5) | c64), s, z);
+    const uint32_t q1 = pkfma((x8 & MASK) | (((P << 3) & M5) | c64), s, z);
+    const uint32_t q2 = pkfma((y & MASK) | (((P << 2) & M5) | c64), s, z);
+    const uint32_t q3 = pkfma((y8 & MASK) | (((P << 1) & M5) | c64), s, z);
+    return __builtin_bit_cast(half8_t, make_uint4(q0, q1, q2, q3));
+}
 template <uint32_t MASK>
 __device__ __forceinline__ half8_t dq8(uint32_t x, uint32_t y, uint32_t c64, half2_t s, half2_t z) {
     return dq8s<MASK>(x, y, x >> 8, y >> 8, c64, s, z);
@@ -70,6 +85,12 @@ template <int OFF>
 __device__ __forceinline__ u32x2 lds_b64(uint32_t a) {
     u32x2 v;
     asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_u16(uint32_t a) {
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
     return v;
 }
 // two 8-byte reads, at a and a + 256
@@ -161,6 +182,9 @@ struct KqArgs {
     int ksplit;
     float* part;
     int pld;
+    // Q5_K: the fifth-bit plane of the GEMM (aeth_weights.hip, p3), null for Q4_K
+    const uint8_t* fifth;
+    int f_bytes;
 };
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s);
 

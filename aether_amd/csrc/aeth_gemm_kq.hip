@@ -1,4 +1,4 @@
-// Q4_K prefill GEMM, K-split form (m > 1):  C[m][n] = Σ_k A[m][k]·W[n][k]
+// Q4_K and Q5_K prefill GEMM, K-split form (m > 1):  C[m][n] = Σ_k A[m][k]·W[n][k]
 // (avx2::matmul_q4_k with m rows, src/quant/avx2.rs:23-57; quantized_matmul_impl).
 //
 // Operands as in the exact mode of aeth_gemm.hip: A·2^-e split into fp16 hi/lo
@@ -32,6 +32,17 @@
 // rows' sub-block sums (2 KiB), which the wave copies to registers when it starts
 // the super-block. Per wave: 3 A slots, 2 quant slots, 1 header slot (20 KiB);
 // slice s + 2 is issued before slice s is computed.
+//
+// Q5_K (avx2::matmul_q5_k with m rows, src/quant/avx2.rs:97-131) runs the same kernel with a
+// fifth bit per quant: w = d·sc·(q + 16·h) − dmin·m, h bit 32·s + l of the block's qh for
+// element l of sub-block s (q5_k.rs:49-56). q5·sc ≤ 1953 is still an exact fp16 integer, so
+// the two MFMA passes and the min term are Q4_K's. The GEMM's fifth-bit plane (p3,
+// aeth_weights.hip) holds per 16-row tile and super-block [J 4][kg 2][row 16][half 2] 16-bit
+// words: the bits of the 8 elements a lane takes in the slice pair (J, kg), arranged for
+// dq8s5; a slice pair's words for the workgroup's 128 columns (512 B) ride in its quant slot.
+// The LDS they need comes from the header slot: the sub-block sums go to registers instead
+// (loaded a super-block ahead, after the last slice used them). Per wave: 3 A slots, 2 quant
+// slots of 2.5 KiB, 1 header slot of 2 KiB (19 KiB).
 #include <math.h>
 #include <stdint.h>
 
@@ -39,20 +50,38 @@
 #include "aeth_gemm_common.hpp"
 #include "aeth_internal.hpp"
 
-#define K8_A 4096                                       // A fragments of a slice
-#define K8_NA 3                                         // A slots
-#define K8_B 2048                                       // quants of a slice pair
-#define K8_HS 4096                                      // headers + sub-block sums of a super-block
-#define K8_BOFF (K8_NA * K8_A)                          // quant slots
-#define K8_HOFF (K8_BOFF + 2 * K8_B)                    // header slot
-#define K8_WAVE (K8_HOFF + K8_HS)                       // LDS per wave: 20 KiB
-#define K8_W 8                                          // waves
+#define K8_A 4096   // A fragments of a slice
+#define K8_NA 3     // A slots
+#define K8_W 8      // waves
 
-// buffer loads issued for slice s (s = position in the wave's run)
-__host__ __device__ constexpr int k8_loads(int s) { return 4 + ((s & 1) == 0 ? 2 : 0) + ((s & 15) == 0 ? 4 : 0); }
+// LDS of a wave: A slots, the quant slots of a slice pair (Q5_K: + its fifth bits), the
+// header slot of a super-block (Q4_K: + its sub-block sums)
+template <bool Q5>
+struct K8L {
+    static constexpr int B = Q5 ? 2560 : 2048;
+    static constexpr int HS = Q5 ? 2048 : 4096;
+    static constexpr int BOFF = K8_NA * K8_A;
+    static constexpr int HOFF = BOFF + 2 * B;
+    static constexpr int WAVE = HOFF + HS;  // 20 KiB (Q4_K), 19 KiB (Q5_K)
+};
 
-__global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
-    __shared__ __attribute__((aligned(1024))) char smem[K8_W * K8_WAVE];
+// buffer loads issued for slice s (s = position in the wave's run): A fragments, a pair's quants
+// (Q5_K: and fifth bits), a super-block's headers (Q4_K: and sums)
+template <bool Q5>
+__host__ __device__ constexpr int k8_loads(int s) {
+    return 4 + ((s & 1) == 0 ? (Q5 ? 4 : 2) : 0) + ((s & 15) == 0 ? (Q5 ? 2 : 4) : 0);
+}
+// loads allowed outstanding when slice position j starts: slice j + 1's, and at j = 0 (Q5_K) the
+// two sub-block-sum loads issued after it, at the end of the previous super-block
+template <bool Q5>
+__host__ __device__ constexpr int k8_wait(int j) {
+    return k8_loads<Q5>(j + 1) + (Q5 && j == 0 ? 2 : 0);
+}
+
+template <bool Q5>
+__global__ void __launch_bounds__(64 * K8_W) k_gemm_kq(KqArgs G) {
+    using L = K8L<Q5>;
+    __shared__ __attribute__((aligned(1024))) char smem[K8_W * L::WAVE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // workgroup → (K split ks, tile): splits of one tile are T workgroups apart, so each keeps
@@ -64,7 +93,7 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
     const int nb = G.nb, nks = G.k >> 4, ksb = G.k >> 5;
     const int lo = nb * ks / G.ksplit, len = nb * (ks + 1) / G.ksplit - lo;  // this split's super-blocks
     const int sb0 = lo + len * wave / K8_W, nsb = lo + len * (wave + 1) / K8_W - sb0, ns = 16 * nsb;
-    char* wl = smem + wave * K8_WAVE;
+    char* wl = smem + wave * L::WAVE;
     const uint32_t wl_lds = lds_addr(wl);
 
     // buffer resources; per-lane offsets are fixed, per-slice offsets go in the scalar offset
@@ -88,6 +117,10 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
         s_v[mt] = (uint32_t)(((lane >> 5) * G.mp * ksb + row * ksb) * 2);
     }
     const uint32_t a_v = (uint32_t)(lane * 16);
+    // Q5_K fifth bits, DMA piece i (4 B): lane → tile 4i + lane/16 of the workgroup's 8, row
+    // lane%16 (both halves' words), at q_v[i] / 4
+    __amdgpu_buffer_rsrc_t rF = rQ;
+    if constexpr (Q5) rF = __builtin_amdgcn_make_buffer_rsrc((void*)G.fifth, (short)0, G.f_bytes, 0x00020000);
 
     // Loads of slice s = 16·(b − sb0) + jl of this wave, into A slot sa (a byte
     // offset in the wave's LDS). Offsets are a per-super-block scalar base plus
@@ -106,32 +139,44 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void*)(st + (mt * 2 + p) * 1024), 16, a_v,
                                                          (mt ? aB1 : aB0) + kso + p * 1024, 0, 0);
         if ((jl & 1) == 0) {
-            char* sq = wl + K8_BOFF + ((jl >> 1) & 1) * K8_B;
+            char* sq = wl + L::BOFF + ((jl >> 1) & 1) * L::B;
             const int qoff = b * 2048 + (J >> 1) * 1024 + (2 * (J & 1) + kg) * 256;
 #pragma unroll
             for (int i = 0; i < 2; i++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void*)(sq + i * 1024), 16, q_v[i], qoff, 0, 0);
+            if constexpr (Q5) {
+                const int foff = b * 512 + (2 * J + kg) * 64;
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rF, (lds_void*)(sq + 2048 + i * 256), 4, q_v[i] >> 2, foff, 0,
+                                                             0);
+            }
         }
         if (jl == 0) {
-            char* hs = wl + K8_HOFF;
+            char* hs = wl + L::HOFF;
 #pragma unroll
             for (int i = 0; i < 2; i++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rH, (lds_void*)(hs + i * 1024), 16, h_v[i], b * 256, 0, 0);
+            if constexpr (!Q5) {
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(hs + 2048 + mt * 1024), 16, s_v[mt], b * 16, 0,
-                                                         0);
+                for (int mt = 0; mt < 2; mt++)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_void*)(hs + 2048 + mt * 1024), 16, s_v[mt],
+                                                             b * 16, 0, 0);
+            }
         }
     };
-
-    // LDS offsets of column tile c: quants of lane (col, k-group lane/32), header of col
-    int b_off[4], h_off[4];
+    // Q5_K: the sub-block sums of super-block b straight into registers
+    auto load_sums = [&](int b, half8_t* sv) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const int col = 32 * c + (lane & 31);
-        b_off[c] = (col >> 4) * 256 + (col & 15) * 16 + 8 * (lane >> 5);
-        h_off[c] = (col >> 4) * 256 + (col & 15) * 16;
-    }
+        for (int mt = 0; mt < 2; mt++)
+            sv[mt] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rS, s_v[mt], b * 16, 0));
+    };
+
+    // LDS offsets of column tile 0: quants of lane (col, k-group lane/32), header of col (column
+    // tile c: + 512c)
+    const int h_off = ((lane & 31) >> 4) * 256 + (lane & 15) * 16, b_off = h_off + 8 * (lane >> 5);
+    // Q5_K: this lane's fifth-bit word of column tile c in a quant slot: + 2048 + 128c
+    const int f_off = (lane & 31) * 4 + 2 * (lane >> 5);
 
     f32x16 U[2][4];
 #pragma unroll
@@ -144,22 +189,26 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
     half2_t sp[4] = {}, zp[4] = {};
     u32x2 raw[4] = {};
     uint32_t x8[4] = {}, y8[4] = {};
+    uint32_t P5[4] = {};  // Q5_K: this slice pair's fifth bits of each column (dq8s5)
     uint32_t c64;  // 0x64006400 in a VGPR (see dq8s)
     asm("v_mov_b32 %0, 0x64006400" : "=v"(c64));
 
     if (ns > 0) {
         issue(sb0, 0, 0);
         issue(sb0, 1, K8_A);
+        if constexpr (Q5) load_sums(sb0, sv);
     }
     int s3 = 0;  // (16·bi) mod 3: slice 16·bi + j uses A slot (s3 + j) mod 3
     for (int bi = 0; bi < nsb; bi++) {
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             const int nib = j & 1;
-            // slice s has landed when only slice s + 1's loads are outstanding
-            const int nxt = k8_loads(j + 1);  // 4, 6 or 10 (folded: j is unrolled)
-            if (nxt == 10) vm_wait<10>();
-            else if (nxt == 6) vm_wait<6>();
+            // slice s has landed when only slice s + 1's loads (and at j = 0 the sums, Q5_K) are
+            // outstanding
+            const int nw = k8_wait<Q5>(j);  // 4, 6, 8 or 10 (folded: j is unrolled)
+            if (nw == 10) vm_wait<10>();
+            else if (nw == 8) vm_wait<8>();
+            else if (nw == 6) vm_wait<6>();
             else vm_wait<4>();
             {
                 int sl = s3 + (j + 2) % 3;
@@ -169,17 +218,32 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
             int sc3 = s3 + j % 3;
             sc3 = sc3 >= 3 ? sc3 - 3 : sc3;
             const uint32_t sa = wl_lds + sc3 * K8_A;
-            const uint32_t sq = wl_lds + K8_BOFF + ((j >> 1) & 1) * K8_B;
+            const uint32_t sq = wl_lds + L::BOFF + ((j >> 1) & 1) * L::B;
             if (j == 0) {
-                const uint32_t hs = wl_lds + K8_HOFF;
-#pragma unroll
-                for (int c = 0; c < 4; c++) hd[c] = lds_b128<0>(hs + h_off[c]);
-                sv[0] = lds_b128h<2048>(hs + a_v);
-                sv[1] = lds_b128h<3072>(hs + a_v);
+                const uint32_t hs = wl_lds + L::HOFF;
+                hd[0] = lds_b128<0>(hs + h_off);
+                hd[1] = lds_b128<512>(hs + h_off);
+                hd[2] = lds_b128<1024>(hs + h_off);
+                hd[3] = lds_b128<1536>(hs + h_off);
+                if constexpr (!Q5) {
+                    sv[0] = lds_b128h<2048>(hs + a_v);
+                    sv[1] = lds_b128h<3072>(hs + a_v);
+                }
             }
             if (nib == 0) {
-#pragma unroll
-                for (int c = 0; c < 4; c++) raw[c] = lds_b64<0>(sq + b_off[c]);
+                raw[0] = lds_b64<0>(sq + b_off);
+                raw[1] = lds_b64<512>(sq + b_off);
+                raw[2] = lds_b64<1024>(sq + b_off);
+                raw[3] = lds_b64<1536>(sq + b_off);
+                if constexpr (Q5) {
+                    P5[0] = lds_u16<2048>(sq + f_off);
+                    P5[1] = lds_u16<2048 + 128>(sq + f_off);
+                    P5[2] = lds_u16<2048 + 256>(sq + f_off);
+                    P5[3] = lds_u16<2048 + 384>(sq + f_off);
+                }
+            }
+            if constexpr (Q5) {
+                if (j == 0) lgkm_wait<11>();  // at most 15 LDS reads outstanding: the first header read is back
             }
             half8_t a[2][2];  // [mt][part]
             a[0][0] = lds_b128h<0>(sa + a_v);
@@ -190,8 +254,10 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
             if (j == 0) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) pin(hd[c]);
-                pin(sv[0]);
-                pin(sv[1]);
+                if constexpr (!Q5) {
+                    pin(sv[0]);
+                    pin(sv[1]);
+                }
                 // entering the super-block: rescale U to this block's d (a zero d keeps the scale;
                 // its weights are zeroed through the scales below)
 #pragma unroll
@@ -231,6 +297,21 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     pin(raw[c]);
+                    if constexpr (Q5) {
+                        pin(P5[c]);
+                        P5[c] = __builtin_amdgcn_perm(0u, P5[c], 0x0C010C00u);  // word bytes → bits 0-7, 16-23
+                    } else {
+                        x8[c] = raw[c][0] >> 8;
+                        y8[c] = raw[c][1] >> 8;
+                    }
+                }
+            }
+            if constexpr (Q5) {
+                // the shifted quant words are formed in each slice (registers: Q5_K holds the fifth
+                // bits instead); a fresh name per slice keeps the two slices' shifts apart
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    if (nib == 1) pin(raw[c]);
                     x8[c] = raw[c][0] >> 8;
                     y8[c] = raw[c][1] >> 8;
                 }
@@ -238,6 +319,17 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
             half8_t bv[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
+                if constexpr (Q5) {
+                    if (nib == 0)
+                        bv[c] = dq8s5<0x000F000Fu, 0x00100010u>(raw[c][0], raw[c][1], x8[c], y8[c], P5[c], c64,
+                                                                __builtin_shufflevector(sp[c], sp[c], 0, 0),
+                                                                __builtin_shufflevector(zp[c], zp[c], 0, 0));
+                    else
+                        bv[c] = dq8s5<0x00F000F0u, 0x01000100u>(raw[c][0], raw[c][1], x8[c], y8[c], P5[c], c64,
+                                                                __builtin_shufflevector(sp[c], sp[c], 1, 1),
+                                                                __builtin_shufflevector(zp[c], zp[c], 1, 1));
+                    continue;
+                }
                 if (nib == 0)
                     bv[c] = dq8s<0x000F000Fu>(raw[c][0], raw[c][1], x8[c], y8[c], c64,
                                               __builtin_shufflevector(sp[c], sp[c], 0, 0),
@@ -277,6 +369,7 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
                         for (int r = 0; r < 16; r++) U[mt][c][r] = fmaf(ndm, q[r], U[mt][c][r]);
                     }
                 }
+                if constexpr (Q5) load_sums(sb0 + bi + 1, sv);  // the next super-block's (past the run: unread)
             }
         }
         s3 = s3 == 2 ? 0 : s3 + 1;
@@ -343,7 +436,10 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_q4k_kq(KqArgs G) {
 }
 
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s) {
-    hipLaunchKernelGGL(k_gemm_q4k_kq, dim3((unsigned)(G.gm * G.gn * G.ksplit)), dim3(64 * K8_W), 0, s, G);
+    if (G.fifth)
+        hipLaunchKernelGGL(k_gemm_kq<true>, dim3((unsigned)(G.gm * G.gn * G.ksplit)), dim3(64 * K8_W), 0, s, G);
+    else
+        hipLaunchKernelGGL(k_gemm_kq<false>, dim3((unsigned)(G.gm * G.gn * G.ksplit)), dim3(64 * K8_W), 0, s, G);
     AETH_LAUNCH_CHECK();
     if (G.ksplit == 1) return AETH_OK;
     const SplitSum S{G.part, G.ksplit, G.mp, G.pld, G.escale, G.C, G.ldc, G.m, G.n, G.accumulate, G.swiglu};

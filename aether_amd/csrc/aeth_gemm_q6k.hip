@@ -69,12 +69,6 @@ __device__ __forceinline__ u32x4 lds_2b64_2k(uint32_t a) {
     asm volatile("ds_read2st64_b64 %0, %1 offset1:4" : "=v"(v) : "v"(a));
     return v;
 }
-template <int OFF>
-__device__ __forceinline__ uint32_t lds_u16(uint32_t a) {
-    uint32_t v;
-    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
-    return v;
-}
 
 __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
     __shared__ __attribute__((aligned(1024))) char smem[K6_W * K6_WAVE];

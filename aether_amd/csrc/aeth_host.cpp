@@ -101,6 +101,7 @@ int aeth_qmatmul_ld(const aeth_weight* w, const float* d_a, int64_t m, float* d_
         return aeth_dequant_gemm_launch(w, d_a, m, d_c, ldc, flags, s);
     if (m > 1 && w->dtype == AETH_DTYPE_Q4_K && w->order == AETH_ORDER_PLANAR && aeth_q4k_gemm_rows(w, m))
         return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);
+    if (m > 1 && aeth_q5k_gemm_rows(w, m)) return aeth_gemm_q4k_launch(w, d_a, m, d_c, flags, s, ldc);  // Q5_K
     if (m > 1 && aeth_q6k_gemm_rows(w, m)) return aeth_gemm_q6k_launch(w, d_a, m, d_c, flags, s, ldc);  // Q6_K
     if (m > 1 && aeth_q80_gemm_rows(w, m)) return aeth_gemm_q80_launch(w, d_a, m, d_c, flags, s, ldc);  // Q8_0
     // the other block formats from a few hundred rows on: dequantized once, one DGEMM (instead

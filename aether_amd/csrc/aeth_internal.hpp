@@ -138,16 +138,20 @@ struct GemmIn {
 // 150 MB. Below that the GEMM's near-constant cost (its 64-row tile idles most of its
 // MFMA work) exceeds the GEMV's, which streams the weight once per row.
 bool aeth_q4k_gemm_rows(const aeth_weight* w, int64_t m);
+// The same for planar Q5_K weights (the K-split GEMM's Q5_K form): whole super-blocks, buffers
+// within its 32-bit offsets, from 16 rows or from 5 once m · (weight bytes) reaches 150 MB.
+bool aeth_q5k_gemm_rows(const aeth_weight* w, int64_t m);
 // Whether aeth_gemm_q4k_launch runs producer `mode` for this weight and A (else
-// the caller runs the producer itself): a planar Q4_K weight, m > 1, and for
+// the caller runs the producer itself): a planar Q4_K or Q5_K weight, m > 1, and for
 // the RMSNorm and SwiGLU producers whole super-blocks, k ≤ 16384 and 16-byte
 // aligned A (and norm weight).
 bool aeth_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w);
 // Whether aeth_gemm_q4k_launch can apply GemmIn::swiglu_out for this weight: a planar
-// Q4_K weight of even n and whole super-blocks, m > 1 (no accumulate).
+// Q4_K or Q5_K weight of even n and whole super-blocks, m > 1 (no accumulate).
 bool aeth_gemm_swiglu_out(const aeth_weight* w, int64_t m);
-// Q4_K prefill GEMM (m > 1); ldc = output row stride (0: n); in = the fused
-// producer (nullptr: plain A; any other mode must pass aeth_gemm_fuses).
+// Q4_K and Q5_K prefill GEMM (m > 1; Q5_K: where aeth_q5k_gemm_rows says so); ldc = output
+// row stride (0: n); in = the fused producer (nullptr: plain A; any other mode must pass
+// aeth_gemm_fuses).
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s, int64_t ldc = 0, void* ws = nullptr, size_t ws_bytes = 0,
                          const GemmIn* in = nullptr);

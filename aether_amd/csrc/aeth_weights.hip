@@ -89,7 +89,9 @@ int64_t aeth_weight_raw_bytes(int dtype, int order, int64_t n, int64_t k) {
 //  Q5_K: p0, p1 as Q4_K (header bytes 0..15; qs = bytes 48..175 in Q4_K's qs
 //        order); p2 = fifth bits [tile][b][lane][8 B], lane (n, kg) holding, per
 //        half h, the 16-bit runs of qh for its low-nibble elements
-//        (128h + 64(kg/2) + 16(kg%2) + [0,16)) and high-nibble elements (+32).
+//        (128h + 64(kg/2) + 16(kg%2) + [0,16)) and high-nibble elements (+32);
+//        p3 = the same bits again for the GEMM (aeth_gemm_kq.hip), [tile][b][J 4][kg 2]
+//        [row 16][half 2] 16-bit words (k_q5_gemm_bits).
 //  Q6_K: p0 = [tile][b][part][lane][16 B], lane (n, kg = 2h + g'): part 0 =
 //        ql[64h + 16g', +16), part 1 = ql[64h + 32 + 16g', +16), part 2 =
 //        qh[32h + 16g', +16); p1 = sc [tile][b][16 rows][16 B]; p2 = d [tile][b][16 rows].
@@ -184,6 +186,31 @@ static int relayout(aeth_weight* w, uint8_t* d_raw, int to_planar, hipStream_t s
     return AETH_OK;
 }
 
+// The Q5_K GEMM's fifth-bit words (aeth_gemm_kq.hip). GEMM lane half h of slice pair (J, kg)
+// takes elements l = 16kg + 8h + p (p = 0..7) of sub-blocks 2J and 2J + 1, whose fifth bits
+// (bit 32·s + l of qh) are bits p of qh bytes 8J + 2kg + h and 8J + 4 + 2kg + h. The word holds
+// them in the order of the MFMA operand's halves: bits 0-3 the low sub-block's p = 0, 1, 4, 5,
+// bits 4-7 the high sub-block's, bits 8-11 and 12-15 the same for p = 2, 3, 6, 7. One thread
+// per (row, super-block) of the raw [n][nb] blocks; the padding rows stay zero.
+__device__ __forceinline__ uint32_t q5_pick(uint32_t v, int a, int b, int c, int d) {
+    return ((v >> a) & 1u) | (((v >> b) & 1u) << 1) | (((v >> c) & 1u) << 2) | (((v >> d) & 1u) << 3);
+}
+__global__ void k_q5_gemm_bits(const uint8_t* __restrict__ raw, int64_t n, int64_t nb, uint8_t* __restrict__ p3) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * nb) return;
+    const int64_t row = i / nb, b = i - row * nb;
+    const uint8_t* qh = raw + i * Q5K_BLOCK_BYTES + 16;
+    uint16_t* dst = (uint16_t*)(p3 + ((row >> 4) * nb + b) * 512) + (row & 15) * 2;
+    for (int J = 0; J < 4; J++)
+        for (int kg = 0; kg < 2; kg++)
+            for (int h = 0; h < 2; h++) {
+                const uint32_t lo = qh[8 * J + 2 * kg + h], hi = qh[8 * J + 4 + 2 * kg + h];
+                const uint32_t w = q5_pick(lo, 0, 1, 4, 5) | (q5_pick(hi, 0, 1, 4, 5) << 4) |
+                                   (q5_pick(lo, 2, 3, 6, 7) << 8) | (q5_pick(hi, 2, 3, 6, 7) << 12);
+                dst[(J * 2 + kg) * 32 + h] = (uint16_t)w;
+            }
+}
+
 // Raw (GGUF-order or row) weights: the bytes as given, one allocation.
 static int create_raw(int dtype, int order, int64_t n, int64_t k, const void* raw, int raw_is_device, hipStream_t s,
                       aeth_weight** out) {
@@ -263,7 +290,12 @@ int aeth_weight_create_ex(int dtype, int order, int64_t n, int64_t k, const void
     int64_t sz[4] = {0, 0, 0, 0};
     const int64_t prow = aeth_cdiv(n, 16) * 16;  // whole 16-row tiles
     if (dtype == AETH_DTYPE_Q4_K) { sz[0] = prow * w->nb * 16; sz[1] = prow * w->nb * 128; }
-    else if (dtype == AETH_DTYPE_Q5_K) { sz[0] = prow * w->nb * 16; sz[1] = prow * w->nb * 128; sz[2] = prow * w->nb * 32; }
+    else if (dtype == AETH_DTYPE_Q5_K) {
+        sz[0] = prow * w->nb * 16;
+        sz[1] = prow * w->nb * 128;
+        sz[2] = prow * w->nb * 32;
+        sz[3] = prow * w->nb * 32;
+    }
     else if (dtype == AETH_DTYPE_Q6_K) { sz[0] = prow * w->nb * 192; sz[1] = prow * w->nb * 16; sz[2] = prow * w->nb * 2; }
     else { const int64_t pb = aeth_cdiv(w->nb, 4) * 4; sz[0] = prow * pb * 32; sz[1] = prow * pb * 2; }
     int64_t off[4], tot = 0;
@@ -309,6 +341,12 @@ int aeth_weight_create_ex(int dtype, int order, int64_t n, int64_t k, const void
         }
     }
     rc = relayout(w, staging, 1, s, (int*)(w->base + flag_off));
+    if (rc == AETH_OK && dtype == AETH_DTYPE_Q5_K) {
+        hipLaunchKernelGGL(k_q5_gemm_bits, dim3((unsigned)aeth_cdiv(n * w->nb, 256)), dim3(256), 0, s, staging, n,
+                           w->nb, w->p3);
+        const hipError_t le = hipGetLastError();
+        if (le != hipSuccess) rc = aeth_set_error(AETH_EHIP, "aeth_weight_create: launch failed: %s", hipGetErrorString(le));
+    }
     int special = 0;
     if (rc == AETH_OK) {
         hipError_t e2 = hipMemcpyAsync(&special, w->base + flag_off, sizeof(int), hipMemcpyDeviceToHost, s);

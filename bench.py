@@ -498,9 +498,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--extra",
-                    default="floor,q8,q6,boundary,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,gemm_q80,decode,q4_k_m,q8_0_model",
+                    default="floor,q8,q6,boundary,q5,dotprod,mfma,gemm,gemm_q8,gemm_q6k,gemm_q5k,gemm_q80,decode,q4_k_m,q8_0_model",
                     help="comma-separated extra sections to run: floor, q8, q6, boundary (host-slice calls; after q6), "
-                         "q5, dotprod, gemm, gemm_q8, gemm_q6k, gemm_q80, "
+                         "q5, dotprod, gemm, gemm_q8, gemm_q6k, gemm_q5k, gemm_q80, "
                          "decode, q4_k_m, q8_0_model (default), f16, q2k (GGUF-order formats), decode_eager (the decode step "
                          "without its HIP graph; these three not run by default)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -645,6 +645,15 @@ def main():
             if mfma:  # three passes: the ceiling is a third of the fp16 rate
                 extra[key]["frac_exact_mode_ceiling"] = round(r["tflops"] / (mfma["fp16_TFLOP/s"] / 3), 4)
             print("[bench] Q6_K GEMM m=512 n=%d k=%d: %s" % (nn, kk, extra[key]), file=sys.stderr, flush=True)
+    if "gemm_q5k" in sections:  # the Q5_K GEMM (a Q5_K_M file's q, k, o, gate and up projections)
+        for nn, kk in ((4096, 4096), (14336, 4096)):
+            r = bench_batched(torch, A, 13, nn, kk, 512, max(3, min(args.steps, 20)), 2)
+            key = "q5_k_gemm_m512_n%d_k%d" % (nn, kk)
+            extra[key] = {"TFLOP/s": round(r["tflops"], 2), "ms": round(r["ms"], 4),
+                          "path": "Q5_K GEMM: exact mode, two fp16 MFMA passes per product"}
+            if mfma:
+                extra[key]["frac_exact_mode_ceiling"] = round(r["tflops"] / (mfma["fp16_TFLOP/s"] / 2), 4)
+            print("[bench] Q5_K GEMM m=512 n=%d k=%d: %s" % (nn, kk, extra[key]), file=sys.stderr, flush=True)
     if "gemm_q80" in sections:  # the Q8_0 GEMM (a Q8_0 file's prefill projections)
         for nn, kk in ((4096, 4096), (4096, 14336)):
             r = bench_batched(torch, A, 8, nn, kk, 512, max(3, min(args.steps, 20)), 2)

@@ -229,11 +229,12 @@ def test_runner_decode_matches_oracle(gpu, layer_dtype):
 
 # Batched prefill (forward_batch) against the oracle's restatement: one query /
 # key block (37), a full cache (64), a single token, and several ragged blocks
-# with the GEMM path (150 of 192); GEMM for Q4_K and Q8_0 from 16 tokens (the fused
+# with the GEMM path (150 of 192); GEMM for Q4_K, Q5_K and Q8_0 from 16 tokens (the fused
 # RMSNorm prep and SwiGLU output included), the row-batched GEMV and standalone RMSNorm /
 # SwiGLU below that (5, 12) and for the other formats.
 @pytest.mark.parametrize("layer_dtype,n,max_seq", [(Q4_K, 37, 64), (Q8_0, 64, 64), (Q6_K, 1, 64), (Q4_K, 150, 192),
-                                                   (Q5_K, 40, 64), (Q4_K, 5, 64), (Q4_K, 12, 64), (Q8_0, 150, 192)])
+                                                   (Q5_K, 40, 64), (Q4_K, 5, 64), (Q4_K, 12, 64), (Q8_0, 150, 192),
+                                                   (Q5_K, 150, 192)])
 def test_runner_prefill_matches_oracle(gpu, layer_dtype, n, max_seq):
     c = dict(TINY, max_seq_len=max_seq)
     m = build_tiny(seed=7, layer_dtype=layer_dtype)

@@ -363,6 +363,110 @@ def test_q4k_small_batches(gpu, m, n, k):
     assert_close(got_q8, ref_q8, what="q4_k dot-product mode m=%d n=%d k=%d" % (m, n, k))
 
 
+def check_q5k_gemm(torch, m, n, k):
+    """Q5_K product of m rows against the oracle (avx2::matmul_q5_k with m rows), as
+    check_q4k_gemm: per-row exponents (2^20, 2^-12, a zero row, a block of 2^15 rows past
+    fp16 range), plain, accumulate and the dot-product mode. The fifth bits are random, so
+    quants reach 31 and rows of magnitude 1 are anchored on the float64 product of the same
+    operands too (as check_q6k_gemm explains)."""
+    rng = np.random.default_rng(m * 43 + n * 13 + k)
+    raw = weight(Q5_K, n, k, 11 * n + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    scale = np.ones(m, dtype=np.float32)
+    scale[m // 3] = 2.0 ** 20
+    scale[m // 2] = 2.0 ** -12
+    scale[(2 * m) // 3] = 0.0
+    if m > 40:
+        scale[33:40] = 2.0 ** 15
+    x *= scale[:, None]
+    w = make_weight(torch, Q5_K, n, k, raw)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    got = gemv(torch, w, x.ravel(), n, m)
+    got_acc = gemv(torch, w, x.ravel(), n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    got_q8 = gemv(torch, w, x.ravel(), n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q5_K, x.ravel(), raw, m, n, k).reshape(m, n)
+    plain = scale == 1.0
+    w64 = O.dequant(Q5_K, raw, n * k).reshape(n, k).astype(np.float64)
+    ex = x[plain].astype(np.float64) @ w64.T
+    what = "q5_k m=%d n=%d k=%d" % (m, n, k)
+    assert_close_logits(got[plain], ref[plain], floor=0.0, exact=ex, what=what)
+    assert_close_rows(got, ref, what=what + " (scaled rows)")
+    assert_close_logits(got_acc[plain], (ref + y0)[plain], floor=0.0, exact=ex + y0[plain], what=what + " accumulate")
+    assert np.all(got[(2 * m) // 3] == 0.0)
+    aq = O.quantize_activations_q8_0(x.ravel(), m, k)
+    ref_q8 = O.dotprod_ref(Q5_K, aq, raw, m, n, k).reshape(m, n)
+    ex_q8 = O.dequant(Q8_0, aq, m * k).reshape(m, k)[plain].astype(np.float64) @ w64.T
+    assert_close_rows(got_q8, ref_q8, what=what + " dot-product mode")
+    assert_close_logits(got_q8[plain], ref_q8[plain], floor=0.0, exact=ex_q8, what=what + " dot-product mode")
+
+
+# The Q5_K GEMM (the K-split kernel's Q5_K form: planar Q5_K, whole super-blocks, from 16
+# rows): super-block counts that split unevenly over its 8 waves, K split over workgroups
+# where the tiles are fewer than the CUs (the last four shapes), m and n off the 64 × 128 grid.
+@pytest.mark.parametrize("m,n,k", [(70, 130, 768), (65, 300, 1024), (130, 40, 2560), (16, 16, 512), (45, 48, 16384),
+                                   (34, 64, 20480), (37, 96, 8192), (200, 100, 14336)])
+def test_gemm_q5k_tiles_exponents_accumulate(gpu, m, n, k):
+    check_q5k_gemm(gpu, m, n, k)
+
+
+def test_gemm_q5k_without_fifth_bits_is_the_q4k_gemm(gpu):
+    """A Q5_K weight whose qh bytes are all zero is the Q4_K weight with the same d, dmin,
+    scales and qs (q5_k.rs:49-56 adds 16 per set bit): the Q5_K GEMM's result equals the Q4_K
+    GEMM's bit for bit (same kernel frame, same K split, every operand exact), and setting
+    every fifth bit moves each output by 16·Σ d·sc·x, the product of a weight whose q are all
+    16 and whose mins are zero (anchored on float64)."""
+    m, n, k = 70, 200, 2048
+    rng = np.random.default_rng(5)
+    q4 = weight(Q4_K, n, k, 77).reshape(-1, 144)
+    q5 = np.zeros((q4.shape[0], 176), np.uint8)
+    q5[:, 0:16] = q4[:, 0:16]
+    q5[:, 48:176] = q4[:, 16:144]
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    outs = []
+    for dt, raw in ((Q4_K, q4.reshape(-1)), (Q5_K, q5.reshape(-1))):
+        w = make_weight(gpu, dt, n, k, raw)
+        outs.append(gemv(gpu, w, x.ravel(), n, m))
+        A.lib().aeth_weight_free(w)
+    assert np.array_equal(outs[0], outs[1])
+    q5[:, 16:48] = 0xFF
+    w = make_weight(gpu, Q5_K, n, k, q5.reshape(-1))
+    got = gemv(gpu, w, x.ravel(), n, m)
+    A.lib().aeth_weight_free(w)
+    w64 = O.dequant(Q5_K, q5.reshape(-1), n * k).reshape(n, k).astype(np.float64)
+    w64_4 = O.dequant(Q4_K, q4.reshape(-1), n * k).reshape(n, k).astype(np.float64)
+    ex = x.astype(np.float64) @ w64.T
+    assert np.abs(w64 - w64_4).max() > 0  # the bits matter
+    ref = O.reference_matmul(Q5_K, x.ravel(), q5.reshape(-1), m, n, k).reshape(m, n)
+    assert_close_logits(got, ref, floor=0.0, exact=ex, what="q5_k, every fifth bit set")
+
+
+# Small batches of Q5_K rows: the row-batched GEMV below 16 rows unless m · (weight bytes)
+# reaches 150 MB from 5 rows, else the GEMM (aeth_q5k_gemm_rows); both sides of each boundary.
+@pytest.mark.parametrize("m,n,k", [(15, 4096, 4096), (16, 4096, 4096), (4, 14336, 4096), (5, 14336, 4096),
+                                   (4, 4096, 14336), (5, 4096, 14336)])
+def test_q5k_small_batches(gpu, m, n, k):
+    rng = np.random.default_rng(m * 103 + n + k)
+    raw = weight(Q5_K, n, k, 7 * n + m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = make_weight(gpu, Q5_K, n, k, raw)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    got = gemv(gpu, w, x.ravel(), n, m)
+    got_acc = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    got_q8 = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q5_K, x.ravel(), raw, m, n, k).reshape(m, n)
+    w64 = O.dequant(Q5_K, raw, n * k).reshape(n, k).astype(np.float64)
+    ex = x.astype(np.float64) @ w64.T
+    what = "q5_k m=%d n=%d k=%d" % (m, n, k)
+    assert_close_logits(got, ref, floor=0.0, exact=ex, what=what)
+    assert_close_logits(got_acc, ref + y0, floor=0.0, exact=ex + y0, what=what + " accumulate")
+    aq = O.quantize_activations_q8_0(x.ravel(), m, k)
+    ref_q8 = O.dotprod_ref(Q5_K, aq, raw, m, n, k).reshape(m, n)
+    ex_q8 = O.dequant(Q8_0, aq, m * k).reshape(m, k).astype(np.float64) @ w64.T
+    assert_close_logits(got_q8, ref_q8, floor=0.0, exact=ex_q8, what=what + " dot-product mode")
+
+
 def check_q6k_gemm(torch, m, n, k):
     """Q6_K product of m rows against the oracle: per-row exponents (2^20, 2^-12, a zero
     row, a block of 2^15 rows past fp16 range when m > 40), plain, accumulate and the
@@ -901,18 +1005,17 @@ def test_q6k_gemm_small_weights(gpu):
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-2000:]
 
 
-# Batched products of the block formats without a GEMM kernel of their own (and
-# Q6_K rows the Q6_K GEMM does not take: k not a whole number of super-blocks):
-# below a per-format row count (Q8_0 112, Q5_K and Q6_K 80) the row-batched
-# GEMV, from it the weight dequantized once and one DGEMM — planar Q8_0 / Q5_K /
-# Q6_K rows (including Q8_0's ragged k and K-quant rows whose tail past k/256
+# Batched products of the rows the format's GEMM does not take (k not a whole number of
+# blocks / super-blocks): below a per-format row count (Q8_0 112, Q5_K and Q6_K 80) the
+# row-batched GEMV, from it the weight dequantized once and one DGEMM — planar Q8_0 /
+# Q5_K / Q6_K rows (including Q8_0's ragged k and K-quant rows whose tail past k/256
 # blocks the reference ignores), accumulate, and the dot-product mode's Q8_0
-# activation blocks, on both paths. Q6_K with whole super-blocks takes the Q6_K GEMM
-# once m · weight bytes reaches 200 MB (the 150-row case here), else the GEMV.
+# activation blocks, on both paths. With whole blocks the Q8_0, Q5_K and Q6_K GEMMs
+# take the product (the Q8_0 150-row, Q5_K 70- and 300-row and Q6_K 150-row cases).
 @pytest.mark.parametrize("dtype,m,n,k", [(Q8_0, 16, 300, 1000), (Q8_0, 400, 128, 1000), (Q8_0, 150, 512, 4096),
                                          (Q5_K, 70, 256, 2048), (Q5_K, 300, 64, 2048), (Q6_K, 150, 1024, 4096),
                                          (Q6_K, 260, 96, 4096), (Q6_K, 33, 96, 14336), (Q5_K, 20, 64, 600),
-                                         (Q6_K, 100, 200, 1100), (Q6_K, 40, 64, 1300)])
+                                         (Q5_K, 100, 64, 600), (Q6_K, 100, 200, 1100), (Q6_K, 40, 64, 1300)])
 def test_batched_dequant_gemm(gpu, dtype, m, n, k):
     rng = np.random.default_rng(m + n + k + dtype)
     raw = weight(dtype, n, k, 5 * n + k)
