@@ -177,8 +177,9 @@ struct AttnArgs {
 
 // Thread layout (512 threads = 8 waves, two per SIMD; chunk of T = 64
 // positions, HD = 128):
-//  scores: thread (p = tid/8, eighth e = tid%8) holds K[p][16e, +16) and dots
-//          it with every query head of the group; 8-lane reduction.
+//  scores: thread (p = tid/8, e = tid%8) holds K[p][32i + 4e, +4) for i < 4
+//          (each load instruction reads 128 contiguous bytes of 8 rows) and
+//          dots it with every query head of the group; 8-lane reduction.
 //  P·V:    thread (dims 4(tid%32), position group pg = tid/32) holds
 //          V[4pg + j][4(tid%32), +4) for j < 4; lanes l, l+32 and then the
 //          8 waves are summed.
@@ -188,7 +189,7 @@ template <int HD, int NT>
 __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
     static_assert(HD == 128 && (NT == 512 || NT == 1024), "decode attention is laid out for head_dim 128");
     constexpr int HALF = HD / 2, NWV = NT / 64;
-    constexpr int LP = NT / 64, KD = HD / LP, K4 = KD / 4;  // scores: lanes per position, dims per lane
+    constexpr int LP = NT / 64, K4 = HD / LP / 4;  // scores: lanes per position, float4s per lane
     constexpr int PP = 2048 / NT;                            // P·V: positions per thread
     __shared__ __attribute__((aligned(16))) float qs[ATTN_MAX_GROUPS][HD];
     __shared__ __attribute__((aligned(16))) float knew[HD];
@@ -244,9 +245,9 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
     const int sp = tid / LP, qe = tid % LP;
     float4 kk[K4];
     {
-        const float4* kr = (const float4*)(K + (t0 + min(sp, nt - 1)) * HD + KD * qe);
+        const float* kr = K + (t0 + min(sp, nt - 1)) * HD + 4 * qe;
 #pragma unroll
-        for (int i = 0; i < K4; i++) kk[i] = kr[i];
+        for (int i = 0; i < K4; i++) kk[i] = *(const float4*)(kr + 4 * LP * i);
     }
     const int vd4 = tid & 31, pg = tid >> 5;
     float4 vv[PP];
@@ -282,7 +283,7 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
     const bool knew_here = has_new && t0 + sp == fill;
     if (knew_here) {
 #pragma unroll
-        for (int i = 0; i < K4; i++) kk[i] = *(const float4*)(&knew[KD * qe + 4 * i]);
+        for (int i = 0; i < K4; i++) kk[i] = *(const float4*)(&knew[4 * qe + 4 * LP * i]);
     }
 #pragma unroll
     for (int g = 0; g < ATTN_MAX_GROUPS; g++) {
@@ -290,7 +291,7 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
             float a = 0.0f;
 #pragma unroll
             for (int i = 0; i < K4; i++) {
-                const float4 qv = *(const float4*)(&qs[g][KD * qe + 4 * i]);
+                const float4 qv = *(const float4*)(&qs[g][4 * qe + 4 * LP * i]);
                 a += qv.x * kk[i].x + qv.y * kk[i].y + qv.z * kk[i].z + qv.w * kk[i].w;
             }
             a += aeth_dpp_xor1f(a);
@@ -364,53 +365,43 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
 // Merge of the chunk partials of one query head (grid = n_heads, HD threads):
 // out = Σ_c e^{m_c-M} o_c / Σ_c e^{m_c-M} l_c. A separate launch: a kernel
 // boundary makes every chunk's partials visible across the XCDs' L2s, which a
-// device-scope fence inside one kernel would buy with L2 write-backs. Thread d
-// loads its column of up to 64 chunks at a time in one batch; the chunk
-// statistics are loaded first.
+// device-scope fence inside one kernel would buy with L2 write-backs.
+// Every wave reduces the chunk statistics itself — lane c holds chunk c (and
+// c + 64 past 4096 positions), the weights reach the other lanes by readlane —
+// so the kernel has no LDS traffic and no barrier. Thread d loads its column of
+// the first 64 chunk slots in one batch together with the statistics, before
+// the sequence length is known; slots past the live chunks are never used.
 template <int HD>
 __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
-    static_assert(ATTN_MAX_CHUNKS <= HD, "one thread per chunk statistic");
-    constexpr int CB = 64;  // one load batch up to seq 4096
-    __shared__ float cw[ATTN_MAX_CHUNKS];
-    __shared__ float red[HD / 64][2];
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    static_assert(ATTN_MAX_CHUNKS <= 128, "two chunk statistics per lane");
+    constexpr int CB = 64;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const float* base = A.ws + (int64_t)h * A.max_chunks * (HD + 2);
+    const int cmax = A.max_chunks - 1;
+    const float* s0 = base + (int64_t)min(lane, cmax) * (HD + 2) + HD;
+    const float* s1 = base + (int64_t)min(lane + 64, cmax) * (HD + 2) + HD;
+    float m0 = s0[0], l0 = s0[1], m1 = s1[0], l1 = s1[1];
+    float v[CB];
+#pragma unroll
+    for (int j = 0; j < CB; j++) v[j] = base[(int64_t)min(j, cmax) * (HD + 2) + tid];
     int64_t seq = A.st ? (int64_t)A.st[2] + 1 : A.seq_host;
     if (seq > A.max_seq) seq = A.max_seq;
     const int nch = (int)((seq + ATTN_T - 1) / ATTN_T);
     const int c_lo = A.window > 0 && seq > A.window ? (int)((seq - A.window) / ATTN_T) : 0;  // chunks before: none
-    const float* base = A.ws + (int64_t)h * A.max_chunks * (HD + 2);
-    float mc = -INFINITY, lc = 0.0f;
-    if (tid >= c_lo && tid < nch) {
-        mc = base[(int64_t)tid * (HD + 2) + HD];
-        lc = base[(int64_t)tid * (HD + 2) + HD + 1];
-    }
-    float v[CB];
-#pragma unroll
-    for (int j = 0; j < CB; j++) v[j] = base[(int64_t)min(j, nch - 1) * (HD + 2) + tid];
-    float M = aeth_wave_max(mc);
-    if (lane == 0) red[wave][0] = M;
-    __syncthreads();
-    M = red[0][0];
-#pragma unroll
-    for (int w = 1; w < HD / 64; w++) M = fmaxf(M, red[w][0]);
-    const float wgt = tid >= c_lo && tid < nch ? expf(mc - M) : 0.0f;
-    float L = aeth_wave_sum(wgt * lc);
-    if (lane == 0) red[wave][1] = L;
-    if (tid < nch) cw[tid] = wgt;
-    __syncthreads();
-    L = 0.0f;
-#pragma unroll
-    for (int w = 0; w < HD / 64; w++) L += red[w][1];
+    const bool in0 = lane >= c_lo && lane < nch, in1 = lane + 64 >= c_lo && lane + 64 < nch;
+    const float M = aeth_wave_max(fmaxf(in0 ? m0 : -INFINITY, in1 ? m1 : -INFINITY));
+    const float w0 = in0 ? expf(m0 - M) : 0.0f, w1 = in1 ? expf(m1 - M) : 0.0f;
+    const float L = aeth_wave_sum(w0 * l0 + w1 * l1);
+    // selects, not branches: a branch per chunk let the compiler sink each load into it
     float acc = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += CB) {
-        if (c0 > 0) {
 #pragma unroll
-            for (int j = 0; j < CB; j++) v[j] = base[(int64_t)min(c0 + j, nch - 1) * (HD + 2) + tid];
-        }
-#pragma unroll
-        for (int j = 0; j < CB; j++)
-            if (c0 + j >= c_lo && c0 + j < nch) acc += cw[c0 + j] * v[j];
+    for (int j = 0; j < CB; j++) {
+        const bool live = j >= c_lo && j < nch;
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w0), j));
+        acc += (live ? wj : 0.0f) * (live ? v[j] : 0.0f);
     }
+    for (int c = max(CB, c_lo); c < nch; c++)  // past 4096 positions
+        acc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w1), c - CB)) * base[(int64_t)c * (HD + 2) + tid];
     A.out[(int64_t)h * HD + tid] = acc / L;
 }
 
