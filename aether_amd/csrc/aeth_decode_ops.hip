@@ -152,12 +152,12 @@ int aeth_kv_append_launch(float* layer_kv, const float* k, const float* v, int64
 // A sliding window w (attn_direct's sliding_window, runner.rs:1768-1777)
 // masks the positions before seq - w: chunks wholly before it return at
 // once, and the merge leaves them out.
-#define ATTN_T 64
-#define ATTN_MAX_GROUPS 8
-#define ATTN_MAX_CHUNKS 128  // max_seq <= 8192
 #ifndef ATTN_NT
-#define ATTN_NT 512  // threads of k_attn (512 or 1024; 1024 measured 7 % slower at seq 2049)
+#define ATTN_NT 512  // threads of k_attn (256, 512 or 1024; 256 measured 5 %, 1024 7 % slower at seq 2049)
 #endif
+#define ATTN_T (ATTN_NT == 1024 ? 64 : ATTN_NT / 8)  // positions per chunk: 8 lanes per position (16 at 1024)
+#define ATTN_MAX_GROUPS 8
+#define ATTN_MAX_CHUNKS (8192 / ATTN_T)  // max_seq <= 8192
 
 struct AttnArgs {
     const float* q;      // [n_heads][hd] (already rotated) when qkv == nullptr
@@ -176,7 +176,7 @@ struct AttnArgs {
 };
 
 // Thread layout (512 threads = 8 waves, two per SIMD; chunk of T = 64
-// positions, HD = 128):
+// positions, HD = 128; 256 threads take T = 32 the same way):
 //  scores: thread (p = tid/8, e = tid%8) holds K[p][32i + 4e, +4) for i < 4
 //          (each load instruction reads 128 contiguous bytes of 8 rows) and
 //          dots it with every query head of the group; 8-lane reduction.
@@ -187,14 +187,17 @@ struct AttnArgs {
 // the order q/rope inputs → K → V, so each phase waits only for its own data.
 template <int HD, int NT>
 __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
-    static_assert(HD == 128 && (NT == 512 || NT == 1024), "decode attention is laid out for head_dim 128");
+    static_assert(HD == 128 && (NT == 256 || NT == 512 || NT == 1024), "decode attention is laid out for head_dim 128");
     constexpr int HALF = HD / 2, NWV = NT / 64;
-    constexpr int LP = NT / 64, K4 = HD / LP / 4;  // scores: lanes per position, float4s per lane
-    constexpr int PP = 2048 / NT;                            // P·V: positions per thread
+    constexpr int LP = NT == 1024 ? 16 : 8, K4 = HD / LP / 4;  // scores: lanes per position, float4s per lane
+    constexpr int T = NT / LP;                                  // positions per chunk (ATTN_T)
+    constexpr int PP = T * HD / 4 / NT;                         // P·V: positions per thread
+    constexpr int QP = (ATTN_MAX_GROUPS * HALF + NT - 1) / NT;  // rotation pairs of q per thread
+    static_assert(T == ATTN_T && PP * (NT / 32) == T, "chunk layout");
     __shared__ __attribute__((aligned(16))) float qs[ATTN_MAX_GROUPS][HD];
     __shared__ __attribute__((aligned(16))) float knew[HD];
     __shared__ __attribute__((aligned(16))) float vnew[HD];
-    __shared__ float sc[ATTN_MAX_GROUPS][ATTN_T];
+    __shared__ float sc[ATTN_MAX_GROUPS][T];
     __shared__ __attribute__((aligned(16))) float ov[NWV][ATTN_MAX_GROUPS][HD];
     __shared__ float mstat[ATTN_MAX_GROUPS][2];
     const int kvh = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -230,13 +233,14 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
     const float* cos_t = fused ? A.cos_t : qsrc;
     const float* ksrc = fused ? A.qkv + (int64_t)A.n_heads * HD + (int64_t)kvh * HD : qsrc;
     const float* vsrc = fused ? A.qkv + (int64_t)(A.n_heads + A.kv_heads) * HD + (int64_t)kvh * HD : qsrc;
-    float qx0, qx1, qsn, qcs;
-    {
-        const int i = min(tid, groups * HALF - 1), g = i / HALF, e = i - g * HALF;
-        qx0 = qsrc[g * HD + e];
-        qx1 = qsrc[g * HD + e + HALF];
-        qsn = sin_t[prow * HALF + e];
-        qcs = cos_t[prow * HALF + e];
+    float qx0[QP], qx1[QP], qsn[QP], qcs[QP];
+#pragma unroll
+    for (int u = 0; u < QP; u++) {
+        const int i = min(tid + u * NT, groups * HALF - 1), g = i / HALF, e = i - g * HALF;
+        qx0[u] = qsrc[g * HD + e];
+        qx1[u] = qsrc[g * HD + e + HALF];
+        qsn[u] = sin_t[prow * HALF + e];
+        qcs[u] = cos_t[prow * HALF + e];
     }
     const float kx0 = ksrc[tid & (HALF - 1)], kx1 = ksrc[(tid & (HALF - 1)) + HALF];
     const float vx = vsrc[tid & (HD - 1)];
@@ -256,20 +260,25 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
     // Consume the q / rope inputs here, after the K/V batch is issued: otherwise the
     // compiler sinks their loads into the conditional stores below, behind K and V.
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" : "+v"(qx0), "+v"(qx1), "+v"(qsn), "+v"(qcs));
+#pragma unroll
+    for (int u = 0; u < QP; u++) asm volatile("" : "+v"(qx0[u]), "+v"(qx1[u]), "+v"(qsn[u]), "+v"(qcs[u]));
     float kvx[3] = {kx0, kx1, vx};
     asm volatile("" : "+v"(kvx[0]), "+v"(kvx[1]), "+v"(kvx[2]));
 
     // 3. rotated q (and the new k / v) to LDS
-    if (tid < groups * HALF) {
-        const int g = tid / HALF, e = tid - g * HALF;
-        qs[g][e] = fused ? qx0 * qcs - qx1 * qsn : qx0;
-        qs[g][e + HALF] = fused ? qx0 * qsn + qx1 * qcs : qx1;
+#pragma unroll
+    for (int u = 0; u < QP; u++) {
+        const int i = tid + u * NT;
+        if (i < groups * HALF) {
+            const int g = i / HALF, e = i - g * HALF;
+            qs[g][e] = fused ? qx0[u] * qcs[u] - qx1[u] * qsn[u] : qx0[u];
+            qs[g][e + HALF] = fused ? qx0[u] * qsn[u] + qx1[u] * qcs[u] : qx1[u];
+        }
     }
     if (fused) {
         if (tid < HALF) {  // the pair of thread tid < HALF is (head 0, e = tid): same table entries
-            knew[tid] = kvx[0] * qcs - kvx[1] * qsn;
-            knew[tid + HALF] = kvx[0] * qsn + kvx[1] * qcs;
+            knew[tid] = kvx[0] * qcs[0] - kvx[1] * qsn[0];
+            knew[tid + HALF] = kvx[0] * qsn[0] + kvx[1] * qcs[0];
         }
         if (tid < HD) vnew[tid] = kvx[2];
     }
@@ -302,21 +311,20 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
         }
     }
     __syncthreads();
-    // 5. softmax over the chunk: wave w handles head w
-    if (wave < groups) {
-        const int g = wave;
-        const float sv = sc[g][lane];
+    // 5. softmax over the chunk: wave w handles heads w, w + NWV, ...
+    for (int g = wave; g < groups; g += NWV) {
+        const float sv = lane < T ? sc[g][lane] : -INFINITY;
         const float m = aeth_wave_max(sv);
         const float pr = lane < nt ? expf(sv - m) : 0.0f;
         const float l = aeth_wave_sum(pr);
-        sc[g][lane] = pr;
+        if (lane < T) sc[g][lane] = pr;
         if (lane == 0) {
             mstat[g][0] = m;
             mstat[g][1] = l;
         }
     }
     __syncthreads();
-    // 6. Σ_t p_t v_t: 4 positions per thread, then lanes l / l+32 and the 8 waves
+    // 6. Σ_t p_t v_t: PP positions per thread, then lanes l / l+32 and the NWV waves
     if (has_new) {
         const float4 nv = *(const float4*)(&vnew[4 * vd4]);
 #pragma unroll
@@ -366,21 +374,26 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
 // out = Σ_c e^{m_c-M} o_c / Σ_c e^{m_c-M} l_c. A separate launch: a kernel
 // boundary makes every chunk's partials visible across the XCDs' L2s, which a
 // device-scope fence inside one kernel would buy with L2 write-backs.
-// Every wave reduces the chunk statistics itself — lane c holds chunk c (and
-// c + 64 past 4096 positions), the weights reach the other lanes by readlane —
-// so the kernel has no LDS traffic and no barrier. Thread d loads its column of
-// the first 64 chunk slots in one batch together with the statistics, before
-// the sequence length is known; slots past the live chunks are never used.
+// Every wave reduces the chunk statistics itself — lane c holds chunks c,
+// c + 64, ... — and the weights reach the other lanes by readlane, so the kernel
+// has no LDS traffic and no barrier. Thread d loads its column of the chunk
+// slots that cover 4096 positions in one batch together with the statistics,
+// before the sequence length is known (slots past the live chunks are never
+// used); the chunks of a longer cache are read afterwards.
 template <int HD>
 __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
-    static_assert(ATTN_MAX_CHUNKS <= 128, "two chunk statistics per lane");
-    constexpr int CB = 64;
+    constexpr int S = (ATTN_MAX_CHUNKS + 63) / 64;                                  // statistics per lane
+    constexpr int CB = 4096 / ATTN_T < ATTN_MAX_CHUNKS ? 4096 / ATTN_T : ATTN_MAX_CHUNKS;  // batched slots
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const float* base = A.ws + (int64_t)h * A.max_chunks * (HD + 2);
     const int cmax = A.max_chunks - 1;
-    const float* s0 = base + (int64_t)min(lane, cmax) * (HD + 2) + HD;
-    const float* s1 = base + (int64_t)min(lane + 64, cmax) * (HD + 2) + HD;
-    float m0 = s0[0], l0 = s0[1], m1 = s1[0], l1 = s1[1];
+    float m[S], l[S];
+#pragma unroll
+    for (int u = 0; u < S; u++) {
+        const float* st = base + (int64_t)min(lane + 64 * u, cmax) * (HD + 2) + HD;
+        m[u] = st[0];
+        l[u] = st[1];
+    }
     float v[CB];
 #pragma unroll
     for (int j = 0; j < CB; j++) v[j] = base[(int64_t)min(j, cmax) * (HD + 2) + tid];
@@ -388,20 +401,38 @@ __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
     if (seq > A.max_seq) seq = A.max_seq;
     const int nch = (int)((seq + ATTN_T - 1) / ATTN_T);
     const int c_lo = A.window > 0 && seq > A.window ? (int)((seq - A.window) / ATTN_T) : 0;  // chunks before: none
-    const bool in0 = lane >= c_lo && lane < nch, in1 = lane + 64 >= c_lo && lane + 64 < nch;
-    const float M = aeth_wave_max(fmaxf(in0 ? m0 : -INFINITY, in1 ? m1 : -INFINITY));
-    const float w0 = in0 ? expf(m0 - M) : 0.0f, w1 = in1 ? expf(m1 - M) : 0.0f;
-    const float L = aeth_wave_sum(w0 * l0 + w1 * l1);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < S; u++) {
+        const int c = lane + 64 * u;
+        if (!(c >= c_lo && c < nch)) m[u] = -INFINITY;
+        mx = fmaxf(mx, m[u]);
+    }
+    const float M = aeth_wave_max(mx);
+    float w[S], wl = 0.0f;
+#pragma unroll
+    for (int u = 0; u < S; u++) {  // a slot past the live chunks holds whatever an earlier call left
+        const int c = lane + 64 * u;
+        const bool live = c >= c_lo && c < nch;
+        w[u] = live ? expf(m[u] - M) : 0.0f;
+        wl += live ? w[u] * l[u] : 0.0f;
+    }
+    const float L = aeth_wave_sum(wl);
     // selects, not branches: a branch per chunk let the compiler sink each load into it
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < CB; j++) {
         const bool live = j >= c_lo && j < nch;
-        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w0), j));
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[j / 64]), j % 64));
         acc += (live ? wj : 0.0f) * (live ? v[j] : 0.0f);
     }
-    for (int c = max(CB, c_lo); c < nch; c++)  // past 4096 positions
-        acc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w1), c - CB)) * base[(int64_t)c * (HD + 2) + tid];
+    for (int c = max(CB, c_lo); c < nch; c++) {  // past 4096 positions
+        float wc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < S; u++)
+            if (u == c / 64) wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[u]), c % 64));
+        acc += wc * base[(int64_t)c * (HD + 2) + tid];
+    }
     A.out[(int64_t)h * HD + tid] = acc / L;
 }
 

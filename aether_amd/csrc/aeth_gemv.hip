@@ -696,7 +696,7 @@ static int mq_dispatch(MqParams G, int64_t m, hipStream_t s) {
     const int nbw = (nc + W - 1) / W;
     const int NBW = nbw <= 1 ? 1 : nbw <= 2 ? 2 : nbw <= 4 ? 4 : 8;
     if (nbw > 8) return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d is beyond this kernel's range", G.k);
-    const int RD = NBW <= 2 || (W == 8 && NBW == 4 && F != FQ6K) ? 2 : 1;
+    int RD = NBW <= 2 || (W == 8 && NBW == 4 && F != FQ6K) ? 2 : 1;
     // (Q6_K on the ring: ~4 workgroups per CU, measured 1.5 % faster on the 128256-row LM head)
     // (4 to 8 tiles per CU, other formats: one workgroup per CU on the ring — the 28672-row gate|up GEMV
     // of the 8B decode step, 3.6 % faster decode than 2 tiles per workgroup)
@@ -709,6 +709,9 @@ static int mq_dispatch(MqParams G, int64_t m, hipStream_t s) {
     if (env_tpw > 0) tpw = env_tpw;
     if (tpw > MQ_TPW_MAX) tpw = MQ_TPW_MAX;
     G.tpw = (int)tpw;
+    // one tile per workgroup: a single load slot (with two, the second repeats the first tile's loads;
+    // the o GEMV of the 8B decode step measured 4.17 -> 3.92 us)
+    if (tpw == 1 && W == 8 && (NBW == 2 || NBW == 4)) RD = 1;
     const size_t lds = (size_t)nc * (T::AB + T::MB) + (size_t)tpw * W * 16 * 4 + (size_t)W * 16;
     if (lds > MQ_LDS_MAX)
         return aeth_set_error(AETH_EUNSUPPORTED, "gemv: k=%d needs %zu B of LDS (max %d)", G.k, lds, MQ_LDS_MAX);
@@ -720,7 +723,10 @@ static int mq_dispatch(MqParams G, int64_t m, hipStream_t s) {
         return mq_launch<F, 8, 1, 16, RAG, Q8A>(grid, lds, s, G);
     }
     if (NBW == 1) return mq_launch<F, 1, 2, 8, RAG, Q8A>(grid, lds, s, G);
-    if (NBW == 2) return mq_launch<F, 2, 2, 8, RAG, Q8A>(grid, lds, s, G);
+    if (NBW == 2) {
+        if (RD == 1) return mq_launch<F, 2, 1, 8, RAG, Q8A>(grid, lds, s, G);
+        return mq_launch<F, 2, 2, 8, RAG, Q8A>(grid, lds, s, G);
+    }
     if (NBW == 4) {
         if (RD == 2) return mq_launch<F, 4, 2, 8, RAG, Q8A>(grid, lds, s, G);
         return mq_launch<F, 4, 1, 8, RAG, Q8A>(grid, lds, s, G);

@@ -75,6 +75,35 @@ def test_attention_and_kv_append(gpu, seq):
     assert_close(od.cpu().numpy(), ref, tol=1e-4)
 
 
+@pytest.mark.parametrize("seq", [1, 65, 700])
+def test_attention_ignores_stale_chunk_partials(gpu, seq):
+    """The merge loads every chunk slot of its scratch before it reads the
+    sequence length; slots past the live chunks hold what an earlier call left.
+    An earlier call over 2049 positions with a NaN query leaves NaN partials in
+    every slot: a shorter call after it on the same stream must match the
+    oracle with no NaN."""
+    torch = gpu
+    L = A.lib()
+    nh, nkv, hd, ms = 32, 8, 128, 2304
+    rng = np.random.default_rng(100 + seq)
+    kv = rng.standard_normal((2, nkv, ms, hd)).astype(np.float32)
+    kvd = dev(torch, kv)
+    od = torch.empty(nh * hd, dtype=torch.float32, device="cuda")
+    qnan = dev(torch, np.full(nh * hd, np.nan, dtype=np.float32))
+    A.check(L.aeth_attn_decode(qnan.data_ptr(), kvd.data_ptr(), nh, nkv, hd, ms, 2049, od.data_ptr(), None))
+    torch.cuda.synchronize()
+    assert np.isnan(od.cpu().numpy()).all()
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    qd = dev(torch, q)
+    A.check(L.aeth_attn_decode(qd.data_ptr(), kvd.data_ptr(), nh, nkv, hd, ms, seq, od.data_ptr(), None))
+    torch.cuda.synchronize()
+    got = od.cpu().numpy()
+    ref = np.concatenate([O.attn_direct(q[h * hd:(h + 1) * hd], kv[0, h // (nh // nkv)], kv[1, h // (nh // nkv)], seq,
+                                        hd) for h in range(nh)])
+    assert np.isfinite(got).all()
+    assert_close(got, ref, tol=1e-4)
+
+
 def test_attention_one_hot(gpu):
     """A query aligned with one cached key far above the rest attends only to
     that position: out = v_t."""
