@@ -722,7 +722,12 @@ bool aeth_q80_gemm_rows(const aeth_weight* w, int64_t m) {
     // AETH_Q80_GEMM_ROWS=r takes the GEMM from r rows (tests and measurements; read once)
     static const int64_t env_rows = getenv("AETH_Q80_GEMM_ROWS") ? atoll(getenv("AETH_Q80_GEMM_ROWS")) : 0;
     if (env_rows > 0) return m >= env_rows;
-    return m >= 16 || (m >= 5 && m * w->nb * w->n * 34 >= 150000000LL);
+    // The GEMM's cost is nearly flat in m (26.9 / 34.4 / 30.0 / 26.1 us for 4096 x 4096, 4096 x 14336,
+    // 14336 x 4096, 1024 x 4096 at m = 2 ... 48); the row-batched GEMV adds one weight stream per row,
+    // ~1.2 us for a weight the memory-side cache holds (17.8 MB) and ~8-12 us for 62 MB. Measured
+    // crossovers: 4096 x 4096 at ~21 rows, 4096 x 14336 ~2.6, 14336 x 4096 ~3.5, 1024 x 4096 past 48.
+    const int64_t bytes = w->nb * w->n * 34;
+    return m >= 4096 || (m >= 3 && m * bytes >= (bytes <= (32LL << 20) ? 380000000LL : 180000000LL));
 }
 
 bool aeth_q80_gemm_fuses(const aeth_weight* w, int64_t m, int mode, const float* d_a, const float* norm_w) {

@@ -363,6 +363,28 @@ def test_q4k_small_batches(gpu, m, n, k):
     assert_close(got_q8, ref_q8, what="q4_k dot-product mode m=%d n=%d k=%d" % (m, n, k))
 
 
+# Small batches of Q8_0 rows (aeth_q80_gemm_rows): the row-batched GEMV until m · (weight bytes)
+# reaches 380 MB for weights up to 32 MiB and 180 MB above (from 3 rows), else the GEMM; both sides
+# of the switch at the measured crossovers, plain, accumulate and the dot-product mode.
+@pytest.mark.parametrize("m,n,k", [(21, 4096, 4096), (22, 4096, 4096), (2, 4096, 14336), (3, 4096, 14336),
+                                   (2, 14336, 4096), (3, 14336, 4096)])
+def test_q80_small_batches(gpu, m, n, k):
+    rng = np.random.default_rng(m * 103 + n + k)
+    raw = weight(Q8_0, n, k, 7 * n + m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = make_weight(gpu, Q8_0, n, k, raw)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    got = gemv(gpu, w, x.ravel(), n, m)
+    got_acc = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    got_q8 = gemv(gpu, w, x.ravel(), n, m, flags=A.MM_Q8_ACTIVATIONS)
+    A.lib().aeth_weight_free(w)
+    ref = O.reference_matmul(Q8_0, x.ravel(), raw, m, n, k).reshape(m, n)
+    assert_close(got, ref, what="q8_0 m=%d n=%d k=%d" % (m, n, k))
+    assert_close(got_acc, ref + y0, what="q8_0 accumulate m=%d n=%d k=%d" % (m, n, k))
+    ref_q8 = O.dotprod_ref(Q8_0, O.quantize_activations_q8_0(x.ravel(), m, k), raw, m, n, k).reshape(m, n)
+    assert_close(got_q8, ref_q8, what="q8_0 dot-product mode m=%d n=%d k=%d" % (m, n, k))
+
+
 def check_q5k_gemm(torch, m, n, k):
     """Q5_K product of m rows against the oracle (avx2::matmul_q5_k with m rows), as
     check_q4k_gemm: per-row exponents (2^20, 2^-12, a zero row, a block of 2^15 rows past
