@@ -155,7 +155,11 @@ int aeth_kv_append_launch(float* layer_kv, const float* k, const float* v, int64
 #ifndef ATTN_NT
 #define ATTN_NT 512  // threads of k_attn (256, 512 or 1024; 256 measured 5 %, 1024 7 % slower at seq 2049)
 #endif
-#define ATTN_T (ATTN_NT == 1024 ? 64 : ATTN_NT / 8)  // positions per chunk: 8 lanes per position (16 at 1024)
+#ifndef ATTN_LP
+#define ATTN_LP (ATTN_NT == 1024 ? 16 : 8)  // lanes per position in the scores (16 at 512 threads, 32-position
+                                             // chunks: k_attn 7.80 -> 8.57 us, merge 4.81 -> 6.96 us, not used)
+#endif
+#define ATTN_T (ATTN_NT / ATTN_LP)  // positions per chunk
 #define ATTN_MAX_GROUPS 8
 #define ATTN_MAX_CHUNKS (8192 / ATTN_T)  // max_seq <= 8192
 
@@ -189,7 +193,7 @@ template <int HD, int NT>
 __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
     static_assert(HD == 128 && (NT == 256 || NT == 512 || NT == 1024), "decode attention is laid out for head_dim 128");
     constexpr int HALF = HD / 2, NWV = NT / 64;
-    constexpr int LP = NT == 1024 ? 16 : 8, K4 = HD / LP / 4;  // scores: lanes per position, float4s per lane
+    constexpr int LP = ATTN_LP, K4 = HD / LP / 4;  // scores: lanes per position, float4s per lane
     constexpr int T = NT / LP;                                  // positions per chunk (ATTN_T)
     constexpr int PP = T * HD / 4 / NT;                         // P·V: positions per thread
     constexpr int QP = (ATTN_MAX_GROUPS * HALF + NT - 1) / NT;  // rotation pairs of q per thread
