@@ -124,15 +124,17 @@ AETH_API int aeth_load_quant(int dtype, const void* d_src, int64_t k, int64_t n,
  * (src/quant/matmul/registry.rs:7-19) / quantized_matmul_impl
  * (src/quant/matmul/dispatch.rs:98-135) with device operands. Routing:
  *   - m == 1: the matrix-core decode GEMV (Q8_0, Q4_K, Q5_K, Q6_K rows);
- *   - m > 1, Q4_K / Q6_K / Q8_0 rows: the exact-mode fp16 MFMA GEMMs from 16
- *     rows (from 5 once m · weight bytes reaches 150 MB, 200 MB for Q6_K),
- *     the row-batched GEMV below that; Q6_K / Q8_0 products the GEMMs do not
- *     take (k not whole super-blocks / blocks, buffers past 32-bit offsets)
- *     run the row-batched GEMV up to 80 / 112 rows, then the DGEMM below;
- *   - m > 1, Q5_K rows and GGUF-order Q2_K / Q3_K: the row-batched GEMV up to
- *     a per-format row count (Q5_K 80, Q2_K 40, Q3_K 32), then the weight
- *     dequantized once and one rocBLAS f64 DGEMM (also every K-quant product
- *     of the dot-product mode with k not a multiple of 256);
+ *   - m > 1, Q4_K / Q5_K / Q6_K / Q8_0 rows: the exact-mode fp16 MFMA GEMMs —
+ *     Q4_K and Q5_K from 16 rows (from 5 once m · weight bytes reaches 150 MB),
+ *     Q6_K once m · weight bytes reaches 200 MB, Q8_0 from 3 rows once it
+ *     reaches 180 MB (380 MB for a weight up to 32 MiB) — the row-batched GEMV
+ *     below that; Q5_K / Q6_K / Q8_0 products the GEMMs do not take (k not
+ *     whole super-blocks / blocks, buffers past 32-bit offsets) run the
+ *     row-batched GEMV up to 80 / 80 / 112 rows, then the DGEMM below;
+ *   - m > 1, GGUF-order Q2_K / Q3_K: the row-batched GEMV up to a per-format
+ *     row count (Q2_K 40, Q3_K 32), then the weight dequantized once and one
+ *     rocBLAS f64 DGEMM (also every K-quant product of the dot-product mode
+ *     with k not a multiple of 256);
  *   - F32 / F16 / Q2_K / Q3_K in GGUF order: the kernel of matmul_f32_gguf
  *     (dispatch.rs:541-574) for the rows not sent to the DGEMM.
  * Stream scratch: the GEMMs' activation fragments and split-K partials, the
