@@ -594,6 +594,12 @@ bool aeth_gemm_swiglu_out(const aeth_weight* w, int64_t m) {
            m > 1 && w->k == w->nb * 256 && (w->n & 1) == 0 && kq_gemm_rows(w, m);
 }
 
+// AETH_GEMM_TAIL_SPLIT=0 turns the last-round K split off (A/B timing; the results agree to rounding)
+static bool tail_split_off() {
+    static const bool off = getenv("AETH_GEMM_TAIL_SPLIT") && atoi(getenv("AETH_GEMM_TAIL_SPLIT")) == 0;
+    return off;
+}
+
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s, int64_t ldc, void* ws, size_t ws_bytes, const GemmIn* in) {
     const int k = (int)w->k, nb = (int)w->nb;
@@ -635,11 +641,17 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
         // at most half as many tiles as CUs: K split over workgroups too, as many splits as fit in one
         // round of workgroups (each wave keeps at least one super-block), the partial tiles in the
         // stream's scratch (not with a caller's workspace)
-        const int ksplit = ws ? 1 : (int)std::max<int64_t>(1, std::min<int64_t>(aeth_num_cus() / ((int64_t)gm * gn), nb / 8));
+        const int64_t cus = aeth_num_cus(), T = (int64_t)gm * gn;
+        const int ksplit = ws ? 1 : (int)std::max<int64_t>(1, std::min<int64_t>(cus / T, nb / 8));
+        // more tiles than CUs, the last round at most half full: its tiles split K over the idle CUs
+        const int64_t tail = T % cus;
+        const int tsplit = (ws || ksplit > 1 || T < cus || tail == 0 || 2 * tail > cus || tail_split_off())
+                               ? 1 : (int)std::min<int64_t>(cus / tail, nb / 8);
+        const int nsplit = std::max(ksplit, tsplit);
         float* part = nullptr;
-        if (ksplit > 1) {
+        if (nsplit > 1) {
             void* p = nullptr;
-            rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)ksplit * mp * gn * G2_BN * sizeof(float), &p);
+            rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)nsplit * mp * gn * G2_BN * sizeof(float), &p);
             if (rc) return rc;
             part = (float*)p;
         }
@@ -647,6 +659,10 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
                  (int)mp, gm, gn, (int)ab, (int)(mp * (k / 32) * 4), (int)qb, (int)std::min(hb, (int64_t)INT32_MAX),
                  d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0, ksplit, part, gn * G2_BN,
                  q5 ? w->p3 : nullptr, q5 ? (int)(ntiles * nb * 512) : 0};
+        if (tsplit > 1) {
+            Q.t_full = (int)(T - tail);
+            Q.tsplit = tsplit;
+        }
         return aeth_gemm_kq_launch(Q, s);
     }
     hipLaunchKernelGGL(k_gemm_q4k_ring, dim3((unsigned)(gm * gn)), dim3(256), 0, s, G);

@@ -185,6 +185,10 @@ struct KqArgs {
     // Q5_K: the fifth-bit plane of the GEMM (aeth_weights.hip, p3), null for Q4_K
     const uint8_t* fifth;
     int f_bytes;
+    // Tail split (ksplit == 1, tsplit > 1): tiles [t_full, gm·gn) — the last, partial round of
+    // workgroups — have K split over tsplit workgroups each (partials in part, as with ksplit)
+    // and are summed by the tail-sum kernel; tiles below t_full run whole
+    int t_full = 0, tsplit = 1;
 };
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s);
 
@@ -199,6 +203,8 @@ struct SplitSum {
     float* C;
     int64_t ldc;
     int m, n, accumulate, swiglu;
+    // gm > 0: only the 64 × 128 tiles [t_full, gm·gn) in g2_tile's order (a tail split)
+    int t_full = 0, gm = 0, gn = 0;
 };
 int aeth_gemm_split_sum_launch(const SplitSum& S, hipStream_t s);
 

@@ -85,13 +85,18 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_kq(KqArgs G) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // workgroup → (K split ks, tile): splits of one tile are T workgroups apart, so each keeps
-    // the tile's XCD when T is a multiple of 8
-    const int T = G.gm * G.gn, ks = (int)blockIdx.x / T;
+    // the tile's XCD when T is a multiple of 8. With a tail split, workgroups past t_full take the
+    // tail tiles' K parts (the splits of one tile ntail workgroups apart).
+    const int T = G.gm * G.gn, tail = G.tsplit > 1 && (int)blockIdx.x >= G.t_full;
+    const int ntail = T - G.t_full, jt = (int)blockIdx.x - G.t_full;
+    const int nsplit = tail ? G.tsplit : G.ksplit;
+    const int ks = tail ? jt / ntail : (int)blockIdx.x / T;
+    const int tile = tail ? G.t_full + (jt - ks * ntail) : (int)blockIdx.x - ks * T;
     int tm, tn;
-    g2_tile((int)blockIdx.x - ks * T, G.gm, G.gn, tm, tn);
+    g2_tile(tile, G.gm, G.gn, tm, tn);
     const int n0 = tn * 128, m0 = tm * 64, t0 = n0 >> 4;
     const int nb = G.nb, nks = G.k >> 4, ksb = G.k >> 5;
-    const int lo = nb * ks / G.ksplit, len = nb * (ks + 1) / G.ksplit - lo;  // this split's super-blocks
+    const int lo = nb * ks / nsplit, len = nb * (ks + 1) / nsplit - lo;  // this split's super-blocks
     const int sb0 = lo + len * wave / K8_W, nsb = lo + len * (wave + 1) / K8_W - sb0, ns = 16 * nsb;
     char* wl = smem + wave * L::WAVE;
     const uint32_t wl_lds = lds_addr(wl);
@@ -387,7 +392,7 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_kq(KqArgs G) {
 #pragma unroll
     for (int r = 0; r < 16; r++) rows[r] = m0 + 32 * mt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
     G2Epi E;  // in flight during the reduction
-    if (G.ksplit == 1) g2_epi_load(E, G.escale, G.C, G.ldc, G.m, G.n, rows, col, G.accumulate);
+    if (nsplit == 1) g2_epi_load(E, G.escale, G.C, G.ldc, G.m, G.n, rows, col, G.accumulate);
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -422,7 +427,7 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_kq(KqArgs G) {
 #pragma unroll
         for (int w = 1; w < 4; w++) sum[r] += red[(((w * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
     }
-    if (G.ksplit > 1) {  // the split's partial tile (rows < mp, columns < pld: no bounds to check)
+    if (nsplit > 1) {  // the split's partial tile (rows < mp, columns < pld: no bounds to check)
         float* P = G.part + (int64_t)ks * G.mp * G.pld + col;
 #pragma unroll
         for (int r = 0; r < 16; r++) P[(int64_t)rows[r] * G.pld] = sum[r];
@@ -436,12 +441,20 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_kq(KqArgs G) {
 }
 
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s) {
+    const int T = G.gm * G.gn;
+    const bool tail = G.ksplit == 1 && G.tsplit > 1 && G.t_full >= 0 && G.t_full < T;
+    const unsigned grid = (unsigned)(tail ? G.t_full + (T - G.t_full) * G.tsplit : T * G.ksplit);
     if (G.fifth)
-        hipLaunchKernelGGL(k_gemm_kq<true>, dim3((unsigned)(G.gm * G.gn * G.ksplit)), dim3(64 * K8_W), 0, s, G);
+        hipLaunchKernelGGL(k_gemm_kq<true>, dim3(grid), dim3(64 * K8_W), 0, s, G);
     else
-        hipLaunchKernelGGL(k_gemm_kq<false>, dim3((unsigned)(G.gm * G.gn * G.ksplit)), dim3(64 * K8_W), 0, s, G);
+        hipLaunchKernelGGL(k_gemm_kq<false>, dim3(grid), dim3(64 * K8_W), 0, s, G);
     AETH_LAUNCH_CHECK();
-    if (G.ksplit == 1) return AETH_OK;
-    const SplitSum S{G.part, G.ksplit, G.mp, G.pld, G.escale, G.C, G.ldc, G.m, G.n, G.accumulate, G.swiglu};
+    if (G.ksplit == 1 && !tail) return AETH_OK;
+    SplitSum S{G.part, tail ? G.tsplit : G.ksplit, G.mp, G.pld, G.escale, G.C, G.ldc, G.m, G.n, G.accumulate, G.swiglu};
+    if (tail) {
+        S.t_full = G.t_full;
+        S.gm = G.gm;
+        S.gn = G.gn;
+    }
     return aeth_gemm_split_sum_launch(S, s);
 }

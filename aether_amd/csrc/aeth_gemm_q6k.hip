@@ -371,13 +371,8 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
     }
 }
 
-// Sum of the K splits, in split order, and the epilogue (SplitSum). One thread per 4 columns of a row.
-__global__ void __launch_bounds__(256) k_gemm_split_sum(SplitSum G) {
-    const int q4 = G.pld >> 2;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)G.m * q4) return;
-    const int row = (int)(i / q4), col = (int)(i - (int64_t)row * q4) * 4;
-    if (col >= G.n) return;
+// Sum of the K splits, in split order, and the epilogue (SplitSum), for 4 columns of a row.
+__device__ __forceinline__ void split_sum_out(const SplitSum& G, int row, int col) {
     const float4* P = (const float4*)(G.part + (int64_t)row * G.pld + col);
     const int64_t split = (int64_t)G.mp * G.pld / 4;
     float4 v = P[0];
@@ -402,7 +397,35 @@ __global__ void __launch_bounds__(256) k_gemm_split_sum(SplitSum G) {
     }
 }
 
+// Every row of C: one thread per 4 columns of a row.
+__global__ void __launch_bounds__(256) k_gemm_split_sum(SplitSum G) {
+    const int q4 = G.pld >> 2;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)G.m * q4) return;
+    const int row = (int)(i / q4), col = (int)(i - (int64_t)row * q4) * 4;
+    if (col >= G.n) return;
+    split_sum_out(G, row, col);
+}
+
+// The tiles of a tail split only: 8 workgroups per 64 × 128 tile, one thread per 4 columns of a
+// row, the tile found by the GEMM's own order (g2_tile).
+__global__ void __launch_bounds__(256) k_gemm_tail_sum(SplitSum G) {
+    const int tile = G.t_full + (int)blockIdx.x / 8, idx = ((int)blockIdx.x % 8) * 256 + (int)threadIdx.x;
+    int tm, tn;
+    g2_tile(tile, G.gm, G.gn, tm, tn);
+    const int row = tm * 64 + (idx >> 5), col = tn * 128 + (idx & 31) * 4;
+    if (row >= G.m || col >= G.n) return;
+    split_sum_out(G, row, col);
+}
+
 int aeth_gemm_split_sum_launch(const SplitSum& S, hipStream_t s) {
+    if (S.gm > 0) {
+        const int ntail = S.gm * S.gn - S.t_full;
+        if (ntail <= 0) return AETH_OK;
+        hipLaunchKernelGGL(k_gemm_tail_sum, dim3((unsigned)ntail * 8), dim3(256), 0, s, S);
+        AETH_LAUNCH_CHECK();
+        return AETH_OK;
+    }
     const int64_t threads = (int64_t)S.m * (S.pld / 4);
     hipLaunchKernelGGL(k_gemm_split_sum, dim3((unsigned)aeth_cdiv(threads, 256)), dim3(256), 0, s, S);
     AETH_LAUNCH_CHECK();

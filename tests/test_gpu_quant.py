@@ -708,6 +708,59 @@ def test_prefill_gemm_config_parity(gpu, n):
     assert_close(got[:, cols], ref, what="prefill GEMM n=%d" % n)
 
 
+def g2_tile(i, gm, gn):
+    """The K-split GEMM's workgroup → 64 × 128 tile order (g2_tile, aeth_gemm_common.hpp):
+    tile ids dealt round-robin over the 8 XCDs when their count is a multiple of 8, then
+    column-major within groups of 4 row-tiles."""
+    T = gm * gn
+    if T % 8 == 0:
+        i = (i & 7) * (T >> 3) + (i >> 3)
+    grp = i // (4 * gn)
+    rows = min(4, gm - 4 * grp)
+    j = i - grp * 4 * gn
+    return 4 * grp + j % rows, j // rows
+
+
+# More 64 × 128 tiles than CUs with the last round at most half full: the GEMM splits the K
+# range of those last tiles over the idle CUs and a second kernel sums them. Up to 8 of each
+# shape's tail tiles (the first and last among them) and three whole tiles are checked against
+# the oracle: 19 tail tiles split in 2, 69 in 3, 4 in 8, 119 in 2 (at 256 CUs), Q4_K and Q5_K,
+# plain and accumulate.
+@pytest.mark.parametrize("dtype,m,n,k", [(Q4_K, 300, 7000, 4096), (Q4_K, 260, 8320, 16384), (Q4_K, 100, 16600, 16384),
+                                         (Q5_K, 130, 16000, 8192)])
+def test_gemm_tail_round_split(gpu, dtype, m, n, k):
+    torch = gpu
+    L = A.lib()
+    nb = k // 256
+    be, bb = GEOM[dtype]
+    raw_d = torch.empty(n * nb * bb, dtype=torch.uint8, device="cuda")
+    A.check(L.aeth_fill_synthetic_raw(dtype, 0x7A11 + n, raw_d.data_ptr(), n * nb, None), "fill")
+    rng = np.random.default_rng(m + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    w = ctypes.c_void_p()
+    A.check(L.aeth_weight_create(dtype, n, k, raw_d.data_ptr(), 1, None, ctypes.byref(w)), "create")
+    try:
+        got = gemv(torch, w, x.ravel(), n, m)
+        got_acc = gemv(torch, w, x.ravel(), n, m, flags=A.MM_ACCUMULATE, y0=y0)
+    finally:
+        L.aeth_weight_free(w)
+    raw = raw_d.cpu().numpy().reshape(n, nb * bb)
+    gm, gn = -(-m // 64), -(-n // 128)
+    T, cus = gm * gn, torch.cuda.get_device_properties(0).multi_processor_count
+    tail = T % cus
+    assert T > cus and 0 < 2 * tail <= cus, "shape %d x %d does not leave a short last round on %d CUs" % (m, n, cus)
+    print("tiles %d, tail %d split %d ways" % (T, tail, min(cus // tail, nb // 8)), flush=True)
+    tails = sorted(set(np.linspace(T - tail, T - 1, min(tail, 8)).round().astype(int).tolist()))
+    for t in tails + [0, T // 2, T - tail - 1]:
+        tm, tn = g2_tile(t, gm, gn)
+        r0, r1, c0, c1 = 64 * tm, min(m, 64 * tm + 64), 128 * tn, min(n, 128 * tn + 128)
+        ref = O.reference_matmul(dtype, x[r0:r1].ravel(), raw[c0:c1].ravel(), r1 - r0, c1 - c0, k).reshape(r1 - r0, -1)
+        what = "tile %d (%d, %d) of %d x %d x %d" % (t, tm, tn, m, n, k)
+        assert_close(got[r0:r1, c0:c1], ref, what=what)
+        assert_close(got_acc[r0:r1, c0:c1], ref + y0[r0:r1, c0:c1], what=what + " accumulate")
+
+
 # ── F32 / F16 / Q2_K / Q3_K: GGUF-order and row kernels ───────────────────
 # quantized_matmul_impl keeps these formats in GGUF [k][n] order and multiplies
 # by dequantize + matmul_f32_gguf (dispatch.rs:126-133, 541-574); the
