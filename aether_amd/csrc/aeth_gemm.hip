@@ -600,6 +600,32 @@ static bool tail_split_off() {
     return off;
 }
 
+// K splits of a K-split GEMM launch over gm × gn tiles (each split keeps at least maxsplit⁻¹ of K,
+// so that every wave has whole units): with at most half as many tiles as CUs, ksplit ways for
+// every tile, as many as fit one round of workgroups; with more tiles than CUs and a last round at
+// most half full, tsplit ways for that round's tiles (g2_tail_ways). The partial tiles go to the
+// stream's scratch; with `whole` (a caller's workspace) nothing is split.
+struct SplitPlan {
+    int ksplit = 1, tsplit = 1, t_full = 0;
+    float* part = nullptr;
+};
+static int split_plan(hipStream_t s, int64_t gm, int64_t gn, int64_t maxsplit, bool whole, SplitPlan& P) {
+    P = SplitPlan{};
+    if (whole) return AETH_OK;
+    const int64_t cus = aeth_num_cus(), T = gm * gn;
+    P.ksplit = (int)std::max<int64_t>(1, std::min<int64_t>(cus / T, maxsplit));
+    if (P.ksplit == 1 && !tail_split_off()) {
+        P.tsplit = g2_tail_ways(T, cus, maxsplit);
+        if (P.tsplit > 1) P.t_full = (int)(T - T % cus);
+    }
+    const int ways = std::max(P.ksplit, P.tsplit);
+    if (ways == 1) return AETH_OK;
+    void* p = nullptr;
+    const int rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)ways * gm * G2_BM * gn * G2_BN * sizeof(float), &p);
+    P.part = (float*)p;
+    return rc;
+}
+
 int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, float* d_c, unsigned flags,
                          hipStream_t s, int64_t ldc, void* ws, size_t ws_bytes, const GemmIn* in) {
     const int k = (int)w->k, nb = (int)w->nb;
@@ -641,28 +667,12 @@ int aeth_gemm_q4k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
         // at most half as many tiles as CUs: K split over workgroups too, as many splits as fit in one
         // round of workgroups (each wave keeps at least one super-block), the partial tiles in the
         // stream's scratch (not with a caller's workspace)
-        const int64_t cus = aeth_num_cus(), T = (int64_t)gm * gn;
-        const int ksplit = ws ? 1 : (int)std::max<int64_t>(1, std::min<int64_t>(cus / T, nb / 8));
-        // more tiles than CUs, the last round at most half full: its tiles split K over the idle CUs
-        const int64_t tail = T % cus;
-        const int tsplit = (ws || ksplit > 1 || T < cus || tail == 0 || 2 * tail > cus || tail_split_off())
-                               ? 1 : (int)std::min<int64_t>(cus / tail, nb / 8);
-        const int nsplit = std::max(ksplit, tsplit);
-        float* part = nullptr;
-        if (nsplit > 1) {
-            void* p = nullptr;
-            rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)nsplit * mp * gn * G2_BN * sizeof(float), &p);
-            if (rc) return rc;
-            part = (float*)p;
-        }
+        SplitPlan P;
+        if ((rc = split_plan(s, gm, gn, nb / 8, ws != nullptr, P))) return rc;
         KqArgs Q{(const uint8_t*)frag, (const uint8_t*)Sh, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, (int)ntiles,
                  (int)mp, gm, gn, (int)ab, (int)(mp * (k / 32) * 4), (int)qb, (int)std::min(hb, (int64_t)INT32_MAX),
-                 d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0, ksplit, part, gn * G2_BN,
-                 q5 ? w->p3 : nullptr, q5 ? (int)(ntiles * nb * 512) : 0};
-        if (tsplit > 1) {
-            Q.t_full = (int)(T - tail);
-            Q.tsplit = tsplit;
-        }
+                 d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0, P.ksplit, P.part, gn * G2_BN,
+                 q5 ? w->p3 : nullptr, q5 ? (int)(ntiles * nb * 512) : 0, P.t_full, P.tsplit};
         return aeth_gemm_kq_launch(Q, s);
     }
     hipLaunchKernelGGL(k_gemm_q4k_ring, dim3((unsigned)(gm * gn)), dim3(256), 0, s, G);
@@ -710,20 +720,13 @@ int aeth_gemm_q6k_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     int rc = gemm_prep(d_a, m, k, flags, in, s, nullptr, 0, frag, Sh, esc);
     if (rc) return rc;
     const int64_t ntiles = aeth_cdiv(w->n, 16), gm = mp / G2_BM, gn = aeth_cdiv(w->n, G2_BN);
-    // at most half as many tiles as CUs: split K over workgroups too, as many splits as fit in one
-    // round of workgroups (each wave keeps at least one super-block)
-    const int ksplit = (int)std::max<int64_t>(1, std::min<int64_t>(aeth_num_cus() / (gm * gn), nb / 8));
-    float* part = nullptr;
-    if (ksplit > 1) {
-        void* p = nullptr;
-        rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)ksplit * mp * gn * G2_BN * sizeof(float), &p);
-        if (rc) return rc;
-        part = (float*)p;
-    }
+    // K split over workgroups (split_plan; each wave keeps at least one super-block)
+    SplitPlan P;
+    if ((rc = split_plan(s, gm, gn, nb / 8, false, P))) return rc;
     Q6Args Q{(const uint8_t*)frag, esc, w->p0, w->p1, w->p2, (int)m, (int)w->n, k, nb, (int)ntiles, (int)mp,
              (int)gm, (int)gn, (int)(mp * k * 4), (int)(ntiles * nb * 3072), (int)(ntiles * nb * 256),
              (int)(ntiles * nb * 32), d_c, ldc, (flags & AETH_MM_ACCUMULATE) ? 1 : 0, 0,
-             ksplit, part, (int)(gn * G2_BN)};
+             P.ksplit, P.part, (int)(gn * G2_BN), P.t_full, P.tsplit};
     return aeth_gemm_q6k_kq_launch(Q, s);
 }
 
@@ -773,19 +776,14 @@ int aeth_gemm_q80_launch(const aeth_weight* w, const float* d_a, int64_t m, floa
     int rc = gemm_prep(d_a, m, k, flags, in, s, nullptr, 0, frag, Sh, esc);
     if (rc) return rc;
     const int64_t ntiles = aeth_cdiv(w->n, 16), ngr = aeth_cdiv(nb, 4), gm = mp / G2_BM, gn = aeth_cdiv(w->n, G2_BN);
-    // at most half as many tiles as CUs: K split over workgroups too (each wave keeps 8 blocks at least,
-    // the 256 elements of a K-quant super-block)
-    const int ksplit = (int)std::max<int64_t>(1, std::min<int64_t>(aeth_num_cus() / (gm * gn), nb / 64));
-    float* part = nullptr;
-    if (ksplit > 1) {
-        void* p = nullptr;
-        rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)ksplit * mp * gn * G2_BN * sizeof(float), &p);
-        if (rc) return rc;
-        part = (float*)p;
-    }
+    // K split over workgroups (split_plan; each wave keeps 8 blocks at least, the 256 elements of a
+    // K-quant super-block)
+    SplitPlan P;
+    if ((rc = split_plan(s, gm, gn, nb / 64, false, P))) return rc;
     Q80Args Q{(const uint8_t*)frag, esc, w->p0, w->p1, (int)m, (int)w->n, k, nb, (int)ngr, (int)ntiles, (int)mp,
               (int)gm, (int)gn, (int)(mp * k * 4), (int)(ntiles * ngr * 2048), (int)(ntiles * ngr * 128), d_c, ldc,
-              (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0, ksplit, part, (int)(gn * G2_BN)};
+              (flags & AETH_MM_ACCUMULATE) ? 1 : 0, swo ? 1 : 0, P.ksplit, P.part, (int)(gn * G2_BN), P.t_full,
+              P.tsplit};
     return aeth_gemm_q80_kq_launch(Q, s);
 }
 

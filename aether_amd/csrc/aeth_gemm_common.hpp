@@ -126,6 +126,35 @@ __device__ __forceinline__ void g2_tile(int id, int gm, int gn, int& tm, int& tn
     tn = in / rows;
 }
 
+// Workgroup bid → (tile, K part ks of nsplit). Without a tail split the ksplit parts of a tile
+// are T = gm·gn workgroups apart (each keeps the tile's XCD when T is a multiple of 8). With one
+// (ksplit == 1, tsplit > 1) the workgroups below t_full take the whole tiles [0, t_full) and the
+// rest the tsplit parts of the tail tiles [t_full, T), the parts of one tile T − t_full apart.
+__device__ __forceinline__ void g2_work(int bid, int gm, int gn, int ksplit, int t_full, int tsplit, int& tile,
+                                        int& ks, int& nsplit) {
+    const int T = gm * gn;
+    if (tsplit > 1 && bid >= t_full) {
+        const int ntail = T - t_full, jt = bid - t_full;
+        nsplit = tsplit;
+        ks = jt / ntail;
+        tile = t_full + (jt - ks * ntail);
+    } else {
+        nsplit = ksplit;
+        ks = bid / T;
+        tile = bid - ks * T;
+    }
+}
+
+// Ways to split the K range of every tile of a short last round (the launch has no K split):
+// more tiles than CUs and a last round at most half full → as many ways as fill the idle CUs,
+// at most maxsplit; otherwise 1.
+inline int g2_tail_ways(int64_t T, int64_t cus, int64_t maxsplit) {
+    const int64_t tail = T % cus;
+    if (T < cus || tail == 0 || 2 * tail > cus) return 1;
+    const int64_t w = cus / tail < maxsplit ? cus / tail : maxsplit;
+    return w > 1 ? (int)w : 1;
+}
+
 // Epilogue of one lane: 16 outputs at rows row(r) (r < 16, each < mp) of column col.
 // g2_epi_load fetches the rows' scales 2^e and, with accumulate, C's previous values
 // (from clamped addresses, so every load is issued) before the first store: a store to C
@@ -229,6 +258,7 @@ struct Q6Args {
     int ksplit;
     float* part;
     int pld;
+    int t_full = 0, tsplit = 1;  // tail split: as KqArgs
 };
 int aeth_gemm_q6k_kq_launch(const Q6Args& G, hipStream_t s);
 
@@ -249,5 +279,25 @@ struct Q80Args {
     int ksplit;            // K split over workgroups: as Q6Args
     float* part;
     int pld;
+    int t_full = 0, tsplit = 1;  // tail split: as KqArgs
 };
 int aeth_gemm_q80_kq_launch(const Q80Args& G, hipStream_t s);
+
+// Grid of a K-split GEMM launch (see g2_work) and its second kernel (none without a split).
+template <class Args>
+unsigned g2_grid(const Args& G) {
+    const int T = G.gm * G.gn;
+    return (unsigned)(G.tsplit > 1 ? G.t_full + (T - G.t_full) * G.tsplit : T * G.ksplit);
+}
+template <class Args>
+int g2_split_sum(const Args& G, hipStream_t s) {
+    const bool tail = G.tsplit > 1;
+    if (G.ksplit == 1 && !tail) return 0;
+    SplitSum S{G.part, tail ? G.tsplit : G.ksplit, G.mp, G.pld, G.escale, G.C, G.ldc, G.m, G.n, G.accumulate, G.swiglu};
+    if (tail) {
+        S.t_full = G.t_full;
+        S.gm = G.gm;
+        S.gn = G.gn;
+    }
+    return aeth_gemm_split_sum_launch(S, s);
+}

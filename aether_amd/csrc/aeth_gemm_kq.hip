@@ -84,15 +84,8 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_kq(KqArgs G) {
     __shared__ __attribute__((aligned(1024))) char smem[K8_W * L::WAVE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // workgroup → (K split ks, tile): splits of one tile are T workgroups apart, so each keeps
-    // the tile's XCD when T is a multiple of 8. With a tail split, workgroups past t_full take the
-    // tail tiles' K parts (the splits of one tile ntail workgroups apart).
-    const int T = G.gm * G.gn, tail = G.tsplit > 1 && (int)blockIdx.x >= G.t_full;
-    const int ntail = T - G.t_full, jt = (int)blockIdx.x - G.t_full;
-    const int nsplit = tail ? G.tsplit : G.ksplit;
-    const int ks = tail ? jt / ntail : (int)blockIdx.x / T;
-    const int tile = tail ? G.t_full + (jt - ks * ntail) : (int)blockIdx.x - ks * T;
-    int tm, tn;
+    int tile, ks, nsplit, tm, tn;
+    g2_work((int)blockIdx.x, G.gm, G.gn, G.ksplit, G.t_full, G.tsplit, tile, ks, nsplit);
     g2_tile(tile, G.gm, G.gn, tm, tn);
     const int n0 = tn * 128, m0 = tm * 64, t0 = n0 >> 4;
     const int nb = G.nb, nks = G.k >> 4, ksb = G.k >> 5;
@@ -441,20 +434,10 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_kq(KqArgs G) {
 }
 
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s) {
-    const int T = G.gm * G.gn;
-    const bool tail = G.ksplit == 1 && G.tsplit > 1 && G.t_full >= 0 && G.t_full < T;
-    const unsigned grid = (unsigned)(tail ? G.t_full + (T - G.t_full) * G.tsplit : T * G.ksplit);
     if (G.fifth)
-        hipLaunchKernelGGL(k_gemm_kq<true>, dim3(grid), dim3(64 * K8_W), 0, s, G);
+        hipLaunchKernelGGL(k_gemm_kq<true>, dim3(g2_grid(G)), dim3(64 * K8_W), 0, s, G);
     else
-        hipLaunchKernelGGL(k_gemm_kq<false>, dim3(grid), dim3(64 * K8_W), 0, s, G);
+        hipLaunchKernelGGL(k_gemm_kq<false>, dim3(g2_grid(G)), dim3(64 * K8_W), 0, s, G);
     AETH_LAUNCH_CHECK();
-    if (G.ksplit == 1 && !tail) return AETH_OK;
-    SplitSum S{G.part, tail ? G.tsplit : G.ksplit, G.mp, G.pld, G.escale, G.C, G.ldc, G.m, G.n, G.accumulate, G.swiglu};
-    if (tail) {
-        S.t_full = G.t_full;
-        S.gm = G.gm;
-        S.gn = G.gn;
-    }
-    return aeth_gemm_split_sum_launch(S, s);
+    return g2_split_sum(G, s);
 }

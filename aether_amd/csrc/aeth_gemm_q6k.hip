@@ -74,14 +74,12 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
     __shared__ __attribute__((aligned(1024))) char smem[K6_W * K6_WAVE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // workgroup → (K split ks, tile): splits of one tile are T workgroups apart, so each keeps
-    // the tile's XCD when T is a multiple of 8
-    const int T = G.gm * G.gn, ks = (int)blockIdx.x / T;
-    int tm, tn;
-    g2_tile((int)blockIdx.x - ks * T, G.gm, G.gn, tm, tn);
+    int tile, ks, nsplit, tm, tn;
+    g2_work((int)blockIdx.x, G.gm, G.gn, G.ksplit, G.t_full, G.tsplit, tile, ks, nsplit);
+    g2_tile(tile, G.gm, G.gn, tm, tn);
     const int n0 = tn * 128, m0 = tm * 64, t0 = n0 >> 4;
     const int nb = G.nb, nks = G.k >> 4;
-    const int lo = nb * ks / G.ksplit, len = nb * (ks + 1) / G.ksplit - lo;  // this split's super-blocks
+    const int lo = nb * ks / nsplit, len = nb * (ks + 1) / nsplit - lo;  // this split's super-blocks
     const int sb0 = lo + len * wave / K6_W, nsb = lo + len * (wave + 1) / K6_W - sb0;
     char* wl = smem + wave * K6_WAVE;
     const uint32_t wl_lds = lds_addr(wl);
@@ -323,7 +321,7 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
 #pragma unroll
     for (int r = 0; r < 16; r++) rows[r] = m0 + 32 * mt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
     G2Epi E;  // in flight during the reduction
-    if (G.ksplit == 1) g2_epi_load(E, G.escale, G.C, G.ldc, G.m, G.n, rows, col, G.accumulate);
+    if (nsplit == 1) g2_epi_load(E, G.escale, G.C, G.ldc, G.m, G.n, rows, col, G.accumulate);
 #pragma unroll
     for (int q = 0; q < 2; q++)
 #pragma unroll
@@ -358,7 +356,7 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
 #pragma unroll
         for (int w = 1; w < 4; w++) sum[r] += red[(((w * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
     }
-    if (G.ksplit > 1) {  // the split's partial tile (rows < mp, columns < pld: no bounds to check)
+    if (nsplit > 1) {  // the split's partial tile (rows < mp, columns < pld: no bounds to check)
         float* P = G.part + ((int64_t)ks * G.mp + m0 + 32 * mt) * G.pld + col;
 #pragma unroll
         for (int r = 0; r < 16; r++) P[(int64_t)(rows[r] - m0 - 32 * mt) * G.pld] = sum[r];
@@ -433,9 +431,7 @@ int aeth_gemm_split_sum_launch(const SplitSum& S, hipStream_t s) {
 }
 
 int aeth_gemm_q6k_kq_launch(const Q6Args& G, hipStream_t s) {
-    hipLaunchKernelGGL(k_gemm_q6k_kq, dim3((unsigned)(G.gm * G.gn * G.ksplit)), dim3(64 * K6_W), 0, s, G);
+    hipLaunchKernelGGL(k_gemm_q6k_kq, dim3(g2_grid(G)), dim3(64 * K6_W), 0, s, G);
     AETH_LAUNCH_CHECK();
-    if (G.ksplit == 1) return AETH_OK;
-    const SplitSum S{G.part, G.ksplit, G.mp, G.pld, G.escale, G.C, G.ldc, G.m, G.n, G.accumulate, G.swiglu};
-    return aeth_gemm_split_sum_launch(S, s);
+    return g2_split_sum(G, s);
 }

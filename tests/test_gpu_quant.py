@@ -724,15 +724,18 @@ def g2_tile(i, gm, gn):
 # More 64 × 128 tiles than CUs with the last round at most half full: the GEMM splits the K
 # range of those last tiles over the idle CUs and a second kernel sums them. Up to 8 of each
 # shape's tail tiles (the first and last among them) and three whole tiles are checked against
-# the oracle: 19 tail tiles split in 2, 69 in 3, 4 in 8, 119 in 2 (at 256 CUs), Q4_K and Q5_K,
-# plain and accumulate.
+# the oracle: 19 tail tiles split in 2, 69 in 3, 4 in 8, 119 in 2 (at 256 CUs), each of the four
+# GEMMs (Q4_K, Q5_K, Q6_K, Q8_0), plain and accumulate; Q6_K and Q8_0 with the float64 anchor of
+# their own GEMM tests (check_q6k_gemm), since the reference's f32 sums of their rows drift past
+# the element-wise bar.
 @pytest.mark.parametrize("dtype,m,n,k", [(Q4_K, 300, 7000, 4096), (Q4_K, 260, 8320, 16384), (Q4_K, 100, 16600, 16384),
-                                         (Q5_K, 130, 16000, 8192)])
+                                         (Q5_K, 130, 16000, 8192), (Q6_K, 260, 8320, 16384), (Q6_K, 300, 7000, 4096),
+                                         (Q8_0, 300, 7000, 4096), (Q8_0, 100, 16600, 16384)])
 def test_gemm_tail_round_split(gpu, dtype, m, n, k):
     torch = gpu
     L = A.lib()
-    nb = k // 256
     be, bb = GEOM[dtype]
+    nb = k // be
     raw_d = torch.empty(n * nb * bb, dtype=torch.uint8, device="cuda")
     A.check(L.aeth_fill_synthetic_raw(dtype, 0x7A11 + n, raw_d.data_ptr(), n * nb, None), "fill")
     rng = np.random.default_rng(m + n)
@@ -750,15 +753,22 @@ def test_gemm_tail_round_split(gpu, dtype, m, n, k):
     T, cus = gm * gn, torch.cuda.get_device_properties(0).multi_processor_count
     tail = T % cus
     assert T > cus and 0 < 2 * tail <= cus, "shape %d x %d does not leave a short last round on %d CUs" % (m, n, cus)
-    print("tiles %d, tail %d split %d ways" % (T, tail, min(cus // tail, nb // 8)), flush=True)
+    print("tiles %d, tail %d split %d ways" % (T, tail, min(cus // tail, k // 2048)), flush=True)
     tails = sorted(set(np.linspace(T - tail, T - 1, min(tail, 8)).round().astype(int).tolist()))
     for t in tails + [0, T // 2, T - tail - 1]:
         tm, tn = g2_tile(t, gm, gn)
         r0, r1, c0, c1 = 64 * tm, min(m, 64 * tm + 64), 128 * tn, min(n, 128 * tn + 128)
         ref = O.reference_matmul(dtype, x[r0:r1].ravel(), raw[c0:c1].ravel(), r1 - r0, c1 - c0, k).reshape(r1 - r0, -1)
         what = "tile %d (%d, %d) of %d x %d x %d" % (t, tm, tn, m, n, k)
-        assert_close(got[r0:r1, c0:c1], ref, what=what)
-        assert_close(got_acc[r0:r1, c0:c1], ref + y0[r0:r1, c0:c1], what=what + " accumulate")
+        if dtype in (Q6_K, Q8_0):  # rows in the hundreds: also anchored on the float64 product (check_q6k_gemm)
+            w64 = O.dequant(dtype, raw[c0:c1].ravel(), (c1 - c0) * k).reshape(c1 - c0, k).astype(np.float64)
+            ex = x[r0:r1].astype(np.float64) @ w64.T
+            assert_close_logits(got[r0:r1, c0:c1], ref, floor=0.0, exact=ex, what=what)
+            assert_close_logits(got_acc[r0:r1, c0:c1], ref + y0[r0:r1, c0:c1], floor=0.0, exact=ex + y0[r0:r1, c0:c1],
+                                what=what + " accumulate")
+        else:
+            assert_close(got[r0:r1, c0:c1], ref, what=what)
+            assert_close(got_acc[r0:r1, c0:c1], ref + y0[r0:r1, c0:c1], what=what + " accumulate")
 
 
 # ── F32 / F16 / Q2_K / Q3_K: GGUF-order and row kernels ───────────────────
