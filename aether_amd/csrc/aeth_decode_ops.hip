@@ -139,8 +139,8 @@ int aeth_kv_append_launch(float* layer_kv, const float* k, const float* v, int64
 // fused with the RoPE of q and k (apply_rope_inplace :1886-1909) and the KV
 // append of the new token (StaticKVCache::append, kv_cache.rs:40-65).
 //
-// Workgroup (chunk c, kv head h) covers positions [64c, 64c+64) of the
-// sequence [0, seq) for the `groups` query heads sharing h. It writes the
+// Workgroup (chunk c, kv head h) covers positions [Tc, Tc+T) (T = ATTN_T = 128) of
+// the sequence [0, seq) for the `groups` query heads sharing h. It writes the
 // chunk's softmax partials (max m, Σe^{s-m}, Σe^{s-m}·v); k_attn_merge then
 // combines them: out = Σ_c e^{m_c-M} o_c / Σ_c e^{m_c-M} l_c.
 //
@@ -152,12 +152,17 @@ int aeth_kv_append_launch(float* layer_kv, const float* k, const float* v, int64
 // A sliding window w (attn_direct's sliding_window, runner.rs:1768-1777)
 // masks the positions before seq - w: chunks wholly before it return at
 // once, and the merge leaves them out.
+// Chunk shape, compile-time options: ATTN_NT threads (256, 512 or 1024), ATTN_LP lanes per
+// position in the scores (2, 4, 8 or 16), ATTN_T = ATTN_NT / ATTN_LP positions per chunk. The 8B
+// decode step at 2049-2176 positions measured (tok/s, two runs each): 512 threads × 4 lanes (T =
+// 128) 675.6-677.0; 512 × 8 (T = 64) 658.0-660.8; 1024 × 8 (T = 128) 669.5-669.6; 256 × 2 (T = 128)
+// 657.3-658.3; 256 × 4 (T = 64) 656.4-656.9; 1024 × 4 and 512 × 2 (T = 256) 640.1-643.6; 32-position
+// chunks 617.
 #ifndef ATTN_NT
-#define ATTN_NT 512  // threads of k_attn (256, 512 or 1024; 256 measured 5 %, 1024 7 % slower at seq 2049)
+#define ATTN_NT 512
 #endif
 #ifndef ATTN_LP
-#define ATTN_LP (ATTN_NT == 1024 ? 16 : 8)  // lanes per position in the scores (16 at 512 threads, 32-position
-                                             // chunks: k_attn 7.80 -> 8.57 us, merge 4.81 -> 6.96 us, not used)
+#define ATTN_LP 4
 #endif
 #define ATTN_T (ATTN_NT / ATTN_LP)  // positions per chunk
 #define ATTN_MAX_GROUPS 8
@@ -179,13 +184,14 @@ struct AttnArgs {
     float* out;          // [n_heads][hd]
 };
 
-// Thread layout (512 threads = 8 waves, two per SIMD; chunk of T = 64
-// positions, HD = 128; 256 threads take T = 32 the same way):
-//  scores: thread (p = tid/8, e = tid%8) holds K[p][32i + 4e, +4) for i < 4
-//          (each load instruction reads 128 contiguous bytes of 8 rows) and
-//          dots it with every query head of the group; 8-lane reduction.
+// Thread layout (shown for the default 512 threads = 8 waves, two per SIMD,
+// LP = 4 lanes per position, chunk of T = 128 positions, HD = 128):
+//  scores: thread (p = tid/4, e = tid%4) holds K[p][16i + 4e, +4) for i < 8
+//          (each load instruction reads 64 contiguous bytes of 16 rows) and
+//          dots it with every query head of the group; 4-lane reduction.
+//  softmax: wave w takes query heads w, w + 8, ...; lane l the positions l, l + 64.
 //  P·V:    thread (dims 4(tid%32), position group pg = tid/32) holds
-//          V[4pg + j][4(tid%32), +4) for j < 4; lanes l, l+32 and then the
+//          V[8pg + j][4(tid%32), +4) for j < 8; lanes l, l+32 and then the
 //          8 waves are summed.
 // All loads are unconditional (clamped indices) and issued in one batch in
 // the order q/rope inputs → K → V, so each phase waits only for its own data.
@@ -308,20 +314,34 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
                 a += qv.x * kk[i].x + qv.y * kk[i].y + qv.z * kk[i].z + qv.w * kk[i].w;
             }
             a += aeth_dpp_xor1f(a);
-            a += aeth_dpp_xor2f(a);
-            a += aeth_dpp_mirror8f(a);
+            if (LP >= 4) a += aeth_dpp_xor2f(a);
+            if (LP >= 8) a += aeth_dpp_mirror8f(a);
             if (LP == 16) a += aeth_dpp_mirror16f(a);
             if (qe == 0) sc[g][sp] = sp < nt && t0 + sp >= wstart ? a * scale : -INFINITY;
         }
     }
     __syncthreads();
-    // 5. softmax over the chunk: wave w handles heads w, w + NWV, ...
+    // 5. softmax over the chunk: wave w handles heads w, w + NWV, ...; lane l holds positions
+    // l, l + 64, ... of the chunk
+    constexpr int ST = (T + 63) / 64;
     for (int g = wave; g < groups; g += NWV) {
-        const float sv = lane < T ? sc[g][lane] : -INFINITY;
-        const float m = aeth_wave_max(sv);
-        const float pr = lane < nt ? expf(sv - m) : 0.0f;
-        const float l = aeth_wave_sum(pr);
-        if (lane < T) sc[g][lane] = pr;
+        float sv[ST], mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < ST; u++) {
+            const int p = lane + 64 * u;
+            sv[u] = p < T ? sc[g][p] : -INFINITY;
+            mx = fmaxf(mx, sv[u]);
+        }
+        const float m = aeth_wave_max(mx);
+        float ps = 0.0f;
+#pragma unroll
+        for (int u = 0; u < ST; u++) {
+            const int p = lane + 64 * u;
+            const float pr = p < nt ? expf(sv[u] - m) : 0.0f;
+            ps += pr;
+            if (p < T) sc[g][p] = pr;
+        }
+        const float l = aeth_wave_sum(ps);
         if (lane == 0) {
             mstat[g][0] = m;
             mstat[g][1] = l;

@@ -201,7 +201,7 @@ extern "C" AETH_API int aeth_attn_decode_noalloc(const float* d_q, const float* 
     const int64_t need = aeth_attn_ws_floats(n_heads, head_dim, max_seq);
     if (need > kNoAllocFloats)
         return aeth_set_error(AETH_EINVAL,
-                              "aeth_attn_decode_noalloc: %lld scratch floats needed (n_heads x ceil(max_seq/64) x "
+                              "aeth_attn_decode_noalloc: %lld scratch floats needed (n_heads x ceil(max_seq/128) x "
                               "(head_dim+2)), more than the %lld the library holds",
                               (long long)need, (long long)kNoAllocFloats);
     int dev = 0;

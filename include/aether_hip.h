@@ -234,7 +234,7 @@ AETH_API int aeth_attn_decode(const float* d_q, const float* d_layer_kv, int64_t
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). Same arguments and results; the chunk partials go to a
  * static device array of 4 MiB (1,048,576 floats) per GPU instead of a
- * library allocation, so n_heads·ceil(max_seq/64)·(head_dim+2) must not exceed
+ * library allocation, so n_heads·ceil(max_seq/128)·(head_dim+2) must not exceed
  * 1,048,576 (AETH_EINVAL otherwise). Calls that overlap on one GPU share that
  * array and race: serialise them (one stream, or one caller at a time). */
 AETH_API int aeth_attn_decode_noalloc(const float* d_q, const float* d_layer_kv, int64_t n_heads, int64_t kv_heads,

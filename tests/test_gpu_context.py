@@ -25,9 +25,9 @@ pytestmark = pytest.mark.gpu
 # (query heads, KV heads, window, prompt length, cache length): G = 2, 8, 1 take the
 # f32-MFMA prefill attention, G = 3 the VALU one; windows shorter than a 16-key block,
 # spanning several, and longer than the prompt; n = 150 and 130 run the GEMM
-# projections and make the decode steps skip whole 64-position chunks (window start
-# 131 → chunks 0 and 1 left out, chunk 2 partly masked; window 64 at seq 131 → start
-# 67). The random test models attend sharply (a query's weights past a few keys often
+# projections and make the decode steps skip a whole 128-position chunk (window start
+# 131 → chunk 0 left out, chunk 1 partly masked; window 64 at seq 131 → start 67, chunk
+# 0 partly masked). The random test models attend sharply (a query's weights past a few keys often
 # underflow to 0), so the windows are chosen where masking changes the oracle's
 # logits, which the test checks.
 CASES = [(4, 2, 4, 37, 64), (4, 2, 20, 150, 192), (8, 1, 33, 70, 96), (4, 4, 6, 45, 64), (6, 2, 9, 70, 96),

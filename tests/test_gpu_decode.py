@@ -51,7 +51,7 @@ def test_rope(gpu, pos):
         assert np.array_equal(xd.cpu().numpy(), x)  # θ = 0: identity
 
 
-@pytest.mark.parametrize("seq", [1, 63, 64, 65, 2049])
+@pytest.mark.parametrize("seq", [1, 63, 64, 65, 127, 128, 129, 2049])
 def test_attention_and_kv_append(gpu, seq):
     torch = gpu
     L = A.lib()
@@ -126,9 +126,9 @@ def test_attention_one_hot(gpu):
 @pytest.mark.parametrize("nh,nkv,ms,seq", [(64, 8, 4096, 3000), (8, 8, 512, 300), (16, 2, 8192, 8192),
                                            (32, 8, 2688, 2600), (4, 1, 256, 1)])
 def test_attention_shapes(gpu, nh, nkv, ms, seq):
-    """Query-head groups of 1, 4 and 8, several chunk-merge batches (seq past
-    2560), the longest cache (128 chunks): back-to-back calls of different
-    shapes share one workspace and its chunk counters."""
+    """Query-head groups of 1, 4 and 8; the longest cache (8192 positions: 64
+    chunks of 128, past the 32 the merge loads in one batch); back-to-back calls
+    of different shapes share one workspace."""
     torch = gpu
     hd = 128
     rng = np.random.default_rng(seq + nh)

@@ -26,7 +26,7 @@ def test_attn_decode_noalloc_matches_attn_decode(gpu):
         torch.cuda.synchronize()
         assert torch.equal(got, ref), (ms, seq)
         assert torch.isfinite(got).all()
-    # 64 heads over 16384 positions need 64·256·130 floats > 2^20
+    # 64 heads over 16384 positions need 64·128·130 floats (chunks of 128 positions) > 2^20
     assert L.aeth_attn_decode_noalloc(q.data_ptr(), kv.data_ptr(), 64, 8, hd, 16384, 10, got.data_ptr(),
                                       None) == A.AETH_EINVAL
     assert "more than" in A.last_error()
