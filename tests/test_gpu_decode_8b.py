@@ -97,6 +97,10 @@ WIDTHS = {
                      "4 / 4"),
     "d9216_ff3072": (dict(vocab_size=4096, d_model=9216, num_layers=1, num_heads=72, num_kv_heads=9, d_ff=3072),
                      "8 (18 steps: 5 5 4 4) / 2"),
+    # the gate|up GEMM's 2 × 260 = 520 tiles leave a last round of 8, split in two over K, under the SwiGLU
+    # epilogue (k_gemm_tail_sum writes h); the down GEMM's plain prep reads k = 16640 in two register chunks
+    "d4096_ff16640": (dict(vocab_size=4096, d_model=4096, num_layers=1, num_heads=32, num_kv_heads=8, d_ff=16640),
+                      "2 / plain, 33 steps (8 8 8 9) in two chunks"),
     "d2048_ff5632": (dict(vocab_size=4096, d_model=2048, num_layers=1, num_heads=16, num_kv_heads=4, d_ff=5632),
                      "1 / 4 (11 steps: 2 3 3 3)"),
 }
@@ -107,8 +111,9 @@ def test_prefill_8b_widths_match_oracle(gpu, width):
     """Batched prefill (forward_batch, runner.rs:833-993) of 70 tokens: the
     Q4_K GEMMs with the RMSNorm (q|k|v, gate|up at k = d_model) and the
     SwiGLU (down, k = d_ff) run inside their activation prep; 70 rows leave
-    58 rows of the last 64-row tile empty. The 8B widths and three others
-    that reach the prep's other register shares."""
+    58 rows of the last 64-row tile empty. The 8B widths and four others
+    that reach the prep's other register shares (and, at d_ff 16640, the
+    gate|up GEMM's last-round K split under its SwiGLU epilogue)."""
     c = dict(C8B, max_seq_len=256, **WIDTHS[width][0])
     L = A.lib()
     d, dff, V = c["d_model"], c["d_ff"], c["vocab_size"]
