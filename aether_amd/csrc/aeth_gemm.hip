@@ -600,8 +600,8 @@ static bool tail_split_off() {
     return off;
 }
 
-// K splits of a K-split GEMM launch over gm × gn tiles (each split keeps at least maxsplit⁻¹ of K,
-// so that every wave has whole units): with at most half as many tiles as CUs, ksplit ways for
+// K splits of a K-split GEMM launch over gm × gn tiles (at most maxsplit ways, so that every wave
+// keeps whole units of K): with at most half as many tiles as CUs, ksplit ways for
 // every tile, as many as fit one round of workgroups; with more tiles than CUs and a last round at
 // most half full, tsplit ways for that round's tiles (g2_tail_ways). The partial tiles go to the
 // stream's scratch; with `whole` (a caller's workspace) nothing is split.
