@@ -722,18 +722,24 @@ def g2_tile(i, gm, gn):
 
 
 # More 64 × 128 tiles than CUs with the last round at most half full: the GEMM splits the K
-# range of those last tiles over the idle CUs and a second kernel sums them. Up to 8 of each
-# shape's tail tiles (the first and last among them) and three whole tiles are checked against
-# the oracle: 19 tail tiles split in 2, 69 in 3, 4 in 8, 119 in 2 (at 256 CUs), each of the four
-# GEMMs (Q4_K, Q5_K, Q6_K, Q8_0), plain and accumulate; Q6_K and Q8_0 with the float64 anchor of
-# their own GEMM tests (check_q6k_gemm), since the reference's f32 sums of their rows drift past
+# range of those last tiles over the idle CUs and a second kernel sums them. n is chosen from the
+# device's CU count so that the tiles are one round plus `tail` (19 split in 2, 69 in 3, 4 in 8,
+# 119 in 2 at 256 CUs), its last column tile `nrag` columns short. Up to 8 of the tail tiles (the
+# first and last among them) and three whole tiles are checked against the oracle, for each of the
+# four GEMMs (Q4_K, Q5_K, Q6_K, Q8_0), plain and accumulate; Q6_K and Q8_0 with the float64 anchor
+# of their own GEMM tests (check_q6k_gemm), since the reference's f32 sums of their rows drift past
 # the element-wise bar.
-@pytest.mark.parametrize("dtype,m,n,k", [(Q4_K, 300, 7000, 4096), (Q4_K, 260, 8320, 16384), (Q4_K, 100, 16600, 16384),
-                                         (Q5_K, 130, 16000, 8192), (Q6_K, 260, 8320, 16384), (Q6_K, 300, 7000, 4096),
-                                         (Q8_0, 300, 7000, 4096), (Q8_0, 100, 16600, 16384)])
-def test_gemm_tail_round_split(gpu, dtype, m, n, k):
+@pytest.mark.parametrize("dtype,m,k,tail,nrag", [(Q4_K, 300, 4096, 19, 40), (Q4_K, 260, 16384, 69, 0),
+                                                 (Q4_K, 100, 16384, 4, 40), (Q5_K, 130, 8192, 119, 0),
+                                                 (Q6_K, 260, 16384, 69, 0), (Q6_K, 300, 4096, 19, 40),
+                                                 (Q8_0, 300, 4096, 19, 40), (Q8_0, 100, 16384, 4, 40)])
+def test_gemm_tail_round_split(gpu, dtype, m, k, tail, nrag):
     torch = gpu
     L = A.lib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    gm = -(-m // 64)
+    gn = -(-(cus + tail) // gm)
+    n = 128 * gn - nrag
     be, bb = GEOM[dtype]
     nb = k // be
     raw_d = torch.empty(n * nb * bb, dtype=torch.uint8, device="cuda")
@@ -749,8 +755,7 @@ def test_gemm_tail_round_split(gpu, dtype, m, n, k):
     finally:
         L.aeth_weight_free(w)
     raw = raw_d.cpu().numpy().reshape(n, nb * bb)
-    gm, gn = -(-m // 64), -(-n // 128)
-    T, cus = gm * gn, torch.cuda.get_device_properties(0).multi_processor_count
+    T = gm * gn
     tail = T % cus
     assert T > cus and 0 < 2 * tail <= cus, "shape %d x %d does not leave a short last round on %d CUs" % (m, n, cus)
     print("tiles %d, tail %d split %d ways" % (T, tail, min(cus // tail, k // 2048)), flush=True)
