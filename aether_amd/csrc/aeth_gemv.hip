@@ -325,15 +325,17 @@ __device__ __forceinline__ void mq_load_x(const float* __restrict__ x, int o0, i
 // q = sat_i8(RNE(x·(1/d))) with the f32 d, zeros when d is not > 0; digit 0
 // holds q, the others zero; meta Q4_K / Q5_K {Σq, d_a}, Q8_0 {0, d_a}, Q6_K
 // per 16 elements {Σq, d_a} (d_a = the stored f16 scale as f32).
-// Returns nonzero (wave-uniform) if the slice holds a NaN or an infinity.
+// Converts the octet sets xv[ib .. ie) (set i: this lane's octet o0 + lane + 64i), each set
+// independently; returns nonzero (wave-uniform) if they hold a NaN or an infinity.
 template <int F, int XO, bool Q8A>
-__device__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase, char* Mbase) {
+__device__ __forceinline__ int mq_build(float (&xv)[XO][8], int c0, int nbw, int kx, char* Abase, char* Mbase,
+                                        int ib = 0, int ie = XO) {
     typedef MF<F> T;
     const int lane = threadIdx.x & 63;
     const int o0 = c0 * (T::CE / 8), o1 = (c0 + nbw) * (T::CE / 8);
     int bad = 0;
 #pragma unroll
-    for (int i = 0; i < XO; i++) {
+    for (int i = ib; i < ie; i++) {
         const int o = o0 + lane + 64 * i;
         const bool live = o < o1;
         float* v = xv[i];
@@ -548,22 +550,30 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
 
     // a NaN or infinity in the slice makes every partial of this wave NaN
     if (lane == 0) *(uint4*)zs = make_uint4(0u, 0u, 0u, 0u);
-    const float poison = mq_build<F, XO, Q8A>(xv, c0, nbw, G.kx, Abase, Mbase) ? __int_as_float(0x7FC00000) : 0.0f;
+    // With several octet sets per lane (long rows), only the first is converted before the
+    // first tile's dots; set x is converted within them, just before chunk CPX·x, the first it
+    // feeds, so that the conversion of a long slice does not hold back every dot
+    constexpr int CPX = 512 / T::CE;  // chunks per octet set
+    constexpr bool LAZY = XO > 1 && !Q8A;
+    int bad = mq_build<F, XO, Q8A>(xv, c0, nbw, G.kx, Abase, Mbase, 0, LAZY ? 1 : XO);
 
-    auto tile = [&](const Dt (&b)[NBW]) {
+    auto tile = [&](const Dt (&b)[NBW], bool first) {
         float acc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NBW; i++)
+        for (int i = 0; i < NBW; i++) {
+            if (LAZY && first && i > 0 && i % CPX == 0 && i / CPX < XO)
+                bad |= mq_build<F, XO, Q8A>(xv, c0, nbw, G.kx, Abase, Mbase, i / CPX, i / CPX + 1);
             if (i < nbw)
                 acc += T::template dot<Q8A, PD>(b[i], Abase + (size_t)(c0 + i) * T::AB, Mbase + (size_t)(c0 + i) * T::MB,
                                             lane, L, zs);
-        return aeth_sum_rows(acc) + poison;
+        }
+        return aeth_sum_rows(acc) + (bad ? __int_as_float(0x7FC00000) : 0.0f);
     };
     if (!RING) {  // every tile already in flight: no refills
 #pragma unroll
         for (int r = 0; r < RD; r++) {
             if (r < ntw) {
-                const float acc = tile(buf[r]);
+                const float acc = tile(buf[r], r == 0);
                 if (lane < 16) part[(r * W + wave) * 16 + lane] = acc;
             }
             __builtin_amdgcn_sched_barrier(0);  // tiles in arrival order: wait for each one alone
@@ -574,7 +584,7 @@ __global__ void __launch_bounds__(64 * W) k_gemv_mf(MqParams G) {
             for (int r = 0; r < RD; r++) {
                 const int j = j0 + r;
                 if (j < ntw) {
-                    const float acc = tile(buf[r]);
+                    const float acc = tile(buf[r], j == 0);
                     if (lane < 16) part[(j * W + wave) * 16 + lane] = acc;
                 }
                 // refill with tile j + RD; past the run, the same loads of chunk 0 of tile 0,
