@@ -401,13 +401,17 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
 // Every wave reduces the chunk statistics itself — lane c holds chunks c,
 // c + 64, ... — and the weights reach the other lanes by readlane, so the kernel
 // has no LDS traffic and no barrier. Thread d loads its column of the chunk
-// slots that cover 4096 positions in one batch together with the statistics,
+// slots that cover 2560 positions in one batch together with the statistics,
 // before the sequence length is known (slots past the live chunks are never
-// used); the chunks of a longer cache are read afterwards.
+// used); the live chunks of a longer cache follow in batches of 16. (Slots for
+// 2560, 3072 and 4096 positions measured 677.6-680.3, 675.8-676.2 and
+// 672.8-673.3 tok/s on the 8B decode step at 2049-2176 positions: a slot loaded
+// and not used costs more than the later batch at these lengths.)
 template <int HD>
 __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
     constexpr int S = (ATTN_MAX_CHUNKS + 63) / 64;                                  // statistics per lane
-    constexpr int CB = 4096 / ATTN_T < ATTN_MAX_CHUNKS ? 4096 / ATTN_T : ATTN_MAX_CHUNKS;  // batched slots
+    constexpr int CB = 2560 / ATTN_T < ATTN_MAX_CHUNKS ? 2560 / ATTN_T : ATTN_MAX_CHUNKS;  // batched slots
+    constexpr int CG = 16;                                                         // later batches
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const float* base = A.ws + (int64_t)h * A.max_chunks * (HD + 2);
     const int cmax = A.max_chunks - 1;
@@ -450,12 +454,20 @@ __global__ void __launch_bounds__(HD) k_attn_merge(AttnArgs A) {
         const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[j / 64]), j % 64));
         acc += (live ? wj : 0.0f) * (live ? v[j] : 0.0f);
     }
-    for (int c = max(CB, c_lo); c < nch; c++) {  // past 4096 positions
-        float wc = 0.0f;
+    for (int c0 = CB; c0 < nch; c0 += CG) {  // past the first batch: CG slots per batch, loads issued together
+        float vr[CG];
 #pragma unroll
-        for (int u = 0; u < S; u++)
-            if (u == c / 64) wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[u]), c % 64));
-        acc += wc * base[(int64_t)c * (HD + 2) + tid];
+        for (int j = 0; j < CG; j++) vr[j] = base[(int64_t)min(c0 + j, cmax) * (HD + 2) + tid];
+#pragma unroll
+        for (int j = 0; j < CG; j++) {
+            const int c = c0 + j;
+            const bool live = c >= c_lo && c < nch;
+            float wc = 0.0f;
+#pragma unroll
+            for (int u = 0; u < S; u++)
+                if (u == c / 64) wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[u]), c % 64));
+            acc += (live ? wc : 0.0f) * (live ? vr[j] : 0.0f);
+        }
     }
     A.out[(int64_t)h * HD + tid] = acc / L;
 }
