@@ -210,7 +210,10 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs A) {
     __shared__ float sc[ATTN_MAX_GROUPS][T];
     __shared__ __attribute__((aligned(16))) float ov[NWV][ATTN_MAX_GROUPS][HD];
     __shared__ float mstat[ATTN_MAX_GROUPS][2];
-    const int kvh = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // grid (kv head, chunk), kv head fastest: the workgroups of the live chunks are dispatched
+    // before those past the sequence (a captured step's grid covers max_seq), which return at
+    // once (decode 682.3 tok/s against 679.9 with the chunk index fastest, six runs each)
+    const int kvh = blockIdx.x, chunk = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int groups = A.n_heads / A.kv_heads;
     int64_t fill = -1, pos = 0, seq;
     if (A.st) {
@@ -502,7 +505,7 @@ int aeth_attn_launch(const float* q, const float* qkv, float* layer_kv, const fl
     A.out = out;
     const int grid_chunks = d_st ? A.max_chunks : (int)aeth_cdiv(min(seq, max_seq), ATTN_T);
     if (grid_chunks <= 0) return AETH_OK;
-    hipLaunchKernelGGL((k_attn<128, ATTN_NT>), dim3(grid_chunks, (unsigned)kv_heads), dim3(ATTN_NT), 0, s, A);
+    hipLaunchKernelGGL((k_attn<128, ATTN_NT>), dim3((unsigned)kv_heads, (unsigned)grid_chunks), dim3(ATTN_NT), 0, s, A);
     AETH_LAUNCH_CHECK();
     hipLaunchKernelGGL(k_attn_merge<128>, dim3((unsigned)n_heads), dim3(128), 0, s, A);
     AETH_LAUNCH_CHECK();
