@@ -604,7 +604,8 @@ static bool tail_split_off() {
 // keeps whole units of K): with at most half as many tiles as CUs, ksplit ways for
 // every tile, as many as fit one round of workgroups; with more tiles than CUs and a last round at
 // most half full, tsplit ways for that round's tiles (g2_tail_ways). The partial tiles go to the
-// stream's scratch; with `whole` (a caller's workspace) nothing is split.
+// stream's scratch (g2_part's layouts: all of C per split, or the tail tiles only); with `whole`
+// (a caller's workspace) nothing is split.
 struct SplitPlan {
     int ksplit = 1, tsplit = 1, t_full = 0;
     float* part = nullptr;
@@ -618,10 +619,11 @@ static int split_plan(hipStream_t s, int64_t gm, int64_t gn, int64_t maxsplit, b
         P.tsplit = g2_tail_ways(T, cus, maxsplit);
         if (P.tsplit > 1) P.t_full = (int)(T - T % cus);
     }
-    const int ways = std::max(P.ksplit, P.tsplit);
-    if (ways == 1) return AETH_OK;
+    if (P.ksplit == 1 && P.tsplit == 1) return AETH_OK;
+    const size_t floats = P.tsplit > 1 ? (size_t)P.tsplit * (size_t)(T - P.t_full) * G2_BM * G2_BN
+                                       : (size_t)P.ksplit * gm * G2_BM * gn * G2_BN;
     void* p = nullptr;
-    const int rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, (size_t)ways * gm * G2_BM * gn * G2_BN * sizeof(float), &p);
+    const int rc = aeth_stream_scratch(s, AETH_SCRATCH_SPLIT, floats * sizeof(float), &p);
     P.part = (float*)p;
     return rc;
 }

@@ -145,6 +145,19 @@ __device__ __forceinline__ void g2_work(int bid, int gm, int gn, int ksplit, int
     }
 }
 
+// Partial tile of split ks of `tile` (its 64 × 128 block at rows m0, columns n0 of C): the address of
+// its element (0, 0) and the row stride ld. A K split over every tile keeps C's layout, part[ks][mp][pld];
+// a tail split stores only the tail tiles, part[ks][tile − t_full][64][128].
+__device__ __forceinline__ float* g2_part(float* part, int ks, int tile, int t_full, int tsplit, int T, int mp, int pld,
+                                          int m0, int n0, int& ld) {
+    if (tsplit > 1) {
+        ld = 128;
+        return part + ((int64_t)ks * (T - t_full) + (tile - t_full)) * (64 * 128);
+    }
+    ld = pld;
+    return part + ((int64_t)ks * mp + m0) * pld + n0;
+}
+
 // Ways to split the K range of every tile of a short last round (the launch has no K split):
 // more tiles than CUs and a last round at most half full → as many ways as fill the idle CUs,
 // at most maxsplit; otherwise 1.
@@ -215,8 +228,8 @@ struct KqArgs {
     const uint8_t* fifth;
     int f_bytes;
     // Tail split (ksplit == 1, tsplit > 1): tiles [t_full, gm·gn) — the last, partial round of
-    // workgroups — have K split over tsplit workgroups each (partials in part, as with ksplit)
-    // and are summed by the tail-sum kernel; tiles below t_full run whole
+    // workgroups — have K split over tsplit workgroups each (partials in part as g2_part lays them
+    // out) and are summed by the tail-sum kernel; tiles below t_full run whole
     int t_full = 0, tsplit = 1;
 };
 int aeth_gemm_kq_launch(const KqArgs& G, hipStream_t s);
@@ -232,7 +245,8 @@ struct SplitSum {
     float* C;
     int64_t ldc;
     int m, n, accumulate, swiglu;
-    // gm > 0: only the 64 × 128 tiles [t_full, gm·gn) in g2_tile's order (a tail split)
+    // gm > 0: only the 64 × 128 tiles [t_full, gm·gn) in g2_tile's order (a tail split; partials
+    // part[split][tile − t_full][64][128])
     int t_full = 0, gm = 0, gn = 0;
 };
 int aeth_gemm_split_sum_launch(const SplitSum& S, hipStream_t s);

@@ -421,9 +421,10 @@ __global__ void __launch_bounds__(64 * K8_W) k_gemm_kq(KqArgs G) {
         for (int w = 1; w < 4; w++) sum[r] += red[(((w * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
     }
     if (nsplit > 1) {  // the split's partial tile (rows < mp, columns < pld: no bounds to check)
-        float* P = G.part + (int64_t)ks * G.mp * G.pld + col;
+        int ld;
+        float* P = g2_part(G.part, ks, tile, G.t_full, G.tsplit, G.gm * G.gn, G.mp, G.pld, m0, n0, ld) + (col - n0);
 #pragma unroll
-        for (int r = 0; r < 16; r++) P[(int64_t)rows[r] * G.pld] = sum[r];
+        for (int r = 0; r < 16; r++) P[(int64_t)(rows[r] - m0) * ld] = sum[r];
     } else if (G.swiglu) {
 #pragma unroll
         for (int r = 0; r < 16; r += 2) g2_store_swiglu(E, r, G.C, G.ldc, G.m, G.n, rows[r], col, sum[r], sum[r + 1]);

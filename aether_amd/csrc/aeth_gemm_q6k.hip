@@ -357,9 +357,11 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
         for (int w = 1; w < 4; w++) sum[r] += red[(((w * 2 + mt) * 4 + c) * 16 + r) * 64 + lane];
     }
     if (nsplit > 1) {  // the split's partial tile (rows < mp, columns < pld: no bounds to check)
-        float* P = G.part + ((int64_t)ks * G.mp + m0 + 32 * mt) * G.pld + col;
+        int ld;
+        float* P = g2_part(G.part, ks, tile, G.t_full, G.tsplit, G.gm * G.gn, G.mp, G.pld, m0, n0, ld) +
+                   32 * mt * ld + (col - n0);
 #pragma unroll
-        for (int r = 0; r < 16; r++) P[(int64_t)(rows[r] - m0 - 32 * mt) * G.pld] = sum[r];
+        for (int r = 0; r < 16; r++) P[(int64_t)(rows[r] - m0 - 32 * mt) * ld] = sum[r];
     } else if (G.swiglu) {
 #pragma unroll
         for (int r = 0; r < 16; r += 2) g2_store_swiglu(E, r, G.C, G.ldc, G.m, G.n, rows[r], col, sum[r], sum[r + 1]);
@@ -369,10 +371,9 @@ __global__ void __launch_bounds__(64 * K6_W) k_gemm_q6k_kq(Q6Args G) {
     }
 }
 
-// Sum of the K splits, in split order, and the epilogue (SplitSum), for 4 columns of a row.
-__device__ __forceinline__ void split_sum_out(const SplitSum& G, int row, int col) {
-    const float4* P = (const float4*)(G.part + (int64_t)row * G.pld + col);
-    const int64_t split = (int64_t)G.mp * G.pld / 4;
+// Sum of the K splits, in split order, and the epilogue (SplitSum), for 4 columns of a row: the
+// splits' partials at P, P + split, ... (float4 units).
+__device__ __forceinline__ void split_sum_out(const SplitSum& G, const float4* P, int64_t split, int row, int col) {
     float4 v = P[0];
     for (int s = 1; s < G.ksplit; s++) {
         const float4 t = P[s * split];
@@ -402,7 +403,7 @@ __global__ void __launch_bounds__(256) k_gemm_split_sum(SplitSum G) {
     if (i >= (int64_t)G.m * q4) return;
     const int row = (int)(i / q4), col = (int)(i - (int64_t)row * q4) * 4;
     if (col >= G.n) return;
-    split_sum_out(G, row, col);
+    split_sum_out(G, (const float4*)(G.part + (int64_t)row * G.pld + col), (int64_t)G.mp * G.pld / 4, row, col);
 }
 
 // The tiles of a tail split only: 8 workgroups per 64 × 128 tile, one thread per 4 columns of a
@@ -413,7 +414,9 @@ __global__ void __launch_bounds__(256) k_gemm_tail_sum(SplitSum G) {
     g2_tile(tile, G.gm, G.gn, tm, tn);
     const int row = tm * 64 + (idx >> 5), col = tn * 128 + (idx & 31) * 4;
     if (row >= G.m || col >= G.n) return;
-    split_sum_out(G, row, col);
+    const int ntail = G.gm * G.gn - G.t_full;
+    const float* P = G.part + (int64_t)(tile - G.t_full) * (64 * 128) + (idx >> 5) * 128 + (idx & 31) * 4;
+    split_sum_out(G, (const float4*)P, (int64_t)ntail * (64 * 128 / 4), row, col);
 }
 
 int aeth_gemm_split_sum_launch(const SplitSum& S, hipStream_t s) {
