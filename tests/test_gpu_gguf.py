@@ -208,3 +208,65 @@ def test_aether_load_sliding_window_and_context_cap(gpu, tmp_path):
         assert_close_logits(logits, ref2, what="windowed decode at position 5000")
     finally:
         L.aether_free(m)
+
+
+def test_aether_load_greedy_generation_is_deterministic(gpu, tmp_path):
+    """The reference's end-to-end determinism property (tests/e2e.rs:220-250): a
+    GGUF file loaded, prompted and decoded greedily for 16 tokens, then freed and
+    loaded again, gives the same tokens. Here the logits of every step must also
+    be bit-identical between the two loads, and each step's logits are checked
+    against the oracle's decode step fed the same tokens (teacher-forced on the
+    device's own greedy path, runner.rs:1557-1646, sample :1964-1973)."""
+    L = A.lib()
+    c = CFG
+    path = tmp_path / "e2e.gguf"
+    mdl = build_file(path, layer_dtype=Q4_K_M, lm_dtype=Q6_K)
+    prompt = np.random.default_rng(11).integers(0, c["vocab_size"], 6).astype(np.int32)
+    n_gen = 16
+
+    def run():
+        m = L.aether_load(str(path).encode())
+        assert m, last_error(L)
+        toks, rows = [], []
+        try:
+            logits = np.empty(c["vocab_size"], dtype=np.float32)
+            assert L.aether_prefill(m, prompt.ctypes.data, len(prompt), logits.ctypes.data) == 0, last_error(L)
+            rows.append(logits.copy())
+            for i in range(n_gen):
+                tok = L.aether_argmax(m, logits.ctypes.data)
+                assert 0 <= tok < c["vocab_size"]
+                toks.append(tok)
+                if i + 1 < n_gen:
+                    assert L.aether_decode(m, tok, len(prompt) + i, logits.ctypes.data) == 0, last_error(L)
+                    rows.append(logits.copy())
+        finally:
+            L.aether_free(m)
+        return toks, rows
+
+    toks1, rows1 = run()
+    toks2, rows2 = run()
+    assert toks1 == toks2, "greedy generation differs between two loads of the same file"
+    for i, (a, b) in enumerate(zip(rows1, rows2)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), "step %d logits differ between loads" % i
+
+    # every step against the oracle, on the device's tokens
+    ocfg = O.LlamaCfg(c["vocab_size"], c["d_model"], c["num_layers"], c["num_heads"], c["num_kv_heads"],
+                      c["head_dim"], c["d_ff"], 64, c["rope_base"], c["rms_norm_eps"])
+    s, co = O.precompute_rope(64, c["head_dim"], c["rope_base"])
+    kv = np.zeros((c["num_layers"], 2, c["num_kv_heads"], 64, c["head_dim"]), dtype=np.float32)
+    ref = O.forward_batch(ocfg, mdl["emb"][prompt], mdl["layers"], mdl["layer_dtype"], mdl["norms"], mdl["final"],
+                          mdl["lm"], mdl["lm_dtype"], s, co, kv)
+    seq = list(prompt)
+    ex = lambda sq: logits64(dict(c, max_seq_len=64), mdl["emb"], mdl["layers"], mdl["layer_dtype"], mdl["norms"],
+                             mdl["final"], mdl["lm"], mdl["lm_dtype"], sq)
+    assert_close_logits(rows1[0], ref, what="e2e prefill", exact=ex(seq))
+    fill = len(prompt)
+    for i in range(1, n_gen):
+        tok = toks1[i - 1]
+        ref, fill = O.decode_step(ocfg, mdl["emb"][tok], len(prompt) + i - 1, mdl["layers"], mdl["layer_dtype"],
+                                  mdl["norms"], mdl["final"], mdl["lm"], mdl["lm_dtype"], s, co, kv, fill)
+        seq.append(tok)
+        assert_close_logits(rows1[i], ref, what="e2e decode step %d" % i, exact=ex(seq))
+    # aether_argmax keeps the last maximal index on ties (Iterator::max_by, c_api.rs:384-396)
+    for i, row in enumerate(rows1):
+        assert toks1[i] == len(row) - 1 - int(np.argmax(row[::-1])), "step %d: argmax" % i
